@@ -1,0 +1,204 @@
+"""Benchmark of the packed-KV decode hot path on one MI355X.
+
+Workload: batched decode over 2-bit KIVI-packed KV,
+GQA 28/4, head_dim 128, 28 layers, batch 8, 8192 tokens per sequence (8064
+packed + 128 bf16 residual), one bf16 query token per sequence per step.
+A step is one decode pass over all 28 layers x 8 sequences: a single
+uc_kivi_attn_decode_batch launch (split-K partials + LSE combine) over 28
+distinct layer buffers (755 MB, more than the 256 MB Infinity Cache).
+
+Prints one JSON line: metric value = algorithmic bytes moved per step / step
+time (GB/s), plus the roofline of the decode kernel and a CPU baseline (the
+numpy oracle on a bounded sample of the same workload, rank 0, N=1).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+LAYERS, BATCH, TOKENS, HKV, HQ, D = 28, 8, 8192, 4, 28, 128
+BITS, GROUP, RESIDUAL = 2, 32, 128
+
+
+def make_kv(tokens, *, seed, device, heads=HKV, head_dim=D):
+    """N(0,1) K with 8 random channels per head scaled x10, N(0,1) V (bf16)."""
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    key = torch.randn(tokens, heads, head_dim, generator=g, device=device, dtype=torch.float32)
+    value = torch.randn(tokens, heads, head_dim, generator=g, device=device, dtype=torch.float32)
+    for h in range(heads):
+        ch = torch.randperm(head_dim, generator=g, device=device)[:8]
+        key[:, h, ch] *= 10.0
+    return key.to(torch.bfloat16), value.to(torch.bfloat16)
+
+
+def build_workload(device, layers=LAYERS, batch=BATCH, tokens=TOKENS):
+    from unicache_amd.storage import PackedKIVICache
+
+    caches, queries = [], []
+    pack_ms = 0.0
+    pack_bytes = 0
+    for layer in range(layers):
+        for b in range(batch):
+            key, value = make_kv(tokens, seed=1000 * layer + b, device=device)
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            cache = PackedKIVICache.from_dense(key, value, logical_token_ids=torch.arange(tokens, device=device),
+                                               token_type_id=3, k_bits=BITS, v_bits=BITS, group_size=GROUP,
+                                               residual_length=RESIDUAL, backend="cuda")
+            stop.record()
+            torch.cuda.synchronize()
+            pack_ms += start.elapsed_time(stop)
+            pack_bytes += key.numel() * 2 * 2 + cache.resident_bytes - cache.logical_token_ids.numel() * 8
+            caches.append(cache)
+            g = torch.Generator(device=device).manual_seed(7 + 1000 * layer + b)
+            queries.append(torch.randn(1, HQ, D, generator=g, device=device).to(torch.bfloat16))
+            del key, value
+    return caches, queries, pack_ms, pack_bytes
+
+
+def time_steps(fn, steps, warmup, stream):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def cpu_baseline(algorithmic_bytes_per_seq_layer, budget_s=12.0):
+    """The numpy oracle's decode (dequantize + fp64 attention) on one layer of
+    the workload, sequences processed until ~budget_s of CPU time."""
+
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention as A
+    from oracle import kivi as K
+
+    g = torch.Generator().manual_seed(0)
+    key = torch.randn(TOKENS, HKV, D, generator=g)
+    value = torch.randn(TOKENS, HKV, D, generator=g)
+    for h in range(HKV):
+        key[:, h, torch.randperm(D, generator=g)[:8]] *= 10.0
+    kb = key.to(torch.bfloat16).float().numpy()
+    vb = value.to(torch.bfloat16).float().numpy()
+    seg = K.from_dense(kb, vb, k_bits=BITS, v_bits=BITS, group_size=GROUP, residual_length=RESIDUAL)
+    q = torch.randn(1, HQ, D, generator=g).to(torch.bfloat16).float().numpy()
+    done, t0 = 0, time.perf_counter()
+    with threadpool_limits(limits=1):
+        while True:
+            A.packed_summary(seg, q, include_residual=True, kv_dtype="bf16")
+            done += 1
+            if time.perf_counter() - t0 >= budget_s or done >= 64:
+                break
+    elapsed = time.perf_counter() - t0
+    return {
+        "value": round(done * algorithmic_bytes_per_seq_layer / elapsed / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{done} sequence-layers of the config-1 decode (8064 packed 2-bit + 128 bf16 tokens, "
+                  f"GQA 28/4) through oracle.kivi.dequantize + oracle.attention, numpy, BLAS limited to 1 "
+                  f"thread, {elapsed:.1f} s",
+    }
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--layers", type=int, default=LAYERS)
+    parser.add_argument("--calibrate-copy", action="store_true",
+                        help="only run a 1 GiB device copy (PMC traffic calibration)")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the decode hot path shards by sequence / KV head with no "
+              "exchange, and this build runs on a single MI355X (use --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_copy_bytes": 1 << 30}))
+        return
+
+    from unicache_amd.storage.decode import KiviDecodeBatch
+
+    caches, queries, pack_ms, pack_bytes = build_workload(device, layers=args.layers)
+    batch = KiviDecodeBatch(caches, queries)
+    stream = torch.cuda.current_stream(device)
+    sid = stream.cuda_stream
+    run = lambda: batch.run(sid)  # noqa: E731
+    ms = time_steps(run, args.steps, args.warmup, stream)
+    step_bytes = batch.algorithmic_bytes
+    value = step_bytes / (ms * 1e-3) / 1e9
+
+    # per-layer launches (28 launches of 8 sequences each) for comparison
+    per_layer = [KiviDecodeBatch(caches[i * BATCH:(i + 1) * BATCH], queries[i * BATCH:(i + 1) * BATCH])
+                 for i in range(args.layers)]
+    ms_layers = time_steps(lambda: [p.run(sid) for p in per_layer], max(5, args.steps // 5), 2, stream)
+
+    seq_layer_bytes = step_bytes // (args.layers * BATCH)
+    result = {
+        "metric": "packed-KV decode attention GB/s (2-bit KIVI, config 1: 28 layers x batch 8 x 8192 ctx)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u2 codes + fp16 stats, bf16 q/residual, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1), 8 K outlier channels x10 per head)",
+        "config": {
+            "workload": "config 1: batched decode, 2-bit packed KV, GQA 28/4, head_dim 128, "
+                        f"{args.layers} layers, batch {BATCH}, 8192 tokens (8064 packed + 128 residual), Lq=1",
+            "layers": args.layers, "batch": BATCH, "context": TOKENS, "bits": BITS, "group_size": GROUP,
+            "residual": RESIDUAL,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(value, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "uc_kivi_attn_decode_batch (split-K partial + LSE combine), one launch per step",
+            "bytes_per_launch": step_bytes,
+        },
+        "per_layer_launches_gbs": round(step_bytes / (ms_layers * 1e-3) / 1e9, 2),
+        "pack_gbs": round(pack_bytes / (pack_ms * 1e-3) / 1e9, 2),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(seq_layer_bytes)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,302 @@
+/*
+ * unicache_hip.h -- C ABI of libunicache_hip.so, the MI355X (gfx950) kernels
+ * behind UniCache's physical KV-cache engine (KIVI pack, packed attention,
+ * H2O selection and GQA compaction).
+ *
+ * Conventions shared by every entry point
+ *  - Every pointer argument is a device pointer unless the comment says
+ *    otherwise.  Sizes and strides are int64 element counts (not bytes).
+ *  - Tensors named "dense" are token-major [tokens, heads, head_dim] as in
+ *    UniCache (physical.py:242-246).  Packed KIVI tensors use the kernel-native
+ *    layout of kivi_cuda.py:177-182:
+ *        key_code   int32 [Hkv, D, T*bits/32]   (codes LSB-first along tokens)
+ *        key_scale  fp16  [Hkv, D, T/G]          key_min likewise
+ *        value_code int32 [Hkv, T, D*bits/32]   (codes LSB-first along channels)
+ *        value_scale fp16 [Hkv, T, D/G]          value_min likewise
+ *    The pack/dequant entry points take explicit strides so the same kernels
+ *    also produce UniCache's non-native "reference" layout (physical.py:291-304).
+ *  - The library never allocates or frees device memory and never
+ *    synchronises: callers own every output and workspace, and all work is
+ *    enqueued on the hipStream_t passed as `stream` (NULL = default stream).
+ *  - Return value: UC_OK (0), UC_EINVAL (-1, bad shape/bits/group: Python
+ *    maps it to ValueError) or UC_ERUNTIME (-2, layout or HIP launch error:
+ *    RuntimeError).  uc_last_error() returns the calling thread's message.
+ */
+#ifndef UNICACHE_HIP_H
+#define UNICACHE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UC_ABI_VERSION 1
+
+/* element type codes */
+#define UC_BF16 0
+#define UC_FP16 1
+#define UC_FP32 2
+
+/* return codes */
+#define UC_OK 0
+#define UC_EINVAL (-1)
+#define UC_ERUNTIME (-2)
+
+/* uc_workspace_bytes() operation codes */
+#define UC_OP_KIVI_DECODE 1
+#define UC_OP_KIVI_AV 2
+#define UC_OP_H2O_SCORES 3
+
+/* hipStream_t, kept opaque so the header needs no HIP include */
+typedef void *uc_stream_t;
+
+/* Version of this header the library was built from (UC_ABI_VERSION). */
+int uc_abi_version(void);
+
+/* Thread-local description of the last error ("" after a success). */
+const char *uc_last_error(void);
+
+/*
+ * KIVI quantize + pack of one dense K/V segment.
+ * Replaces: quant.new_pack.triton_quantize_and_pack_along_last_dim as called by
+ * quantize_kivi_native (kivi_cuda.py:157-190) and, through the stride
+ * arguments, _quantize_grouped / _pack_codes (physical.py:66-85, 139-175).
+ * Arithmetic (fp32 throughout): mn/mx over each group, scale =
+ * max((mx-mn)/(2^b-1), FLT_EPSILON), code = clamp(rint((x-mn)/scale)),
+ * scale/mn stored as `stats_dtype` (round to nearest even).
+ * Keys are grouped along tokens, values along channels (KIVI).
+ *   key, value: dense [tokens, heads, head_dim] of `in_dtype`, strides (st,sh,sd)
+ *   k_bits, v_bits in {2,4,8}; 8-bit codes are stored one per byte (uint8).
+ *   group_size in {16,32,64,128}; tokens % group_size == 0,
+ *   head_dim % group_size == 0.
+ *   key_code element (h,d,w) at kc_sh*h + kc_sd*d + kc_sw*w (w = word, or
+ *   token when k_bits==8); key stats (h,d,g) at ks_sh*h + ks_sd*d + ks_sg*g.
+ *   value_code (h,t,w) at vc_sh*h + vc_st*t + vc_sw*w; value stats (h,t,g) at
+ *   vs_sh*h + vs_st*t + vs_sg*g.
+ */
+int uc_kivi_pack(const void *key, int64_t k_st, int64_t k_sh, int64_t k_sd,
+                 const void *value, int64_t v_st, int64_t v_sh, int64_t v_sd,
+                 int in_dtype, int64_t tokens, int64_t heads, int64_t head_dim,
+                 int k_bits, int v_bits, int group_size, int stats_dtype,
+                 void *key_code, int64_t kc_sh, int64_t kc_sd, int64_t kc_sw,
+                 void *key_scale, void *key_min, int64_t ks_sh, int64_t ks_sd, int64_t ks_sg,
+                 void *value_code, int64_t vc_sh, int64_t vc_st, int64_t vc_sw,
+                 void *value_scale, void *value_min, int64_t vs_sh, int64_t vs_st, int64_t vs_sg,
+                 uc_stream_t stream);
+
+/*
+ * Dequantize tokens [start, stop) of a packed segment into dense outputs
+ * out_key/out_value [n, heads, head_dim] (strides o_st,o_sh,o_sd) beginning at
+ * row `output_offset`.  Bit-exact with PackedKIVICache.dequantize:
+ * fp32 code*scale, then +min (two roundings, physical.py:190-201), then a
+ * round-to-nearest-even cast to `out_dtype`.
+ * Replaces: _dequantize_kv_chunk_kernel / dequantize_kv_chunk_tiled
+ * (kivi_triton.py:385-502, 690-770) behind dequantize_kivi_chunk
+ * (kivi_cuda.py:58-93), and the full dequantize (physical.py:379-423).
+ * Code/stat strides follow uc_kivi_pack.  Either key_code or value_code may be
+ * NULL to restore only the other tensor.
+ */
+int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_sd, int64_t kc_sw,
+                    const void *key_scale, const void *key_min, int64_t ks_sh, int64_t ks_sd, int64_t ks_sg,
+                    const void *value_code, int64_t vc_sh, int64_t vc_st, int64_t vc_sw,
+                    const void *value_scale, const void *value_min, int64_t vs_sh, int64_t vs_st, int64_t vs_sg,
+                    int stats_dtype, int64_t heads, int64_t head_dim,
+                    int k_bits, int v_bits, int group_size, int64_t start, int64_t stop,
+                    void *out_key, void *out_value, int out_dtype,
+                    int64_t o_st, int64_t o_sh, int64_t o_sd, int64_t output_offset,
+                    uc_stream_t stream);
+
+/*
+ * KIVI fake quantization (quantize then dequantize, no packing) of a dense
+ * [tokens, heads, head_dim] tensor, grouped along `dim` (0 = tokens for keys,
+ * 2 = channels for values), written to `out` (same strides as the input).
+ * Arithmetic of asymmetric_fake_quant (operators/builtin.py:31-53):
+ * scale = max(mx-mn, FLT_EPSILON)/(2^b-1), out = code*scale + mn.
+ * Groups are min(group_size, length) wide; the last one may be partial.
+ * Replaces: kivi_fake_quant_key / kivi_fake_quant_value (builtin.py:56-65).
+ */
+int uc_kivi_fake_quant(const void *data, int64_t st, int64_t sh, int64_t sd,
+                       int dtype, int64_t tokens, int64_t heads, int64_t head_dim,
+                       int bits, int dim, int group_size,
+                       void *out, uc_stream_t stream);
+
+/*
+ * Scaled logits over a packed segment plus its dense residual:
+ *   logits[hq, i, t] = sm_scale * <query[i, hq, :], K[t, hq / group, :]>
+ * for t < quantized_tokens from the packed keys (native layout, contiguous)
+ * and t >= quantized_tokens from the dense residual_key, element (t, h, d) at
+ * r_st*t + r_sh*h + d.  logits is fp32 [Hq, Lq, Tq+Tr] (contiguous).  With
+ * quantized_tokens == 0 this is the dense GQA QK of gqa_query_key_logits
+ * (physical.py:20-39).
+ * Replaces: the KIVI GEMV QK (cuda_bmm_fA_qB_outer, kivi_cuda.py:257-266),
+ * packed_qk_tiled (kivi_triton.py:505-556) and the residual logits, concat and
+ * 1/sqrt(D) scaling of packed_kivi_attention_parts (kivi_cuda.py:283-287).
+ * bits in {2,4,8}; 8 uses UniCache's uint8 layout (codes [Tq,Hkv,D],
+ * stats [Tq/G,Hkv,D] of stats_dtype).
+ */
+int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int64_t heads_q,
+               const void *key_code, const void *key_scale, const void *key_min, int stats_dtype,
+               int64_t quantized_tokens, int bits, int group_size,
+               const void *residual_key, int res_dtype, int64_t residual_tokens,
+               int64_t r_st, int64_t r_sh,
+               int64_t heads_kv, int64_t head_dim, float sm_scale,
+               float *logits, uc_stream_t stream);
+
+/*
+ * Probability-value product over a packed segment plus its residual:
+ *   out[hq, i, :] = sum_t probs[hq, i, t] * V[t, hq / group, :]
+ * probs [Hq, Lq, Tq+Tr] of p_dtype with strides (p_sh, p_si, p_st); out is
+ * [Hq, Lq, D] of out_dtype (contiguous); residual_value element (t, h, d) at
+ * r_st*t + r_sh*h + d.  `workspace` must hold
+ * uc_workspace_bytes(UC_OP_KIVI_AV, ...) bytes.  With quantized_tokens == 0
+ * this is gqa_probability_value (physical.py:42-63).
+ * Replaces: the KIVI GEMV AV (kivi_cuda.py:295-307), packed_av_tiled
+ * (kivi_triton.py:559-612) and the residual AV + sum (kivi_cuda.py:324-327).
+ */
+int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t p_si, int64_t p_st,
+               int64_t query_len, int64_t heads_q,
+               const void *value_code, const void *value_scale, const void *value_min, int stats_dtype,
+               int64_t quantized_tokens, int bits, int group_size,
+               const void *residual_value, int res_dtype, int64_t residual_tokens,
+               int64_t r_st, int64_t r_sh,
+               int64_t heads_kv, int64_t head_dim,
+               void *out, int out_dtype, void *workspace, uc_stream_t stream);
+
+/*
+ * One packed KIVI segment (native layout, contiguous) with its residual, and
+ * the query/outputs of one attention call over it.  Used by the decode entry
+ * points; a table of these lets one launch cover many sequences and layers.
+ */
+typedef struct uc_kivi_item {
+  const void *key_code;      /* int32 [Hkv, D, Tq*bits/32] */
+  const void *key_scale;     /* fp16  [Hkv, D, Tq/G] */
+  const void *key_min;
+  const void *value_code;    /* int32 [Hkv, Tq, D*bits/32] */
+  const void *value_scale;   /* fp16  [Hkv, Tq, D/G] */
+  const void *value_min;
+  const void *residual_key;  /* [Tr, Hkv, D] of res_dtype, may be NULL if Tr==0 */
+  const void *residual_value;
+  const void *query;         /* [Lq, Hq, D] of q_dtype */
+  void *out;                 /* [Lq, Hq, D] of out_dtype, normalised */
+  float *lse;                /* [Hq, Lq] natural-log LSE, may be NULL */
+  int64_t quantized_tokens;  /* Tq, a multiple of group_size */
+  int64_t residual_tokens;   /* Tr */
+} uc_kivi_item;
+
+/*
+ * Fused dequant attention for short queries (decode) over one packed segment
+ * plus residual: out = softmax(sm_scale * q K^T) V over all Tq+Tr keys, and
+ * lse = log sum_t exp(sm_scale * q.k_t).  Split-K over tokens; the splits are
+ * merged with a log-sum-exp combine.  group = Hq/Hkv query heads share one KV
+ * head; group*query_len <= 16.
+ * Replaces: the decode use of packed_kivi_attention_parts (kivi_cuda.py:238-329)
+ * followed by the caller's softmax and AV (adapters/bagel.py:1205-1297), and
+ * packed_kivi_quantized_attention_summary (kivi_cuda.py:96-120) for Lq small.
+ * `workspace` must hold uc_workspace_bytes(UC_OP_KIVI_DECODE, 1, ...) bytes.
+ */
+int uc_kivi_attn_decode(const uc_kivi_item *item_host, int bits, int group_size,
+                        int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t query_len,
+                        int q_dtype, int res_dtype, int out_dtype, float sm_scale,
+                        void *workspace, int64_t workspace_bytes, uc_stream_t stream);
+
+/*
+ * The same kernel over `n_items` segments (sequences x layers) in one launch.
+ * `items_device` is a device array of uc_kivi_item; every item shares bits,
+ * group, head counts and query_len; token counts may differ, up to
+ * max_quantized_tokens / max_residual_tokens.
+ * No reference counterpart: this is the all-layer decode launch.
+ */
+int uc_kivi_attn_decode_batch(const uc_kivi_item *items_device, int64_t n_items,
+                              int bits, int group_size,
+                              int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t query_len,
+                              int q_dtype, int res_dtype, int out_dtype, float sm_scale,
+                              int64_t max_quantized_tokens, int64_t max_residual_tokens,
+                              void *workspace, int64_t workspace_bytes, uc_stream_t stream);
+
+/*
+ * Merge normalised attention summaries of n_segments disjoint key segments:
+ *   lse = logsumexp_s lse_s;  out = sum_s out_s * exp(lse_s - lse)
+ * outs[s] are [Lq, Hq, D] of out_dtype (contiguous), lses[s] fp32 [Hq, Lq].
+ * `outs` and `lses` are HOST arrays of n_segments device pointers
+ * (n_segments <= 16).  out_lse may be NULL.
+ * Replaces: merge_attention_summaries (adapters/bagel.py:57-72).
+ */
+int uc_lse_merge(const void *const *outs, const float *const *lses, int n_segments,
+                 int out_dtype, int64_t query_len, int64_t heads_q, int64_t head_dim,
+                 void *out, float *out_lse, uc_stream_t stream);
+
+/*
+ * H2O per-KV-head attention mass received by each key:
+ *   P = bf16(softmax_t(sm_scale * q_i . k_t))   per query head and query row
+ *   scores[h, t] (+)= sum_{g < group} sum_i float(P[h*group+g, i, t])
+ * query [Lq, Hq, D], key [T, Hkv, D] (strides given), fp32 scores [Hkv, T]
+ * contiguous.  accumulate != 0 adds to the existing scores.
+ * `workspace` must hold uc_workspace_bytes(UC_OP_H2O_SCORES, ...) bytes.
+ * Replaces: the softmax + bf16 cast of adapters/bagel.py:1205-1243 followed
+ * by H2OPhysicalGQAOperator.update_after_attention (operators/physical.py:62-65),
+ * without materialising P in HBM.
+ */
+int uc_h2o_scores(const void *query, int64_t q_si, int64_t q_sh, int64_t q_sd,
+                  const void *key, int64_t k_st, int64_t k_sh, int64_t k_sd, int dtype,
+                  int64_t query_len, int64_t heads_q, int64_t tokens, int64_t heads_kv,
+                  int64_t head_dim, float sm_scale, int accumulate,
+                  float *scores, void *workspace, uc_stream_t stream);
+
+/*
+ * H2O column sums of given probabilities (no softmax):
+ *   out[h, t] (+)= sum_{g<group} sum_i float(probs[h*group+g, i, t])
+ * probs [Hq, Lq, T] of p_dtype with strides (p_sh, p_si, p_st).
+ * Replaces: GQAH2OCache.update_scores (physical.py:598-610) and the reduction of
+ * operators/physical.py:62-65 when P already exists.
+ */
+int uc_h2o_colsum(const void *probs, int p_dtype, int64_t p_sh, int64_t p_si, int64_t p_st,
+                  int64_t heads_q, int64_t query_len, int64_t tokens, int64_t heads_kv,
+                  int accumulate, float *out, uc_stream_t stream);
+
+/*
+ * H2O selection per KV head: the heavy_k highest scores among tokens
+ * [0, tokens - recent) (ties broken by lowest token index, NaN ranked
+ * highest), written in ascending token order, followed by the recent window
+ * tokens-recent .. tokens-1.  scores fp32 [Hkv, tokens] with strides
+ * (s_sh, s_st); indices int64 [Hkv, heavy_k + recent] contiguous.
+ * Replaces: torch.topk(...).indices.sort() + arange + cat of
+ * GQAH2OCache.from_dense / trim (physical.py:511-532, 624-649).
+ */
+int uc_h2o_select(const float *scores, int64_t s_sh, int64_t s_st,
+                  int64_t heads_kv, int64_t tokens, int64_t heavy_k, int64_t recent,
+                  int64_t *indices, uc_stream_t stream);
+
+/*
+ * GQA compaction gather: for each KV head h and slot j, r = indices[h, j]:
+ *   out_key[h, j, :] = key[r, h, :]      out_value likewise
+ *   out_ids[h, j]    = ids[r] (ids_sh == 0) or ids[h, r] (ids_sh != 0)
+ *   out_scores[h, j] = scores[h, r]
+ * key/value use (k_st, k_sh, k_sd) strides; out_key/out_value are contiguous
+ * [Hkv, R, D].  ids/out_ids/scores/out_scores may be NULL to skip them.
+ * Replaces: the torch.gather calls of GQAH2OCache.from_dense / trim
+ * (physical.py:533-546, 650-654).
+ */
+int uc_gqa_gather(const void *key, const void *value, int64_t k_st, int64_t k_sh, int64_t k_sd,
+                  int dtype, int64_t heads_kv, int64_t head_dim,
+                  const int64_t *indices, int64_t retained,
+                  const int64_t *ids, int64_t ids_sh, int64_t ids_st,
+                  const float *scores, int64_t s_sh, int64_t s_st,
+                  void *out_key, void *out_value, int64_t *out_ids, float *out_scores,
+                  uc_stream_t stream);
+
+/*
+ * Bytes of caller-provided workspace an operation needs.
+ *   UC_OP_KIVI_DECODE: (n_items, heads_q, query_len, head_dim, max_tokens)
+ *   UC_OP_KIVI_AV:     (1, heads_q, query_len, head_dim, total_tokens)
+ *   UC_OP_H2O_SCORES:  (1, heads_q, query_len, head_dim, tokens)
+ * max_tokens is Tq + Tr of the longest item.  Returns < 0 for an unknown op.
+ */
+int64_t uc_workspace_bytes(int op, int64_t n_items, int64_t heads_q, int64_t query_len,
+                           int64_t head_dim, int64_t max_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UNICACHE_HIP_H */

@@ -1,0 +1,73 @@
+"""The C-ABI library loads on a machine without a GPU and exports every
+entry point declared in include/unicache_hip.h; argument validation runs on
+the host before any launch."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from unicache_amd import _native as nat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "unicache_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(uc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_functions():
+    assert declared_functions() == nat.exported_symbols()
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nat.load_library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", nat.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (uc_[a-z0-9_]+)$", out, flags=re.M))
+    assert set(declared_functions()) <= exported
+
+
+def test_abi_version_and_error_state():
+    lib = nat.load_library()
+    assert lib.uc_abi_version() == nat.ABI_VERSION
+    rc = lib.uc_kivi_pack(None, 0, 0, 0, None, 0, 0, 0, nat.UC_BF16, 64, 4, 128, 3, 2, 32, nat.UC_FP16,
+                          None, 0, 0, 0, None, None, 0, 0, 0, None, 0, 0, 0, None, None, 0, 0, 0, None)
+    assert rc == nat.UC_EINVAL
+    assert b"2, 4, or 8" in lib.uc_last_error()
+    with pytest.raises(ValueError, match="group_size"):
+        nat.call("uc_kivi_pack", None, 0, 0, 0, None, 0, 0, 0, nat.UC_BF16, 64, 4, 128, 2, 2, 48, nat.UC_FP16,
+                 None, 0, 0, 0, None, None, 0, 0, 0, None, 0, 0, 0, None, None, 0, 0, 0, None)
+    with pytest.raises(ValueError, match="multiple of group_size"):
+        nat.call("uc_kivi_pack", None, 0, 0, 0, None, 0, 0, 0, nat.UC_BF16, 70, 4, 128, 2, 2, 32, nat.UC_FP16,
+                 None, 0, 0, 0, None, None, 0, 0, 0, None, 0, 0, 0, None, None, 0, 0, 0, None)
+
+
+def test_select_rejects_oversized_window():
+    with pytest.raises(ValueError, match="exceeds"):
+        nat.call("uc_h2o_select", None, 10, 1, 4, 10, 8, 3, None, None)
+
+
+def test_decode_validation():
+    item = nat.KiviItem()
+    item.quantized_tokens = 64
+    with pytest.raises(ValueError, match="<= 16"):
+        nat.call("uc_kivi_attn_decode", ctypes.byref(item), 2, 32, 28, 4, 128, 3, nat.UC_BF16, nat.UC_BF16,
+                 nat.UC_BF16, 0.1, None, 0, None)
+    with pytest.raises(ValueError, match="workspace"):
+        nat.call("uc_kivi_attn_decode", ctypes.byref(item), 2, 32, 28, 4, 128, 1, nat.UC_BF16, nat.UC_BF16,
+                 nat.UC_BF16, 0.1, None, 0, None)
+
+
+def test_workspace_bytes():
+    # decode: per (item, q head, row, split) D + 2 floats; splits = ceil(T/512) + 1
+    assert nat.workspace_bytes(nat.UC_OP_KIVI_DECODE, 2, 28, 1, 128, 8192) == 2 * 28 * 1 * 17 * 130 * 4
+    assert nat.workspace_bytes(nat.UC_OP_H2O_SCORES, 1, 28, 512, 128, 4096) == 28 * 512 * 2 * 4
+    with pytest.raises(ValueError):
+        nat.workspace_bytes(99, 1, 1, 1, 1, 1)

@@ -1,0 +1,157 @@
+"""GPU parity of the packed attention kernels against the oracle's fp32
+dequant path: max abs <= 2e-2, mean abs <= 1e-3 (outputs), LSE within 1e-3."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import kivi as K
+from tests.helpers import assert_close, f32, kv_pair, queries
+from unicache_amd import _native as nat
+from unicache_amd.adapters import merge_attention_summaries
+from unicache_amd.storage import PackedKIVICache, gqa_probability_value, gqa_query_key_logits
+from unicache_amd.storage.kivi_cuda import (
+    packed_kivi_attention_summary,
+    packed_kivi_quantized_attention_summary,
+)
+
+pytestmark = pytest.mark.gpu
+
+
+def check_summary(out, lse, seg, q, *, include_residual=True, what="summary"):
+    """Outputs within 2e-2 max / 1e-3 mean of the fp32 dequant path (the
+    contract) and of the bf16-dequant runtime path of UniCache; the natural
+    LSE within 2e-3 of the fp32 path."""
+
+    eo, el = A.packed_summary(seg, f32(q), include_residual=include_residual, kv_dtype="fp32")
+    assert_close(f32(out), eo, what=f"{what} out (fp32 path)")
+    assert_close(f32(lse), el, max_abs=2e-3, mean_abs=5e-4, what=f"{what} lse (fp32 path)")
+    bo, _ = A.packed_summary(seg, f32(q), include_residual=include_residual, kv_dtype="bf16")
+    assert_close(f32(out), bo, what=f"{what} out (bf16 path)")
+
+
+def _pair(tokens, seed, bits, group, residual, device, heads=4, head_dim=128):
+    key, value = kv_pair(tokens, heads=heads, head_dim=head_dim, seed=seed)
+    cache = PackedKIVICache.from_dense(key.to(device), value.to(device), logical_token_ids=torch.arange(tokens),
+                                       token_type_id=3, k_bits=bits, v_bits=bits, group_size=group,
+                                       residual_length=residual, backend="cuda")
+    seg = K.from_dense(f32(key), f32(value), k_bits=bits, v_bits=bits, group_size=group,
+                       residual_length=residual, native=bits != 8)
+    return cache, seg
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("lq", [1, 37])
+def test_attention_parts_qk_av(device, bits, lq):
+    cache, seg = _pair(320, 5, bits, 64, 32, device)
+    q = queries(lq, seed=7)
+    logits, apply_value = cache.attention_parts(q.to(device))
+    assert logits.dtype == torch.float32 and tuple(logits.shape) == (28, lq, 320)
+    exp_logits = A.packed_logits(seg, f32(q), kv_dtype="fp32")
+    assert_close(f32(logits), exp_logits, max_abs=2e-3, mean_abs=2e-4, what="logits")
+    probs = torch.softmax(logits, dim=-1).to(torch.bfloat16)
+    out = apply_value(probs)
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (28, lq, 128)
+    exp = A.packed_pv(seg, f32(probs), kv_dtype="bf16")
+    assert_close(f32(out), exp, what="av")
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_decode_summary_config0(device, bits):
+    # config 0: 2048 tokens (1920 packed + 128 residual), G=32, q [1, 28, 128]
+    cache, seg = _pair(2048, 0, bits, 32, 128, device)
+    q = queries(1, seed=1)
+    out, lse = packed_kivi_attention_summary(cache, q.to(device))
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (1, 28, 128) and tuple(lse.shape) == (28, 1)
+    check_summary(out, lse, seg, q, include_residual=True)
+    # the packed prefix alone (kivi_cuda.py:96-120)
+    po, pl = packed_kivi_quantized_attention_summary(cache, q.to(device))
+    check_summary(po, pl, seg, q, include_residual=False)
+
+
+def test_decode_summary_matches_parts_and_merge(device):
+    cache, seg = _pair(1536, 9, 2, 32, 128, device)
+    q = queries(1, seed=3).to(device)
+    out, lse = packed_kivi_attention_summary(cache, q)
+    logits, apply_value = cache.attention_parts(q)
+    probs = torch.softmax(logits, dim=-1)
+    ref = apply_value(probs.to(torch.bfloat16)).transpose(0, 1)
+    assert_close(f32(out), f32(ref), what="summary vs parts")
+    assert_close(f32(lse), f32(torch.logsumexp(logits, dim=-1)), max_abs=1e-3, mean_abs=1e-4, what="lse")
+
+
+def test_multi_query_summary(device):
+    cache, seg = _pair(1024, 4, 4, 32, 128, device)
+    q = queries(37, seed=5)
+    out, lse = packed_kivi_attention_summary(cache, q.to(device))
+    check_summary(out, lse, seg, q, what="mq")
+
+
+def test_batched_decode_items(device):
+    from unicache_amd.storage.decode import KiviDecodeBatch
+
+    caches, segs, qs = [], [], []
+    for i, tokens in enumerate((1000, 2048, 700)):
+        c, s = _pair(tokens, 30 + i, 2, 32, 128, device)
+        caches.append(c)
+        segs.append(s)
+        qs.append(queries(1, seed=40 + i))
+    batch = KiviDecodeBatch(caches, [q.to(device) for q in qs])
+    batch.run()
+    for i in range(3):
+        check_summary(batch.outputs[i], batch.lses[i], segs[i], qs[i], what=f"item {i}")
+
+
+def test_decode_is_deterministic(device):
+    cache, _ = _pair(4096, 11, 2, 32, 128, device)
+    q = queries(1, seed=2).to(device)
+    a = packed_kivi_attention_summary(cache, q)
+    b = packed_kivi_attention_summary(cache, q)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_gqa_helpers(device):
+    key, value = kv_pair(77, seed=8)
+    q = queries(5, seed=9)
+    logits = gqa_query_key_logits(q.to(device), key.to(device))
+    assert_close(f32(logits), A.gqa_logits(f32(q), f32(key)), max_abs=1e-3, mean_abs=1e-4, what="qk")
+    p = torch.softmax(logits / math.sqrt(128), dim=-1)
+    pv = gqa_probability_value(p, value.to(device))
+    assert pv.dtype == torch.bfloat16
+    assert_close(f32(pv), A.gqa_pv(f32(p), f32(value)), what="pv")
+
+
+def test_lse_merge(device):
+    # test_physical.py:181-202 on the GPU kernel
+    torch.manual_seed(11)
+    sa, sb = torch.randn(4, 3, 7), torch.randn(4, 3, 5)
+    va, vb = torch.randn(4, 7, 8), torch.randn(4, 5, 8)
+    summaries = [
+        (torch.matmul(torch.softmax(sa, -1), va).transpose(0, 1).to(device), torch.logsumexp(sa, -1).to(device)),
+        (torch.matmul(torch.softmax(sb, -1), vb).transpose(0, 1).to(device), torch.logsumexp(sb, -1).to(device)),
+    ]
+    out, lse = merge_attention_summaries(summaries)
+    allsc = torch.cat([sa, sb], -1)
+    expected = torch.matmul(torch.softmax(allsc, -1), torch.cat([va, vb], 1)).transpose(0, 1)
+    assert torch.allclose(out.cpu(), expected, atol=1e-5, rtol=1e-5)
+    assert torch.allclose(lse.cpu(), torch.logsumexp(allsc, -1), atol=1e-6)
+    eo, el = A.merge_summaries([(f32(o), f32(l)) for o, l in summaries])
+    assert np.allclose(f32(out), eo, atol=1e-6) and np.allclose(f32(lse), el, atol=1e-6)
+
+
+def test_summaries_merge_to_full_attention(device):
+    # packed+residual summary merged with a dense bf16 segment equals attention over all keys
+    cache, seg = _pair(1024, 12, 2, 32, 128, device)
+    dk, dv = kv_pair(256, seed=13)
+    q = queries(1, seed=14)
+    s1 = packed_kivi_attention_summary(cache, q.to(device))
+    logits = gqa_query_key_logits(q.to(device), dk.to(device)) / math.sqrt(128)
+    p = torch.softmax(logits, -1)
+    s2 = (gqa_probability_value(p, dv.to(device)).transpose(0, 1), torch.logsumexp(logits, -1))
+    out, _ = merge_attention_summaries([s1, s2])
+    key, value = K.dequantize(seg, "bf16")
+    eo, _ = A.attention_summary(f32(q), np.concatenate([key, f32(dk)]), np.concatenate([value, f32(dv)]))
+    assert_close(f32(out), eo, what="merged")

@@ -1,0 +1,158 @@
+"""GPU parity of KIVI pack / dequantize / fake quant: bit-exact with the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kivi as K
+from tests.helpers import f32, kv_pair
+from unicache_amd.operators import asymmetric_fake_quant, kivi_fake_quant_key, kivi_fake_quant_value
+from unicache_amd.storage import PackedKIVICache
+from unicache_amd.storage.kivi_cuda import dequantize_kivi_chunk, quantize_kivi_native
+
+pytestmark = pytest.mark.gpu
+
+
+def _cache(key, value, device, **kw):
+    t = key.shape[0]
+    return PackedKIVICache.from_dense(key.to(device), value.to(device), logical_token_ids=torch.arange(t),
+                                      token_type_id=3, backend="cuda", **kw)
+
+
+def _assert_cache_equal(cache, seg):
+    assert cache.quantized_tokens == seg.quantized_tokens
+    assert cache.kernel_native_layout == seg.native
+    for name in ("key_code", "value_code"):
+        got = getattr(cache, name).cpu().numpy()
+        exp = getattr(seg, name)
+        assert got.shape == exp.shape, name
+        assert np.array_equal(got.view(exp.dtype) if got.dtype != exp.dtype else got, exp), name
+    for name in ("key_scale", "key_minimum", "value_scale", "value_minimum"):
+        assert np.array_equal(f32(getattr(cache, name)), getattr(seg, name)), name
+    assert np.array_equal(f32(cache.residual_key), seg.residual_key)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_native_pack_bit_exact(device, bits, group):
+    # the shapes and seed of test_physical.py:984-1015
+    torch.manual_seed(19)
+    key = torch.randn(256, 4, 128, dtype=torch.bfloat16)
+    value = torch.randn(256, 4, 128, dtype=torch.bfloat16)
+    cache = _cache(key, value, device, k_bits=bits, v_bits=bits, group_size=group, residual_length=0)
+    seg = K.from_dense(f32(key), f32(value), k_bits=bits, v_bits=bits, group_size=group, residual_length=0)
+    _assert_cache_equal(cache, seg)
+
+
+def test_config0_pack_with_outliers_and_residual(device):
+    key, value = kv_pair(2048, seed=0)
+    cache = _cache(key, value, device, k_bits=2, v_bits=2, group_size=32, residual_length=128)
+    seg = K.from_dense(f32(key), f32(value), k_bits=2, v_bits=2, group_size=32, residual_length=128)
+    assert (cache.quantized_tokens, cache.residual_tokens) == (1920, 128)
+    assert tuple(cache.key_code.shape) == (4, 128, 120) and tuple(cache.value_code.shape) == (4, 1920, 8)
+    _assert_cache_equal(cache, seg)
+    # residual is a compact clone (test_physical.py:1070-1097)
+    assert cache.residual_key.untyped_storage().nbytes() == cache.residual_key.numel() * 2
+
+
+@pytest.mark.parametrize("kb,vb", [(4, 2), (2, 4), (8, 8), (8, 2)])
+def test_mixed_and_8bit_layouts(device, kb, vb):
+    key, value = kv_pair(192, heads=2, head_dim=64, seed=3)
+    cache = _cache(key, value, device, k_bits=kb, v_bits=vb, group_size=32, residual_length=40)
+    seg = K.from_dense(f32(key), f32(value), k_bits=kb, v_bits=vb, group_size=32, residual_length=40,
+                       native=True, in_dtype="bf16")
+    _assert_cache_equal(cache, seg)
+    rk, rv = cache.dequantize(torch.bfloat16)
+    ok, ov = K.dequantize(seg, "bf16")
+    assert np.array_equal(f32(rk), ok) and np.array_equal(f32(rv), ov)
+
+
+def test_fp16_and_strided_inputs(device):
+    key, value = kv_pair(128, seed=4, dtype=torch.float16)
+    seg = K.from_dense(f32(key), f32(value), k_bits=4, v_bits=4, group_size=64, residual_length=0)
+    _assert_cache_equal(_cache(key, value, device, k_bits=4, v_bits=4, group_size=64, residual_length=0), seg)
+    # channel stride 2 (scalar path) and a head-major view (token stride != H*D)
+    wide = torch.randn(128, 4, 256, dtype=torch.bfloat16)
+    k2 = wide[:, :, ::2]
+    v2 = torch.randn(4, 128, 128, dtype=torch.bfloat16).transpose(0, 1)
+    seg2 = K.from_dense(f32(k2), f32(v2), k_bits=2, v_bits=2, group_size=32, residual_length=0)
+    wide_d = wide.to(device)
+    v2_d = v2.to(device)  # preserve_format keeps the head-major strides
+    assert v2_d.stride() == v2.stride()
+    c2 = PackedKIVICache.from_dense(wide_d[:, :, ::2], v2_d, logical_token_ids=torch.arange(128), token_type_id=3,
+                                    k_bits=2, v_bits=2, group_size=32, residual_length=0, backend="cuda")
+    _assert_cache_equal(c2, seg2)
+
+
+def test_quantize_kivi_native_signature(device):
+    key, value = kv_pair(64, heads=2, head_dim=64, seed=6)
+    out = quantize_kivi_native(key.to(device), value.to(device), k_bits=2, v_bits=2, group_size=64)
+    shapes = [tuple(t.shape) for t in out]
+    # test_physical.py:1047-1053 (T=64 here: half the words)
+    assert shapes == [(2, 64, 4), (2, 64, 1), (2, 64, 1), (2, 64, 4), (2, 64, 1), (2, 64, 1)]
+    assert all(t.dtype == torch.float16 for t in out[1:3] + out[4:])
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_dequantize_bit_exact(device, bits):
+    key, value = kv_pair(384, seed=13)
+    cache = _cache(key, value, device, k_bits=bits, v_bits=bits, group_size=32, residual_length=100)
+    seg = K.from_dense(f32(key), f32(value), k_bits=bits, v_bits=bits, group_size=32, residual_length=100)
+    for dtype, name in ((torch.bfloat16, "bf16"), (torch.float16, "fp16"), (torch.float32, "fp32")):
+        rk, rv = cache.dequantize(dtype)
+        ok, ov = K.dequantize(seg, name)
+        assert np.array_equal(f32(rk), ok) and np.array_equal(f32(rv), ov), name
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_chunk_dequant_into_workspace(device, bits):
+    # test_physical.py:650-688
+    torch.manual_seed(13)
+    key = torch.randn(384, 4, 128, dtype=torch.bfloat16)
+    value = torch.randn_like(key)
+    cache = _cache(key, value, device, k_bits=bits, v_bits=bits, group_size=128, residual_length=0)
+    ek, ev = cache.dequantize(dtype=torch.bfloat16)
+    ak, av = dequantize_kivi_chunk(cache, start=128, stop=384, dtype=torch.bfloat16)
+    assert torch.equal(ak, ek[128:384]) and torch.equal(av, ev[128:384])
+    wk = torch.full((300, 4, 128), -7.0, device=device, dtype=torch.bfloat16)
+    wv = torch.full_like(wk, -9.0)
+    dk, dv = dequantize_kivi_chunk(cache, start=128, stop=384, dtype=torch.bfloat16, output_key=wk,
+                                   output_value=wv, output_offset=16)
+    assert torch.equal(dk, ek[128:384]) and torch.equal(dv, ev[128:384])
+    assert torch.all(wk[:16] == -7.0) and torch.all(wv[:16] == -9.0)
+    assert torch.all(wk[272:] == -7.0)
+    # unaligned start inside a word and a group
+    uk, uv = dequantize_kivi_chunk(cache, start=37, stop=301, dtype=torch.bfloat16)
+    assert torch.equal(uk, ek[37:301]) and torch.equal(uv, ev[37:301])
+    with pytest.raises(ValueError):
+        dequantize_kivi_chunk(cache, start=0, stop=384, dtype=torch.bfloat16, output_key=wk, output_value=wv)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+def test_fake_quant_bit_exact(device, bits):
+    key, value = kv_pair(200, seed=21)  # 200 tokens: a partial last key group
+    for fn, dim in ((kivi_fake_quant_key, 0), (kivi_fake_quant_value, 2)):
+        got = fn(key.to(device) if dim == 0 else value.to(device), bits=bits, group_size=32)
+        src = key if dim == 0 else value
+        exp = K.fake_quant(f32(src), bits=bits, dim=dim, group_size=32, out_dtype="bf16")
+        assert got.dtype == torch.bfloat16
+        assert np.array_equal(f32(got), exp), (bits, dim)
+    assert asymmetric_fake_quant(key.to(device), bits=16, dim=0, group_size=32) is not None
+
+
+def test_pack_is_deterministic(device):
+    key, value = kv_pair(512, seed=2)
+    a = _cache(key, value, device, k_bits=2, v_bits=2, group_size=32, residual_length=128)
+    b = _cache(key, value, device, k_bits=2, v_bits=2, group_size=32, residual_length=128)
+    assert torch.equal(a.key_code, b.key_code) and torch.equal(a.value_minimum, b.value_minimum)
+
+
+def test_repack_monotonic(device):
+    # test_physical.py:1099-1132
+    key, value = kv_pair(256, heads=2, head_dim=64, seed=1)
+    cache = _cache(key, value, device, k_bits=4, v_bits=4, group_size=32, residual_length=32)
+    assert cache.repack_monotonic(bits=2, group_size=64)
+    assert cache.k_bits == 2 and cache.group_size == 64
+    assert not cache.repack_monotonic(bits=4, group_size=64)
+    assert cache.budget_shortfall_events == 1
+    assert cache.resident_bytes < cache.full_precision_bytes

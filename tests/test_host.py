@@ -1,0 +1,79 @@
+"""Host-side behaviour of the drop-in API that needs no GPU: dispatch rules,
+budget arithmetic and the fail-closed error contract (no CPU fallback)."""
+
+import pytest
+import torch
+
+from oracle import h2o as H
+from unicache_amd.core.decisions import PhysicalCacheRequest
+from unicache_amd.operators import KIVIPackedQuantizationOperator, H2OPhysicalGQAOperator
+from unicache_amd.storage import GQAH2OCache, PackedKIVICache
+from unicache_amd.storage import kivi_cuda
+from unicache_amd.storage.tensor_backend import h2o_budget
+
+
+def test_kernel_backend_selection(monkeypatch):
+    # kivi_cuda.py:26-34, test_physical.py:505-508
+    monkeypatch.delenv("UNICACHE_KIVI_MULTI_QUERY_BACKEND", raising=False)
+    assert kivi_cuda.select_kivi_kernel_backend(1) == "official_gemv"
+    assert kivi_cuda.select_kivi_kernel_backend(2) == "triton_tiled"
+    assert kivi_cuda.select_kivi_kernel_backend(802) == "triton_tiled"
+    monkeypatch.setenv("UNICACHE_KIVI_MULTI_QUERY_BACKEND", "official_gemv")
+    assert kivi_cuda.select_kivi_kernel_backend(802) == "official_gemv"
+    monkeypatch.setenv("UNICACHE_KIVI_MULTI_QUERY_BACKEND", "bogus")
+    with pytest.raises(ValueError):
+        kivi_cuda.select_kivi_kernel_backend(1)
+
+
+@pytest.mark.parametrize("n", [12, 256, 3840, 4096, 8192, 10, 1])
+def test_budget_matches_oracle(n):
+    for params in ({"target_budget_ratio": 0.2, "recent_budget_fraction": 0.25},
+                   {"target_budget_ratio": 0.5}, {"budget": 7, "recent_size": 3}, {"keep_k": 5}):
+        assert h2o_budget(n, params) == H.budget(n, params)
+
+
+def test_cpu_tensors_fail_closed():
+    key = torch.randn(64, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3, k_bits=2,
+                                   v_bits=2, group_size=32, residual_length=0, backend="cuda")
+    with pytest.raises(RuntimeError, match="reference"):
+        PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3, k_bits=2,
+                                   v_bits=2, group_size=32, residual_length=0, backend="reference")
+    with pytest.raises(RuntimeError):
+        GQAH2OCache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=1,
+                               per_kv_head_scores=torch.rand(4, 64), target_tokens=8, recent_tokens=2)
+
+
+def test_argument_errors_are_value_errors():
+    key = torch.randn(64, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        PackedKIVICache.from_dense(key, key[:, :2], logical_token_ids=torch.arange(64), token_type_id=3,
+                                   k_bits=2, v_bits=2, group_size=32, residual_length=0)
+    with pytest.raises(ValueError):
+        PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3,
+                                   k_bits=3, v_bits=2, group_size=32, residual_length=0)
+    with pytest.raises(ValueError):
+        PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3,
+                                   k_bits=2, v_bits=2, group_size=48, residual_length=0)
+    with pytest.raises(ValueError):
+        GQAH2OCache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=1,
+                               per_kv_head_scores=torch.rand(3, 64), target_tokens=8, recent_tokens=2)
+
+
+def test_operator_params_and_requests():
+    op = KIVIPackedQuantizationOperator()
+    params = op.build_params({"bits": 2, "group_size": 32, "residual_length": 128})
+    assert params["k_bits"] == 2 and params["backend"] == "cuda" and params["residual_length"] == 128
+    with pytest.raises(ValueError):
+        op.build_params({"bits": 3})
+    h2o = H2OPhysicalGQAOperator()
+    assert h2o.build_params({})["target_budget_ratio"] == 0.2
+    with pytest.raises(ValueError):
+        h2o.build_params({"target_budget_ratio": 0.0})
+    mask = torch.ones(5, dtype=torch.bool)
+    with pytest.raises(ValueError):
+        PhysicalCacheRequest(operator="x", segment_id="s", token_count=4, segment_mask=mask)
+    with pytest.raises(ValueError):
+        PhysicalCacheRequest(operator="x", segment_id="s", token_count=5, segment_mask=mask,
+                             per_kv_head_scores=torch.zeros(2, 4))

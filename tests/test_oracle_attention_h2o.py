@@ -1,0 +1,148 @@
+"""Pins oracle.attention and oracle.h2o.
+
+Known answers come from UniCache's tests (test_physical.py:181-202 LSE merge,
+1195-1215 H2O per-head selection, 1217-1270 budget counts); the rest are
+closed forms (LSE of the logits, GQA == repeated-KV attention computed by
+torch) and a brute-force selection by Python's sort.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import h2o as H
+
+
+def test_lse_merge_equals_global_softmax():
+    # test_physical.py:181-202
+    rng = np.random.default_rng(11)
+    sa, sb = rng.standard_normal((4, 3, 7)), rng.standard_normal((4, 3, 5))
+    va, vb = rng.standard_normal((4, 7, 8)), rng.standard_normal((4, 5, 8))
+    summaries = [
+        ((A.softmax(sa) @ va).transpose(1, 0, 2), A.logsumexp(sa)),
+        ((A.softmax(sb) @ vb).transpose(1, 0, 2), A.logsumexp(sb)),
+    ]
+    out, lse = A.merge_summaries(summaries)
+    allv = np.concatenate([va, vb], axis=1)
+    alls = np.concatenate([sa, sb], axis=-1)
+    expected = (A.softmax(alls) @ allv).transpose(1, 0, 2)
+    assert np.allclose(out, expected, atol=1e-5)
+    assert np.allclose(lse, A.logsumexp(alls), atol=1e-6)
+
+
+def test_gqa_matches_repeated_kv_torch():
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((5, 28, 16)).astype(np.float32)
+    k = rng.standard_normal((9, 4, 16)).astype(np.float32)
+    v = rng.standard_normal((9, 4, 16)).astype(np.float32)
+    logits = A.gqa_logits(q, k)
+    kt = torch.from_numpy(k).double().repeat_interleave(7, dim=1)
+    ref = torch.matmul(torch.from_numpy(q).double().transpose(0, 1), kt.transpose(0, 1).transpose(-1, -2))
+    assert np.allclose(logits, ref.numpy(), atol=1e-10)
+    p = A.softmax(logits)
+    pv = A.gqa_pv(p, v)
+    vt = torch.from_numpy(v).double().repeat_interleave(7, dim=1)
+    ref_pv = torch.matmul(torch.from_numpy(p), vt.transpose(0, 1))
+    assert np.allclose(pv, ref_pv.numpy(), atol=1e-10)
+
+
+def test_attention_summary_closed_forms():
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((3, 14, 32))
+    k = rng.standard_normal((50, 2, 32))
+    v = rng.standard_normal((50, 2, 32))
+    out, lse = A.attention_summary(q, k, v)
+    logits = A.gqa_logits(q, k) / math.sqrt(32)
+    ref_lse = np.log(np.exp(logits).sum(-1))
+    assert np.allclose(lse, ref_lse, atol=1e-10)
+    # constant values -> the output is that constant whatever the weights
+    out_c, _ = A.attention_summary(q, k, np.full_like(v, 2.5))
+    assert np.allclose(out_c, 2.5)
+    assert out.shape == (3, 14, 32)
+
+
+# --------------------------------------------------------------------- H2O --
+def test_h2o_known_answer_per_kv_head():
+    # test_physical.py:1195-1215
+    key = np.arange(8 * 2 * 4, dtype=np.float32).reshape(8, 2, 4)
+    scores = np.array([[9, 8, 5, 4, 3, 2, 0, 0], [0, 8, 1, 1, 1, 9, 0, 0]], dtype=np.float32)
+    ok, ov, ids, sc, heavy, recent = H.from_dense(key, key + 1000, np.arange(8), scores, 4, 2)
+    assert ids[0].tolist() == [0, 1, 6, 7]
+    assert ids[1].tolist() == [1, 5, 6, 7]
+    assert (heavy, recent) == (2, 2)
+    assert np.array_equal(ok[1, 1], key[5, 1]) and np.array_equal(ov[0, 2], key[6, 0] + 1000)
+    assert sc[1].tolist() == [8.0, 9.0, 0.0, 0.0]
+
+
+@pytest.mark.parametrize(
+    "n,ratio,target,recent",
+    [
+        (256, 0.2, 51, 13),    # config 3 instruction
+        (3840, 0.2, 768, 192),  # config 3 ViT
+        (4096, 0.2, 819, 205),  # config 4 instruction
+        (8192, 0.2, 1638, 410),  # config 4 ViT: round(409.5) == 410 (half to even)
+        (12, 0.5, 6, 2),        # test_physical.py:1217-1270 (round(1.5) == 2)
+        (10, 0.25, 2, 0),       # round(2.5) == 2, round(0.5) == 0
+    ],
+)
+def test_h2o_budget_round_half_even(n, ratio, target, recent):
+    assert H.budget(n, {"target_budget_ratio": ratio, "recent_budget_fraction": 0.25}) == (target, recent)
+
+
+def test_h2o_budget_clamps():
+    # physical.py:511-515
+    assert H.clamp_budget(10, 50, 3) == (7, 3, 7)
+    assert H.clamp_budget(10, 0, 0) == (1, 0, 1)
+    assert H.clamp_budget(10, 4, 9) == (0, 4, 0)
+
+
+def test_select_brute_force_with_ties():
+    rng = np.random.default_rng(9)
+    for trial in range(50):
+        t = int(rng.integers(1, 60))
+        recent = int(rng.integers(0, t))
+        k = int(rng.integers(0, t - recent + 1))
+        s = rng.integers(0, 5, size=(3, t)).astype(np.float32)  # many ties
+        got = H.select(s, k, recent)
+        for h in range(3):
+            order = sorted(range(t - recent), key=lambda i: (-float(s[h, i]), i))
+            assert got[h, :k].tolist() == sorted(order[:k])
+            assert got[h, k:].tolist() == list(range(t - recent, t))
+
+
+def test_select_nan_ranks_highest():
+    s = np.array([[1.0, np.nan, 5.0, np.inf, 2.0]], dtype=np.float32)
+    assert H.select(s, 2, 0)[0].tolist() == [1, 3]
+    assert H.select(s, 1, 0)[0].tolist() == [1]
+
+
+def test_scores_from_probs_order_of_sums():
+    # operators/physical.py:62-65: query sum per head, then group sum
+    rng = np.random.default_rng(5)
+    p = rng.random((28, 3, 11)).astype(np.float32)
+    s = H.scores_from_probs(p, 4)
+    ref = np.array([[p[h * 7 + g, :, t].sum() for t in range(11)] for h in range(4) for g in range(7)])
+    ref = ref.reshape(4, 7, 11).sum(1)
+    assert np.allclose(s, ref, rtol=1e-6)
+
+
+def test_scores_from_qk_rows_sum_to_query_count():
+    # every softmax row sums to 1, so sum_t scores[h, t] ~= group * Lq (bf16 rounding aside)
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((6, 28, 32)).astype(np.float32)
+    k = rng.standard_normal((40, 4, 32)).astype(np.float32)
+    s = H.scores_from_qk(q, k)
+    assert s.shape == (4, 40)
+    assert np.allclose(s.sum(1), 7 * 6, rtol=2e-2)
+
+
+def test_trim_reselects_within_retained():
+    key = np.arange(2 * 6 * 3, dtype=np.float32).reshape(2, 6, 3)
+    ids = np.array([[10, 11, 12, 13, 14, 15], [20, 21, 22, 23, 24, 25]])
+    sc = np.array([[5, 1, 4, 0, 0, 0], [0, 9, 9, 1, 0, 0]], dtype=np.float32)
+    k2, _, i2, s2 = H.trim(key, key, ids, sc, 3, 1)
+    assert i2.tolist() == [[10, 12, 15], [21, 22, 25]]
+    assert s2.tolist() == [[5, 4, 0], [9, 9, 0]]

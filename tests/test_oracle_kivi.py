@@ -1,0 +1,200 @@
+"""Pins oracle.kivi (the CPU restatement of UniCache's KIVI arithmetic).
+
+Each check is a closed form, a hand-computed known answer, a shape/golden
+value from UniCache's own tests, or an invariant linking two independently
+written reference functions; none re-types the oracle's formula.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import kivi as K
+
+
+# ------------------------------------------------------------ bit layout --
+def test_pack_layout_closed_form_2bit():
+    # codes 0..3 repeated: word = sum_j code_j << 2j, LSB first (physical.py:81-84)
+    codes = np.array([[0, 1, 2, 3] * 4], dtype=np.uint8)  # one word of 16 codes
+    word = K.pack_codes(codes, 2, dim=1)
+    expected = sum(c << (2 * j) for j, c in enumerate([0, 1, 2, 3] * 4))
+    assert word.shape == (1, 1)
+    assert int(word.view(np.uint32)[0, 0]) == expected == 0xE4E4E4E4
+
+
+def test_pack_sign_wrap_top_slot():
+    # a 3 in slot 15 sets bit 31: the int32 word is negative (physical.py:81-84)
+    codes = np.zeros((16,), dtype=np.uint8)
+    codes[15] = 3
+    word = K.pack_codes(codes, 2, dim=0)
+    assert word.dtype == np.int32 and int(word[0]) == -(1 << 30)
+    assert int(word.view(np.uint32)[0]) == 0xC0000000
+
+
+def test_pack_4bit_and_padding():
+    codes = np.array([15, 0, 7, 1, 2], dtype=np.uint8)  # 5 codes -> padded to 8
+    word = K.pack_codes(codes, 4, dim=0)
+    assert word.shape == (1,)
+    assert int(word.view(np.uint32)[0]) == 0xF | (0 << 4) | (7 << 8) | (1 << 12) | (2 << 16)
+    back = K.unpack_codes(word, 4, dim=0, length=5)
+    assert back.tolist() == [15, 0, 7, 1, 2]
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_pack_round_trip_brute_force(bits):
+    rng = np.random.default_rng(3)
+    codes = rng.integers(0, 1 << bits, size=(3, 37, 5), dtype=np.uint8)
+    for dim in range(3):
+        packed = K.pack_codes(codes, bits, dim)
+        assert np.array_equal(K.unpack_codes(packed, bits, dim, codes.shape[dim]), codes)
+        # every code sits at bit (index % per_word) * bits of word index // per_word
+        per = 32 // bits
+        flat = np.moveaxis(codes, dim, -1)
+        words = np.moveaxis(packed.view(np.uint32), dim, -1)
+        for idx in [(0, 0, 0), (2, 36, 4), (1, 17, 3)]:
+            pos = idx[dim]
+            other = tuple(i for d, i in enumerate(idx) if d != dim)
+            w = int(words[other + (pos // per,)])
+            assert (w >> ((pos % per) * bits)) & ((1 << bits) - 1) == int(flat[other + (pos,)])
+
+
+# ----------------------------------------------------------- known answers --
+def q(values, bits):
+    codes, scale, mn = K.quantize_codes(np.array(values, dtype=np.float32)[:, None], bits=bits, group_dim=0,
+                                        group_size=len(values))
+    return codes[:, 0].tolist(), float(scale[0, 0]), float(mn[0, 0])
+
+
+def test_quantize_ramp_is_identity():
+    assert q([0.0, 1.0, 2.0, 3.0], 2) == ([0, 1, 2, 3], 1.0, 0.0)
+    codes, scale, mn = q([float(i) for i in range(16)], 4)
+    assert codes == list(range(16)) and scale == 1.0 and mn == 0.0
+
+
+def test_quantize_constant_group():
+    codes, scale, mn = q([1.5] * 8, 2)
+    assert codes == [0] * 8 and scale == float(np.finfo(np.float32).eps) and mn == 1.5
+
+
+def test_quantize_round_half_even():
+    # scale 1: (x - mn) = 0.5 -> 0 and 1.5 -> 2 under round-half-even (torch.round)
+    codes, scale, _ = q([0.0, 0.5, 1.5, 2.5, 3.0], 2)
+    assert scale == 1.0 and codes == [0, 0, 2, 2, 3]
+
+
+def test_quantize_single_max_hits_top_code():
+    codes, _, _ = q([-2.0, -2.0, -2.0, 7.25], 4)
+    assert codes == [0, 0, 0, 15]
+
+
+def test_quantize_partial_last_group():
+    data = np.arange(10, dtype=np.float32)[:, None]
+    codes, scale, mn = K.quantize_codes(data, bits=2, group_dim=0, group_size=4)
+    # groups [0..3], [4..7], [8, 9]
+    assert scale.shape == (3, 1) and mn[:, 0].tolist() == [0.0, 4.0, 8.0]
+    assert float(scale[2, 0]) == np.float32(1.0) / np.float32(3.0)
+    assert codes[:, 0].tolist() == [0, 1, 2, 3, 0, 1, 2, 3, 0, 3]
+
+
+# --------------------------------------------------------------- invariants --
+def test_dequant_error_within_half_step():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((64, 4, 32)).astype(np.float32)
+    for bits in (2, 4, 8):
+        codes, scale, mn = K.quantize_codes(x, bits=bits, group_dim=0, group_size=32)
+        s = np.repeat(scale, 32, axis=0)
+        m = np.repeat(mn, 32, axis=0)
+        recon = codes.astype(np.float32) * s + m
+        assert np.all(np.abs(recon - x) <= s * 0.5 * (1 + 1e-5))
+
+
+def test_fake_quant_agrees_with_packed_codes():
+    # operators/builtin.py:31-53 computes scale as max(mx-mn, eps)/max; physical.py:129
+    # as max((mx-mn)/max, eps).  For non-degenerate groups both give the same codes,
+    # so fake quant equals code*scale+min of the packing quantizer.
+    rng = np.random.default_rng(11)
+    x = K.round_bf16(rng.standard_normal((96, 2, 64)).astype(np.float32) * 3)
+    for bits in (2, 4):
+        for dim, gs in ((0, 32), (2, 16)):
+            fq = K.fake_quant(x, bits=bits, dim=dim, group_size=gs, out_dtype="fp32")
+            codes, scale, mn = K.quantize_codes(x, bits=bits, group_dim=dim, group_size=gs)
+            s = np.repeat(scale, gs, axis=dim)
+            m = np.repeat(mn, gs, axis=dim)
+            assert np.array_equal(fq, (codes.astype(np.float32) * s).astype(np.float32) + m)
+
+
+def test_bf16_rounding_known_values():
+    vals = np.array([1.0, 1.00390625, 1.005859375, 1.0078125, -0.0, np.inf, 3.0e38], dtype=np.float32)
+    out = K.round_bf16(vals)
+    # 1 + 2^-8 is a tie -> even (1.0); 1 + 1.5*2^-8 rounds up to 1 + 2^-7
+    assert out[:4].tolist() == [1.0, 1.0, 1.0078125, 1.0078125]
+    assert out[4] == 0.0 and np.signbit(out[4]) and out[5] == np.inf
+    assert out[6] == np.float32(3.0040553e38)  # 0x7F61B1E6 -> 0x7F62 (low half > 0x8000)
+    assert np.isnan(K.round_bf16(np.array([np.nan], dtype=np.float32)))[0]
+
+
+# ------------------------------------------------------- layouts and split --
+def test_residual_split_reference_cases():
+    # test_physical.py:1070-1097: 320 tokens, G=128, R=32 -> 256 packed + 64 residual
+    assert K.split_tokens(320, 128, 32) == (256, 64)
+    assert K.split_tokens(96, 32, 16) == (64, 32)          # test_physical.py:959-982
+    assert K.split_tokens(2048, 32, 128) == (1920, 128)    # config 0
+    assert K.split_tokens(8192, 32, 128) == (8064, 128)    # config 1
+    assert K.split_tokens(1024, 32, 128) == (896, 128)     # config 2
+    assert K.split_tokens(1024, 128, 32) == (896, 128)     # engine preset on config 2
+    assert K.split_tokens(20352, 32, 128) == (20224, 128)  # config 4
+    assert K.split_tokens(10, 32, 4) == (0, 10)
+
+
+def test_native_layout_shapes_from_reference_test():
+    # test_physical.py:1047-1053: T=128, Hkv=2, D=64, G=64, 2-bit
+    rng = np.random.default_rng(6)
+    key = K.round_bf16(rng.standard_normal((128, 2, 64)).astype(np.float32))
+    seg = K.from_dense(key, key, k_bits=2, v_bits=2, group_size=64, residual_length=0)
+    assert seg.native
+    assert seg.key_code.shape == (2, 64, 8)
+    assert seg.key_scale.shape == (2, 64, 2)
+    assert seg.value_code.shape == (2, 128, 4)
+    assert seg.value_scale.shape == (2, 128, 1)
+    assert np.array_equal(seg.key_scale, K.round_f16(seg.key_scale))
+
+
+def test_native_and_reference_layouts_hold_the_same_codes():
+    rng = np.random.default_rng(5)
+    key = K.round_bf16(rng.standard_normal((96, 4, 64)).astype(np.float32))
+    value = K.round_bf16(rng.standard_normal((96, 4, 64)).astype(np.float32))
+    nat = K.from_dense(key, value, k_bits=4, v_bits=2, group_size=32, residual_length=0, native=True)
+    ref = K.from_dense(key, value, k_bits=4, v_bits=2, group_size=32, residual_length=0, native=False)
+    assert np.array_equal(np.transpose(nat.key_code, (2, 0, 1)), ref.key_code)
+    assert np.array_equal(np.transpose(nat.value_code, (1, 0, 2)), ref.value_code)
+    k1, v1 = K.dequantize(nat, "fp32")
+    k2, v2 = K.dequantize(ref, "fp32")
+    # stats differ only by their storage rounding (fp16 vs bf16)
+    assert np.allclose(k1, k2, atol=0.05) and np.allclose(v1, v2, atol=0.05)
+
+
+def test_round_trip_keeps_residual_exact():
+    # test_physical.py:959-982
+    rng = np.random.default_rng(0)
+    key = K.round_bf16(rng.standard_normal((96, 4, 128)).astype(np.float32))
+    value = K.round_bf16(rng.standard_normal((96, 4, 128)).astype(np.float32))
+    for bits in (2, 4, 8):
+        seg = K.from_dense(key, value, k_bits=bits, v_bits=bits, group_size=32, residual_length=16,
+                           native=bits != 8)
+        rk, rv = K.dequantize(seg, "bf16")
+        assert rk.shape == key.shape
+        assert np.array_equal(rk[-32:], key[-32:]) and np.array_equal(rv[-32:], value[-32:])
+        assert seg.quantized_tokens % 32 == 0
+        assert float(np.abs(rk - key).mean()) > 0
+
+
+def test_rounding_matches_torch_casts():
+    # independent implementation: torch's Float->BFloat16 / Float->Half casts
+    import torch
+
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(100000) * np.exp(rng.uniform(-30, 30, 100000))).astype(np.float32)
+    x[:4] = [np.inf, -np.inf, 0.0, -0.0]
+    tb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    th = torch.from_numpy(x).to(torch.float16).float().numpy()
+    assert np.array_equal(K.round_bf16(x), tb)
+    assert np.array_equal(K.round_f16(x), th)

@@ -1,0 +1,204 @@
+"""ctypes binding of libunicache_hip.so (the C ABI in include/unicache_hip.h).
+
+The library is loaded lazily on first use, after ``torch`` so that it binds to
+the HIP runtime torch already loaded.  A missing or incompatible library
+raises ``RuntimeError``: the engine has no CPU or torch fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libunicache_hip.so")
+ABI_VERSION = 1
+
+UC_BF16, UC_FP16, UC_FP32 = 0, 1, 2
+UC_OK, UC_EINVAL, UC_ERUNTIME = 0, -1, -2
+UC_OP_KIVI_DECODE, UC_OP_KIVI_AV, UC_OP_H2O_SCORES = 1, 2, 3
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+
+
+class KiviItem(ctypes.Structure):
+    """Mirror of ``uc_kivi_item``."""
+
+    _fields_ = [
+        ("key_code", _P),
+        ("key_scale", _P),
+        ("key_min", _P),
+        ("value_code", _P),
+        ("value_scale", _P),
+        ("value_min", _P),
+        ("residual_key", _P),
+        ("residual_value", _P),
+        ("query", _P),
+        ("out", _P),
+        ("lse", _P),
+        ("quantized_tokens", _L),
+        ("residual_tokens", _L),
+    ]
+
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "uc_abi_version": (_I, []),
+    "uc_last_error": (ctypes.c_char_p, []),
+    "uc_kivi_pack": (
+        _I,
+        [_P, _L, _L, _L, _P, _L, _L, _L, _I, _L, _L, _L, _I, _I, _I, _I,
+         _P, _L, _L, _L, _P, _P, _L, _L, _L,
+         _P, _L, _L, _L, _P, _P, _L, _L, _L, _P],
+    ),
+    "uc_kivi_dequant": (
+        _I,
+        [_P, _L, _L, _L, _P, _P, _L, _L, _L,
+         _P, _L, _L, _L, _P, _P, _L, _L, _L,
+         _I, _L, _L, _I, _I, _I, _L, _L, _P, _P, _I, _L, _L, _L, _L, _P],
+    ),
+    "uc_kivi_fake_quant": (_I, [_P, _L, _L, _L, _I, _L, _L, _L, _I, _I, _I, _P, _P]),
+    "uc_kivi_qk": (
+        _I,
+        [_P, _I, _L, _L, _P, _P, _P, _I, _L, _I, _I, _P, _I, _L, _L, _L, _L, _L, _F, _P, _P],
+    ),
+    "uc_kivi_av": (
+        _I,
+        [_P, _I, _L, _L, _L, _L, _L, _P, _P, _P, _I, _L, _I, _I, _P, _I, _L, _L, _L, _L, _L,
+         _P, _I, _P, _P],
+    ),
+    "uc_kivi_attn_decode": (
+        _I,
+        [ctypes.POINTER(KiviItem), _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _P, _L, _P],
+    ),
+    "uc_kivi_attn_decode_batch": (
+        _I,
+        [_P, _L, _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _L, _L, _P, _L, _P],
+    ),
+    "uc_lse_merge": (_I, [_P, _P, _I, _I, _L, _L, _L, _P, _P, _P]),
+    "uc_h2o_scores": (
+        _I,
+        [_P, _L, _L, _L, _P, _L, _L, _L, _I, _L, _L, _L, _L, _L, _F, _I, _P, _P, _P],
+    ),
+    "uc_h2o_colsum": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _L, _I, _P, _P]),
+    "uc_h2o_select": (_I, [_P, _L, _L, _L, _L, _L, _L, _P, _P]),
+    "uc_gqa_gather": (
+        _I,
+        [_P, _P, _L, _L, _L, _I, _L, _L, _P, _L, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _P],
+    ),
+    "uc_workspace_bytes": (_L, [_I, _L, _L, _L, _L, _L]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def exported_symbols() -> list[str]:
+    """Names of the C entry points this binding expects the library to export."""
+
+    return sorted(_SIGNATURES)
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the HIP library (without touching the GPU) and declare signatures."""
+
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise RuntimeError(
+                "libunicache_hip.so is not built; run `python -m unicache_amd.build` "
+                "(the MI355X engine has no CPU fallback)"
+            )
+        try:
+            lib = ctypes.CDLL(path)
+        except OSError as exc:
+            raise RuntimeError(f"Cannot load {path}: {exc}") from exc
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            try:
+                fn = getattr(lib, name)
+            except AttributeError as exc:
+                raise RuntimeError(f"{path} does not export {name}") from exc
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.uc_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(
+                f"libunicache_hip.so ABI version {version} != expected {ABI_VERSION}; rebuild it"
+            )
+        _lib = lib
+        return lib
+
+
+def lib() -> ctypes.CDLL:
+    return _lib if _lib is not None else load_library()
+
+
+def check(rc: int, name: str) -> None:
+    """Map a C return code to the reference's exception types."""
+
+    if rc == UC_OK:
+        return
+    message = (lib().uc_last_error() or b"").decode(errors="replace") or f"{name} failed"
+    if rc == UC_EINVAL:
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+_DTYPE_CODES = {torch.bfloat16: UC_BF16, torch.float16: UC_FP16, torch.float32: UC_FP32}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError as exc:
+        raise ValueError(f"Unsupported dtype for the MI355X kernels: {dtype}") from exc
+
+
+def ptr(tensor: torch.Tensor | None) -> int | None:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(*tensors: torch.Tensor | None, what: str) -> torch.device:
+    """All given tensors must live on one GPU; returns that device."""
+
+    device = None
+    for tensor in tensors:
+        if tensor is None:
+            continue
+        if tensor.device.type != "cuda":
+            raise RuntimeError(f"{what} requires GPU tensors (got {tensor.device})")
+        if device is None:
+            device = tensor.device
+        elif tensor.device != device:
+            raise RuntimeError(f"{what} received tensors on different devices")
+    if device is None:
+        raise RuntimeError(f"{what} received no GPU tensor")
+    return device
+
+
+def workspace_bytes(op: int, n_items: int, heads_q: int, query_len: int, head_dim: int, max_tokens: int) -> int:
+    size = int(lib().uc_workspace_bytes(op, n_items, heads_q, query_len, head_dim, max_tokens))
+    if size < 0:
+        raise ValueError("uc_workspace_bytes: unknown operation")
+    return size
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A caller-owned uint8 workspace from torch's caching allocator."""
+
+    return torch.empty(max(1, int(nbytes)), dtype=torch.uint8, device=device)

@@ -1,0 +1,54 @@
+// Error state, version and workspace sizing of the C ABI.
+#include "uc_common.h"
+#include "uc_decode.h"
+
+namespace uc {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int check_launch(const char *what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("%s: kernel launch failed: %s", what, hipGetErrorString(err));
+    return UC_ERUNTIME;
+  }
+  clear_error();
+  return UC_OK;
+}
+
+}  // namespace uc
+
+extern "C" int uc_abi_version(void) { return UC_ABI_VERSION; }
+
+extern "C" const char *uc_last_error(void) { return uc::g_last_error.c_str(); }
+
+extern "C" int64_t uc_workspace_bytes(int op, int64_t n_items, int64_t heads_q, int64_t query_len,
+                                      int64_t head_dim, int64_t max_tokens) {
+  if (n_items < 0 || heads_q < 0 || query_len < 0 || head_dim < 0 || max_tokens < 0) return -1;
+  switch (op) {
+    case UC_OP_KIVI_DECODE:
+    case UC_OP_KIVI_AV: {
+      int64_t splits = uc::decode_num_splits(max_tokens);
+      // per (item, query head, query row, split): D partial outputs + (max, sum)
+      return n_items * heads_q * query_len * splits * (head_dim + 2) * int64_t(sizeof(float));
+    }
+    case UC_OP_H2O_SCORES:
+      // per (query head, row): running max and sum of the softmax
+      return heads_q * query_len * 2 * int64_t(sizeof(float));
+    default:
+      return -1;
+  }
+}

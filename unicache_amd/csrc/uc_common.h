@@ -1,0 +1,177 @@
+// Shared helpers for the gfx950 kernels of libunicache_hip.so: element
+// conversions with explicit rounding, error reporting for the C ABI, and
+// wavefront reductions.  Every kernel in this library is written for CDNA4
+// (64-lane wavefronts).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/unicache_hip.h"
+
+namespace uc {
+
+constexpr int kWave = 64;
+constexpr float kEps = 1.1920928955078125e-07f;  // FLT_EPSILON == torch.finfo(float32).eps
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------- errors --
+void set_error(const char *fmt, ...);
+void clear_error();
+int check_launch(const char *what);
+
+#define UC_REQUIRE(cond, ...)                 \
+  do {                                        \
+    if (!(cond)) {                            \
+      ::uc::set_error(__VA_ARGS__);           \
+      return UC_EINVAL;                       \
+    }                                         \
+  } while (0)
+
+#define UC_REQUIRE_RT(cond, ...)              \
+  do {                                        \
+    if (!(cond)) {                            \
+      ::uc::set_error(__VA_ARGS__);           \
+      return UC_ERUNTIME;                     \
+    }                                         \
+  } while (0)
+
+inline hipStream_t as_stream(uc_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool valid_dtype(int d) { return d == UC_BF16 || d == UC_FP16 || d == UC_FP32; }
+inline bool half_dtype(int d) { return d == UC_BF16 || d == UC_FP16; }
+
+// ------------------------------------------------------------ conversions --
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+// Round-to-nearest-even float -> bfloat16 with canonical NaN, the rounding of
+// torch's Float->BFloat16 cast.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  _Float16 h = __builtin_bit_cast(_Float16, b);
+  return static_cast<float>(h);
+}
+
+// v_cvt_f16_f32 rounds to nearest even, like torch's Float->Half cast.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// Load element `i` of a buffer of dtype D as float.
+template <int D>
+__device__ __forceinline__ float load_as_f32(const void *p, int64_t i) {
+  if constexpr (D == UC_BF16) {
+    return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  } else if constexpr (D == UC_FP16) {
+    return f16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  } else {
+    return static_cast<const float *>(p)[i];
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void store_from_f32(void *p, int64_t i, float v) {
+  if constexpr (D == UC_BF16) {
+    static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(v);
+  } else if constexpr (D == UC_FP16) {
+    static_cast<uint16_t *>(p)[i] = f32_to_f16_bits(v);
+  } else {
+    static_cast<float *>(p)[i] = v;
+  }
+}
+
+// Element `i` of a buffer whose dtype is only known at run time (uniform
+// branch; used by the kernels that are not on the hot path).
+__device__ __forceinline__ float load_dyn(const void *p, int64_t i, int dt) {
+  if (dt == UC_BF16) return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  if (dt == UC_FP16) return f16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  return static_cast<const float *>(p)[i];
+}
+
+__device__ __forceinline__ void store_dyn(void *p, int64_t i, float v, int dt) {
+  if (dt == UC_BF16) {
+    static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(v);
+  } else if (dt == UC_FP16) {
+    static_cast<uint16_t *>(p)[i] = f32_to_f16_bits(v);
+  } else {
+    static_cast<float *>(p)[i] = v;
+  }
+}
+
+// Value of a 16-bit element (bf16 or fp16) already in a register.
+template <int D>
+__device__ __forceinline__ float half_bits_to_f32(uint32_t b) {
+  if constexpr (D == UC_BF16) {
+    return bf16_bits_to_f32(b & 0xffffu);
+  } else {
+    return f16_bits_to_f32(static_cast<uint16_t>(b & 0xffffu));
+  }
+}
+
+// Exact IEEE single-rounding arithmetic (never contracted into an FMA).
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
+
+// Code `pos_in_word` of the word at `word_off` (2/4-bit, LSB first), or the
+// byte at `word_off` for 8-bit codes (physical.py:88-104).
+template <int BITS>
+__device__ __forceinline__ uint32_t read_code(const void *code, int64_t word_off, int64_t pos_in_word) {
+  if constexpr (BITS == 8) {
+    return static_cast<const uint8_t *>(code)[word_off];
+  } else {
+    const uint32_t w = static_cast<const uint32_t *>(code)[word_off];
+    return (w >> (pos_in_word * BITS)) & ((1u << BITS) - 1u);
+  }
+}
+
+// ------------------------------------------------------------ reductions --
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Dispatch a runtime dtype code to a template parameter.
+#define UC_DISPATCH_DTYPE(code, NAME, ...)                  \
+  [&] {                                                     \
+    switch (code) {                                         \
+      case UC_BF16: { constexpr int NAME = UC_BF16; return __VA_ARGS__(); } \
+      case UC_FP16: { constexpr int NAME = UC_FP16; return __VA_ARGS__(); } \
+      default: { constexpr int NAME = UC_FP32; return __VA_ARGS__(); }      \
+    }                                                       \
+  }()
+
+#define UC_DISPATCH_BITS(code, NAME, ...)                   \
+  [&] {                                                     \
+    switch (code) {                                         \
+      case 2: { constexpr int NAME = 2; return __VA_ARGS__(); } \
+      case 4: { constexpr int NAME = 4; return __VA_ARGS__(); } \
+      default: { constexpr int NAME = 8; return __VA_ARGS__(); } \
+    }                                                       \
+  }()
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace uc

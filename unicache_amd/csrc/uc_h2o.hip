@@ -1,0 +1,392 @@
+// H2O attention-mass accumulation, deterministic top-k selection and the GQA
+// compaction gather (operators/physical.py:51-101; physical.py:493-654).
+#include "uc_common.h"
+
+namespace uc {
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr int kRows = 16;
+constexpr int kTile = 64;
+constexpr int kThreads = 256;
+constexpr int kMaxD = 256;
+
+// ----------------------------------------------------------------- scores --
+struct ScoreArgs {
+  const void *q;
+  int64_t q_si, q_sh, q_sd;
+  const void *k;
+  int64_t k_st, k_sh, k_sd;
+  int64_t Lq, Hq, T, Hkv, D, group, rows;
+  float scale;  // sm_scale
+  float *stats; // [Hq, Lq, 2]: row max and sum of exp(x - max)
+  float *scores;
+  int accumulate;
+};
+
+struct ScoreShared {
+  float q[kRows][kMaxD];
+  float red[4][kRows][kTile];
+  float col[4][kTile];
+};
+
+template <int DT>
+__device__ void load_rows(ScoreShared &s, const ScoreArgs &a, int64_t h, int64_t row0) {
+  for (int64_t idx = threadIdx.x; idx < kRows * a.D; idx += kThreads) {
+    const int64_t r = idx / a.D, d = idx % a.D;
+    float v = 0.0f;
+    if (row0 + r < a.rows) {
+      const int64_t g = (row0 + r) / a.Lq, i = (row0 + r) % a.Lq;
+      v = load_as_f32<DT>(a.q, i * a.q_si + (h * a.group + g) * a.q_sh + d * a.q_sd);
+    }
+    s.q[r][d] = v;
+  }
+}
+
+// red[wave][r][lane] = partial q_r . k_t over the wave's quarter of channels
+template <int DT>
+__device__ void logits_tile(ScoreShared &s, const ScoreArgs &a, int64_t h, int64_t t) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  float acc[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+  if (t < a.T) {
+    const int64_t dq = (a.D + 3) / 4, d0 = wave * dq, d1 = min(a.D, d0 + dq);
+    for (int64_t d = d0; d < d1; ++d) {
+      const float k = load_as_f32<DT>(a.k, t * a.k_st + h * a.k_sh + d * a.k_sd);
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) acc[r] = fmaf(s.q[r][d], k, acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) s.red[wave][r][lane] = acc[r];
+}
+
+// Pass 1: per (KV head, 16-row chunk), the softmax max and denominator of each
+// query row over all T keys.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void score_stats_kernel(ScoreArgs a) {
+  __shared__ ScoreShared s;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int64_t h = blockIdx.y, row0 = int64_t(blockIdx.x) * kRows;
+  load_rows<DT>(s, a, h, row0);
+  __syncthreads();
+  float m[4], l[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    m[j] = kNegInf;
+    l[j] = 0.0f;
+  }
+  for (int64_t t0 = 0; t0 < a.T; t0 += kTile) {
+    const int64_t t = t0 + lane;
+    logits_tile<DT>(s, a, h, t);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = wave + 4 * j;
+      float x = kNegInf;
+      if (t < a.T) x = (s.red[0][r][lane] + s.red[1][r][lane] + s.red[2][r][lane] + s.red[3][r][lane]) * a.scale;
+      const float mn = fmaxf(m[j], wave_max(x));
+      const float e = (x == kNegInf) ? 0.0f : expf(x - mn);
+      l[j] = l[j] * ((m[j] == kNegInf) ? 0.0f : expf(m[j] - mn)) + wave_sum(e);
+      m[j] = mn;
+    }
+    __syncthreads();
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t rr = row0 + wave + 4 * j;
+      if (rr >= a.rows) continue;
+      const int64_t g = rr / a.Lq, i = rr % a.Lq, hq = h * a.group + g;
+      a.stats[(hq * a.Lq + i) * 2 + 0] = m[j];
+      a.stats[(hq * a.Lq + i) * 2 + 1] = l[j];
+    }
+  }
+}
+
+// Pass 2: per (KV head, 64-key tile), recompute the logits of every query row
+// of the head, form p = bf16(exp(x - max) / sum) and sum p over rows in a
+// fixed order (deterministic).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void score_colsum_kernel(ScoreArgs a) {
+  __shared__ ScoreShared s;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int64_t h = blockIdx.y, t0 = int64_t(blockIdx.x) * kTile, t = t0 + lane;
+  float col = 0.0f;
+  for (int64_t row0 = 0; row0 < a.rows; row0 += kRows) {
+    load_rows<DT>(s, a, h, row0);
+    __syncthreads();
+    logits_tile<DT>(s, a, h, t);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = wave + 4 * j;
+      const int64_t rr = row0 + r;
+      if (rr >= a.rows || t >= a.T) continue;
+      const int64_t g = rr / a.Lq, i = rr % a.Lq, hq = h * a.group + g;
+      const float mx = a.stats[(hq * a.Lq + i) * 2 + 0];
+      const float sum = a.stats[(hq * a.Lq + i) * 2 + 1];
+      const float x = (s.red[0][r][lane] + s.red[1][r][lane] + s.red[2][r][lane] + s.red[3][r][lane]) * a.scale;
+      const float pr = expf(x - mx) * (1.0f / sum);
+      col += bf16_bits_to_f32(f32_to_bf16_bits(pr));
+    }
+    __syncthreads();
+  }
+  s.col[wave][lane] = col;
+  __syncthreads();
+  if (wave == 0 && t < a.T) {
+    const float total = s.col[0][lane] + s.col[1][lane] + s.col[2][lane] + s.col[3][lane];
+    float *dst = a.scores + h * a.T + t;
+    *dst = a.accumulate ? *dst + total : total;
+  }
+}
+
+// ------------------------------------------------------------------ colsum --
+struct ColsumArgs {
+  const void *p;
+  int64_t p_sh, p_si, p_st;
+  int64_t Hq, Lq, T, Hkv, group;
+  int accumulate;
+  float *out;
+};
+
+// out[h, t] (+)= sum over (g, i) of probs[h*group+g, i, t]: the query sum of
+// each query head first, then the sum over the group (physical.py:607-609).
+template <int PD>
+__global__ __launch_bounds__(256) void colsum_kernel(ColsumArgs a) {
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= a.Hkv * a.T) return;
+  const int64_t h = idx / a.T, t = idx % a.T;
+  float total = 0.0f;
+  for (int64_t g = 0; g < a.group; ++g) {
+    float s = 0.0f;
+    const int64_t base = (h * a.group + g) * a.p_sh + t * a.p_st;
+    for (int64_t i = 0; i < a.Lq; ++i) s += load_as_f32<PD>(a.p, base + i * a.p_si);
+    total += s;
+  }
+  a.out[idx] = a.accumulate ? a.out[idx] + total : total;
+}
+
+// ------------------------------------------------------------------ select --
+constexpr int kSelThreads = 1024;
+
+// Order-preserving map of fp32 to uint32 (larger float -> larger key); NaN is
+// canonicalised to the largest key, matching torch.topk's NaN-is-largest.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+struct SelectArgs {
+  const float *scores;
+  int64_t s_sh, s_st;
+  int64_t T, heavy_k, recent;
+  int64_t *indices;
+};
+
+// One workgroup per KV head.  A four-pass 8-bit radix select finds the key of
+// the heavy_k-th largest score; tokens strictly above it are all kept and
+// equal ones are taken in ascending index order until heavy_k are chosen.
+// An ordered block scan writes the kept indices in ascending order.
+__global__ __launch_bounds__(kSelThreads) void h2o_select_kernel(SelectArgs a) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t sh_prefix, sh_need;
+  __shared__ uint32_t wave_tot[2][kSelThreads / kWave];
+  const int64_t h = blockIdx.x;
+  const int64_t hist_end = a.T - a.recent;
+  const float *sc = a.scores + h * a.s_sh;
+  int64_t *out = a.indices + h * (a.heavy_k + a.recent);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+
+  if (a.heavy_k > 0) {
+    uint32_t prefix = 0, mask = 0;
+    uint32_t need = static_cast<uint32_t>(a.heavy_k);
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 24 - 8 * pass;
+      if (tid < 256) hist[tid] = 0;
+      __syncthreads();
+      for (int64_t t = tid; t < hist_end; t += kSelThreads) {
+        const uint32_t key = order_key(sc[t * a.s_st]);
+        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t above = 0;
+        int b = 255;
+        for (; b > 0; --b) {
+          if (above + hist[b] >= need) break;
+          above += hist[b];
+        }
+        sh_prefix = prefix | (uint32_t(b) << shift);
+        sh_need = need - above;
+      }
+      __syncthreads();
+      prefix = sh_prefix;
+      need = sh_need;
+      mask |= 255u << shift;
+      __syncthreads();
+    }
+    // prefix is the threshold key; `need` tokens equal to it are kept.
+    uint32_t base_sel = 0, base_eq = 0;
+    for (int64_t c0 = 0; c0 < hist_end; c0 += kSelThreads) {
+      const int64_t t = c0 + tid;
+      uint32_t key = 0;
+      if (t < hist_end) key = order_key(sc[t * a.s_st]);
+      const bool eq = t < hist_end && key == prefix;
+      const bool gt = t < hist_end && key > prefix;
+      // exclusive scan of eq, then of selection
+      const uint64_t eq_ball = __ballot(eq);
+      const uint32_t eq_before_lane = __popcll(eq_ball & ((1ull << lane) - 1ull));
+      if (lane == 0) wave_tot[0][wave] = __popcll(eq_ball);
+      __syncthreads();
+      uint32_t eq_before = base_eq + eq_before_lane;
+      for (int w = 0; w < wave; ++w) eq_before += wave_tot[0][w];
+      const bool sel = gt || (eq && eq_before < need);
+      const uint64_t sel_ball = __ballot(sel);
+      const uint32_t sel_before_lane = __popcll(sel_ball & ((1ull << lane) - 1ull));
+      if (lane == 0) wave_tot[1][wave] = __popcll(sel_ball);
+      __syncthreads();
+      uint32_t sel_before = base_sel + sel_before_lane;
+      for (int w = 0; w < wave; ++w) sel_before += wave_tot[1][w];
+      if (sel) out[sel_before] = t;
+      uint32_t tot_eq = 0, tot_sel = 0;
+      for (int w = 0; w < kSelThreads / kWave; ++w) {
+        tot_eq += wave_tot[0][w];
+        tot_sel += wave_tot[1][w];
+      }
+      base_eq += tot_eq;
+      base_sel += tot_sel;
+      __syncthreads();
+    }
+  }
+  for (int64_t j = tid; j < a.recent; j += kSelThreads) out[a.heavy_k + j] = hist_end + j;
+}
+
+// ------------------------------------------------------------------ gather --
+struct GatherArgs {
+  const void *key, *value;
+  int64_t k_st, k_sh, k_sd;
+  int64_t Hkv, D, R;
+  const int64_t *idx;
+  const int64_t *ids;
+  int64_t ids_sh, ids_st;
+  const float *scores;
+  int64_t s_sh, s_st;
+  void *okey, *ovalue;
+  int64_t *oids;
+  float *oscores;
+};
+
+template <typename E>
+__global__ __launch_bounds__(256) void gqa_gather_kernel(GatherArgs a) {
+  // one thread per output element of [Hkv, R, D]
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= a.Hkv * a.R * a.D) return;
+  const int64_t d = idx % a.D, j = (idx / a.D) % a.R, h = idx / (a.D * a.R);
+  const int64_t r = a.idx[h * a.R + j];
+  const int64_t src = r * a.k_st + h * a.k_sh + d * a.k_sd;
+  static_cast<E *>(a.okey)[idx] = static_cast<const E *>(a.key)[src];
+  static_cast<E *>(a.ovalue)[idx] = static_cast<const E *>(a.value)[src];
+  if (d == 0) {
+    if (a.oids) a.oids[h * a.R + j] = a.ids[h * a.ids_sh + r * a.ids_st];
+    if (a.oscores) a.oscores[h * a.R + j] = a.scores[h * a.s_sh + r * a.s_st];
+  }
+}
+
+}  // namespace
+}  // namespace uc
+
+using namespace uc;
+
+extern "C" int uc_h2o_scores(const void *query, int64_t q_si, int64_t q_sh, int64_t q_sd,
+                             const void *key, int64_t k_st, int64_t k_sh, int64_t k_sd, int dtype,
+                             int64_t query_len, int64_t heads_q, int64_t tokens, int64_t heads_kv,
+                             int64_t head_dim, float sm_scale, int accumulate,
+                             float *scores, void *workspace, uc_stream_t stream) {
+  UC_REQUIRE(valid_dtype(dtype), "uc_h2o_scores: unknown dtype code");
+  UC_REQUIRE(heads_q > 0 && heads_kv > 0 && heads_q % heads_kv == 0,
+             "BAGEL query heads must be divisible by KV heads");
+  UC_REQUIRE(head_dim > 0 && head_dim <= kMaxD, "uc_h2o_scores: head_dim must be <= %d", kMaxD);
+  UC_REQUIRE(query_len >= 0 && tokens >= 0, "uc_h2o_scores: bad shape");
+  UC_REQUIRE(workspace != nullptr || query_len == 0, "uc_h2o_scores: workspace is NULL");
+  hipStream_t s = as_stream(stream);
+  if (tokens == 0) return UC_OK;
+  if (query_len == 0) {
+    if (!accumulate)
+      UC_REQUIRE_RT(hipMemsetAsync(scores, 0, heads_kv * tokens * sizeof(float), s) == hipSuccess,
+                    "uc_h2o_scores: memset failed");
+    return UC_OK;
+  }
+  ScoreArgs a{};
+  a.q = query; a.q_si = q_si; a.q_sh = q_sh; a.q_sd = q_sd;
+  a.k = key; a.k_st = k_st; a.k_sh = k_sh; a.k_sd = k_sd;
+  a.Lq = query_len; a.Hq = heads_q; a.T = tokens; a.Hkv = heads_kv; a.D = head_dim;
+  a.group = heads_q / heads_kv; a.rows = a.group * query_len; a.scale = sm_scale;
+  a.stats = static_cast<float *>(workspace); a.scores = scores; a.accumulate = accumulate;
+  UC_DISPATCH_DTYPE(dtype, DT, [&] {
+    hipLaunchKernelGGL((score_stats_kernel<DT>), dim3(ceil_div(a.rows, kRows), heads_kv), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((score_colsum_kernel<DT>), dim3(ceil_div(tokens, kTile), heads_kv), dim3(kThreads), 0, s, a);
+  });
+  return check_launch("uc_h2o_scores");
+}
+
+extern "C" int uc_h2o_colsum(const void *probs, int p_dtype, int64_t p_sh, int64_t p_si, int64_t p_st,
+                             int64_t heads_q, int64_t query_len, int64_t tokens, int64_t heads_kv,
+                             int accumulate, float *out, uc_stream_t stream) {
+  UC_REQUIRE(valid_dtype(p_dtype), "uc_h2o_colsum: unknown dtype code");
+  UC_REQUIRE(heads_q > 0 && heads_kv > 0 && heads_q % heads_kv == 0,
+             "Query heads must be divisible by KV heads for GQA H2O");
+  UC_REQUIRE(query_len >= 0 && tokens >= 0, "uc_h2o_colsum: bad shape");
+  if (tokens == 0) return UC_OK;
+  ColsumArgs a{};
+  a.p = probs; a.p_sh = p_sh; a.p_si = p_si; a.p_st = p_st;
+  a.Hq = heads_q; a.Lq = query_len; a.T = tokens; a.Hkv = heads_kv; a.group = heads_q / heads_kv;
+  a.accumulate = accumulate; a.out = out;
+  hipStream_t s = as_stream(stream);
+  UC_DISPATCH_DTYPE(p_dtype, PD, [&] {
+    hipLaunchKernelGGL((colsum_kernel<PD>), dim3(ceil_div(heads_kv * tokens, 256)), dim3(256), 0, s, a);
+  });
+  return check_launch("uc_h2o_colsum");
+}
+
+extern "C" int uc_h2o_select(const float *scores, int64_t s_sh, int64_t s_st, int64_t heads_kv, int64_t tokens,
+                             int64_t heavy_k, int64_t recent, int64_t *indices, uc_stream_t stream) {
+  UC_REQUIRE(heads_kv >= 0 && tokens >= 0 && heavy_k >= 0 && recent >= 0, "uc_h2o_select: negative size");
+  UC_REQUIRE(recent <= tokens && heavy_k <= tokens - recent,
+             "uc_h2o_select: heavy_k + recent exceeds the token count");
+  UC_REQUIRE(tokens < (int64_t(1) << 31), "uc_h2o_select: too many tokens");
+  if (heads_kv == 0 || heavy_k + recent == 0) return UC_OK;
+  SelectArgs a{};
+  a.scores = scores; a.s_sh = s_sh; a.s_st = s_st; a.T = tokens; a.heavy_k = heavy_k; a.recent = recent;
+  a.indices = indices;
+  hipLaunchKernelGGL(h2o_select_kernel, dim3(heads_kv), dim3(kSelThreads), 0, as_stream(stream), a);
+  return check_launch("uc_h2o_select");
+}
+
+extern "C" int uc_gqa_gather(const void *key, const void *value, int64_t k_st, int64_t k_sh, int64_t k_sd,
+                             int dtype, int64_t heads_kv, int64_t head_dim,
+                             const int64_t *indices, int64_t retained,
+                             const int64_t *ids, int64_t ids_sh, int64_t ids_st,
+                             const float *scores, int64_t s_sh, int64_t s_st,
+                             void *out_key, void *out_value, int64_t *out_ids, float *out_scores,
+                             uc_stream_t stream) {
+  UC_REQUIRE(valid_dtype(dtype), "uc_gqa_gather: unknown dtype code");
+  UC_REQUIRE(heads_kv >= 0 && head_dim > 0 && retained >= 0, "uc_gqa_gather: bad shape");
+  UC_REQUIRE((ids == nullptr) == (out_ids == nullptr), "uc_gqa_gather: ids and out_ids go together");
+  UC_REQUIRE((scores == nullptr) == (out_scores == nullptr), "uc_gqa_gather: scores and out_scores go together");
+  if (heads_kv == 0 || retained == 0) return UC_OK;
+  GatherArgs a{};
+  a.key = key; a.value = value; a.k_st = k_st; a.k_sh = k_sh; a.k_sd = k_sd;
+  a.Hkv = heads_kv; a.D = head_dim; a.R = retained; a.idx = indices;
+  a.ids = ids; a.ids_sh = ids_sh; a.ids_st = ids_st; a.scores = scores; a.s_sh = s_sh; a.s_st = s_st;
+  a.okey = out_key; a.ovalue = out_value; a.oids = out_ids; a.oscores = out_scores;
+  const int64_t blocks = ceil_div(heads_kv * retained * head_dim, 256);
+  hipStream_t s = as_stream(stream);
+  if (dtype == UC_FP32)
+    hipLaunchKernelGGL((gqa_gather_kernel<float>), dim3(blocks), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((gqa_gather_kernel<uint16_t>), dim3(blocks), dim3(256), 0, s, a);
+  return check_launch("uc_gqa_gather");
+}

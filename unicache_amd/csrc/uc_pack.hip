@@ -1,0 +1,503 @@
+// KIVI quantize/pack, dequantize and fake-quant kernels (HBM-bound byte work).
+//
+// Bit-exactness contract (physical.py:160-175, 190-201; builtin.py:42-53):
+// every value is widened to fp32; min/max are exact; the subtraction,
+// division (IEEE correctly rounded, the HIP default) and round-half-even
+// (v_rndne_f32) happen once each, in the same order as the torch code, and
+// dequantisation is a rounded multiply followed by a rounded add (never an
+// FMA: the library is built with -ffp-contract=off and these use __f*_rn).
+#include "uc_common.h"
+
+#include <type_traits>
+
+namespace uc {
+namespace {
+
+// ----------------------------------------------------------------- keys --
+// One lane owns a channel pair (c, c+1) of one head and quantizes one token
+// group per iteration: keys are grouped along tokens, so the min/max
+// reduction stays inside the lane and a wave reads whole 256-byte head rows.
+template <int IN, int BITS, int G, bool VEC>
+__device__ void pack_key_group(const void *__restrict__ key, int64_t st, int64_t sh, int64_t sd,
+                               int64_t h, int64_t c, int64_t g, int64_t head_dim,
+                               void *__restrict__ code, int64_t kc_sh, int64_t kc_sd, int64_t kc_sw,
+                               void *__restrict__ kscale, void *__restrict__ kmin, int stats_dtype,
+                               int64_t ks_sh, int64_t ks_sd, int64_t ks_sg) {
+  constexpr float kMaxCode = float((1 << BITS) - 1);
+  const bool has1 = (c + 1) < head_dim;
+  float x0[G], x1[G];
+  const int64_t t0 = g * G;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int64_t off = (t0 + i) * st + h * sh + c * sd;
+    if constexpr (VEC) {
+      const uint32_t pair = *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(key) + off);
+      x0[i] = half_bits_to_f32<IN>(pair);
+      x1[i] = half_bits_to_f32<IN>(pair >> 16);
+    } else {
+      x0[i] = load_as_f32<IN>(key, off);
+      x1[i] = has1 ? load_as_f32<IN>(key, off + sd) : 0.0f;
+    }
+  }
+  float mn0 = x0[0], mx0 = x0[0], mn1 = x1[0], mx1 = x1[0];
+#pragma unroll
+  for (int i = 1; i < G; ++i) {
+    mn0 = fminf(mn0, x0[i]);
+    mx0 = fmaxf(mx0, x0[i]);
+    mn1 = fminf(mn1, x1[i]);
+    mx1 = fmaxf(mx1, x1[i]);
+  }
+  const float s0 = fmaxf(div_rn(sub_rn(mx0, mn0), kMaxCode), kEps);
+  const float s1 = fmaxf(div_rn(sub_rn(mx1, mn1), kMaxCode), kEps);
+
+  if constexpr (BITS == 8) {
+    uint8_t *out = static_cast<uint8_t *>(code);
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const float q0 = fminf(fmaxf(rintf(div_rn(sub_rn(x0[i], mn0), s0)), 0.0f), kMaxCode);
+      out[h * kc_sh + c * kc_sd + (t0 + i) * kc_sw] = static_cast<uint8_t>(q0);
+      if (has1) {
+        const float q1 = fminf(fmaxf(rintf(div_rn(sub_rn(x1[i], mn1), s1)), 0.0f), kMaxCode);
+        out[h * kc_sh + (c + 1) * kc_sd + (t0 + i) * kc_sw] = static_cast<uint8_t>(q1);
+      }
+    }
+  } else {
+    constexpr int kPerWord = 32 / BITS;
+    constexpr int kWords = G / kPerWord;
+    int32_t *out = static_cast<int32_t *>(code);
+#pragma unroll
+    for (int w = 0; w < kWords; ++w) {
+      uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+      for (int j = 0; j < kPerWord; ++j) {
+        const int i = w * kPerWord + j;
+        const uint32_t q0 = static_cast<uint32_t>(
+            fminf(fmaxf(rintf(div_rn(sub_rn(x0[i], mn0), s0)), 0.0f), kMaxCode));
+        const uint32_t q1 = static_cast<uint32_t>(
+            fminf(fmaxf(rintf(div_rn(sub_rn(x1[i], mn1), s1)), 0.0f), kMaxCode));
+        w0 |= q0 << (j * BITS);
+        w1 |= q1 << (j * BITS);
+      }
+      const int64_t wi = g * kWords + w;
+      out[h * kc_sh + c * kc_sd + wi * kc_sw] = static_cast<int32_t>(w0);
+      if (has1) out[h * kc_sh + (c + 1) * kc_sd + wi * kc_sw] = static_cast<int32_t>(w1);
+    }
+  }
+  const int64_t so0 = h * ks_sh + c * ks_sd + g * ks_sg;
+  const int64_t so1 = so0 + ks_sd;
+  if (stats_dtype == UC_FP16) {
+    store_from_f32<UC_FP16>(kscale, so0, s0);
+    store_from_f32<UC_FP16>(kmin, so0, mn0);
+    if (has1) {
+      store_from_f32<UC_FP16>(kscale, so1, s1);
+      store_from_f32<UC_FP16>(kmin, so1, mn1);
+    }
+  } else if (stats_dtype == UC_BF16) {
+    store_from_f32<UC_BF16>(kscale, so0, s0);
+    store_from_f32<UC_BF16>(kmin, so0, mn0);
+    if (has1) {
+      store_from_f32<UC_BF16>(kscale, so1, s1);
+      store_from_f32<UC_BF16>(kmin, so1, mn1);
+    }
+  } else {
+    store_from_f32<UC_FP32>(kscale, so0, s0);
+    store_from_f32<UC_FP32>(kmin, so0, mn0);
+    if (has1) {
+      store_from_f32<UC_FP32>(kscale, so1, s1);
+      store_from_f32<UC_FP32>(kmin, so1, mn1);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- values --
+// One lane owns 16 consecutive channels of one (head, token); a value group
+// of G channels spans G/16 neighbouring lanes, reduced with shuffles.  The 16
+// codes of a lane form exactly one 2-bit word / two 4-bit words.
+template <int IN, int BITS, int G, bool VEC>
+__device__ void pack_value_chunk(const void *__restrict__ value, int64_t st, int64_t sh, int64_t sd,
+                                 int64_t h, int64_t t, int64_t chunk, bool active,
+                                 void *__restrict__ code, int64_t vc_sh, int64_t vc_st, int64_t vc_sw,
+                                 void *__restrict__ vscale, void *__restrict__ vmin, int stats_dtype,
+                                 int64_t vs_sh, int64_t vs_st, int64_t vs_sg) {
+  constexpr float kMaxCode = float((1 << BITS) - 1);
+  constexpr int kLanesPerGroup = G / 16;
+  float x[16];
+  if (active) {
+    const int64_t base = t * st + h * sh + chunk * 16 * sd;
+    if constexpr (VEC) {
+      const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(value) + base);
+      const uint4 a = p[0], b = p[1];
+      const uint32_t words[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        x[2 * i] = half_bits_to_f32<IN>(words[i]);
+        x[2 * i + 1] = half_bits_to_f32<IN>(words[i] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = load_as_f32<IN>(value, base + i * sd);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = 0.0f;
+  }
+  float mn = x[0], mx = x[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    mn = fminf(mn, x[i]);
+    mx = fmaxf(mx, x[i]);
+  }
+#pragma unroll
+  for (int o = 1; o < kLanesPerGroup; o <<= 1) {
+    mn = fminf(mn, __shfl_xor(mn, o, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  }
+  if (!active) return;
+  const float s = fmaxf(div_rn(sub_rn(mx, mn), kMaxCode), kEps);
+  uint32_t q[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    q[i] = static_cast<uint32_t>(fminf(fmaxf(rintf(div_rn(sub_rn(x[i], mn), s)), 0.0f), kMaxCode));
+
+  if constexpr (BITS == 8) {
+    uint8_t *out = static_cast<uint8_t *>(code);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) out[h * vc_sh + t * vc_st + (chunk * 16 + i) * vc_sw] = static_cast<uint8_t>(q[i]);
+  } else {
+    constexpr int kPerWord = 32 / BITS;
+    constexpr int kWords = 16 / kPerWord;
+    int32_t *out = static_cast<int32_t *>(code);
+#pragma unroll
+    for (int w = 0; w < kWords; ++w) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int j = 0; j < kPerWord; ++j) word |= q[w * kPerWord + j] << (j * BITS);
+      out[h * vc_sh + t * vc_st + (chunk * kWords + w) * vc_sw] = static_cast<int32_t>(word);
+    }
+  }
+  if ((chunk % kLanesPerGroup) == 0) {
+    const int64_t so = h * vs_sh + t * vs_st + (chunk / kLanesPerGroup) * vs_sg;
+    if (stats_dtype == UC_FP16) {
+      store_from_f32<UC_FP16>(vscale, so, s);
+      store_from_f32<UC_FP16>(vmin, so, mn);
+    } else if (stats_dtype == UC_BF16) {
+      store_from_f32<UC_BF16>(vscale, so, s);
+      store_from_f32<UC_BF16>(vmin, so, mn);
+    } else {
+      store_from_f32<UC_FP32>(vscale, so, s);
+      store_from_f32<UC_FP32>(vmin, so, mn);
+    }
+  }
+}
+
+struct PackArgs {
+  const void *key;
+  int64_t k_st, k_sh, k_sd;
+  const void *value;
+  int64_t v_st, v_sh, v_sd;
+  int64_t tokens, heads, head_dim;
+  int stats_dtype;
+  void *key_code;
+  int64_t kc_sh, kc_sd, kc_sw;
+  void *key_scale, *key_min;
+  int64_t ks_sh, ks_sd, ks_sg;
+  void *value_code;
+  int64_t vc_sh, vc_st, vc_sw;
+  void *value_scale, *value_min;
+  int64_t vs_sh, vs_st, vs_sg;
+  int64_t key_waves;   // waves doing key work (first part of the grid)
+  int64_t value_waves; // waves doing value work
+};
+
+constexpr int kPackThreads = 256;
+
+// wave -> (head, group, 128-channel slab); lane -> channel pair
+template <int IN, int KB, int G, bool VEC>
+__global__ __launch_bounds__(kPackThreads) void kivi_pack_key_kernel(PackArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = int64_t(blockIdx.x) * (kPackThreads / kWave) + (threadIdx.x / kWave);
+  if (wave >= a.key_waves) return;
+  const int64_t slabs = (a.head_dim + 127) / 128;
+  const int64_t groups = a.tokens / G;
+  const int64_t slab = wave % slabs;
+  const int64_t g = (wave / slabs) % groups;
+  const int64_t h = wave / (slabs * groups);
+  const int64_t c = slab * 128 + 2 * lane;
+  if (c < a.head_dim)
+    pack_key_group<IN, KB, G, VEC>(a.key, a.k_st, a.k_sh, a.k_sd, h, c, g, a.head_dim, a.key_code, a.kc_sh,
+                                   a.kc_sd, a.kc_sw, a.key_scale, a.key_min, a.stats_dtype, a.ks_sh, a.ks_sd,
+                                   a.ks_sg);
+}
+
+// wave -> (head, run of tokens); lane -> (token in run, 16-channel chunk)
+template <int IN, int VB, int G, bool VEC>
+__global__ __launch_bounds__(kPackThreads) void kivi_pack_value_kernel(PackArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t vw = int64_t(blockIdx.x) * (kPackThreads / kWave) + (threadIdx.x / kWave);
+  if (vw >= a.value_waves) return;
+  const int64_t lanes_per_token = a.head_dim / 16;
+  const int64_t tokens_per_wave = kWave / lanes_per_token;
+  const int64_t runs = (a.tokens + tokens_per_wave - 1) / tokens_per_wave;
+  const int64_t h = vw / runs;
+  const int64_t t = (vw % runs) * tokens_per_wave + lane / lanes_per_token;
+  const int64_t chunk = lane % lanes_per_token;
+  const bool active = (lane < tokens_per_wave * lanes_per_token) && t < a.tokens;
+  pack_value_chunk<IN, VB, G, VEC>(a.value, a.v_st, a.v_sh, a.v_sd, h, t, chunk, active, a.value_code, a.vc_sh,
+                                   a.vc_st, a.vc_sw, a.value_scale, a.value_min, a.stats_dtype, a.vs_sh, a.vs_st,
+                                   a.vs_sg);
+}
+
+int64_t wave_blocks(int64_t waves) { return (waves + (kPackThreads / kWave) - 1) / (kPackThreads / kWave); }
+
+template <int IN, int G>
+void launch_pack(const PackArgs &a, int kb, int vb, bool kvec, bool vvec, hipStream_t stream) {
+  if (a.key_waves > 0) {
+    const dim3 grid(wave_blocks(a.key_waves));
+    UC_DISPATCH_BITS(kb, KB, [&] {
+      if (kvec)
+        hipLaunchKernelGGL((kivi_pack_key_kernel<IN, KB, G, true>), grid, dim3(kPackThreads), 0, stream, a);
+      else
+        hipLaunchKernelGGL((kivi_pack_key_kernel<IN, KB, G, false>), grid, dim3(kPackThreads), 0, stream, a);
+    });
+  }
+  if (a.value_waves > 0) {
+    const dim3 grid(wave_blocks(a.value_waves));
+    UC_DISPATCH_BITS(vb, VB, [&] {
+      if (vvec)
+        hipLaunchKernelGGL((kivi_pack_value_kernel<IN, VB, G, true>), grid, dim3(kPackThreads), 0, stream, a);
+      else
+        hipLaunchKernelGGL((kivi_pack_value_kernel<IN, VB, G, false>), grid, dim3(kPackThreads), 0, stream, a);
+    });
+  }
+}
+
+bool aligned(const void *p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+// -------------------------------------------------------------- dequant --
+struct DequantArgs {
+  const void *key_code;
+  int64_t kc_sh, kc_sd, kc_sw;
+  const void *key_scale, *key_min;
+  int64_t ks_sh, ks_sd, ks_sg;
+  const void *value_code;
+  int64_t vc_sh, vc_st, vc_sw;
+  const void *value_scale, *value_min;
+  int64_t vs_sh, vs_st, vs_sg;
+  int64_t heads, head_dim, start, count;
+  void *out_key, *out_value;
+  int64_t o_st, o_sh, o_sd, offset;
+  int lg;      // log2(group_size)
+  int sd, od;  // stats and output dtype codes
+};
+
+// One thread per output element (token, head, channel); keys and values are
+// restored by separate halves of the grid.
+template <int KB, int VB>
+__global__ __launch_bounds__(256) void kivi_dequant_kernel(DequantArgs a) {
+  const int64_t per_tensor = a.count * a.heads * a.head_dim;
+  int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool is_value = idx >= per_tensor;
+  if (is_value) idx -= per_tensor;
+  if (idx >= per_tensor) return;
+  const int64_t d = idx % a.head_dim;
+  const int64_t h = (idx / a.head_dim) % a.heads;
+  const int64_t n = idx / (a.head_dim * a.heads);
+  const int64_t t = a.start + n;
+  float out;
+  if (!is_value) {
+    if (a.key_code == nullptr) return;
+    constexpr int kPerWord = KB == 8 ? 1 : 32 / KB;
+    const uint32_t c = read_code<KB>(a.key_code, h * a.kc_sh + d * a.kc_sd + (t / kPerWord) * a.kc_sw,
+                                     t % kPerWord);
+    const int64_t so = h * a.ks_sh + d * a.ks_sd + (t >> a.lg) * a.ks_sg;
+    const float s = load_dyn(a.key_scale, so, a.sd);
+    const float m = load_dyn(a.key_min, so, a.sd);
+    out = add_rn(mul_rn(float(c), s), m);
+    store_dyn(a.out_key, (a.offset + n) * a.o_st + h * a.o_sh + d * a.o_sd, out, a.od);
+  } else {
+    if (a.value_code == nullptr) return;
+    constexpr int kPerWord = VB == 8 ? 1 : 32 / VB;
+    const uint32_t c = read_code<VB>(a.value_code, h * a.vc_sh + t * a.vc_st + (d / kPerWord) * a.vc_sw,
+                                     d % kPerWord);
+    const int64_t so = h * a.vs_sh + t * a.vs_st + (d >> a.lg) * a.vs_sg;
+    const float s = load_dyn(a.value_scale, so, a.sd);
+    const float m = load_dyn(a.value_min, so, a.sd);
+    out = add_rn(mul_rn(float(c), s), m);
+    store_dyn(a.out_value, (a.offset + n) * a.o_st + h * a.o_sh + d * a.o_sd, out, a.od);
+  }
+}
+
+// ----------------------------------------------------------- fake quant --
+struct FakeQuantArgs {
+  const void *data;
+  int64_t st, sh, sd;
+  int64_t tokens, heads, head_dim;
+  int dim;
+  int64_t group;  // effective group width min(group_size, length)
+  float max_code;
+  void *out;
+};
+
+// One thread per (group, fixed coordinates): two passes over the group
+// (min/max, then quantize-dequantize), following builtin.py:42-53.
+template <int DT>
+__global__ __launch_bounds__(256) void fake_quant_kernel(FakeQuantArgs a) {
+  const int64_t length = a.dim == 0 ? a.tokens : a.head_dim;
+  const int64_t groups = (length + a.group - 1) / a.group;
+  // fixed coordinates: (heads, head_dim) for dim 0, (tokens, heads) for dim 2
+  const int64_t fixed = a.dim == 0 ? a.heads * a.head_dim : a.tokens * a.heads;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= fixed * groups) return;
+  const int64_t f = idx % fixed;  // fixed coordinate varies fastest for coalescing
+  const int64_t g = idx / fixed;
+  int64_t base, step;
+  if (a.dim == 0) {
+    const int64_t d = f % a.head_dim, h = f / a.head_dim;
+    base = h * a.sh + d * a.sd;
+    step = a.st;
+  } else {
+    const int64_t h = f % a.heads, t = f / a.heads;
+    base = t * a.st + h * a.sh;
+    step = a.sd;
+  }
+  const int64_t start = g * a.group;
+  const int64_t stop = min(length, start + a.group);
+  float mn = load_as_f32<DT>(a.data, base + start * step), mx = mn;
+  for (int64_t i = start + 1; i < stop; ++i) {
+    const float x = load_as_f32<DT>(a.data, base + i * step);
+    mn = fminf(mn, x);
+    mx = fmaxf(mx, x);
+  }
+  const float scale = div_rn(fmaxf(sub_rn(mx, mn), kEps), a.max_code);
+  for (int64_t i = start; i < stop; ++i) {
+    const float x = load_as_f32<DT>(a.data, base + i * step);
+    const float code = fminf(fmaxf(rintf(div_rn(sub_rn(x, mn), scale)), 0.0f), a.max_code);
+    store_from_f32<DT>(a.out, base + i * step, add_rn(mul_rn(code, scale), mn));
+  }
+}
+
+}  // namespace
+}  // namespace uc
+
+using namespace uc;
+
+extern "C" int uc_kivi_pack(const void *key, int64_t k_st, int64_t k_sh, int64_t k_sd,
+                            const void *value, int64_t v_st, int64_t v_sh, int64_t v_sd,
+                            int in_dtype, int64_t tokens, int64_t heads, int64_t head_dim,
+                            int k_bits, int v_bits, int group_size, int stats_dtype,
+                            void *key_code, int64_t kc_sh, int64_t kc_sd, int64_t kc_sw,
+                            void *key_scale, void *key_min, int64_t ks_sh, int64_t ks_sd, int64_t ks_sg,
+                            void *value_code, int64_t vc_sh, int64_t vc_st, int64_t vc_sw,
+                            void *value_scale, void *value_min, int64_t vs_sh, int64_t vs_st, int64_t vs_sg,
+                            uc_stream_t stream) {
+  UC_REQUIRE(valid_dtype(in_dtype) && valid_dtype(stats_dtype), "uc_kivi_pack: unknown dtype code");
+  UC_REQUIRE(k_bits == 2 || k_bits == 4 || k_bits == 8, "KIVI physical cache supports 2, 4, or 8 bit payloads");
+  UC_REQUIRE(v_bits == 2 || v_bits == 4 || v_bits == 8, "KIVI physical cache supports 2, 4, or 8 bit payloads");
+  UC_REQUIRE(group_size == 16 || group_size == 32 || group_size == 64 || group_size == 128,
+             "The MI355X KIVI kernels support group_size 16, 32, 64 or 128, got %d", group_size);
+  UC_REQUIRE(tokens >= 0 && heads > 0 && head_dim > 0, "uc_kivi_pack: bad shape");
+  UC_REQUIRE(tokens % group_size == 0, "uc_kivi_pack: tokens (%lld) must be a multiple of group_size",
+             (long long)tokens);
+  UC_REQUIRE(head_dim % group_size == 0,
+             "The MI355X KIVI value kernel requires head_dim divisible by group_size");
+  UC_REQUIRE(head_dim <= 1024, "uc_kivi_pack: head_dim must be <= 1024");
+  if (tokens == 0) return UC_OK;
+  PackArgs a{};
+  a.key = key; a.k_st = k_st; a.k_sh = k_sh; a.k_sd = k_sd;
+  a.value = value; a.v_st = v_st; a.v_sh = v_sh; a.v_sd = v_sd;
+  a.tokens = tokens; a.heads = heads; a.head_dim = head_dim; a.stats_dtype = stats_dtype;
+  a.key_code = key_code; a.kc_sh = kc_sh; a.kc_sd = kc_sd; a.kc_sw = kc_sw;
+  a.key_scale = key_scale; a.key_min = key_min; a.ks_sh = ks_sh; a.ks_sd = ks_sd; a.ks_sg = ks_sg;
+  a.value_code = value_code; a.vc_sh = vc_sh; a.vc_st = vc_st; a.vc_sw = vc_sw;
+  a.value_scale = value_scale; a.value_min = value_min; a.vs_sh = vs_sh; a.vs_st = vs_st; a.vs_sg = vs_sg;
+  const int64_t slabs = (head_dim + 127) / 128;
+  a.key_waves = key ? heads * (tokens / group_size) * slabs : 0;
+  const int64_t lanes_per_token = head_dim / 16;
+  const int64_t tokens_per_wave = kWave / lanes_per_token;
+  a.value_waves = value ? heads * ((tokens + tokens_per_wave - 1) / tokens_per_wave) : 0;
+  const bool half = half_dtype(in_dtype);
+  const bool kvec = half && k_sd == 1 && (k_st % 2 == 0) && (k_sh % 2 == 0) && aligned(key, 4);
+  const bool vvec = half && v_sd == 1 && (v_st % 8 == 0) && (v_sh % 8 == 0) && aligned(value, 16);
+  hipStream_t s = as_stream(stream);
+  // 16-bit inputs only take the vectorised path; fp32 inputs use scalar loads
+  auto go = [&](auto in_tag) {
+    constexpr int IN = decltype(in_tag)::value;
+    switch (group_size) {
+      case 16: launch_pack<IN, 16>(a, k_bits, v_bits, kvec, vvec, s); break;
+      case 32: launch_pack<IN, 32>(a, k_bits, v_bits, kvec, vvec, s); break;
+      case 64: launch_pack<IN, 64>(a, k_bits, v_bits, kvec, vvec, s); break;
+      default: launch_pack<IN, 128>(a, k_bits, v_bits, kvec, vvec, s); break;
+    }
+  };
+  if (in_dtype == UC_BF16) go(std::integral_constant<int, UC_BF16>{});
+  else if (in_dtype == UC_FP16) go(std::integral_constant<int, UC_FP16>{});
+  else go(std::integral_constant<int, UC_FP32>{});
+  return check_launch("uc_kivi_pack");
+}
+
+extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_sd, int64_t kc_sw,
+                               const void *key_scale, const void *key_min, int64_t ks_sh, int64_t ks_sd, int64_t ks_sg,
+                               const void *value_code, int64_t vc_sh, int64_t vc_st, int64_t vc_sw,
+                               const void *value_scale, const void *value_min, int64_t vs_sh, int64_t vs_st, int64_t vs_sg,
+                               int stats_dtype, int64_t heads, int64_t head_dim,
+                               int k_bits, int v_bits, int group_size, int64_t start, int64_t stop,
+                               void *out_key, void *out_value, int out_dtype,
+                               int64_t o_st, int64_t o_sh, int64_t o_sd, int64_t output_offset,
+                               uc_stream_t stream) {
+  UC_REQUIRE(valid_dtype(stats_dtype) && valid_dtype(out_dtype), "uc_kivi_dequant: unknown dtype code");
+  UC_REQUIRE(k_bits == 2 || k_bits == 4 || k_bits == 8, "KIVI physical cache supports 2, 4, or 8 bit payloads");
+  UC_REQUIRE(v_bits == 2 || v_bits == 4 || v_bits == 8, "KIVI physical cache supports 2, 4, or 8 bit payloads");
+  UC_REQUIRE(group_size == 16 || group_size == 32 || group_size == 64 || group_size == 128,
+             "The MI355X KIVI kernels support group_size 16, 32, 64 or 128, got %d", group_size);
+  UC_REQUIRE(heads > 0 && head_dim > 0 && start >= 0 && stop >= start && output_offset >= 0,
+             "uc_kivi_dequant: bad range");
+  UC_REQUIRE(key_code == nullptr || out_key != nullptr, "uc_kivi_dequant: missing key output");
+  UC_REQUIRE(value_code == nullptr || out_value != nullptr, "uc_kivi_dequant: missing value output");
+  const int64_t count = stop - start;
+  if (count == 0) return UC_OK;
+  DequantArgs a{};
+  a.key_code = key_code; a.kc_sh = kc_sh; a.kc_sd = kc_sd; a.kc_sw = kc_sw;
+  a.key_scale = key_scale; a.key_min = key_min; a.ks_sh = ks_sh; a.ks_sd = ks_sd; a.ks_sg = ks_sg;
+  a.value_code = value_code; a.vc_sh = vc_sh; a.vc_st = vc_st; a.vc_sw = vc_sw;
+  a.value_scale = value_scale; a.value_min = value_min; a.vs_sh = vs_sh; a.vs_st = vs_st; a.vs_sg = vs_sg;
+  a.heads = heads; a.head_dim = head_dim; a.start = start; a.count = count;
+  a.out_key = out_key; a.out_value = out_value;
+  a.o_st = o_st; a.o_sh = o_sh; a.o_sd = o_sd; a.offset = output_offset;
+  const int64_t total = 2 * count * heads * head_dim;
+  const int64_t blocks = ceil_div(total, 256);
+  a.lg = group_size == 16 ? 4 : group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
+  a.sd = stats_dtype; a.od = out_dtype;
+  hipStream_t s = as_stream(stream);
+  UC_DISPATCH_BITS(k_bits, KB, [&] {
+    UC_DISPATCH_BITS(v_bits, VB, [&] {
+      hipLaunchKernelGGL((kivi_dequant_kernel<KB, VB>), dim3(blocks), dim3(256), 0, s, a);
+    });
+  });
+  return check_launch("uc_kivi_dequant");
+}
+
+extern "C" int uc_kivi_fake_quant(const void *data, int64_t st, int64_t sh, int64_t sd,
+                                  int dtype, int64_t tokens, int64_t heads, int64_t head_dim,
+                                  int bits, int dim, int group_size,
+                                  void *out, uc_stream_t stream) {
+  UC_REQUIRE(valid_dtype(dtype), "uc_kivi_fake_quant: unknown dtype code");
+  UC_REQUIRE(bits == 2 || bits == 3 || bits == 4 || bits == 8, "Unsupported fake quant bits: %d", bits);
+  UC_REQUIRE(dim == 0 || dim == 2, "uc_kivi_fake_quant: dim must be 0 (tokens) or 2 (channels)");
+  UC_REQUIRE(tokens >= 0 && heads >= 0 && head_dim >= 0, "uc_kivi_fake_quant: bad shape");
+  const int64_t length = dim == 0 ? tokens : head_dim;
+  if (tokens == 0 || heads == 0 || head_dim == 0) return UC_OK;
+  FakeQuantArgs a{};
+  a.data = data; a.st = st; a.sh = sh; a.sd = sd;
+  a.tokens = tokens; a.heads = heads; a.head_dim = head_dim; a.dim = dim;
+  a.group = group_size <= 0 ? 1 : (group_size < length ? group_size : length);
+  a.max_code = float((1 << bits) - 1);
+  a.out = out;
+  const int64_t groups = ceil_div(length, a.group);
+  const int64_t fixed = dim == 0 ? heads * head_dim : tokens * heads;
+  const int64_t blocks = ceil_div(fixed * groups, 256);
+  hipStream_t s = as_stream(stream);
+  UC_DISPATCH_DTYPE(dtype, DT, [&] {
+    hipLaunchKernelGGL((fake_quant_kernel<DT>), dim3(blocks), dim3(256), 0, s, a);
+  });
+  return check_launch("uc_kivi_fake_quant");
+}

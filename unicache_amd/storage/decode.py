@@ -1,0 +1,90 @@
+"""All-layer decode over many packed KIVI segments in one launch.
+
+KiviDecodeBatch fixes, once, a device table of (packed segment, residual,
+query, output) items -- e.g. every (layer, sequence) of a decode step -- plus
+the outputs and the split-K workspace.  run() then enqueues a single
+uc_kivi_attn_decode_batch launch (and its LSE combine) and allocates nothing,
+so it can sit in a tight decode loop or a captured HIP graph.  Callers update
+the query tensors in place between steps.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from .. import _native as nat
+
+
+class KiviDecodeBatch:
+    def __init__(self, caches, queries, *, out_dtype: torch.dtype | None = None):
+        if not caches or len(caches) != len(queries):
+            raise ValueError("KiviDecodeBatch needs one query per packed segment")
+        first = caches[0]
+        for c in caches:
+            if not c.kernel_native_layout or c.k_bits != c.v_bits or c.k_bits not in (2, 4):
+                raise ValueError("Batched decode needs native equal 2/4-bit packed segments")
+            if (c.k_bits, c.group_size, c.num_kv_heads, c.head_dim) != (
+                first.k_bits, first.group_size, first.num_kv_heads, first.head_dim
+            ):
+                raise ValueError("Batched decode segments must share bits, group size and head shapes")
+        q0 = queries[0]
+        for q in queries:
+            if q.shape != q0.shape or q.dtype != q0.dtype or not q.is_contiguous():
+                raise ValueError("Batched decode queries must be contiguous and of one shape/dtype")
+        self.device = nat.require_device(*queries, first.key_code, what="Batched KIVI decode")
+        lq, hq, d = map(int, q0.shape)
+        if hq % first.num_kv_heads:
+            raise ValueError("Query heads must be divisible by KIVI KV heads")
+        res_dtypes = {c.residual_key.dtype for c in caches if c.residual_tokens}
+        if len(res_dtypes) > 1:
+            raise ValueError("Batched decode residuals must share one dtype")
+        self.res_dtype = res_dtypes.pop() if res_dtypes else q0.dtype
+        self.out_dtype = out_dtype or q0.dtype
+        self.caches = list(caches)
+        self.queries = list(queries)
+        self.outputs = [torch.empty((lq, hq, d), dtype=self.out_dtype, device=self.device) for _ in caches]
+        self.lses = [torch.empty((hq, lq), dtype=torch.float32, device=self.device) for _ in caches]
+        items = (nat.KiviItem * len(caches))()
+        for i, (c, q) in enumerate(zip(caches, queries)):
+            tr = c.residual_tokens
+            items[i] = nat.KiviItem(
+                c.key_code.data_ptr(), c.key_scale.data_ptr(), c.key_minimum.data_ptr(),
+                c.value_code.data_ptr(), c.value_scale.data_ptr(), c.value_minimum.data_ptr(),
+                c.residual_key.data_ptr() if tr else None, c.residual_value.data_ptr() if tr else None,
+                q.data_ptr(), self.outputs[i].data_ptr(), self.lses[i].data_ptr(), c.quantized_tokens, tr,
+            )
+        raw = bytes(ctypes.string_at(ctypes.addressof(items), ctypes.sizeof(items)))
+        self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
+        self.max_tq = max(c.quantized_tokens for c in caches)
+        self.max_tr = max(c.residual_tokens for c in caches)
+        self.ws_bytes = nat.workspace_bytes(nat.UC_OP_KIVI_DECODE, len(caches), hq, lq, d, self.max_tq + self.max_tr)
+        self.workspace = nat.workspace(self.device, self.ws_bytes)
+        self.shape = (lq, hq, d)
+        self.sm_scale = 1.0 / math.sqrt(d)
+
+    @property
+    def algorithmic_bytes(self) -> int:
+        """HBM bytes one run must move at least once: packed codes + stats,
+        residual K/V, queries and outputs."""
+
+        total = 0
+        for c, q, o in zip(self.caches, self.queries, self.outputs):
+            for t in (c.key_code, c.key_scale, c.key_minimum, c.value_code, c.value_scale, c.value_minimum):
+                total += t.numel() * t.element_size()
+            total += 2 * c.residual_key.numel() * c.residual_key.element_size()
+            total += q.numel() * q.element_size() + o.numel() * o.element_size()
+        return total
+
+    def run(self, stream: int | None = None) -> None:
+        lq, hq, d = self.shape
+        first = self.caches[0]
+        nat.call(
+            "uc_kivi_attn_decode_batch", self.table.data_ptr(), len(self.caches), first.k_bits,
+            first.group_size, hq, first.num_kv_heads, d, lq, nat.dtype_code(self.queries[0].dtype),
+            nat.dtype_code(self.res_dtype), nat.dtype_code(self.out_dtype), self.sm_scale, self.max_tq,
+            self.max_tr, self.workspace.data_ptr(), self.ws_bytes,
+            nat.stream(self.device) if stream is None else stream,
+        )

@@ -1,0 +1,227 @@
+"""GPU dispatch of the physical KIVI engine, on MI355X HIP kernels.
+
+Drop-in for ``unicache/storage/kivi_cuda.py``: same function names, arguments,
+return layouts and exceptions.  Where UniCache binds the pinned KIVI CUDA GEMV
+and Triton kernels, these functions call libunicache_hip.so.  The engine fails
+closed: a missing library raises RuntimeError, never a CPU or torch fallback.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+from typing import TYPE_CHECKING, Callable
+
+import torch
+
+from .. import _native as nat
+from .physical import _pack_native, gqa_probability_value, gqa_query_key_logits  # noqa: F401
+
+if TYPE_CHECKING:
+    from .physical import PackedKIVICache
+
+
+def select_kivi_kernel_backend(query_length: int) -> str:
+    """GEMV for decode and a tiled kernel for multi-query attention
+    (kivi_cuda.py:26-34).  The names are UniCache's; on MI355X "official_gemv"
+    is the split-K decode kernel and "triton_tiled" the multi-query path."""
+
+    requested = os.environ.get("UNICACHE_KIVI_MULTI_QUERY_BACKEND", "auto").lower()
+    if requested not in {"auto", "official_gemv", "triton_tiled"}:
+        raise ValueError(f"Unknown KIVI multi-query backend: {requested}")
+    if requested != "auto":
+        return requested
+    return "official_gemv" if int(query_length) == 1 else "triton_tiled"
+
+
+def _check_native(cache: "PackedKIVICache", what: str) -> None:
+    if not cache.kernel_native_layout:
+        raise RuntimeError(f"{what} requires kernel-native layout")
+
+
+def dequantize_kivi_chunk(
+    cache: "PackedKIVICache",
+    *,
+    start: int,
+    stop: int,
+    dtype: torch.dtype,
+    output_key: torch.Tensor | None = None,
+    output_value: torch.Tensor | None = None,
+    output_offset: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Restore packed tokens [start, stop) without a full bf16 replica,
+    optionally into caller workspaces (kivi_cuda.py:58-93; kivi_triton.py:690-770)."""
+
+    start = max(0, int(start))
+    stop = min(int(stop), int(cache.quantized_tokens))
+    if stop <= start:
+        empty = cache.residual_key[:0].to(dtype)
+        return empty, empty
+    if not cache.kernel_native_layout or cache.k_bits != cache.v_bits:
+        raise RuntimeError("Chunked KIVI dequantization requires native equal-bit KV")
+    token_count = stop - start
+    kv_heads, d_size = int(cache.key_code.shape[0]), int(cache.key_code.shape[1])
+    output_offset = int(output_offset)
+    if output_key is None or output_value is None:
+        if output_key is not None or output_value is not None:
+            raise ValueError("Both KIVI output buffers must be provided together")
+        output_offset = 0
+        output_key = torch.empty((token_count, kv_heads, d_size), device=cache.key_code.device, dtype=dtype)
+        output_value = torch.empty_like(output_key)
+    if (
+        output_key.dim() != 3
+        or output_value.shape != output_key.shape
+        or tuple(output_key.shape[1:]) != (kv_heads, d_size)
+        or output_key.device != cache.key_code.device
+        or output_value.device != cache.key_code.device
+        or output_key.dtype != dtype
+        or output_value.dtype != dtype
+        or output_offset < 0
+        or output_offset + token_count > int(output_key.shape[0])
+    ):
+        raise ValueError("KIVI dequantization output workspace has an invalid layout")
+    if output_key.stride() != output_value.stride():
+        raise ValueError("KIVI dequantization output workspace has an invalid layout")
+    cache.dequantize_into(output_key, output_value, start=start, stop=stop, output_offset=output_offset)
+    chunk = slice(output_offset, output_offset + token_count)
+    return output_key[chunk], output_value[chunk]
+
+
+def _decode_summary(cache: "PackedKIVICache", query: torch.Tensor, *, include_residual: bool,
+                    out_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fused split-K attention over the packed prefix (and optionally the
+    residual) for a short query: (out [Lq, Hq, D], lse [Hq, Lq])."""
+
+    device = nat.require_device(query, cache.key_code, what="Packed KIVI attention")
+    q = query.contiguous()
+    lq, hq, d = map(int, q.shape)
+    tr = cache.residual_tokens if include_residual else 0
+    out = torch.empty((lq, hq, d), dtype=out_dtype, device=device)
+    lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
+    item = nat.KiviItem(
+        cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
+        cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
+        nat.ptr(cache.residual_key) if tr else None, nat.ptr(cache.residual_value) if tr else None,
+        q.data_ptr(), out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr,
+    )
+    ws_bytes = nat.workspace_bytes(nat.UC_OP_KIVI_DECODE, 1, hq, lq, d, cache.quantized_tokens + tr)
+    ws = nat.workspace(device, ws_bytes)
+    res_dtype = cache.residual_key.dtype if tr else q.dtype
+    nat.call(
+        "uc_kivi_attn_decode", item, cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq,
+        nat.dtype_code(q.dtype), nat.dtype_code(res_dtype), nat.dtype_code(out_dtype),
+        1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device),
+    )
+    return out, lse
+
+
+def _max_decode_query_len(cache: "PackedKIVICache", heads_q: int) -> int:
+    return max(1, 16 // max(1, heads_q // cache.num_kv_heads))
+
+
+def packed_kivi_attention_summary(
+    cache: "PackedKIVICache", query: torch.Tensor, *, include_residual: bool = True
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Normalised output [Lq, Hq, D] and natural-log LSE [Hq, Lq] of softmax
+    attention over the packed prefix plus (by default) the residual, in one
+    fused dequant-attention pass.  With include_residual=False this is
+    packed_kivi_quantized_attention_summary."""
+
+    if not cache.quantized_tokens:
+        raise ValueError("Packed KIVI summary requires a non-empty quantized prefix")
+    if cache.k_bits != cache.v_bits or cache.k_bits not in {2, 4}:
+        raise ValueError("Packed KIVI fused summary supports equal 2-bit or 4-bit KV")
+    _check_native(cache, "Packed KIVI fused summary")
+    if query.dim() != 3 or int(query.shape[1]) % cache.num_kv_heads:
+        raise ValueError("Packed KIVI attention requires query heads divisible by KV heads")
+    if query.dtype not in (torch.bfloat16, torch.float16):
+        query = query.to(torch.bfloat16)
+    lq = int(query.shape[0])
+    step = _max_decode_query_len(cache, int(query.shape[1]))
+    if lq <= step:
+        return _decode_summary(cache, query, include_residual=include_residual, out_dtype=query.dtype)
+    from .kivi_mq import packed_attention_mq
+
+    return packed_attention_mq(cache, query, include_residual=include_residual)
+
+
+def packed_kivi_quantized_attention_summary(
+    cache: "PackedKIVICache", query: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Normalised output and LSE for the packed quantized prefix
+    (kivi_cuda.py:96-120)."""
+
+    return packed_kivi_attention_summary(cache, query, include_residual=False)
+
+
+def quantize_kivi_native(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    k_bits: int,
+    v_bits: int,
+    group_size: int,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """KIVI's kernel-native packed layout in one HIP pass (kivi_cuda.py:157-190):
+    keys grouped along tokens -> [Hkv, D, T*b/32] words, values grouped along
+    channels -> [Hkv, T, D*b/32] words, fp16 scale/minimum."""
+
+    if key.shape != value.shape or key.dim() != 3:
+        raise ValueError("KIVI native packing expects matching [tokens, heads, dim] KV")
+    if key.device.type != "cuda":
+        raise RuntimeError("KIVI native packing requires CUDA tensors")
+    if k_bits not in {2, 4} or v_bits not in {2, 4}:
+        raise ValueError("KIVI native packing supports 2-bit or 4-bit codes")
+    return _pack_native(key, value, k_bits=int(k_bits), v_bits=int(v_bits), group_size=int(group_size))
+
+
+def packed_kivi_attention_parts(
+    cache: "PackedKIVICache",
+    query: torch.Tensor,
+) -> tuple[torch.Tensor, Callable[[torch.Tensor], torch.Tensor]]:
+    """Scaled fp32 logits [Hq, Lq, Tq+Tr] over [packed | residual] and an AV
+    closure returning [Hq, Lq, D] in the residual dtype (kivi_cuda.py:238-329)."""
+
+    if query.device.type != "cuda":
+        raise RuntimeError("Physical KIVI CUDA backend received a non-CUDA query")
+    if cache.k_bits != cache.v_bits:
+        raise ValueError("Official KIVI kernel path requires equal key/value bit widths")
+    repeat = int(query.shape[1]) // cache.num_kv_heads
+    if repeat * cache.num_kv_heads != int(query.shape[1]):
+        raise ValueError("Query heads must be divisible by KIVI KV heads")
+    if cache.quantized_tokens and cache.k_bits in {2, 4} and not cache.kernel_native_layout:
+        raise RuntimeError("Physical KIVI CUDA cache is not stored in kernel-native layout")
+    device = nat.require_device(query, cache.residual_key, what="Physical KIVI attention")
+    q = query.contiguous()
+    lq, hq, d = map(int, q.shape)
+    tq, tr = cache.quantized_tokens, cache.residual_tokens
+    res = cache.residual_key
+    stats_dtype = cache.key_scale.dtype if tq else torch.float16
+    logits = torch.empty((hq, lq, tq + tr), dtype=torch.float32, device=device)
+    nat.call(
+        "uc_kivi_qk", q.data_ptr(), nat.dtype_code(q.dtype), lq, hq,
+        nat.ptr(cache.key_code), nat.ptr(cache.key_scale), nat.ptr(cache.key_minimum),
+        nat.dtype_code(stats_dtype), tq, cache.k_bits, cache.group_size,
+        res.data_ptr(), nat.dtype_code(res.dtype), tr, int(res.stride(0)), int(res.stride(1)),
+        cache.num_kv_heads, d, 1.0 / math.sqrt(d), logits.data_ptr(), nat.stream(device),
+    )
+
+    def apply_value(probabilities: torch.Tensor) -> torch.Tensor:
+        if tuple(probabilities.shape) != (hq, lq, tq + tr):
+            raise ValueError("KIVI AV probabilities must be [query_heads, queries, tokens]")
+        nat.require_device(probabilities, what="Physical KIVI AV")
+        val = cache.residual_value
+        out = torch.empty((hq, lq, d), dtype=val.dtype, device=device)
+        ws = nat.workspace(device, nat.workspace_bytes(nat.UC_OP_KIVI_AV, 1, hq, lq, d, tq + tr))
+        nat.call(
+            "uc_kivi_av", probabilities.data_ptr(), nat.dtype_code(probabilities.dtype),
+            *map(int, probabilities.stride()), lq, hq,
+            nat.ptr(cache.value_code), nat.ptr(cache.value_scale), nat.ptr(cache.value_minimum),
+            nat.dtype_code(stats_dtype), tq, cache.v_bits, cache.group_size,
+            val.data_ptr(), nat.dtype_code(val.dtype), tr, int(val.stride(0)), int(val.stride(1)),
+            cache.num_kv_heads, d, out.data_ptr(), nat.dtype_code(val.dtype), ws.data_ptr(),
+            nat.stream(device),
+        )
+        return out
+
+    return logits, apply_value

@@ -1,0 +1,639 @@
+"""Physical KV-cache layouts of UniCache's engine, backed by MI355X kernels.
+
+Drop-in for ``unicache/storage/physical.py``: the same classes, constructor
+arguments, attributes, return layouts and exceptions.  Every tensor operation
+on the cache contents (pack, dequantize, QK/AV, H2O selection and gather) runs
+in libunicache_hip.so; torch only allocates memory and orders streams.
+
+Backends: ``backend="cuda"`` (the engine's only GPU backend in UniCache) maps
+to the HIP kernels.  UniCache's ``backend="reference"`` is its CPU test oracle;
+this package does not ship a CPU path, so it is rejected with a RuntimeError
+(the CPU restatement lives under ``oracle/`` as test infrastructure).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Callable
+
+import torch
+
+from .. import _native as nat
+
+
+def tensor_bytes(tensor: torch.Tensor | None) -> int:
+    return 0 if tensor is None else int(tensor.numel() * tensor.element_size())
+
+
+def _require_hip_backend(backend: str) -> None:
+    if backend == "reference":
+        raise RuntimeError(
+            "The MI355X engine implements the 'cuda' physical backend on HIP kernels only; "
+            "UniCache's CPU 'reference' backend is not part of this build"
+        )
+    if backend != "cuda":
+        raise ValueError(f"Unknown KIVI physical backend: {backend}")
+
+
+def _dense_strides(t: torch.Tensor) -> tuple[int, int, int]:
+    st, sh, sd = t.stride()
+    return int(st), int(sh), int(sd)
+
+
+def gqa_query_key_logits(query: torch.Tensor, key: torch.Tensor) -> torch.Tensor:
+    """QK for native GQA tensors without repeating KV heads (physical.py:20-39).
+
+    query [Lq, Hq, D], key [T, Hkv, D] -> fp32 [Hq, Lq, T] (unscaled).
+    """
+
+    if query.dim() != 3 or key.dim() != 3:
+        raise ValueError("GQA QK expects [tokens, heads, head_dim] tensors")
+    if int(query.shape[-1]) != int(key.shape[-1]):
+        raise ValueError("GQA QK query/key head dimensions must match")
+    query_heads, kv_heads = int(query.shape[1]), int(key.shape[1])
+    if query_heads % kv_heads != 0:
+        raise ValueError("GQA query heads must be divisible by KV heads")
+    return _dense_qk(query, key, scale=1.0)
+
+
+def gqa_probability_value(probabilities: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+    """AV for native GQA tensors (physical.py:42-63): [Hq, Lq, T] x [T, Hkv, D]."""
+
+    if probabilities.dim() != 3 or value.dim() != 3:
+        raise ValueError(
+            "GQA AV expects probabilities [heads, queries, keys] and values [keys, heads, dim]"
+        )
+    query_heads, kv_heads = int(probabilities.shape[0]), int(value.shape[1])
+    if query_heads % kv_heads != 0:
+        raise ValueError("GQA probability heads must be divisible by KV heads")
+    if int(probabilities.shape[-1]) != int(value.shape[0]):
+        raise ValueError("GQA AV probability key width must match value tokens")
+    return _dense_av(probabilities, value)
+
+
+def _dense_qk(query: torch.Tensor, key: torch.Tensor, *, scale: float) -> torch.Tensor:
+    """scale * q.k over a dense key view [T, Hkv, D] (any token/head strides,
+    unit channel stride) through uc_kivi_qk with no packed part."""
+
+    device = nat.require_device(query, key, what="GQA QK")
+    q = query.contiguous()
+    lq, hq, d = map(int, q.shape)
+    if key.stride(-1) != 1:
+        key = key.contiguous()
+    tokens, hkv = int(key.shape[0]), int(key.shape[1])
+    logits = torch.empty((hq, lq, tokens), dtype=torch.float32, device=device)
+    nat.call(
+        "uc_kivi_qk", q.data_ptr(), nat.dtype_code(q.dtype), lq, hq,
+        None, None, None, nat.UC_FP16, 0, 2, 32,
+        key.data_ptr(), nat.dtype_code(key.dtype), tokens, int(key.stride(0)), int(key.stride(1)),
+        hkv, d, float(scale), logits.data_ptr(), nat.stream(device),
+    )
+    return logits
+
+
+def _dense_av(probabilities: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+    """probs [Hq, Lq, T] x dense value view [T, Hkv, D] -> [Hq, Lq, D] of
+    value.dtype, through uc_kivi_av with no packed part."""
+
+    device = nat.require_device(probabilities, value, what="GQA AV")
+    hq, lq, tokens = map(int, probabilities.shape)
+    if value.stride(-1) != 1:
+        value = value.contiguous()
+    hkv, d = int(value.shape[1]), int(value.shape[2])
+    out = torch.empty((hq, lq, d), dtype=value.dtype, device=device)
+    ws = nat.workspace(device, nat.workspace_bytes(nat.UC_OP_KIVI_AV, 1, hq, lq, d, tokens))
+    nat.call(
+        "uc_kivi_av", probabilities.data_ptr(), nat.dtype_code(probabilities.dtype),
+        *map(int, probabilities.stride()), lq, hq,
+        None, None, None, nat.UC_FP16, 0, 2, 32,
+        value.data_ptr(), nat.dtype_code(value.dtype), tokens, int(value.stride(0)), int(value.stride(1)),
+        hkv, d, out.data_ptr(), nat.dtype_code(value.dtype), ws.data_ptr(), nat.stream(device),
+    )
+    return out
+
+
+# --------------------------------------------------------------- layouts --
+def native_pack_layout(tokens: int, heads: int, head_dim: int, k_bits: int, v_bits: int, group_size: int):
+    """Shapes and dtypes of the kernel-native packed tensors (kivi_cuda.py:177-190)."""
+
+    return {
+        "key_code": ((heads, head_dim, tokens * k_bits // 32), torch.int32),
+        "key_stats": ((heads, head_dim, tokens // group_size), torch.float16),
+        "value_code": ((heads, tokens, head_dim * v_bits // 32), torch.int32),
+        "value_stats": ((heads, tokens, head_dim // group_size), torch.float16),
+    }
+
+
+def _pack_native(key: torch.Tensor, value: torch.Tensor, *, k_bits: int, v_bits: int, group_size: int):
+    """HIP quantize+pack into the kernel-native layout (fp16 stats)."""
+
+    device = nat.require_device(key, value, what="KIVI native packing")
+    tokens, heads, head_dim = map(int, key.shape)
+    lay = native_pack_layout(tokens, heads, head_dim, k_bits, v_bits, group_size)
+    kc = torch.empty(lay["key_code"][0], dtype=torch.int32, device=device)
+    ks = torch.empty(lay["key_stats"][0], dtype=torch.float16, device=device)
+    km = torch.empty_like(ks)
+    vc = torch.empty(lay["value_code"][0], dtype=torch.int32, device=device)
+    vs = torch.empty(lay["value_stats"][0], dtype=torch.float16, device=device)
+    vm = torch.empty_like(vs)
+    if key.dtype != value.dtype:
+        raise ValueError("KIVI packing expects key and value of one dtype")
+    nat.call(
+        "uc_kivi_pack",
+        key.data_ptr(), *_dense_strides(key), value.data_ptr(), *_dense_strides(value),
+        nat.dtype_code(key.dtype), tokens, heads, head_dim, k_bits, v_bits, group_size, nat.UC_FP16,
+        kc.data_ptr(), *map(int, kc.stride()), ks.data_ptr(), km.data_ptr(), *map(int, ks.stride()),
+        vc.data_ptr(), *map(int, vc.stride()), vs.data_ptr(), vm.data_ptr(), *map(int, vs.stride()),
+        nat.stream(device),
+    )
+    return kc, ks, km, vc, vs, vm
+
+
+def _reference_layout_shapes(tokens, heads, head_dim, bits, group_size, *, is_key):
+    """UniCache's non-native layout: codes along dim 0 (K) / dim 2 (V)."""
+
+    if is_key:
+        code = (tokens if bits == 8 else tokens * bits // 32, heads, head_dim)
+        stats = (tokens // group_size, heads, head_dim)
+    else:
+        code = (tokens, heads, head_dim if bits == 8 else head_dim * bits // 32)
+        stats = (tokens, heads, head_dim // group_size)
+    return code, stats, (torch.uint8 if bits == 8 else torch.int32)
+
+
+def _pack_reference_layout(key, value, *, k_bits, v_bits, group_size):
+    """HIP quantize+pack into UniCache's non-native layout (stats in the input
+    dtype), used when a payload is 8-bit (physical.py:291-304)."""
+
+    device = nat.require_device(key, value, what="KIVI packing")
+    tokens, heads, head_dim = map(int, key.shape)
+    kshape, kstat_shape, kdt = _reference_layout_shapes(tokens, heads, head_dim, k_bits, group_size, is_key=True)
+    vshape, vstat_shape, vdt = _reference_layout_shapes(tokens, heads, head_dim, v_bits, group_size, is_key=False)
+    kc = torch.empty(kshape, dtype=kdt, device=device)
+    ks = torch.empty(kstat_shape, dtype=key.dtype, device=device)
+    km = torch.empty_like(ks)
+    vc = torch.empty(vshape, dtype=vdt, device=device)
+    vs = torch.empty(vstat_shape, dtype=key.dtype, device=device)
+    vm = torch.empty_like(vs)
+    # key code element (h, d, w) -> [w, h, d]; key stats (h, d, g) -> [g, h, d]
+    kc_s = (kc.stride(1), kc.stride(2), kc.stride(0))
+    ks_s = (ks.stride(1), ks.stride(2), ks.stride(0))
+    # value code (h, t, w) -> [t, h, w]; value stats (h, t, g) -> [t, h, g]
+    vc_s = (vc.stride(1), vc.stride(0), vc.stride(2))
+    vs_s = (vs.stride(1), vs.stride(0), vs.stride(2))
+    nat.call(
+        "uc_kivi_pack",
+        key.data_ptr(), *_dense_strides(key), value.data_ptr(), *_dense_strides(value),
+        nat.dtype_code(key.dtype), tokens, heads, head_dim, k_bits, v_bits, group_size,
+        nat.dtype_code(key.dtype),
+        kc.data_ptr(), *map(int, kc_s), ks.data_ptr(), km.data_ptr(), *map(int, ks_s),
+        vc.data_ptr(), *map(int, vc_s), vs.data_ptr(), vm.data_ptr(), *map(int, vs_s),
+        nat.stream(device),
+    )
+    return kc, ks, km, vc, vs, vm
+
+
+# ------------------------------------------------------------------ KIVI --
+@dataclass
+class PackedKIVICache:
+    """A KIVI packed KV segment with a full-precision residual suffix
+    (physical.py:204-475)."""
+
+    key_code: torch.Tensor | None
+    key_scale: torch.Tensor | None
+    key_minimum: torch.Tensor | None
+    value_code: torch.Tensor | None
+    value_scale: torch.Tensor | None
+    value_minimum: torch.Tensor | None
+    residual_key: torch.Tensor
+    residual_value: torch.Tensor
+    logical_token_ids: torch.Tensor
+    token_type_id: int
+    k_bits: int
+    v_bits: int
+    group_size: int
+    quantized_tokens: int
+    head_dim: int
+    num_kv_heads: int
+    backend: str = "cuda"
+    kernel_native_layout: bool = False
+    budget_shortfall_events: int = 0
+
+    @classmethod
+    def from_dense(
+        cls,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        *,
+        logical_token_ids: torch.Tensor,
+        token_type_id: int,
+        k_bits: int,
+        v_bits: int,
+        group_size: int,
+        residual_length: int,
+        backend: str = "cuda",
+    ) -> "PackedKIVICache":
+        """Split [tokens, Hkv, D] K/V into a group-aligned packed prefix and a
+        residual suffix (physical.py:228-332)."""
+
+        if key.shape != value.shape or key.dim() != 3:
+            raise ValueError("KIVI physical cache expects matching [tokens, kv_heads, head_dim] tensors")
+        if k_bits not in {2, 4, 8} or v_bits not in {2, 4, 8}:
+            raise ValueError("KIVI physical cache supports 2, 4, or 8 bit payloads")
+        tokens, heads, head_dim = map(int, key.shape)
+        if group_size <= 0:
+            raise ValueError("KIVI physical cache group_size must be positive")
+        _require_hip_backend(backend)
+        if group_size not in {16, 32, 64, 128}:
+            raise ValueError("The MI355X KIVI kernels support group_size 16, 32, 64 or 128")
+        if head_dim % group_size != 0:
+            raise ValueError("The MI355X KIVI value kernel requires head_dim divisible by group_size")
+        requested_residual = min(tokens, max(0, int(residual_length)))
+        # keep any incomplete prefix group in the residual (physical.py:258-263)
+        quantized = ((tokens - requested_residual) // group_size) * group_size
+        q_key, q_value = key[:quantized], value[:quantized]
+        kernel_native_layout = bool(quantized and k_bits in {2, 4} and v_bits in {2, 4})
+        if quantized:
+            if kernel_native_layout:
+                from .kivi_cuda import quantize_kivi_native
+
+                packed = quantize_kivi_native(
+                    q_key, q_value, k_bits=k_bits, v_bits=v_bits, group_size=group_size
+                )
+            else:
+                packed = _pack_reference_layout(
+                    q_key, q_value, k_bits=k_bits, v_bits=v_bits, group_size=group_size
+                )
+            key_code, key_scale, key_minimum, value_code, value_scale, value_minimum = packed
+        else:
+            nat.require_device(key, value, what="KIVI physical cache")
+            key_code = key_scale = key_minimum = None
+            value_code = value_scale = value_minimum = None
+        return cls(
+            key_code=key_code,
+            key_scale=key_scale,
+            key_minimum=key_minimum,
+            value_code=value_code,
+            value_scale=value_scale,
+            value_minimum=value_minimum,
+            # a clone, so a suffix view does not pin the whole dense segment
+            residual_key=key[quantized:].clone(),
+            residual_value=value[quantized:].clone(),
+            logical_token_ids=logical_token_ids.detach().clone(),
+            token_type_id=int(token_type_id),
+            k_bits=int(k_bits),
+            v_bits=int(v_bits),
+            group_size=int(group_size),
+            quantized_tokens=quantized,
+            head_dim=head_dim,
+            num_kv_heads=heads,
+            backend=str(backend),
+            kernel_native_layout=kernel_native_layout,
+        )
+
+    @property
+    def token_count(self) -> int:
+        return int(self.logical_token_ids.numel())
+
+    @property
+    def residual_tokens(self) -> int:
+        return int(self.residual_key.shape[0])
+
+    @property
+    def resident_bytes(self) -> int:
+        tensors = (
+            self.key_code, self.key_scale, self.key_minimum,
+            self.value_code, self.value_scale, self.value_minimum,
+            self.residual_key, self.residual_value, self.logical_token_ids,
+        )
+        return sum(tensor_bytes(item) for item in tensors)
+
+    @property
+    def byte_breakdown(self) -> dict[str, int]:
+        return {
+            "payload_bytes": tensor_bytes(self.key_code) + tensor_bytes(self.value_code),
+            "scale_bytes": tensor_bytes(self.key_scale) + tensor_bytes(self.value_scale),
+            "minimum_bytes": tensor_bytes(self.key_minimum) + tensor_bytes(self.value_minimum),
+            "residual_bytes": tensor_bytes(self.residual_key) + tensor_bytes(self.residual_value),
+            "indices_bytes": tensor_bytes(self.logical_token_ids),
+            "score_bytes": 0,
+        }
+
+    @property
+    def full_precision_bytes(self) -> int:
+        element_size = int(self.residual_key.element_size())
+        return self.token_count * self.num_kv_heads * self.head_dim * 2 * element_size
+
+    def _code_strides(self):
+        """(key code, key stats, value code, value stats) strides in the
+        (h, d, w) / (h, d, g) / (h, t, w) / (h, t, g) order of the C ABI."""
+
+        kc, ks, vc, vs = self.key_code, self.key_scale, self.value_code, self.value_scale
+        if self.kernel_native_layout:
+            return tuple(kc.stride()), tuple(ks.stride()), tuple(vc.stride()), tuple(vs.stride())
+        return (
+            (kc.stride(1), kc.stride(2), kc.stride(0)),
+            (ks.stride(1), ks.stride(2), ks.stride(0)),
+            (vc.stride(1), vc.stride(0), vc.stride(2)),
+            (vs.stride(1), vs.stride(0), vs.stride(2)),
+        )
+
+    def dequantize_into(self, out_key: torch.Tensor | None, out_value: torch.Tensor | None,
+                        *, start: int, stop: int, output_offset: int) -> None:
+        """Restore packed tokens [start, stop) into rows output_offset.. of the
+        given [n, Hkv, D] buffers (either may be None)."""
+
+        if stop <= start:
+            return
+        ref = out_key if out_key is not None else out_value
+        device = nat.require_device(self.key_code, ref, what="KIVI dequantization")
+        kcs, kss, vcs, vss = self._code_strides()
+        if out_key is not None and out_value is not None:
+            if out_key.stride() != out_value.stride() or out_key.dtype != out_value.dtype:
+                raise ValueError("KIVI dequantization output workspace has an invalid layout")
+        nat.call(
+            "uc_kivi_dequant",
+            nat.ptr(self.key_code) if out_key is not None else None, *map(int, kcs),
+            self.key_scale.data_ptr(), self.key_minimum.data_ptr(), *map(int, kss),
+            nat.ptr(self.value_code) if out_value is not None else None, *map(int, vcs),
+            self.value_scale.data_ptr(), self.value_minimum.data_ptr(), *map(int, vss),
+            nat.dtype_code(self.key_scale.dtype), self.num_kv_heads, self.head_dim,
+            self.k_bits, self.v_bits, self.group_size, int(start), int(stop),
+            nat.ptr(out_key), nat.ptr(out_value), nat.dtype_code(ref.dtype),
+            *map(int, ref.stride()), int(output_offset), nat.stream(device),
+        )
+
+    def dequantize(self, dtype: torch.dtype | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """Restore [tokens, Hkv, D] K and V (physical.py:379-423)."""
+
+        dtype = dtype or self.residual_key.dtype
+        if not self.quantized_tokens:
+            return self.residual_key.to(dtype), self.residual_value.to(dtype)
+        total = self.quantized_tokens + self.residual_tokens
+        shape = (total, self.num_kv_heads, self.head_dim)
+        key = torch.empty(shape, dtype=dtype, device=self.key_code.device)
+        value = torch.empty_like(key)
+        self.dequantize_into(key, value, start=0, stop=self.quantized_tokens, output_offset=0)
+        key[self.quantized_tokens:].copy_(self.residual_key)
+        value[self.quantized_tokens:].copy_(self.residual_value)
+        return key, value
+
+    def repack_monotonic(self, *, bits: int, group_size: int | None = None) -> bool:
+        """Lower precision, never raising it back (physical.py:425-450)."""
+
+        target_bits = int(bits)
+        target_group = int(group_size or self.group_size)
+        if target_bits > self.k_bits or target_bits > self.v_bits or target_group < self.group_size:
+            self.budget_shortfall_events += 1
+            return False
+        if target_bits == self.k_bits and target_bits == self.v_bits and target_group == self.group_size:
+            return True
+        key, value = self.dequantize(dtype=self.residual_key.dtype)
+        replacement = PackedKIVICache.from_dense(
+            key,
+            value,
+            logical_token_ids=self.logical_token_ids,
+            token_type_id=self.token_type_id,
+            k_bits=target_bits,
+            v_bits=target_bits,
+            group_size=target_group,
+            residual_length=int(self.residual_key.shape[0]),
+            backend=self.backend,
+        )
+        shortfalls = self.budget_shortfall_events
+        self.__dict__.update(replacement.__dict__)
+        self.budget_shortfall_events = shortfalls
+        return True
+
+    def attention_parts(
+        self, query: torch.Tensor
+    ) -> tuple[torch.Tensor, Callable[[torch.Tensor], torch.Tensor]]:
+        """Scaled logits over [packed | residual] and an AV closure
+        (physical.py:452-475)."""
+
+        _require_hip_backend(self.backend)
+        from .kivi_cuda import packed_kivi_attention_parts
+
+        return packed_kivi_attention_parts(self, query)
+
+
+# ------------------------------------------------------------------- H2O --
+def h2o_select_indices(scores: torch.Tensor, *, heavy_k: int, recent: int) -> torch.Tensor:
+    """[Hkv, heavy_k + recent] int64: per KV head the heavy_k top scores of the
+    history (lowest index wins ties), ascending, then the recent window."""
+
+    device = nat.require_device(scores, what="H2O selection")
+    if scores.dtype != torch.float32:
+        scores = scores.float()
+    heads, tokens = map(int, scores.shape)
+    out = torch.empty((heads, int(heavy_k) + int(recent)), dtype=torch.long, device=device)
+    nat.call(
+        "uc_h2o_select", scores.data_ptr(), *map(int, scores.stride()), heads, tokens,
+        int(heavy_k), int(recent), out.data_ptr(), nat.stream(device),
+    )
+    return out
+
+
+def _gather(key, value, key_strides, indexes, ids, ids_strides, scores, *, heads, head_dim):
+    device = nat.require_device(key, value, indexes, what="GQA compaction")
+    retained = int(indexes.shape[1])
+    out_key = torch.empty((heads, retained, head_dim), dtype=key.dtype, device=device)
+    out_value = torch.empty_like(out_key)
+    ids64 = ids if ids.dtype == torch.int64 else ids.to(torch.int64)
+    out_ids = torch.empty((heads, retained), dtype=torch.int64, device=device)
+    scores32 = scores if scores.dtype == torch.float32 else scores.float()
+    out_scores = torch.empty((heads, retained), dtype=torch.float32, device=device)
+    nat.call(
+        "uc_gqa_gather", key.data_ptr(), value.data_ptr(), *map(int, key_strides),
+        nat.dtype_code(key.dtype), heads, head_dim, indexes.data_ptr(), retained,
+        ids64.data_ptr(), int(ids_strides[0]), int(ids_strides[1]),
+        scores32.data_ptr(), *map(int, scores32.stride()),
+        out_key.data_ptr(), out_value.data_ptr(), out_ids.data_ptr(), out_scores.data_ptr(),
+        nat.stream(device),
+    )
+    if ids.dtype != torch.int64:
+        out_ids = out_ids.to(ids.dtype)
+    return out_key, out_value, out_ids, out_scores
+
+
+@dataclass
+class GQAH2OCache:
+    """Per-KV-head physical H2O cache with fixed-width selected storage
+    (physical.py:478-654)."""
+
+    key: torch.Tensor  # [kv_heads, retained_tokens, head_dim]
+    value: torch.Tensor
+    logical_token_ids: torch.Tensor  # [kv_heads, retained_tokens]
+    cumulative_scores: torch.Tensor
+    token_type_id: int
+    original_tokens: int
+    heavy_tokens: int
+    recent_tokens: int
+    selection_frozen: bool = False
+    budget_shortfall_tokens: int = 0
+
+    @classmethod
+    def from_dense(
+        cls,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        *,
+        logical_token_ids: torch.Tensor,
+        token_type_id: int,
+        per_kv_head_scores: torch.Tensor,
+        target_tokens: int,
+        recent_tokens: int,
+        selection_frozen: bool = False,
+    ) -> "GQAH2OCache":
+        if key.shape != value.shape or key.dim() != 3:
+            raise ValueError("Physical H2O expects matching [tokens, kv_heads, head_dim] tensors")
+        tokens, kv_heads, head_dim = map(int, key.shape)
+        if tuple(per_kv_head_scores.shape) != (kv_heads, tokens):
+            raise ValueError("Physical H2O scores must be [kv_heads, segment_tokens]")
+        if key.stride() != value.stride():
+            value = value.contiguous()
+            key = key.contiguous()
+        # budget arithmetic of physical.py:511-515
+        target = min(tokens, max(1, int(target_tokens)))
+        recent = min(target, max(0, int(recent_tokens)))
+        heavy = target - recent
+        history_end = tokens - recent
+        heavy_k = min(heavy, history_end)
+        scores = per_kv_head_scores.to(device=key.device)
+        indexes = h2o_select_indices(scores, heavy_k=heavy_k, recent=recent)
+        logical = logical_token_ids.to(device=key.device)
+        if logical.dim() != 1:
+            raise ValueError("Physical H2O logical_token_ids must be [segment_tokens]")
+        out_key, out_value, out_ids, out_scores = _gather(
+            key, value, key.stride(), indexes, logical, (0, logical.stride(0)), scores,
+            heads=kv_heads, head_dim=head_dim,
+        )
+        return cls(
+            key=out_key,
+            value=out_value,
+            logical_token_ids=out_ids,
+            cumulative_scores=out_scores,
+            token_type_id=int(token_type_id),
+            original_tokens=tokens,
+            heavy_tokens=heavy,
+            recent_tokens=recent,
+            selection_frozen=bool(selection_frozen),
+        )
+
+    @property
+    def num_kv_heads(self) -> int:
+        return int(self.key.shape[0])
+
+    @property
+    def retained_tokens(self) -> int:
+        return int(self.key.shape[1])
+
+    @property
+    def resident_bytes(self) -> int:
+        return sum(
+            tensor_bytes(item)
+            for item in (self.key, self.value, self.logical_token_ids, self.cumulative_scores)
+        )
+
+    @property
+    def byte_breakdown(self) -> dict[str, int]:
+        return {
+            "payload_bytes": tensor_bytes(self.key) + tensor_bytes(self.value),
+            "scale_bytes": 0,
+            "minimum_bytes": 0,
+            "residual_bytes": 0,
+            "indices_bytes": tensor_bytes(self.logical_token_ids),
+            "score_bytes": tensor_bytes(self.cumulative_scores),
+        }
+
+    @property
+    def full_precision_bytes(self) -> int:
+        return (
+            self.original_tokens * self.num_kv_heads * int(self.key.shape[-1]) * 2 * self.key.element_size()
+        )
+
+    def attention_parts(
+        self, query: torch.Tensor
+    ) -> tuple[torch.Tensor, Callable[[torch.Tensor], torch.Tensor]]:
+        """Scaled logits over the retained tokens and an AV closure
+        (physical.py:585-596); the head-major [Hkv, R, D] storage is read in
+        place through strides."""
+
+        key = self.key.transpose(0, 1)
+        value = self.value.transpose(0, 1)
+        if query.dim() != 3 or int(query.shape[1]) % self.num_kv_heads:
+            raise ValueError("GQA query heads must be divisible by KV heads")
+        logits = _dense_qk(query, key, scale=1.0 / math.sqrt(query.shape[-1]))
+
+        def apply_value(probabilities: torch.Tensor) -> torch.Tensor:
+            return gqa_probability_value(probabilities, value)
+
+        return logits, apply_value
+
+    def update_scores(self, probabilities: torch.Tensor) -> None:
+        """Accumulate the attention each surviving token receives per KV head
+        (physical.py:598-610)."""
+
+        if probabilities.dim() != 3:
+            raise ValueError("H2O probabilities must be [query_heads, queries, tokens]")
+        query_heads = int(probabilities.shape[0])
+        if query_heads % self.num_kv_heads != 0:
+            raise ValueError("Query heads must be divisible by KV heads for GQA H2O")
+        device = nat.require_device(probabilities, self.cumulative_scores, what="H2O update")
+        updated = self.cumulative_scores.float().clone()
+        nat.call(
+            "uc_h2o_colsum", probabilities.data_ptr(), nat.dtype_code(probabilities.dtype),
+            *map(int, probabilities.stride()), query_heads, int(probabilities.shape[1]),
+            self.retained_tokens, self.num_kv_heads, 1, updated.data_ptr(), nat.stream(device),
+        )
+        self.cumulative_scores = updated
+
+    def enforce_budget(self) -> None:
+        self.trim(self.heavy_tokens + self.recent_tokens, self.recent_tokens)
+
+    def request_budget(self, target_tokens: int, recent_tokens: int) -> int:
+        requested = max(1, int(target_tokens))
+        effective = min(requested, self.retained_tokens)
+        self.budget_shortfall_tokens += requested - effective
+        self.recent_tokens = min(effective, max(0, int(recent_tokens)))
+        self.heavy_tokens = effective - self.recent_tokens
+        self.enforce_budget()
+        return effective
+
+    def trim(self, target_tokens: int, recent_tokens: int) -> None:
+        """Per-head re-selection over the retained tokens (physical.py:624-654)."""
+
+        target = min(self.retained_tokens, max(1, int(target_tokens)))
+        if target >= self.retained_tokens:
+            return
+        recent = min(target, max(0, int(recent_tokens)))
+        heavy = target - recent
+        history_end = self.retained_tokens - recent
+        heavy_k = min(heavy, history_end) if heavy else 0
+        indexes = h2o_select_indices(self.cumulative_scores, heavy_k=heavy_k, recent=recent)
+        key_strides = (self.key.stride(1), self.key.stride(0), self.key.stride(2))
+        self.key, self.value, self.logical_token_ids, self.cumulative_scores = _gather(
+            self.key, self.value, key_strides, indexes, self.logical_token_ids,
+            (self.logical_token_ids.stride(0), self.logical_token_ids.stride(1)),
+            self.cumulative_scores, heads=self.num_kv_heads, head_dim=int(self.key.shape[-1]),
+        )
+
+
+PhysicalSegment = PackedKIVICache | GQAH2OCache
+
+
+@dataclass
+class PhysicalLayerCache:
+    segments: list[PhysicalSegment]
+
+    @property
+    def resident_bytes(self) -> int:
+        return sum(segment.resident_bytes for segment in self.segments)
+
+    @property
+    def full_precision_bytes(self) -> int:
+        return sum(segment.full_precision_bytes for segment in self.segments)
+
+    def add(self, segment: PhysicalSegment) -> None:
+        self.segments.append(segment)
