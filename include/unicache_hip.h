@@ -44,7 +44,6 @@ extern "C" {
 #define UC_ERUNTIME (-2)
 
 /* uc_workspace_bytes() operation codes */
-#define UC_OP_KIVI_DECODE 1
 #define UC_OP_KIVI_AV 2
 #define UC_OP_H2O_SCORES 3
 
@@ -193,7 +192,9 @@ typedef struct uc_kivi_item {
  * Replaces: the decode use of packed_kivi_attention_parts (kivi_cuda.py:238-329)
  * followed by the caller's softmax and AV (adapters/bagel.py:1205-1297), and
  * packed_kivi_quantized_attention_summary (kivi_cuda.py:96-120) for Lq small.
- * `workspace` must hold uc_workspace_bytes(UC_OP_KIVI_DECODE, 1, ...) bytes.
+ * `workspace` must hold uc_kivi_decode_workspace_bytes(1, ...) bytes.
+ * head_dim 128 with bits 2/4 and group 32/64/128 runs the MFMA kernel; other
+ * shapes a generic split-K kernel.
  */
 int uc_kivi_attn_decode(const uc_kivi_item *item_host, int bits, int group_size,
                         int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t query_len,
@@ -287,13 +288,20 @@ int uc_gqa_gather(const void *key, const void *value, int64_t k_st, int64_t k_sh
 
 /*
  * Bytes of caller-provided workspace an operation needs.
- *   UC_OP_KIVI_DECODE: (n_items, heads_q, query_len, head_dim, max_tokens)
  *   UC_OP_KIVI_AV:     (1, heads_q, query_len, head_dim, total_tokens)
  *   UC_OP_H2O_SCORES:  (1, heads_q, query_len, head_dim, tokens)
- * max_tokens is Tq + Tr of the longest item.  Returns < 0 for an unknown op.
+ * Returns < 0 for an unknown op.
  */
 int64_t uc_workspace_bytes(int op, int64_t n_items, int64_t heads_q, int64_t query_len,
                            int64_t head_dim, int64_t max_tokens);
+
+/*
+ * Bytes of workspace uc_kivi_attn_decode(_batch) needs for n_items items of
+ * at most max_quantized_tokens packed and max_residual_tokens residual keys.
+ */
+int64_t uc_kivi_decode_workspace_bytes(int64_t n_items, int bits, int group_size, int64_t heads_q,
+                                       int64_t heads_kv, int64_t head_dim, int64_t query_len,
+                                       int64_t max_quantized_tokens, int64_t max_residual_tokens);
 
 #ifdef __cplusplus
 }

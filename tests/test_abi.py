@@ -66,8 +66,13 @@ def test_decode_validation():
 
 
 def test_workspace_bytes():
-    # decode: per (item, q head, row, split) D + 2 floats; splits = ceil(T/512) + 1
-    assert nat.workspace_bytes(nat.UC_OP_KIVI_DECODE, 2, 28, 1, 128, 8192) == 2 * 28 * 1 * 17 * 130 * 4
+    # AV: per (q head, row, split) D + 2 floats; splits = ceil(T/512) + 1
+    assert nat.workspace_bytes(nat.UC_OP_KIVI_AV, 1, 28, 1, 128, 8192) == 28 * 1 * 17 * 130 * 4
+    # MFMA decode (head_dim 128, 2-bit): per (item, KV head, split) 16x128 fp16 + 16x2 fp32;
+    # 8064 packed tokens in 1024-token splits (8) + 128 residual tokens (1 split)
+    assert nat.decode_workspace_bytes(2, 2, 32, 28, 4, 128, 1, 8064, 128) == 2 * 4 * 9 * (16 * 128 * 2 + 16 * 2 * 4)
+    # other shapes: generic split-K, per (item, q head, row, split) D + 2 floats
+    assert nat.decode_workspace_bytes(1, 2, 32, 28, 4, 64, 1, 1024, 0) == 28 * 2 * 66 * 4
     assert nat.workspace_bytes(nat.UC_OP_H2O_SCORES, 1, 28, 512, 128, 4096) == 28 * 512 * 2 * 4
     with pytest.raises(ValueError):
         nat.workspace_bytes(99, 1, 1, 1, 1, 1)

@@ -28,9 +28,12 @@ def check_summary(out, lse, seg, q, *, include_residual=True, what="summary"):
 
     eo, el = A.packed_summary(seg, f32(q), include_residual=include_residual, kv_dtype="fp32")
     assert_close(f32(out), eo, what=f"{what} out (fp32 path)")
-    assert_close(f32(lse), el, max_abs=2e-3, mean_abs=5e-4, what=f"{what} lse (fp32 path)")
+    # the kernel rounds q and dequantized keys to fp16 before the MFMA
+    assert_close(f32(lse), el, max_abs=5e-3, mean_abs=1e-3, what=f"{what} lse (fp32 path)")
+    # UniCache's runtime path rounds dequantized K/V to bf16 itself; it differs
+    # from the fp32 path by up to ~1e-3 mean, so only the max bound is shared
     bo, _ = A.packed_summary(seg, f32(q), include_residual=include_residual, kv_dtype="bf16")
-    assert_close(f32(out), bo, what=f"{what} out (bf16 path)")
+    assert_close(f32(out), bo, max_abs=2e-2, mean_abs=2e-3, what=f"{what} out (bf16 path)")
 
 
 def _pair(tokens, seed, bits, group, residual, device, heads=4, head_dim=128):
@@ -80,7 +83,7 @@ def test_decode_summary_matches_parts_and_merge(device):
     probs = torch.softmax(logits, dim=-1)
     ref = apply_value(probs.to(torch.bfloat16)).transpose(0, 1)
     assert_close(f32(out), f32(ref), what="summary vs parts")
-    assert_close(f32(lse), f32(torch.logsumexp(logits, dim=-1)), max_abs=1e-3, mean_abs=1e-4, what="lse")
+    assert_close(f32(lse), f32(torch.logsumexp(logits, dim=-1)), max_abs=5e-3, mean_abs=1e-3, what="lse")
 
 
 def test_multi_query_summary(device):
@@ -155,3 +158,13 @@ def test_summaries_merge_to_full_attention(device):
     key, value = K.dequantize(seg, "bf16")
     eo, _ = A.attention_summary(f32(q), np.concatenate([key, f32(dk)]), np.concatenate([value, f32(dv)]))
     assert_close(f32(out), eo, what="merged")
+
+
+@pytest.mark.parametrize("bits,group,tokens,residual", [(2, 64, 3000, 300), (4, 128, 2500, 40), (2, 128, 640, 0),
+                                                        (4, 32, 5000, 600)])
+def test_decode_summary_groups_and_long_residual(device, bits, group, tokens, residual):
+    cache, seg = _pair(tokens, 50 + bits, bits, group, residual, device)
+    for lq in (1, 2):
+        q = queries(lq, seed=60 + lq)
+        out, lse = packed_kivi_attention_summary(cache, q.to(device))
+        check_summary(out, lse, seg, q, what=f"G{group} Lq{lq}")

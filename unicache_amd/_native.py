@@ -18,7 +18,7 @@ ABI_VERSION = 1
 
 UC_BF16, UC_FP16, UC_FP32 = 0, 1, 2
 UC_OK, UC_EINVAL, UC_ERUNTIME = 0, -1, -2
-UC_OP_KIVI_DECODE, UC_OP_KIVI_AV, UC_OP_H2O_SCORES = 1, 2, 3
+UC_OP_KIVI_AV, UC_OP_H2O_SCORES = 2, 3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -92,6 +92,7 @@ _SIGNATURES = {
         [_P, _P, _L, _L, _L, _I, _L, _L, _P, _L, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _P],
     ),
     "uc_workspace_bytes": (_L, [_I, _L, _L, _L, _L, _L]),
+    "uc_kivi_decode_workspace_bytes": (_L, [_L, _I, _I, _L, _L, _L, _L, _L, _L]),
 }
 
 _lock = threading.Lock()
@@ -195,6 +196,14 @@ def workspace_bytes(op: int, n_items: int, heads_q: int, query_len: int, head_di
     size = int(lib().uc_workspace_bytes(op, n_items, heads_q, query_len, head_dim, max_tokens))
     if size < 0:
         raise ValueError("uc_workspace_bytes: unknown operation")
+    return size
+
+
+def decode_workspace_bytes(n_items, bits, group_size, heads_q, heads_kv, head_dim, query_len, max_tq, max_tr) -> int:
+    size = int(lib().uc_kivi_decode_workspace_bytes(n_items, bits, group_size, heads_q, heads_kv, head_dim,
+                                                    query_len, max_tq, max_tr))
+    if size < 0:
+        raise ValueError("uc_kivi_decode_workspace_bytes: bad arguments")
     return size
 
 

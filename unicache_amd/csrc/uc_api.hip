@@ -39,7 +39,6 @@ extern "C" int64_t uc_workspace_bytes(int op, int64_t n_items, int64_t heads_q, 
                                       int64_t head_dim, int64_t max_tokens) {
   if (n_items < 0 || heads_q < 0 || query_len < 0 || head_dim < 0 || max_tokens < 0) return -1;
   switch (op) {
-    case UC_OP_KIVI_DECODE:
     case UC_OP_KIVI_AV: {
       int64_t splits = uc::decode_num_splits(max_tokens);
       // per (item, query head, query row, split): D partial outputs + (max, sum)
@@ -51,4 +50,21 @@ extern "C" int64_t uc_workspace_bytes(int op, int64_t n_items, int64_t heads_q, 
     default:
       return -1;
   }
+}
+
+extern "C" int64_t uc_kivi_decode_workspace_bytes(int64_t n_items, int bits, int group_size, int64_t heads_q,
+                                                  int64_t heads_kv, int64_t head_dim, int64_t query_len,
+                                                  int64_t max_quantized_tokens, int64_t max_residual_tokens) {
+  if (n_items < 0 || heads_q <= 0 || heads_kv <= 0 || head_dim <= 0 || query_len <= 0 ||
+      max_quantized_tokens < 0 || max_residual_tokens < 0)
+    return -1;
+  const int64_t rows = (heads_q / heads_kv) * query_len;
+  if (uc::decode_mfma_supported(bits, group_size, head_dim, rows)) {
+    const int64_t splits = uc::ceil_div(max_quantized_tokens, uc::decode_mfma_split_tokens(bits, uc::kDecodeMfmaNst)) +
+                           uc::ceil_div(max_residual_tokens, uc::decode_mfma_res_split_tokens());
+    return uc::decode_mfma_workspace_bytes(n_items, heads_kv, splits);
+  }
+  const int64_t splits = uc::ceil_div(max_quantized_tokens, uc::kDecodeSplitTokens) +
+                         uc::ceil_div(max_residual_tokens, uc::kDecodeSplitTokens);
+  return n_items * heads_q * query_len * splits * (head_dim + 2) * int64_t(sizeof(float));
 }

@@ -1,6 +1,9 @@
 // Split-K geometry shared by the decode kernels and uc_workspace_bytes.
 #pragma once
+#include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "../../include/unicache_hip.h"
 
 namespace uc {
 
@@ -12,5 +15,16 @@ constexpr int64_t kDecodeSplitTokens = 512;
 inline int64_t decode_num_splits(int64_t max_tokens) {
   return (max_tokens + kDecodeSplitTokens - 1) / kDecodeSplitTokens + 1;
 }
+
+// MFMA decode (uc_decode_mfma.hip): head_dim 128, 2/4-bit codes.
+constexpr int64_t kDecodeMfmaNst = 2;  // super-tiles per wave per packed split
+bool decode_mfma_supported(int bits, int group, int64_t head_dim, int64_t rows);
+int64_t decode_mfma_split_tokens(int bits, int64_t nst);
+int64_t decode_mfma_res_split_tokens();
+int64_t decode_mfma_workspace_bytes(int64_t n_items, int64_t heads_kv, int64_t splits);
+int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single, int64_t n_items, int bits,
+                       int group_size, int64_t Hq, int64_t Hkv, int64_t Lq, int q_dtype, int res_dtype,
+                       int out_dtype, float sm_scale, int64_t max_tq, int64_t max_tr, int64_t nst, void *workspace,
+                       int64_t workspace_bytes, hipStream_t stream);
 
 }  // namespace uc

@@ -390,6 +390,10 @@ int decode_common(const uc_kivi_item *items_dev, const uc_kivi_item *single, int
              "%s: query/residual must be bf16 or fp16", name);
   UC_REQUIRE(max_tq % group_size == 0, "%s: quantized tokens must be a multiple of group_size", name);
   if (n_items == 0) return UC_OK;
+  if (decode_mfma_supported(bits, group_size, D, (Hq / Hkv) * Lq))
+    return launch_decode_mfma(items_dev, single, n_items, bits, group_size, Hq, Hkv, Lq, q_dtype, res_dtype,
+                              out_dtype, sm_scale, max_tq, max_tr, kDecodeMfmaNst, workspace, workspace_bytes,
+                              stream);
   const int64_t sp_packed = ceil_div(max_tq, kDecodeSplitTokens);
   const int64_t sp_res = ceil_div(max_tr, kDecodeSplitTokens);
   const int64_t splits = sp_packed + sp_res;

@@ -60,7 +60,8 @@ class KiviDecodeBatch:
         self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
         self.max_tq = max(c.quantized_tokens for c in caches)
         self.max_tr = max(c.residual_tokens for c in caches)
-        self.ws_bytes = nat.workspace_bytes(nat.UC_OP_KIVI_DECODE, len(caches), hq, lq, d, self.max_tq + self.max_tr)
+        self.ws_bytes = nat.decode_workspace_bytes(len(caches), first.k_bits, first.group_size, hq,
+                                                   first.num_kv_heads, d, lq, self.max_tq, self.max_tr)
         self.workspace = nat.workspace(self.device, self.ws_bytes)
         self.shape = (lq, hq, d)
         self.sm_scale = 1.0 / math.sqrt(d)

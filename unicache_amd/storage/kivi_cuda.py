@@ -104,7 +104,8 @@ def _decode_summary(cache: "PackedKIVICache", query: torch.Tensor, *, include_re
         nat.ptr(cache.residual_key) if tr else None, nat.ptr(cache.residual_value) if tr else None,
         q.data_ptr(), out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr,
     )
-    ws_bytes = nat.workspace_bytes(nat.UC_OP_KIVI_DECODE, 1, hq, lq, d, cache.quantized_tokens + tr)
+    ws_bytes = nat.decode_workspace_bytes(1, cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq,
+                                          cache.quantized_tokens, tr)
     ws = nat.workspace(device, ws_bytes)
     res_dtype = cache.residual_key.dtype if tr else q.dtype
     nat.call(
