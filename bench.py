@@ -33,6 +33,11 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0
 LAYERS, BATCH, TOKENS, HKV, HQ, D = 28, 8, 8192, 4, 28, 128
 BITS, GROUP, RESIDUAL = 2, 32, 128
 
+# HBM bytes per step of the default workload from rocprofv3 PMC passes
+# (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 over both decode kernels, the factors
+# from a 1 GiB device copy); profiles/decode_batch_c1.md has the commands.
+MEASURED_TRAFFIC_BYTES = 1_172_804_608
+
 
 def make_kv(tokens, *, seed, device, heads=HKV, head_dim=D):
     """N(0,1) K with 8 random channels per head scaled x10, N(0,1) V (bf16)."""
@@ -188,8 +193,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "uc_kivi_attn_decode_batch (split-K partial + LSE combine), one launch per step",
+            "traffic": MEASURED_TRAFFIC_BYTES if args.layers == LAYERS else None,
+            "kernel": "uc_kivi_attn_decode_batch = decode_mfma_kernel + decode_mfma_combine, one call per step",
             "bytes_per_launch": step_bytes,
         },
         "per_layer_launches_gbs": round(step_bytes / (ms_layers * 1e-3) / 1e9, 2),

@@ -19,8 +19,6 @@ function (paths relative to the UniCache repository):
   top-k selection (lowest index wins ties) and the GQA gather
   (unicache/operators/physical.py, unicache/storage/physical.py,
   unicache/storage/tensor_backend.py).
-- ``oracle.stream``: residual append/flush (new semantics, pinned by the
-  invariant flush == from_dense of the prefix).
 
 How each function is pinned (golden vectors, known answers, invariants) is
 listed next to its tests in tests/test_oracle_*.py.  Parity status: every

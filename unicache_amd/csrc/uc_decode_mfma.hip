@@ -27,6 +27,7 @@
 #include "uc_common.h"
 #include "uc_decode.h"
 
+
 namespace uc {
 namespace {
 
@@ -77,6 +78,11 @@ struct MfmaParams {
 
 __device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
 
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) { return (x & m) | c; }
+
+// 2^x on the hardware exp unit; -inf gives 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ _Float16 to_h(float x) { return static_cast<_Float16>(x); }
 
 __device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
@@ -114,18 +120,19 @@ __device__ __forceinline__ void softmax_tile(f4 (&acc)[NP], const bool (&valid)[
   mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
   mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
   const float m_new = fmaxf(st.m, mx);
+  const float m_ref = m_new == kNegInf ? 0.0f : m_new;  // keeps -inf - m_ref at -inf (exp 0), never NaN
   float sum = 0.0f;
 #pragma unroll
   for (int pp = 0; pp < NP; ++pp)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const float e = acc[pp][v] == kNegInf ? 0.0f : exp2f(acc[pp][v] - m_new);
+      const float e = fast_exp2(acc[pp][v] - m_ref);
       acc[pp][v] = e;
       sum += e;
     }
   sum += __shfl_xor(sum, 16, kWave);
   sum += __shfl_xor(sum, 32, kWave);
-  const float alpha = st.m == kNegInf ? 0.0f : exp2f(st.m - m_new);
+  const float alpha = fast_exp2(st.m - m_ref);
   st.l = st.l * alpha + sum;
   st.m = m_new;
   // rescale the output rows 4k+v by the alpha of query row 4k+v
@@ -188,8 +195,8 @@ __device__ __forceinline__ h4 spread_value_codes(uint32_t word, int kap) {
     m0 = 0x000F000Fu;
     m1 = 0x00F000F0u;
   }
-  const h2 a = as_h2((y & m0) | 0x64006400u);
-  const h2 b = as_h2((y & m1) | 0x64006400u);
+  const h2 a = as_h2(and_or(y, m0, 0x64006400u));
+  const h2 b = as_h2(and_or(y, m1, 0x64006400u));
   return h4{a[0], a[1], b[0], b[1]};
 }
 
@@ -215,190 +222,254 @@ __device__ __forceinline__ h8 query_frag(const _Float16 (*sq)[kQPad], int kb, in
   return *reinterpret_cast<const h8 *>(&sq[lane & 15][32 * kb + 8 * (lane >> 4)]);
 }
 
+// Buffer resources over one (item, KV head) region: loads past `bytes` return
+// zero, which covers the token tail of the last split without branches.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int kRsrcWord3 = 0x00020000;  // 32-bit data format, raw (stride 0) addressing
+
+__device__ __forceinline__ Rsrc make_rsrc(const void *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), kRsrcWord3);
+}
+__device__ __forceinline__ uint32_t bload16(Rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload32(Rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint2 bload64(Rsrc r, uint32_t off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+__device__ __forceinline__ uint4 bload128(Rsrc r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Everything one iteration (T tokens of one KV head) reads from HBM, held in
+// registers so the next iteration's loads overlap this iteration's MFMAs.
 template <int BITS, int G>
-__device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Float16 (*sq)[kQPad],
-                                             const uc_kivi_item &it, int64_t h, int64_t t_split,
-                                             const MfmaParams &p, WaveState &st) {
+struct Prefetch {
+  using Gm = Geo<BITS>;
+  using Sh = DecShared<BITS, G>;
+  static constexpr int NKS = Sh::KG * kD / kThreads;        // key stats per thread (per stat)
+  static constexpr int NVS = Sh::T * Sh::NGD / 8;           // 16-byte chunks of value stats
+  static constexpr int VS4 = (NVS + kThreads - 1) / kThreads;
+  static constexpr int NVW = Gm::ST * Gm::VW / 4 / kWave;   // 16-byte chunks of value words per lane
+  uint32_t ks[NKS], km[NKS];
+  uint4 vs[VS4], vm[VS4];
+  uint4 vw[NVW];
+  uint32_t kw[4][8];
+};
+
+template <int BITS, int G>
+struct PackedRegion {
+  Rsrc kcode, kscale, kmin, vcode, vscale, vmin;
+  uint32_t nkw, nkg;  // key words / key groups per channel row
+};
+
+// Issue the loads of the iteration starting at token t0 (multiple of T).
+template <int BITS, int G>
+__device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedRegion<BITS, G> &rg, uint32_t t0) {
+  using Gm = Geo<BITS>;
+  using Sh = DecShared<BITS, G>;
+  using Pf = Prefetch<BITS, G>;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, kap = lane >> 4;
+  // key stats [D][nkg]: consecutive lanes read consecutive groups of one channel
+  const uint32_t kg0 = t0 / G;
+#pragma unroll
+  for (int q = 0; q < Pf::NKS; ++q) {
+    const int e = q * kThreads + tid, c = e / Sh::KG, j = e % Sh::KG;
+    const uint32_t off = (c * rg.nkg + kg0 + j) * 2u;
+    pf.ks[q] = bload16(rg.kscale, off);
+    pf.km[q] = bload16(rg.kmin, off);
+  }
+  // value stats [Tq][NGD]
+#pragma unroll
+  for (int q = 0; q < Pf::VS4; ++q) {
+    const int i = q * kThreads + tid;
+    const uint32_t off = (t0 * Sh::NGD + 8 * (i < Pf::NVS ? i : 0)) * 2u;
+    pf.vs[q] = bload128(rg.vscale, off);
+    pf.vm[q] = bload128(rg.vmin, off);
+  }
+  // value words [Tq][VW] of this wave's super-tile
+  const uint32_t tw0 = t0 + wave * Gm::ST;
+#pragma unroll
+  for (int q = 0; q < Pf::NVW; ++q) pf.vw[q] = bload128(rg.vcode, (tw0 * Gm::VW + 4 * (q * kWave + lane)) * 4u);
+  // key words [D][nkw]: lane (row r, k-slice kap) reads word J of 32 channels
+  const uint32_t J = t0 / Gm::TPW + wave * 16 + r;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) pf.kw[kb][c] = bload32(rg.kcode, ((32 * kb + 8 * kap + c) * rg.nkw + J) * 4u);
+}
+
+// Move a landed prefetch into the LDS layouts the MFMA loops read.
+template <int BITS, int G>
+__device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch<BITS, G> &pf) {
+  using Gm = Geo<BITS>;
+  using Sh = DecShared<BITS, G>;
+  using Pf = Prefetch<BITS, G>;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, kap = lane >> 4;
+#pragma unroll
+  for (int q = 0; q < Pf::NKS; ++q) {
+    const int e = q * kThreads + tid, c = e / Sh::KG, j = e % Sh::KG;
+    sh.ks[j][c] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(pf.ks[q]));
+    sh.km[j][c] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(pf.km[q]));
+  }
+#pragma unroll
+  for (int q = 0; q < Pf::VS4; ++q) {
+    if (q * kThreads + tid >= Pf::NVS) break;
+    const int e0 = 8 * (q * kThreads + tid);
+    const uint32_t sw[4] = {pf.vs[q].x, pf.vs[q].y, pf.vs[q].z, pf.vs[q].w};
+    const uint32_t mw[4] = {pf.vm[q].x, pf.vm[q].y, pf.vm[q].z, pf.vm[q].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tl = (e0 + e) / Sh::NGD, gd = (e0 + e) % Sh::NGD;
+      sh.vs[gd][tl % Gm::TPW][tl / Gm::TPW] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sw[e / 2] >> (16 * (e % 2))));
+      sh.vm[gd][tl % Gm::TPW][tl / Gm::TPW] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(mw[e / 2] >> (16 * (e % 2))));
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < Pf::NVW; ++q) {
+    const int i = q * kWave + lane;
+    const int tok = (4 * i) / Gm::VW, word = (4 * i) % Gm::VW;  // token within the super-tile
+    *reinterpret_cast<uint4 *>(&sh.vw[wave][tok % Gm::TPW][tok / Gm::TPW][word]) = pf.vw[q];
+  }
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    uint4 *dst = reinterpret_cast<uint4 *>(&sh.kw[wave][kb][kap][r][0]);
+    dst[0] = make_uint4(pf.kw[kb][0], pf.kw[kb][1], pf.kw[kb][2], pf.kw[kb][3]);
+    dst[1] = make_uint4(pf.kw[kb][4], pf.kw[kb][5], pf.kw[kb][6], pf.kw[kb][7]);
+  }
+}
+
+// Logits, softmax and P.V of one staged iteration (this wave's super-tile).
+template <int BITS, int G>
+__device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const _Float16 (*sq)[kQPad],
+                                             uint32_t t0, uint32_t nkw, float scale_log2, WaveState &st) {
   using Gm = Geo<BITS>;
   using Sh = DecShared<BITS, G>;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
-  const int64_t Tq = it.quantized_tokens;
-  const int64_t nkw = Tq / Gm::TPW;  // key words per channel row
-  const int64_t nkg = Tq / G;        // key groups per channel row
-  const uint32_t *kcode = static_cast<const uint32_t *>(it.key_code);
-  const uint16_t *kscale = static_cast<const uint16_t *>(it.key_scale);
-  const uint16_t *kmin = static_cast<const uint16_t *>(it.key_min);
-  const uint32_t *vcode = static_cast<const uint32_t *>(it.value_code);
-  const uint16_t *vscale = static_cast<const uint16_t *>(it.value_scale);
-  const uint16_t *vmin = static_cast<const uint16_t *>(it.value_min);
   const h4 sel = transpose_selector<BITS>(lane);
   // the transposition returns code + 1024/scale; seeding its accumulator with
   // minus that offset (per column) makes it return the code itself
   const float off = (r & 1) ? (BITS == 2 ? 256.0f : 64.0f) : 1024.0f;
   const f4 neg_off = f4{-off, -off, -off, -off};
   constexpr int NP = Gm::TPW / 2;  // positions per half word
-
-  for (int64_t it_st = 0; it_st < p.nst; ++it_st) {
-    const int64_t t0 = t_split + it_st * Sh::T;  // first token of this iteration
-    // ---- issue every HBM load of the iteration before waiting on any
-    uint32_t ks_r[Sh::KG / 2], km_r[Sh::KG / 2];  // key stats of channel tid, two groups per register
-    {
-      const int64_t kg0 = t0 / G;
-      const int64_t off_s = (h * kD + tid) * nkg + kg0;
+  const int gl = ((wave * 16 + r) * Gm::TPW) / G;  // key group of this lane's row
+  bool valid[4];
 #pragma unroll
-      for (int g = 0; g < Sh::KG; g += 2) {
-        const bool ok0 = kg0 + g < nkg, ok1 = kg0 + g + 1 < nkg;
-        ks_r[g / 2] = (ok0 ? uint32_t(kscale[off_s + g]) : 0u) | ((ok1 ? uint32_t(kscale[off_s + g + 1]) : 0u) << 16);
-        km_r[g / 2] = (ok0 ? uint32_t(kmin[off_s + g]) : 0u) | ((ok1 ? uint32_t(kmin[off_s + g + 1]) : 0u) << 16);
-      }
-    }
-    constexpr int NVS = Sh::T * Sh::NGD / 8;  // uint4 of value stats
-    constexpr int VS4 = (NVS + kThreads - 1) / kThreads;
-    uint4 vs_r[VS4], vm_r[VS4];
+  for (int v = 0; v < 4; ++v) valid[v] = (t0 / Gm::TPW + wave * 16 + 4 * kap + v) < nkw;
+#pragma unroll 1
+  for (int half = 0; half < 2; ++half) {
+    // ---- keys: logits for 16 word rows x NP positions x 16 query rows
+    f4 acc[NP];
 #pragma unroll
-    for (int q = 0; q < VS4; ++q) {
-      const int i = q * kThreads + tid;
-      const bool ok = i < NVS && t0 + (8 * i + 8) / Sh::NGD <= Tq;
-      const int64_t o = (h * Tq + t0) * Sh::NGD + 8 * i;
-      vs_r[q] = ok ? *reinterpret_cast<const uint4 *>(vscale + o) : make_uint4(0, 0, 0, 0);
-      vm_r[q] = ok ? *reinterpret_cast<const uint4 *>(vmin + o) : make_uint4(0, 0, 0, 0);
-    }
-    const int64_t tw0 = t0 + wave * Gm::ST;  // first token of this wave's super-tile
-    constexpr int kN4 = Gm::ST * Gm::VW / 4 / kWave;
-    uint4 vw_r[kN4];
-    {
-      const uint4 *src = reinterpret_cast<const uint4 *>(vcode + (h * Tq + tw0) * Gm::VW);
-#pragma unroll
-      for (int q = 0; q < kN4; ++q) {
-        const int i = q * kWave + lane;
-        vw_r[q] = tw0 + (4 * i) / Gm::VW < Tq ? src[i] : make_uint4(0, 0, 0, 0);
-      }
-    }
-    const int64_t J = t0 / Gm::TPW + wave * 16 + r;  // key word of this lane's MFMA row
-    const bool jok = J < nkw;
-    const uint32_t *krow = kcode + (h * kD + 8 * kap) * nkw + J;
-    uint32_t kw_r[4][8];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int c = 0; c < 8; ++c) kw_r[kb][c] = jok ? krow[(32 * kb + c) * nkw] : 0u;
-
-    // ---- stage into LDS
-    __syncthreads();  // the previous iteration is done with LDS
-#pragma unroll
-    for (int g = 0; g < Sh::KG; ++g) {
-      sh.ks[g][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(ks_r[g / 2] >> (16 * (g % 2))));
-      sh.km[g][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(km_r[g / 2] >> (16 * (g % 2))));
-    }
-#pragma unroll
-    for (int q = 0; q < VS4; ++q) {
-      if (q * kThreads + tid >= NVS) break;
-      const int e0 = 8 * (q * kThreads + tid);
-      const uint32_t sw[4] = {vs_r[q].x, vs_r[q].y, vs_r[q].z, vs_r[q].w};
-      const uint32_t mw[4] = {vm_r[q].x, vm_r[q].y, vm_r[q].z, vm_r[q].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int tl = (e0 + e) / Sh::NGD, gd = (e0 + e) % Sh::NGD;
-        sh.vs[gd][tl % Gm::TPW][tl / Gm::TPW] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sw[e / 2] >> (16 * (e % 2))));
-        sh.vm[gd][tl % Gm::TPW][tl / Gm::TPW] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(mw[e / 2] >> (16 * (e % 2))));
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < kN4; ++q) {
-      const int i = q * kWave + lane;
-      const int tok = (4 * i) / Gm::VW, word = (4 * i) % Gm::VW;  // token within the super-tile
-      *reinterpret_cast<uint4 *>(&sh.vw[wave][tok % Gm::TPW][tok / Gm::TPW][word]) = vw_r[q];
-    }
-#pragma unroll
+    for (int q = 0; q < NP; ++q) acc[q] = f4{0, 0, 0, 0};
+    const uint32_t sel_half = half ? 0x07060302u : 0x05040100u;
+#pragma unroll 1
     for (int kb = 0; kb < 4; ++kb) {
-      uint4 *dst = reinterpret_cast<uint4 *>(&sh.kw[wave][kb][kap][r][0]);
-      dst[0] = make_uint4(kw_r[kb][0], kw_r[kb][1], kw_r[kb][2], kw_r[kb][3]);
-      dst[1] = make_uint4(kw_r[kb][4], kw_r[kb][5], kw_r[kb][6], kw_r[kb][7]);
-    }
-    __syncthreads();
-
-    const int gl = ((wave * 16 + r) * Gm::TPW) / G;  // key group of this lane's row
-    bool valid[4];
+      const uint4 *kp = reinterpret_cast<const uint4 *>(&sh.kw[wave][kb][kap][r][0]);
+      const uint4 w0 = kp[0], w1 = kp[1];
+      const uint32_t kw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      const h8 s8 = *reinterpret_cast<const h8 *>(&sh.ks[gl][32 * kb + 8 * kap]);
+      const h8 m8 = *reinterpret_cast<const h8 *>(&sh.km[gl][32 * kb + 8 * kap]);
+      const h8 qfrag = query_frag(sq, kb, lane);
+      uint32_t y[4];
+      h2 sp[4], mp[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) valid[v] = (t0 / Gm::TPW + wave * 16 + 4 * kap + v) < nkw;
-#pragma unroll 1
-    for (int half = 0; half < 2; ++half) {
-      // ---- keys: logits for 16 word rows x NP positions x 16 query rows
-      f4 acc[NP];
-#pragma unroll
-      for (int q = 0; q < NP; ++q) acc[q] = f4{0, 0, 0, 0};
-      const uint32_t sel_half = half ? 0x07060302u : 0x05040100u;
-#pragma unroll 1
-      for (int kb = 0; kb < 4; ++kb) {
-        const uint4 *kp = reinterpret_cast<const uint4 *>(&sh.kw[wave][kb][kap][r][0]);
-        const uint4 w0 = kp[0], w1 = kp[1];
-        const uint32_t kw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        const h8 s8 = *reinterpret_cast<const h8 *>(&sh.ks[gl][32 * kb + 8 * kap]);
-        const h8 m8 = *reinterpret_cast<const h8 *>(&sh.km[gl][32 * kb + 8 * kap]);
-        const h8 qfrag = query_frag(sq, kb, lane);
-        uint32_t y[4];
-        h2 sp[4], mp[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          y[u] = __builtin_amdgcn_perm(kw[2 * u + 1], kw[2 * u], sel_half);
-          sp[u] = h2{s8[2 * u], s8[2 * u + 1]};
-          mp[u] = h2{m8[2 * u], m8[2 * u + 1]};
-        }
-#pragma unroll
-        for (int pq = 0; pq < NP; ++pq) {
-          const bool direct = pq <= Gm::PMAX;
-          const int pe = direct ? pq : pq - (Gm::PMAX + 1);
-          const uint32_t mask = (Gm::MASK << (BITS * pe)) | (Gm::MASK << (16 + BITS * pe));
-          const _Float16 inv = to_h(1.0f / float(1u << (BITS * pe)));
-          h8 a;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const uint32_t src = direct ? y[u] : (y[u] >> Gm::SH);
-            const h2 x = as_h2((src & mask) | 0x64006400u) - h2{to_h(1024.0f), to_h(1024.0f)};
-            const h2 k = __builtin_elementwise_fma(x, sp[u] * h2{inv, inv}, mp[u]);
-            a[2 * u] = k[0];
-            a[2 * u + 1] = k[1];
-          }
-          acc[pq] = mfma32(a, qfrag, acc[pq]);
-        }
+      for (int u = 0; u < 4; ++u) {
+        y[u] = __builtin_amdgcn_perm(kw[2 * u + 1], kw[2 * u], sel_half);
+        sp[u] = h2{s8[2 * u], s8[2 * u + 1]};
+        mp[u] = h2{m8[2 * u], m8[2 * u + 1]};
       }
-      softmax_tile<NP>(acc, valid, p.scale_log2, st, lane);
-
-      // ---- values of these positions
-      const int jw = wave * 16 + 4 * kap;
 #pragma unroll
       for (int pq = 0; pq < NP; ++pq) {
-        const int pp = half * NP + pq;
-        const h4 ap = cvt4(acc[pq]);  // A: rows = query rows, k = word rows 4k..4k+3 at position pp
-        h4 as[Sh::NGD];
+        const bool direct = pq <= Gm::PMAX;
+        const int pe = direct ? pq : pq - (Gm::PMAX + 1);
+        const uint32_t mask = (Gm::MASK << (BITS * pe)) | (Gm::MASK << (16 + BITS * pe));
+        const _Float16 inv = to_h(1.0f / float(1u << (BITS * pe)));
+        h8 a;
 #pragma unroll
-        for (int gd = 0; gd < Sh::NGD; ++gd)
-          as[gd] = ap * *reinterpret_cast<const h4 *>(&sh.vs[gd][pp][jw]);
-        const h4 bm = r < Sh::NGD ? *reinterpret_cast<const h4 *>(&sh.vm[r < Sh::NGD ? r : 0][pp][jw])
-                                  : h4{to_h(0.0f), to_h(0.0f), to_h(0.0f), to_h(0.0f)};
-        st.cmin = mfma16(ap, bm, st.cmin);
-        // the word holding channel block blk for this lane's k-slice: 2-bit rows
-        // keep 16 channels per word, 4-bit rows 8 (even/odd word by k-slice pair)
-        uint32_t words[8];
-        if constexpr (BITS == 2) {
-          const uint4 *row = reinterpret_cast<const uint4 *>(&sh.vw[wave][pp][r][0]);
-          const uint4 a = row[0], b = row[1];
-          words[0] = a.x; words[1] = a.y; words[2] = a.z; words[3] = a.w;
-          words[4] = b.x; words[5] = b.y; words[6] = b.z; words[7] = b.w;
-        } else {
-          const uint32_t *row = &sh.vw[wave][pp][r][kap >> 1];
-#pragma unroll
-          for (int blk = 0; blk < 8; ++blk) words[blk] = row[2 * blk];
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t src = direct ? y[u] : (y[u] >> Gm::SH);
+          const h2 x = as_h2(and_or(src, mask, 0x64006400u)) - h2{to_h(1024.0f), to_h(1024.0f)};
+          const h2 k = __builtin_elementwise_fma(x, sp[u] * h2{inv, inv}, mp[u]);
+          a[2 * u] = k[0];
+          a[2 * u + 1] = k[1];
         }
-#pragma unroll
-        for (int blk = 0; blk < 8; ++blk) {
-          const h4 x = spread_value_codes<BITS>(words[blk], kap);
-          const f4 ct = mfma16(x, sel, neg_off);
-          st.o[blk] = mfma16(as[(16 * blk) / G], cvt4(ct), st.o[blk]);
-        }
+        acc[pq] = mfma32(a, qfrag, acc[pq]);
       }
     }
+    softmax_tile<NP>(acc, valid, scale_log2, st, lane);
+
+    // ---- values of these positions
+    const int jw = wave * 16 + 4 * kap;
+#pragma unroll
+    for (int pq = 0; pq < NP; ++pq) {
+      const int pp = half * NP + pq;
+      const h4 ap = cvt4(acc[pq]);  // A: rows = query rows, k = word rows 4k..4k+3 at position pp
+      h4 as[Sh::NGD];
+#pragma unroll
+      for (int gd = 0; gd < Sh::NGD; ++gd) as[gd] = ap * *reinterpret_cast<const h4 *>(&sh.vs[gd][pp][jw]);
+      const h4 bm = r < Sh::NGD ? *reinterpret_cast<const h4 *>(&sh.vm[r < Sh::NGD ? r : 0][pp][jw])
+                                : h4{to_h(0.0f), to_h(0.0f), to_h(0.0f), to_h(0.0f)};
+      st.cmin = mfma16(ap, bm, st.cmin);
+      // the word holding channel block blk for this lane's k-slice: 2-bit rows
+      // keep 16 channels per word, 4-bit rows 8 (even/odd word by k-slice pair)
+      uint32_t words[8];
+      if constexpr (BITS == 2) {
+        const uint4 *row = reinterpret_cast<const uint4 *>(&sh.vw[wave][pp][r][0]);
+        const uint4 a = row[0], b = row[1];
+        words[0] = a.x; words[1] = a.y; words[2] = a.z; words[3] = a.w;
+        words[4] = b.x; words[5] = b.y; words[6] = b.z; words[7] = b.w;
+      } else {
+        const uint32_t *row = &sh.vw[wave][pp][r][kap >> 1];
+#pragma unroll
+        for (int blk = 0; blk < 8; ++blk) words[blk] = row[2 * blk];
+      }
+      // all eight transpositions first, so their latency overlaps
+      f4 ct[8];
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk) ct[blk] = mfma16(spread_value_codes<BITS>(words[blk], kap), sel, neg_off);
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk) st.o[blk] = mfma16(as[(16 * blk) / G], cvt4(ct[blk]), st.o[blk]);
+    }
+  }
+}
+
+template <int BITS, int G>
+__device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Float16 (*sq)[kQPad],
+                                             const uc_kivi_item &it, int64_t h, int64_t t_split,
+                                             const MfmaParams &p, WaveState &st) {
+  using Gm = Geo<BITS>;
+  using Sh = DecShared<BITS, G>;
+  const int lane = threadIdx.x & 63;
+  const int64_t Tq = it.quantized_tokens;
+  PackedRegion<BITS, G> rg;
+  rg.nkw = static_cast<uint32_t>(Tq / Gm::TPW);
+  rg.nkg = static_cast<uint32_t>(Tq / G);
+  const int64_t kcode_bytes = int64_t(kD) * rg.nkw * 4, kstat_bytes = int64_t(kD) * rg.nkg * 2;
+  const int64_t vcode_bytes = Tq * Gm::VW * 4, vstat_bytes = Tq * Sh::NGD * 2;
+  rg.kcode = make_rsrc(static_cast<const char *>(it.key_code) + h * kcode_bytes, kcode_bytes);
+  rg.kscale = make_rsrc(static_cast<const char *>(it.key_scale) + h * kstat_bytes, kstat_bytes);
+  rg.kmin = make_rsrc(static_cast<const char *>(it.key_min) + h * kstat_bytes, kstat_bytes);
+  rg.vcode = make_rsrc(static_cast<const char *>(it.value_code) + h * vcode_bytes, vcode_bytes);
+  rg.vscale = make_rsrc(static_cast<const char *>(it.value_scale) + h * vstat_bytes, vstat_bytes);
+  rg.vmin = make_rsrc(static_cast<const char *>(it.value_min) + h * vstat_bytes, vstat_bytes);
+  const int64_t left = Tq - t_split;
+  const int n_it = static_cast<int>(min<int64_t>(p.nst, (left + Sh::T - 1) / Sh::T));
+  Prefetch<BITS, G> pf;
+  issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(t_split));
+  for (int i = 0; i < n_it; ++i) {
+    const uint32_t t0 = static_cast<uint32_t>(t_split + int64_t(i) * Sh::T);
+    __syncthreads();  // every wave is done reading the previous iteration from LDS
+    stage_lds<BITS, G>(sh, pf);
+    __syncthreads();
+    if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, t0 + Sh::T);  // lands while this iteration computes
+    compute_tile<BITS, G>(sh, sq, t0, rg.nkw, p.scale_log2, st);
   }
   // fold the value minima back in: sum_t P*min of group gd sits in column gd
 #pragma unroll
@@ -411,10 +482,11 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
 
 // --------------------------------------------------------- residual path --
 // Dense residual tokens [tw, tw + kResWaveTokens) of this wave ([Tr, Hkv, 128]
-// contiguous, bf16 or fp16), converted to fp16 for the same MFMAs.
+// contiguous, bf16 or fp16), converted to fp16 for the same MFMAs; rows past
+// Tr read as zero through the buffer range check and are masked.
 template <int RD>
-__device__ __forceinline__ h8 load8_h(const void *p, int64_t i) {
-  const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
+__device__ __forceinline__ h8 load8_h(Rsrc r, uint32_t off) {
+  const uint4 raw = bload128(r, off);
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
   h8 out;
 #pragma unroll
@@ -426,8 +498,8 @@ __device__ __forceinline__ h8 load8_h(const void *p, int64_t i) {
 }
 
 template <int RD>
-__device__ __forceinline__ h4 load4_h(const void *p, int64_t i) {
-  const uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(p) + i);
+__device__ __forceinline__ h4 load4_h(Rsrc r, uint32_t off) {
+  const uint2 raw = bload64(r, off);
   return h4{to_h(half_bits_to_f32<RD>(raw.x)), to_h(half_bits_to_f32<RD>(raw.x >> 16)),
             to_h(half_bits_to_f32<RD>(raw.y)), to_h(half_bits_to_f32<RD>(raw.y >> 16))};
 }
@@ -438,6 +510,8 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
   const int64_t Tr = it.residual_tokens;
+  const int64_t bytes = Tr * p.Hkv * kD * 2;
+  const Rsrc rk = make_rsrc(it.residual_key, bytes), rv = make_rsrc(it.residual_value, bytes);
   const int64_t tw = tr0 + wave * kResWaveTokens;
   constexpr int kBlocks = kResWaveTokens / 16;
   const h4 ident = identity_selector(lane);
@@ -445,20 +519,17 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
 #pragma unroll
   for (int b = 0; b < kBlocks; ++b) {
     acc[b] = f4{0, 0, 0, 0};
-    const int64_t t = tw + 16 * b + r;
-    const int64_t base = ((t < Tr ? t : 0) * p.Hkv + h) * kD;  // rows past Tr read token 0, masked below
+    const uint32_t base = static_cast<uint32_t>(((tw + 16 * b + r) * p.Hkv + h) * kD * 2);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-      acc[b] = mfma32(load8_h<RD>(it.residual_key, base + 32 * kb + 8 * kap), query_frag(sq, kb, lane), acc[b]);
+      acc[b] = mfma32(load8_h<RD>(rk, base + (32 * kb + 8 * kap) * 2), query_frag(sq, kb, lane), acc[b]);
   }
-  bool valid_any = false;
   float mx = kNegInf;
 #pragma unroll
   for (int b = 0; b < kBlocks; ++b)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const bool ok = tw + 16 * b + 4 * kap + v < Tr;
-      valid_any |= ok;
       const float x = ok ? acc[b][v] * p.scale_log2 : kNegInf;
       acc[b][v] = x;
       mx = fmaxf(mx, x);
@@ -478,15 +549,13 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
   sum += __shfl_xor(sum, 32, kWave);
   st.m = mx;
   st.l = sum;
-  (void)valid_any;
 #pragma unroll
   for (int b = 0; b < kBlocks; ++b) {
     const h4 ap = cvt4(acc[b]);
-    const int64_t t = tw + 16 * b + r;
-    const int64_t base = ((t < Tr ? t : 0) * p.Hkv + h) * kD;
+    const uint32_t base = static_cast<uint32_t>(((tw + 16 * b + r) * p.Hkv + h) * kD * 2);
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
-      const f4 ct = mfma16(load4_h<RD>(it.residual_value, base + 16 * blk + 4 * kap), ident, f4{0, 0, 0, 0});
+      const f4 ct = mfma16(load4_h<RD>(rv, base + (16 * blk + 4 * kap) * 2), ident, f4{0, 0, 0, 0});
       st.o[blk] = mfma16(ap, cvt4(ct), st.o[blk]);
     }
   }
@@ -496,7 +565,7 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
 static_assert(kThreads == kD, "key-stat staging maps one thread per channel");
 
 template <int BITS, int G, int RD, bool TABLE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_mfma_kernel(
     const uc_kivi_item *items, uc_kivi_item single, MfmaParams p) {
   __shared__ DecShared<BITS, G> sh;
   __shared__ _Float16 sq[16][kQPad];
@@ -694,6 +763,10 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   p.scale_log2 = sm_scale * kLog2e;
   p.qd = q_dtype; p.rd = res_dtype; p.od = out_dtype;
   if (p.splits_total == 0) return UC_OK;
+  // buffer offsets are 32-bit: one KV head's packed rows and the whole residual must fit
+  UC_REQUIRE(max_tq * (kD / 8) * 4 < (int64_t(1) << 31) && max_tr * Hkv * kD * 2 < (int64_t(1) << 31),
+             "decode: segment too long for 32-bit buffer offsets (%lld packed, %lld residual tokens)",
+             (long long)max_tq, (long long)max_tr);
   const int64_t need = decode_mfma_workspace_bytes(n_items, Hkv, p.splits_total);
   UC_REQUIRE(workspace != nullptr && workspace_bytes >= need, "decode: workspace too small (%lld < %lld bytes)",
              (long long)workspace_bytes, (long long)need);
