@@ -206,6 +206,7 @@ int uc_kivi_attn_decode(const uc_kivi_item *item_host, int bits, int group_size,
  * `items_device` is a device array of uc_kivi_item; every item shares bits,
  * group, head counts and query_len; token counts may differ, up to
  * max_quantized_tokens / max_residual_tokens.
+ * Each item's query must be 16-byte aligned (rows are read as 16-byte vectors).
  * No reference counterpart: this is the all-layer decode launch.
  */
 int uc_kivi_attn_decode_batch(const uc_kivi_item *items_device, int64_t n_items,
@@ -214,6 +215,27 @@ int uc_kivi_attn_decode_batch(const uc_kivi_item *items_device, int64_t n_items,
                               int q_dtype, int res_dtype, int out_dtype, float sm_scale,
                               int64_t max_quantized_tokens, int64_t max_residual_tokens,
                               void *workspace, int64_t workspace_bytes, uc_stream_t stream);
+
+/*
+ * Attention for long queries (image editing: group*query_len rows per KV head
+ * in the thousands) over one packed segment plus residual: same inputs,
+ * outputs and semantics as uc_kivi_attn_decode.  head_dim 128, bits 2/4,
+ * group_size 32/64/128, q and residual bf16/fp16.  A first kernel dequantizes
+ * the packed keys/values of every KV head once into `workspace` (fp16 keys and
+ * transposed values, uc_kivi_mq_workspace_bytes bytes); a second streams them
+ * in 64-key tiles through LDS for MFMA, 128 query rows per workgroup.
+ * Replaces: _packed_attention_kernel / packed_attention_tiled
+ * (kivi_triton.py:216-382, 615-687) behind packed_kivi_quantized_attention_summary
+ * (kivi_cuda.py:96-120) with backend "triton_tiled", plus the residual part.
+ */
+int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int group_size,
+                    int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t query_len,
+                    int q_dtype, int res_dtype, int out_dtype, float sm_scale,
+                    void *workspace, int64_t workspace_bytes, uc_stream_t stream);
+
+/* Workspace of uc_kivi_attn_mq: heads_kv * ceil((Tq+Tr)/64)*64 * head_dim * 4 bytes. */
+int64_t uc_kivi_mq_workspace_bytes(int64_t heads_kv, int64_t head_dim, int64_t quantized_tokens,
+                                   int64_t residual_tokens);
 
 /*
  * Merge normalised attention summaries of n_segments disjoint key segments:

@@ -24,16 +24,19 @@ pytestmark = pytest.mark.gpu
 def check_summary(out, lse, seg, q, *, include_residual=True, what="summary"):
     """Outputs within 2e-2 max / 1e-3 mean of the fp32 dequant path (the
     contract) and of the bf16-dequant runtime path of UniCache; the natural
-    LSE within 2e-3 of the fp32 path."""
+    LSE within 1e-2 max / 1e-3 mean of the fp32 path."""
 
     eo, el = A.packed_summary(seg, f32(q), include_residual=include_residual, kv_dtype="fp32")
     assert_close(f32(out), eo, what=f"{what} out (fp32 path)")
-    # the kernel rounds q and dequantized keys to fp16 before the MFMA
-    assert_close(f32(lse), el, max_abs=5e-3, mean_abs=1e-3, what=f"{what} lse (fp32 path)")
-    # UniCache's runtime path rounds dequantized K/V to bf16 itself; it differs
-    # from the fp32 path by up to ~1e-3 mean, so only the max bound is shared
+    # the kernels round dequantized keys to fp16 before the MFMA (UniCache's
+    # runtime rounds them to bf16, 8x coarser): with x10 outlier channels a key
+    # of ~40 carries up to 0.016 of rounding, ~5e-3 on the largest of ~3e4 LSEs
+    assert_close(f32(lse), el, max_abs=1e-2, mean_abs=1e-3, what=f"{what} lse (fp32 path)")
+    # UniCache's runtime path rounds dequantized K/V to bf16 itself; over the
+    # ~4e6 outputs of config 2 it strays from the fp32 path by up to ~3e-2, so
+    # against it the bounds are looser
     bo, _ = A.packed_summary(seg, f32(q), include_residual=include_residual, kv_dtype="bf16")
-    assert_close(f32(out), bo, max_abs=2e-2, mean_abs=2e-3, what=f"{what} out (bf16 path)")
+    assert_close(f32(out), bo, max_abs=5e-2, mean_abs=2e-3, what=f"{what} out (bf16 path)")
 
 
 def _pair(tokens, seed, bits, group, residual, device, heads=4, head_dim=128):
@@ -168,3 +171,51 @@ def test_decode_summary_groups_and_long_residual(device, bits, group, tokens, re
         q = queries(lq, seed=60 + lq)
         out, lse = packed_kivi_attention_summary(cache, q.to(device))
         check_summary(out, lse, seg, q, what=f"G{group} Lq{lq}")
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_mq_config2_editing(device, bits):
+    # config 2's packed segment: 1024 source-VAE tokens (896 packed + 128 residual),
+    # 1088 queries x 28 heads (7616 query rows per KV head) through uc_kivi_attn_mq
+    cache, seg = _pair(1024, 70 + bits, bits, 32, 128, device)
+    assert (cache.quantized_tokens, cache.residual_tokens) == (896, 128)
+    q = queries(1088, seed=71)
+    out, lse = packed_kivi_attention_summary(cache, q.to(device))
+    assert tuple(out.shape) == (1088, 28, 128) and tuple(lse.shape) == (28, 1088)
+    check_summary(out, lse, seg, q, what=f"mq c2 {bits}-bit")
+    po, pl = packed_kivi_quantized_attention_summary(cache, q.to(device))
+    check_summary(po, pl, seg, q, include_residual=False, what=f"mq c2 packed-only {bits}-bit")
+
+
+@pytest.mark.parametrize("bits,group,tokens,residual,lq", [(2, 32, 500, 20, 20), (4, 128, 700, 50, 3),
+                                                           (2, 64, 1300, 130, 130), (4, 32, 96, 64, 300)])
+def test_mq_ragged_tiles_and_rows(device, bits, group, tokens, residual, lq):
+    # packed and residual lengths that end inside a 64-key tile, query rows that
+    # end inside a 128-row workgroup
+    cache, seg = _pair(tokens, 80 + lq, bits, group, residual, device)
+    q = queries(lq, seed=81)
+    out, lse = packed_kivi_attention_summary(cache, q.to(device))
+    check_summary(out, lse, seg, q, what=f"mq G{group} T{tokens} Lq{lq}")
+
+
+def test_mq_fp16_inputs(device):
+    key, value = kv_pair(800, seed=90, dtype=torch.float16)
+    cache = PackedKIVICache.from_dense(key.to(device), value.to(device), logical_token_ids=torch.arange(800),
+                                       token_type_id=3, k_bits=2, v_bits=2, group_size=32,
+                                       residual_length=128, backend="cuda")
+    seg = K.from_dense(f32(key), f32(value), k_bits=2, v_bits=2, group_size=32, residual_length=128,
+                       in_dtype="fp16")
+    q = queries(64, seed=91, dtype=torch.float16)
+    out, lse = packed_kivi_attention_summary(cache, q.to(device))
+    assert out.dtype == torch.float16
+    eo, el = A.packed_summary(seg, f32(q), include_residual=True, kv_dtype="fp32")
+    assert_close(f32(out), eo, what="mq fp16")
+    assert_close(f32(lse), el, max_abs=5e-3, mean_abs=1e-3, what="mq fp16 lse")
+
+
+def test_mq_is_deterministic(device):
+    cache, _ = _pair(1024, 95, 2, 32, 128, device)
+    q = queries(200, seed=96).to(device)
+    a, la = packed_kivi_attention_summary(cache, q)
+    b, lb = packed_kivi_attention_summary(cache, q)
+    assert torch.equal(a, b) and torch.equal(la, lb)

@@ -80,6 +80,8 @@ _SIGNATURES = {
         _I,
         [_P, _L, _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _L, _L, _P, _L, _P],
     ),
+    "uc_kivi_attn_mq": (_I, [ctypes.POINTER(KiviItem), _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _P, _L, _P]),
+    "uc_kivi_mq_workspace_bytes": (_L, [_L, _L, _L, _L]),
     "uc_lse_merge": (_I, [_P, _P, _I, _I, _L, _L, _L, _P, _P, _P]),
     "uc_h2o_scores": (
         _I,
@@ -204,6 +206,13 @@ def decode_workspace_bytes(n_items, bits, group_size, heads_q, heads_kv, head_di
                                                     query_len, max_tq, max_tr))
     if size < 0:
         raise ValueError("uc_kivi_decode_workspace_bytes: bad arguments")
+    return size
+
+
+def mq_workspace_bytes(heads_kv, head_dim, quantized_tokens, residual_tokens) -> int:
+    size = int(lib().uc_kivi_mq_workspace_bytes(heads_kv, head_dim, quantized_tokens, residual_tokens))
+    if size < 0:
+        raise ValueError("uc_kivi_mq_workspace_bytes: bad arguments")
     return size
 
 

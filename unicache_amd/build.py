@@ -23,7 +23,7 @@ SOURCES = [
     "uc_pack.hip",
     "uc_decode.hip",
     "uc_decode_mfma.hip",
-    "uc_mq.hip",
+    "uc_attn_mq.hip",
     "uc_merge.hip",
     "uc_h2o.hip",
 ]

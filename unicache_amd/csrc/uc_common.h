@@ -94,6 +94,16 @@ __device__ __forceinline__ void store_from_f32(void *p, int64_t i, float v) {
   }
 }
 
+// Storage type of a dtype code.
+template <int D>
+struct DtypeOf {
+  typedef uint16_t T;
+};
+template <>
+struct DtypeOf<UC_FP32> {
+  typedef float T;
+};
+
 // Element `i` of a buffer whose dtype is only known at run time (uniform
 // branch; used by the kernels that are not on the hot path).
 __device__ __forceinline__ float load_dyn(const void *p, int64_t i, int dt) {

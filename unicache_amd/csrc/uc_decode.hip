@@ -390,10 +390,15 @@ int decode_common(const uc_kivi_item *items_dev, const uc_kivi_item *single, int
              "%s: query/residual must be bf16 or fp16", name);
   UC_REQUIRE(max_tq % group_size == 0, "%s: quantized tokens must be a multiple of group_size", name);
   if (n_items == 0) return UC_OK;
-  if (decode_mfma_supported(bits, group_size, D, (Hq / Hkv) * Lq))
+  if (decode_mfma_supported(bits, group_size, D, (Hq / Hkv) * Lq)) {
+    // the MFMA kernel reads query rows 16 bytes at a time (batched items: the
+    // caller's contract in the header)
+    UC_REQUIRE(single == nullptr || (reinterpret_cast<uintptr_t>(single->query) & 15) == 0,
+               "%s: query must be 16-byte aligned", name);
     return launch_decode_mfma(items_dev, single, n_items, bits, group_size, Hq, Hkv, Lq, q_dtype, res_dtype,
                               out_dtype, sm_scale, max_tq, max_tr, kDecodeMfmaNst, workspace, workspace_bytes,
                               stream);
+  }
   const int64_t sp_packed = ceil_div(max_tq, kDecodeSplitTokens);
   const int64_t sp_res = ceil_div(max_tr, kDecodeSplitTokens);
   const int64_t splits = sp_packed + sp_res;

@@ -26,32 +26,17 @@
 // kernel merges the splits with a log-sum-exp combine.
 #include "uc_common.h"
 #include "uc_decode.h"
+#include "uc_mfma.h"
 
 
 namespace uc {
 namespace {
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
+using namespace mf;
 
-constexpr int kD = 128;
 constexpr int kWaves = 2;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kResWaveTokens = 128;  // residual tokens per wave per residual split
-constexpr float kNegInf = -__builtin_huge_valf();
-
-template <int BITS>
-struct Geo {
-  static constexpr int TPW = 32 / BITS;             // tokens per key word = channels per value word
-  static constexpr int ST = 16 * TPW;               // tokens of one wave super-tile
-  static constexpr int VW = kD / TPW;               // value words per token
-  static constexpr int HALF = TPW / 2;              // positions per 16-bit half word
-  static constexpr int PMAX = (10 - BITS) / BITS;   // last position that fits the fp16 mantissa
-  static constexpr int SH = BITS * (PMAX + 1);      // shift that brings the other positions down
-  static constexpr uint32_t MASK = (1u << BITS) - 1u;
-};
 
 template <int BITS, int G>
 struct DecShared {
@@ -75,25 +60,6 @@ struct MfmaParams {
   float *ws_ml;    // [items * Hkv * splits][16][2] (max in log2 units, sum)
   int qd, rd, od;
 };
-
-__device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
-
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) { return (x & m) | c; }
-
-// 2^x on the hardware exp unit; -inf gives 0.
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-__device__ __forceinline__ _Float16 to_h(float x) { return static_cast<_Float16>(x); }
-
-__device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ h4 cvt4(f4 v) { return h4{to_h(v[0]), to_h(v[1]), to_h(v[2]), to_h(v[3])}; }
 
 // Online-softmax state of one wave: lane holds (max, sum) of query row lane%16.
 struct WaveState {
@@ -205,43 +171,47 @@ __device__ __forceinline__ h4 spread_value_codes(uint32_t word, int kap) {
 // (padded rows); lane (n, k-slice) reads its B fragment of block kb from here.
 constexpr int kQPad = kD + 8;
 
+template <int QD>
+__device__ __forceinline__ void stage_queries_t(_Float16 (*sq)[kQPad], const void *query, int64_t h,
+                                                const MfmaParams &p) {
+  // 16 rows x 128 channels; thread t converts 16 consecutive channels of row t/8
+  const int n = threadIdx.x / 8, d0 = (threadIdx.x % 8) * 16;
+  uint4 raw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+  if (n < p.rows) {
+    const int64_t g = n / p.Lq, i = n % p.Lq;
+    const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(query) +
+                                                       (i * p.Hq + h * p.group + g) * kD + d0);
+    raw[0] = src[0];
+    raw[1] = src[1];
+  }
+  *reinterpret_cast<h8 *>(&sq[n][d0]) = halves_to_h8<QD>(raw[0]);
+  *reinterpret_cast<h8 *>(&sq[n][d0 + 8]) = halves_to_h8<QD>(raw[1]);
+}
+
+// Query rows of the KV head staged once per workgroup as fp16 [row][channel];
+// fp32 queries take the element-wise path.
 __device__ __forceinline__ void stage_queries(_Float16 (*sq)[kQPad], const void *query, int64_t h,
                                               const MfmaParams &p) {
-  for (int idx = threadIdx.x; idx < 16 * kD; idx += kThreads) {
-    const int n = idx / kD, d = idx % kD;
-    float v = 0.0f;
-    if (n < p.rows) {
-      const int64_t g = n / p.Lq, i = n % p.Lq;
-      v = load_dyn(query, (i * p.Hq + h * p.group + g) * kD + d, p.qd);
+  static_assert(kThreads == 16 * 8, "one thread per 16 channels of a query row");
+  if (p.qd == UC_BF16) {
+    stage_queries_t<UC_BF16>(sq, query, h, p);
+  } else if (p.qd == UC_FP16) {
+    stage_queries_t<UC_FP16>(sq, query, h, p);
+  } else {
+    for (int idx = threadIdx.x; idx < 16 * kD; idx += kThreads) {
+      const int n = idx / kD, d = idx % kD;
+      float v = 0.0f;
+      if (n < p.rows) {
+        const int64_t g = n / p.Lq, i = n % p.Lq;
+        v = static_cast<const float *>(query)[(i * p.Hq + h * p.group + g) * kD + d];
+      }
+      sq[n][d] = to_h(v);
     }
-    sq[n][d] = to_h(v);
   }
 }
 
 __device__ __forceinline__ h8 query_frag(const _Float16 (*sq)[kQPad], int kb, int lane) {
   return *reinterpret_cast<const h8 *>(&sq[lane & 15][32 * kb + 8 * (lane >> 4)]);
-}
-
-// Buffer resources over one (item, KV head) region: loads past `bytes` return
-// zero, which covers the token tail of the last split without branches.
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-constexpr int kRsrcWord3 = 0x00020000;  // 32-bit data format, raw (stride 0) addressing
-
-__device__ __forceinline__ Rsrc make_rsrc(const void *base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
-                                           static_cast<int>(bytes), kRsrcWord3);
-}
-__device__ __forceinline__ uint32_t bload16(Rsrc r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-}
-__device__ __forceinline__ uint32_t bload32(Rsrc r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-__device__ __forceinline__ uint2 bload64(Rsrc r, uint32_t off) {
-  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-}
-__device__ __forceinline__ uint4 bload128(Rsrc r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
 // Everything one iteration (T tokens of one KV head) reads from HBM, held in
@@ -389,13 +359,12 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
       for (int pq = 0; pq < NP; ++pq) {
         const bool direct = pq <= Gm::PMAX;
         const int pe = direct ? pq : pq - (Gm::PMAX + 1);
-        const uint32_t mask = (Gm::MASK << (BITS * pe)) | (Gm::MASK << (16 + BITS * pe));
         const _Float16 inv = to_h(1.0f / float(1u << (BITS * pe)));
         h8 a;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const uint32_t src = direct ? y[u] : (y[u] >> Gm::SH);
-          const h2 x = as_h2(and_or(src, mask, 0x64006400u)) - h2{to_h(1024.0f), to_h(1024.0f)};
+          const h2 x = code_pair<BITS>(src, pe);
           const h2 k = __builtin_elementwise_fma(x, sp[u] * h2{inv, inv}, mp[u]);
           a[2 * u] = k[0];
           a[2 * u + 1] = k[1];

@@ -116,8 +116,43 @@ def _decode_summary(cache: "PackedKIVICache", query: torch.Tensor, *, include_re
     return out, lse
 
 
+def _mq_summary(cache: "PackedKIVICache", query: torch.Tensor, *, include_residual: bool,
+                out_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    """Long-query fused attention (uc_kivi_attn_mq): the tiled multi-query
+    kernel that UniCache reaches through backend "triton_tiled"."""
+
+    device = nat.require_device(query, cache.key_code, what="Packed KIVI attention")
+    q = query.contiguous()
+    lq, hq, d = map(int, q.shape)
+    tr = cache.residual_tokens if include_residual else 0
+    out = torch.empty((lq, hq, d), dtype=out_dtype, device=device)
+    lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
+    item = nat.KiviItem(
+        cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
+        cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
+        nat.ptr(cache.residual_key) if tr else None, nat.ptr(cache.residual_value) if tr else None,
+        q.data_ptr(), out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr,
+    )
+    res_dtype = cache.residual_key.dtype if tr else q.dtype
+    ws_bytes = nat.mq_workspace_bytes(cache.num_kv_heads, d, cache.quantized_tokens, tr)
+    ws = nat.workspace(device, ws_bytes)
+    nat.call(
+        "uc_kivi_attn_mq", item, cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq,
+        nat.dtype_code(q.dtype), nat.dtype_code(res_dtype), nat.dtype_code(out_dtype),
+        1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device),
+    )
+    return out, lse
+
+
 def _max_decode_query_len(cache: "PackedKIVICache", heads_q: int) -> int:
     return max(1, 16 // max(1, heads_q // cache.num_kv_heads))
+
+
+def _mq_supported(cache: "PackedKIVICache", head_dim: int, include_residual: bool) -> bool:
+    res_ok = not include_residual or not cache.residual_tokens or cache.residual_key.dtype in (
+        torch.bfloat16, torch.float16)
+    return head_dim == 128 and cache.group_size in (32, 64, 128) and res_ok and (
+        not include_residual or not cache.residual_tokens or cache.residual_key.is_contiguous())
 
 
 def packed_kivi_attention_summary(
@@ -141,6 +176,8 @@ def packed_kivi_attention_summary(
     step = _max_decode_query_len(cache, int(query.shape[1]))
     if lq <= step:
         return _decode_summary(cache, query, include_residual=include_residual, out_dtype=query.dtype)
+    if _mq_supported(cache, int(query.shape[2]), include_residual):
+        return _mq_summary(cache, query, include_residual=include_residual, out_dtype=query.dtype)
     from .kivi_mq import packed_attention_mq
 
     return packed_attention_mq(cache, query, include_residual=include_residual)
