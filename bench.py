@@ -89,6 +89,58 @@ def time_steps(fn, steps, warmup, stream):
     return start.elapsed_time(stop) / steps
 
 
+def editing_attention(device, steps, layers=LAYERS, bits=BITS):
+    """Config 2's packed segment: 1088 queries x 28 heads against 1024 source-VAE
+    tokens (896 packed + 128 residual) per layer through uc_kivi_attn_mq (stage
+    + attention kernels), 28 layers of distinct caches; TFLOP/s = 4*Lq*Hq*T*D
+    per layer / time."""
+
+    import math
+
+    from unicache_amd import _native as nat
+    from unicache_amd.storage import PackedKIVICache
+
+    lq, tokens = 1088, 1024
+    calls = []
+    for layer in range(layers):
+        key, value = make_kv(tokens, seed=5000 + layer, device=device)
+        cache = PackedKIVICache.from_dense(key, value, logical_token_ids=torch.arange(tokens, device=device),
+                                           token_type_id=3, k_bits=bits, v_bits=bits, group_size=GROUP,
+                                           residual_length=RESIDUAL, backend="cuda")
+        g = torch.Generator(device=device).manual_seed(9000 + layer)
+        q = torch.randn(lq, HQ, D, generator=g, device=device).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        lse = torch.empty(HQ, lq, dtype=torch.float32, device=device)
+        ws_bytes = nat.mq_workspace_bytes(HKV, D, cache.quantized_tokens, cache.residual_tokens)
+        ws = nat.workspace(device, ws_bytes)
+        item = nat.KiviItem(cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
+                            cache.value_code.data_ptr(), cache.value_scale.data_ptr(),
+                            cache.value_minimum.data_ptr(), cache.residual_key.data_ptr(),
+                            cache.residual_value.data_ptr(), q.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                            cache.quantized_tokens, cache.residual_tokens)
+        calls.append((item, ws, ws_bytes, cache, q, out, lse))
+    stream = torch.cuda.current_stream(device)
+    sid = stream.cuda_stream
+    bf16 = nat.dtype_code(torch.bfloat16)
+
+    def step():
+        for item, ws, ws_bytes, *_ in calls:
+            nat.call("uc_kivi_attn_mq", item, bits, GROUP, HQ, HKV, D, lq, bf16, bf16, bf16, 1.0 / math.sqrt(D),
+                     ws.data_ptr(), ws_bytes, sid)
+
+    ms = time_steps(step, steps, 2, stream)
+    flop = 4 * lq * HQ * tokens * D
+    tflops = flop * layers / (ms * 1e-3) / 1e12
+    return {
+        "workload": f"config 2 packed segment: Lq=1088 x 28 heads, {tokens} tokens ({bits}-bit, 896 packed + "
+                    f"128 residual), {layers} layers, uc_kivi_attn_mq",
+        "ms_per_layer": round(ms / layers, 4),
+        "tflops": round(tflops, 1),
+        "frac_of_bf16_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
+        "flop_per_layer": flop,
+    }
+
+
 def cpu_baseline(algorithmic_bytes_per_seq_layer, budget_s=12.0):
     """The numpy oracle's decode (dequantize + fp64 attention) on one layer of
     the workload, sequences processed until ~budget_s of CPU time."""
@@ -200,6 +252,9 @@ def main():
         "per_layer_launches_gbs": round(step_bytes / (ms_layers * 1e-3) / 1e9, 2),
         "pack_gbs": round(pack_bytes / (pack_ms * 1e-3) / 1e9, 2),
     }
+    del batch, per_layer, caches, queries
+    torch.cuda.empty_cache()
+    result["editing_mq"] = editing_attention(device, max(3, args.steps // 5))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(seq_layer_bytes)
     print(json.dumps(result))
