@@ -70,9 +70,8 @@ struct PackedSrc {
 };
 
 template <int BITS, int G>
-__device__ __forceinline__ void issue_tile(TilePf<BITS> &pf, const PackedSrc &src, uint32_t t0) {
+__device__ __forceinline__ void issue_tile(TilePf<BITS> &pf, const PackedSrc &src, uint32_t t0, int tid) {
   using Gm = Geo<BITS>;
-  const int tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < TilePf<BITS>::NW; ++i) {
     const int e = i * kMqThreads + tid;
@@ -126,10 +125,14 @@ __device__ __forceinline__ void dequant_pair(uint32_t wa, uint32_t wb, uint32_t 
 // ------------------------------------------------------------- stage pass --
 // Workgroup (tile, KV head): keys [64*tile, 64*tile + 64) of the combined
 // sequence [packed | residual | zero tail].
+// The tile's 256 work items are spread over four one-wave workgroups
+// (blockIdx.z), which spreads the pass over more CUs.
+constexpr int kStageThreads = kWave;
+
 template <int BITS, int G, int RD>
-__global__ __launch_bounds__(kMqThreads) void mq_stage_kernel(uc_kivi_item it, StageParams sp) {
+__global__ __launch_bounds__(kStageThreads) void mq_stage_kernel(uc_kivi_item it, StageParams sp) {
   using Gm = Geo<BITS>;
-  const int tid = threadIdx.x;
+  const int tid = blockIdx.z * kStageThreads + threadIdx.x;  // work item of the tile, 0..255
   const int64_t h = blockIdx.y;
   const int64_t x0 = int64_t(blockIdx.x) * kTile;  // first key of the tile
   const int64_t Tq = it.quantized_tokens, Tr = it.residual_tokens, T = Tq + Tr;
@@ -149,7 +152,7 @@ __global__ __launch_bounds__(kMqThreads) void mq_stage_kernel(uc_kivi_item it, S
     src.vscale = make_rsrc(static_cast<const char *>(it.value_scale) + h * vstat_bytes, vstat_bytes);
     src.vmin = make_rsrc(static_cast<const char *>(it.value_min) + h * vstat_bytes, vstat_bytes);
     TilePf<BITS> pf;
-    issue_tile<BITS, G>(pf, src, static_cast<uint32_t>(x0));
+    issue_tile<BITS, G>(pf, src, static_cast<uint32_t>(x0), tid);
 #pragma unroll
     for (int i = 0; i < TilePf<BITS>::NW; ++i) {
       const int e = i * kMqThreads + tid;
@@ -227,30 +230,6 @@ __global__ __launch_bounds__(kMqThreads) void mq_stage_kernel(uc_kivi_item it, S
 }
 
 // --------------------------------------------------------- attention pass --
-// Max / sum over the four lanes n, n+16, n+32, n+48 (the k-slices holding one
-// query column) with the gfx950 lane-swap instructions (VALU, no LDS trip).
-__device__ __forceinline__ float max_over_slices(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
-                                                  false, false);
-  const float y = fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(a[0])),
-                        __builtin_bit_cast(float, static_cast<uint32_t>(a[1])));
-  const auto b = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, y), __builtin_bit_cast(uint32_t, y),
-                                                  false, false);
-  return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(b[0])),
-               __builtin_bit_cast(float, static_cast<uint32_t>(b[1])));
-}
-
-__device__ __forceinline__ float sum_over_slices(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
-                                                  false, false);
-  const float y = __builtin_bit_cast(float, static_cast<uint32_t>(a[0])) +
-                  __builtin_bit_cast(float, static_cast<uint32_t>(a[1]));
-  const auto b = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, y), __builtin_bit_cast(uint32_t, y),
-                                                  false, false);
-  return __builtin_bit_cast(float, static_cast<uint32_t>(b[0])) +
-         __builtin_bit_cast(float, static_cast<uint32_t>(b[1]));
-}
-
 // Output is kept transposed (O^T = V^T P^T) so that every lane owns one query
 // column: the softmax rescale needs no cross-lane traffic.
 struct MqState {
@@ -258,13 +237,13 @@ struct MqState {
   float m[2], l[2];  // lane (n, k): running max of query n; l = this lane's share of the sum
 };
 
-// Global fp16 data of one 64-key tile, per thread: 64 B of keys, 64 B of values.
+// Global fp16 data of one 64-key tile, per thread of a 256-thread key half:
+// 64 B of keys, 64 B of values.
 struct TileRegs {
   uint4 k[4], v[4];
 };
 
-__device__ __forceinline__ void load_tile(TileRegs &tr, Rsrc rk, Rsrc rv, int64_t keys_pad, int64_t x0) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void load_tile(TileRegs &tr, Rsrc rk, Rsrc rv, int64_t keys_pad, int64_t x0, int tid) {
   const int tok = tid / 4, kq = tid % 4;  // key rows: 4 threads x 64 B
   const int ch = tid / 2, vh = tid % 2;   // value rows (per channel): 2 threads x 64 B
   const uint32_t ko = static_cast<uint32_t>(((x0 + tok) * kD + 32 * kq) * 2);
@@ -276,8 +255,7 @@ __device__ __forceinline__ void load_tile(TileRegs &tr, Rsrc rk, Rsrc rv, int64_
   }
 }
 
-__device__ __forceinline__ void store_tile(MqTile &t, const TileRegs &tr) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void store_tile(MqTile &t, const TileRegs &tr, int tid) {
   const int tok = tid / 4, kq = tid % 4;
   const int ch = tid / 2, vh = tid % 2;
 #pragma unroll
@@ -376,14 +354,24 @@ __device__ __forceinline__ void compute_tile(const MqTile &sh, const h8 (&qf)[2]
   }
 }
 
+// 8 waves: waves 0-3 and 4-7 take the first and second half of the key tiles
+// for the same 128 query rows (32 per wave), so each SIMD runs two waves whose
+// softmax VALU work and MFMAs overlap; the halves merge through LDS at the end.
+constexpr int kAttnWaves = 8;
+constexpr int kAttnThreads = kAttnWaves * kWave;
+constexpr int kHalfThreads = kAttnThreads / 2;
+static_assert(kHalfThreads == 256, "tile loads map 256 threads per key half");
+constexpr int kMergeFloats = 2 * 8 * 4 + 4;  // O^T (2 query blocks x 8 channel blocks x 4) + m[2], l[2]
+
 template <int QD, int OD>
-__global__ __launch_bounds__(kMqThreads) __attribute__((amdgpu_waves_per_eu(2))) void mq_attention_kernel(
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void mq_attention_kernel(
     uc_kivi_item it, MqParams p) {
-  __shared__ MqTile sh[2];
+  __shared__ MqTile sh[2][2];  // [key half][buffer]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = wave / 4, rw = wave % 4, tid_h = tid % kHalfThreads;
   const int r = lane & 15, kap = lane >> 4;
   const int64_t h = blockIdx.y;
-  const int64_t row0 = int64_t(blockIdx.x) * kMqRows + wave * kRowsPerWave;
+  const int64_t row0 = int64_t(blockIdx.x) * kMqRows + rw * kRowsPerWave;
 
   // query rows of this wave as the B operand of S^T = K Q^T (bf16/fp16 -> fp16 is
   // exact for these magnitudes; the softmax scale is applied to the fp32 logits);
@@ -414,50 +402,83 @@ __global__ __launch_bounds__(kMqThreads) __attribute__((amdgpu_waves_per_eu(2)))
   const Rsrc rk = make_rsrc(p.wk + h * p.keys_pad * kD, head_bytes);
   const Rsrc rv = make_rsrc(p.wv + h * kD * p.keys_pad, head_bytes);
   const int n_tiles = static_cast<int>(p.keys_pad / kTile);
+  const int n0 = (n_tiles + 1) / 2;                 // tiles of the first half (the longer one)
+  const int first = half ? n0 : 0;
+  const int count = half ? n_tiles - n0 : n0;
+  MqTile *buf = sh[half];
   TileRegs tr;
-  load_tile(tr, rk, rv, p.keys_pad, 0);
-  store_tile(sh[0], tr);
+  if (count > 0) {
+    load_tile(tr, rk, rv, p.keys_pad, int64_t(first) * kTile, tid_h);
+    store_tile(buf[0], tr, tid_h);
+  }
   __syncthreads();
-  for (int i = 0; i < n_tiles; ++i) {
-    if (i + 1 < n_tiles) load_tile(tr, rk, rv, p.keys_pad, int64_t(i + 1) * kTile);
-    const int valid = static_cast<int>(min<int64_t>(kTile, p.keys - int64_t(i) * kTile));
-    compute_tile(sh[i & 1], qf, valid, p.scale_log2, st);
-    if (i + 1 < n_tiles) store_tile(sh[(i + 1) & 1], tr);  // that buffer was last read in tile i-1
+  for (int i = 0; i < n0; ++i) {  // both halves step together: the barrier is shared
+    const bool active = i < count, more = i + 1 < count;
+    if (more) load_tile(tr, rk, rv, p.keys_pad, int64_t(first + i + 1) * kTile, tid_h);
+    if (active) {
+      const int valid = static_cast<int>(min<int64_t>(kTile, p.keys - int64_t(first + i) * kTile));
+      compute_tile(buf[i & 1], qf, valid, p.scale_log2, st);
+    }
+    if (more) store_tile(buf[(i + 1) & 1], tr, tid_h);  // that buffer was last read in tile i-1
     __syncthreads();
   }
 
-  // normalise into LDS (this wave's 32 rows, reusing the tile buffers), then
-  // write whole rows
-  typedef typename DtypeOf<OD>::T OutT;
-  constexpr int kRowPad = kD + 8;
-  OutT *ob = reinterpret_cast<OutT *>(&sh[0]) + wave * kRowsPerWave * kRowPad;
-  static_assert(sizeof(OutT) * kMqRows * (kD + 8) <= sizeof(MqTile) * 2, "output staging fits the tiles");
+  // merge: the second half hands (O^T, m, l) of its lanes to the wave with the
+  // same rows in the first half
+  float *mg = reinterpret_cast<float *>(&sh[1][0]) + rw * kMergeFloats * kWave;
+  static_assert(sizeof(float) * kMergeFloats * kWave * 4 <= sizeof(MqTile) * 2, "merge fits the second half");
+  if (half == 1) {
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const float l = sum_over_slices(st.l[qb]);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    for (int qb = 0; qb < 2; ++qb) {
 #pragma unroll
-    for (int cb = 0; cb < 8; ++cb)
+      for (int cb = 0; cb < 8; ++cb)
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        store_from_f32<OD>(ob, (16 * qb + r) * kRowPad + 16 * cb + 4 * kap + v, st.o[qb][cb][v] * inv);
-    const int64_t row = row0 + 16 * qb + r;
-    if (kap == 0 && row < p.rows && it.lse != nullptr) {
-      const int64_t g = row / p.Lq, i = row % p.Lq;
-      it.lse[(h * p.group + g) * p.Lq + i] = l > 0.0f ? (st.m[qb] + log2f(l)) * kLn2 : kNegInf;
+        for (int v = 0; v < 4; ++v) mg[((qb * 8 + cb) * 4 + v) * kWave + lane] = st.o[qb][cb][v];
+      mg[(64 + qb) * kWave + lane] = st.m[qb];
+      mg[(66 + qb) * kWave + lane] = st.l[qb];
     }
   }
   __syncthreads();
-  constexpr int kChunk = 16 / sizeof(OutT);  // elements per 16-byte store
-  constexpr int kPerRow = kD / kChunk;
+  typedef typename DtypeOf<OD>::T OutT;
+  constexpr int kRowPad = kD + 8;
+  OutT *ob = reinterpret_cast<OutT *>(&sh[0][0]) + rw * kRowsPerWave * kRowPad;
+  static_assert(sizeof(OutT) * kMqRows * kRowPad <= sizeof(MqTile) * 2, "output staging fits the first half");
+  if (half == 0) {
 #pragma unroll
-  for (int q = 0; q < kRowsPerWave * kPerRow / kWave; ++q) {
-    const int idx = q * kWave + lane, rr = idx / kPerRow, cc = (idx % kPerRow) * kChunk;
-    const int64_t row = row0 + rr;
-    if (row >= p.rows) continue;
-    const int64_t g = row / p.Lq, i = row % p.Lq;
-    *reinterpret_cast<uint4 *>(static_cast<OutT *>(it.out) + (i * p.Hq + h * p.group + g) * kD + cc) =
-        *reinterpret_cast<const uint4 *>(&ob[rr * kRowPad + cc]);
+    for (int qb = 0; qb < 2; ++qb) {
+      const float m2 = mg[(64 + qb) * kWave + lane], l2 = mg[(66 + qb) * kWave + lane];
+      const float M = fmaxf(st.m[qb], m2);
+      const float M_ref = M == kNegInf ? 0.0f : M;
+      const float a1 = fast_exp2(st.m[qb] - M_ref), a2 = fast_exp2(m2 - M_ref);
+      const float l = sum_over_slices(st.l[qb] * a1 + l2 * a2);
+      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float o = st.o[qb][cb][v] * a1 + mg[((qb * 8 + cb) * 4 + v) * kWave + lane] * a2;
+          store_from_f32<OD>(ob, (16 * qb + r) * kRowPad + 16 * cb + 4 * kap + v, o * inv);
+        }
+      const int64_t row = row0 + 16 * qb + r;
+      if (kap == 0 && row < p.rows && it.lse != nullptr) {
+        const int64_t g = row / p.Lq, i = row % p.Lq;
+        it.lse[(h * p.group + g) * p.Lq + i] = l > 0.0f ? (M + log2f(l)) * kLn2 : kNegInf;
+      }
+    }
+  }
+  __syncthreads();
+  if (half == 0) {
+    constexpr int kChunk = 16 / sizeof(OutT);  // elements per 16-byte store
+    constexpr int kPerRow = kD / kChunk;
+#pragma unroll
+    for (int q = 0; q < kRowsPerWave * kPerRow / kWave; ++q) {
+      const int idx = q * kWave + lane, rr = idx / kPerRow, cc = (idx % kPerRow) * kChunk;
+      const int64_t row = row0 + rr;
+      if (row >= p.rows) continue;
+      const int64_t g = row / p.Lq, i = row % p.Lq;
+      *reinterpret_cast<uint4 *>(static_cast<OutT *>(it.out) + (i * p.Hq + h * p.group + g) * kD + cc) =
+          *reinterpret_cast<const uint4 *>(&ob[rr * kRowPad + cc]);
+    }
   }
 }
 
@@ -512,13 +533,14 @@ extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int grou
              "attn_mq: segment too long for 32-bit buffer offsets");
   sp.wk = static_cast<_Float16 *>(workspace);
   sp.wv = sp.wk + heads_kv * sp.keys_pad * mf::kD;
-  const dim3 sgrid(static_cast<unsigned>(sp.keys_pad / kTile), static_cast<unsigned>(heads_kv));
+  const dim3 sgrid(static_cast<unsigned>(sp.keys_pad / kTile), static_cast<unsigned>(heads_kv),
+                   static_cast<unsigned>(kMqThreads / kStageThreads));
 #define UC_STAGE(B, G)                                                                                          \
   do {                                                                                                          \
     if (res_dtype == UC_FP16)                                                                                   \
-      hipLaunchKernelGGL((mq_stage_kernel<B, G, UC_FP16>), sgrid, dim3(kMqThreads), 0, stream, it, sp);         \
+      hipLaunchKernelGGL((mq_stage_kernel<B, G, UC_FP16>), sgrid, dim3(kStageThreads), 0, stream, it, sp);         \
     else                                                                                                        \
-      hipLaunchKernelGGL((mq_stage_kernel<B, G, UC_BF16>), sgrid, dim3(kMqThreads), 0, stream, it, sp);         \
+      hipLaunchKernelGGL((mq_stage_kernel<B, G, UC_BF16>), sgrid, dim3(kStageThreads), 0, stream, it, sp);         \
   } while (0)
   if (bits == 2) {
     if (group_size == 32) UC_STAGE(2, 32);
@@ -547,11 +569,11 @@ extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int grou
 #define UC_ATTN(QD)                                                                                \
   do {                                                                                             \
     if (out_dtype == UC_BF16)                                                                      \
-      hipLaunchKernelGGL((mq_attention_kernel<QD, UC_BF16>), grid, dim3(kMqThreads), 0, stream, it, p); \
+      hipLaunchKernelGGL((mq_attention_kernel<QD, UC_BF16>), grid, dim3(kAttnThreads), 0, stream, it, p); \
     else if (out_dtype == UC_FP16)                                                                 \
-      hipLaunchKernelGGL((mq_attention_kernel<QD, UC_FP16>), grid, dim3(kMqThreads), 0, stream, it, p); \
+      hipLaunchKernelGGL((mq_attention_kernel<QD, UC_FP16>), grid, dim3(kAttnThreads), 0, stream, it, p); \
     else                                                                                           \
-      hipLaunchKernelGGL((mq_attention_kernel<QD, UC_FP32>), grid, dim3(kMqThreads), 0, stream, it, p); \
+      hipLaunchKernelGGL((mq_attention_kernel<QD, UC_FP32>), grid, dim3(kAttnThreads), 0, stream, it, p); \
   } while (0)
   if (q_dtype == UC_FP16) UC_ATTN(UC_FP16);
   else UC_ATTN(UC_BF16);

@@ -49,7 +49,10 @@ struct DecShared {
   _Float16 ks[KG][KPAD], km[KG][KPAD];                  // key stats [group][channel]
   _Float16 vs[NGD][Gm::TPW][JW], vm[NGD][Gm::TPW][JW];  // value stats [group][position][word]
   uint32_t kw[kWaves][4][4][16][8];                     // key words [block][k-slice][row][channel]
-  uint32_t vw[kWaves][Gm::TPW][16][Gm::VW];             // value words [position][row][word]
+  // value words [position][word][row], rows padded to 20 dwords: a lane reads
+  // four rows of one word as 16 bytes, and staging writes hit distinct banks
+  static constexpr int VROW = 20;
+  uint32_t vw[kWaves][Gm::TPW][Gm::VW][VROW];
 };
 
 struct MfmaParams {
@@ -61,81 +64,52 @@ struct MfmaParams {
   int qd, rd, od;
 };
 
-// Online-softmax state of one wave: lane holds (max, sum) of query row lane%16.
+// Online-softmax state of one wave.  The output is accumulated transposed
+// (O^T = V^T P^T): lane (n, k) owns query column n, so every rescale is
+// lane-local.
 struct WaveState {
-  f4 o[8];     // unnormalised output: lane (k = lane/16, n = lane%16) -> rows 4k+v, channel 16*blk + n
-  f4 cmin;     // sum_t P*min, column n = value group
-  float m, l;
+  f4 o[8];     // lane (n = lane%16, k = lane/16): query n, channels 16*cb + 4k + v (scaled, see value_pair)
+  f4 cmin[4];  // sum_t P*min of value group g (every row of the block holds it)
+  float m;     // running max of query n (log2 units), equal across the k-slices
+  float l;     // this lane's share of the running sum (reduced over the k-slices at the end)
 };
 
 // Base-2 softmax of a tile of logits (acc[p][v] = row 4k+v of the C layout,
-// column = query row), folded into the running state; returns with acc holding
-// the probabilities and the output rescaled.
+// column = query), folded into the running state; returns with acc holding the
+// probabilities and the output rescaled.
 template <int NP>
-__device__ __forceinline__ void softmax_tile(f4 (&acc)[NP], const bool (&valid)[4], float scale_log2, WaveState &st,
-                                             int lane) {
+__device__ __forceinline__ void softmax_tile(f4 (&acc)[NP], const bool (&valid)[4], float scale_log2,
+                                             WaveState &st) {
   float mx = kNegInf;
 #pragma unroll
   for (int pp = 0; pp < NP; ++pp)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const float x = valid[v] ? acc[pp][v] * scale_log2 : kNegInf;
+      const float x = valid[v] ? acc[pp][v] : kNegInf;
       acc[pp][v] = x;
       mx = fmaxf(mx, x);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-  const float m_new = fmaxf(st.m, mx);
+  mx = max_over_slices(mx);
+  const float m_new = fmaxf(st.m, mx * scale_log2);
   const float m_ref = m_new == kNegInf ? 0.0f : m_new;  // keeps -inf - m_ref at -inf (exp 0), never NaN
   float sum = 0.0f;
 #pragma unroll
   for (int pp = 0; pp < NP; ++pp)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const float e = fast_exp2(acc[pp][v] - m_ref);
+      const float e = fast_exp2(__builtin_fmaf(acc[pp][v], scale_log2, -m_ref));
       acc[pp][v] = e;
       sum += e;
     }
-  sum += __shfl_xor(sum, 16, kWave);
-  sum += __shfl_xor(sum, 32, kWave);
   const float alpha = fast_exp2(st.m - m_ref);
   st.l = st.l * alpha + sum;
   st.m = m_new;
-  // rescale the output rows 4k+v by the alpha of query row 4k+v
-  const int k = lane >> 4;
+  if (__any(alpha != 1.0f)) {
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const float a = __shfl(alpha, 4 * k + v, kWave);
+    for (int b = 0; b < 8; ++b) st.o[b] *= alpha;
 #pragma unroll
-    for (int b = 0; b < 8; ++b) st.o[b][v] *= a;
-    st.cmin[v] *= a;
+    for (int g = 0; g < 4; ++g) st.cmin[g] *= alpha;
   }
-}
-
-// Selection matrix of the value transposition: B[k][n] = 1/scale(k) when the
-// channel spread into k-slot k is channel n of the 16-channel block.
-template <int BITS>
-__device__ __forceinline__ h4 transpose_selector(int lane) {
-  const int n = lane & 15, kap = lane >> 4;
-  h4 b;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    int ch;
-    float inv;
-    if constexpr (BITS == 2) {
-      const int a = 2 * kap;
-      const int chans[4] = {a, a + 8, a + 1, a + 9};
-      ch = chans[v];
-      inv = v < 2 ? 1.0f : 0.25f;
-    } else {
-      const int base = 8 * (kap >> 1), sub = kap & 1;
-      const int chans[4] = {base + 2 * sub, base + 2 * sub + 4, base + 2 * sub + 1, base + 2 * sub + 5};
-      ch = chans[v];
-      inv = v < 2 ? 1.0f : 0.0625f;
-    }
-    b[v] = to_h(ch == n ? inv : 0.0f);
-  }
-  return b;
 }
 
 // Identity selection (k-slot k -> column k) for dense residual rows.
@@ -147,23 +121,25 @@ __device__ __forceinline__ h4 identity_selector(int lane) {
   return b;
 }
 
-// Codes of 16-channel block `blk` of one token, spread into the lane's four
-// k-slots as fp16 (1024 + code * scale) for the transposition MFMA.
+// Value codes of channel c (lane%16 of a 16-channel block) for two tokens,
+// whose words are wa / wb, as fp16 code * 2^e with e = value_shift<BITS>(c):
+// the byte holding the channel is gathered from both words into the two
+// halves, its bits OR-ed into the mantissa of 1024 and 1024 subtracted.
 template <int BITS>
-__device__ __forceinline__ h4 spread_value_codes(uint32_t word, int kap) {
-  uint32_t y, m0, m1;
-  if constexpr (BITS == 2) {
-    y = word >> (4 * kap);
-    m0 = 0x00030003u;
-    m1 = 0x000C000Cu;
-  } else {
-    y = word >> (8 * (kap & 1));
-    m0 = 0x000F000Fu;
-    m1 = 0x00F000F0u;
-  }
-  const h2 a = as_h2(and_or(y, m0, 0x64006400u));
-  const h2 b = as_h2(and_or(y, m1, 0x64006400u));
-  return h4{a[0], a[1], b[0], b[1]};
+__device__ __forceinline__ int value_shift(int c) {
+  return BITS == 2 ? 2 * (c & 3) : 4 * (c & 1);
+}
+
+template <int BITS>
+__device__ __forceinline__ uint32_t value_selector(int c) {
+  const uint32_t b = BITS == 2 ? uint32_t(c) / 4u : uint32_t(c & 7) / 2u;  // byte of the channel in its word
+  return b | (0x0cu << 8) | ((4u + b) << 16) | (0x0cu << 24);              // [wa.b, 0, wb.b, 0]
+}
+
+template <int BITS>
+__device__ __forceinline__ h2 value_pair(uint32_t wa, uint32_t wb, uint32_t sel, uint32_t mask) {
+  const uint32_t x = __builtin_amdgcn_perm(wb, wa, sel);
+  return as_h2(and_or(x, mask, 0x64006400u)) - h2{to_h(1024.0f), to_h(1024.0f)};
 }
 
 // ------------------------------------------------------------ packed path --
@@ -220,11 +196,11 @@ template <int BITS, int G>
 struct Prefetch {
   using Gm = Geo<BITS>;
   using Sh = DecShared<BITS, G>;
-  static constexpr int NKS = Sh::KG * kD / kThreads;        // key stats per thread (per stat)
+  static constexpr int NKD = Sh::KG / 2 + 1;               // dwords of one key-stat row segment
   static constexpr int NVS = Sh::T * Sh::NGD / 8;           // 16-byte chunks of value stats
   static constexpr int VS4 = (NVS + kThreads - 1) / kThreads;
   static constexpr int NVW = Gm::ST * Gm::VW / 4 / kWave;   // 16-byte chunks of value words per lane
-  uint32_t ks[NKS], km[NKS];
+  uint32_t ks[NKD], km[NKD];  // thread = channel: KG halves from a 4-byte aligned start
   uint4 vs[VS4], vm[VS4];
   uint4 vw[NVW];
   uint32_t kw[4][8];
@@ -236,6 +212,20 @@ struct PackedRegion {
   uint32_t nkw, nkg;  // key words / key groups per channel row
 };
 
+// Which 16-byte chunk of value words load q of lane group a brings: the four
+// groups of one load land on four different 16-dword bank windows of the
+// [position][word][row] staging layout (block stride 20 dwords).
+template <int BITS>
+__device__ __forceinline__ void value_chunk(int q, int a, int &pos, int &quad) {
+  if constexpr (BITS == 2) {  // 8 words = 2 quads per token, 16 positions: 8 loads
+    pos = 2 * q + (a >> 1);
+    quad = a & 1;
+  } else {                    // 16 words = 4 quads per token, 8 positions: 8 loads
+    pos = q;
+    quad = a;
+  }
+}
+
 // Issue the loads of the iteration starting at token t0 (multiple of T).
 template <int BITS, int G>
 __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedRegion<BITS, G> &rg, uint32_t t0) {
@@ -244,14 +234,15 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
   using Pf = Prefetch<BITS, G>;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
-  // key stats [D][nkg]: consecutive lanes read consecutive groups of one channel
-  const uint32_t kg0 = t0 / G;
+  // key stats [D][nkg]: thread = channel, its KG groups as dwords from the
+  // 4-byte boundary at or below the first (realigned when staged)
+  {
+    const uint32_t d0 = (tid * rg.nkg + t0 / G) >> 1;
 #pragma unroll
-  for (int q = 0; q < Pf::NKS; ++q) {
-    const int e = q * kThreads + tid, c = e / Sh::KG, j = e % Sh::KG;
-    const uint32_t off = (c * rg.nkg + kg0 + j) * 2u;
-    pf.ks[q] = bload16(rg.kscale, off);
-    pf.km[q] = bload16(rg.kmin, off);
+    for (int q = 0; q < Pf::NKD; ++q) {
+      pf.ks[q] = bload32(rg.kscale, (d0 + q) * 4u);
+      pf.km[q] = bload32(rg.kmin, (d0 + q) * 4u);
+    }
   }
   // value stats [Tq][NGD]
 #pragma unroll
@@ -261,10 +252,17 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
     pf.vs[q] = bload128(rg.vscale, off);
     pf.vm[q] = bload128(rg.vmin, off);
   }
-  // value words [Tq][VW] of this wave's super-tile
+  // value words [Tq][VW] of this wave's super-tile, 16 bytes (4 words of one
+  // token) per load: lane (row = lane%16, group a = lane/16) takes word-row
+  // `row` at (position, word quad) = value_chunk(q, a)
   const uint32_t tw0 = t0 + wave * Gm::ST;
 #pragma unroll
-  for (int q = 0; q < Pf::NVW; ++q) pf.vw[q] = bload128(rg.vcode, (tw0 * Gm::VW + 4 * (q * kWave + lane)) * 4u);
+  for (int q = 0; q < Pf::NVW; ++q) {
+    int pos, quad;
+    value_chunk<BITS>(q, lane >> 4, pos, quad);
+    const uint32_t tok = tw0 + (lane & 15) * Gm::TPW + pos;
+    pf.vw[q] = bload128(rg.vcode, (tok * Gm::VW + 4 * quad) * 4u);
+  }
   // key words [D][nkw]: lane (row r, k-slice kap) reads word J of 32 channels
   const uint32_t J = t0 / Gm::TPW + wave * 16 + r;
 #pragma unroll
@@ -275,17 +273,24 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
 
 // Move a landed prefetch into the LDS layouts the MFMA loops read.
 template <int BITS, int G>
-__device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch<BITS, G> &pf) {
+__device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch<BITS, G> &pf, uint32_t t0,
+                                          uint32_t nkg) {
   using Gm = Geo<BITS>;
   using Sh = DecShared<BITS, G>;
   using Pf = Prefetch<BITS, G>;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
+  {
+    const uint32_t shift = ((tid * nkg + t0 / G) & 1u) * 16u;  // odd first element: start at the high half
 #pragma unroll
-  for (int q = 0; q < Pf::NKS; ++q) {
-    const int e = q * kThreads + tid, c = e / Sh::KG, j = e % Sh::KG;
-    sh.ks[j][c] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(pf.ks[q]));
-    sh.km[j][c] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(pf.km[q]));
+    for (int q = 0; q < Sh::KG / 2; ++q) {
+      const uint32_t s2 = __builtin_amdgcn_alignbit(pf.ks[q + 1], pf.ks[q], shift);
+      const uint32_t m2 = __builtin_amdgcn_alignbit(pf.km[q + 1], pf.km[q], shift);
+      sh.ks[2 * q][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s2));
+      sh.ks[2 * q + 1][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s2 >> 16));
+      sh.km[2 * q][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(m2));
+      sh.km[2 * q + 1][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(m2 >> 16));
+    }
   }
 #pragma unroll
   for (int q = 0; q < Pf::VS4; ++q) {
@@ -302,9 +307,11 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
   }
 #pragma unroll
   for (int q = 0; q < Pf::NVW; ++q) {
-    const int i = q * kWave + lane;
-    const int tok = (4 * i) / Gm::VW, word = (4 * i) % Gm::VW;  // token within the super-tile
-    *reinterpret_cast<uint4 *>(&sh.vw[wave][tok % Gm::TPW][tok / Gm::TPW][word]) = pf.vw[q];
+    int pos, quad;
+    value_chunk<BITS>(q, lane >> 4, pos, quad);
+    const uint32_t w4[4] = {pf.vw[q].x, pf.vw[q].y, pf.vw[q].z, pf.vw[q].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sh.vw[wave][pos][4 * quad + j][lane & 15] = w4[j];
   }
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
@@ -322,11 +329,10 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
   using Sh = DecShared<BITS, G>;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
-  const h4 sel = transpose_selector<BITS>(lane);
-  // the transposition returns code + 1024/scale; seeding its accumulator with
-  // minus that offset (per column) makes it return the code itself
-  const float off = (r & 1) ? (BITS == 2 ? 256.0f : 64.0f) : 1024.0f;
-  const f4 neg_off = f4{-off, -off, -off, -off};
+  // value extraction for this lane's channel c = r of each 16-channel block
+  const uint32_t vsel = value_selector<BITS>(r);
+  const int ve = value_shift<BITS>(r);
+  const uint32_t vmask = (Gm::MASK << ve) | (Gm::MASK << (16 + ve));
   constexpr int NP = Gm::TPW / 2;  // positions per half word
   const int gl = ((wave * 16 + r) * Gm::TPW) / G;  // key group of this lane's row
   bool valid[4];
@@ -372,39 +378,35 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
         acc[pq] = mfma32(a, qfrag, acc[pq]);
       }
     }
-    softmax_tile<NP>(acc, valid, scale_log2, st, lane);
+    softmax_tile<NP>(acc, valid, scale_log2, st);
 
-    // ---- values of these positions
+    // ---- values of these positions, two at a time: O^T += V^T P^T on
+    // v_mfma_f32_16x16x32_f16 with k = (word rows 4k..4k+3) x (positions pa, pb)
     const int jw = wave * 16 + 4 * kap;
 #pragma unroll
-    for (int pq = 0; pq < NP; ++pq) {
-      const int pp = half * NP + pq;
-      const h4 ap = cvt4(acc[pq]);  // A: rows = query rows, k = word rows 4k..4k+3 at position pp
-      h4 as[Sh::NGD];
+    for (int j = 0; j < NP / 2; ++j) {
+      const int pa = half * NP + 2 * j, pb = pa + 1;
+      const h4 pa4 = cvt4(acc[2 * j]), pb4 = cvt4(acc[2 * j + 1]);
+      const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
+      h8 ps[Sh::NGD];  // P * value scale, per value group
 #pragma unroll
-      for (int gd = 0; gd < Sh::NGD; ++gd) as[gd] = ap * *reinterpret_cast<const h4 *>(&sh.vs[gd][pp][jw]);
-      const h4 bm = r < Sh::NGD ? *reinterpret_cast<const h4 *>(&sh.vm[r < Sh::NGD ? r : 0][pp][jw])
-                                : h4{to_h(0.0f), to_h(0.0f), to_h(0.0f), to_h(0.0f)};
-      st.cmin = mfma16(ap, bm, st.cmin);
-      // the word holding channel block blk for this lane's k-slice: 2-bit rows
-      // keep 16 channels per word, 4-bit rows 8 (even/odd word by k-slice pair)
-      uint32_t words[8];
-      if constexpr (BITS == 2) {
-        const uint4 *row = reinterpret_cast<const uint4 *>(&sh.vw[wave][pp][r][0]);
-        const uint4 a = row[0], b = row[1];
-        words[0] = a.x; words[1] = a.y; words[2] = a.z; words[3] = a.w;
-        words[4] = b.x; words[5] = b.y; words[6] = b.z; words[7] = b.w;
-      } else {
-        const uint32_t *row = &sh.vw[wave][pp][r][kap >> 1];
-#pragma unroll
-        for (int blk = 0; blk < 8; ++blk) words[blk] = row[2 * blk];
+      for (int g = 0; g < Sh::NGD; ++g) {
+        const h4 sa = *reinterpret_cast<const h4 *>(&sh.vs[g][pa][jw]), sb = *reinterpret_cast<const h4 *>(&sh.vs[g][pb][jw]);
+        const h4 ma = *reinterpret_cast<const h4 *>(&sh.vm[g][pa][jw]), mb = *reinterpret_cast<const h4 *>(&sh.vm[g][pb][jw]);
+        ps[g] = p8 * h8{sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+        // every row of A = the value minima: each output row gets sum_t P*min
+        st.cmin[g] = mfma32(h8{ma[0], ma[1], ma[2], ma[3], mb[0], mb[1], mb[2], mb[3]}, p8, st.cmin[g]);
       }
-      // all eight transpositions first, so their latency overlaps
-      f4 ct[8];
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk) ct[blk] = mfma16(spread_value_codes<BITS>(words[blk], kap), sel, neg_off);
-#pragma unroll
-      for (int blk = 0; blk < 8; ++blk) st.o[blk] = mfma16(as[(16 * blk) / G], cvt4(ct[blk]), st.o[blk]);
+      for (int cb = 0; cb < 8; ++cb) {
+        const int wi = BITS == 2 ? cb : 2 * cb + (r >> 3);  // word holding channel 16*cb + r
+        const uint4 wa = *reinterpret_cast<const uint4 *>(&sh.vw[wave][pa][wi][4 * kap]);
+        const uint4 wb = *reinterpret_cast<const uint4 *>(&sh.vw[wave][pb][wi][4 * kap]);
+        const h2 x0 = value_pair<BITS>(wa.x, wa.y, vsel, vmask), x1 = value_pair<BITS>(wa.z, wa.w, vsel, vmask);
+        const h2 x2 = value_pair<BITS>(wb.x, wb.y, vsel, vmask), x3 = value_pair<BITS>(wb.z, wb.w, vsel, vmask);
+        const h8 av = h8{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
+        st.o[cb] = mfma32(av, ps[(16 * cb) / G], st.o[cb]);
+      }
     }
   }
 }
@@ -435,18 +437,19 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
   for (int i = 0; i < n_it; ++i) {
     const uint32_t t0 = static_cast<uint32_t>(t_split + int64_t(i) * Sh::T);
     __syncthreads();  // every wave is done reading the previous iteration from LDS
-    stage_lds<BITS, G>(sh, pf);
+    stage_lds<BITS, G>(sh, pf, t0, rg.nkg);
     __syncthreads();
     if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, t0 + Sh::T);  // lands while this iteration computes
     compute_tile<BITS, G>(sh, sq, t0, rg.nkw, p.scale_log2, st);
   }
-  // fold the value minima back in: sum_t P*min of group gd sits in column gd
+  // undo the code scaling 2^e of output row c (e depends on c mod 4 / mod 2,
+  // i.e. on v) and add the value minima
 #pragma unroll
-  for (int blk = 0; blk < 8; ++blk) {
-    const int gd = (16 * blk) / G;
+  for (int cb = 0; cb < 8; ++cb)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) st.o[blk][v] += __shfl(st.cmin[v], (lane & 48) | gd, kWave);
-  }
+    for (int v = 0; v < 4; ++v)
+      st.o[cb][v] = st.o[cb][v] * (1.0f / float(1 << value_shift<BITS>(v))) + st.cmin[(16 * cb) / G][v];
+  (void)lane;
 }
 
 // --------------------------------------------------------- residual path --
@@ -499,33 +502,37 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const bool ok = tw + 16 * b + 4 * kap + v < Tr;
-      const float x = ok ? acc[b][v] * p.scale_log2 : kNegInf;
+      const float x = ok ? acc[b][v] : kNegInf;
       acc[b][v] = x;
       mx = fmaxf(mx, x);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  const float m = max_over_slices(mx) * p.scale_log2;
+  const float m_ref = m == kNegInf ? 0.0f : m;
   float sum = 0.0f;
 #pragma unroll
   for (int b = 0; b < kBlocks; ++b)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const float e = acc[b][v] == kNegInf ? 0.0f : exp2f(acc[b][v] - mx);
+      const float e = fast_exp2(__builtin_fmaf(acc[b][v], p.scale_log2, -m_ref));
       acc[b][v] = e;
       sum += e;
     }
-  sum += __shfl_xor(sum, 16, kWave);
-  sum += __shfl_xor(sum, 32, kWave);
-  st.m = mx;
+  st.m = m;
   st.l = sum;
+  // O^T += V^T P^T: the 4 channels x 16 tokens a lane loads from a residual row
+  // block come out of an identity MFMA as 4 tokens of one channel (the A layout)
 #pragma unroll
-  for (int b = 0; b < kBlocks; ++b) {
-    const h4 ap = cvt4(acc[b]);
-    const uint32_t base = static_cast<uint32_t>(((tw + 16 * b + r) * p.Hkv + h) * kD * 2);
+  for (int j = 0; j < kBlocks / 2; ++j) {
+    const h4 pa4 = cvt4(acc[2 * j]), pb4 = cvt4(acc[2 * j + 1]);
+    const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
+    const uint32_t base0 = static_cast<uint32_t>(((tw + 32 * j + r) * p.Hkv + h) * kD * 2);
+    const uint32_t base1 = static_cast<uint32_t>(((tw + 32 * j + 16 + r) * p.Hkv + h) * kD * 2);
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk) {
-      const f4 ct = mfma16(load4_h<RD>(rv, base + (16 * blk + 4 * kap) * 2), ident, f4{0, 0, 0, 0});
-      st.o[blk] = mfma16(ap, cvt4(ct), st.o[blk]);
+    for (int cb = 0; cb < 8; ++cb) {
+      const f4 t0 = mfma16(load4_h<RD>(rv, base0 + (16 * cb + 4 * kap) * 2), ident, f4{0, 0, 0, 0});
+      const f4 t1 = mfma16(load4_h<RD>(rv, base1 + (16 * cb + 4 * kap) * 2), ident, f4{0, 0, 0, 0});
+      const h4 a0 = cvt4(t0), a1 = cvt4(t1);
+      st.o[cb] = mfma32(h8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, p8, st.o[cb]);
     }
   }
 }
@@ -534,7 +541,7 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
 static_assert(kThreads == kD, "key-stat staging maps one thread per channel");
 
 template <int BITS, int G, int RD, bool TABLE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_mfma_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma_kernel(
     const uc_kivi_item *items, uc_kivi_item single, MfmaParams p) {
   __shared__ DecShared<BITS, G> sh;
   __shared__ _Float16 sq[16][kQPad];
@@ -548,7 +555,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   WaveState st;
 #pragma unroll
   for (int b = 0; b < 8; ++b) st.o[b] = f4{0, 0, 0, 0};
-  st.cmin = f4{0, 0, 0, 0};
+#pragma unroll
+  for (int g = 0; g < 4; ++g) st.cmin[g] = f4{0, 0, 0, 0};
   st.m = kNegInf;
   st.l = 0.0f;
   __syncthreads();
@@ -561,63 +569,47 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     if (tr0 < it.residual_tokens) residual_split<RD>(sq, it, h, tr0, p, st);
   }
 
-  // ---- merge the two waves: rows 4k+v of o need the (m, l) of query row 4k+v
-  __syncthreads();
-  if ((lane >> 4) == 0) {
-    mrg_ml[wave][lane][0] = st.m;
-    mrg_ml[wave][lane][1] = st.l;
-  }
-  __syncthreads();
-  float *fin = reinterpret_cast<float *>(sh.vw);  // [16][128] partial of wave 1
+  // ---- merge the two waves; lane (n, k) holds query n, channels 16*cb + 4k + v
   const int kap = lane >> 4, n = lane & 15;
-  float scale[4], Lrow[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int row = 4 * kap + v;
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mrg_ml[w][row][0]);
-    float L = 0.0f, mine = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float mw = mrg_ml[w][row][0];
-      const float f = mw == kNegInf ? 0.0f : exp2f(mw - M);
-      L += mrg_ml[w][row][1] * f;
-      if (w == wave) mine = f;
-    }
-    scale[v] = mine;
-    Lrow[v] = L;
+  const float l_all = sum_over_slices(st.l);
+  __syncthreads();
+  if (kap == 0) {
+    mrg_ml[wave][n][0] = st.m;
+    mrg_ml[wave][n][1] = l_all;
   }
+  __syncthreads();
+  float M = kNegInf;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mrg_ml[w][n][0]);
+  const float M_ref = M == kNegInf ? 0.0f : M;
+  float L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) L += mrg_ml[w][n][1] * fast_exp2(mrg_ml[w][n][0] - M_ref);
+  const float mine = fast_exp2(st.m - M_ref);
+  float *fin = reinterpret_cast<float *>(sh.vw);  // [16][128] partial of wave 1
+  static_assert(sizeof(sh.vw) >= 16 * kD * sizeof(float), "wave merge fits the value-word staging");
   if (wave == 1) {
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk)
+    for (int cb = 0; cb < 8; ++cb)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) fin[(4 * kap + v) * kD + 16 * blk + n] = st.o[blk][v] * scale[v];
+      for (int v = 0; v < 4; ++v) fin[n * kD + 16 * cb + 4 * kap + v] = st.o[cb][v] * mine;
   }
   __syncthreads();
   const int64_t slot = (item * p.Hkv + h) * p.splits_total + split;
   if (wave == 0) {
     _Float16 *po = p.ws_o + slot * 16 * kD;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int row = 4 * kap + v;
-      const float inv = Lrow[v] > 0.0f ? 1.0f / Lrow[v] : 0.0f;
+    for (int cb = 0; cb < 8; ++cb) {
+      h4 o4;
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk) {
-        const float o = st.o[blk][v] * scale[v] + fin[row * kD + 16 * blk + n];
-        po[row * kD + 16 * blk + n] = to_h(o * inv);
+      for (int v = 0; v < 4; ++v) {
+        const int c = 16 * cb + 4 * kap + v;
+        o4[v] = to_h((st.o[cb][v] * mine + fin[n * kD + c]) * inv);
       }
+      *reinterpret_cast<h4 *>(&po[n * kD + 16 * cb + 4 * kap]) = o4;
     }
     if (kap == 0) {
-      float M = kNegInf;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mrg_ml[w][n][0]);
-      float L = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float mw = mrg_ml[w][n][0];
-        L += mw == kNegInf ? 0.0f : mrg_ml[w][n][1] * exp2f(mw - M);
-      }
       p.ws_ml[(slot * 16 + n) * 2 + 0] = M;
       p.ws_ml[(slot * 16 + n) * 2 + 1] = L;
     }

@@ -71,6 +71,30 @@ __device__ __forceinline__ h8 halves_to_h8(uint4 raw) {
   }
 }
 
+// Max / sum over the four lanes n, n+16, n+32, n+48 (the k-slices of one
+// MFMA column) with the gfx950 lane-swap instructions (VALU, no LDS trip).
+__device__ __forceinline__ float max_over_slices(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  const float y = fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(a[0])),
+                        __builtin_bit_cast(float, static_cast<uint32_t>(a[1])));
+  const auto b = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, y), __builtin_bit_cast(uint32_t, y),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(b[0])),
+               __builtin_bit_cast(float, static_cast<uint32_t>(b[1])));
+}
+
+__device__ __forceinline__ float sum_over_slices(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  const float y = __builtin_bit_cast(float, static_cast<uint32_t>(a[0])) +
+                  __builtin_bit_cast(float, static_cast<uint32_t>(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, y), __builtin_bit_cast(uint32_t, y),
+                                                  false, false);
+  return __builtin_bit_cast(float, static_cast<uint32_t>(b[0])) +
+         __builtin_bit_cast(float, static_cast<uint32_t>(b[1]));
+}
+
 // Buffer resources over one region: loads past `bytes` return zero.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 constexpr int kRsrcWord3 = 0x00020000;  // 32-bit data format, raw (stride 0) addressing
