@@ -36,7 +36,7 @@ using namespace mf;
 
 constexpr int kWaves = 2;
 constexpr int kThreads = kWaves * kWave;
-constexpr int kResWaveTokens = 128;  // residual tokens per wave per residual split
+constexpr int kResWaveTokens = 64;  // residual tokens per wave per residual split
 
 template <int BITS, int G>
 struct DecShared {
@@ -78,17 +78,20 @@ struct WaveState {
 // column = query), folded into the running state; returns with acc holding the
 // probabilities and the output rescaled.
 template <int NP>
-__device__ __forceinline__ void softmax_tile(f4 (&acc)[NP], const bool (&valid)[4], float scale_log2,
+__device__ __forceinline__ void softmax_tile(f4 (&acc)[NP], const bool (&valid)[4], bool full, float scale_log2,
                                              WaveState &st) {
+  if (!full) {  // only the last iteration of a segment has rows past its end
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (!valid[v]) acc[pp][v] = kNegInf;
+  }
   float mx = kNegInf;
 #pragma unroll
   for (int pp = 0; pp < NP; ++pp)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float x = valid[v] ? acc[pp][v] : kNegInf;
-      acc[pp][v] = x;
-      mx = fmaxf(mx, x);
-    }
+    for (int v = 0; v < 4; ++v) mx = fmaxf(mx, acc[pp][v]);
   mx = max_over_slices(mx);
   const float m_new = fmaxf(st.m, mx * scale_log2);
   const float m_ref = m_new == kNegInf ? 0.0f : m_new;  // keeps -inf - m_ref at -inf (exp 0), never NaN
@@ -338,6 +341,7 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
   bool valid[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) valid[v] = (t0 / Gm::TPW + wave * 16 + 4 * kap + v) < nkw;
+  const bool full = t0 / Gm::TPW + Sh::JW <= nkw;  // every word row of the iteration is a real token
 #pragma unroll 1
   for (int half = 0; half < 2; ++half) {
     // ---- keys: logits for 16 word rows x NP positions x 16 query rows
@@ -345,6 +349,16 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
 #pragma unroll
     for (int q = 0; q < NP; ++q) acc[q] = f4{0, 0, 0, 0};
     const uint32_t sel_half = half ? 0x07060302u : 0x05040100u;
+    // field masks and the fp16 magic kept in registers so each extraction is a
+    // single v_and_or_b32 (with them as literals the compiler splits it in two);
+    // the empty asm only hides the constants from constant folding
+    uint32_t kmask[Gm::PMAX + 1], magic = 0x64006400u;
+#pragma unroll
+    for (int e = 0; e <= Gm::PMAX; ++e) {
+      kmask[e] = (Gm::MASK << (BITS * e)) | (Gm::MASK << (16 + BITS * e));
+      asm("" : "+v"(kmask[e]));
+    }
+    asm("" : "+v"(magic));
 #pragma unroll 1
     for (int kb = 0; kb < 4; ++kb) {
       const uint4 *kp = reinterpret_cast<const uint4 *>(&sh.kw[wave][kb][kap][r][0]);
@@ -370,7 +384,7 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const uint32_t src = direct ? y[u] : (y[u] >> Gm::SH);
-          const h2 x = code_pair<BITS>(src, pe);
+          const h2 x = as_h2(and_or(src, kmask[pe], magic)) - h2{to_h(1024.0f), to_h(1024.0f)};
           const h2 k = __builtin_elementwise_fma(x, sp[u] * h2{inv, inv}, mp[u]);
           a[2 * u] = k[0];
           a[2 * u + 1] = k[1];
@@ -378,7 +392,7 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
         acc[pq] = mfma32(a, qfrag, acc[pq]);
       }
     }
-    softmax_tile<NP>(acc, valid, scale_log2, st);
+    softmax_tile<NP>(acc, valid, full, scale_log2, st);
 
     // ---- values of these positions, two at a time: O^T += V^T P^T on
     // v_mfma_f32_16x16x32_f16 with k = (word rows 4k..4k+3) x (positions pa, pb)
@@ -543,7 +557,7 @@ static_assert(kThreads == kD, "key-stat staging maps one thread per channel");
 template <int BITS, int G, int RD, bool TABLE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma_kernel(
     const uc_kivi_item *items, uc_kivi_item single, MfmaParams p) {
-  __shared__ DecShared<BITS, G> sh;
+  __shared__ __align__(16) DecShared<BITS, G> sh;
   __shared__ _Float16 sq[16][kQPad];
   __shared__ float mrg_ml[kWaves][16][2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -561,11 +575,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   st.l = 0.0f;
   __syncthreads();
 
-  if (split < p.splits_packed) {
-    const int64_t t_split = split * p.nst * DecShared<BITS, G>::T;
+  // residual splits first, so their short runs are spread over the launch
+  // instead of forming its tail
+  const int64_t splits_res = p.splits_total - p.splits_packed;
+  if (split >= splits_res) {
+    const int64_t t_split = (split - splits_res) * p.nst * DecShared<BITS, G>::T;
     if (t_split < it.quantized_tokens) packed_split<BITS, G>(sh, sq, it, h, t_split, p, st);
   } else {
-    const int64_t tr0 = (split - p.splits_packed) * kWaves * kResWaveTokens;
+    const int64_t tr0 = split * kWaves * kResWaveTokens;
     if (tr0 < it.residual_tokens) residual_split<RD>(sq, it, h, tr0, p, st);
   }
 
