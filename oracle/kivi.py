@@ -269,3 +269,26 @@ def fake_quant(data, *, bits: int, dim: int, group_size: int, out_dtype: str = "
         code = np.clip(np.rint((chunk - mn) / scale), F32(0), max_int).astype(F32)
         chunks.append((code * scale).astype(F32) + mn)
     return round_to(np.concatenate(chunks, axis=dim).astype(F32), out_dtype)
+
+
+def streamed_split(initial_residual: int, appended: int, *, flush_at: int, group_size: int) -> int:
+    """Tokens moved from the residual into the packed prefix when `appended`
+    tokens arrive one at a time and the residual (starting at
+    `initial_residual` tokens) is flushed -- its whole group-aligned head
+    quantized -- whenever it reaches `flush_at` tokens.
+
+    Streaming has no reference counterpart (UniCache packs once,
+    unicache/storage/physical.py:228-332).  What pins it is the invariant the
+    GPU tests check: after the flushes the packed state equals from_dense of
+    the flushed prefix with residual_length=0, because K groups run along
+    tokens and never straddle the prefix boundary, and V is grouped per token.
+    """
+
+    residual, packed = int(initial_residual), 0
+    for _ in range(int(appended)):
+        residual += 1
+        if residual >= flush_at:
+            moved = (residual // group_size) * group_size
+            packed += moved
+            residual -= moved
+    return packed

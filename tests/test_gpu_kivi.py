@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from oracle import kivi as K
-from tests.helpers import f32, kv_pair
+from tests.helpers import f32, kv_pair, queries
 from unicache_amd.operators import asymmetric_fake_quant, kivi_fake_quant_key, kivi_fake_quant_value
 from unicache_amd.storage import PackedKIVICache
 from unicache_amd.storage.kivi_cuda import dequantize_kivi_chunk, quantize_kivi_native
@@ -156,3 +156,52 @@ def test_repack_monotonic(device):
     assert not cache.repack_monotonic(bits=4, group_size=64)
     assert cache.budget_shortfall_events == 1
     assert cache.resident_bytes < cache.full_precision_bytes
+
+
+@pytest.mark.parametrize("bits,group,tokens,appended", [(2, 32, 1000, 300), (4, 64, 640, 200), (2, 128, 300, 170)])
+def test_streaming_append_flush_equals_from_dense(device, bits, group, tokens, appended):
+    # decode appends one token per step and flushes the residual at 128 tokens;
+    # the result must be bit-identical to packing the same tokens in one go
+    key, value = kv_pair(tokens + appended, seed=120 + bits)
+    kd, vd = key.to(device), value.to(device)
+    ids = torch.arange(tokens + appended)
+    cache = PackedKIVICache.from_dense(kd[:tokens], vd[:tokens], logical_token_ids=ids[:tokens], token_type_id=3,
+                                       k_bits=bits, v_bits=bits, group_size=group, residual_length=128,
+                                       backend="cuda")
+    tq0, tr0 = cache.quantized_tokens, cache.residual_tokens
+    flushed = 0
+    for t in range(tokens, tokens + appended):
+        flushed += cache.append(kd[t:t + 1], vd[t:t + 1], logical_token_ids=ids[t:t + 1], flush_at=128)
+    expect_packed = tq0 + K.streamed_split(tr0, appended, flush_at=128, group_size=group)
+    assert cache.quantized_tokens == expect_packed == tq0 + flushed
+    total = tokens + appended
+    ref = PackedKIVICache.from_dense(kd, vd, logical_token_ids=ids, token_type_id=3, k_bits=bits, v_bits=bits,
+                                     group_size=group, residual_length=total - expect_packed, backend="cuda")
+    assert ref.quantized_tokens == expect_packed
+    for name in ("key_code", "key_scale", "key_minimum", "value_code", "value_scale", "value_minimum",
+                 "residual_key", "residual_value"):
+        assert torch.equal(getattr(cache, name), getattr(ref, name)), name
+    assert torch.equal(cache.logical_token_ids.cpu(), ids)
+    # and the oracle's packing of the flushed prefix
+    seg = K.from_dense(f32(key), f32(value), k_bits=bits, v_bits=bits, group_size=group,
+                       residual_length=total - expect_packed)
+    assert np.array_equal(cache.key_code.cpu().numpy().view(np.uint32), seg.key_code.view(np.uint32))
+    assert np.array_equal(cache.value_code.cpu().numpy().view(np.uint32), seg.value_code.view(np.uint32))
+
+
+def test_streaming_decode_matches_fresh_cache(device):
+    key, value = kv_pair(1500, seed=131)
+    kd, vd = key.to(device), value.to(device)
+    ids = torch.arange(1500)
+    cache = PackedKIVICache.from_dense(kd[:1200], vd[:1200], logical_token_ids=ids[:1200], token_type_id=3,
+                                       k_bits=2, v_bits=2, group_size=32, residual_length=128, backend="cuda")
+    for t in range(1200, 1500):
+        cache.append(kd[t:t + 1], vd[t:t + 1], logical_token_ids=ids[t:t + 1], flush_at=128)
+    fresh = PackedKIVICache.from_dense(kd, vd, logical_token_ids=ids, token_type_id=3, k_bits=2, v_bits=2,
+                                       group_size=32, residual_length=1500 - cache.quantized_tokens, backend="cuda")
+    from unicache_amd.storage.kivi_cuda import packed_kivi_attention_summary
+
+    q = queries(1, seed=132).to(device)
+    a, la = packed_kivi_attention_summary(cache, q)
+    b, lb = packed_kivi_attention_summary(fresh, q)
+    assert torch.equal(a, b) and torch.equal(la, lb)

@@ -198,3 +198,14 @@ def test_rounding_matches_torch_casts():
     th = torch.from_numpy(x).to(torch.float16).float().numpy()
     assert np.array_equal(K.round_bf16(x), tb)
     assert np.array_equal(K.round_f16(x), th)
+
+
+@pytest.mark.parametrize("initial,appended,flush_at,group", [(128, 64, 128, 32), (100, 300, 128, 32),
+                                                           (0, 1000, 128, 32), (130, 7, 160, 64), (31, 1, 32, 32)])
+def test_streamed_split_matches_closed_form(initial, appended, flush_at, group):
+    # flush_at is a multiple of group here, so each flush empties the window:
+    # the packed count is the number of completed windows
+    packed = K.streamed_split(initial, appended, flush_at=flush_at, group_size=group)
+    if initial < flush_at:
+        assert packed == flush_at * ((initial + appended) // flush_at)
+    assert packed % group == 0 and 0 <= initial + appended - packed < flush_at + group

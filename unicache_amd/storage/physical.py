@@ -406,6 +406,78 @@ class PackedKIVICache:
         self.budget_shortfall_events = shortfalls
         return True
 
+    # ------------------------------------------------------------ streaming --
+    # Decode appends one token per step to the full-precision residual; once the
+    # residual reaches `flush_at` tokens its group-aligned head is quantized and
+    # appended to the packed prefix (keys as new token words per channel, values
+    # as new rows).  Because groups never straddle the prefix boundary, the
+    # packed state after a flush equals from_dense(all flushed tokens,
+    # residual_length=0).  UniCache builds caches once (physical.py:228-332);
+    # this is the streaming extension long-context decode needs.
+
+    def append(self, key: torch.Tensor, value: torch.Tensor, *, logical_token_ids: torch.Tensor,
+               flush_at: int | None = None) -> int:
+        """Append [n, Hkv, D] tokens to the residual; flush when it reaches
+        `flush_at` tokens.  Returns the number of tokens packed by the flush."""
+
+        if key.shape != value.shape or key.dim() != 3 or tuple(key.shape[1:]) != (self.num_kv_heads, self.head_dim):
+            raise ValueError("KIVI append expects [tokens, kv_heads, head_dim] K/V matching the cache")
+        if key.dtype != self.residual_key.dtype or value.dtype != self.residual_value.dtype:
+            raise ValueError("KIVI append expects K/V in the residual dtype")
+        nat.require_device(key, value, self.residual_key, what="KIVI append")
+        n = int(key.shape[0])
+        if int(logical_token_ids.numel()) != n:
+            raise ValueError("KIVI append needs one logical id per appended token")
+        tr = self.residual_tokens
+        cap = getattr(self, "_residual_capacity", None)
+        if cap is None or cap[0].shape[0] < tr + n or cap[0].data_ptr() != self.residual_key.data_ptr():
+            size = max(tr + n, 2 * max(tr, 64))
+            buf_k = torch.empty((size, self.num_kv_heads, self.head_dim), dtype=key.dtype, device=key.device)
+            buf_v = torch.empty_like(buf_k)
+            buf_k[:tr].copy_(self.residual_key)
+            buf_v[:tr].copy_(self.residual_value)
+            cap = (buf_k, buf_v)
+            self._residual_capacity = cap
+        cap[0][tr:tr + n].copy_(key)
+        cap[1][tr:tr + n].copy_(value)
+        self.residual_key, self.residual_value = cap[0][:tr + n], cap[1][:tr + n]
+        self.logical_token_ids = torch.cat([self.logical_token_ids, logical_token_ids.to(self.logical_token_ids)])
+        if flush_at is not None and self.residual_tokens >= int(flush_at):
+            return self.flush_residual()
+        return 0
+
+    def flush_residual(self, keep: int = 0) -> int:
+        """Quantize the residual except its last `keep` tokens (rounded so the
+        packed length stays a multiple of group_size) and append it to the
+        packed prefix.  Returns the number of tokens packed."""
+
+        tr = self.residual_tokens
+        count = ((tr - max(0, int(keep))) // self.group_size) * self.group_size
+        if count <= 0:
+            return 0
+        if self.k_bits != self.v_bits or self.k_bits not in (2, 4):
+            raise ValueError("Streaming KIVI flush supports equal 2-bit or 4-bit K/V")
+        if self.quantized_tokens and not self.kernel_native_layout:
+            raise RuntimeError("Streaming KIVI flush requires the kernel-native layout")
+        from .kivi_cuda import quantize_kivi_native
+
+        new = quantize_kivi_native(self.residual_key[:count], self.residual_value[:count],
+                                   k_bits=self.k_bits, v_bits=self.v_bits, group_size=self.group_size)
+        if self.quantized_tokens:
+            old = (self.key_code, self.key_scale, self.key_minimum, self.value_code, self.value_scale,
+                   self.value_minimum)
+            dims = (2, 2, 2, 1, 1, 1)  # keys grow along token words / groups, values along rows
+            new = tuple(torch.cat([a, b], dim=d) for a, b, d in zip(old, new, dims))
+        (self.key_code, self.key_scale, self.key_minimum,
+         self.value_code, self.value_scale, self.value_minimum) = new
+        self.quantized_tokens += count
+        self.kernel_native_layout = True
+        rest_k = self.residual_key[count:].clone()
+        rest_v = self.residual_value[count:].clone()
+        self.residual_key, self.residual_value = rest_k, rest_v
+        self._residual_capacity = None
+        return count
+
     def attention_parts(
         self, query: torch.Tensor
     ) -> tuple[torch.Tensor, Callable[[torch.Tensor], torch.Tensor]]:
