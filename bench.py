@@ -36,7 +36,7 @@ BITS, GROUP, RESIDUAL = 2, 32, 128
 # HBM bytes per step of the default workload from rocprofv3 PMC passes
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 over both decode kernels, the factors
 # from a 1 GiB device copy); profiles/decode_batch_c1.md has the commands.
-MEASURED_TRAFFIC_BYTES = 1_172_804_608
+MEASURED_TRAFFIC_BYTES = 1_232_172_441
 
 
 def make_kv(tokens, *, seed, device, heads=HKV, head_dim=D):
@@ -87,6 +87,38 @@ def time_steps(fn, steps, warmup, stream):
     stop.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
+
+
+def long_context_decode(device, steps, layers=LAYERS, tokens=32768):
+    """Config 4's packed segment as a pure-packed variant: batch 1, 28 layers x
+    32768 tokens (32640 packed 2-bit + 128 residual), one decode step = one
+    uc_kivi_attn_decode_batch over the 28 layers."""
+
+    from unicache_amd.storage import PackedKIVICache
+    from unicache_amd.storage.decode import KiviDecodeBatch
+
+    caches, queries = [], []
+    for layer in range(layers):
+        key, value = make_kv(tokens, seed=7000 + layer, device=device)
+        caches.append(PackedKIVICache.from_dense(key, value, logical_token_ids=torch.arange(tokens, device=device),
+                                                 token_type_id=3, k_bits=BITS, v_bits=BITS, group_size=GROUP,
+                                                 residual_length=RESIDUAL, backend="cuda"))
+        g = torch.Generator(device=device).manual_seed(7500 + layer)
+        queries.append(torch.randn(1, HQ, D, generator=g, device=device).to(torch.bfloat16))
+        del key, value
+    batch = KiviDecodeBatch(caches, queries)
+    stream = torch.cuda.current_stream(device)
+    sid = stream.cuda_stream
+    ms = time_steps(lambda: batch.run(sid), steps, 3, stream)
+    gbs = batch.algorithmic_bytes / (ms * 1e-3) / 1e9
+    return {
+        "workload": f"pure-packed 32k decode: batch 1, {layers} layers x {tokens} tokens "
+                    f"({caches[0].quantized_tokens} packed 2-bit + {caches[0].residual_tokens} residual), Lq=1",
+        "ms_per_step": round(ms, 5),
+        "gbs": round(gbs, 1),
+        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "bytes_per_step": batch.algorithmic_bytes,
+    }
 
 
 def editing_attention(device, steps, layers=LAYERS, bits=BITS):
@@ -253,6 +285,8 @@ def main():
         "pack_gbs": round(pack_bytes / (pack_ms * 1e-3) / 1e9, 2),
     }
     del batch, per_layer, caches, queries
+    torch.cuda.empty_cache()
+    result["decode_32k"] = long_context_decode(device, max(5, args.steps // 2))
     torch.cuda.empty_cache()
     result["editing_mq"] = editing_attention(device, max(3, args.steps // 5))
     if not args.no_cpu_baseline:
