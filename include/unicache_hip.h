@@ -312,6 +312,8 @@ int uc_gqa_gather(const void *key, const void *value, int64_t k_st, int64_t k_sh
  * Bytes of caller-provided workspace an operation needs.
  *   UC_OP_KIVI_AV:     (1, heads_q, query_len, head_dim, total_tokens)
  *   UC_OP_H2O_SCORES:  (1, heads_q, query_len, head_dim, tokens)
+ *                      = max(8 Hq Lq, 2048 (B + 1024) + 4 T B),
+ *                      B = ceil(Hq Lq / 256) + Hq
  * Returns < 0 for an unknown op.
  */
 int64_t uc_workspace_bytes(int op, int64_t n_items, int64_t heads_q, int64_t query_len,

@@ -101,6 +101,50 @@ def test_fused_scores_and_selection_margin(device):
             assert all(abs(exp[h, i] - kth) <= 2 * tol for i in diff)
 
 
+# (Lq, Hq, Hkv, T, D, dtype): ragged row blocks (group * Lq not a multiple of
+# 256), several key chunks with a ragged last tile, one key, group 1, fp16,
+# and head_dim 64 (the generic kernels)
+SCORE_SHAPES = [
+    (5, 28, 4, 300, 128, torch.bfloat16),
+    (100, 8, 2, 1000, 128, torch.float16),
+    (1, 28, 4, 4097, 128, torch.bfloat16),
+    (37, 4, 4, 64, 128, torch.bfloat16),
+    (300, 28, 4, 1, 128, torch.bfloat16),
+    (9, 6, 2, 200, 64, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("lq,hq,hkv,tokens,d,dtype", SCORE_SHAPES)
+def test_fused_scores_shapes(device, lq, hq, hkv, tokens, d, dtype):
+    key, _ = kv_pair(tokens, heads=hkv, head_dim=d, seed=11, dtype=dtype)
+    q = queries(lq, heads=hq, head_dim=d, seed=12, dtype=dtype)
+    got = per_kv_head_scores_from_qk(q.to(device), key.to(device)).cpu().numpy()
+    exp = H.scores_from_qk(f32(q), f32(key))
+    # a probability p whose bf16 rounding flips moves its key's score by at most
+    # p * 2^-8 (one bf16 ulp); flips come from fp32 rounding of the logits and
+    # of the exponential, so the bound is a few ulps of the largest score
+    tol = 2e-3 * max(1.0, float(np.abs(exp).max()))
+    assert np.abs(got - exp).max() <= tol, np.abs(got - exp).max()
+    # mass conservation: every valid row's probabilities sum to 1 up to bf16 rounding
+    assert abs(float(got.sum()) - hq * lq) <= 4e-3 * hq * lq + 1e-3
+
+
+def test_fused_scores_accumulate_strided_deterministic(device):
+    key, _ = kv_pair(777, seed=13)
+    big = queries(64, heads=28, head_dim=256, seed=14)
+    q = big[..., 64:192]
+    exp = H.scores_from_qk(f32(q), f32(key))
+    qd, kd = big.to(device)[..., 64:192], key.to(device)  # head and row strides 256, 7168
+    assert qd.stride() == (28 * 256, 256, 1)
+    first = per_kv_head_scores_from_qk(qd, kd)
+    again = per_kv_head_scores_from_qk(qd, kd)
+    assert torch.equal(first, again)
+    base = torch.full_like(first, 0.25)
+    acc = per_kv_head_scores_from_qk(qd, kd, out=base.clone())
+    assert torch.equal(acc, base + first)
+    assert np.abs(first.cpu().numpy() - exp).max() <= 2e-3 * max(1.0, float(np.abs(exp).max()))
+
+
 def test_trim_update_and_budget(device):
     key, value = kv_pair(64, heads=2, head_dim=16, seed=7)
     rng = np.random.default_rng(7)

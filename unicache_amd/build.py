@@ -26,6 +26,7 @@ SOURCES = [
     "uc_attn_mq.hip",
     "uc_merge.hip",
     "uc_h2o.hip",
+    "uc_h2o_mfma.hip",
 ]
 
 # -ffp-contract=off keeps the pack/dequant arithmetic bit-exact (no implicit

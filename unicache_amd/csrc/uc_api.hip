@@ -4,6 +4,8 @@
 
 namespace uc {
 
+int64_t h2o_mfma_workspace_bytes(int64_t heads_q, int64_t query_len, int64_t tokens);
+
 namespace {
 thread_local std::string g_last_error;
 }
@@ -44,9 +46,13 @@ extern "C" int64_t uc_workspace_bytes(int op, int64_t n_items, int64_t heads_q, 
       // per (item, query head, query row, split): D partial outputs + (max, sum)
       return n_items * heads_q * query_len * splits * (head_dim + 2) * int64_t(sizeof(float));
     }
-    case UC_OP_H2O_SCORES:
-      // per (query head, row): running max and sum of the softmax
-      return heads_q * query_len * 2 * int64_t(sizeof(float));
+    case UC_OP_H2O_SCORES: {
+      // generic path: per (query head, row) the softmax max and sum; MFMA path:
+      // per (query row block, KV head) a partial score for every key
+      const int64_t stats = heads_q * query_len * 2 * int64_t(sizeof(float));
+      const int64_t partial = uc::h2o_mfma_workspace_bytes(heads_q, query_len, max_tokens);
+      return stats > partial ? stats : partial;
+    }
     default:
       return -1;
   }

@@ -3,7 +3,21 @@
 #include "uc_common.h"
 
 namespace uc {
+
+bool h2o_mfma_supported(int dtype, int64_t head_dim, const void *q, int64_t q_si, int64_t q_sh, int64_t q_sd,
+                        const void *k, int64_t k_st, int64_t k_sh, int64_t k_sd);
+int64_t h2o_mfma_workspace_bytes(int64_t heads_q, int64_t query_len, int64_t tokens);
+int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const void *k, int64_t k_st, int64_t k_sh,
+                    int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, float sm_scale, int accumulate, float *scores,
+                    void *workspace, hipStream_t stream);
+
 namespace {
+
+// Zero fill (used instead of a memset node so the call can be graph-captured).
+__global__ void zero_kernel(float *p, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
 
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr int kRows = 16;
@@ -314,11 +328,16 @@ extern "C" int uc_h2o_scores(const void *query, int64_t q_si, int64_t q_sh, int6
   hipStream_t s = as_stream(stream);
   if (tokens == 0) return UC_OK;
   if (query_len == 0) {
-    if (!accumulate)
-      UC_REQUIRE_RT(hipMemsetAsync(scores, 0, heads_kv * tokens * sizeof(float), s) == hipSuccess,
-                    "uc_h2o_scores: memset failed");
+    if (!accumulate) {
+      hipLaunchKernelGGL(zero_kernel, dim3(static_cast<unsigned>(ceil_div(heads_kv * tokens, int64_t(256)))),
+                         dim3(256), 0, s, scores, heads_kv * tokens);
+      return check_launch("uc_h2o_scores (zero)");
+    }
     return UC_OK;
   }
+  if (h2o_mfma_supported(dtype, head_dim, query, q_si, q_sh, q_sd, key, k_st, k_sh, k_sd))
+    return launch_h2o_mfma(dtype, query, q_si, q_sh, key, k_st, k_sh, query_len, heads_q, tokens, heads_kv, sm_scale,
+                           accumulate, scores, workspace, s);
   ScoreArgs a{};
   a.q = query; a.q_si = q_si; a.q_sh = q_sh; a.q_sd = q_sd;
   a.k = key; a.k_st = k_st; a.k_sh = k_sh; a.k_sd = k_sd;
