@@ -5,7 +5,8 @@
 namespace uc {
 
 bool h2o_mfma_supported(int dtype, int64_t head_dim, const void *q, int64_t q_si, int64_t q_sh, int64_t q_sd,
-                        const void *k, int64_t k_st, int64_t k_sh, int64_t k_sd);
+                        const void *k, int64_t k_st, int64_t k_sh, int64_t k_sd, int64_t query_len, int64_t heads_q,
+                        int64_t tokens, int64_t heads_kv);
 int64_t h2o_mfma_workspace_bytes(int64_t heads_q, int64_t query_len, int64_t tokens);
 int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const void *k, int64_t k_st, int64_t k_sh,
                     int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, float sm_scale, int accumulate, float *scores,
@@ -335,7 +336,8 @@ extern "C" int uc_h2o_scores(const void *query, int64_t q_si, int64_t q_sh, int6
     }
     return UC_OK;
   }
-  if (h2o_mfma_supported(dtype, head_dim, query, q_si, q_sh, q_sd, key, k_st, k_sh, k_sd))
+  if (h2o_mfma_supported(dtype, head_dim, query, q_si, q_sh, q_sd, key, k_st, k_sh, k_sd, query_len, heads_q, tokens,
+                         heads_kv))
     return launch_h2o_mfma(dtype, query, q_si, q_sh, key, k_st, k_sh, query_len, heads_q, tokens, heads_kv, sm_scale,
                            accumulate, scores, workspace, s);
   ScoreArgs a{};

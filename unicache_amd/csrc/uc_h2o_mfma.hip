@@ -6,7 +6,8 @@
 //
 // The rows of one KV head (group * Lq of them) are cut into blocks of 256
 // (4 waves x 64 rows, held in registers as MFMA fragments) and the keys into
-// chunks of whole 64-key tiles, staged through double-buffered LDS:
+// chunks of whole 64-key tiles.  Tiles stream into a ring of LDS slots by
+// direct buffer-to-LDS loads issued kHsStages - 1 tiles ahead:
 //   h2o_stats_kernel   (row block, key chunk): S^T = K Q^T, running max and
 //                      sum per row over the chunk -> (max, sum) per chunk;
 //   h2o_scores_kernel  (row block, key chunk): merges the chunks' (max, sum)
@@ -48,7 +49,6 @@ constexpr int kHsQB = 4;  // 16-row blocks per wave
 constexpr int kHsRowsPerWave = 16 * kHsQB;
 constexpr int kHsRows = kHsWaves * kHsRowsPerWave;
 constexpr int kHsTile = 64;
-constexpr int kHsPad = kD + 8;
 constexpr int64_t kHsMinChunk = 256;
 constexpr int64_t kHsTargetBlocks = 1024;
 
@@ -59,125 +59,189 @@ struct HsParams {
   int64_t k_st, k_sh;  // element strides of key tokens and heads
   int64_t Lq, Hq, Hkv, group, rows, T;
   int64_t row_blocks, chunks, chunk;
+  int64_t items, per_xcd;  // work items (KV head, row block, chunk) and items per XCD
   float scale_log2;
   float2 *ml;          // [Hkv][row_blocks][chunks][kHsRows]: (max * log2 e units, sum)
   float *partial;      // [row_blocks][Hkv][T]
 };
 
+// Workgroups are dealt to the 8 XCDs round-robin by launch index.  Work item
+// w = (h * row_blocks + rb) * chunks + c goes to launch index
+// 8 * (w % per_xcd) + w / per_xcd, so each XCD walks one contiguous run of
+// items: one or two KV heads' keys and a few query row blocks at a time,
+// which its own L2 holds.
+constexpr int kXcds = 8;
+
+struct HsItem {
+  int64_t h, rb, c;
+  bool valid;
+};
+
+__device__ __forceinline__ HsItem hs_item(const HsParams &p) {
+  const int64_t id = blockIdx.x;
+  const int64_t w = (id % kXcds) * p.per_xcd + id / kXcds;
+  HsItem it;
+  it.valid = w < p.items;
+  it.c = w % p.chunks;
+  it.rb = (w / p.chunks) % p.row_blocks;
+  it.h = w / (p.chunks * p.row_blocks);
+  return it;
+}
+
+constexpr int kHsStages = 3;
+
+// Key tile slot: row t (256 B of one key) holds its 16-byte chunk c at
+// position c ^ (t & 15), so the 16 rows one MFMA fragment read touches sit in
+// 16 different bank groups.
 struct HsShared {
-  uint16_t kt[2][kHsTile][kHsPad];
+  uint4 kt[kHsStages][kHsTile * 16];
   float col[2][kHsWaves][kHsTile];
 };
 
-// 64 B of one key row per thread: key t0 + tid/4, channels 32*(tid%4) + [0, 32).
-__device__ __forceinline__ void load_keys(uint4 (&r)[4], const HsParams &p, int64_t h, int64_t t0) {
-  const int tid = threadIdx.x, tok = tid / 4, cq = tid % 4;
-  const int64_t t = t0 + tok;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) r[q] = make_uint4(0, 0, 0, 0);
-  if (t < p.T) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(p.k + t * p.k_st + h * p.k_sh + 32 * cq);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) r[q] = src[q];
-  }
-}
+// The key rows [t_begin, t_end) of one KV head, streamed a tile at a time.
+// Rows past t_end fall outside the buffer resource and read as zero.
+struct KeyStream {
+  Rsrc rs;
+  uint32_t row_bytes;
+  int n_tiles;
 
-__device__ __forceinline__ void store_keys(uint16_t (*kt)[kHsPad], const uint4 (&r)[4]) {
-  const int tid = threadIdx.x, tok = tid / 4, cq = tid % 4;
+  __device__ KeyStream(const HsParams &p, int64_t h, int64_t t_begin, int64_t t_end) {
+    row_bytes = static_cast<uint32_t>(p.k_st * 2);
+    rs = make_rsrc(p.k + h * p.k_sh + t_begin * p.k_st, (t_end - t_begin - 1) * p.k_st * 2 + kD * 2);
+    n_tiles = static_cast<int>((t_end - t_begin + kHsTile - 1) / kHsTile);
+  }
+
+  // every thread: 4 loads of 16 B; wave w fills rows 16w .. 16w + 15 of the slot
+  __device__ __forceinline__ void issue(HsShared &sh, int tile) const {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint4 *slot = sh.kt[tile % kHsStages];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4 *>(&kt[tok][32 * cq + 8 * q]) = r[q];
-}
+    for (int j = 0; j < 4; ++j) {
+      const int row = 16 * wave + 4 * j + (lane >> 4);
+      const uint32_t off = static_cast<uint32_t>(tile * kHsTile + row) * row_bytes + 16u * ((lane & 15) ^ (row & 15));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void *)(slot + (16 * wave + 4 * j) * 16), 16, off, 0,
+          0, 0);
+    }
+  }
+
+  __device__ __forceinline__ void prologue(HsShared &sh) const {
+    for (int t = 0; t < kHsStages - 1 && t < n_tiles; ++t) issue(sh, t);
+  }
+
+  // Tile i is in LDS for the whole workgroup; then the slot freed by tile i - 1
+  // is refilled with tile i + kHsStages - 1.
+  __device__ __forceinline__ void acquire(HsShared &sh, int i) const {
+    const int ahead = min(n_tiles - 1, i + kHsStages - 2) - i;  // later tiles this thread still loads
+    static_assert(kHsStages <= 4, "vmcnt cases below");
+    if (ahead >= 2)
+      __builtin_amdgcn_s_waitcnt(kWaitVm8);
+    else if (ahead == 1)
+      __builtin_amdgcn_s_waitcnt(kWaitVm4);
+    else
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (i + kHsStages - 1 < n_tiles) issue(sh, i + kHsStages - 1);
+  }
+
+  // s_waitcnt immediates (gfx9 layout): vmcnt <= N, expcnt and lgkmcnt not waited on
+  static constexpr int kWaitVm0 = 0x0F70, kWaitVm4 = 0x0F74, kWaitVm8 = 0x0F78;
+};
 
 template <int DT>
-__device__ __forceinline__ typename HsOp<DT>::V key_frag(const uint16_t (*kt)[kHsPad], int row, int col) {
-  return __builtin_bit_cast(typename HsOp<DT>::V, *reinterpret_cast<const uint4 *>(&kt[row][col]));
+__device__ __forceinline__ typename HsOp<DT>::V key_frag(const uint4 *slot, int row, int chunk) {
+  return __builtin_bit_cast(typename HsOp<DT>::V, slot[row * 16 + (chunk ^ (row & 15))]);
 }
 
 // Query fragments of the wave's 64 rows: lane (n, k) holds row 16*qb + n,
 // channels 32*kb + 8k + [0, 8).  They are the B operand of K Q^T and the A
-// operand of Q K^T alike.  Rows past the end are zero.
+// operand of Q K^T alike.  Rows past the end load the last row again; their
+// statistics are never used and their probabilities are zeroed.
 template <int DT>
 __device__ __forceinline__ void load_queries(typename HsOp<DT>::V (&qf)[kHsQB][4], const HsParams &p, int64_t h,
                                              int64_t row0) {
   const int lane = threadIdx.x & 63, r = lane & 15, kap = lane >> 4;
 #pragma unroll
   for (int qb = 0; qb < kHsQB; ++qb) {
-    const int64_t row = row0 + 16 * qb + r;
-    const bool ok = row < p.rows;
-    const int64_t g = ok ? row / p.Lq : 0, i = ok ? row % p.Lq : 0;
+    const int64_t row = min(row0 + 16 * qb + r, p.rows - 1);  // rows past the end repeat the last one
+    const uint32_t row32 = static_cast<uint32_t>(row), lq = static_cast<uint32_t>(p.Lq);
+    const int64_t g = row32 / lq, i = row32 % lq;
     const uint16_t *q16 = p.q + i * p.q_si + (h * p.group + g) * p.q_sh + 8 * kap;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-      qf[qb][kb] = __builtin_bit_cast(typename HsOp<DT>::V, ok ? *reinterpret_cast<const uint4 *>(q16 + 32 * kb)
-                                                                : make_uint4(0, 0, 0, 0));
+      qf[qb][kb] = __builtin_bit_cast(typename HsOp<DT>::V, *reinterpret_cast<const uint4 *>(q16 + 32 * kb));
   }
 }
 
+// Exponentials are taken against a per-row reference that is raised only
+// when a logit exceeds it by more than kHsSlack (log2 units): terms stay below
+// 2^kHsSlack, and the common 16-key block needs no rescale and no wait for the
+// rest of the tile.
+constexpr float kHsSlack = 8.0f;
+
 template <int DT>
-__global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(2))) void h2o_stats_kernel(HsParams p) {
+__global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3))) void h2o_stats_kernel(HsParams p) {
   __shared__ __align__(16) HsShared sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
-  const int64_t rb = blockIdx.x, c = blockIdx.y, h = blockIdx.z;
+  const HsItem it = hs_item(p);
+  if (!it.valid) return;
+  const int64_t rb = it.rb, c = it.c, h = it.h;
   const int64_t t_begin = c * p.chunk, t_end = min(p.T, t_begin + p.chunk);
-  const int n_tiles = static_cast<int>((t_end - t_begin + kHsTile - 1) / kHsTile);
 
   typename HsOp<DT>::V qf[kHsQB][4];
   load_queries<DT>(qf, p, h, rb * kHsRows + wave * kHsRowsPerWave);
+  const KeyStream ks(p, h, t_begin, t_end);
+  ks.prologue(sh);
 
-  float m[kHsQB], l[kHsQB];
+  // m: reference of row 16*qb + n (equal in the four k-slices), thr: the raw
+  // logit above which it must move; l: this lane's share of the row sum
+  float m[kHsQB], thr[kHsQB], l[kHsQB];
 #pragma unroll
-  for (int qb = 0; qb < kHsQB; ++qb) m[qb] = kNegInf, l[qb] = 0.0f;
+  for (int qb = 0; qb < kHsQB; ++qb) m[qb] = kNegInf, thr[qb] = kNegInf, l[qb] = 0.0f;
 
-  uint4 kr[4];
-  load_keys(kr, p, h, t_begin);
-  store_keys(sh.kt[0], kr);
-  __syncthreads();
-  for (int i = 0; i < n_tiles; ++i) {
+  for (int i = 0; i < ks.n_tiles; ++i) {
+    ks.acquire(sh, i);
     const int64_t t0 = t_begin + int64_t(i) * kHsTile;
-    if (i + 1 < n_tiles) load_keys(kr, p, h, t0 + kHsTile);
-    const uint16_t(*kt)[kHsPad] = sh.kt[i & 1];
-    f4 acc[4][kHsQB];  // lane (n, k): keys 16*tb + 4k + v of row 16*qb + n
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-      for (int qb = 0; qb < kHsQB; ++qb) acc[tb][qb] = f4{0, 0, 0, 0};
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        const auto a = key_frag<DT>(kt, 16 * tb + r, 32 * kb + 8 * kap);
-#pragma unroll
-        for (int qb = 0; qb < kHsQB; ++qb) acc[tb][qb] = HsOp<DT>::mma(a, qf[qb][kb], acc[tb][qb]);
-      }
+    const uint4 *kt = sh.kt[i % kHsStages];
     const int valid = static_cast<int>(min<int64_t>(kHsTile, t_end - t0));
-    if (valid < kHsTile) {
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
+    for (int tb = 0; tb < 4; ++tb) {
+      f4 acc[kHsQB];  // lane (n, k): keys 16*tb + 4k + v of row 16*qb + n
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const auto a = key_frag<DT>(kt, 16 * tb + r, 4 * kb + kap);
+#pragma unroll
+        for (int qb = 0; qb < kHsQB; ++qb) acc[qb] = HsOp<DT>::mma(a, qf[qb][kb], kb ? acc[qb] : f4{0, 0, 0, 0});
+      }
+      if (valid < kHsTile) {
 #pragma unroll
         for (int v = 0; v < 4; ++v)
           if (16 * tb + 4 * kap + v >= valid)
 #pragma unroll
-            for (int qb = 0; qb < kHsQB; ++qb) acc[tb][qb][v] = kNegInf;
+            for (int qb = 0; qb < kHsQB; ++qb) acc[qb][v] = kNegInf;
+      }
+      float bm[kHsQB];
+      bool raise = false;
+#pragma unroll
+      for (int qb = 0; qb < kHsQB; ++qb) {
+        bm[qb] = fmaxf(fmaxf(acc[qb][0], acc[qb][1]), fmaxf(acc[qb][2], acc[qb][3]));
+        raise |= bm[qb] > thr[qb];
+      }
+      if (__any(raise)) {
+#pragma unroll
+        for (int qb = 0; qb < kHsQB; ++qb) {
+          const float m_new = fmaxf(m[qb], max_over_slices(bm[qb]) * p.scale_log2);
+          l[qb] *= fast_exp2(m[qb] - m_new);
+          m[qb] = m_new;
+          thr[qb] = (m_new + kHsSlack) / p.scale_log2;
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < kHsQB; ++qb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) l[qb] += fast_exp2(__builtin_fmaf(acc[qb][v], p.scale_log2, -m[qb]));
     }
-#pragma unroll
-    for (int qb = 0; qb < kHsQB; ++qb) {
-      float mx = kNegInf;
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) mx = fmaxf(mx, acc[tb][qb][v]);
-      const float m_new = fmaxf(m[qb], max_over_slices(mx) * p.scale_log2);
-      float sum = 0.0f;
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sum += fast_exp2(__builtin_fmaf(acc[tb][qb][v], p.scale_log2, -m_new));
-      l[qb] = l[qb] * fast_exp2(m[qb] - m_new) + sum;
-      m[qb] = m_new;
-    }
-    if (i + 1 < n_tiles) store_keys(sh.kt[(i + 1) & 1], kr);
-    __syncthreads();
   }
 
   float2 *out = p.ml + ((h * p.row_blocks + rb) * p.chunks + c) * kHsRows + wave * kHsRowsPerWave;
@@ -189,17 +253,16 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(2)))
 }
 
 template <int DT>
-__global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(2))) void h2o_scores_kernel(HsParams p) {
+__global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3))) void h2o_scores_kernel(HsParams p) {
   __shared__ __align__(16) HsShared sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
-  const int64_t rb = blockIdx.x, c = blockIdx.y, h = blockIdx.z;
+  const HsItem it = hs_item(p);
+  if (!it.valid) return;
+  const int64_t rb = it.rb, c = it.c, h = it.h;
   const int64_t t_begin = c * p.chunk, t_end = min(p.T, t_begin + p.chunk);
-  const int n_tiles = static_cast<int>((t_end - t_begin + kHsTile - 1) / kHsTile);
   const int64_t row0 = rb * kHsRows + wave * kHsRowsPerWave;
 
-  uint4 kr[4];
-  load_keys(kr, p, h, t_begin);
   typename HsOp<DT>::V qf[kHsQB][4];
   load_queries<DT>(qf, p, h, row0);
 
@@ -208,15 +271,22 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(2)))
   float bias;
   {
     const float2 *src = p.ml + (h * p.row_blocks + rb) * p.chunks * kHsRows + wave * kHsRowsPerWave + lane;
-    float mt = kNegInf;
-    for (int64_t s = 0; s < p.chunks; ++s) mt = fmaxf(mt, src[s * kHsRows].x);
-    float lt = 0.0f;
-    for (int64_t s = 0; s < p.chunks; ++s) {
-      const float2 ml = src[s * kHsRows];
-      lt += ml.y * fast_exp2(ml.x - mt);
+    float mt = kNegInf, lt = 0.0f;
+    for (int64_t s0 = 0; s0 < p.chunks; s0 += 8) {  // eight loads in flight, merged in chunk order
+      float2 ml[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ml[j] = s0 + j < p.chunks ? src[(s0 + j) * kHsRows] : make_float2(kNegInf, 0.0f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float m_new = fmaxf(mt, ml[j].x);
+        if (m_new != kNegInf) lt = lt * fast_exp2(mt - m_new) + ml[j].y * fast_exp2(ml[j].x - m_new);
+        mt = m_new;
+      }
     }
     bias = row0 + lane < p.rows ? mt + __log2f(lt) : __builtin_inff();
   }
+  const KeyStream ks(p, h, t_begin, t_end);
+  ks.prologue(sh);
   float nb[kHsQB][4];  // -bias of rows 16*qb + 4k + v, the rows lane (n, k) sees in Q K^T
 #pragma unroll
   for (int qb = 0; qb < kHsQB; ++qb)
@@ -227,18 +297,21 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
   for (int j = 0; j < 8; ++j) ones[j] = static_cast<__bf16>(1.0f);
 
-  store_keys(sh.kt[0], kr);
-  __syncthreads();
   float *out = p.partial + (rb * p.Hkv + h) * p.T;
-  for (int i = 0; i < n_tiles; ++i) {
+  for (int i = 0; i < ks.n_tiles; ++i) {
+    ks.acquire(sh, i);
     const int64_t t0 = t_begin + int64_t(i) * kHsTile;
-    if (i + 1 < n_tiles) load_keys(kr, p, h, t0 + kHsTile);
-    const uint16_t(*kt)[kHsPad] = sh.kt[i & 1];
+    if (i > 0 && tid < kHsTile) {  // previous tile: its sums were completed before the barrier
+      const float *cp = &sh.col[(i - 1) & 1][0][tid];
+      const int64_t t = t0 - kHsTile + tid;
+      if (t < t_end) out[t] = ((cp[0] + cp[kHsTile]) + cp[2 * kHsTile]) + cp[3 * kHsTile];
+    }
+    const uint4 *kt = sh.kt[i % kHsStages];
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
       typename HsOp<DT>::V kf[4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) kf[kb] = key_frag<DT>(kt, 16 * tb + r, 32 * kb + 8 * kap);
+      for (int kb = 0; kb < 4; ++kb) kf[kb] = key_frag<DT>(kt, 16 * tb + r, 4 * kb + kap);
       f8 e[2];
 #pragma unroll
       for (int qb = 0; qb < kHsQB; ++qb) {
@@ -255,29 +328,30 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(2)))
       cs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_convertvector(e[1], bf8), cs, 0, 0, 0);
       if (kap == 0) sh.col[i & 1][wave][16 * tb + r] = cs[0];
     }
-    if (i > 0 && tid < kHsTile) {  // previous tile: its sums were completed before the last barrier
-      const float *cp = &sh.col[(i - 1) & 1][0][tid];
-      const int64_t t = t0 - kHsTile + tid;
-      if (t < t_end) out[t] = ((cp[0] + cp[kHsTile]) + cp[2 * kHsTile]) + cp[3 * kHsTile];
-    }
-    if (i + 1 < n_tiles) store_keys(sh.kt[(i + 1) & 1], kr);
-    __syncthreads();
   }
+  __syncthreads();
   if (tid < kHsTile) {
-    const float *cp = &sh.col[(n_tiles - 1) & 1][0][tid];
-    const int64_t t = t_begin + int64_t(n_tiles - 1) * kHsTile + tid;
+    const float *cp = &sh.col[(ks.n_tiles - 1) & 1][0][tid];
+    const int64_t t = t_begin + int64_t(ks.n_tiles - 1) * kHsTile + tid;
     if (t < t_end) out[t] = ((cp[0] + cp[kHsTile]) + cp[2 * kHsTile]) + cp[3 * kHsTile];
   }
 }
 
 // scores[h, t] (+)= sum over row blocks, in order, of the partials.
-__global__ __launch_bounds__(256) void h2o_reduce_kernel(const float *partial, int64_t row_blocks, int64_t Hkv,
-                                                         int64_t T, float *scores, int accumulate) {
-  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+__global__ __launch_bounds__(64) void h2o_reduce_kernel(const float *partial, int64_t row_blocks, int64_t Hkv,
+                                                        int64_t T, float *scores, int accumulate) {
+  const int64_t idx = int64_t(blockIdx.x) * 64 + threadIdx.x;
   if (idx >= Hkv * T) return;
-  const int64_t h = idx / T, t = idx % T;
+  const float *src = partial + idx;  // (rb * Hkv + h) * T + t = rb * Hkv * T + idx
+  const int64_t stride = Hkv * T;
   float s = 0.0f;
-  for (int64_t rb = 0; rb < row_blocks; ++rb) s += partial[(rb * Hkv + h) * T + t];
+  for (int64_t rb0 = 0; rb0 < row_blocks; rb0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = rb0 + j < row_blocks ? src[(rb0 + j) * stride] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[j];
+  }
   scores[idx] = accumulate ? scores[idx] + s : s;
 }
 
@@ -304,11 +378,17 @@ int64_t row_block_bound(int64_t heads_q, int64_t query_len) {
 
 }  // namespace
 
+// 16-byte aligned rows of 128 contiguous channels, keys at least a row apart,
+// and 32-bit byte offsets within a key chunk.
 bool h2o_mfma_supported(int dtype, int64_t head_dim, const void *q, int64_t q_si, int64_t q_sh, int64_t q_sd,
-                        const void *k, int64_t k_st, int64_t k_sh, int64_t k_sd) {
+                        const void *k, int64_t k_st, int64_t k_sh, int64_t k_sd, int64_t query_len, int64_t heads_q,
+                        int64_t tokens, int64_t heads_kv) {
   const bool aligned = (reinterpret_cast<uintptr_t>(q) & 15) == 0 && (reinterpret_cast<uintptr_t>(k) & 15) == 0 &&
                        q_si % 8 == 0 && q_sh % 8 == 0 && k_st % 8 == 0 && k_sh % 8 == 0;
-  return (dtype == UC_BF16 || dtype == UC_FP16) && head_dim == kD && q_sd == 1 && k_sd == 1 && aligned;
+  if (!((dtype == UC_BF16 || dtype == UC_FP16) && head_dim == kD && q_sd == 1 && k_sd == 1 && aligned && k_st >= kD))
+    return false;
+  const HsShape shape = h2o_shape(heads_q, heads_kv, query_len, tokens);
+  return (shape.chunk + kHsTile) * k_st * 2 < (int64_t(1) << 32) && heads_q / heads_kv * query_len < (int64_t(1) << 31);
 }
 
 // Stats first ((max, sum) per row block, chunk and row: at most
@@ -326,7 +406,7 @@ int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const 
   const int64_t rbb = row_block_bound(Hq, Lq);
   UC_REQUIRE(shape.row_blocks * Hkv <= rbb && shape.row_blocks * Hkv * shape.chunks <= rbb + kHsTargetBlocks,
              "uc_h2o_scores: internal workspace bound violated");
-  UC_REQUIRE(shape.row_blocks <= 65535 && shape.chunks <= 65535 && Hkv <= 65535, "uc_h2o_scores: grid too large");
+  UC_REQUIRE(shape.row_blocks * shape.chunks * Hkv < (int64_t(1) << 31), "uc_h2o_scores: grid too large");
   HsParams p{};
   p.q = static_cast<const uint16_t *>(q);
   p.q_si = q_si; p.q_sh = q_sh;
@@ -338,7 +418,9 @@ int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const 
   p.ml = static_cast<float2 *>(workspace);
   p.partial = reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                         (rbb + kHsTargetBlocks) * kHsRows * int64_t(sizeof(float2)));
-  const dim3 grid(static_cast<unsigned>(p.row_blocks), static_cast<unsigned>(p.chunks), static_cast<unsigned>(Hkv));
+  p.items = p.row_blocks * p.chunks * Hkv;
+  p.per_xcd = ceil_div(p.items, int64_t(kXcds));
+  const dim3 grid(static_cast<unsigned>(p.per_xcd * kXcds));
   if (dtype == UC_FP16)
     hipLaunchKernelGGL((h2o_stats_kernel<UC_FP16>), grid, dim3(kHsThreads), 0, stream, p);
   else
@@ -351,7 +433,7 @@ int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const 
     hipLaunchKernelGGL((h2o_scores_kernel<UC_BF16>), grid, dim3(kHsThreads), 0, stream, p);
   rc = check_launch("uc_h2o_scores (MFMA scores)");
   if (rc != UC_OK) return rc;
-  hipLaunchKernelGGL(h2o_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(Hkv * T, int64_t(256)))), dim3(256), 0,
+  hipLaunchKernelGGL(h2o_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(Hkv * T, int64_t(64)))), dim3(64), 0,
                      stream, p.partial, p.row_blocks, Hkv, T, scores, accumulate);
   return check_launch("uc_h2o_scores (MFMA reduce)");
 }
