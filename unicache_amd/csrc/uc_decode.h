@@ -18,9 +18,9 @@ inline int64_t decode_num_splits(int64_t max_tokens) {
 
 // MFMA decode (uc_decode_mfma.hip): head_dim 128, 2/4-bit codes.
 #ifndef UC_DECODE_MFMA_NST
-#define UC_DECODE_MFMA_NST 4
+#define UC_DECODE_MFMA_NST 8
 #endif
-constexpr int64_t kDecodeMfmaNst = UC_DECODE_MFMA_NST;  // super-tiles per wave per packed split
+constexpr int64_t kDecodeMfmaNst = UC_DECODE_MFMA_NST;  // super-tiles per packed split
 bool decode_mfma_supported(int bits, int group, int64_t head_dim, int64_t rows);
 int64_t decode_mfma_split_tokens(int bits, int64_t nst);
 int64_t decode_mfma_res_split_tokens();

@@ -1,16 +1,18 @@
 // MFMA split-K decode over KIVI-packed KV (head_dim 128, 2/4-bit codes).
 //
 // One workgroup (2 waves) owns (item, KV head, split of S packed tokens) or
-// a residual split.  The <= 16 query rows of a KV head (query heads x query
+// a residual split.  An iteration stages one super-tile (16 key words of
+// every channel) and each wave takes half of its token positions.  The <= 16 query rows of a KV head (query heads x query
 // length) form the N = 16 columns of every MFMA, so each packed byte is read
 // from HBM once per (item, KV head).
 //
 // Keys (QK^T on v_mfma_f32_16x16x32_f16).  A key word holds TPW = 32/bits
 // tokens of one channel.  MFMA rows are 16 consecutive words at one token
 // position p, so each lane keeps its row's words for 32 channels in
-// registers and reuses them for all TPW positions.  A code is turned into
-// fp16 by OR-ing its bits into the mantissa of 1024 (0x6400), subtracting
-// 1024 exactly and one packed FMA with the fp16 scale/min:
+// registers and reuses them for all positions of its half.  A code at bit
+// offset BITS*e of a 16-bit half is turned into fp16 by OR-ing its bits into
+// the mantissa of 2^(10 - BITS*e), whose mantissa unit is then exactly 1, and
+// subtracting that power of two; one packed FMA with the fp16 scale/min gives
 // k = fp16(code*scale + min).  The query (fp16) is the constant B operand.
 //
 // Values (P.V on v_mfma_f32_16x16x16f16).  A value word holds TPW channels of
@@ -41,23 +43,23 @@ constexpr int kResWaveTokens = 64;  // residual tokens per wave per residual spl
 template <int BITS, int G>
 struct DecShared {
   using Gm = Geo<BITS>;
-  static constexpr int T = kWaves * Gm::ST;  // tokens staged per iteration
+  static constexpr int T = Gm::ST;           // tokens staged per iteration (one super-tile)
   static constexpr int KG = T / G;           // key groups per iteration
   static constexpr int NGD = kD / G;         // value groups per token
   static constexpr int JW = T / Gm::TPW;     // key words per channel per iteration
-  static constexpr int KPAD = kD + 8;        // padded key-stat row (spreads LDS banks)
+  static constexpr int KPAD = kD + 16;       // key-stat row of 72 dwords: the 8 groups one read touches start 8 banks apart
   _Float16 ks[KG][KPAD], km[KG][KPAD];                  // key stats [group][channel]
   _Float16 vs[NGD][Gm::TPW][JW], vm[NGD][Gm::TPW][JW];  // value stats [group][position][word]
-  uint32_t kw[kWaves][4][4][16][8];                     // key words [block][k-slice][row][channel]
+  uint32_t kw[4][4][16][8];                             // key words [block][k-slice][row][channel]
   // value words [position][word][row], rows padded to 20 dwords: a lane reads
   // four rows of one word as 16 bytes, and staging writes hit distinct banks
   static constexpr int VROW = 20;
-  uint32_t vw[kWaves][Gm::TPW][Gm::VW][VROW];
+  uint32_t vw[Gm::TPW][Gm::VW][VROW];
 };
 
 struct MfmaParams {
   int64_t Hq, Hkv, Lq, group, rows;
-  int64_t splits_packed, splits_total, nst;  // nst: super-tiles per wave per packed split
+  int64_t splits_packed, splits_total, nst;  // nst: super-tiles per packed split
   float scale_log2;
   _Float16 *ws_o;  // [items * Hkv * splits][16][128] normalised partial outputs
   float *ws_ml;    // [items * Hkv * splits][16][2] (max in log2 units, sum)
@@ -199,14 +201,15 @@ template <int BITS, int G>
 struct Prefetch {
   using Gm = Geo<BITS>;
   using Sh = DecShared<BITS, G>;
-  static constexpr int NKD = Sh::KG / 2 + 1;               // dwords of one key-stat row segment
+  static constexpr int NKD = (Sh::KG + 1) / 2 + 1;         // dwords of one key-stat row segment
   static constexpr int NVS = Sh::T * Sh::NGD / 8;           // 16-byte chunks of value stats
   static constexpr int VS4 = (NVS + kThreads - 1) / kThreads;
-  static constexpr int NVW = Gm::ST * Gm::VW / 4 / kWave;   // 16-byte chunks of value words per lane
+  static constexpr int NVW = Gm::ST * Gm::VW / 4 / kThreads;  // 16-byte chunks of value words per thread
+  static constexpr int NKB = 4 / kWaves;                       // key-word blocks per thread
   uint32_t ks[NKD], km[NKD];  // thread = channel: KG halves from a 4-byte aligned start
   uint4 vs[VS4], vm[VS4];
   uint4 vw[NVW];
-  uint32_t kw[4][8];
+  uint32_t kw[NKB][8];
 };
 
 template <int BITS, int G>
@@ -229,6 +232,23 @@ __device__ __forceinline__ void value_chunk(int q, int a, int &pos, int &quad) {
   }
 }
 
+// N consecutive dwords from byte offset `off` (4-byte aligned) in the fewest loads.
+template <int N>
+__device__ __forceinline__ void load_dwords(uint32_t (&d)[N], Rsrc r, uint32_t off) {
+  int q = 0;
+#pragma unroll
+  for (; q + 4 <= N; q += 4) {
+    const uint4 v = bload128(r, off + 4u * q);
+    d[q] = v.x, d[q + 1] = v.y, d[q + 2] = v.z, d[q + 3] = v.w;
+  }
+  if constexpr (N % 4 >= 2) {
+    const uint2 v = bload64(r, off + 4u * q);
+    d[q] = v.x, d[q + 1] = v.y;
+    q += 2;
+  }
+  if constexpr (N % 2 == 1) d[N - 1] = bload32(r, off + 4u * (N - 1));
+}
+
 // Issue the loads of the iteration starting at token t0 (multiple of T).
 template <int BITS, int G>
 __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedRegion<BITS, G> &rg, uint32_t t0) {
@@ -239,13 +259,12 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
   const int r = lane & 15, kap = lane >> 4;
   // key stats [D][nkg]: thread = channel, its KG groups as dwords from the
   // 4-byte boundary at or below the first (realigned when staged)
+  // (one 16-byte load per four dwords: each load of a wave touches 64 rows, so
+  // fewer, wider loads mean fewer memory requests)
   {
     const uint32_t d0 = (tid * rg.nkg + t0 / G) >> 1;
-#pragma unroll
-    for (int q = 0; q < Pf::NKD; ++q) {
-      pf.ks[q] = bload32(rg.kscale, (d0 + q) * 4u);
-      pf.km[q] = bload32(rg.kmin, (d0 + q) * 4u);
-    }
+    load_dwords<Pf::NKD>(pf.ks, rg.kscale, d0 * 4u);
+    load_dwords<Pf::NKD>(pf.km, rg.kmin, d0 * 4u);
   }
   // value stats [Tq][NGD]
 #pragma unroll
@@ -255,23 +274,24 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
     pf.vs[q] = bload128(rg.vscale, off);
     pf.vm[q] = bload128(rg.vmin, off);
   }
-  // value words [Tq][VW] of this wave's super-tile, 16 bytes (4 words of one
-  // token) per load: lane (row = lane%16, group a = lane/16) takes word-row
-  // `row` at (position, word quad) = value_chunk(q, a)
-  const uint32_t tw0 = t0 + wave * Gm::ST;
+  // value words [Tq][VW] of the super-tile, 16 bytes (4 words of one token)
+  // per load: lane (row = lane%16, group a = lane/16) of wave w takes word-row
+  // `row` at (position, word quad) = value_chunk(q * kWaves + w, a)
 #pragma unroll
   for (int q = 0; q < Pf::NVW; ++q) {
     int pos, quad;
-    value_chunk<BITS>(q, lane >> 4, pos, quad);
-    const uint32_t tok = tw0 + (lane & 15) * Gm::TPW + pos;
+    value_chunk<BITS>(q * kWaves + wave, lane >> 4, pos, quad);
+    const uint32_t tok = t0 + (lane & 15) * Gm::TPW + pos;
     pf.vw[q] = bload128(rg.vcode, (tok * Gm::VW + 4 * quad) * 4u);
   }
-  // key words [D][nkw]: lane (row r, k-slice kap) reads word J of 32 channels
-  const uint32_t J = t0 / Gm::TPW + wave * 16 + r;
+  // key words [D][nkw]: lane (row r, k-slice kap) of wave w reads word J of
+  // the 16 channels 32 kb + 8 kap + [0, 8) of its blocks kb = NKB w + [0, NKB)
+  const uint32_t J = t0 / Gm::TPW + r;
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
+  for (int b = 0; b < Pf::NKB; ++b)
 #pragma unroll
-    for (int c = 0; c < 8; ++c) pf.kw[kb][c] = bload32(rg.kcode, ((32 * kb + 8 * kap + c) * rg.nkw + J) * 4u);
+    for (int c = 0; c < 8; ++c)
+      pf.kw[b][c] = bload32(rg.kcode, ((32 * (Pf::NKB * wave + b) + 8 * kap + c) * rg.nkw + J) * 4u);
 }
 
 // Move a landed prefetch into the LDS layouts the MFMA loops read.
@@ -286,13 +306,15 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
   {
     const uint32_t shift = ((tid * nkg + t0 / G) & 1u) * 16u;  // odd first element: start at the high half
 #pragma unroll
-    for (int q = 0; q < Sh::KG / 2; ++q) {
+    for (int q = 0; q < (Sh::KG + 1) / 2; ++q) {
       const uint32_t s2 = __builtin_amdgcn_alignbit(pf.ks[q + 1], pf.ks[q], shift);
       const uint32_t m2 = __builtin_amdgcn_alignbit(pf.km[q + 1], pf.km[q], shift);
       sh.ks[2 * q][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s2));
-      sh.ks[2 * q + 1][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s2 >> 16));
       sh.km[2 * q][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(m2));
-      sh.km[2 * q + 1][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(m2 >> 16));
+      if (2 * q + 1 < Sh::KG) {
+        sh.ks[2 * q + 1][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s2 >> 16));
+        sh.km[2 * q + 1][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(m2 >> 16));
+      }
     }
   }
 #pragma unroll
@@ -311,116 +333,115 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
 #pragma unroll
   for (int q = 0; q < Pf::NVW; ++q) {
     int pos, quad;
-    value_chunk<BITS>(q, lane >> 4, pos, quad);
+    value_chunk<BITS>(q * kWaves + wave, lane >> 4, pos, quad);
     const uint32_t w4[4] = {pf.vw[q].x, pf.vw[q].y, pf.vw[q].z, pf.vw[q].w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sh.vw[wave][pos][4 * quad + j][lane & 15] = w4[j];
+    for (int j = 0; j < 4; ++j) sh.vw[pos][4 * quad + j][lane & 15] = w4[j];
   }
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    uint4 *dst = reinterpret_cast<uint4 *>(&sh.kw[wave][kb][kap][r][0]);
-    dst[0] = make_uint4(pf.kw[kb][0], pf.kw[kb][1], pf.kw[kb][2], pf.kw[kb][3]);
-    dst[1] = make_uint4(pf.kw[kb][4], pf.kw[kb][5], pf.kw[kb][6], pf.kw[kb][7]);
+  for (int b = 0; b < Pf::NKB; ++b) {
+    uint4 *dst = reinterpret_cast<uint4 *>(&sh.kw[Pf::NKB * wave + b][kap][r][0]);
+    dst[0] = make_uint4(pf.kw[b][0], pf.kw[b][1], pf.kw[b][2], pf.kw[b][3]);
+    dst[1] = make_uint4(pf.kw[b][4], pf.kw[b][5], pf.kw[b][6], pf.kw[b][7]);
   }
 }
 
-// Logits, softmax and P.V of one staged iteration (this wave's super-tile).
+// Logits, softmax and P.V of this wave's half of the staged super-tile.
 template <int BITS, int G>
 __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const _Float16 (*sq)[kQPad],
                                              uint32_t t0, uint32_t nkw, float scale_log2, WaveState &st) {
   using Gm = Geo<BITS>;
   using Sh = DecShared<BITS, G>;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, half = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
   // value extraction for this lane's channel c = r of each 16-channel block
   const uint32_t vsel = value_selector<BITS>(r);
   const int ve = value_shift<BITS>(r);
   const uint32_t vmask = (Gm::MASK << ve) | (Gm::MASK << (16 + ve));
   constexpr int NP = Gm::TPW / 2;  // positions per half word
-  const int gl = ((wave * 16 + r) * Gm::TPW) / G;  // key group of this lane's row
+  const int gl = (r * Gm::TPW) / G;  // key group of this lane's row
   bool valid[4];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) valid[v] = (t0 / Gm::TPW + wave * 16 + 4 * kap + v) < nkw;
-  const bool full = t0 / Gm::TPW + Sh::JW <= nkw;  // every word row of the iteration is a real token
+  for (int v = 0; v < 4; ++v) valid[v] = (t0 / Gm::TPW + 4 * kap + v) < nkw;
+  const bool full = t0 / Gm::TPW + 16 <= nkw;  // every word row of the iteration is a real token
+
+  // ---- keys: logits for 16 word rows x NP positions x 16 query rows
+  f4 acc[NP];
+#pragma unroll
+  for (int q = 0; q < NP; ++q) acc[q] = f4{0, 0, 0, 0};
+  const uint32_t sel_half = half ? 0x07060302u : 0x05040100u;
+  // field masks and per-offset fp16 powers of two, kept in registers so each
+  // extraction is a single v_and_or_b32 (as literals the compiler splits it
+  // in two); the empty asm only hides the constants from constant folding
+  uint32_t kmask[Gm::PMAX + 1], magic[Gm::PMAX + 1];
+#pragma unroll
+  for (int e = 0; e <= Gm::PMAX; ++e) {
+    kmask[e] = (Gm::MASK << (BITS * e)) | (Gm::MASK << (16 + BITS * e));
+    const uint32_t m16 = uint32_t(25 - BITS * e) << 10;  // fp16 2^(10 - BITS*e)
+    magic[e] = m16 | (m16 << 16);
+    asm("" : "+v"(kmask[e]));
+    asm("" : "+v"(magic[e]));
+  }
 #pragma unroll 1
-  for (int half = 0; half < 2; ++half) {
-    // ---- keys: logits for 16 word rows x NP positions x 16 query rows
-    f4 acc[NP];
+  for (int kb = 0; kb < 4; ++kb) {
+    const uint4 *kp = reinterpret_cast<const uint4 *>(&sh.kw[kb][kap][r][0]);
+    const uint4 w0 = kp[0], w1 = kp[1];
+    const uint32_t kw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    const h8 s8 = *reinterpret_cast<const h8 *>(&sh.ks[gl][32 * kb + 8 * kap]);
+    const h8 m8 = *reinterpret_cast<const h8 *>(&sh.km[gl][32 * kb + 8 * kap]);
+    const h8 qfrag = query_frag(sq, kb, lane);
+    uint32_t y[4];
+    h2 sp[4], mp[4];
 #pragma unroll
-    for (int q = 0; q < NP; ++q) acc[q] = f4{0, 0, 0, 0};
-    const uint32_t sel_half = half ? 0x07060302u : 0x05040100u;
-    // field masks and the fp16 magic kept in registers so each extraction is a
-    // single v_and_or_b32 (with them as literals the compiler splits it in two);
-    // the empty asm only hides the constants from constant folding
-    uint32_t kmask[Gm::PMAX + 1], magic = 0x64006400u;
-#pragma unroll
-    for (int e = 0; e <= Gm::PMAX; ++e) {
-      kmask[e] = (Gm::MASK << (BITS * e)) | (Gm::MASK << (16 + BITS * e));
-      asm("" : "+v"(kmask[e]));
+    for (int u = 0; u < 4; ++u) {
+      y[u] = __builtin_amdgcn_perm(kw[2 * u + 1], kw[2 * u], sel_half);
+      sp[u] = h2{s8[2 * u], s8[2 * u + 1]};
+      mp[u] = h2{m8[2 * u], m8[2 * u + 1]};
     }
-    asm("" : "+v"(magic));
-#pragma unroll 1
-    for (int kb = 0; kb < 4; ++kb) {
-      const uint4 *kp = reinterpret_cast<const uint4 *>(&sh.kw[wave][kb][kap][r][0]);
-      const uint4 w0 = kp[0], w1 = kp[1];
-      const uint32_t kw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-      const h8 s8 = *reinterpret_cast<const h8 *>(&sh.ks[gl][32 * kb + 8 * kap]);
-      const h8 m8 = *reinterpret_cast<const h8 *>(&sh.km[gl][32 * kb + 8 * kap]);
-      const h8 qfrag = query_frag(sq, kb, lane);
-      uint32_t y[4];
-      h2 sp[4], mp[4];
+#pragma unroll
+    for (int pq = 0; pq < NP; ++pq) {
+      const bool direct = pq <= Gm::PMAX;
+      const int pe = direct ? pq : pq - (Gm::PMAX + 1);
+      h8 a;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        y[u] = __builtin_amdgcn_perm(kw[2 * u + 1], kw[2 * u], sel_half);
-        sp[u] = h2{s8[2 * u], s8[2 * u + 1]};
-        mp[u] = h2{m8[2 * u], m8[2 * u + 1]};
+        const uint32_t src = direct ? y[u] : (y[u] >> Gm::SH);
+        const h2 x = as_h2(and_or(src, kmask[pe], magic[pe])) - as_h2(magic[pe]);
+        const h2 k = __builtin_elementwise_fma(x, sp[u], mp[u]);
+        a[2 * u] = k[0];
+        a[2 * u + 1] = k[1];
       }
-#pragma unroll
-      for (int pq = 0; pq < NP; ++pq) {
-        const bool direct = pq <= Gm::PMAX;
-        const int pe = direct ? pq : pq - (Gm::PMAX + 1);
-        const _Float16 inv = to_h(1.0f / float(1u << (BITS * pe)));
-        h8 a;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t src = direct ? y[u] : (y[u] >> Gm::SH);
-          const h2 x = as_h2(and_or(src, kmask[pe], magic)) - h2{to_h(1024.0f), to_h(1024.0f)};
-          const h2 k = __builtin_elementwise_fma(x, sp[u] * h2{inv, inv}, mp[u]);
-          a[2 * u] = k[0];
-          a[2 * u + 1] = k[1];
-        }
-        acc[pq] = mfma32(a, qfrag, acc[pq]);
-      }
+      acc[pq] = mfma32(a, qfrag, acc[pq]);
     }
-    softmax_tile<NP>(acc, valid, full, scale_log2, st);
+  }
+  softmax_tile<NP>(acc, valid, full, scale_log2, st);
 
-    // ---- values of these positions, two at a time: O^T += V^T P^T on
-    // v_mfma_f32_16x16x32_f16 with k = (word rows 4k..4k+3) x (positions pa, pb)
-    const int jw = wave * 16 + 4 * kap;
+  // ---- values of these positions, two at a time: O^T += V^T P^T on
+  // v_mfma_f32_16x16x32_f16 with k = (word rows 4k..4k+3) x (positions pa, pb)
+  const int jw = 4 * kap;
 #pragma unroll
-    for (int j = 0; j < NP / 2; ++j) {
-      const int pa = half * NP + 2 * j, pb = pa + 1;
-      const h4 pa4 = cvt4(acc[2 * j]), pb4 = cvt4(acc[2 * j + 1]);
-      const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
-      h8 ps[Sh::NGD];  // P * value scale, per value group
+  for (int j = 0; j < NP / 2; ++j) {
+    const int pa = half * NP + 2 * j, pb = pa + 1;
+    const h4 pa4 = cvt4(acc[2 * j]), pb4 = cvt4(acc[2 * j + 1]);
+    const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
+    h8 ps[Sh::NGD];  // P * value scale, per value group
 #pragma unroll
-      for (int g = 0; g < Sh::NGD; ++g) {
-        const h4 sa = *reinterpret_cast<const h4 *>(&sh.vs[g][pa][jw]), sb = *reinterpret_cast<const h4 *>(&sh.vs[g][pb][jw]);
-        const h4 ma = *reinterpret_cast<const h4 *>(&sh.vm[g][pa][jw]), mb = *reinterpret_cast<const h4 *>(&sh.vm[g][pb][jw]);
-        ps[g] = p8 * h8{sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
-        // every row of A = the value minima: each output row gets sum_t P*min
-        st.cmin[g] = mfma32(h8{ma[0], ma[1], ma[2], ma[3], mb[0], mb[1], mb[2], mb[3]}, p8, st.cmin[g]);
-      }
+    for (int g = 0; g < Sh::NGD; ++g) {
+      const h4 sa = *reinterpret_cast<const h4 *>(&sh.vs[g][pa][jw]), sb = *reinterpret_cast<const h4 *>(&sh.vs[g][pb][jw]);
+      const h4 ma = *reinterpret_cast<const h4 *>(&sh.vm[g][pa][jw]), mb = *reinterpret_cast<const h4 *>(&sh.vm[g][pb][jw]);
+      ps[g] = p8 * h8{sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+      // every row of A = the value minima: each output row gets sum_t P*min
+      st.cmin[g] = mfma32(h8{ma[0], ma[1], ma[2], ma[3], mb[0], mb[1], mb[2], mb[3]}, p8, st.cmin[g]);
+    }
 #pragma unroll
-      for (int cb = 0; cb < 8; ++cb) {
-        const int wi = BITS == 2 ? cb : 2 * cb + (r >> 3);  // word holding channel 16*cb + r
-        const uint4 wa = *reinterpret_cast<const uint4 *>(&sh.vw[wave][pa][wi][4 * kap]);
-        const uint4 wb = *reinterpret_cast<const uint4 *>(&sh.vw[wave][pb][wi][4 * kap]);
-        const h2 x0 = value_pair<BITS>(wa.x, wa.y, vsel, vmask), x1 = value_pair<BITS>(wa.z, wa.w, vsel, vmask);
-        const h2 x2 = value_pair<BITS>(wb.x, wb.y, vsel, vmask), x3 = value_pair<BITS>(wb.z, wb.w, vsel, vmask);
-        const h8 av = h8{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
-        st.o[cb] = mfma32(av, ps[(16 * cb) / G], st.o[cb]);
-      }
+    for (int cb = 0; cb < 8; ++cb) {
+      const int wi = BITS == 2 ? cb : 2 * cb + (r >> 3);  // word holding channel 16*cb + r
+      const uint4 wa = *reinterpret_cast<const uint4 *>(&sh.vw[pa][wi][4 * kap]);
+      const uint4 wb = *reinterpret_cast<const uint4 *>(&sh.vw[pb][wi][4 * kap]);
+      const h2 x0 = value_pair<BITS>(wa.x, wa.y, vsel, vmask), x1 = value_pair<BITS>(wa.z, wa.w, vsel, vmask);
+      const h2 x2 = value_pair<BITS>(wb.x, wb.y, vsel, vmask), x3 = value_pair<BITS>(wb.z, wb.w, vsel, vmask);
+      const h8 av = h8{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
+      st.o[cb] = mfma32(av, ps[(16 * cb) / G], st.o[cb]);
     }
   }
 }
@@ -695,8 +716,8 @@ __global__ __launch_bounds__(256) void decode_mfma_combine(const uc_kivi_item *i
 }  // namespace
 
 // Packed tokens per split of the MFMA decode for `bits` (super-tiles per
-// wave x waves x tokens per super-tile).
-int64_t decode_mfma_split_tokens(int bits, int64_t nst) { return nst * kWaves * 16 * (32 / bits); }
+// split x tokens per super-tile).
+int64_t decode_mfma_split_tokens(int bits, int64_t nst) { return nst * 16 * (32 / bits); }
 
 int64_t decode_mfma_res_split_tokens() { return kWaves * kResWaveTokens; }
 
