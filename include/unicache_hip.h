@@ -309,6 +309,28 @@ int uc_gqa_gather(const void *key, const void *value, int64_t k_st, int64_t k_sh
                   uc_stream_t stream);
 
 /*
+ * Keep-mask compaction, step 1: for the n rows of a packed dense cache,
+ *   dst_index[t] = number of kept rows before t   if keep[t] != 0
+ *                = -1                             otherwise
+ * and *total (device int64) = number of kept rows.  keep is one byte per row
+ * (torch.bool), 16-byte aligned; n < 2^31.
+ * Replaces: the per-sample boolean masks of TensorCacheStorageBackend.compact
+ * (tensor_backend.py:54-77).
+ */
+int uc_mask_scan(const uint8_t *keep, int64_t n, int32_t *dst_index, int64_t *total, uc_stream_t stream);
+
+/*
+ * Keep-mask compaction, step 2: row t of src (row_bytes contiguous bytes at
+ * t * src_row_stride_bytes) is copied to dst + dst_index[t] * row_bytes for
+ * every t with dst_index[t] >= 0 (the output of uc_mask_scan).  Used for the
+ * key, value and type-id rows.
+ * Replaces: key[mask], value[mask], key_type_ids[mask]
+ * (tensor_backend.py:66-77).
+ */
+int uc_compact_rows(const void *src, int64_t src_row_stride_bytes, int64_t row_bytes,
+                    const int32_t *dst_index, int64_t n, void *dst, uc_stream_t stream);
+
+/*
  * Bytes of caller-provided workspace an operation needs.
  *   UC_OP_KIVI_AV:     (1, heads_q, query_len, head_dim, total_tokens)
  *   UC_OP_H2O_SCORES:  (1, heads_q, query_len, head_dim, tokens)

@@ -139,3 +139,24 @@ def min_selection_margin(scores, heavy_k: int, recent: int) -> float:
         if 0 < heavy_k < row.shape[0]:
             gaps.append(row[heavy_k - 1] - row[heavy_k])
     return float(min(gaps)) if gaps else math.inf
+
+
+def compact(key, value, type_ids, sample_lens, keep_masks):
+    """tensor_backend.py:54-77: per packed sample, the rows its keep mask
+    keeps, samples concatenated in order; returns (key, value, type_ids,
+    kept per sample)."""
+
+    k, v = np.asarray(key), np.asarray(value)
+    ids = None if type_ids is None else np.asarray(type_ids)
+    ok, ov, oi, lens = [], [], [], []
+    off = 0
+    for n, m in zip(sample_lens, keep_masks):
+        m = np.asarray(m, dtype=bool)
+        ok.append(k[off:off + n][m])
+        ov.append(v[off:off + n][m])
+        if ids is not None:
+            oi.append(ids[off:off + n][m])
+        lens.append(int(m.sum()))
+        off += n
+    cat = lambda xs, like: np.concatenate(xs) if xs else like[:0]
+    return cat(ok, k), cat(ov, v), None if ids is None else cat(oi, ids), lens

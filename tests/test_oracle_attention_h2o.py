@@ -146,3 +146,27 @@ def test_trim_reselects_within_retained():
     k2, _, i2, s2 = H.trim(key, key, ids, sc, 3, 1)
     assert i2.tolist() == [[10, 12, 15], [21, 22, 25]]
     assert s2.tolist() == [[5, 4, 0], [9, 9, 0]]
+
+
+def test_compact_brute_force_and_known_answer():
+    # rows 0..9 in two samples of 4 and 6: keep rows 1, 3 of the first and
+    # 0, 4, 5 of the second -> source rows 1, 3, 4, 8, 9 in order
+    key = np.arange(10 * 2 * 3, dtype=np.float32).reshape(10, 2, 3)
+    ids = np.arange(100, 110, dtype=np.int64)
+    masks = [np.array([0, 1, 0, 1], bool), np.array([1, 0, 0, 0, 1, 1], bool)]
+    ok, ov, oi, lens = H.compact(key, -key, ids, [4, 6], masks)
+    assert np.array_equal(ok, key[[1, 3, 4, 8, 9]]) and np.array_equal(ov, -key[[1, 3, 4, 8, 9]])
+    assert np.array_equal(oi, [101, 103, 104, 108, 109]) and lens == [2, 3]
+    # brute force: explicit row loop over random ragged samples
+    rng = np.random.default_rng(3)
+    lens_in = [0, 7, 1, 13]
+    full = rng.random((sum(lens_in), 2, 3)).astype(np.float32)
+    masks = [rng.random(n) < 0.4 for n in lens_in]
+    ok, _, _, lens = H.compact(full, full, None, lens_in, masks)
+    rows, off = [], 0
+    for n, m in zip(lens_in, masks):
+        for i in range(n):
+            if m[i]:
+                rows.append(full[off + i])
+        off += n
+    assert np.array_equal(ok, np.stack(rows)) and lens == [int(m.sum()) for m in masks]

@@ -27,6 +27,7 @@ SOURCES = [
     "uc_merge.hip",
     "uc_h2o.hip",
     "uc_h2o_mfma.hip",
+    "uc_compact.hip",
 ]
 
 # -ffp-contract=off keeps the pack/dequant arithmetic bit-exact (no implicit

@@ -1,0 +1,118 @@
+// Keep-mask row compaction of the dense cache (tensor_backend.py:54-77): the
+// rows t with keep[t] != 0 move, in order, to the front of the output.
+//
+// uc_mask_scan: one workgroup of 1024 threads; thread i counts the kept rows
+// of its contiguous chunk (16-byte mask loads), a workgroup exclusive scan
+// turns the counts into chunk offsets, and every thread writes the
+// destination row of each of its kept rows.  Deterministic, one pass over the
+// mask plus one over the destination array.
+//
+// uc_compact_rows: one thread per 16 (or 8, 4, 2, 1) bytes of a row, rows of
+// dropped tokens exit at once; the copy of a kept row is fully coalesced.
+#include "uc_common.h"
+
+namespace uc {
+namespace {
+
+constexpr int kScanThreads = 1024;
+
+__global__ __launch_bounds__(kScanThreads) void mask_scan_kernel(const uint8_t *keep, int64_t n, int64_t chunk,
+                                                                 int32_t *dst, int64_t *total) {
+  __shared__ int64_t part[kScanThreads];
+  const int tid = threadIdx.x;
+  const int64_t b = tid * chunk, e = min(n, b + chunk);
+  int64_t cnt = 0;
+  if (b < e) {
+    int64_t t = b;
+    // chunk is a multiple of 16 and keep is 16-byte aligned: whole uint4 runs
+    for (; t + 16 <= e; t += 16) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(keep + t);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // one per nonzero byte: set bit 0 of each nonzero byte, then count
+        const uint32_t nz = ((w[j] | (w[j] >> 1) | (w[j] >> 2) | (w[j] >> 3) | (w[j] >> 4) | (w[j] >> 5) |
+                              (w[j] >> 6) | (w[j] >> 7)) & 0x01010101u);
+        cnt += __builtin_popcount(nz);
+      }
+    }
+    for (; t < e; ++t) cnt += keep[t] != 0;
+  }
+  part[tid] = cnt;
+  __syncthreads();
+  // Hillis-Steele inclusive scan over 1024 partial counts
+  for (int off = 1; off < kScanThreads; off <<= 1) {
+    const int64_t add = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  int64_t pos = part[tid] - cnt;
+  if (tid == kScanThreads - 1) *total = part[tid];
+  for (int64_t t = b; t < e; ++t) {
+    if (keep[t] != 0) {
+      dst[t] = static_cast<int32_t>(pos);
+      ++pos;
+    } else {
+      dst[t] = -1;
+    }
+  }
+}
+
+template <typename V>
+__global__ __launch_bounds__(256) void compact_rows_kernel(const char *src, int64_t src_stride, int64_t row_bytes,
+                                                           const int32_t *dst_index, int64_t n, char *dst,
+                                                           int64_t per_row) {
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t t = idx / per_row, c = idx % per_row;
+  if (t >= n) return;
+  const int32_t d = dst_index[t];
+  if (d < 0) return;
+  const V v = *reinterpret_cast<const V *>(src + t * src_stride + c * int64_t(sizeof(V)));
+  *reinterpret_cast<V *>(dst + int64_t(d) * row_bytes + c * int64_t(sizeof(V))) = v;
+}
+
+template <typename V>
+int launch_compact(const void *src, int64_t src_stride, int64_t row_bytes, const int32_t *dst_index, int64_t n,
+                   void *dst, hipStream_t s) {
+  const int64_t per_row = row_bytes / int64_t(sizeof(V));
+  const int64_t threads = n * per_row;
+  hipLaunchKernelGGL(compact_rows_kernel<V>, dim3(static_cast<unsigned>(ceil_div(threads, int64_t(256)))), dim3(256),
+                     0, s, static_cast<const char *>(src), src_stride, row_bytes, dst_index, n,
+                     static_cast<char *>(dst), per_row);
+  return check_launch("uc_compact_rows");
+}
+
+}  // namespace
+}  // namespace uc
+
+using namespace uc;
+
+extern "C" int uc_mask_scan(const uint8_t *keep, int64_t n, int32_t *dst_index, int64_t *total,
+                            uc_stream_t stream) {
+  clear_error();
+  UC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "uc_mask_scan: row count %lld out of range", (long long)n);
+  UC_REQUIRE(total != nullptr && (n == 0 || (keep != nullptr && dst_index != nullptr)),
+             "uc_mask_scan: null pointer");
+  UC_REQUIRE((reinterpret_cast<uintptr_t>(keep) & 15) == 0, "uc_mask_scan: keep must be 16-byte aligned");
+  const int64_t chunk = ceil_div(ceil_div(n, int64_t(kScanThreads)), int64_t(16)) * 16;
+  hipLaunchKernelGGL(mask_scan_kernel, dim3(1), dim3(kScanThreads), 0, as_stream(stream), keep, n,
+                     chunk > 0 ? chunk : 16, dst_index, total);
+  return check_launch("uc_mask_scan");
+}
+
+extern "C" int uc_compact_rows(const void *src, int64_t src_row_stride_bytes, int64_t row_bytes,
+                               const int32_t *dst_index, int64_t n, void *dst, uc_stream_t stream) {
+  clear_error();
+  UC_REQUIRE(n >= 0 && row_bytes >= 0 && src_row_stride_bytes >= row_bytes, "uc_compact_rows: bad shape");
+  if (n == 0 || row_bytes == 0) return UC_OK;
+  UC_REQUIRE(src != nullptr && dst != nullptr && dst_index != nullptr, "uc_compact_rows: null pointer");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) |
+                          static_cast<uintptr_t>(src_row_stride_bytes) | static_cast<uintptr_t>(row_bytes);
+  const hipStream_t s = as_stream(stream);
+  if ((align & 15) == 0) return launch_compact<uint4>(src, src_row_stride_bytes, row_bytes, dst_index, n, dst, s);
+  if ((align & 7) == 0) return launch_compact<uint2>(src, src_row_stride_bytes, row_bytes, dst_index, n, dst, s);
+  if ((align & 3) == 0) return launch_compact<uint32_t>(src, src_row_stride_bytes, row_bytes, dst_index, n, dst, s);
+  if ((align & 1) == 0) return launch_compact<uint16_t>(src, src_row_stride_bytes, row_bytes, dst_index, n, dst, s);
+  return launch_compact<uint8_t>(src, src_row_stride_bytes, row_bytes, dst_index, n, dst, s);
+}

@@ -3,8 +3,8 @@
 
 compact_and_materialize turns PhysicalCacheRequests into PackedKIVICache /
 GQAH2OCache segments (HIP pack, H2O select and gather) and removes the
-materialised tokens from the dense cache.  The boolean keep-mask row
-compaction of the remaining dense tokens uses torch indexing on the GPU.
+materialised tokens from the dense cache.  The keep-mask row compaction of
+the remaining dense tokens runs as a HIP mask scan plus row copies.
 """
 
 from __future__ import annotations
@@ -14,8 +14,42 @@ from typing import Any
 
 import torch
 
+from .. import _native as nat
 from ..core.decisions import PhysicalCacheRequest
 from .physical import GQAH2OCache, PackedKIVICache
+
+
+def compact_rows(tensors: list[torch.Tensor | None], keep: torch.Tensor) -> list[torch.Tensor | None]:
+    """tensor[keep] for every tensor (rows along dim 0, each row contiguous),
+    in order, on the HIP scan + copy kernels (tensor_backend.py:66-77)."""
+
+    device = nat.require_device(keep, *[t for t in tensors if t is not None], what="Dense cache compaction")
+    n = int(keep.numel())
+    mask = keep.to(device=device, dtype=torch.bool).contiguous()
+    if mask.data_ptr() % 16:
+        mask = mask.clone()
+    dst = torch.empty(n, dtype=torch.int32, device=device)
+    total = torch.zeros(1, dtype=torch.int64, device=device)
+    stream = nat.stream(device)
+    nat.call("uc_mask_scan", mask.data_ptr(), n, dst.data_ptr(), total.data_ptr(), stream)
+    kept = int(total.item()) if n else 0
+    out: list[torch.Tensor | None] = []
+    for t in tensors:
+        if t is None:
+            out.append(None)
+            continue
+        if int(t.shape[0]) != n:
+            raise ValueError("Keep mask does not match the cache token count")
+        row = t[0] if n else t.new_empty(t.shape[1:])
+        if n and not row.is_contiguous():
+            t = t.contiguous()
+        row_bytes = int(row.numel() * t.element_size())
+        res = torch.empty((kept, *t.shape[1:]), dtype=t.dtype, device=device)
+        if kept:
+            nat.call("uc_compact_rows", t.data_ptr(), int(t.stride(0)) * t.element_size(), row_bytes,
+                     dst.data_ptr(), n, res.data_ptr(), stream)
+        out.append(res)
+    return out
 
 
 @dataclass
@@ -78,10 +112,10 @@ class TensorCacheStorageBackend:
                 raise ValueError("Keep mask does not match its packed sample length")
             masks.append(mask)
         full = torch.cat(masks) if masks else torch.zeros(0, dtype=torch.bool, device=key.device)
-        compacted_key = key[full]
-        compacted_value = value[full]
-        compacted_types = None
-        if key_type_ids is not None:
+        same = key_type_ids is None or key_type_ids.device == key.device
+        compacted_key, compacted_value, compacted_types = compact_rows(
+            [key, value, key_type_ids if same else None], full)
+        if not same:  # type ids kept on another device are indexed there, as the reference does
             compacted_types = key_type_ids[full.to(key_type_ids.device)]
         original_bytes = int(key.numel() * key.element_size() + value.numel() * value.element_size())
         compacted_bytes = int(
