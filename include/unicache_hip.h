@@ -309,6 +309,20 @@ int uc_gqa_gather(const void *key, const void *value, int64_t k_st, int64_t k_sh
                   uc_stream_t stream);
 
 /*
+ * uc_h2o_scores with the softmax normaliser given instead of computed:
+ *   P = bf16(exp(sm_scale * q_i . k_t - lse[h, i]))
+ * lse is fp32 [Hq, Lq] (natural log), e.g. the global LSE of a mixed-segment
+ * attention call; the workspace is sized as for uc_h2o_scores.
+ * Replaces: the H2O update of _run_fused_mixed_attention, exp(logits -
+ * global_lse).to(bf16) followed by update_scores (adapters/bagel.py:1845-1856).
+ */
+int uc_h2o_scores_lse(const void *query, int64_t q_si, int64_t q_sh, int64_t q_sd,
+                      const void *key, int64_t k_st, int64_t k_sh, int64_t k_sd, int dtype,
+                      int64_t query_len, int64_t heads_q, int64_t tokens, int64_t heads_kv,
+                      int64_t head_dim, float sm_scale, const float *lse, int accumulate,
+                      float *scores, void *workspace, uc_stream_t stream);
+
+/*
  * Keep-mask compaction, step 1: for the n rows of a packed dense cache,
  *   dst_index[t] = number of kept rows before t   if keep[t] != 0
  *                = -1                             otherwise

@@ -7,6 +7,7 @@ import pytest
 import torch
 
 from oracle import h2o as H
+from oracle.kivi import round_bf16
 from tests.helpers import f32, kv_pair, queries
 from unicache_amd.operators import per_kv_head_scores_from_probs, per_kv_head_scores_from_qk
 from unicache_amd.storage import GQAH2OCache
@@ -143,6 +144,25 @@ def test_fused_scores_accumulate_strided_deterministic(device):
     acc = per_kv_head_scores_from_qk(qd, kd, out=base.clone())
     assert torch.equal(acc, base + first)
     assert np.abs(first.cpu().numpy() - exp).max() <= 2e-3 * max(1.0, float(np.abs(exp).max()))
+
+
+@pytest.mark.parametrize("d,lq,tokens", [(128, 20, 500), (64, 9, 200)])
+def test_fused_scores_with_given_lse(device, d, lq, tokens):
+    # probabilities against a caller LSE (the global LSE of a mixed-segment
+    # call): bf16(exp(logit - lse)); here the LSE of a larger key set, so rows
+    # do not sum to one
+    import math
+
+    from oracle import attention as A
+
+    key, _ = kv_pair(tokens, head_dim=d, seed=14)
+    extra, _ = kv_pair(300, head_dim=d, seed=15)
+    q = queries(lq, head_dim=d, seed=16)
+    lse = A.logsumexp(A.gqa_logits(f32(q), np.concatenate([f32(key), f32(extra)])) / math.sqrt(d))
+    got = per_kv_head_scores_from_qk(q.to(device), key.to(device), lse=torch.from_numpy(lse).to(device))
+    probs = round_bf16(np.exp(A.gqa_logits(f32(q), f32(key)) / math.sqrt(d) - lse[:, :, None]).astype(np.float32))
+    exp = H.scores_from_probs(probs, 4)
+    assert np.abs(got.cpu().numpy() - exp).max() <= 2e-3 * max(1.0, float(np.abs(exp).max()))
 
 
 def test_trim_update_and_budget(device):

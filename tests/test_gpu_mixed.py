@@ -1,0 +1,93 @@
+"""GPU parity of mixed-segment attention (_run_fused_mixed_attention,
+adapters/bagel.py:1598-1858): dense + H2O + packed segments in one call
+against the fp32 oracle softmax over the concatenated (dequantized) keys, and
+the H2O update against exp(logit - global LSE) rounded to bf16."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import h2o as H
+from oracle import kivi as K
+from oracle.kivi import round_bf16
+from tests.helpers import assert_close, f32, kv_pair, queries
+from unicache_amd.adapters.bagel import run_fused_mixed_attention
+from unicache_amd.storage import GQAH2OCache, PackedKIVICache
+
+pytestmark = pytest.mark.gpu
+
+
+def _segments(device, *, second_packed):
+    dk, dv = kv_pair(64, seed=21)
+    hk, hv = kv_pair(300, seed=22)
+    h2o_live = GQAH2OCache.from_dense(hk.to(device), hv.to(device), logical_token_ids=torch.arange(300),
+                                      token_type_id=1, per_kv_head_scores=torch.rand(4, 300).to(device),
+                                      target_tokens=60, recent_tokens=15)
+    fk, fv = kv_pair(200, seed=23)
+    h2o_frozen = GQAH2OCache.from_dense(fk.to(device), fv.to(device), logical_token_ids=torch.arange(200),
+                                        token_type_id=2, per_kv_head_scores=torch.rand(4, 200).to(device),
+                                        target_tokens=40, recent_tokens=10, selection_frozen=True)
+    pk, pv = kv_pair(1000, seed=24)
+    packed = [PackedKIVICache.from_dense(pk.to(device), pv.to(device), logical_token_ids=torch.arange(1000),
+                                         token_type_id=3, k_bits=2, v_bits=2, group_size=32, residual_length=128,
+                                         backend="cuda")]
+    segs = [K.from_dense(f32(pk), f32(pv), k_bits=2, v_bits=2, group_size=32, residual_length=128)]
+    if second_packed:
+        sk, sv = kv_pair(700, seed=25)
+        packed.append(PackedKIVICache.from_dense(sk.to(device), sv.to(device), logical_token_ids=torch.arange(700),
+                                                 token_type_id=4, k_bits=4, v_bits=4, group_size=64,
+                                                 residual_length=32, backend="cuda"))
+        segs.append(K.from_dense(f32(sk), f32(sv), k_bits=4, v_bits=4, group_size=64, residual_length=32))
+    return (dk, dv), [h2o_live, h2o_frozen], packed, segs
+
+
+def _oracle_keys(dense, h2o, segs):
+    """[dense, H2O..., residuals...] then the packed prefixes: one softmax over
+    all of them is what the LSE merge of UniCache's segments computes."""
+
+    ks, vs = [f32(dense[0])], [f32(dense[1])]
+    for s in h2o:
+        ks.append(np.transpose(f32(s.key), (1, 0, 2)))
+        vs.append(np.transpose(f32(s.value), (1, 0, 2)))
+    for seg in segs:
+        ks.append(np.asarray(seg.residual_key, dtype=np.float32))
+        vs.append(np.asarray(seg.residual_value, dtype=np.float32))
+    for seg in segs:
+        k, v = K.dequantize(seg, "fp32")
+        ks.append(k[: seg.quantized_tokens])
+        vs.append(v[: seg.quantized_tokens])
+    return np.concatenate(ks), np.concatenate(vs)
+
+
+@pytest.mark.parametrize("lq", [1, 40])
+@pytest.mark.parametrize("second_packed", [False, True])
+def test_mixed_attention_matches_global_softmax(device, lq, second_packed):
+    dense, h2o, packed, segs = _segments(device, second_packed=second_packed)
+    q = queries(lq, seed=30 + lq)
+    live = h2o[0]
+    before = live.cumulative_scores.clone().cpu().numpy()
+    live_key = np.transpose(f32(live.key), (1, 0, 2))
+    ek, ev = _oracle_keys(dense, h2o, segs)
+    eo, el = A.attention_summary(f32(q), ek, ev)
+    out, lse = run_fused_mixed_attention(q.to(device), dense[0].to(device), dense[1].to(device),
+                                         [*h2o, *packed], return_lse=True)
+    assert out.shape == (lq, 28, 128) and out.dtype == torch.bfloat16
+    assert_close(f32(out), eo, what="mixed out")
+    assert_close(f32(lse), el, max_abs=1e-2, mean_abs=1e-3, what="mixed lse")
+    # the live H2O segment received bf16(exp(logit - global lse)) per retained key
+    logits = A.gqa_logits(f32(q), live_key) / math.sqrt(128)
+    probs = round_bf16(np.exp(logits - f32(lse)[:, :, None]).astype(np.float32))
+    expect = before + H.scores_from_probs(probs, 4)
+    got = live.cumulative_scores.cpu().numpy()
+    assert np.abs(got - expect).max() <= 2e-3 * max(1.0, float(np.abs(expect).max()))
+    # the frozen one is untouched
+    assert h2o[1].retained_tokens == 40
+
+
+def test_mixed_attention_requires_packed(device):
+    dk, dv = kv_pair(16, seed=1)
+    with pytest.raises(RuntimeError):
+        run_fused_mixed_attention(queries(1).to(device), dk.to(device), dv.to(device), [])

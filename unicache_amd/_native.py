@@ -87,6 +87,10 @@ _SIGNATURES = {
         _I,
         [_P, _L, _L, _L, _P, _L, _L, _L, _I, _L, _L, _L, _L, _L, _F, _I, _P, _P, _P],
     ),
+    "uc_h2o_scores_lse": (
+        _I,
+        [_P, _L, _L, _L, _P, _L, _L, _L, _I, _L, _L, _L, _L, _L, _F, _P, _I, _P, _P, _P],
+    ),
     "uc_h2o_colsum": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _L, _I, _P, _P]),
     "uc_h2o_select": (_I, [_P, _L, _L, _L, _L, _L, _L, _P, _P]),
     "uc_mask_scan": (_I, [_P, _L, _P, _P, _P]),

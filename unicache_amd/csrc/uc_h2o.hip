@@ -9,10 +9,19 @@ bool h2o_mfma_supported(int dtype, int64_t head_dim, const void *q, int64_t q_si
                         int64_t tokens, int64_t heads_kv);
 int64_t h2o_mfma_workspace_bytes(int64_t heads_q, int64_t query_len, int64_t tokens);
 int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const void *k, int64_t k_st, int64_t k_sh,
-                    int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, float sm_scale, int accumulate, float *scores,
-                    void *workspace, hipStream_t stream);
+                    int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, float sm_scale, const float *lse, int accumulate,
+                    float *scores, void *workspace, hipStream_t stream);
 
 namespace {
+
+// stats[row] = (lse, 1): the generic score pass then yields exp(x - lse).
+__global__ void lse_stats_kernel(const float *lse, int64_t n, float *stats) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) {
+    stats[2 * i] = lse[i];
+    stats[2 * i + 1] = 1.0f;
+  }
+}
 
 // Zero fill (used instead of a memset node so the call can be graph-captured).
 __global__ void zero_kernel(float *p, int64_t n) {
@@ -315,11 +324,13 @@ __global__ __launch_bounds__(256) void gqa_gather_kernel(GatherArgs a) {
 
 using namespace uc;
 
-extern "C" int uc_h2o_scores(const void *query, int64_t q_si, int64_t q_sh, int64_t q_sd,
-                             const void *key, int64_t k_st, int64_t k_sh, int64_t k_sd, int dtype,
-                             int64_t query_len, int64_t heads_q, int64_t tokens, int64_t heads_kv,
-                             int64_t head_dim, float sm_scale, int accumulate,
-                             float *scores, void *workspace, uc_stream_t stream) {
+namespace uc {
+namespace {
+
+int h2o_scores_impl(const void *query, int64_t q_si, int64_t q_sh, int64_t q_sd, const void *key, int64_t k_st,
+                    int64_t k_sh, int64_t k_sd, int dtype, int64_t query_len, int64_t heads_q, int64_t tokens,
+                    int64_t heads_kv, int64_t head_dim, float sm_scale, const float *lse, int accumulate,
+                    float *scores, void *workspace, uc_stream_t stream) {
   UC_REQUIRE(valid_dtype(dtype), "uc_h2o_scores: unknown dtype code");
   UC_REQUIRE(heads_q > 0 && heads_kv > 0 && heads_q % heads_kv == 0,
              "BAGEL query heads must be divisible by KV heads");
@@ -339,18 +350,44 @@ extern "C" int uc_h2o_scores(const void *query, int64_t q_si, int64_t q_sh, int6
   if (h2o_mfma_supported(dtype, head_dim, query, q_si, q_sh, q_sd, key, k_st, k_sh, k_sd, query_len, heads_q, tokens,
                          heads_kv))
     return launch_h2o_mfma(dtype, query, q_si, q_sh, key, k_st, k_sh, query_len, heads_q, tokens, heads_kv, sm_scale,
-                           accumulate, scores, workspace, s);
+                           lse, accumulate, scores, workspace, s);
   ScoreArgs a{};
   a.q = query; a.q_si = q_si; a.q_sh = q_sh; a.q_sd = q_sd;
   a.k = key; a.k_st = k_st; a.k_sh = k_sh; a.k_sd = k_sd;
   a.Lq = query_len; a.Hq = heads_q; a.T = tokens; a.Hkv = heads_kv; a.D = head_dim;
   a.group = heads_q / heads_kv; a.rows = a.group * query_len; a.scale = sm_scale;
   a.stats = static_cast<float *>(workspace); a.scores = scores; a.accumulate = accumulate;
+  if (lse != nullptr)
+    hipLaunchKernelGGL(lse_stats_kernel, dim3(static_cast<unsigned>(ceil_div(heads_q * query_len, int64_t(256)))),
+                       dim3(256), 0, s, lse, heads_q * query_len, a.stats);
   UC_DISPATCH_DTYPE(dtype, DT, [&] {
-    hipLaunchKernelGGL((score_stats_kernel<DT>), dim3(ceil_div(a.rows, kRows), heads_kv), dim3(kThreads), 0, s, a);
+    if (lse == nullptr)
+      hipLaunchKernelGGL((score_stats_kernel<DT>), dim3(ceil_div(a.rows, kRows), heads_kv), dim3(kThreads), 0, s, a);
     hipLaunchKernelGGL((score_colsum_kernel<DT>), dim3(ceil_div(tokens, kTile), heads_kv), dim3(kThreads), 0, s, a);
   });
   return check_launch("uc_h2o_scores");
+}
+
+}  // namespace
+}  // namespace uc
+
+extern "C" int uc_h2o_scores(const void *query, int64_t q_si, int64_t q_sh, int64_t q_sd,
+                             const void *key, int64_t k_st, int64_t k_sh, int64_t k_sd, int dtype,
+                             int64_t query_len, int64_t heads_q, int64_t tokens, int64_t heads_kv,
+                             int64_t head_dim, float sm_scale, int accumulate,
+                             float *scores, void *workspace, uc_stream_t stream) {
+  return uc::h2o_scores_impl(query, q_si, q_sh, q_sd, key, k_st, k_sh, k_sd, dtype, query_len, heads_q, tokens,
+                             heads_kv, head_dim, sm_scale, nullptr, accumulate, scores, workspace, stream);
+}
+
+extern "C" int uc_h2o_scores_lse(const void *query, int64_t q_si, int64_t q_sh, int64_t q_sd,
+                                 const void *key, int64_t k_st, int64_t k_sh, int64_t k_sd, int dtype,
+                                 int64_t query_len, int64_t heads_q, int64_t tokens, int64_t heads_kv,
+                                 int64_t head_dim, float sm_scale, const float *lse, int accumulate,
+                                 float *scores, void *workspace, uc_stream_t stream) {
+  UC_REQUIRE(lse != nullptr || query_len == 0, "uc_h2o_scores_lse: lse is NULL");
+  return uc::h2o_scores_impl(query, q_si, q_sh, q_sd, key, k_st, k_sh, k_sd, dtype, query_len, heads_q, tokens,
+                             heads_kv, head_dim, sm_scale, lse, accumulate, scores, workspace, stream);
 }
 
 extern "C" int uc_h2o_colsum(const void *probs, int p_dtype, int64_t p_sh, int64_t p_si, int64_t p_st,

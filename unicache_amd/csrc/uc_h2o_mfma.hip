@@ -63,6 +63,7 @@ struct HsParams {
   float scale_log2;
   float2 *ml;          // [Hkv][row_blocks][chunks][kHsRows]: (max * log2 e units, sum)
   float *partial;      // [row_blocks][Hkv][T]
+  const float *lse;    // optional [Hq][Lq] natural-log normaliser given by the caller
 };
 
 // Workgroups are dealt to the 8 XCDs round-robin by launch index.  Work item
@@ -269,7 +270,12 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
   // lane j merges the chunks of row row0 + j: p = 2^(s*scale - bias),
   // bias = max + log2(sum); rows past the end get +inf (p = 0)
   float bias;
-  {
+  if (p.lse != nullptr) {  // probabilities against the caller's normaliser
+    const int64_t row = row0 + lane;
+    const int64_t rc = row < p.rows ? row : 0;
+    const int64_t g = rc / p.Lq, i = rc % p.Lq;
+    bias = row < p.rows ? p.lse[(h * p.group + g) * p.Lq + i] * kLog2e : __builtin_inff();
+  } else {
     const float2 *src = p.ml + (h * p.row_blocks + rb) * p.chunks * kHsRows + wave * kHsRowsPerWave + lane;
     float mt = kNegInf, lt = 0.0f;
     for (int64_t s0 = 0; s0 < p.chunks; s0 += 8) {  // eight loads in flight, merged in chunk order
@@ -400,8 +406,8 @@ int64_t h2o_mfma_workspace_bytes(int64_t heads_q, int64_t query_len, int64_t tok
 }
 
 int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const void *k, int64_t k_st, int64_t k_sh,
-                    int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, float sm_scale, int accumulate, float *scores,
-                    void *workspace, hipStream_t stream) {
+                    int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, float sm_scale, const float *lse, int accumulate,
+                    float *scores, void *workspace, hipStream_t stream) {
   const HsShape shape = h2o_shape(Hq, Hkv, Lq, T);
   const int64_t rbb = row_block_bound(Hq, Lq);
   UC_REQUIRE(shape.row_blocks * Hkv <= rbb && shape.row_blocks * Hkv * shape.chunks <= rbb + kHsTargetBlocks,
@@ -415,18 +421,22 @@ int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const 
   p.Lq = Lq; p.Hq = Hq; p.Hkv = Hkv; p.group = Hq / Hkv; p.rows = p.group * Lq; p.T = T;
   p.row_blocks = shape.row_blocks; p.chunks = shape.chunks; p.chunk = shape.chunk;
   p.scale_log2 = sm_scale * kLog2e;
+  p.lse = lse;
   p.ml = static_cast<float2 *>(workspace);
   p.partial = reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                         (rbb + kHsTargetBlocks) * kHsRows * int64_t(sizeof(float2)));
   p.items = p.row_blocks * p.chunks * Hkv;
   p.per_xcd = ceil_div(p.items, int64_t(kXcds));
   const dim3 grid(static_cast<unsigned>(p.per_xcd * kXcds));
-  if (dtype == UC_FP16)
-    hipLaunchKernelGGL((h2o_stats_kernel<UC_FP16>), grid, dim3(kHsThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL((h2o_stats_kernel<UC_BF16>), grid, dim3(kHsThreads), 0, stream, p);
-  int rc = check_launch("uc_h2o_scores (MFMA stats)");
-  if (rc != UC_OK) return rc;
+  int rc;
+  if (lse == nullptr) {
+    if (dtype == UC_FP16)
+      hipLaunchKernelGGL((h2o_stats_kernel<UC_FP16>), grid, dim3(kHsThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((h2o_stats_kernel<UC_BF16>), grid, dim3(kHsThreads), 0, stream, p);
+    rc = check_launch("uc_h2o_scores (MFMA stats)");
+    if (rc != UC_OK) return rc;
+  }
   if (dtype == UC_FP16)
     hipLaunchKernelGGL((h2o_scores_kernel<UC_FP16>), grid, dim3(kHsThreads), 0, stream, p);
   else

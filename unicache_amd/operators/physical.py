@@ -32,11 +32,14 @@ def per_kv_head_scores_from_probs(attention_probs: torch.Tensor, kv_heads: int) 
 
 
 def per_kv_head_scores_from_qk(query: torch.Tensor, key: torch.Tensor, *, sm_scale: float | None = None,
-                               out: torch.Tensor | None = None) -> torch.Tensor:
+                               out: torch.Tensor | None = None, lse: torch.Tensor | None = None) -> torch.Tensor:
     """The same scores computed from Q [Lq, Hq, D] and K [T, Hkv, D] without
     materialising P: softmax over all T keys, each probability rounded to
     bf16 as the adapter's cast does (adapters/bagel.py:1213-1243), then the
-    per-KV-head column sums.  With ``out`` given, accumulates into it."""
+    per-KV-head column sums.  With ``out`` given, accumulates into it.  With
+    ``lse`` ([Hq, Lq] fp32, natural log) the probabilities are
+    exp(logit - lse) instead, as for H2O segments of a mixed-segment call
+    (adapters/bagel.py:1845-1856)."""
 
     device = nat.require_device(query, key, what="Physical H2O scores")
     lq, hq, d = map(int, query.shape)
@@ -50,10 +53,20 @@ def per_kv_head_scores_from_qk(query: torch.Tensor, key: torch.Tensor, *, sm_sca
         out = torch.empty((hkv, tokens), dtype=torch.float32, device=device)
     ws = nat.workspace(device, nat.workspace_bytes(nat.UC_OP_H2O_SCORES, 1, hq, lq, d, tokens))
     scale = 1.0 / math.sqrt(d) if sm_scale is None else float(sm_scale)
+    if lse is None:
+        nat.call(
+            "uc_h2o_scores", query.data_ptr(), *map(int, query.stride()), key.data_ptr(), *map(int, key.stride()),
+            nat.dtype_code(query.dtype), lq, hq, tokens, hkv, d, scale, int(accumulate), out.data_ptr(),
+            ws.data_ptr(), nat.stream(device),
+        )
+        return out
+    if tuple(lse.shape) != (hq, lq):
+        raise ValueError("H2O scores expect lse [query_heads, query_len]")
+    lse32 = lse.to(device=device, dtype=torch.float32).contiguous()
     nat.call(
-        "uc_h2o_scores", query.data_ptr(), *map(int, query.stride()), key.data_ptr(), *map(int, key.stride()),
-        nat.dtype_code(query.dtype), lq, hq, tokens, hkv, d, scale, int(accumulate), out.data_ptr(),
-        ws.data_ptr(), nat.stream(device),
+        "uc_h2o_scores_lse", query.data_ptr(), *map(int, query.stride()), key.data_ptr(), *map(int, key.stride()),
+        nat.dtype_code(query.dtype), lq, hq, tokens, hkv, d, scale, lse32.data_ptr(), int(accumulate),
+        out.data_ptr(), ws.data_ptr(), nat.stream(device),
     )
     return out
 

@@ -183,6 +183,55 @@ def packed_kivi_attention_summary(
     return packed_attention_mq(cache, query, include_residual=include_residual)
 
 
+def packed_summary_with_dense(
+    cache: "PackedKIVICache", query: torch.Tensor, dense_key: torch.Tensor, dense_value: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """One fused attention pass over [packed prefix of `cache` | dense keys]:
+    the dense [T, Hkv, D] tokens take the place of the cache's residual.  This
+    is the first chunk of _run_fused_mixed_attention with the bf16 segments
+    folded in (adapters/bagel.py:1812-1826).  (out [Lq, Hq, D], lse [Hq, Lq])."""
+
+    if not cache.quantized_tokens:
+        raise ValueError("Packed KIVI summary requires a non-empty quantized prefix")
+    if cache.k_bits != cache.v_bits or cache.k_bits not in {2, 4}:
+        raise ValueError("Packed KIVI fused summary supports equal 2-bit or 4-bit KV")
+    _check_native(cache, "Packed KIVI fused summary")
+    if dense_key.shape != dense_value.shape or dense_key.dim() != 3 or int(dense_key.shape[1]) != cache.num_kv_heads:
+        raise ValueError("Dense segments must be matching [tokens, kv_heads, head_dim] tensors")
+    if query.dtype not in (torch.bfloat16, torch.float16):
+        query = query.to(torch.bfloat16)
+    device = nat.require_device(query, cache.key_code, dense_key, dense_value, what="Mixed-segment attention")
+    q = query.contiguous()
+    lq, hq, d = map(int, q.shape)
+    dk, dv = dense_key.contiguous(), dense_value.contiguous()
+    tr = int(dk.shape[0])
+    out = torch.empty((lq, hq, d), dtype=q.dtype, device=device)
+    lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
+    item = nat.KiviItem(
+        cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
+        cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
+        dk.data_ptr() if tr else None, dv.data_ptr() if tr else None,
+        q.data_ptr(), out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr,
+    )
+    res_code = nat.dtype_code(dk.dtype if tr else q.dtype)
+    if lq <= _max_decode_query_len(cache, hq):
+        ws_bytes = nat.decode_workspace_bytes(1, cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq,
+                                              cache.quantized_tokens, tr)
+        entry = "uc_kivi_attn_decode"
+    else:
+        if d != 128 or cache.group_size not in (32, 64, 128) or (tr and dk.dtype not in (torch.bfloat16,
+                                                                                        torch.float16)):
+            raise ValueError("Mixed-segment attention needs head_dim 128, group 32/64/128 and 16-bit dense KV")
+        ws_bytes = nat.mq_workspace_bytes(cache.num_kv_heads, d, cache.quantized_tokens, tr)
+        entry = "uc_kivi_attn_mq"
+    ws = nat.workspace(device, ws_bytes)
+    nat.call(
+        entry, item, cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq, nat.dtype_code(q.dtype),
+        res_code, nat.dtype_code(q.dtype), 1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device),
+    )
+    return out, lse
+
+
 def packed_kivi_quantized_attention_summary(
     cache: "PackedKIVICache", query: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor]:

@@ -661,6 +661,20 @@ class GQAH2OCache:
         )
         self.cumulative_scores = updated
 
+    def update_scores_from_query(self, query: torch.Tensor, lse: torch.Tensor) -> None:
+        """update_scores(exp(logits - lse).to(bf16)) for the retained keys without
+        materialising the probabilities: the H2O update of a mixed-segment
+        call, whose normaliser is the global LSE (adapters/bagel.py:1845-1856)."""
+
+        from ..operators.physical import per_kv_head_scores_from_qk
+
+        if query.dim() != 3 or int(query.shape[1]) % self.num_kv_heads:
+            raise ValueError("Query heads must be divisible by KV heads for GQA H2O")
+        q = query if query.dtype == self.key.dtype else query.to(self.key.dtype)
+        updated = self.cumulative_scores.float().clone()
+        per_kv_head_scores_from_qk(q, self.key.transpose(0, 1), out=updated, lse=lse)
+        self.cumulative_scores = updated
+
     def enforce_budget(self) -> None:
         self.trim(self.heavy_tokens + self.recent_tokens, self.recent_tokens)
 
