@@ -217,6 +217,25 @@ int uc_kivi_attn_decode_batch(const uc_kivi_item *items_device, int64_t n_items,
                               void *workspace, int64_t workspace_bytes, uc_stream_t stream);
 
 /*
+ * Segment table: the n_items items form n_items / segments_per_query groups
+ * of consecutive items that share one query (a KV cache split into segments,
+ * e.g. a packed prefix and a dense bf16 segment given as an item with
+ * quantized_tokens == 0).  Every group is attended as one softmax over all
+ * its segments and written to its first item's out / lse; the other items'
+ * out / lse are not used.  MFMA decode shapes only (head_dim 128, bits 2/4,
+ * group 32/64/128, query heads per KV head * query_len <= 16).  Workspace as
+ * for uc_kivi_attn_decode_batch over n_items.
+ * Replaces: the per-segment summaries plus merge_attention_summaries of
+ * _run_fused_mixed_attention (adapters/bagel.py:1598-1858) for decode.
+ */
+int uc_kivi_attn_decode_segments(const uc_kivi_item *items_device, int64_t n_items, int64_t segments_per_query,
+                                 int bits, int group_size,
+                                 int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t query_len,
+                                 int q_dtype, int res_dtype, int out_dtype, float sm_scale,
+                                 int64_t max_quantized_tokens, int64_t max_residual_tokens,
+                                 void *workspace, int64_t workspace_bytes, uc_stream_t stream);
+
+/*
  * Attention for long queries (image editing: group*query_len rows per KV head
  * in the thousands) over one packed segment plus residual: same inputs,
  * outputs and semantics as uc_kivi_attn_decode.  head_dim 128, bits 2/4,

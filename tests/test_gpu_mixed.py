@@ -91,3 +91,48 @@ def test_mixed_attention_requires_packed(device):
     dk, dv = kv_pair(16, seed=1)
     with pytest.raises(RuntimeError):
         run_fused_mixed_attention(queries(1).to(device), dk.to(device), dv.to(device), [])
+
+
+def test_segment_table_decode_matches_global_softmax(device):
+    # group 0: packed + dense; group 1: packed only (padded to two segments);
+    # group 2: two packed segments and no dense one
+    from unicache_amd.storage.decode import MixedDecodeBatch
+
+    def packed(tokens, seed):
+        k, v = kv_pair(tokens, seed=seed)
+        c = PackedKIVICache.from_dense(k.to(device), v.to(device), logical_token_ids=torch.arange(tokens),
+                                       token_type_id=3, k_bits=2, v_bits=2, group_size=32, residual_length=128,
+                                       backend="cuda")
+        return c, K.from_dense(f32(k), f32(v), k_bits=2, v_bits=2, group_size=32, residual_length=128)
+
+    (c0, s0), (c1, s1), (c2, s2), (c3, s3) = packed(2200, 41), packed(700, 42), packed(1500, 43), packed(300, 44)
+    dk, dv = kv_pair(333, seed=45)
+    groups = [[c0, (dk.to(device), dv.to(device))], [c1], [c2, c3]]
+    qs = [queries(1, seed=50 + i).to(device) for i in range(3)]
+    batch = MixedDecodeBatch(groups, qs)
+
+    def check(expect_segs, dense, i):
+        ks, vs = [], []
+        for seg in expect_segs:
+            k, v = K.dequantize(seg, "fp32")
+            ks.append(k)
+            vs.append(v)
+        if dense is not None:
+            ks.append(f32(dense[0]))
+            vs.append(f32(dense[1]))
+        eo, el = A.attention_summary(f32(qs[i]), np.concatenate(ks), np.concatenate(vs))
+        assert_close(f32(batch.outputs[i]), eo, what=f"group {i} out")
+        assert_close(f32(batch.lses[i]), el, max_abs=1e-2, mean_abs=1e-3, what=f"group {i} lse")
+
+    batch.run()
+    check([s0], (dk, dv), 0)
+    check([s1], None, 1)
+    check([s2, s3], None, 2)
+    # a streaming append to group 1's residual, then refresh
+    nk, nv = kv_pair(5, seed=46)
+    c1.append(nk.to(device), nv.to(device), logical_token_ids=torch.arange(700, 705))
+    batch.refresh()
+    batch.run()
+    s1.residual_key = np.concatenate([s1.residual_key, f32(nk)])
+    s1.residual_value = np.concatenate([s1.residual_value, f32(nv)])
+    check([s1], None, 1)

@@ -80,6 +80,10 @@ _SIGNATURES = {
         _I,
         [_P, _L, _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _L, _L, _P, _L, _P],
     ),
+    "uc_kivi_attn_decode_segments": (
+        _I,
+        [_P, _L, _L, _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _L, _L, _P, _L, _P],
+    ),
     "uc_kivi_attn_mq": (_I, [ctypes.POINTER(KiviItem), _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _P, _L, _P]),
     "uc_kivi_mq_workspace_bytes": (_L, [_L, _L, _L, _L]),
     "uc_lse_merge": (_I, [_P, _P, _I, _I, _L, _L, _L, _P, _P, _P]),

@@ -27,7 +27,7 @@ int64_t decode_mfma_res_split_tokens();
 int64_t decode_mfma_workspace_bytes(int64_t n_items, int64_t heads_kv, int64_t splits);
 int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single, int64_t n_items, int bits,
                        int group_size, int64_t Hq, int64_t Hkv, int64_t Lq, int q_dtype, int res_dtype,
-                       int out_dtype, float sm_scale, int64_t max_tq, int64_t max_tr, int64_t nst, void *workspace,
-                       int64_t workspace_bytes, hipStream_t stream);
+                       int out_dtype, float sm_scale, int64_t max_tq, int64_t max_tr, int64_t nst, int64_t segs,
+                       void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 }  // namespace uc

@@ -377,7 +377,8 @@ bool ok_bits_group(int bits, int group) {
 int decode_common(const uc_kivi_item *items_dev, const uc_kivi_item *single, int64_t n_items, int bits,
                   int group_size, int64_t Hq, int64_t Hkv, int64_t D, int64_t Lq, int q_dtype,
                   int res_dtype, int out_dtype, float sm_scale, int64_t max_tq, int64_t max_tr,
-                  void *workspace, int64_t workspace_bytes, hipStream_t stream, const char *name) {
+                  void *workspace, int64_t workspace_bytes, hipStream_t stream, const char *name,
+                  int64_t segs = 1) {
   UC_REQUIRE(bits == 2 || bits == 4, "%s: packed decode supports 2 or 4 bit codes", name);
   UC_REQUIRE(group_size == 16 || group_size == 32 || group_size == 64 || group_size == 128,
              "%s: group_size must be 16, 32, 64 or 128", name);
@@ -390,14 +391,16 @@ int decode_common(const uc_kivi_item *items_dev, const uc_kivi_item *single, int
              "%s: query/residual must be bf16 or fp16", name);
   UC_REQUIRE(max_tq % group_size == 0, "%s: quantized tokens must be a multiple of group_size", name);
   if (n_items == 0) return UC_OK;
+  UC_REQUIRE(segs == 1 || decode_mfma_supported(bits, group_size, D, (Hq / Hkv) * Lq),
+             "%s: segment groups need head_dim 128, group 32/64/128 and at most 16 query rows per KV head", name);
   if (decode_mfma_supported(bits, group_size, D, (Hq / Hkv) * Lq)) {
     // the MFMA kernel reads query rows 16 bytes at a time (batched items: the
     // caller's contract in the header)
     UC_REQUIRE(single == nullptr || (reinterpret_cast<uintptr_t>(single->query) & 15) == 0,
                "%s: query must be 16-byte aligned", name);
     return launch_decode_mfma(items_dev, single, n_items, bits, group_size, Hq, Hkv, Lq, q_dtype, res_dtype,
-                              out_dtype, sm_scale, max_tq, max_tr, kDecodeMfmaNst, workspace, workspace_bytes,
-                              stream);
+                              out_dtype, sm_scale, max_tq, max_tr, kDecodeMfmaNst, segs, workspace,
+                              workspace_bytes, stream);
   }
   const int64_t sp_packed = ceil_div(max_tq, kDecodeSplitTokens);
   const int64_t sp_res = ceil_div(max_tr, kDecodeSplitTokens);
@@ -471,6 +474,25 @@ extern "C" int uc_kivi_attn_decode_batch(const uc_kivi_item *items_device, int64
   return decode_common(items_device, nullptr, n_items, bits, group_size, heads_q, heads_kv, head_dim, query_len,
                        q_dtype, res_dtype, out_dtype, sm_scale, max_quantized_tokens, max_residual_tokens,
                        workspace, workspace_bytes, as_stream(stream), "uc_kivi_attn_decode_batch");
+}
+
+extern "C" int uc_kivi_attn_decode_segments(const uc_kivi_item *items_device, int64_t n_items,
+                                            int64_t segments_per_query, int bits, int group_size, int64_t heads_q,
+                                            int64_t heads_kv, int64_t head_dim, int64_t query_len, int q_dtype,
+                                            int res_dtype, int out_dtype, float sm_scale,
+                                            int64_t max_quantized_tokens, int64_t max_residual_tokens,
+                                            void *workspace, int64_t workspace_bytes, uc_stream_t stream) {
+  UC_REQUIRE(n_items >= 0 && (n_items == 0 || items_device != nullptr),
+             "uc_kivi_attn_decode_segments: bad item table");
+  UC_REQUIRE(segments_per_query >= 1 && n_items % segments_per_query == 0,
+             "uc_kivi_attn_decode_segments: %lld items do not form groups of %lld", (long long)n_items,
+             (long long)segments_per_query);
+  UC_REQUIRE(max_quantized_tokens >= 0 && max_residual_tokens >= 0,
+             "uc_kivi_attn_decode_segments: negative tokens");
+  return decode_common(items_device, nullptr, n_items, bits, group_size, heads_q, heads_kv, head_dim, query_len,
+                       q_dtype, res_dtype, out_dtype, sm_scale, max_quantized_tokens, max_residual_tokens,
+                       workspace, workspace_bytes, as_stream(stream), "uc_kivi_attn_decode_segments",
+                       segments_per_query);
 }
 
 extern "C" int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int64_t heads_q,

@@ -60,6 +60,7 @@ struct DecShared {
 struct MfmaParams {
   int64_t Hq, Hkv, Lq, group, rows;
   int64_t splits_packed, splits_total, nst;  // nst: super-tiles per packed split
+  int64_t segs;                              // consecutive items that share one query and output
   float scale_log2;
   _Float16 *ws_o;  // [items * Hkv * splits][16][128] normalised partial outputs
   float *ws_ml;    // [items * Hkv * splits][16][2] (max in log2 units, sum)
@@ -654,33 +655,39 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   }
 }
 
-// Merge the split partials of one (item, KV head): per query row the split
-// weights l_s 2^(m_s - M) / L, then the weighted sum of the fp16 partials.
+// Merge the split partials of one (query, KV head) -- every split of the
+// p.segs items that share the query: per query row the weights
+// l_s 2^(m_s - M) / L, then the weighted sum of the fp16 partials.  The output
+// goes to the first item of the group.
 template <bool TABLE>
 __global__ __launch_bounds__(256) void decode_mfma_combine(const uc_kivi_item *items, uc_kivi_item single,
                                                             MfmaParams p) {
   constexpr int kMaxSplits = 64;
   __shared__ float wts[16][kMaxSplits];
-  const int64_t item = TABLE ? blockIdx.y : 0;
-  const uc_kivi_item it = TABLE ? items[item] : single;
+  const int64_t first = TABLE ? blockIdx.y * p.segs : 0;
+  const uc_kivi_item it = TABLE ? items[first] : single;
   const int64_t h = blockIdx.x;
-  const int64_t slot0 = (item * p.Hkv + h) * p.splits_total;
   const int tid = threadIdx.x;
-  const int nsplit = int(p.splits_total);
-  for (int s0 = 0; s0 < nsplit; s0 += kMaxSplits) {
-    const int ns = min(kMaxSplits, nsplit - s0);
+  const int nflat = int(p.segs * p.splits_total);
+  // flattened (segment, split) index -> workspace slot
+  auto slot = [&](int f) {
+    return ((first + f / p.splits_total) * p.Hkv + h) * p.splits_total + f % p.splits_total;
+  };
+  for (int s0 = 0; s0 < nflat; s0 += kMaxSplits) {
+    const int ns = min(kMaxSplits, nflat - s0);
     __syncthreads();
     if (tid < p.rows) {
       float M = kNegInf;
-      for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.ws_ml[((slot0 + s) * 16 + tid) * 2]);
+      for (int f = 0; f < nflat; ++f) M = fmaxf(M, p.ws_ml[(slot(f) * 16 + tid) * 2]);
       float L = 0.0f;
-      for (int s = 0; s < nsplit; ++s) {
-        const float m = p.ws_ml[((slot0 + s) * 16 + tid) * 2], l = p.ws_ml[((slot0 + s) * 16 + tid) * 2 + 1];
+      for (int f = 0; f < nflat; ++f) {
+        const float m = p.ws_ml[(slot(f) * 16 + tid) * 2], l = p.ws_ml[(slot(f) * 16 + tid) * 2 + 1];
         if (l > 0.0f && m != kNegInf) L += l * exp2f(m - M);
       }
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
       for (int s = 0; s < ns; ++s) {
-        const float m = p.ws_ml[((slot0 + s0 + s) * 16 + tid) * 2], l = p.ws_ml[((slot0 + s0 + s) * 16 + tid) * 2 + 1];
+        const int64_t sl = slot(s0 + s);
+        const float m = p.ws_ml[(sl * 16 + tid) * 2], l = p.ws_ml[(sl * 16 + tid) * 2 + 1];
         wts[tid][s] = (l > 0.0f && m != kNegInf) ? l * exp2f(m - M) * inv : 0.0f;
       }
       if (s0 == 0 && it.lse != nullptr) {
@@ -702,7 +709,7 @@ __global__ __launch_bounds__(256) void decode_mfma_combine(const uc_kivi_item *i
       for (int s = 0; s < ns; ++s) {
         const float w = wts[row][s];
         if (w == 0.0f) continue;
-        const h8 v = *reinterpret_cast<const h8 *>(p.ws_o + ((slot0 + s0 + s) * 16 + row) * kD + c8);
+        const h8 v = *reinterpret_cast<const h8 *>(p.ws_o + (slot(s0 + s) * 16 + row) * kD + c8);
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = fmaf(float(v[j]), w, o[j]);
       }
@@ -750,8 +757,8 @@ static void launch_group(bool table, int rd, dim3 grid, hipStream_t stream, cons
 
 int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single, int64_t n_items, int bits,
                        int group_size, int64_t Hq, int64_t Hkv, int64_t Lq, int q_dtype, int res_dtype,
-                       int out_dtype, float sm_scale, int64_t max_tq, int64_t max_tr, int64_t nst, void *workspace,
-                       int64_t workspace_bytes, hipStream_t stream) {
+                       int out_dtype, float sm_scale, int64_t max_tq, int64_t max_tr, int64_t nst, int64_t segs,
+                       void *workspace, int64_t workspace_bytes, hipStream_t stream) {
   const int64_t s_tok = decode_mfma_split_tokens(bits, nst);
   const int64_t r_tok = decode_mfma_res_split_tokens();
   MfmaParams p{};
@@ -759,6 +766,7 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   p.splits_packed = ceil_div(max_tq, s_tok);
   p.splits_total = p.splits_packed + ceil_div(max_tr, r_tok);
   p.nst = nst;
+  p.segs = segs;
   p.scale_log2 = sm_scale * kLog2e;
   p.qd = q_dtype; p.rd = res_dtype; p.od = out_dtype;
   if (p.splits_total == 0) return UC_OK;
@@ -786,8 +794,11 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   }
   int rc = check_launch("decode (MFMA)");
   if (rc != UC_OK) return rc;
+  UC_REQUIRE(segs >= 1 && n_items % segs == 0, "decode: %lld items do not form groups of %lld segments",
+             (long long)n_items, (long long)segs);
   if (table)
-    hipLaunchKernelGGL((decode_mfma_combine<true>), dim3(Hkv, n_items), dim3(256), 0, stream, items_dev, one, p);
+    hipLaunchKernelGGL((decode_mfma_combine<true>), dim3(Hkv, n_items / segs), dim3(256), 0, stream, items_dev, one,
+                       p);
   else
     hipLaunchKernelGGL((decode_mfma_combine<false>), dim3(Hkv, n_items), dim3(256), 0, stream, items_dev, one, p);
   return check_launch("decode (MFMA combine)");

@@ -89,3 +89,125 @@ class KiviDecodeBatch:
             self.max_tr, self.workspace.data_ptr(), self.ws_bytes,
             nat.stream(self.device) if stream is None else stream,
         )
+
+
+class MixedDecodeBatch:
+    """Decode over groups of KV segments that share one query: each group is a
+    list of PackedKIVICache segments and dense (key, value) [T, Hkv, D]
+    segments (bf16 H2O / protected tokens) and is attended as one softmax over
+    all of them by a single uc_kivi_attn_decode_segments launch for every
+    group -- the decode form of _run_fused_mixed_attention
+    (adapters/bagel.py:1598-1858) without concatenating the segments.
+
+    Dense segments and residual windows must share one dtype (the kernel reads
+    them as fp16 either way).  refresh() rebuilds the item table after
+    segments change (a residual append or flush); run() allocates nothing."""
+
+    def __init__(self, groups, queries, *, out_dtype: torch.dtype | None = None):
+        if not groups or len(groups) != len(queries):
+            raise ValueError("MixedDecodeBatch needs one query per segment group")
+        packed = [s for g in groups for s in g if not isinstance(s, tuple)]
+        if not packed:
+            raise ValueError("MixedDecodeBatch needs at least one packed segment")
+        first = packed[0]
+        for c in packed:
+            if not c.kernel_native_layout or c.k_bits != c.v_bits or c.k_bits not in (2, 4):
+                raise ValueError("Mixed decode needs native equal 2/4-bit packed segments")
+            if (c.k_bits, c.group_size, c.num_kv_heads, c.head_dim) != (
+                first.k_bits, first.group_size, first.num_kv_heads, first.head_dim
+            ):
+                raise ValueError("Mixed decode packed segments must share bits, group size and head shapes")
+        q0 = queries[0]
+        for q in queries:
+            if q.shape != q0.shape or q.dtype != q0.dtype or not q.is_contiguous():
+                raise ValueError("Mixed decode queries must be contiguous and of one shape/dtype")
+        self.device = nat.require_device(*queries, first.key_code, what="Mixed KIVI decode")
+        lq, hq, d = map(int, q0.shape)
+        dtypes = set()
+        for g in groups:
+            for s in g:
+                if isinstance(s, tuple):
+                    k, v = s
+                    if k.shape != v.shape or k.dim() != 3 or tuple(k.shape[1:]) != (first.num_kv_heads, d):
+                        raise ValueError("Dense segments must be matching [tokens, kv_heads, head_dim] tensors")
+                    if not (k.is_contiguous() and v.is_contiguous()):
+                        raise ValueError("Dense segments must be contiguous")
+                    dtypes.add(k.dtype)
+                elif s.residual_tokens:
+                    dtypes.add(s.residual_key.dtype)
+        if len(dtypes) > 1:
+            raise ValueError("Dense segments and residual windows must share one dtype")
+        self.res_dtype = dtypes.pop() if dtypes else q0.dtype
+        self.out_dtype = out_dtype or q0.dtype
+        self.bits, self.group_size, self.kv_heads = first.k_bits, first.group_size, first.num_kv_heads
+        self.groups = [list(g) for g in groups]
+        self.queries = list(queries)
+        self.segs = max(len(g) for g in groups)
+        self.outputs = [torch.empty((lq, hq, d), dtype=self.out_dtype, device=self.device) for _ in groups]
+        self.lses = [torch.empty((hq, lq), dtype=torch.float32, device=self.device) for _ in groups]
+        self.shape = (lq, hq, d)
+        self.sm_scale = 1.0 / math.sqrt(d)
+        self.refresh()
+
+    def refresh(self) -> None:
+        n = len(self.groups) * self.segs
+        items = (nat.KiviItem * n)()
+        max_tq = max_tr = 0
+        for gi, (g, q) in enumerate(zip(self.groups, self.queries)):
+            out, lse = self.outputs[gi], self.lses[gi]
+            for j in range(self.segs):
+                idx = gi * self.segs + j
+                s = g[j] if j < len(g) else None
+                if s is None:  # padding: an empty segment
+                    items[idx] = nat.KiviItem(None, None, None, None, None, None, None, None, q.data_ptr(),
+                                              out.data_ptr(), lse.data_ptr(), 0, 0)
+                elif isinstance(s, tuple):
+                    k, v = s
+                    tr = int(k.shape[0])
+                    items[idx] = nat.KiviItem(None, None, None, None, None, None, k.data_ptr() if tr else None,
+                                              v.data_ptr() if tr else None, q.data_ptr(), out.data_ptr(),
+                                              lse.data_ptr(), 0, tr)
+                    max_tr = max(max_tr, tr)
+                else:
+                    tr = s.residual_tokens
+                    items[idx] = nat.KiviItem(
+                        s.key_code.data_ptr(), s.key_scale.data_ptr(), s.key_minimum.data_ptr(),
+                        s.value_code.data_ptr(), s.value_scale.data_ptr(), s.value_minimum.data_ptr(),
+                        s.residual_key.data_ptr() if tr else None, s.residual_value.data_ptr() if tr else None,
+                        q.data_ptr(), out.data_ptr(), lse.data_ptr(), s.quantized_tokens, tr)
+                    max_tq, max_tr = max(max_tq, s.quantized_tokens), max(max_tr, tr)
+        raw = bytes(ctypes.string_at(ctypes.addressof(items), ctypes.sizeof(items)))
+        self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
+        self.n_items, self.max_tq, self.max_tr = n, max_tq, max_tr
+        lq, hq, d = self.shape
+        self.ws_bytes = nat.decode_workspace_bytes(n, self.bits, self.group_size, hq, self.kv_heads, d, lq,
+                                                   max_tq, max_tr)
+        if getattr(self, "workspace", None) is None or self.workspace.numel() < self.ws_bytes:
+            self.workspace = nat.workspace(self.device, self.ws_bytes)
+
+    @property
+    def algorithmic_bytes(self) -> int:
+        """Packed codes + stats, residual and dense K/V, queries and outputs,
+        each counted once."""
+
+        total = 0
+        for g, q, o in zip(self.groups, self.queries, self.outputs):
+            for s in g:
+                if isinstance(s, tuple):
+                    total += sum(t.numel() * t.element_size() for t in s)
+                    continue
+                for t in (s.key_code, s.key_scale, s.key_minimum, s.value_code, s.value_scale, s.value_minimum):
+                    total += t.numel() * t.element_size()
+                total += 2 * s.residual_key.numel() * s.residual_key.element_size()
+            total += q.numel() * q.element_size() + o.numel() * o.element_size()
+        return total
+
+    def run(self, stream: int | None = None) -> None:
+        lq, hq, d = self.shape
+        nat.call(
+            "uc_kivi_attn_decode_segments", self.table.data_ptr(), self.n_items, self.segs, self.bits,
+            self.group_size, hq, self.kv_heads, d, lq, nat.dtype_code(self.queries[0].dtype),
+            nat.dtype_code(self.res_dtype), nat.dtype_code(self.out_dtype), self.sm_scale, self.max_tq,
+            self.max_tr, self.workspace.data_ptr(), self.ws_bytes,
+            nat.stream(self.device) if stream is None else stream,
+        )
