@@ -122,35 +122,41 @@ def long_context_decode(device, steps, layers=LAYERS, tokens=32768):
 
 
 def editing_attention(device, steps, layers=LAYERS, bits=BITS):
-    """Config 2's packed segment: 1088 queries x 28 heads against 1024 source-VAE
-    tokens (896 packed + 128 residual) per layer through uc_kivi_attn_mq (stage
-    + attention kernels), 28 layers of distinct caches; TFLOP/s = 4*Lq*Hq*T*D
-    per layer / time."""
-
-    import math
+    """Config 2, the whole editing attention of a layer: 1088 queries x 28 heads
+    against 2304 keys -- the 1024 source-VAE tokens (896 packed at `bits` + 128
+    residual) and the 256 instruction + 1024 ViT bf16 tokens -- in one fused
+    uc_kivi_attn_mq pass (stage + MFMA attention kernels), the bf16 segments
+    riding as its dense part; 28 layers of distinct caches.  TFLOP/s =
+    4*Lq*Hq*T*D per layer / time."""
 
     from unicache_amd import _native as nat
     from unicache_amd.storage import PackedKIVICache
 
-    lq, tokens = 1088, 1024
+    lq, vae, instr, vit = 1088, 1024, 256, 1024
     calls = []
     for layer in range(layers):
-        key, value = make_kv(tokens, seed=5000 + layer, device=device)
-        cache = PackedKIVICache.from_dense(key, value, logical_token_ids=torch.arange(tokens, device=device),
+        key, value = make_kv(vae, seed=5000 + layer, device=device)
+        cache = PackedKIVICache.from_dense(key, value, logical_token_ids=torch.arange(vae, device=device),
                                            token_type_id=3, k_bits=bits, v_bits=bits, group_size=GROUP,
                                            residual_length=RESIDUAL, backend="cuda")
+        ik, iv = make_kv(instr, seed=5100 + layer, device=device)
+        tk, tv = make_kv(vit, seed=5200 + layer, device=device)
+        dk = torch.cat([ik, tk, cache.residual_key]).contiguous()
+        dv = torch.cat([iv, tv, cache.residual_value]).contiguous()
         g = torch.Generator(device=device).manual_seed(9000 + layer)
         q = torch.randn(lq, HQ, D, generator=g, device=device).to(torch.bfloat16)
         out = torch.empty_like(q)
         lse = torch.empty(HQ, lq, dtype=torch.float32, device=device)
-        ws_bytes = nat.mq_workspace_bytes(HKV, D, cache.quantized_tokens, cache.residual_tokens)
+        tr = int(dk.shape[0])
+        ws_bytes = nat.mq_workspace_bytes(HKV, D, cache.quantized_tokens, tr)
         ws = nat.workspace(device, ws_bytes)
         item = nat.KiviItem(cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
                             cache.value_code.data_ptr(), cache.value_scale.data_ptr(),
-                            cache.value_minimum.data_ptr(), cache.residual_key.data_ptr(),
-                            cache.residual_value.data_ptr(), q.data_ptr(), out.data_ptr(), lse.data_ptr(),
-                            cache.quantized_tokens, cache.residual_tokens)
-        calls.append((item, ws, ws_bytes, cache, q, out, lse))
+                            cache.value_minimum.data_ptr(), dk.data_ptr(), dv.data_ptr(), q.data_ptr(),
+                            out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr)
+        calls.append((item, ws, ws_bytes, cache, dk, dv, q, out, lse))
+        del key, value, ik, iv, tk, tv
+    keys = calls[0][3].quantized_tokens + int(calls[0][4].shape[0])
     stream = torch.cuda.current_stream(device)
     sid = stream.cuda_stream
     bf16 = nat.dtype_code(torch.bfloat16)
@@ -161,15 +167,128 @@ def editing_attention(device, steps, layers=LAYERS, bits=BITS):
                      ws.data_ptr(), ws_bytes, sid)
 
     ms = time_steps(step, steps, 2, stream)
-    flop = 4 * lq * HQ * tokens * D
+    flop = 4 * lq * HQ * keys * D
     tflops = flop * layers / (ms * 1e-3) / 1e12
     return {
-        "workload": f"config 2 packed segment: Lq=1088 x 28 heads, {tokens} tokens ({bits}-bit, 896 packed + "
-                    f"128 residual), {layers} layers, uc_kivi_attn_mq",
+        "workload": f"config 2 editing attention: Lq=1088 x 28 heads over {keys} keys (VAE {vae} at {bits}-bit: "
+                    f"896 packed + 128 residual; instruction {instr} + ViT {vit} bf16), {layers} layers, "
+                    f"one uc_kivi_attn_mq pass per layer",
         "ms_per_layer": round(ms / layers, 4),
         "tflops": round(tflops, 1),
         "frac_of_bf16_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
         "flop_per_layer": flop,
+    }
+
+
+def h2o_eviction(device, steps):
+    """Config 3, one layer: bf16-probability attention mass of 512 queries over
+    4096 keys summed per KV head (uc_h2o_scores, MFMA), then per segment
+    (256 instruction, 3840 ViT tokens) the 20% budget top-k + recent window and
+    the GQA gather into [4, 819, 128] (GQAH2OCache.from_dense), then the
+    keep-mask compaction of the dense cache."""
+
+    from unicache_amd.operators.physical import per_kv_head_scores_from_qk
+    from unicache_amd.storage import GQAH2OCache
+    from unicache_amd.storage.tensor_backend import TensorCacheStorageBackend, h2o_budget
+
+    lq, tokens = 512, 4096
+    key, value = make_kv(tokens, seed=3, device=device)
+    g = torch.Generator(device=device).manual_seed(33)
+    q = torch.randn(lq, HQ, D, generator=g, device=device).to(torch.bfloat16)
+    scores = torch.empty(HKV, tokens, dtype=torch.float32, device=device)
+    stream = torch.cuda.current_stream(device)
+    ms_scores = time_steps(lambda: per_kv_head_scores_from_qk(q, key, out=scores.zero_()), steps, 2, stream)
+    spans = [(0, 256), (256, 4096)]
+
+    def select_gather():
+        segs = []
+        for lo, hi in spans:
+            target, recent = h2o_budget(hi - lo, {"target_budget_ratio": 0.2})
+            segs.append(GQAH2OCache.from_dense(key[lo:hi], value[lo:hi], logical_token_ids=torch.arange(
+                lo, hi, device=device), token_type_id=1, per_kv_head_scores=scores[:, lo:hi],
+                target_tokens=target, recent_tokens=recent, selection_frozen=True))
+        return segs
+
+    ms_sel = time_steps(select_gather, steps, 2, stream)
+    retained = sum(s.retained_tokens for s in select_gather())
+    keep = torch.ones(tokens, dtype=torch.bool, device=device)
+    keep[:256] = False
+    keep[256:4096:2] = False
+    ms_compact = time_steps(lambda: TensorCacheStorageBackend.compact(
+        key=key, value=value, key_type_ids=None, sample_lens=torch.tensor([tokens], device=device),
+        keep_masks=[keep], sample_lengths=[tokens]), steps, 2, stream)
+    kept = int(keep.sum())
+    flop = 2 * lq * HQ * tokens * D
+    gather_bytes = 2 * (2 * HKV * retained * D * 2) + 2 * HKV * retained * (8 + 4) + HKV * tokens * 4
+    compact_bytes = 2 * 2 * kept * HKV * D * 2
+    return {
+        "workload": "config 3, one layer: scores of Lq=512 x 28 heads over 4096 keys (uc_h2o_scores), "
+                    f"select + gather of 2 segments to {retained} tokens per head, keep-mask compaction "
+                    f"keeping {kept} of {tokens} dense rows",
+        "scores_ms": round(ms_scores, 4),
+        "scores_tflops": round(flop / (ms_scores * 1e-3) / 1e12, 1),
+        "scores_frac_of_bf16_mfma_peak": round(flop / (ms_scores * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
+        "select_gather_ms": round(ms_sel, 4),
+        "select_gather_gbs": round(gather_bytes / (ms_sel * 1e-3) / 1e9, 1),
+        "compact_ms": round(ms_compact, 4),
+        "compact_gbs": round(compact_bytes / (ms_compact * 1e-3) / 1e9, 1),
+    }
+
+
+def mixed_decode(device, steps, layers=LAYERS):
+    """Config 4 decode step: per layer the VAE segment (20352 tokens: 20224
+    packed 2-bit + 128 fp16 residual) and the bf16 tokens kept dense (128
+    protected + instruction 4096 -> 819 and ViT 8192 -> 1638 after H2O at a 20%
+    budget) attended as one softmax; all 28 layers in one
+    uc_kivi_attn_decode_segments launch.  Plus the residual flush: 128 tokens
+    quantized and appended to the packed prefix."""
+
+    from unicache_amd.storage import PackedKIVICache
+    from unicache_amd.storage.decode import MixedDecodeBatch
+
+    vae, dense_tokens = 20352, 128 + 819 + 1638
+    groups, queries, caches = [], [], []
+    for layer in range(layers):
+        key, value = make_kv(vae, seed=11000 + layer, device=device)
+        cache = PackedKIVICache.from_dense(key.half(), value.half(),
+                                           logical_token_ids=torch.arange(vae, device=device), token_type_id=3,
+                                           k_bits=BITS, v_bits=BITS, group_size=GROUP, residual_length=RESIDUAL,
+                                           backend="cuda")
+        dk, dv = make_kv(dense_tokens, seed=12000 + layer, device=device)
+        groups.append([cache, (dk.half().contiguous(), dv.half().contiguous())])
+        caches.append(cache)
+        gq = torch.Generator(device=device).manual_seed(13000 + layer)
+        queries.append(torch.randn(1, HQ, D, generator=gq, device=device).to(torch.bfloat16))
+        del key, value, dk, dv
+    batch = MixedDecodeBatch(groups, queries)
+    stream = torch.cuda.current_stream(device)
+    sid = stream.cuda_stream
+    ms = time_steps(lambda: batch.run(sid), steps, 3, stream)
+    gbs = batch.algorithmic_bytes / (ms * 1e-3) / 1e9
+    # one residual flush: 128 appended fp16 tokens quantized into the packed prefix
+    c = caches[0]
+    nk, nv = make_kv(128, seed=14000, device=device)
+    flush_ms = []
+    for i in range(3):
+        c.append(nk.half(), nv.half(), logical_token_ids=torch.arange(vae + 128 * i, vae + 128 * (i + 1),
+                                                                      device=device))
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        c.flush_residual(keep=RESIDUAL)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        flush_ms.append(t0.elapsed_time(t1))
+    return {
+        "workload": f"config 4 decode step: {layers} layers x (VAE {vae} tokens: {caches[1].quantized_tokens} packed "
+                    f"2-bit + {caches[1].residual_tokens} fp16 residual | {dense_tokens} dense tokens: 128 protected "
+                    "+ 819 + 1638 H2O-retained), batch 1, Lq=1, one uc_kivi_attn_decode_segments launch",
+        "ms_per_step": round(ms, 5),
+        "gbs": round(gbs, 1),
+        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "bytes_per_step": batch.algorithmic_bytes,
+        "flush_ms_per_layer": round(sorted(flush_ms)[1], 4),
     }
 
 
@@ -288,7 +407,11 @@ def main():
     torch.cuda.empty_cache()
     result["decode_32k"] = long_context_decode(device, max(5, args.steps // 2))
     torch.cuda.empty_cache()
-    result["editing_mq"] = editing_attention(device, max(3, args.steps // 5))
+    result["mixed_decode_c4"] = mixed_decode(device, max(5, args.steps // 2))
+    torch.cuda.empty_cache()
+    result["editing_c2"] = {f"{b}bit": editing_attention(device, max(3, args.steps // 5), bits=b) for b in (2, 4)}
+    torch.cuda.empty_cache()
+    result["h2o_c3"] = h2o_eviction(device, max(5, args.steps // 5))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(seq_layer_bytes)
     print(json.dumps(result))
