@@ -66,8 +66,8 @@ extern "C" int64_t uc_kivi_decode_workspace_bytes(int64_t n_items, int bits, int
     return -1;
   const int64_t rows = (heads_q / heads_kv) * query_len;
   if (uc::decode_mfma_supported(bits, group_size, head_dim, rows)) {
-    const int64_t splits = uc::ceil_div(max_quantized_tokens, uc::decode_mfma_split_tokens(bits, uc::kDecodeMfmaNst)) +
-                           uc::ceil_div(max_residual_tokens, uc::decode_mfma_res_split_tokens());
+    const int64_t splits = uc::decode_mfma_num_splits(bits, uc::kDecodeMfmaNst, max_quantized_tokens,
+                                                      max_residual_tokens);
     return uc::decode_mfma_workspace_bytes(n_items, heads_kv, splits);
   }
   const int64_t splits = uc::ceil_div(max_quantized_tokens, uc::kDecodeSplitTokens) +

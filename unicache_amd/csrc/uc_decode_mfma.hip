@@ -656,67 +656,93 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 }
 
 // Merge the split partials of one (query, KV head) -- every split of the
-// p.segs items that share the query: per query row the weights
-// l_s 2^(m_s - M) / L, then the weighted sum of the fp16 partials.  The output
-// goes to the first item of the group.
+// p.segs items that share the query -- for half of the channels (blockIdx.z):
+// the (max, sum) of up to 64 slots at a time are staged in LDS by all threads
+// and folded per query row into a running (M, L); a second sweep turns them
+// into weights l_s 2^(m_s - M) / L and accumulates the fp16 partials.  The
+// output goes to the first item of the group.
+constexpr int kCombineThreads = 128;
+constexpr int kCombineParts = 2;  // channel halves per (query, KV head)
+
 template <bool TABLE>
-__global__ __launch_bounds__(256) void decode_mfma_combine(const uc_kivi_item *items, uc_kivi_item single,
-                                                            MfmaParams p) {
-  constexpr int kMaxSplits = 64;
-  __shared__ float wts[16][kMaxSplits];
+__global__ __launch_bounds__(kCombineThreads) void decode_mfma_combine(const uc_kivi_item *items, uc_kivi_item single,
+                                                                       MfmaParams p) {
+  constexpr int kChunk = 64;
+  __shared__ float sm[16][kChunk + 1], sl[16][kChunk + 1];
+  __shared__ float row_m[16], row_inv[16];
   const int64_t first = TABLE ? blockIdx.y * p.segs : 0;
   const uc_kivi_item it = TABLE ? items[first] : single;
   const int64_t h = blockIdx.x;
+  const int part = blockIdx.z;
   const int tid = threadIdx.x;
   const int nflat = int(p.segs * p.splits_total);
   // flattened (segment, split) index -> workspace slot
   auto slot = [&](int f) {
     return ((first + f / p.splits_total) * p.Hkv + h) * p.splits_total + f % p.splits_total;
   };
-  for (int s0 = 0; s0 < nflat; s0 += kMaxSplits) {
-    const int ns = min(kMaxSplits, nflat - s0);
+  auto stage = [&](int s0, int ns) {
+    for (int idx = tid; idx < 16 * ns; idx += kCombineThreads) {
+      const int r = idx & 15, sidx = idx >> 4;
+      const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + (slot(s0 + sidx) * 16 + r) * 2);
+      sm[r][sidx] = ml.x;
+      sl[r][sidx] = ml.y;
+    }
+  };
+  // pass 1: running (M, L) per row
+  float M = kNegInf, L = 0.0f;
+  for (int s0 = 0; s0 < nflat; s0 += kChunk) {
+    const int ns = min(kChunk, nflat - s0);
+    __syncthreads();
+    stage(s0, ns);
     __syncthreads();
     if (tid < p.rows) {
-      float M = kNegInf;
-      for (int f = 0; f < nflat; ++f) M = fmaxf(M, p.ws_ml[(slot(f) * 16 + tid) * 2]);
-      float L = 0.0f;
-      for (int f = 0; f < nflat; ++f) {
-        const float m = p.ws_ml[(slot(f) * 16 + tid) * 2], l = p.ws_ml[(slot(f) * 16 + tid) * 2 + 1];
-        if (l > 0.0f && m != kNegInf) L += l * exp2f(m - M);
-      }
-      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      for (int s = 0; s < ns; ++s) {
-        const int64_t sl = slot(s0 + s);
-        const float m = p.ws_ml[(sl * 16 + tid) * 2], l = p.ws_ml[(sl * 16 + tid) * 2 + 1];
-        wts[tid][s] = (l > 0.0f && m != kNegInf) ? l * exp2f(m - M) * inv : 0.0f;
-      }
-      if (s0 == 0 && it.lse != nullptr) {
-        const int64_t g = tid / p.Lq, i = tid % p.Lq;
-        it.lse[(h * p.group + g) * p.Lq + i] = L > 0.0f ? (M + log2f(L)) * kLn2 : kNegInf;
+      float cm = kNegInf;
+      for (int s = 0; s < ns; ++s)
+        if (sl[tid][s] > 0.0f) cm = fmaxf(cm, sm[tid][s]);
+      const float m_new = fmaxf(M, cm);
+      if (m_new != kNegInf) {
+        float acc = L > 0.0f ? L * exp2f(M - m_new) : 0.0f;
+        for (int s = 0; s < ns; ++s)
+          if (sl[tid][s] > 0.0f && sm[tid][s] != kNegInf) acc += sl[tid][s] * exp2f(sm[tid][s] - m_new);
+        L = acc;
+        M = m_new;
       }
     }
+  }
+  if (tid < p.rows) {
+    row_m[tid] = M;
+    row_inv[tid] = L > 0.0f ? 1.0f / L : 0.0f;
+    if (part == 0 && it.lse != nullptr) {
+      const int64_t g = tid / p.Lq, i = tid % p.Lq;
+      it.lse[(h * p.group + g) * p.Lq + i] = L > 0.0f ? (M + log2f(L)) * kLn2 : kNegInf;
+    }
+  }
+  // pass 2: thread -> (row, 8 channels of this part)
+  constexpr int kC8 = kD / 8 / kCombineParts;
+  const int row = tid / kC8, c8 = (part * kC8 + tid % kC8) * 8;
+  const bool active = row < p.rows;
+  float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int s0 = 0; s0 < nflat; s0 += kChunk) {
+    const int ns = min(kChunk, nflat - s0);
     __syncthreads();
-    // each thread: 8 channels of one row
-    for (int idx = tid; idx < p.rows * (kD / 8); idx += blockDim.x) {
-      const int row = idx / (kD / 8), c8 = (idx % (kD / 8)) * 8;
-      float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (s0 > 0) {
-        // later chunks accumulate onto the output written by the first chunk
-        const int64_t g = row / p.Lq, i = row % p.Lq;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = load_dyn(it.out, (i * p.Hq + h * p.group + g) * kD + c8 + j, p.od);
-      }
+    stage(s0, ns);
+    __syncthreads();
+    if (active) {
+      const float rm = row_m[row], rinv = row_inv[row];
       for (int s = 0; s < ns; ++s) {
-        const float w = wts[row][s];
-        if (w == 0.0f) continue;
+        const float l = sl[row][s], m = sm[row][s];
+        if (!(l > 0.0f && m != kNegInf)) continue;
+        const float w = l * exp2f(m - rm) * rinv;
         const h8 v = *reinterpret_cast<const h8 *>(p.ws_o + (slot(s0 + s) * 16 + row) * kD + c8);
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = fmaf(float(v[j]), w, o[j]);
       }
-      const int64_t g = row / p.Lq, i = row % p.Lq;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) store_dyn(it.out, (i * p.Hq + h * p.group + g) * kD + c8 + j, o[j], p.od);
     }
+  }
+  if (active) {
+    const int64_t g = row / p.Lq, i = row % p.Lq;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) store_dyn(it.out, (i * p.Hq + h * p.group + g) * kD + c8 + j, o[j], p.od);
   }
 }
 
@@ -727,6 +753,11 @@ __global__ __launch_bounds__(256) void decode_mfma_combine(const uc_kivi_item *i
 int64_t decode_mfma_split_tokens(int bits, int64_t nst) { return nst * 16 * (32 / bits); }
 
 int64_t decode_mfma_res_split_tokens() { return kWaves * kResWaveTokens; }
+
+// Splits per (item, KV head): packed splits, then residual splits.
+int64_t decode_mfma_num_splits(int bits, int64_t nst, int64_t max_tq, int64_t max_tr) {
+  return ceil_div(max_tq, decode_mfma_split_tokens(bits, nst)) + ceil_div(max_tr, decode_mfma_res_split_tokens());
+}
 
 bool decode_mfma_supported(int bits, int group, int64_t D, int64_t rows) {
   return (bits == 2 || bits == 4) && (group == 32 || group == 64 || group == 128) && D == kD && rows <= 16;
@@ -760,11 +791,10 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
                        int out_dtype, float sm_scale, int64_t max_tq, int64_t max_tr, int64_t nst, int64_t segs,
                        void *workspace, int64_t workspace_bytes, hipStream_t stream) {
   const int64_t s_tok = decode_mfma_split_tokens(bits, nst);
-  const int64_t r_tok = decode_mfma_res_split_tokens();
   MfmaParams p{};
   p.Hq = Hq; p.Hkv = Hkv; p.Lq = Lq; p.group = Hq / Hkv; p.rows = p.group * Lq;
   p.splits_packed = ceil_div(max_tq, s_tok);
-  p.splits_total = p.splits_packed + ceil_div(max_tr, r_tok);
+  p.splits_total = decode_mfma_num_splits(bits, nst, max_tq, max_tr);
   p.nst = nst;
   p.segs = segs;
   p.scale_log2 = sm_scale * kLog2e;
@@ -797,10 +827,11 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   UC_REQUIRE(segs >= 1 && n_items % segs == 0, "decode: %lld items do not form groups of %lld segments",
              (long long)n_items, (long long)segs);
   if (table)
-    hipLaunchKernelGGL((decode_mfma_combine<true>), dim3(Hkv, n_items / segs), dim3(256), 0, stream, items_dev, one,
-                       p);
+    hipLaunchKernelGGL((decode_mfma_combine<true>), dim3(Hkv, n_items / segs, kCombineParts), dim3(kCombineThreads),
+                       0, stream, items_dev, one, p);
   else
-    hipLaunchKernelGGL((decode_mfma_combine<false>), dim3(Hkv, n_items), dim3(256), 0, stream, items_dev, one, p);
+    hipLaunchKernelGGL((decode_mfma_combine<false>), dim3(Hkv, n_items, kCombineParts), dim3(kCombineThreads), 0,
+                       stream, items_dev, one, p);
   return check_launch("decode (MFMA combine)");
 }
 
