@@ -27,6 +27,7 @@ namespace {
 
 using namespace mf;
 
+constexpr int kXcds = 8;  // XCDs of an MI355X; launch index i runs on XCD i % 8
 constexpr int kMqWaves = 4;
 constexpr int kMqThreads = kMqWaves * kWave;
 constexpr int kRowsPerWave = 32;
@@ -46,6 +47,7 @@ struct MqParams {
   float scale_log2;
   const _Float16 *wk;  // [Hkv][keys_pad][128]
   const _Float16 *wv;  // [Hkv][128][keys_pad]
+  int64_t row_blocks, per_xcd;  // row blocks per KV head; work items per XCD
 };
 
 struct StageParams {
@@ -370,8 +372,14 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = wave / 4, rw = wave % 4, tid_h = tid % kHalfThreads;
   const int r = lane & 15, kap = lane >> 4;
-  const int64_t h = blockIdx.y;
-  const int64_t row0 = int64_t(blockIdx.x) * kMqRows + rw * kRowsPerWave;
+  // Workgroups are dealt to the 8 XCDs round-robin by launch index; work item
+  // w = h * row_blocks + rb goes to index 8 * (w % per_xcd) + w / per_xcd, so
+  // each XCD serves a contiguous run of row blocks -- mostly of one KV head,
+  // whose staged keys and values its own L2 then holds.
+  const int64_t id = blockIdx.x, w = (id % kXcds) * p.per_xcd + id / kXcds;
+  if (w >= p.row_blocks * p.Hkv) return;  // uniform: the whole workgroup leaves
+  const int64_t h = w / p.row_blocks;
+  const int64_t row0 = (w % p.row_blocks) * kMqRows + rw * kRowsPerWave;
 
   // query rows of this wave as the B operand of S^T = K Q^T (bf16/fp16 -> fp16 is
   // exact for these magnitudes; the softmax scale is applied to the fp32 logits);
@@ -565,7 +573,9 @@ extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int grou
   p.scale_log2 = sm_scale * kLog2e;
   p.wk = sp.wk;
   p.wv = sp.wv;
-  const dim3 grid(static_cast<unsigned>(ceil_div(p.rows, int64_t(kMqRows))), static_cast<unsigned>(heads_kv));
+  p.row_blocks = ceil_div(p.rows, int64_t(kMqRows));
+  p.per_xcd = ceil_div(p.row_blocks * heads_kv, int64_t(kXcds));
+  const dim3 grid(static_cast<unsigned>(p.per_xcd * kXcds));
 #define UC_ATTN(QD)                                                                                \
   do {                                                                                             \
     if (out_dtype == UC_BF16)                                                                      \
