@@ -15,14 +15,17 @@
 // subtracting that power of two; one packed FMA with the fp16 scale/min gives
 // k = fp16(code*scale + min).  The query (fp16) is the constant B operand.
 //
-// Values (P.V on v_mfma_f32_16x16x16f16).  A value word holds TPW channels of
-// one token, but the B operand wants token pairs per register.  Codes of a
-// word are spread into an A fragment (rows = 16 tokens, k = 16 channels) and
-// transposed by an MFMA with a constant selection matrix whose accumulator is
-// seeded with minus the mantissa offset, so it returns the exact codes in the
-// B layout.  The per-token value scale rides in the A operand (P * scale);
-// the per-token value minimum is folded back with one more MFMA (P x min)
-// whose column g holds sum_t P*min of value group g.
+// Values (O^T += V^T P^T on v_mfma_f32_16x16x32_f16).  A value word holds
+// TPW channels of one token; the A operand wants token pairs of one channel
+// per register.  A 32-channel block is split into its even and odd channels
+// (MFMA row r = channel 32b + 2r + i), so the two channels of a lane share one
+// byte: one v_perm gathers that byte of two tokens into the two 16-bit halves
+// and one AND per channel leaves code << offset in each half -- an fp16
+// denormal code * 2^(offset - 24), which the MFMA multiplies exactly; the
+// power of two is undone per channel at the end.  The per-token value scale
+// rides in the B operand (P * scale); the per-token value minimum is folded
+// back with one more MFMA (min x P) whose rows all hold sum_t P*min of value
+// group g.
 //
 // Each split writes a normalised fp16 partial with its (max, sum); a second
 // kernel merges the splits with a log-sum-exp combine.
@@ -49,7 +52,10 @@ struct DecShared {
   static constexpr int JW = T / Gm::TPW;     // key words per channel per iteration
   static constexpr int KPAD = kD + 16;       // key-stat row of 72 dwords: the 8 groups one read touches start 8 banks apart
   _Float16 ks[KG][KPAD], km[KG][KPAD];                  // key stats [group][channel]
-  _Float16 vs[NGD][Gm::TPW][JW], vm[NGD][Gm::TPW][JW];  // value stats [group][position][word]
+  // value stats [group][position / 2][word / 4][position % 2][word % 4]: the
+  // 8 values one MFMA k-slice needs (words 4k..4k+3 at positions 2j, 2j+1) are
+  // one 16-byte read
+  _Float16 vs[NGD][Gm::TPW / 2][JW / 4][2][4], vm[NGD][Gm::TPW / 2][JW / 4][2][4];
   uint32_t kw[4][4][16][8];                             // key words [block][k-slice][row][channel]
   // value words [position][word][row], rows padded to 20 dwords: a lane reads
   // four rows of one word as 16 bytes, and staging writes hit distinct banks
@@ -71,7 +77,7 @@ struct MfmaParams {
 // (O^T = V^T P^T): lane (n, k) owns query column n, so every rescale is
 // lane-local.
 struct WaveState {
-  f4 o[8];     // lane (n = lane%16, k = lane/16): query n, channels 16*cb + 4k + v (scaled, see value_pair)
+  f4 o[8];     // lane (n = lane%16, k = lane/16): query n, channel out_channel(cb, k, v)
   f4 cmin[4];  // sum_t P*min of value group g (every row of the block holds it)
   float m;     // running max of query n (log2 units), equal across the k-slices
   float l;     // this lane's share of the running sum (reduced over the k-slices at the end)
@@ -118,34 +124,28 @@ __device__ __forceinline__ void softmax_tile(f4 (&acc)[NP], const bool (&valid)[
   }
 }
 
-// Identity selection (k-slot k -> column k) for dense residual rows.
-__device__ __forceinline__ h4 identity_selector(int lane) {
-  const int n = lane & 15, kap = lane >> 4;
-  h4 b;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) b[v] = to_h(4 * kap + v == n ? 1.0f : 0.0f);
-  return b;
+// Output row v of accumulator cb in lane k-slice kap: channel
+// 32 (cb / 2) + 8 kap + 2 v + cb % 2 -- MFMA cb holds the even (cb % 2 = 0) or
+// odd channels of the 32-channel block cb / 2, so a lane's eight outputs of a
+// block are the contiguous channels 32 (cb / 2) + 8 kap + [0, 8).
+__device__ __forceinline__ constexpr int out_channel(int cb, int kap, int v) {
+  return 32 * (cb >> 1) + 8 * kap + 2 * v + (cb & 1);
 }
 
-// Value codes of channel c (lane%16 of a 16-channel block) for two tokens,
-// whose words are wa / wb, as fp16 code * 2^e with e = value_shift<BITS>(c):
-// the byte holding the channel is gathered from both words into the two
-// halves, its bits OR-ed into the mantissa of 1024 and 1024 subtracted.
+// Bit offset of channel c's code inside the byte that holds it.
 template <int BITS>
-__device__ __forceinline__ int value_shift(int c) {
+__device__ __forceinline__ constexpr int value_shift(int c) {
   return BITS == 2 ? 2 * (c & 3) : 4 * (c & 1);
 }
 
-template <int BITS>
-__device__ __forceinline__ uint32_t value_selector(int c) {
-  const uint32_t b = BITS == 2 ? uint32_t(c) / 4u : uint32_t(c & 7) / 2u;  // byte of the channel in its word
-  return b | (0x0cu << 8) | ((4u + b) << 16) | (0x0cu << 24);              // [wa.b, 0, wb.b, 0]
-}
-
-template <int BITS>
-__device__ __forceinline__ h2 value_pair(uint32_t wa, uint32_t wb, uint32_t sel, uint32_t mask) {
-  const uint32_t x = __builtin_amdgcn_perm(wb, wa, sel);
-  return as_h2(and_or(x, mask, 0x64006400u)) - h2{to_h(1024.0f), to_h(1024.0f)};
+// Selection B operand that picks channel 2n + i of a 32-channel A fragment
+// into column n: B[k][n] = (k == 2n + i).
+__device__ __forceinline__ h8 channel_selector(int lane, int i) {
+  const int n = lane & 15, kap = lane >> 4;
+  h8 b;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) b[j] = to_h(8 * kap + j == 2 * n + i ? 1.0f : 0.0f);
+  return b;
 }
 
 // ------------------------------------------------------------ packed path --
@@ -327,8 +327,11 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int tl = (e0 + e) / Sh::NGD, gd = (e0 + e) % Sh::NGD;
-      sh.vs[gd][tl % Gm::TPW][tl / Gm::TPW] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sw[e / 2] >> (16 * (e % 2))));
-      sh.vm[gd][tl % Gm::TPW][tl / Gm::TPW] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(mw[e / 2] >> (16 * (e % 2))));
+      const int pos = tl % Gm::TPW, row = tl / Gm::TPW;
+      sh.vs[gd][pos / 2][row / 4][pos % 2][row % 4] =
+          __builtin_bit_cast(_Float16, static_cast<uint16_t>(sw[e / 2] >> (16 * (e % 2))));
+      sh.vm[gd][pos / 2][row / 4][pos % 2][row % 4] =
+          __builtin_bit_cast(_Float16, static_cast<uint16_t>(mw[e / 2] >> (16 * (e % 2))));
     }
   }
 #pragma unroll
@@ -355,10 +358,6 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
   using Sh = DecShared<BITS, G>;
   const int tid = threadIdx.x, lane = tid & 63, half = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
-  // value extraction for this lane's channel c = r of each 16-channel block
-  const uint32_t vsel = value_selector<BITS>(r);
-  const int ve = value_shift<BITS>(r);
-  const uint32_t vmask = (Gm::MASK << ve) | (Gm::MASK << (16 + ve));
   constexpr int NP = Gm::TPW / 2;  // positions per half word
   const int gl = (r * Gm::TPW) / G;  // key group of this lane's row
   bool valid[4];
@@ -418,8 +417,16 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
   softmax_tile<NP>(acc, valid, full, scale_log2, st);
 
   // ---- values of these positions, two at a time: O^T += V^T P^T on
-  // v_mfma_f32_16x16x32_f16 with k = (word rows 4k..4k+3) x (positions pa, pb)
-  const int jw = 4 * kap;
+  // v_mfma_f32_16x16x32_f16 with k = (word rows 4k..4k+3) x (positions pa, pb).
+  // Row r of MFMA (b, i) is channel 32b + 2r + i: both channels of the lane
+  // sit in byte vbyte of word vword(b) of every token (2-bit: a byte holds 4
+  // channels, the lane takes two neighbours; 4-bit: a byte holds 2)
+  const int vbyte = BITS == 2 ? (r >> 1) & 3 : r & 3;
+  const int vword = BITS == 2 ? r >> 3 : r >> 2;  // word of the block
+  constexpr int WPB = 32 / Gm::TPW;               // value words per 32-channel block
+  const uint32_t vsel = uint32_t(vbyte) | (0x0cu << 8) | ((4u + vbyte) << 16) | (0x0cu << 24);  // [lo.b, 0, hi.b, 0]
+  const int o0 = value_shift<BITS>(2 * r);
+  uint32_t vmask[2] = {(Gm::MASK << o0) | (Gm::MASK << (16 + o0)), (Gm::MASK << (o0 + BITS)) | (Gm::MASK << (16 + o0 + BITS))};
 #pragma unroll
   for (int j = 0; j < NP / 2; ++j) {
     const int pa = half * NP + 2 * j, pb = pa + 1;
@@ -428,21 +435,24 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
     h8 ps[Sh::NGD];  // P * value scale, per value group
 #pragma unroll
     for (int g = 0; g < Sh::NGD; ++g) {
-      const h4 sa = *reinterpret_cast<const h4 *>(&sh.vs[g][pa][jw]), sb = *reinterpret_cast<const h4 *>(&sh.vs[g][pb][jw]);
-      const h4 ma = *reinterpret_cast<const h4 *>(&sh.vm[g][pa][jw]), mb = *reinterpret_cast<const h4 *>(&sh.vm[g][pb][jw]);
-      ps[g] = p8 * h8{sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+      const h8 s8 = *reinterpret_cast<const h8 *>(&sh.vs[g][pa / 2][kap][0][0]);
+      const h8 m8 = *reinterpret_cast<const h8 *>(&sh.vm[g][pa / 2][kap][0][0]);
+      ps[g] = p8 * s8;
       // every row of A = the value minima: each output row gets sum_t P*min
-      st.cmin[g] = mfma32(h8{ma[0], ma[1], ma[2], ma[3], mb[0], mb[1], mb[2], mb[3]}, p8, st.cmin[g]);
+      st.cmin[g] = mfma32(m8, p8, st.cmin[g]);
     }
 #pragma unroll
-    for (int cb = 0; cb < 8; ++cb) {
-      const int wi = BITS == 2 ? cb : 2 * cb + (r >> 3);  // word holding channel 16*cb + r
+    for (int b = 0; b < 4; ++b) {
+      const int wi = WPB * b + vword;
       const uint4 wa = *reinterpret_cast<const uint4 *>(&sh.vw[pa][wi][4 * kap]);
       const uint4 wb = *reinterpret_cast<const uint4 *>(&sh.vw[pb][wi][4 * kap]);
-      const h2 x0 = value_pair<BITS>(wa.x, wa.y, vsel, vmask), x1 = value_pair<BITS>(wa.z, wa.w, vsel, vmask);
-      const h2 x2 = value_pair<BITS>(wb.x, wb.y, vsel, vmask), x3 = value_pair<BITS>(wb.z, wb.w, vsel, vmask);
-      const h8 av = h8{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
-      st.o[cb] = mfma32(av, ps[(16 * cb) / G], st.o[cb]);
+      const uint32_t y[4] = {__builtin_amdgcn_perm(wa.y, wa.x, vsel), __builtin_amdgcn_perm(wa.w, wa.z, vsel),
+                             __builtin_amdgcn_perm(wb.y, wb.x, vsel), __builtin_amdgcn_perm(wb.w, wb.z, vsel)};
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint4 x = make_uint4(y[0] & vmask[i], y[1] & vmask[i], y[2] & vmask[i], y[3] & vmask[i]);
+        st.o[2 * b + i] = mfma32(__builtin_bit_cast(h8, x), ps[(32 * b) / G], st.o[2 * b + i]);
+      }
     }
   }
 }
@@ -478,13 +488,15 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
     if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, t0 + Sh::T);  // lands while this iteration computes
     compute_tile<BITS, G>(sh, sq, t0, rg.nkw, p.scale_log2, st);
   }
-  // undo the code scaling 2^e of output row c (e depends on c mod 4 / mod 2,
-  // i.e. on v) and add the value minima
+  // undo the denormal code scaling 2^(e - 24) of each output channel (e
+  // depends on the channel mod 4 / mod 2, i.e. on cb and v) and add the
+  // value minima
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb)
 #pragma unroll
     for (int v = 0; v < 4; ++v)
-      st.o[cb][v] = st.o[cb][v] * (1.0f / float(1 << value_shift<BITS>(v))) + st.cmin[(16 * cb) / G][v];
+      st.o[cb][v] = st.o[cb][v] * (16777216.0f / float(1 << value_shift<BITS>(out_channel(cb, 0, v)))) +
+                    st.cmin[(32 * (cb >> 1)) / G][v];
   (void)lane;
 }
 
@@ -506,13 +518,6 @@ __device__ __forceinline__ h8 load8_h(Rsrc r, uint32_t off) {
 }
 
 template <int RD>
-__device__ __forceinline__ h4 load4_h(Rsrc r, uint32_t off) {
-  const uint2 raw = bload64(r, off);
-  return h4{to_h(half_bits_to_f32<RD>(raw.x)), to_h(half_bits_to_f32<RD>(raw.x >> 16)),
-            to_h(half_bits_to_f32<RD>(raw.y)), to_h(half_bits_to_f32<RD>(raw.y >> 16))};
-}
-
-template <int RD>
 __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], const uc_kivi_item &it, int64_t h,
                                                int64_t tr0, const MfmaParams &p, WaveState &st) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -522,7 +527,7 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
   const Rsrc rk = make_rsrc(it.residual_key, bytes), rv = make_rsrc(it.residual_value, bytes);
   const int64_t tw = tr0 + wave * kResWaveTokens;
   constexpr int kBlocks = kResWaveTokens / 16;
-  const h4 ident = identity_selector(lane);
+  const h8 csel[2] = {channel_selector(lane, 0), channel_selector(lane, 1)};
   f4 acc[kBlocks];
 #pragma unroll
   for (int b = 0; b < kBlocks; ++b) {
@@ -555,8 +560,9 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
     }
   st.m = m;
   st.l = sum;
-  // O^T += V^T P^T: the 4 channels x 16 tokens a lane loads from a residual row
-  // block come out of an identity MFMA as 4 tokens of one channel (the A layout)
+  // O^T += V^T P^T: the 8 channels x 16 tokens a lane loads from a residual
+  // row block come out of a selection MFMA as 4 tokens of channel 32b + 2n + i
+  // (the A layout of accumulator 2b + i, as in the packed path)
 #pragma unroll
   for (int j = 0; j < kBlocks / 2; ++j) {
     const h4 pa4 = cvt4(acc[2 * j]), pb4 = cvt4(acc[2 * j + 1]);
@@ -564,11 +570,14 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
     const uint32_t base0 = static_cast<uint32_t>(((tw + 32 * j + r) * p.Hkv + h) * kD * 2);
     const uint32_t base1 = static_cast<uint32_t>(((tw + 32 * j + 16 + r) * p.Hkv + h) * kD * 2);
 #pragma unroll
-    for (int cb = 0; cb < 8; ++cb) {
-      const f4 t0 = mfma16(load4_h<RD>(rv, base0 + (16 * cb + 4 * kap) * 2), ident, f4{0, 0, 0, 0});
-      const f4 t1 = mfma16(load4_h<RD>(rv, base1 + (16 * cb + 4 * kap) * 2), ident, f4{0, 0, 0, 0});
-      const h4 a0 = cvt4(t0), a1 = cvt4(t1);
-      st.o[cb] = mfma32(h8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, p8, st.o[cb]);
+    for (int b = 0; b < 4; ++b) {
+      const h8 v0 = load8_h<RD>(rv, base0 + (32 * b + 8 * kap) * 2);
+      const h8 v1 = load8_h<RD>(rv, base1 + (32 * b + 8 * kap) * 2);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const h4 a0 = cvt4(mfma32(v0, csel[i], f4{0, 0, 0, 0})), a1 = cvt4(mfma32(v1, csel[i], f4{0, 0, 0, 0}));
+        st.o[2 * b + i] = mfma32(h8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, p8, st.o[2 * b + i]);
+      }
     }
   }
 }
@@ -608,7 +617,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     if (tr0 < it.residual_tokens) residual_split<RD>(sq, it, h, tr0, p, st);
   }
 
-  // ---- merge the two waves; lane (n, k) holds query n, channels 16*cb + 4k + v
+  // ---- merge the two waves; lane (n, k) holds query n, channels out_channel(cb, k, v)
   const int kap = lane >> 4, n = lane & 15;
   const float l_all = sum_over_slices(st.l);
   __syncthreads();
@@ -631,7 +640,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) fin[n * kD + 16 * cb + 4 * kap + v] = st.o[cb][v] * mine;
+      for (int v = 0; v < 4; ++v) fin[n * kD + out_channel(cb, kap, v)] = st.o[cb][v] * mine;
   }
   __syncthreads();
   const int64_t slot = (item * p.Hkv + h) * p.splits_total + split;
@@ -639,14 +648,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     _Float16 *po = p.ws_o + slot * 16 * kD;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
 #pragma unroll
-    for (int cb = 0; cb < 8; ++cb) {
-      h4 o4;
+    for (int b = 0; b < 4; ++b) {  // channels 32b + 8kap + [0, 8): accumulators 2b (even), 2b + 1 (odd)
+      h8 o8;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int c = 16 * cb + 4 * kap + v;
-        o4[v] = to_h((st.o[cb][v] * mine + fin[n * kD + c]) * inv);
-      }
-      *reinterpret_cast<h4 *>(&po[n * kD + 16 * cb + 4 * kap]) = o4;
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          o8[2 * v + i] = to_h((st.o[2 * b + i][v] * mine + fin[n * kD + out_channel(2 * b + i, kap, v)]) * inv);
+      *reinterpret_cast<h8 *>(&po[n * kD + 32 * b + 8 * kap]) = o8;
     }
     if (kap == 0) {
       p.ws_ml[(slot * 16 + n) * 2 + 0] = M;
