@@ -1,10 +1,13 @@
 // MFMA split-K decode over KIVI-packed KV (head_dim 128, 2/4-bit codes).
 //
-// One workgroup (2 waves) owns (item, KV head, split of S packed tokens) or
-// a residual split.  An iteration stages one super-tile (16 key words of
-// every channel) and each wave takes half of its token positions.  The <= 16 query rows of a KV head (query heads x query
-// length) form the N = 16 columns of every MFMA, so each packed byte is read
-// from HBM once per (item, KV head).
+// One workgroup (2 waves) owns a packed split of one unit (item, KV head) --
+// every S-th super-tile (16 key words of every channel) starting at the split
+// index -- or a residual split.  The S splits of a unit run side by side on
+// one XCD, so the 128-byte lines of the channel-major key streams are read
+// from HBM about once although each split uses a part of them.  An iteration
+// stages one super-tile and each wave takes half of its token positions.  The
+// <= 16 query rows of a KV head (query heads x query length) form the N = 16
+// columns of every MFMA.
 //
 // Keys (QK^T on v_mfma_f32_16x16x32_f16).  A key word holds TPW = 32/bits
 // tokens of one channel.  MFMA rows are 16 consecutive words at one token
@@ -39,6 +42,7 @@ namespace {
 
 using namespace mf;
 
+constexpr int kXcds = 8;  // XCDs of an MI355X; workgroup i of a launch runs on XCD i % 8
 constexpr int kWaves = 2;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kResWaveTokens = 64;  // residual tokens per wave per residual split
@@ -67,6 +71,8 @@ struct MfmaParams {
   int64_t Hq, Hkv, Lq, group, rows;
   int64_t splits_packed, splits_total, nst;  // nst: super-tiles per packed split
   int64_t segs;                              // consecutive items that share one query and output
+  int64_t units;                             // items x KV heads
+  int xcd_grouped;                           // splits of a unit on one XCD (see the kernel)
   float scale_log2;
   _Float16 *ws_o;  // [items * Hkv * splits][16][128] normalised partial outputs
   float *ws_ml;    // [items * Hkv * splits][16][2] (max in log2 units, sum)
@@ -459,7 +465,7 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
 
 template <int BITS, int G>
 __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Float16 (*sq)[kQPad],
-                                             const uc_kivi_item &it, int64_t h, int64_t t_split,
+                                             const uc_kivi_item &it, int64_t h, int64_t split,
                                              const MfmaParams &p, WaveState &st) {
   using Gm = Geo<BITS>;
   using Sh = DecShared<BITS, G>;
@@ -476,16 +482,20 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
   rg.vcode = make_rsrc(static_cast<const char *>(it.value_code) + h * vcode_bytes, vcode_bytes);
   rg.vscale = make_rsrc(static_cast<const char *>(it.value_scale) + h * vstat_bytes, vstat_bytes);
   rg.vmin = make_rsrc(static_cast<const char *>(it.value_min) + h * vstat_bytes, vstat_bytes);
-  const int64_t left = Tq - t_split;
-  const int n_it = static_cast<int>(min<int64_t>(p.nst, (left + Sh::T - 1) / Sh::T));
+  // super-tiles split, split + S, split + 2S, ... (S = packed splits): the S
+  // splits of a unit run side by side on one XCD and read neighbouring parts
+  // of the same 128-byte key-code and key-stat lines at about the same time
+  const int64_t n_super = (Tq + Sh::T - 1) / Sh::T;
+  const int64_t stride = p.splits_packed * Sh::T;
+  const int n_it = static_cast<int>(min<int64_t>(p.nst, (n_super - split + p.splits_packed - 1) / p.splits_packed));
   Prefetch<BITS, G> pf;
-  issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(t_split));
+  issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(split * Sh::T));
   for (int i = 0; i < n_it; ++i) {
-    const uint32_t t0 = static_cast<uint32_t>(t_split + int64_t(i) * Sh::T);
+    const uint32_t t0 = static_cast<uint32_t>((split + int64_t(i) * p.splits_packed) * Sh::T);
     __syncthreads();  // every wave is done reading the previous iteration from LDS
     stage_lds<BITS, G>(sh, pf, t0, rg.nkg);
     __syncthreads();
-    if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, t0 + Sh::T);  // lands while this iteration computes
+    if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(t0 + stride));  // lands during this iteration
     compute_tile<BITS, G>(sh, sq, t0, rg.nkw, p.scale_log2, st);
   }
   // undo the denormal code scaling 2^(e - 24) of each output channel (e
@@ -592,9 +602,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   __shared__ _Float16 sq[16][kQPad];
   __shared__ float mrg_ml[kWaves][16][2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t item = TABLE ? blockIdx.z : 0;
+  // Workgroup i runs on XCD i % 8; with enough units its k = i / 8-th
+  // workgroup there is split k % S of unit (item, KV head) u = 8 (k / S) + i % 8,
+  // so the S splits of a unit are dispatched back to back on one XCD and share
+  // its L2.  A launch of few units spreads each unit's splits over the XCDs.
+  int64_t u, split;
+  if (p.xcd_grouped) {
+    const int64_t x = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
+    u = (k / p.splits_total) * kXcds + x;
+    split = k % p.splits_total;
+  } else {
+    u = blockIdx.x / p.splits_total;
+    split = blockIdx.x % p.splits_total;
+  }
+  if (u >= p.units) return;  // uniform: the whole workgroup leaves
+  const int64_t item = TABLE ? u / p.Hkv : 0;
   const uc_kivi_item it = TABLE ? items[item] : single;
-  const int64_t h = blockIdx.y, split = blockIdx.x;
+  const int64_t h = u % p.Hkv;
 
   stage_queries(sq, it.query, h, p);
   WaveState st;
@@ -610,8 +634,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // instead of forming its tail
   const int64_t splits_res = p.splits_total - p.splits_packed;
   if (split >= splits_res) {
-    const int64_t t_split = (split - splits_res) * p.nst * DecShared<BITS, G>::T;
-    if (t_split < it.quantized_tokens) packed_split<BITS, G>(sh, sq, it, h, t_split, p, st);
+    const int64_t sp = split - splits_res;
+    if (sp * DecShared<BITS, G>::T < it.quantized_tokens) packed_split<BITS, G>(sh, sq, it, h, sp, p, st);
   } else {
     const int64_t tr0 = split * kWaves * kResWaveTokens;
     if (tr0 < it.residual_tokens) residual_split<RD>(sq, it, h, tr0, p, st);
@@ -821,7 +845,10 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   p.ws_ml = reinterpret_cast<float *>(static_cast<char *>(workspace) + slots * 16 * kD * sizeof(_Float16));
   const bool table = items_dev != nullptr;
   const uc_kivi_item one = single ? *single : uc_kivi_item{};
-  const dim3 grid(p.splits_total, Hkv, n_items);
+  p.units = n_items * Hkv;
+  p.xcd_grouped = p.units >= 4 * kXcds;  // at most one unit of imbalance per XCD in four
+  const dim3 grid(static_cast<unsigned>((p.xcd_grouped ? ceil_div(p.units, int64_t(kXcds)) * kXcds : p.units) *
+                                        p.splits_total));
   if (bits == 2) {
     if (group_size == 32) launch_group<2, 32>(table, res_dtype, grid, stream, items_dev, one, p);
     else if (group_size == 64) launch_group<2, 64>(table, res_dtype, grid, stream, items_dev, one, p);
