@@ -239,9 +239,11 @@ __device__ __forceinline__ void value_chunk(int q, int a, int &pos, int &quad) {
   }
 }
 
-// N consecutive dwords from byte offset `off` (4-byte aligned) in the fewest loads.
-template <int N>
-__device__ __forceinline__ void load_dwords(uint32_t (&d)[N], Rsrc r, uint32_t off) {
+// The first N dwords of d: consecutive dwords from byte offset `off` (4-byte
+// aligned) in the fewest loads.
+template <int N, int M>
+__device__ __forceinline__ void load_dwords(uint32_t (&d)[M], Rsrc r, uint32_t off) {
+  static_assert(N <= M, "load fits the array");
   int q = 0;
 #pragma unroll
   for (; q + 4 <= N; q += 4) {
@@ -267,11 +269,18 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
   // key stats [D][nkg]: thread = channel, its KG groups as dwords from the
   // 4-byte boundary at or below the first (realigned when staged)
   // (one 16-byte load per four dwords: each load of a wave touches 64 rows, so
-  // fewer, wider loads mean fewer memory requests)
+  // fewer, wider loads mean fewer memory requests; when every row segment
+  // starts on a dword -- even nkg and t0 / G -- the last dword is not needed)
   {
     const uint32_t d0 = (tid * rg.nkg + t0 / G) >> 1;
-    load_dwords<Pf::NKD>(pf.ks, rg.kscale, d0 * 4u);
-    load_dwords<Pf::NKD>(pf.km, rg.kmin, d0 * 4u);
+    if (((rg.nkg | (t0 / G)) & 1u) == 0u) {
+      load_dwords<Pf::NKD - 1>(pf.ks, rg.kscale, d0 * 4u);
+      load_dwords<Pf::NKD - 1>(pf.km, rg.kmin, d0 * 4u);
+      pf.ks[Pf::NKD - 1] = pf.km[Pf::NKD - 1] = 0u;  // read by the realignment with shift 0
+    } else {
+      load_dwords<Pf::NKD>(pf.ks, rg.kscale, d0 * 4u);
+      load_dwords<Pf::NKD>(pf.km, rg.kmin, d0 * 4u);
+    }
   }
   // value stats [Tq][NGD]
 #pragma unroll
