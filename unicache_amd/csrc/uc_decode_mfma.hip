@@ -698,93 +698,88 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 }
 
 // Merge the split partials of one (query, KV head) -- every split of the
-// p.segs items that share the query -- for half of the channels (blockIdx.z):
-// the (max, sum) of up to 64 slots at a time are staged in LDS by all threads
-// and folded per query row into a running (M, L); a second sweep turns them
-// into weights l_s 2^(m_s - M) / L and accumulates the fp16 partials.  The
+// p.segs items that share the query -- for a quarter of the channels
+// (blockIdx.z).  Thread (row = tid / 8, j = tid % 8) folds the (max, sum) of
+// slots j, j + 8, ... into an online (M, L), the 8 threads of a row combine
+// theirs with lane shuffles, and each then accumulates its 4 channels over all
+// slots with weights l_s 2^(m_s - M) / L, eight slots' loads in flight.  No
+// LDS and no barrier: the launch is a short chain of independent loads.  The
 // output goes to the first item of the group.
 constexpr int kCombineThreads = 128;
-constexpr int kCombineParts = 2;  // channel halves per (query, KV head)
+constexpr int kCombineParts = 4;  // channel quarters per (query, KV head)
+constexpr int kCombineLanes = 8;  // threads per query row
+
+__device__ __forceinline__ void ml_fold(float &M, float &L, float m, float l) {
+  if (!(l > 0.0f) || m == kNegInf) return;
+  if (m > M) {
+    L = (L > 0.0f ? L * exp2f(M - m) : 0.0f) + l;
+    M = m;
+  } else {
+    L += l * exp2f(m - M);
+  }
+}
 
 template <bool TABLE>
 __global__ __launch_bounds__(kCombineThreads) void decode_mfma_combine(const uc_kivi_item *items, uc_kivi_item single,
                                                                        MfmaParams p) {
-  constexpr int kChunk = 64;
-  __shared__ float sm[16][kChunk + 1], sl[16][kChunk + 1];
-  __shared__ float row_m[16], row_inv[16];
   const int64_t first = TABLE ? blockIdx.y * p.segs : 0;
   const uc_kivi_item it = TABLE ? items[first] : single;
   const int64_t h = blockIdx.x;
   const int part = blockIdx.z;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, row = tid / kCombineLanes, j = tid % kCombineLanes;
   const int nflat = int(p.segs * p.splits_total);
+  static_assert(16 * kCombineLanes == kCombineThreads && kD / kCombineParts == 4 * kCombineLanes,
+                "thread = (row, 4 channels of the part)");
   // flattened (segment, split) index -> workspace slot
   auto slot = [&](int f) {
     return ((first + f / p.splits_total) * p.Hkv + h) * p.splits_total + f % p.splits_total;
   };
-  auto stage = [&](int s0, int ns) {
-    for (int idx = tid; idx < 16 * ns; idx += kCombineThreads) {
-      const int r = idx & 15, sidx = idx >> 4;
-      const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + (slot(s0 + sidx) * 16 + r) * 2);
-      sm[r][sidx] = ml.x;
-      sl[r][sidx] = ml.y;
-    }
-  };
-  // pass 1: running (M, L) per row
+  auto ml_at = [&](int f) { return *reinterpret_cast<const float2 *>(p.ws_ml + (slot(f) * 16 + row) * 2); };
+  // pass 1: this thread's slots, four loads in flight, then the row's 8 threads
   float M = kNegInf, L = 0.0f;
-  for (int s0 = 0; s0 < nflat; s0 += kChunk) {
-    const int ns = min(kChunk, nflat - s0);
-    __syncthreads();
-    stage(s0, ns);
-    __syncthreads();
-    if (tid < p.rows) {
-      float cm = kNegInf;
-      for (int s = 0; s < ns; ++s)
-        if (sl[tid][s] > 0.0f) cm = fmaxf(cm, sm[tid][s]);
-      const float m_new = fmaxf(M, cm);
-      if (m_new != kNegInf) {
-        float acc = L > 0.0f ? L * exp2f(M - m_new) : 0.0f;
-        for (int s = 0; s < ns; ++s)
-          if (sl[tid][s] > 0.0f && sm[tid][s] != kNegInf) acc += sl[tid][s] * exp2f(sm[tid][s] - m_new);
-        L = acc;
-        M = m_new;
-      }
-    }
-  }
-  if (tid < p.rows) {
-    row_m[tid] = M;
-    row_inv[tid] = L > 0.0f ? 1.0f / L : 0.0f;
-    if (part == 0 && it.lse != nullptr) {
-      const int64_t g = tid / p.Lq, i = tid % p.Lq;
-      it.lse[(h * p.group + g) * p.Lq + i] = L > 0.0f ? (M + log2f(L)) * kLn2 : kNegInf;
-    }
-  }
-  // pass 2: thread -> (row, 8 channels of this part)
-  constexpr int kC8 = kD / 8 / kCombineParts;
-  const int row = tid / kC8, c8 = (part * kC8 + tid % kC8) * 8;
-  const bool active = row < p.rows;
-  float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int s0 = 0; s0 < nflat; s0 += kChunk) {
-    const int ns = min(kChunk, nflat - s0);
-    __syncthreads();
-    stage(s0, ns);
-    __syncthreads();
-    if (active) {
-      const float rm = row_m[row], rinv = row_inv[row];
-      for (int s = 0; s < ns; ++s) {
-        const float l = sl[row][s], m = sm[row][s];
-        if (!(l > 0.0f && m != kNegInf)) continue;
-        const float w = l * exp2f(m - rm) * rinv;
-        const h8 v = *reinterpret_cast<const h8 *>(p.ws_o + (slot(s0 + s) * 16 + row) * kD + c8);
+  for (int f0 = j; f0 < nflat; f0 += 4 * kCombineLanes) {
+    float2 ml[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = fmaf(float(v[j]), w, o[j]);
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int f = f0 + u * kCombineLanes;
+      ml[u] = f < nflat ? ml_at(f) : make_float2(kNegInf, 0.0f);
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ml_fold(M, L, ml[u].x, ml[u].y);
   }
+#pragma unroll
+  for (int o = 1; o < kCombineLanes; o <<= 1) {
+    const float m2 = __shfl_xor(M, o, kWave), l2 = __shfl_xor(L, o, kWave);
+    ml_fold(M, L, m2, l2);
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  const bool active = row < p.rows;
+  if (active && part == 0 && j == 0 && it.lse != nullptr) {
+    const int64_t g = row / p.Lq, i = row % p.Lq;
+    it.lse[(h * p.group + g) * p.Lq + i] = L > 0.0f ? (M + log2f(L)) * kLn2 : kNegInf;
+  }
+  // pass 2: 4 channels of this part over every slot
+  const int c4 = (part * kCombineLanes + j) * 4;
+  float o[4] = {0, 0, 0, 0};
   if (active) {
+    for (int f0 = 0; f0 < nflat; f0 += 8) {
+      h4 v[8];
+      float w[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int f = f0 + u < nflat ? f0 + u : f0;
+        const float2 ml = ml_at(f);
+        w[u] = (f0 + u < nflat && ml.y > 0.0f && ml.x != kNegInf) ? ml.y * exp2f(ml.x - M) * inv : 0.0f;
+        v[u] = *reinterpret_cast<const h4 *>(p.ws_o + (slot(f) * 16 + row) * kD + c4);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = w[u] != 0.0f ? fmaf(float(v[u][c]), w[u], o[c]) : o[c];
+    }
     const int64_t g = row / p.Lq, i = row % p.Lq;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) store_dyn(it.out, (i * p.Hq + h * p.group + g) * kD + c8 + j, o[j], p.od);
+    for (int c = 0; c < 4; ++c) store_dyn(it.out, (i * p.Hq + h * p.group + g) * kD + c4 + c, o[c], p.od);
   }
 }
 
