@@ -48,6 +48,7 @@ struct MqParams {
   const _Float16 *wk;  // [Hkv][keys_pad][128]
   const _Float16 *wv;  // [Hkv][128][keys_pad]
   int64_t row_blocks, per_xcd;  // row blocks per KV head; work items per XCD
+  FastDiv lq;                   // row -> (query head of the group, query position)
 };
 
 struct StageParams {
@@ -389,7 +390,8 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
   for (int qb = 0; qb < 2; ++qb) {
     const int64_t row = row0 + 16 * qb + r;
     const bool ok = row < p.rows;
-    const int64_t g = ok ? row / p.Lq : 0, i = ok ? row % p.Lq : 0;
+    const uint32_t gq = ok ? fast_div(static_cast<uint32_t>(row), p.lq) : 0;
+    const int64_t g = gq, i = ok ? row - int64_t(gq) * p.Lq : 0;
     const int64_t base = (i * p.Hq + h * p.group + g) * kD;
     const uint16_t *q16 = static_cast<const uint16_t *>(it.query) + base + 8 * kap;
 #pragma unroll
@@ -469,8 +471,8 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
         }
       const int64_t row = row0 + 16 * qb + r;
       if (kap == 0 && row < p.rows && it.lse != nullptr) {
-        const int64_t g = row / p.Lq, i = row % p.Lq;
-        it.lse[(h * p.group + g) * p.Lq + i] = l > 0.0f ? (M + log2f(l)) * kLn2 : kNegInf;
+        // (h * group + g) * Lq + i = h * rows + row
+        it.lse[h * p.rows + row] = l > 0.0f ? (M + log2f(l)) * kLn2 : kNegInf;
       }
     }
   }
@@ -483,7 +485,8 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
       const int idx = q * kWave + lane, rr = idx / kPerRow, cc = (idx % kPerRow) * kChunk;
       const int64_t row = row0 + rr;
       if (row >= p.rows) continue;
-      const int64_t g = row / p.Lq, i = row % p.Lq;
+      const uint32_t gq = fast_div(static_cast<uint32_t>(row), p.lq);
+      const int64_t g = gq, i = row - int64_t(gq) * p.Lq;
       *reinterpret_cast<uint4 *>(static_cast<OutT *>(it.out) + (i * p.Hq + h * p.group + g) * kD + cc) =
           *reinterpret_cast<const uint4 *>(&ob[rr * kRowPad + cc]);
     }
@@ -516,7 +519,8 @@ extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int grou
   UC_REQUIRE(heads_kv > 0 && heads_q > 0 && heads_q % heads_kv == 0,
              "attn_mq: query heads (%lld) must be a multiple of KV heads (%lld)", (long long)heads_q,
              (long long)heads_kv);
-  UC_REQUIRE(query_len > 0, "attn_mq: query_len must be positive");
+  UC_REQUIRE(query_len > 0 && query_len * (heads_q / heads_kv) < (int64_t(1) << 31),
+             "attn_mq: query_len must be positive and query rows per KV head below 2^31");
   UC_REQUIRE((q_dtype == UC_BF16 || q_dtype == UC_FP16) && (res_dtype == UC_BF16 || res_dtype == UC_FP16),
              "attn_mq: query and residual must be bf16 or fp16");
   UC_REQUIRE(out_dtype == UC_BF16 || out_dtype == UC_FP16 || out_dtype == UC_FP32, "attn_mq: bad out dtype");
@@ -574,6 +578,7 @@ extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int grou
   p.wk = sp.wk;
   p.wv = sp.wv;
   p.row_blocks = ceil_div(p.rows, int64_t(kMqRows));
+  p.lq = make_fastdiv(static_cast<uint32_t>(query_len));
   p.per_xcd = ceil_div(p.row_blocks * heads_kv, int64_t(kXcds));
   const dim3 grid(static_cast<unsigned>(p.per_xcd * kXcds));
 #define UC_ATTN(QD)                                                                                \

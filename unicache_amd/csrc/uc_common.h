@@ -43,6 +43,25 @@ int check_launch(const char *what);
 
 inline hipStream_t as_stream(uc_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Division of n < 2^31 by a launch constant d >= 1 without a divide sequence:
+// with l = ceil(log2 d) and m = floor(2^(31+l) / d) + 1 (< 2^32),
+// floor(n / d) = (n m) >> (31 + l) exactly (m d - 2^(31+l) is in (0, d] <= 2^l,
+// so the error term stays below 1/d).
+struct FastDiv {
+  uint32_t d, m, shift;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  const uint64_t m = ((uint64_t(1) << (31 + l)) / d) + 1;
+  return FastDiv{d, static_cast<uint32_t>(m), 31 + l};
+}
+
+__host__ __device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
+  return static_cast<uint32_t>((uint64_t(n) * f.m) >> f.shift);
+}
+
 inline bool valid_dtype(int d) { return d == UC_BF16 || d == UC_FP16 || d == UC_FP32; }
 inline bool half_dtype(int d) { return d == UC_BF16 || d == UC_FP16; }
 
