@@ -214,10 +214,17 @@ struct SelectArgs {
 // the heavy_k-th largest score; tokens strictly above it are all kept and
 // equal ones are taken in ascending index order until heavy_k are chosen.
 // An ordered block scan writes the kept indices in ascending order.
+// Each pass counts into per-wave histograms (scores of a head share their top
+// bytes, so one shared histogram would serialise on a few bins), sums them per
+// bin, and wave 0 finds the bin holding the threshold with a suffix scan over
+// its lanes (4 bins each).
+constexpr int kSelWaves = kSelThreads / kWave;
+
 __global__ __launch_bounds__(kSelThreads) void h2o_select_kernel(SelectArgs a) {
+  __shared__ uint32_t whist[kSelWaves][256];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t sh_prefix, sh_need;
-  __shared__ uint32_t wave_tot[2][kSelThreads / kWave];
+  __shared__ uint32_t wave_tot[2][kSelWaves];
   const int64_t h = blockIdx.x;
   const int64_t hist_end = a.T - a.recent;
   const float *sc = a.scores + h * a.s_sh;
@@ -229,22 +236,47 @@ __global__ __launch_bounds__(kSelThreads) void h2o_select_kernel(SelectArgs a) {
     uint32_t need = static_cast<uint32_t>(a.heavy_k);
     for (int pass = 0; pass < 4; ++pass) {
       const int shift = 24 - 8 * pass;
-      if (tid < 256) hist[tid] = 0;
+      for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&whist[0][0])[i] = 0;
       __syncthreads();
       for (int64_t t = tid; t < hist_end; t += kSelThreads) {
         const uint32_t key = order_key(sc[t * a.s_st]);
-        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        if ((key & mask) == prefix) atomicAdd(&whist[wave][(key >> shift) & 255u], 1u);
       }
       __syncthreads();
-      if (tid == 0) {
-        uint32_t above = 0;
-        int b = 255;
-        for (; b > 0; --b) {
-          if (above + hist[b] >= need) break;
-          above += hist[b];
+      if (tid < 256) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int w = 0; w < kSelWaves; ++w) c += whist[w][tid];
+        hist[tid] = c;
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // lane l owns bins 4l .. 4l + 3; above = count in bins above lane l's
+        const uint32_t b0 = hist[4 * lane], b1 = hist[4 * lane + 1], b2 = hist[4 * lane + 2], b3 = hist[4 * lane + 3];
+        const uint32_t mine = b0 + b1 + b2 + b3;
+        uint32_t incl = mine;  // suffix sum over lanes >= l
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t v = __shfl_down(incl, o, kWave);
+          if (lane + o < kWave) incl += v;
         }
-        sh_prefix = prefix | (uint32_t(b) << shift);
-        sh_need = need - above;
+        const uint32_t above = incl - mine;
+        // the threshold bin is in the lane whose range crosses `need` (the
+        // lowest bin, 0, takes whatever is left)
+        const bool here = above < need && (incl >= need || lane == 0);
+        if (here) {
+          uint32_t acc = above;
+          int b = 4 * lane + 3;
+          const uint32_t bins[4] = {b0, b1, b2, b3};
+#pragma unroll
+          for (int j = 3; j > 0; --j) {
+            if (acc + bins[j] >= need) break;
+            acc += bins[j];
+            --b;
+          }
+          sh_prefix = prefix | (uint32_t(b) << shift);
+          sh_need = need - acc;
+        }
       }
       __syncthreads();
       prefix = sh_prefix;
@@ -276,7 +308,7 @@ __global__ __launch_bounds__(kSelThreads) void h2o_select_kernel(SelectArgs a) {
       for (int w = 0; w < wave; ++w) sel_before += wave_tot[1][w];
       if (sel) out[sel_before] = t;
       uint32_t tot_eq = 0, tot_sel = 0;
-      for (int w = 0; w < kSelThreads / kWave; ++w) {
+      for (int w = 0; w < kSelWaves; ++w) {
         tot_eq += wave_tot[0][w];
         tot_sel += wave_tot[1][w];
       }
