@@ -2,10 +2,11 @@
 // rows t with keep[t] != 0 move, in order, to the front of the output.
 //
 // uc_mask_scan: one workgroup of 1024 threads; thread i counts the kept rows
-// of its contiguous chunk (16-byte mask loads), a workgroup exclusive scan
-// turns the counts into chunk offsets, and every thread writes the
-// destination row of each of its kept rows.  Deterministic, one pass over the
-// mask plus one over the destination array.
+// of its contiguous chunk (16-byte mask loads), an exclusive scan (lane
+// shuffles within each wave, then over the 16 wave totals) turns the counts
+// into chunk offsets, and every thread writes the destination row of each of
+// its kept rows.  Deterministic, one pass over the mask plus one over the
+// destination array.
 //
 // uc_compact_rows: one thread per 16 (or 8, 4, 2, 1) bytes of a row, rows of
 // dropped tokens exit at once; the copy of a kept row is fully coalesced.
@@ -18,7 +19,7 @@ constexpr int kScanThreads = 1024;
 
 __global__ __launch_bounds__(kScanThreads) void mask_scan_kernel(const uint8_t *keep, int64_t n, int64_t chunk,
                                                                  int32_t *dst, int64_t *total) {
-  __shared__ int64_t part[kScanThreads];
+  __shared__ int64_t part[2 * kScanThreads / kWave];
   const int tid = threadIdx.x;
   const int64_t b = tid * chunk, e = min(n, b + chunk);
   int64_t cnt = 0;
@@ -38,17 +39,29 @@ __global__ __launch_bounds__(kScanThreads) void mask_scan_kernel(const uint8_t *
     }
     for (; t < e; ++t) cnt += keep[t] != 0;
   }
-  part[tid] = cnt;
-  __syncthreads();
-  // Hillis-Steele inclusive scan over 1024 partial counts
-  for (int off = 1; off < kScanThreads; off <<= 1) {
-    const int64_t add = tid >= off ? part[tid - off] : 0;
-    __syncthreads();
-    part[tid] += add;
-    __syncthreads();
+  // exclusive scan of the 1024 counts: inclusive within each wave by lane
+  // shuffles, then the 16 wave totals (scanned by wave 0) are added
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  int64_t incl = cnt;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int64_t v = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += v;
   }
-  int64_t pos = part[tid] - cnt;
-  if (tid == kScanThreads - 1) *total = part[tid];
+  if (lane == kWave - 1) part[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int64_t w = lane < kScanThreads / kWave ? part[lane] : 0, wi = w;
+#pragma unroll
+    for (int o = 1; o < kScanThreads / kWave; o <<= 1) {
+      const int64_t v = __shfl_up(wi, o, kWave);
+      if (lane >= o) wi += v;
+    }
+    if (lane < kScanThreads / kWave) part[kScanThreads / kWave + lane] = wi - w;  // exclusive wave offsets
+    if (lane == kScanThreads / kWave - 1) *total = wi;
+  }
+  __syncthreads();
+  int64_t pos = part[kScanThreads / kWave + wave] + incl - cnt;
   for (int64_t t = b; t < e; ++t) {
     if (keep[t] != 0) {
       dst[t] = static_cast<int32_t>(pos);
