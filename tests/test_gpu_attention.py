@@ -111,6 +111,28 @@ def test_batched_decode_items(device):
         check_summary(batch.outputs[i], batch.lses[i], segs[i], qs[i], what=f"item {i}")
 
 
+@pytest.mark.parametrize("bits", [2, 4])
+def test_batched_decode_many_units_ragged(device, bits):
+    # 9 items x 4 KV heads = 36 units: the launch deals a unit's splits to one
+    # XCD and interleaves their super-tiles (taken at >= 32 units); ragged
+    # lengths leave splits with fewer super-tiles or none, one item packs a
+    # single 32-token group and one has no residual
+    from unicache_amd.storage.decode import KiviDecodeBatch
+
+    lengths = (4500, 2048, 700, 3300, 1000, 6000, 513, 2600, 160)
+    caches, segs, qs = [], [], []
+    for i, tokens in enumerate(lengths):
+        residual = 0 if i == 1 else 128
+        c, s = _pair(tokens, 60 + i, bits, 32, residual, device)
+        caches.append(c)
+        segs.append(s)
+        qs.append(queries(1, seed=70 + i))
+    batch = KiviDecodeBatch(caches, [q.to(device) for q in qs])
+    batch.run()
+    for i in range(len(lengths)):
+        check_summary(batch.outputs[i], batch.lses[i], segs[i], qs[i], what=f"item {i} ({lengths[i]} tokens)")
+
+
 def test_decode_is_deterministic(device):
     cache, _ = _pair(4096, 11, 2, 32, 128, device)
     q = queries(1, seed=2).to(device)
