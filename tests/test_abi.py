@@ -69,8 +69,8 @@ def test_workspace_bytes():
     # AV: per (q head, row, split) D + 2 floats; splits = ceil(T/512) + 1
     assert nat.workspace_bytes(nat.UC_OP_KIVI_AV, 1, 28, 1, 128, 8192) == 28 * 1 * 17 * 130 * 4
     # MFMA decode (head_dim 128, 2-bit): per (item, KV head, split) 16x128 fp16 + 16x2 fp32;
-    # 8064 packed tokens in 1024-token splits (8) + 128 residual tokens (1 split)
-    # MFMA path: packed splits of 4 super-tiles x 2 waves x 256 tokens (2-bit), residual splits of 128
+    # MFMA path: packed splits of 8 super-tiles of 256 tokens (2-bit), residual splits of
+    # 2 waves x 128 tokens: 8064 packed tokens -> 4 splits, 128 residual tokens -> 1 split
     splits = -(-8064 // (4 * 2 * 256)) + 1
     assert nat.decode_workspace_bytes(2, 2, 32, 28, 4, 128, 1, 8064, 128) == 2 * 4 * splits * (16 * 128 * 2 + 16 * 2 * 4)
     # other shapes: generic split-K, per (item, q head, row, split) D + 2 floats

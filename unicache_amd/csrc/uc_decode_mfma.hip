@@ -45,7 +45,7 @@ using namespace mf;
 constexpr int kXcds = 8;  // XCDs of an MI355X; workgroup i of a launch runs on XCD i % 8
 constexpr int kWaves = 2;
 constexpr int kThreads = kWaves * kWave;
-constexpr int kResWaveTokens = 64;  // residual tokens per wave per residual split
+constexpr int kResWaveTokens = 128;  // residual tokens per wave per residual split
 
 template <int BITS, int G>
 struct DecShared {
