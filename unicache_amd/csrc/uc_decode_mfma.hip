@@ -72,12 +72,23 @@ struct MfmaParams {
   int64_t splits_packed, splits_total, nst;  // nst: super-tiles per packed split
   int64_t segs;                              // consecutive items that share one query and output
   int64_t units;                             // items x KV heads
+  int64_t super_tokens;                      // tokens per super-tile (16 key words)
   int xcd_grouped;                           // splits of a unit on one XCD (see the kernel)
   float scale_log2;
   _Float16 *ws_o;  // [items * Hkv * splits][16][128] normalised partial outputs
   float *ws_ml;    // [items * Hkv * splits][16][2] (max in log2 units, sum)
   int qd, rd, od;
 };
+
+// Whether split `split` of an item with tq packed and tr residual tokens has
+// work: residual splits come first, then packed splits of every S-th
+// super-tile.  Splits without work write no partial and the combine skips
+// them, so a segment table whose items differ in length launches cheap
+// empty splits only.
+__device__ __forceinline__ bool split_has_work(int64_t split, int64_t tq, int64_t tr, const MfmaParams &p) {
+  const int64_t splits_res = p.splits_total - p.splits_packed;
+  return split >= splits_res ? (split - splits_res) * p.super_tokens < tq : split * kWaves * kResWaveTokens < tr;
+}
 
 // Online-softmax state of one wave.  The output is accumulated transposed
 // (O^T = V^T P^T): lane (n, k) owns query column n, so every rescale is
@@ -628,6 +639,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int64_t item = TABLE ? u / p.Hkv : 0;
   const uc_kivi_item it = TABLE ? items[item] : single;
   const int64_t h = u % p.Hkv;
+  if (!split_has_work(split, it.quantized_tokens, it.residual_tokens, p)) return;  // uniform
 
   stage_queries(sq, it.query, h, p);
   WaveState st;
@@ -734,7 +746,15 @@ __global__ __launch_bounds__(kCombineThreads) void decode_mfma_combine(const uc_
   auto slot = [&](int f) {
     return ((first + f / p.splits_total) * p.Hkv + h) * p.splits_total + f % p.splits_total;
   };
-  auto ml_at = [&](int f) { return *reinterpret_cast<const float2 *>(p.ws_ml + (slot(f) * 16 + row) * 2); };
+  // splits without work wrote nothing: they count as (-inf, 0)
+  auto ml_at = [&](int f) {
+    const int64_t seg = first + f / p.splits_total;
+    const int64_t tq = TABLE ? items[seg].quantized_tokens : single.quantized_tokens;
+    const int64_t tr = TABLE ? items[seg].residual_tokens : single.residual_tokens;
+    return split_has_work(f % p.splits_total, tq, tr, p)
+               ? *reinterpret_cast<const float2 *>(p.ws_ml + (slot(f) * 16 + row) * 2)
+               : make_float2(kNegInf, 0.0f);
+  };
   // pass 1: this thread's slots, four loads in flight, then the row's 8 threads
   float M = kNegInf, L = 0.0f;
   for (int f0 = j; f0 < nflat; f0 += 4 * kCombineLanes) {
@@ -850,6 +870,7 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   const bool table = items_dev != nullptr;
   const uc_kivi_item one = single ? *single : uc_kivi_item{};
   p.units = n_items * Hkv;
+  p.super_tokens = 16 * (32 / bits);
   p.xcd_grouped = p.units >= 4 * kXcds;  // at most one unit of imbalance per XCD in four
   const dim3 grid(static_cast<unsigned>((p.xcd_grouped ? ceil_div(p.units, int64_t(kXcds)) * kXcds : p.units) *
                                         p.splits_total));
