@@ -367,7 +367,7 @@ int uc_compact_rows(const void *src, int64_t src_row_stride_bytes, int64_t row_b
  * Bytes of caller-provided workspace an operation needs.
  *   UC_OP_KIVI_AV:     (1, heads_q, query_len, head_dim, total_tokens)
  *   UC_OP_H2O_SCORES:  (1, heads_q, query_len, head_dim, tokens)
- *                      = max(8 Hq Lq, 2048 (B + 1024) + 4 T B),
+ *                      = max(8 Hq Lq, 2048 (B + 768) + 4 T B),
  *                      B = ceil(Hq Lq / 256) + Hq
  * Returns < 0 for an unknown op.
  */

@@ -76,11 +76,11 @@ def test_workspace_bytes():
     # other shapes: generic split-K, per (item, q head, row, split) D + 2 floats
     assert nat.decode_workspace_bytes(1, 2, 32, 28, 4, 64, 1, 1024, 0) == 28 * 2 * 66 * 4
     # MFMA score path: (max, sum) per (row block of 256, key chunk, row), at most
-    # (blocks + 1024) * 256 of them, then one fp32 partial per (row block, KV head,
+    # (blocks + 768) * 256 of them, then one fp32 partial per (row block, KV head,
     # key), with at most ceil(Hq * Lq / 256) + Hq row blocks; this also covers the
     # generic path's (max, sum) per (query head, row)
     blocks = -(-28 * 512 // 256) + 28
     assert nat.workspace_bytes(nat.UC_OP_H2O_SCORES, 1, 28, 512, 128, 4096) == (
-        (blocks + 1024) * 256 * 8 + blocks * 4096 * 4)
+        (blocks + 768) * 256 * 8 + blocks * 4096 * 4)
     with pytest.raises(ValueError):
         nat.workspace_bytes(99, 1, 1, 1, 1, 1)

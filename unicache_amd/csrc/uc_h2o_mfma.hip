@@ -50,7 +50,7 @@ constexpr int kHsRowsPerWave = 16 * kHsQB;
 constexpr int kHsRows = kHsWaves * kHsRowsPerWave;
 constexpr int kHsTile = 64;
 constexpr int64_t kHsMinChunk = 256;
-constexpr int64_t kHsTargetBlocks = 1024;
+constexpr int64_t kHsTargetBlocks = 768;  // one round: 3 workgroups (51 KB LDS) x 256 CUs
 
 struct HsParams {
   const uint16_t *q;
@@ -369,7 +369,9 @@ HsShape h2o_shape(int64_t heads_q, int64_t heads_kv, int64_t query_len, int64_t 
   HsShape s{};
   s.row_blocks = ceil_div((heads_q / heads_kv) * query_len, int64_t(kHsRows));
   const int64_t blocks = s.row_blocks * heads_kv;
-  const int64_t want = ceil_div(kHsTargetBlocks, blocks);
+  // at most one round of workgroups: a second, mostly empty round would cost
+  // as much as the first
+  const int64_t want = blocks < kHsTargetBlocks ? kHsTargetBlocks / blocks : 1;
   s.chunk = ceil_div(ceil_div(tokens, want), int64_t(kHsTile)) * kHsTile;
   if (s.chunk < kHsMinChunk) s.chunk = kHsMinChunk;
   s.chunks = ceil_div(tokens, s.chunk);
