@@ -82,9 +82,8 @@ struct MfmaParams {
 
 // Whether split `split` of an item with tq packed and tr residual tokens has
 // work: residual splits come first, then packed splits of every S-th
-// super-tile.  Splits without work write no partial and the combine skips
-// them, so a segment table whose items differ in length launches cheap
-// empty splits only.
+// super-tile.  Splits without work write only (max, sum) = (-inf, 0), so a
+// segment table whose items differ in length launches cheap empty splits.
 __device__ __forceinline__ bool split_has_work(int64_t split, int64_t tq, int64_t tr, const MfmaParams &p) {
   const int64_t splits_res = p.splits_total - p.splits_packed;
   return split >= splits_res ? (split - splits_res) * p.super_tokens < tq : split * kWaves * kResWaveTokens < tr;
@@ -639,7 +638,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int64_t item = TABLE ? u / p.Hkv : 0;
   const uc_kivi_item it = TABLE ? items[item] : single;
   const int64_t h = u % p.Hkv;
-  if (!split_has_work(split, it.quantized_tokens, it.residual_tokens, p)) return;  // uniform
+  if (!split_has_work(split, it.quantized_tokens, it.residual_tokens, p)) {  // uniform
+    // only the statistics: (-inf, 0) gives the split weight 0 in the combine,
+    // which then never reads its (unwritten) partial output
+    if (tid < 16) {
+      const int64_t slot = (item * p.Hkv + h) * p.splits_total + split;
+      reinterpret_cast<float2 *>(p.ws_ml)[slot * 16 + tid] = make_float2(kNegInf, 0.0f);
+    }
+    return;
+  }
 
   stage_queries(sq, it.query, h, p);
   WaveState st;
@@ -746,15 +753,8 @@ __global__ __launch_bounds__(kCombineThreads) void decode_mfma_combine(const uc_
   auto slot = [&](int f) {
     return ((first + f / p.splits_total) * p.Hkv + h) * p.splits_total + f % p.splits_total;
   };
-  // splits without work wrote nothing: they count as (-inf, 0)
-  auto ml_at = [&](int f) {
-    const int64_t seg = first + f / p.splits_total;
-    const int64_t tq = TABLE ? items[seg].quantized_tokens : single.quantized_tokens;
-    const int64_t tr = TABLE ? items[seg].residual_tokens : single.residual_tokens;
-    return split_has_work(f % p.splits_total, tq, tr, p)
-               ? *reinterpret_cast<const float2 *>(p.ws_ml + (slot(f) * 16 + row) * 2)
-               : make_float2(kNegInf, 0.0f);
-  };
+  // splits without work wrote (-inf, 0) and no output
+  auto ml_at = [&](int f) { return *reinterpret_cast<const float2 *>(p.ws_ml + (slot(f) * 16 + row) * 2); };
   // pass 1: this thread's slots, four loads in flight, then the row's 8 threads
   float M = kNegInf, L = 0.0f;
   for (int f0 = j; f0 < nflat; f0 += 4 * kCombineLanes) {
