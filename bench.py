@@ -292,6 +292,107 @@ def mixed_decode(device, steps, layers=LAYERS):
     }
 
 
+def _hbm_line(workload, ms, nbytes, **extra):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": workload, "ms": round(ms, 5), "bytes": int(nbytes), "gbs": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), **extra}
+
+
+def secondary_rows(device, steps):
+    """The remaining operators of the path, each at a configuration's shapes,
+    timed with HIP events on the current stream; bytes are the algorithmic
+    reads + writes (each tensor once)."""
+
+    from unicache_amd.adapters.bagel import merge_attention_summaries
+    from unicache_amd.operators.builtin import kivi_fake_quant_key, kivi_fake_quant_value
+    from unicache_amd.storage import GQAH2OCache, PackedKIVICache
+    from unicache_amd.storage.kivi_cuda import dequantize_kivi_chunk, packed_kivi_attention_parts
+    from unicache_amd.storage.physical import gqa_probability_value, gqa_query_key_logits
+
+    stream = torch.cuda.current_stream(device)
+    rows = {}
+
+    # fake quantization (operators/builtin.py:31-65): K over 32-token groups, V over
+    # 32-channel groups, bf16 in and out
+    for tokens, label in ((2048, "config 0"), (32768, "32k tokens")):
+        k, v = make_kv(tokens, seed=21000 + tokens, device=device)
+        ms = time_steps(lambda: (kivi_fake_quant_key(k, bits=BITS, group_size=GROUP),
+                                 kivi_fake_quant_value(v, bits=BITS, group_size=GROUP)), steps, 2, stream)
+        rows[f"fake_quant_{tokens}"] = _hbm_line(
+            f"{label}: kivi_fake_quant_key + kivi_fake_quant_value on [{tokens}, 4, 128] bf16, 2-bit, G=32",
+            ms, 2 * 2 * k.numel() * 2)
+
+    # chunked dequantization (kivi_cuda.py:58-93) of a 32k-token packed cache
+    tokens = 32768
+    k, v = make_kv(tokens, seed=22000, device=device)
+    cache = PackedKIVICache.from_dense(k, v, logical_token_ids=torch.arange(tokens, device=device), token_type_id=3,
+                                       k_bits=BITS, v_bits=BITS, group_size=GROUP, residual_length=RESIDUAL,
+                                       backend="cuda")
+    tq = cache.quantized_tokens
+    out_k = torch.empty(tq, HKV, D, dtype=torch.bfloat16, device=device)
+    out_v = torch.empty_like(out_k)
+    ms = time_steps(lambda: dequantize_kivi_chunk(cache, start=0, stop=tq, dtype=torch.bfloat16, output_key=out_k,
+                                                  output_value=out_v), steps, 2, stream)
+    rows["dequantize_chunk_32k"] = _hbm_line(
+        f"dequantize_kivi_chunk of {tq} packed 2-bit tokens into bf16 K/V workspaces (GQA 4 x 128)",
+        ms, tq * 384 + 2 * tq * HKV * D * 2)
+
+    # packed attention parts (kivi_cuda.py:238-329): logits then P.V at config 0
+    tokens = 2048
+    k, v = make_kv(tokens, seed=23000, device=device)
+    c0 = PackedKIVICache.from_dense(k, v, logical_token_ids=torch.arange(tokens, device=device), token_type_id=3,
+                                    k_bits=BITS, v_bits=BITS, group_size=GROUP, residual_length=RESIDUAL,
+                                    backend="cuda")
+    q1 = torch.randn(1, HQ, D, device=device).to(torch.bfloat16)
+
+    def parts():
+        logits, apply_value = packed_kivi_attention_parts(c0, q1)
+        return apply_value(torch.softmax(logits, -1))
+
+    ms = time_steps(parts, steps, 2, stream)
+    t_all = c0.quantized_tokens + c0.residual_tokens
+    rows["attention_parts_c0"] = _hbm_line(
+        f"config 0: packed_kivi_attention_parts ({c0.quantized_tokens} packed + {c0.residual_tokens} residual, "
+        "Lq=1) + torch softmax + the AV closure",
+        ms, 2 * (c0.quantized_tokens * 384 // 2 + c0.residual_tokens * 1024) + 2 * HQ * t_all * 4 * 2)
+
+    # GQA logits and P.V over dense keys (physical.py:20-63) at config 3's shapes
+    lq, tokens = 512, 4096
+    k, v = make_kv(tokens, seed=24000, device=device)
+    q = torch.randn(lq, HQ, D, device=device).to(torch.bfloat16)
+    ms = time_steps(lambda: gqa_query_key_logits(q, k), max(3, steps // 4), 1, stream)
+    rows["gqa_logits_c3"] = _hbm_line(
+        "config 3 shapes: gqa_query_key_logits, q [512, 28, 128] bf16 x k [4096, 4, 128] -> fp32 [28, 512, 4096]",
+        ms, q.numel() * 2 + k.numel() * 2 + HQ * lq * tokens * 4,
+        tflops=round(2 * lq * HQ * tokens * D / (ms * 1e-3) / 1e12, 1))
+    probs = torch.softmax(gqa_query_key_logits(q, k) / math.sqrt(D), -1).to(torch.bfloat16)
+    ms = time_steps(lambda: gqa_probability_value(probs, v), max(3, steps // 4), 1, stream)
+    rows["gqa_pv_c3"] = _hbm_line(
+        "config 3 shapes: gqa_probability_value, p [28, 512, 4096] bf16 x v [4096, 4, 128] -> [28, 512, 128]",
+        ms, probs.numel() * 2 + v.numel() * 2 + HQ * lq * D * 2,
+        tflops=round(2 * lq * HQ * tokens * D / (ms * 1e-3) / 1e12, 1))
+
+    # H2O score update from materialised probabilities (physical.py:598-610)
+    seg = GQAH2OCache.from_dense(k, v, logical_token_ids=torch.arange(tokens, device=device), token_type_id=1,
+                                 per_kv_head_scores=torch.rand(HKV, tokens, device=device), target_tokens=tokens,
+                                 recent_tokens=0, selection_frozen=True)
+    ms = time_steps(lambda: seg.update_scores(probs), steps, 2, stream)
+    rows["h2o_update_scores_c3"] = _hbm_line(
+        "config 3 shapes: GQAH2OCache.update_scores, bf16 probabilities [28, 512, 4096] summed per KV head",
+        ms, probs.numel() * 2 + 2 * HKV * tokens * 4)
+    del probs
+
+    # LSE merge of config 2's three segment summaries (adapters/bagel.py:57-72)
+    lq = 1088
+    summaries = [(torch.randn(lq, HQ, D, device=device).to(torch.bfloat16), torch.randn(HQ, lq, device=device))
+                 for _ in range(3)]
+    ms = time_steps(lambda: merge_attention_summaries(summaries), steps, 2, stream)
+    rows["lse_merge_c2"] = _hbm_line(
+        "config 2: merge_attention_summaries of 3 segment summaries ([1088, 28, 128] bf16 + LSE [28, 1088])",
+        ms, (3 + 1) * (lq * HQ * D * 2 + HQ * lq * 4))
+    return rows
+
+
 def cpu_baseline(algorithmic_bytes_per_seq_layer, budget_s=12.0):
     """The numpy oracle's decode (dequantize + fp64 attention) on one layer of
     the workload, sequences processed until ~budget_s of CPU time."""
@@ -412,6 +513,8 @@ def main():
     result["editing_c2"] = {f"{b}bit": editing_attention(device, max(3, args.steps // 5), bits=b) for b in (2, 4)}
     torch.cuda.empty_cache()
     result["h2o_c3"] = h2o_eviction(device, max(5, args.steps // 5))
+    torch.cuda.empty_cache()
+    result["rows"] = secondary_rows(device, max(5, args.steps // 5))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(seq_layer_bytes)
     print(json.dumps(result))

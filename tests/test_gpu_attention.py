@@ -170,6 +170,28 @@ def test_lse_merge(device):
     assert np.allclose(f32(out), eo, atol=1e-6) and np.allclose(f32(lse), el, atol=1e-6)
 
 
+def test_lse_merge_vector_and_row_kernels_agree(device):
+    # 16-byte aligned summaries take the vector kernel, 2-byte offset ones the
+    # per-row kernel: the same arithmetic, so equal bits; both match the oracle
+    torch.manual_seed(12)
+    lq, hq, d = 37, 28, 128
+    outs = [torch.randn(lq, hq, d).to(torch.bfloat16) for _ in range(3)]
+    lses = [torch.randn(hq, lq) * 4 for _ in range(3)]
+    lses[1][0, :5] = -math.inf  # rows where one segment is empty
+    a, la = merge_attention_summaries([(o.to(device), l.to(device)) for o, l in zip(outs, lses)])
+    shifted = []
+    for o in outs:
+        buf = torch.empty(o.numel() + 1, dtype=torch.bfloat16, device=device)
+        view = buf[1:].view(lq, hq, d)
+        view.copy_(o.to(device))
+        shifted.append(view)
+    b, lb = merge_attention_summaries([(o, l.to(device)) for o, l in zip(shifted, lses)])
+    assert torch.equal(a, b) and torch.equal(la, lb)
+    eo, el = A.merge_summaries([(f32(o), f32(l)) for o, l in zip(outs, lses)])
+    assert_close(f32(a), eo, what="merge")
+    assert np.allclose(f32(la), el, atol=1e-5)
+
+
 def test_summaries_merge_to_full_attention(device):
     # packed+residual summary merged with a dense bf16 segment equals attention over all keys
     cache, seg = _pair(1024, 12, 2, 32, 128, device)

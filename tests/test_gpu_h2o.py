@@ -186,6 +186,30 @@ def test_trim_update_and_budget(device):
     assert cache.request_budget(16, 4) == 8 and cache.budget_shortfall_tokens == 8
 
 
+def test_update_scores_row_and_element_kernels_agree(device):
+    # contiguous probabilities (a workgroup per 64 keys, one wave per query head)
+    # and a key-strided view (one thread per key) make the same additions
+    rng = np.random.default_rng(9)
+    key, value = kv_pair(200, heads=4, head_dim=32, seed=9)
+    probs = torch.from_numpy(rng.random((28, 37, 200)).astype(np.float32)).to(torch.bfloat16)
+    wide = torch.zeros(28, 37, 400, dtype=torch.bfloat16)
+    wide[:, :, ::2] = probs
+    init = torch.from_numpy(rng.random((4, 200)).astype(np.float32)).to(device)
+
+    def cache():
+        return GQAH2OCache.from_dense(key.to(device), value.to(device), logical_token_ids=torch.arange(200),
+                                      token_type_id=1, per_kv_head_scores=init.clone(), target_tokens=200,
+                                      recent_tokens=0)
+
+    a, b = cache(), cache()
+    before = a.cumulative_scores.cpu().numpy()
+    a.update_scores(probs.to(device))
+    b.update_scores(wide.to(device)[:, :, ::2])
+    assert torch.equal(a.cumulative_scores, b.cumulative_scores)
+    exp = before + H.scores_from_probs(f32(probs), 4)
+    assert np.allclose(a.cumulative_scores.cpu().numpy(), exp, rtol=1e-5)
+
+
 def test_h2o_attention_parts(device):
     import math
 

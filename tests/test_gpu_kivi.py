@@ -140,6 +140,40 @@ def test_fake_quant_bit_exact(device, bits):
     assert asymmetric_fake_quant(key.to(device), bits=16, dim=0, group_size=32) is not None
 
 
+@pytest.mark.parametrize("group,dtype,name", [(16, torch.float16, "fp16"), (64, torch.bfloat16, "bf16"),
+                                              (128, torch.bfloat16, "bf16"), (32, torch.float32, "fp32")])
+def test_fake_quant_groups_and_dtypes(device, group, dtype, name):
+    # token groups held in registers (16, 64), channel groups over 2 and 8 lanes,
+    # and the element-wise kernel (group 128, fp32 data); 300 tokens leave a
+    # partial last key group
+    key, value = kv_pair(300, seed=22, dtype=dtype)
+    for fn, dim in ((kivi_fake_quant_key, 0), (kivi_fake_quant_value, 2)):
+        src = key if dim == 0 else value
+        got = fn(src.to(device), bits=4, group_size=group)
+        exp = K.fake_quant(f32(src), bits=4, dim=dim, group_size=group, out_dtype=name)
+        assert got.dtype == dtype
+        assert np.array_equal(f32(got), exp), (group, dim)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_dequantize_long_chunks_and_fp16_stats(device, bits):
+    # whole-run and partial-run key words (start/stop inside words and runs),
+    # fp16 input with fp16 stats, output into a wider workspace
+    key, value = kv_pair(1024, seed=23, dtype=torch.float16)
+    cache = _cache(key, value, device, k_bits=bits, v_bits=bits, group_size=16, residual_length=0)
+    seg = K.from_dense(f32(key), f32(value), k_bits=bits, v_bits=bits, group_size=16, residual_length=0,
+                       in_dtype="fp16")
+    ek, ev = K.dequantize(seg, "fp16")
+    assert cache.quantized_tokens == 1024
+    for start, stop in ((0, 1024), (5, 1023), (64, 128), (17, 18), (300, 701)):
+        wk = torch.zeros((stop - start + 9, 4, 128), device=device, dtype=torch.float16)
+        wv = torch.zeros_like(wk)
+        dk, dv = dequantize_kivi_chunk(cache, start=start, stop=stop, dtype=torch.float16, output_key=wk,
+                                       output_value=wv, output_offset=9)
+        assert np.array_equal(f32(dk), ek[start:stop]) and np.array_equal(f32(dv), ev[start:stop]), (start, stop)
+        assert torch.all(wk[:9] == 0) and torch.all(wv[:9] == 0)
+
+
 def test_pack_is_deterministic(device):
     key, value = kv_pair(512, seed=2)
     a = _cache(key, value, device, k_bits=2, v_bits=2, group_size=32, residual_length=128)

@@ -192,6 +192,41 @@ __global__ __launch_bounds__(256) void colsum_kernel(ColsumArgs a) {
   a.out[idx] = a.accumulate ? a.out[idx] + total : total;
 }
 
+// Unit token stride: one workgroup per (KV head, 64 tokens), lane = token;
+// wave w sums the rows of query heads w, w + 8, ... in row order, sixteen
+// loads in flight, and wave 0 adds the heads in order -- the same additions
+// as colsum_kernel, so the same result.
+constexpr int kCsWaves = 8;
+constexpr int kCsMaxGroup = 64;
+
+template <int PD>
+__global__ __launch_bounds__(kCsWaves * kWave) void colsum_rows_kernel(ColsumArgs a) {
+  __shared__ float part[kCsMaxGroup][kWave];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int64_t tiles = (a.T + kWave - 1) / kWave;
+  const int64_t h = blockIdx.x / tiles, t = (blockIdx.x % tiles) * kWave + lane;
+  const int64_t tc = t < a.T ? t : a.T - 1;  // lanes past the end read the last column and store nothing
+  for (int64_t g = wave; g < a.group; g += kCsWaves) {
+    const int64_t base = (h * a.group + g) * a.p_sh + tc;
+    float s = 0.0f;
+    for (int64_t i0 = 0; i0 < a.Lq; i0 += 16) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = i0 + j < a.Lq ? load_as_f32<PD>(a.p, base + (i0 + j) * a.p_si) : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s += v[j];  // + 0 past the last row: s starts at +0, so it is never -0
+    }
+    part[g][lane] = s;
+  }
+  __syncthreads();
+  if (wave == 0 && t < a.T) {
+    float total = 0.0f;
+    for (int64_t g = 0; g < a.group; ++g) total += part[g][lane];
+    float *dst = a.out + h * a.T + t;
+    *dst = a.accumulate ? *dst + total : total;
+  }
+}
+
 // ------------------------------------------------------------------ select --
 constexpr int kSelThreads = 1024;
 
@@ -435,6 +470,13 @@ extern "C" int uc_h2o_colsum(const void *probs, int p_dtype, int64_t p_sh, int64
   a.Hq = heads_q; a.Lq = query_len; a.T = tokens; a.Hkv = heads_kv; a.group = heads_q / heads_kv;
   a.accumulate = accumulate; a.out = out;
   hipStream_t s = as_stream(stream);
+  if (p_st == 1 && a.group <= kCsMaxGroup) {
+    const int64_t blocks = heads_kv * ceil_div(tokens, int64_t(kWave));
+    UC_DISPATCH_DTYPE(p_dtype, PD, [&] {
+      hipLaunchKernelGGL((colsum_rows_kernel<PD>), dim3(blocks), dim3(kCsWaves * kWave), 0, s, a);
+    });
+    return check_launch("uc_h2o_colsum");
+  }
   UC_DISPATCH_DTYPE(p_dtype, PD, [&] {
     hipLaunchKernelGGL((colsum_kernel<PD>), dim3(ceil_div(heads_kv * tokens, 256)), dim3(256), 0, s, a);
   });

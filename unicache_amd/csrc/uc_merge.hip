@@ -44,6 +44,67 @@ __global__ __launch_bounds__(128) void lse_merge_kernel(MergeArgs a) {
   if (threadIdx.x == 0 && a.out_lse != nullptr) a.out_lse[hq * a.Lq + i] = total;
 }
 
+// Segment weights of one (query head, row): the lse and w of lse_merge_kernel.
+__device__ __forceinline__ float merge_weights(const MergeArgs &a, int64_t li, float (&w)[kMaxSegments]) {
+  float l[kMaxSegments];
+  float m = -__builtin_huge_valf();
+  for (int s = 0; s < a.n; ++s) {
+    l[s] = a.lses[s][li];
+    m = fmaxf(m, l[s]);
+  }
+  if (fabsf(m) == __builtin_huge_valf()) m = 0.0f;
+  float sum = 0.0f;
+  for (int s = 0; s < a.n; ++s) sum = add_rn(sum, expf(sub_rn(l[s], m)));
+  const float total = add_rn(logf(sum), m);
+  for (int s = 0; s < a.n; ++s) w[s] = expf(sub_rn(l[s], total));
+  return total;
+}
+
+// Rows as whole 16-byte chunks (8 half or 4 float channels per thread, chunks
+// of a row on neighbouring lanes); every thread of a row recomputes its
+// weights.  The same arithmetic per element as lse_merge_kernel.
+template <int OD>
+__global__ __launch_bounds__(256) void lse_merge_vec_kernel(MergeArgs a) {
+  constexpr int CH = OD == UC_FP32 ? 4 : 8;
+  const int64_t chunks = a.D / CH;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= a.Lq * a.Hq * chunks) return;
+  const int64_t c = idx % chunks, row = idx / chunks;  // row = i * Hq + hq (memory order of out)
+  const int64_t i = row / a.Hq, hq = row % a.Hq;
+  float w[kMaxSegments];
+  const float total = merge_weights(a, hq * a.Lq + i, w);
+  const int64_t off = row * a.D + c * CH;
+  float o[CH];
+#pragma unroll
+  for (int e = 0; e < CH; ++e) o[e] = 0.0f;
+  for (int s = 0; s < a.n; ++s) {
+    const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const char *>(a.outs[s]) +
+                                                      off * (OD == UC_FP32 ? 4 : 2));
+    const uint32_t r4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+      float x;
+      if constexpr (OD == UC_FP32) x = __uint_as_float(r4[e]);
+      else x = half_bits_to_f32<OD>(r4[e / 2] >> (16 * (e % 2)));
+      o[e] = add_rn(o[e], mul_rn(x, w[s]));
+    }
+  }
+  uint32_t r4[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if constexpr (OD == UC_FP32) {
+      r4[q] = __float_as_uint(o[q]);
+    } else {
+      const uint32_t lo = OD == UC_BF16 ? f32_to_bf16_bits(o[2 * q]) : f32_to_f16_bits(o[2 * q]);
+      const uint32_t hi = OD == UC_BF16 ? f32_to_bf16_bits(o[2 * q + 1]) : f32_to_f16_bits(o[2 * q + 1]);
+      r4[q] = lo | (hi << 16);
+    }
+  }
+  *reinterpret_cast<uint4 *>(static_cast<char *>(a.out) + off * (OD == UC_FP32 ? 4 : 2)) =
+      make_uint4(r4[0], r4[1], r4[2], r4[3]);
+  if (c == 0 && a.out_lse != nullptr) a.out_lse[hq * a.Lq + i] = total;
+}
+
 }  // namespace
 }  // namespace uc
 
@@ -66,6 +127,16 @@ extern "C" int uc_lse_merge(const void *const *outs, const float *const *lses, i
   }
   a.n = n_segments; a.Lq = query_len; a.Hq = heads_q; a.D = head_dim; a.out = out; a.out_lse = out_lse;
   hipStream_t s = as_stream(stream);
+  const int ch = out_dtype == UC_FP32 ? 4 : 8;
+  bool vec = head_dim % ch == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  for (int i = 0; i < n_segments; ++i) vec = vec && (reinterpret_cast<uintptr_t>(outs[i]) & 15) == 0;
+  if (vec) {
+    const int64_t n = query_len * heads_q * (head_dim / ch);
+    UC_DISPATCH_DTYPE(out_dtype, OD, [&] {
+      hipLaunchKernelGGL((lse_merge_vec_kernel<OD>), dim3(ceil_div(n, int64_t(256))), dim3(256), 0, s, a);
+    });
+    return check_launch("uc_lse_merge");
+  }
   UC_DISPATCH_DTYPE(out_dtype, OD, [&] {
     hipLaunchKernelGGL((lse_merge_kernel<OD>), dim3(heads_q * query_len), dim3(128), 0, s, a);
   });

@@ -327,6 +327,84 @@ __global__ __launch_bounds__(256) void kivi_dequant_kernel(DequantArgs a) {
   }
 }
 
+// Native 2/4-bit layout (words contiguous along tokens for keys, along
+// channels for values; unit channel stride in the output).  Same arithmetic
+// as kivi_dequant_kernel, laid out for whole-row stores.
+template <int OD>
+__device__ __forceinline__ void store_pair(void *out, int64_t off, float v0, float v1) {
+  if constexpr (OD == UC_FP32) {
+    *reinterpret_cast<float2 *>(static_cast<float *>(out) + off) = make_float2(v0, v1);
+  } else {
+    const uint32_t lo = OD == UC_BF16 ? f32_to_bf16_bits(v0) : f32_to_f16_bits(v0);
+    const uint32_t hi = OD == UC_BF16 ? f32_to_bf16_bits(v1) : f32_to_f16_bits(v1);
+    *reinterpret_cast<uint32_t *>(static_cast<uint16_t *>(out) + off) = lo | (hi << 16);
+  }
+}
+
+constexpr int kDqRunWords = 4;  // key words per lane and channel
+
+// Keys: lane = (head, run of 4 words, channel pair), channel pairs fastest, so
+// a wave writes whole 128-channel head rows for each token of its run.
+template <int BITS, int OD>
+__global__ __launch_bounds__(256) void dequant_key_native_kernel(DequantArgs a, int64_t runs) {
+  constexpr int TPW = 32 / BITS;
+  constexpr uint32_t kMask = (1u << BITS) - 1u;
+  const int64_t pairs = a.head_dim / 2;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= a.heads * runs * pairs) return;
+  const int64_t cp = idx % pairs, run = (idx / pairs) % runs, h = idx / (pairs * runs);
+  const int64_t c = 2 * cp, stop = a.start + a.count;
+  const int64_t w0 = a.start / TPW + run * kDqRunWords, w_end = (stop + TPW - 1) / TPW;
+  const uint32_t *kc = static_cast<const uint32_t *>(a.key_code) + h * a.kc_sh + c * a.kc_sd;
+  uint32_t wa[kDqRunWords], wb[kDqRunWords];
+#pragma unroll
+  for (int j = 0; j < kDqRunWords; ++j) {
+    const bool ok = w0 + j < w_end;
+    wa[j] = ok ? kc[w0 + j] : 0u;
+    wb[j] = ok ? kc[a.kc_sd + w0 + j] : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < kDqRunWords; ++j) {
+    const int64_t w = w0 + j;
+    if (w >= w_end) break;
+    // a word lies inside one group (TPW <= group_size)
+    const int64_t so = h * a.ks_sh + c * a.ks_sd + ((w * TPW) >> a.lg) * a.ks_sg;
+    const float s0 = load_dyn(a.key_scale, so, a.sd), m0 = load_dyn(a.key_min, so, a.sd);
+    const float s1 = load_dyn(a.key_scale, so + a.ks_sd, a.sd), m1 = load_dyn(a.key_min, so + a.ks_sd, a.sd);
+#pragma unroll
+    for (int p = 0; p < TPW; ++p) {
+      const int64_t t = w * TPW + p;
+      if (t < a.start || t >= stop) continue;
+      const float v0 = add_rn(mul_rn(float((wa[j] >> (p * BITS)) & kMask), s0), m0);
+      const float v1 = add_rn(mul_rn(float((wb[j] >> (p * BITS)) & kMask), s1), m1);
+      store_pair<OD>(a.out_key, (a.offset + t - a.start) * a.o_st + h * a.o_sh + c, v0, v1);
+    }
+  }
+}
+
+// Values: lane = (head, token, word), words fastest: one 4-byte word and its
+// group's stats in, 16 (2-bit) or 8 (4-bit) contiguous channels out.
+template <int BITS, int OD>
+__global__ __launch_bounds__(256) void dequant_value_native_kernel(DequantArgs a) {
+  constexpr int CPW = 32 / BITS;  // channels per word
+  constexpr uint32_t kMask = (1u << BITS) - 1u;
+  const int64_t words = a.head_dim / CPW;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= a.heads * a.count * words) return;
+  const int64_t w = idx % words, n = (idx / words) % a.count, h = idx / (words * a.count);
+  const int64_t t = a.start + n;
+  const uint32_t word = static_cast<const uint32_t *>(a.value_code)[h * a.vc_sh + t * a.vc_st + w];
+  const int64_t so = h * a.vs_sh + t * a.vs_st + ((w * CPW) >> a.lg) * a.vs_sg;
+  const float s = load_dyn(a.value_scale, so, a.sd), m = load_dyn(a.value_min, so, a.sd);
+  const int64_t o = (a.offset + n) * a.o_st + h * a.o_sh + w * CPW;
+#pragma unroll
+  for (int p = 0; p < CPW; p += 2) {
+    const float v0 = add_rn(mul_rn(float((word >> (p * BITS)) & kMask), s), m);
+    const float v1 = add_rn(mul_rn(float((word >> ((p + 1) * BITS)) & kMask), s), m);
+    store_pair<OD>(a.out_value, o + p, v0, v1);
+  }
+}
+
 // ----------------------------------------------------------- fake quant --
 struct FakeQuantArgs {
   const void *data;
@@ -374,6 +452,95 @@ __global__ __launch_bounds__(256) void fake_quant_kernel(FakeQuantArgs a) {
     const float code = fminf(fmaxf(rintf(div_rn(sub_rn(x, mn), scale)), 0.0f), a.max_code);
     store_from_f32<DT>(a.out, base + i * step, add_rn(mul_rn(code, scale), mn));
   }
+}
+
+// Groups along tokens, 16-bit data with unit channel stride: lane = (group,
+// head, channel pair), channel pairs fastest, the group's values held in
+// registers (one read, one write of every element).
+template <int DT, int GM>
+__global__ __launch_bounds__(256) void fake_quant_tokens_kernel(FakeQuantArgs a) {
+  const int64_t pairs = a.head_dim / 2, groups = (a.tokens + a.group - 1) / a.group;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= groups * a.heads * pairs) return;
+  const int64_t cp = idx % pairs, h = (idx / pairs) % a.heads, g = idx / (pairs * a.heads);
+  const int64_t t0 = g * a.group, n = min(a.group, a.tokens - t0);
+  const int64_t base = t0 * a.st + h * a.sh + 2 * cp;
+  float x0[GM], x1[GM];
+#pragma unroll
+  for (int i = 0; i < GM; ++i) {
+    const uint32_t pair = i < n ? *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(a.data) + base +
+                                                                       i * a.st)
+                                : 0u;
+    x0[i] = half_bits_to_f32<DT>(pair);
+    x1[i] = half_bits_to_f32<DT>(pair >> 16);
+  }
+  float mn0 = x0[0], mx0 = x0[0], mn1 = x1[0], mx1 = x1[0];
+#pragma unroll
+  for (int i = 1; i < GM; ++i) {
+    if (i < n) {
+      mn0 = fminf(mn0, x0[i]);
+      mx0 = fmaxf(mx0, x0[i]);
+      mn1 = fminf(mn1, x1[i]);
+      mx1 = fmaxf(mx1, x1[i]);
+    }
+  }
+  const float s0 = div_rn(fmaxf(sub_rn(mx0, mn0), kEps), a.max_code);
+  const float s1 = div_rn(fmaxf(sub_rn(mx1, mn1), kEps), a.max_code);
+#pragma unroll
+  for (int i = 0; i < GM; ++i) {
+    if (i < n) {
+      const float c0 = fminf(fmaxf(rintf(div_rn(sub_rn(x0[i], mn0), s0)), 0.0f), a.max_code);
+      const float c1 = fminf(fmaxf(rintf(div_rn(sub_rn(x1[i], mn1), s1)), 0.0f), a.max_code);
+      store_pair<DT>(a.out, base + i * a.st, add_rn(mul_rn(c0, s0), mn0), add_rn(mul_rn(c1, s1), mn1));
+    }
+  }
+}
+
+// Groups along channels (8 to 64 channels, dividing head_dim), 16-bit data
+// with unit channel stride: lane = 8 channels of one (token, head), a group
+// spans group/8 neighbouring lanes reduced with shuffles.
+template <int DT>
+__global__ __launch_bounds__(256) void fake_quant_channels_kernel(FakeQuantArgs a, int lanes_per_group) {
+  const int64_t chunks = a.head_dim / 8;
+  const int64_t total = a.tokens * a.heads * chunks;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool active = idx < total;  // whole groups are active or not: total is a multiple of the group lanes
+  const int64_t k = active ? idx : 0;
+  const int64_t ch = k % chunks, h = (k / chunks) % a.heads, t = k / (chunks * a.heads);
+  const int64_t off = t * a.st + h * a.sh + 8 * ch;
+  const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.data) + off);
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = half_bits_to_f32<DT>(w[j]);
+    x[2 * j + 1] = half_bits_to_f32<DT>(w[j] >> 16);
+  }
+  float mn = x[0], mx = x[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) {
+    mn = fminf(mn, x[j]);
+    mx = fmaxf(mx, x[j]);
+  }
+  for (int o = 1; o < lanes_per_group; o <<= 1) {
+    mn = fminf(mn, __shfl_xor(mn, o, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  }
+  if (!active) return;
+  const float s = div_rn(fmaxf(sub_rn(mx, mn), kEps), a.max_code);
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float c = fminf(fmaxf(rintf(div_rn(sub_rn(x[2 * j + e], mn), s)), 0.0f), a.max_code);
+      v[e] = add_rn(mul_rn(c, s), mn);
+    }
+    o[j] = DT == UC_BF16 ? (f32_to_bf16_bits(v[0]) | (uint32_t(f32_to_bf16_bits(v[1])) << 16))
+                         : (f32_to_f16_bits(v[0]) | (uint32_t(f32_to_f16_bits(v[1])) << 16));
+  }
+  *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.out) + off) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 }  // namespace
@@ -468,6 +635,35 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
   a.lg = group_size == 16 ? 4 : group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
   a.sd = stats_dtype; a.od = out_dtype;
   hipStream_t s = as_stream(stream);
+  // native 2/4-bit layout with pairwise-aligned unit-stride output rows
+  const int out_bytes = out_dtype == UC_FP32 ? 4 : 2;
+  const bool out_ok = o_sd == 1 && o_st % 2 == 0 && o_sh % 2 == 0 && head_dim % 32 == 0 &&
+                      (out_key == nullptr || aligned(out_key, 2 * out_bytes)) &&
+                      (out_value == nullptr || aligned(out_value, 2 * out_bytes));
+  const bool key_native = key_code != nullptr && (k_bits == 2 || k_bits == 4) && kc_sw == 1;
+  const bool value_native = value_code != nullptr && (v_bits == 2 || v_bits == 4) && vc_sw == 1;
+  if (out_ok && (key_code == nullptr || key_native) && (value_code == nullptr || value_native)) {
+    UC_DISPATCH_DTYPE(out_dtype, OD, [&] {
+      if (key_code != nullptr) {
+        const int tpw = 32 / k_bits;
+        const int64_t words = (start + count + tpw - 1) / tpw - start / tpw;
+        const int64_t runs = ceil_div(words, int64_t(kDqRunWords));
+        const int64_t n = heads * runs * (head_dim / 2);
+        if (k_bits == 2)
+          hipLaunchKernelGGL((dequant_key_native_kernel<2, OD>), dim3(ceil_div(n, 256)), dim3(256), 0, s, a, runs);
+        else
+          hipLaunchKernelGGL((dequant_key_native_kernel<4, OD>), dim3(ceil_div(n, 256)), dim3(256), 0, s, a, runs);
+      }
+      if (value_code != nullptr) {
+        const int64_t n = heads * count * (head_dim * v_bits / 32);
+        if (v_bits == 2)
+          hipLaunchKernelGGL((dequant_value_native_kernel<2, OD>), dim3(ceil_div(n, 256)), dim3(256), 0, s, a);
+        else
+          hipLaunchKernelGGL((dequant_value_native_kernel<4, OD>), dim3(ceil_div(n, 256)), dim3(256), 0, s, a);
+      }
+    });
+    return check_launch("uc_kivi_dequant");
+  }
   UC_DISPATCH_BITS(k_bits, KB, [&] {
     UC_DISPATCH_BITS(v_bits, VB, [&] {
       hipLaunchKernelGGL((kivi_dequant_kernel<KB, VB>), dim3(blocks), dim3(256), 0, s, a);
@@ -496,6 +692,34 @@ extern "C" int uc_kivi_fake_quant(const void *data, int64_t st, int64_t sh, int6
   const int64_t fixed = dim == 0 ? heads * head_dim : tokens * heads;
   const int64_t blocks = ceil_div(fixed * groups, 256);
   hipStream_t s = as_stream(stream);
+  const bool half = dtype == UC_BF16 || dtype == UC_FP16;
+  if (half && dim == 0 && sd == 1 && head_dim % 2 == 0 && st % 2 == 0 && sh % 2 == 0 && aligned(data, 4) &&
+      aligned(out, 4) && a.group <= 64) {
+    const int64_t n = groups * heads * (head_dim / 2);
+    const dim3 grid(static_cast<unsigned>(ceil_div(n, 256)));
+    UC_DISPATCH_DTYPE(dtype, DT, [&] {
+      if constexpr (DT != UC_FP32) {
+        if (a.group <= 16)
+          hipLaunchKernelGGL((fake_quant_tokens_kernel<DT, 16>), grid, dim3(256), 0, s, a);
+        else if (a.group <= 32)
+          hipLaunchKernelGGL((fake_quant_tokens_kernel<DT, 32>), grid, dim3(256), 0, s, a);
+        else
+          hipLaunchKernelGGL((fake_quant_tokens_kernel<DT, 64>), grid, dim3(256), 0, s, a);
+      }
+    });
+    return check_launch("uc_kivi_fake_quant");
+  }
+  const int64_t lanes = a.group / 8;
+  if (half && dim == 2 && sd == 1 && a.group % 8 == 0 && (lanes == 1 || lanes == 2 || lanes == 4 || lanes == 8) &&
+      head_dim % a.group == 0 && st % 8 == 0 && sh % 8 == 0 && aligned(data, 16) && aligned(out, 16)) {
+    const int64_t n = tokens * heads * (head_dim / 8);
+    const dim3 grid(static_cast<unsigned>(ceil_div(n, 256)));
+    UC_DISPATCH_DTYPE(dtype, DT, [&] {
+      if constexpr (DT != UC_FP32)
+        hipLaunchKernelGGL((fake_quant_channels_kernel<DT>), grid, dim3(256), 0, s, a, static_cast<int>(lanes));
+    });
+    return check_launch("uc_kivi_fake_quant");
+  }
   UC_DISPATCH_DTYPE(dtype, DT, [&] {
     hipLaunchKernelGGL((fake_quant_kernel<DT>), dim3(blocks), dim3(256), 0, s, a);
   });
