@@ -152,6 +152,19 @@ def test_gqa_helpers(device):
     assert_close(f32(pv), A.gqa_pv(f32(p), f32(value)), what="pv")
 
 
+@pytest.mark.parametrize("lq,tokens,dtype", [(100, 300, torch.bfloat16), (70, 1000, torch.float16)])
+def test_gqa_logits_mfma_tiles(device, lq, tokens, dtype):
+    # >= 64 query rows per KV head take the MFMA logits kernel: ragged row
+    # blocks and key chunks; fp32 accumulation of up to ~100-sized products
+    key, _ = kv_pair(tokens, seed=31, dtype=dtype)
+    q = queries(lq, seed=32, dtype=dtype)
+    got = gqa_query_key_logits(q.to(device), key.to(device))
+    assert_close(f32(got), A.gqa_logits(f32(q), f32(key)), max_abs=2e-3, mean_abs=1e-4, what="qk mfma")
+    # head-major storage read through strides (the H2O segment layout): same tiles, same bits
+    kh = key.transpose(0, 1).contiguous().to(device).transpose(0, 1)
+    assert torch.equal(gqa_query_key_logits(q.to(device), kh), got)
+
+
 def test_lse_merge(device):
     # test_physical.py:181-202 on the GPU kernel
     torch.manual_seed(11)

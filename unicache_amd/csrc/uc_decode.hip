@@ -8,6 +8,14 @@
 #include "uc_decode.h"
 
 namespace uc {
+
+bool h2o_mfma_supported(int dtype, int64_t head_dim, const void *q, int64_t q_si, int64_t q_sh, int64_t q_sd,
+                        const void *k, int64_t k_st, int64_t k_sh, int64_t k_sd, int64_t query_len, int64_t heads_q,
+                        int64_t tokens, int64_t heads_kv);
+int launch_qk_logits_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const void *k, int64_t k_st,
+                          int64_t k_sh, int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, float scale, float *logits,
+                          hipStream_t stream);
+
 namespace {
 
 constexpr int kRows = 16;     // query rows per workgroup
@@ -510,6 +518,13 @@ extern "C" int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int
   UC_REQUIRE(quantized_tokens % group_size == 0 && residual_tokens >= 0, "uc_kivi_qk: bad token counts");
   const int64_t total = quantized_tokens + residual_tokens;
   if (total == 0 || query_len == 0) return UC_OK;
+  // dense keys and at least one wave of query rows per KV head: MFMA tiles
+  const int64_t rows = heads_q / heads_kv * query_len;
+  if (quantized_tokens == 0 && q_dtype == res_dtype && rows >= kWave &&
+      h2o_mfma_supported(q_dtype, head_dim, query, heads_q * head_dim, head_dim, 1, residual_key, r_st, r_sh, 1,
+                         query_len, heads_q, residual_tokens, heads_kv))
+    return launch_qk_logits_mfma(q_dtype, query, heads_q * head_dim, head_dim, residual_key, r_st, r_sh, query_len,
+                                 heads_q, residual_tokens, heads_kv, sm_scale, logits, as_stream(stream));
   PackedView v = parts_view(key_code, key_scale, key_min, nullptr, nullptr, nullptr, quantized_tokens, bits,
                             group_size, residual_key, nullptr, residual_tokens, r_st, r_sh, heads_kv, head_dim,
                             stats_dtype, res_dtype);

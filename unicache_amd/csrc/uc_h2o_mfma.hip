@@ -64,6 +64,8 @@ struct HsParams {
   float2 *ml;          // [Hkv][row_blocks][chunks][kHsRows]: (max * log2 e units, sum)
   float *partial;      // [row_blocks][Hkv][T]
   const float *lse;    // optional [Hq][Lq] natural-log normaliser given by the caller
+  float *logits;       // qk_logits_kernel: [Hq][Lq][T] = scale * q . k
+  float scale;
 };
 
 // Workgroups are dealt to the 8 XCDs round-robin by launch index.  Work item
@@ -343,6 +345,60 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
   }
 }
 
+// Logits of dense keys: the S = Q K^T tiles of h2o_scores_kernel written out
+// as scale * S, fp32 [Hq][Lq][T] (physical.py:20-39).  Each store of a
+// (query block, v) covers 16 consecutive keys of four rows.
+template <int DT>
+__global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3))) void qk_logits_kernel(HsParams p) {
+  __shared__ __align__(16) HsShared sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, kap = lane >> 4;
+  const HsItem it = hs_item(p);
+  if (!it.valid) return;
+  const int64_t rb = it.rb, c = it.c, h = it.h;
+  const int64_t t_begin = c * p.chunk, t_end = min(p.T, t_begin + p.chunk);
+  const int64_t row0 = rb * kHsRows + wave * kHsRowsPerWave;
+
+  typename HsOp<DT>::V qf[kHsQB][4];
+  load_queries<DT>(qf, p, h, row0);
+  // start of the logits row of rows 16*qb + 4*kap + v (the rows lane (n, k)
+  // holds in S); -1 past the last row
+  int64_t ro[kHsQB][4];
+#pragma unroll
+  for (int qb = 0; qb < kHsQB; ++qb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t row = row0 + 16 * qb + 4 * kap + v;
+      const int64_t g = row / p.Lq, i = row % p.Lq;
+      ro[qb][v] = row < p.rows ? ((h * p.group + g) * p.Lq + i) * p.T : -1;
+    }
+  const KeyStream ks(p, h, t_begin, t_end);
+  ks.prologue(sh);
+  for (int i = 0; i < ks.n_tiles; ++i) {
+    ks.acquire(sh, i);
+    const int64_t t0 = t_begin + int64_t(i) * kHsTile;
+    const uint4 *kt = sh.kt[i % kHsStages];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      typename HsOp<DT>::V kf[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) kf[kb] = key_frag<DT>(kt, 16 * tb + r, 4 * kb + kap);
+      const int64_t t = t0 + 16 * tb + r;
+#pragma unroll
+      for (int qb = 0; qb < kHsQB; ++qb) {
+        f4 s = f4{0, 0, 0, 0};  // lane (n, k): rows 16*qb + 4k + v, key 16*tb + n
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) s = HsOp<DT>::mma(qf[qb][kb], kf[kb], s);
+        if (t < t_end) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (ro[qb][v] >= 0) p.logits[ro[qb][v] + t] = s[v] * p.scale;
+        }
+      }
+    }
+  }
+}
+
 // scores[h, t] (+)= sum over row blocks, in order, of the partials.
 __global__ __launch_bounds__(64) void h2o_reduce_kernel(const float *partial, int64_t row_blocks, int64_t Hkv,
                                                         int64_t T, float *scores, int accumulate) {
@@ -405,6 +461,30 @@ bool h2o_mfma_supported(int dtype, int64_t head_dim, const void *q, int64_t q_si
 int64_t h2o_mfma_workspace_bytes(int64_t heads_q, int64_t query_len, int64_t tokens) {
   const int64_t rbb = row_block_bound(heads_q, query_len);
   return (rbb + kHsTargetBlocks) * kHsRows * int64_t(sizeof(float2)) + rbb * tokens * int64_t(sizeof(float));
+}
+
+int launch_qk_logits_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const void *k, int64_t k_st,
+                          int64_t k_sh, int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, float scale, float *logits,
+                          hipStream_t stream) {
+  const HsShape shape = h2o_shape(Hq, Hkv, Lq, T);
+  UC_REQUIRE(shape.row_blocks * shape.chunks * Hkv < (int64_t(1) << 31), "uc_kivi_qk: grid too large");
+  HsParams p{};
+  p.q = static_cast<const uint16_t *>(q);
+  p.q_si = q_si; p.q_sh = q_sh;
+  p.k = static_cast<const uint16_t *>(k);
+  p.k_st = k_st; p.k_sh = k_sh;
+  p.Lq = Lq; p.Hq = Hq; p.Hkv = Hkv; p.group = Hq / Hkv; p.rows = p.group * Lq; p.T = T;
+  p.row_blocks = shape.row_blocks; p.chunks = shape.chunks; p.chunk = shape.chunk;
+  p.logits = logits;
+  p.scale = scale;
+  p.items = p.row_blocks * p.chunks * Hkv;
+  p.per_xcd = ceil_div(p.items, int64_t(kXcds));
+  const dim3 grid(static_cast<unsigned>(p.per_xcd * kXcds));
+  if (dtype == UC_FP16)
+    hipLaunchKernelGGL((qk_logits_kernel<UC_FP16>), grid, dim3(kHsThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((qk_logits_kernel<UC_BF16>), grid, dim3(kHsThreads), 0, stream, p);
+  return check_launch("uc_kivi_qk (MFMA logits)");
 }
 
 int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const void *k, int64_t k_st, int64_t k_sh,
