@@ -165,6 +165,24 @@ def test_gqa_logits_mfma_tiles(device, lq, tokens, dtype):
     assert torch.equal(gqa_query_key_logits(q.to(device), kh), got)
 
 
+@pytest.mark.parametrize("pdtype,vdtype", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.bfloat16),
+                                           (torch.float32, torch.float16)])
+def test_gqa_pv_mfma_tiles(device, pdtype, vdtype):
+    # >= 64 query rows per KV head take the MFMA P.V kernel, P cast to the value
+    # dtype first (physical.py:59); 301 keys end inside a 64-key tile and inside an
+    # 8-key run, and the row padding past them holds NaN that must not leak in
+    lq, t = 100, 301
+    _, value = kv_pair(t, seed=33, dtype=vdtype)
+    g = torch.Generator().manual_seed(34)
+    probs = torch.softmax(torch.randn(28, lq, t, generator=g) * 3, -1)
+    wide = torch.full((28, lq, 304), float("nan"))
+    wide[..., :t] = probs
+    got = gqa_probability_value(wide.to(pdtype).to(device)[..., :t], value.to(device))
+    assert got.dtype == vdtype
+    exp = A.gqa_pv(f32(probs.to(pdtype).to(vdtype)), f32(value))
+    assert_close(f32(got), exp, max_abs=1e-2, mean_abs=1e-3, what="pv mfma")
+
+
 def test_lse_merge(device):
     # test_physical.py:181-202 on the GPU kernel
     torch.manual_seed(11)

@@ -43,8 +43,11 @@ extern "C" int64_t uc_workspace_bytes(int op, int64_t n_items, int64_t heads_q, 
   switch (op) {
     case UC_OP_KIVI_AV: {
       int64_t splits = uc::decode_num_splits(max_tokens);
-      // per (item, query head, query row, split): D partial outputs + (max, sum)
-      return n_items * heads_q * query_len * splits * (head_dim + 2) * int64_t(sizeof(float));
+      // per (item, query head, query row, split): D partial outputs + (max, sum);
+      // dense MFMA path: V transposed, [KV heads <= query heads][D][tokens rounded up to 64] 16-bit
+      const int64_t partials = n_items * heads_q * query_len * splits * (head_dim + 2) * int64_t(sizeof(float));
+      const int64_t staged = n_items * heads_q * head_dim * uc::ceil_div(max_tokens, int64_t(64)) * 64 * 2;
+      return partials > staged ? partials : staged;
     }
     case UC_OP_H2O_SCORES: {
       // generic path: per (query head, row) the softmax max and sum; MFMA path:

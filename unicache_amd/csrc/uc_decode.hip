@@ -15,6 +15,12 @@ bool h2o_mfma_supported(int dtype, int64_t head_dim, const void *q, int64_t q_si
 int launch_qk_logits_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const void *k, int64_t k_st,
                           int64_t k_sh, int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, float scale, float *logits,
                           hipStream_t stream);
+bool pv_mfma_supported(int p_dtype, const void *probs, int64_t p_sh, int64_t p_si, int64_t p_st, int v_dtype,
+                       const void *v, int64_t v_st, int64_t v_sh, int64_t head_dim, int64_t Lq, int64_t rows,
+                       int64_t T);
+int launch_pv_mfma(int p_dtype, const void *probs, int64_t p_sh, int64_t p_si, int v_dtype, const void *v,
+                   int64_t v_st, int64_t v_sh, int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, void *out,
+                   void *workspace, hipStream_t stream);
 
 namespace {
 
@@ -569,6 +575,13 @@ extern "C" int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t 
     return UC_OK;
   }
   UC_REQUIRE(workspace != nullptr, "uc_kivi_av: workspace is NULL");
+  // dense values and at least one workgroup of query rows per KV head: MFMA
+  // tiles with V staged transposed in the workspace
+  if (quantized_tokens == 0 && out_dtype == res_dtype &&
+      pv_mfma_supported(p_dtype, probs, p_sh, p_si, p_st, res_dtype, residual_value, r_st, r_sh, head_dim, query_len,
+                        heads_q / heads_kv * query_len, total))
+    return launch_pv_mfma(p_dtype, probs, p_sh, p_si, res_dtype, residual_value, r_st, r_sh, query_len, heads_q, total,
+                          heads_kv, out, workspace, s);
   (void)total;
   uc_kivi_item it{};
   it.value_code = value_code; it.value_scale = value_scale; it.value_min = value_min;

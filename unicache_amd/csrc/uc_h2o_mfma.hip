@@ -20,6 +20,8 @@
 #include "uc_common.h"
 #include "uc_mfma.h"
 
+#include <type_traits>
+
 namespace uc {
 namespace {
 
@@ -399,6 +401,225 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
   }
 }
 
+// ------------------------------------------------------------ dense P.V --
+// out[hq, i, :] = P[hq, i, :] . V[:, h, :] with P cast to the value dtype
+// first (physical.py:42-63), fp32 accumulation.  pv_stage_kernel writes V
+// transposed, [Hkv][128][Tp] (Tp = T rounded up to 64, zero tail); in
+// pv_mfma_kernel a workgroup owns 64 query rows of one KV head (a 16-row block
+// per wave), streams 64-key tiles of V^T through an LDS ring and reads the
+// P^T fragments straight from global memory:
+//   O^T[16 channels x 16 rows] += V^T[16 x 32 keys] . P^T[32 keys x 16 rows].
+constexpr int kPvWaves = 4;
+constexpr int kPvThreads = kPvWaves * kWave;
+constexpr int kPvRows = 16 * kPvWaves;
+constexpr int kPvTile = 64;
+constexpr int kPvStages = 4;
+
+template <int VD>
+struct PvOp;
+template <>
+struct PvOp<UC_BF16> {
+  using V = bf8;
+  static __device__ __forceinline__ f4 mma(V a, V b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+  static __device__ __forceinline__ uint16_t bits(float x) { return f32_to_bf16_bits(x); }
+};
+template <>
+struct PvOp<UC_FP16> {
+  using V = h8;
+  static __device__ __forceinline__ f4 mma(V a, V b, f4 c) { return mfma32(a, b, c); }
+  static __device__ __forceinline__ uint16_t bits(float x) { return f32_to_f16_bits(x); }
+};
+
+// One 64-key tile of V for one KV head, transposed through LDS.
+__global__ __launch_bounds__(256) void pv_stage_kernel(const uint16_t *v, int64_t v_st, int64_t v_sh, int64_t T,
+                                                       int64_t Tp, uint16_t *vt) {
+  __shared__ uint16_t tile[kPvTile][kD + 8];
+  const int tid = threadIdx.x;
+  const int64_t h = blockIdx.y, t0 = int64_t(blockIdx.x) * kPvTile;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // 64 keys x 16 chunks of 8 channels
+    const int c = j * 256 + tid, key = c / 16, c8 = c % 16;
+    const uint4 x = t0 + key < T ? *reinterpret_cast<const uint4 *>(v + (t0 + key) * v_st + h * v_sh + 8 * c8)
+                                 : make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4 *>(&tile[key][8 * c8]) = x;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // 128 channels x 8 chunks of 8 keys
+    const int c = j * 256 + tid, ch = c / 8, k8 = c % 8;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = tile[8 * k8 + 2 * e][ch] | (uint32_t(tile[8 * k8 + 2 * e + 1][ch]) << 16);
+    *reinterpret_cast<uint4 *>(vt + (h * kD + ch) * Tp + t0 + 8 * k8) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+struct PvParams {
+  const void *p;
+  int64_t p_sh, p_si;  // element strides of query heads and rows (keys are unit stride)
+  const uint16_t *vt;  // [Hkv][128][Tp]
+  int64_t T, Tp, Lq, Hq, Hkv, group, rows;
+  int64_t row_blocks, items, per_xcd;
+  void *out;  // [Hq][Lq][128], value dtype
+};
+
+// V^T slot: channel row c (128 B = 8 chunks of 8 keys) keeps chunk q at
+// position q ^ (c & 7), so the 16 rows of a fragment read hit 8 bank groups twice.
+struct PvShared {
+  uint4 vt[kPvStages][kD * 8];
+};
+
+// Raw P bytes of one lane's eight keys: one 16-byte load for 16-bit P, two for fp32.
+template <int PD>
+struct PRaw {
+  static constexpr int N = PD == UC_FP32 ? 2 : 1;
+  uint4 x[N];
+};
+
+// P^T fragment in the value dtype (the cast of physical.py:59); keys at or past
+// T are zero.
+template <int PD, int VD>
+__device__ __forceinline__ typename PvOp<VD>::V p_frag(const PRaw<PD> &raw, int64_t t, int64_t T) {
+  uint32_t w[4];
+  if constexpr (PD == VD) {
+    w[0] = raw.x[0].x, w[1] = raw.x[0].y, w[2] = raw.x[0].z, w[3] = raw.x[0].w;
+    if (t + 8 > T) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (t + 2 * e >= T) w[e] &= 0xffff0000u;
+        if (t + 2 * e + 1 >= T) w[e] &= 0x0000ffffu;
+      }
+    }
+  } else {
+    float x[8];
+    if constexpr (PD == UC_FP32) {
+      const uint32_t u[8] = {raw.x[0].x, raw.x[0].y, raw.x[0].z, raw.x[0].w,
+                             raw.x[1].x, raw.x[1].y, raw.x[1].z, raw.x[1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = __uint_as_float(u[e]);
+    } else {
+      const uint32_t u[4] = {raw.x[0].x, raw.x[0].y, raw.x[0].z, raw.x[0].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = half_bits_to_f32<PD>(u[e / 2] >> (16 * (e % 2)));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (t + e >= T) x[e] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = uint32_t(PvOp<VD>::bits(x[2 * e])) | (uint32_t(PvOp<VD>::bits(x[2 * e + 1])) << 16);
+  }
+  return __builtin_bit_cast(typename PvOp<VD>::V, make_uint4(w[0], w[1], w[2], w[3]));
+}
+
+// s_waitcnt immediate (gfx9 layout): vmcnt <= n, expcnt and lgkmcnt not waited on
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+template <int PD, int VD>
+__global__ __launch_bounds__(kPvThreads) void pv_mfma_kernel(PvParams p) {
+  __shared__ __align__(16) PvShared sh;
+  constexpr int kAhead = kPvStages - 1;            // tiles in flight
+  constexpr int kEl = PD == UC_FP32 ? 4 : 2;       // bytes per probability
+  constexpr int kOps = 2 * PRaw<PD>::N + 4;        // memory ops per tile and thread: P halves + V^T slots
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, kap = lane >> 4;
+  const int64_t id = blockIdx.x, w = (id % kXcds) * p.per_xcd + id / kXcds;
+  if (w >= p.items) return;  // uniform: the whole workgroup leaves
+  const int64_t h = w / p.row_blocks, rb = w % p.row_blocks;
+  // the wave's 16 rows are consecutive rows of P (contiguous [query head][row]):
+  // a buffer resource over them reads zero past the last row
+  const int64_t row0w = rb * kPvRows + wave * 16;
+  const int64_t nrows = max<int64_t>(0, min<int64_t>(16, p.rows - row0w));
+  const Rsrc rp = make_rsrc(static_cast<const char *>(p.p) + (h * p.group * p.Lq + row0w) * p.p_si * kEl,
+                            nrows * p.p_si * kEl);
+  const uint32_t p_lane = static_cast<uint32_t>((r * p.p_si + 8 * kap) * kEl);
+  const Rsrc rs = make_rsrc(p.vt + h * kD * p.Tp, kD * p.Tp * 2);
+  const int n_tiles = static_cast<int>(p.Tp / kPvTile);
+
+  auto load_p = [&](PRaw<PD> (&dst)[2], int tile) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < PRaw<PD>::N; ++j)
+        dst[ks].x[j] = bload128(rp, p_lane + static_cast<uint32_t>((tile * kPvTile + 32 * ks) * kEl + 16 * j));
+  };
+  auto issue_vt = [&](int tile) {
+    uint4 *slot = sh.vt[tile % kPvStages];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int s4 = q * kPvThreads + tid, ch = s4 / 8, pos = s4 % 8, chunk = pos ^ (ch & 7);
+      const uint32_t off = static_cast<uint32_t>((ch * p.Tp + int64_t(tile) * kPvTile) * 2 + chunk * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void *)(slot + q * kPvThreads + wave * kWave), 16, off, 0, 0, 0);
+    }
+  };
+
+  PRaw<PD> pb[kAhead][2];  // P of the tiles in flight, oldest first
+#pragma unroll
+  for (int t = 0; t < kAhead; ++t) {
+    if (t < n_tiles) {
+      load_p(pb[t], t);
+      issue_vt(t);
+    }
+  }
+  f4 o[8];
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) o[cb] = f4{0, 0, 0, 0};
+  for (int it = 0; it < n_tiles; ++it) {
+    // tile it has landed once at most (later tiles issued) x kOps ops remain
+    const int later = min(n_tiles - 1, it + kAhead - 1) - it;
+    if (later >= 2)
+      wait_vm<2 * kOps>();
+    else if (later == 1)
+      wait_vm<kOps>();
+    else
+      wait_vm<0>();
+    __syncthreads();
+    PRaw<PD> nb[2];
+    const bool more = it + kAhead < n_tiles;  // the slot it refills was last read in tile it - 1
+    if (more) {
+      load_p(nb, it + kAhead);
+      issue_vt(it + kAhead);
+    }
+    const int64_t t0 = int64_t(it) * kPvTile;
+    const uint4 *vt = sh.vt[it % kPvStages];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const auto b = p_frag<PD, VD>(pb[0][ks], t0 + 32 * ks + 8 * kap, p.T);
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) {
+        const int ch = 16 * cb + r, q = 4 * ks + kap;
+        o[cb] = PvOp<VD>::mma(__builtin_bit_cast(typename PvOp<VD>::V, vt[ch * 8 + (q ^ (ch & 7))]), b, o[cb]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t + 1 < kAhead; ++t) pb[t][0] = pb[t + 1][0], pb[t][1] = pb[t + 1][1];
+    if (more) pb[kAhead - 1][0] = nb[0], pb[kAhead - 1][1] = nb[1];
+  }
+  __syncthreads();  // the ring is free: stage the output rows
+  uint16_t *ob = reinterpret_cast<uint16_t *>(&sh.vt[0][0]);  // [64 rows][136]
+  constexpr int kRowPad = kD + 8;
+  static_assert(sizeof(uint16_t) * kPvRows * kRowPad <= sizeof(PvShared), "output staging fits the ring");
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) ob[(wave * 16 + r) * kRowPad + 16 * cb + 4 * kap + v] = PvOp<VD>::bits(o[cb][v]);
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kPvRows * (kD / 8) / kPvThreads; ++q) {  // 16-byte chunks of whole rows
+    const int c = q * kPvThreads + tid, rr = c / (kD / 8), c8 = c % (kD / 8);
+    const int64_t orow = rb * kPvRows + rr;
+    if (orow >= p.rows) continue;
+    const int64_t og = orow / p.Lq, oi = orow % p.Lq;
+    *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(p.out) + ((h * p.group + og) * p.Lq + oi) * kD + 8 * c8) =
+        *reinterpret_cast<const uint4 *>(&ob[rr * kRowPad + 8 * c8]);
+  }
+}
+
 // scores[h, t] (+)= sum over row blocks, in order, of the partials.
 __global__ __launch_bounds__(64) void h2o_reduce_kernel(const float *partial, int64_t row_blocks, int64_t Hkv,
                                                         int64_t T, float *scores, int accumulate) {
@@ -485,6 +706,52 @@ int launch_qk_logits_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, 
   else
     hipLaunchKernelGGL((qk_logits_kernel<UC_BF16>), grid, dim3(kHsThreads), 0, stream, p);
   return check_launch("uc_kivi_qk (MFMA logits)");
+}
+
+// Dense P.V on MFMA: 16-bit values with unit channel stride and 8-element
+// aligned token/head strides; probabilities with unit key stride whose rows
+// of consecutive query heads follow each other ([Hq][Lq][>= T]).
+bool pv_mfma_supported(int p_dtype, const void *probs, int64_t p_sh, int64_t p_si, int64_t p_st, int v_dtype,
+                       const void *v, int64_t v_st, int64_t v_sh, int64_t head_dim, int64_t Lq, int64_t rows,
+                       int64_t T) {
+  const bool aligned = (reinterpret_cast<uintptr_t>(probs) & 15) == 0 && (reinterpret_cast<uintptr_t>(v) & 15) == 0 &&
+                       p_sh % 8 == 0 && p_si % 8 == 0 && v_st % 8 == 0 && v_sh % 8 == 0;
+  const int64_t el = p_dtype == UC_FP32 ? 4 : 2;
+  return (v_dtype == UC_BF16 || v_dtype == UC_FP16) && head_dim == kD && p_st == 1 && aligned && rows >= kPvRows &&
+         kD * ceil_div(T, int64_t(kPvTile)) * kPvTile * 2 < (int64_t(1) << 31) && p_si >= T && p_sh == Lq * p_si &&
+         16 * p_si * el < (int64_t(1) << 31);
+}
+
+int launch_pv_mfma(int p_dtype, const void *probs, int64_t p_sh, int64_t p_si, int v_dtype, const void *v,
+                   int64_t v_st, int64_t v_sh, int64_t Lq, int64_t Hq, int64_t T, int64_t Hkv, void *out,
+                   void *workspace, hipStream_t stream) {
+  PvParams p{};
+  p.p = probs; p.p_sh = p_sh; p.p_si = p_si;
+  p.vt = static_cast<const uint16_t *>(workspace);
+  p.T = T; p.Tp = ceil_div(T, int64_t(kPvTile)) * kPvTile;
+  p.Lq = Lq; p.Hq = Hq; p.Hkv = Hkv; p.group = Hq / Hkv; p.rows = p.group * Lq;
+  p.row_blocks = ceil_div(p.rows, int64_t(kPvRows));
+  p.items = p.row_blocks * Hkv;
+  p.per_xcd = ceil_div(p.items, int64_t(kXcds));
+  p.out = out;
+  UC_REQUIRE(p.per_xcd * kXcds < (int64_t(1) << 31), "uc_kivi_av: grid too large");
+  hipLaunchKernelGGL(pv_stage_kernel, dim3(static_cast<unsigned>(p.Tp / kPvTile), static_cast<unsigned>(Hkv)),
+                     dim3(256), 0, stream, static_cast<const uint16_t *>(v), v_st, v_sh, T, p.Tp,
+                     static_cast<uint16_t *>(workspace));
+  int rc = check_launch("uc_kivi_av (V staging)");
+  if (rc != UC_OK) return rc;
+  const dim3 grid(static_cast<unsigned>(p.per_xcd * kXcds));
+  auto go = [&](auto pd_tag) {
+    constexpr int PD = decltype(pd_tag)::value;
+    if (v_dtype == UC_FP16)
+      hipLaunchKernelGGL((pv_mfma_kernel<PD, UC_FP16>), grid, dim3(kPvThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((pv_mfma_kernel<PD, UC_BF16>), grid, dim3(kPvThreads), 0, stream, p);
+  };
+  if (p_dtype == UC_BF16) go(std::integral_constant<int, UC_BF16>{});
+  else if (p_dtype == UC_FP16) go(std::integral_constant<int, UC_FP16>{});
+  else go(std::integral_constant<int, UC_FP32>{});
+  return check_launch("uc_kivi_av (MFMA)");
 }
 
 int launch_h2o_mfma(int dtype, const void *q, int64_t q_si, int64_t q_sh, const void *k, int64_t k_st, int64_t k_sh,
