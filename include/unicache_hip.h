@@ -149,7 +149,9 @@ int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int64_t heads_
  * [Hq, Lq, D] of out_dtype (contiguous); residual_value element (t, h, d) at
  * r_st*t + r_sh*h + d.  `workspace` must hold
  * uc_workspace_bytes(UC_OP_KIVI_AV, ...) bytes.  With quantized_tokens == 0
- * this is gqa_probability_value (physical.py:42-63).
+ * this is gqa_probability_value (physical.py:42-63); there, with 16-bit values
+ * and >= 64 query rows per KV head, the MFMA path rounds P to the value dtype
+ * first, as physical.py:59 does (the other paths multiply fp32 P).
  * Replaces: the KIVI GEMV AV (kivi_cuda.py:295-307), packed_av_tiled
  * (kivi_triton.py:559-612) and the residual AV + sum (kivi_cuda.py:324-327).
  */
@@ -366,6 +368,8 @@ int uc_compact_rows(const void *src, int64_t src_row_stride_bytes, int64_t row_b
 /*
  * Bytes of caller-provided workspace an operation needs.
  *   UC_OP_KIVI_AV:     (1, heads_q, query_len, head_dim, total_tokens)
+ *                      = max(4 Hq Lq S (D + 2), Hq Lq >= 64 ? 2 Hq D ceil64(T) : 0),
+ *                      S = ceil(T / (Hq Lq <= 64 ? 64 : 512)) + 1
  *   UC_OP_H2O_SCORES:  (1, heads_q, query_len, head_dim, tokens)
  *                      = max(8 Hq Lq, 2048 (B + 768) + 4 T B),
  *                      B = ceil(Hq Lq / 256) + Hq

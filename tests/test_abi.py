@@ -67,7 +67,11 @@ def test_decode_validation():
 
 def test_workspace_bytes():
     # AV: per (q head, row, split) D + 2 floats; splits = ceil(T/512) + 1
-    assert nat.workspace_bytes(nat.UC_OP_KIVI_AV, 1, 28, 1, 128, 8192) == 28 * 1 * 17 * 130 * 4
+    # decode-like AV (28 x 1 query rows) splits every 64 keys: 8192 / 64 + 1 splits
+    assert nat.workspace_bytes(nat.UC_OP_KIVI_AV, 1, 28, 1, 128, 8192) == 28 * 1 * 129 * 130 * 4
+    # longer calls split every 512 keys and also fit V^T staged for the MFMA path
+    assert nat.workspace_bytes(nat.UC_OP_KIVI_AV, 1, 28, 512, 128, 4096) == max(28 * 512 * 9 * 130 * 4,
+                                                                               28 * 128 * 4096 * 2)
     # MFMA decode (head_dim 128, 2-bit): per (item, KV head, split) 16x128 fp16 + 16x2 fp32;
     # MFMA path: packed splits of 8 super-tiles of 256 tokens (2-bit), residual splits of
     # 2 waves x 128 tokens: 8064 packed tokens -> 4 splits, 128 residual tokens -> 1 split

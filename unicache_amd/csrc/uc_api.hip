@@ -42,11 +42,14 @@ extern "C" int64_t uc_workspace_bytes(int op, int64_t n_items, int64_t heads_q, 
   if (n_items < 0 || heads_q < 0 || query_len < 0 || head_dim < 0 || max_tokens < 0) return -1;
   switch (op) {
     case UC_OP_KIVI_AV: {
-      int64_t splits = uc::decode_num_splits(max_tokens);
+      int64_t splits = uc::av_num_splits(heads_q, query_len, max_tokens);
       // per (item, query head, query row, split): D partial outputs + (max, sum);
       // dense MFMA path: V transposed, [KV heads <= query heads][D][tokens rounded up to 64] 16-bit
       const int64_t partials = n_items * heads_q * query_len * splits * (head_dim + 2) * int64_t(sizeof(float));
-      const int64_t staged = n_items * heads_q * head_dim * uc::ceil_div(max_tokens, int64_t(64)) * 64 * 2;
+      // (taken only with >= 64 query rows per KV head, so only when heads_q * query_len >= 64)
+      const int64_t staged = heads_q * query_len >= 64
+                                 ? n_items * heads_q * head_dim * uc::ceil_div(max_tokens, int64_t(64)) * 64 * 2
+                                 : 0;
       return partials > staged ? partials : staged;
     }
     case UC_OP_H2O_SCORES: {

@@ -16,6 +16,17 @@ inline int64_t decode_num_splits(int64_t max_tokens) {
   return (max_tokens + kDecodeSplitTokens - 1) / kDecodeSplitTokens + 1;
 }
 
+// uc_kivi_av (probabilities given): calls with few query rows (decode-like,
+// heads_q * query_len <= 64) split every 64 keys so a short segment still
+// spreads over the CUs; longer calls keep kDecodeSplitTokens.
+inline int64_t av_split_tokens(int64_t heads_q, int64_t query_len) {
+  return heads_q * query_len <= 64 ? 64 : kDecodeSplitTokens;
+}
+inline int64_t av_num_splits(int64_t heads_q, int64_t query_len, int64_t max_tokens) {
+  const int64_t s = av_split_tokens(heads_q, query_len);
+  return (max_tokens + s - 1) / s + 1;
+}
+
 // MFMA decode (uc_decode_mfma.hip): head_dim 128, 2/4-bit codes.
 #ifndef UC_DECODE_MFMA_NST
 #define UC_DECODE_MFMA_NST 8

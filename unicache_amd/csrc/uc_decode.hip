@@ -139,6 +139,7 @@ __device__ void qk_tile(SharedTile &s, const PackedView &v, int64_t h, int64_t t
 struct DecodeParams {
   int64_t Hq, Hkv, D, Lq, group, rows;
   int64_t splits_packed, splits_total;
+  int64_t split_tokens;  // keys per split
   float scale_log2;  // sm_scale * log2(e)
   float *ws_o;       // [items, Hq, Lq, splits, D]
   float *ws_ml;      // [items, Hq, Lq, splits, 2]
@@ -167,11 +168,11 @@ __global__ __launch_bounds__(kThreads) void decode_partial_kernel(const uc_kivi_
 
   int64_t t_begin, t_end;
   if (split < p.splits_packed) {
-    t_begin = split * kDecodeSplitTokens;
-    t_end = min(v.Tq, t_begin + kDecodeSplitTokens);
+    t_begin = split * p.split_tokens;
+    t_end = min(v.Tq, t_begin + p.split_tokens);
   } else {
-    t_begin = v.Tq + (split - p.splits_packed) * kDecodeSplitTokens;
-    t_end = min(v.Tq + v.Tr, t_begin + kDecodeSplitTokens);
+    t_begin = v.Tq + (split - p.splits_packed) * p.split_tokens;
+    t_end = min(v.Tq + v.Tr, t_begin + p.split_tokens);
   }
 
   if (!AV) load_query_rows(s, it.query, p.qd, h, row0, p.rows, p.group, p.Lq, p.Hq, D);
@@ -425,7 +426,7 @@ int decode_common(const uc_kivi_item *items_dev, const uc_kivi_item *single, int
              (long long)workspace_bytes, (long long)need);
   DecodeParams p{};
   p.Hq = Hq; p.Hkv = Hkv; p.D = D; p.Lq = Lq; p.group = Hq / Hkv; p.rows = p.group * Lq;
-  p.splits_packed = sp_packed; p.splits_total = splits;
+  p.splits_packed = sp_packed; p.splits_total = splits; p.split_tokens = kDecodeSplitTokens;
   p.scale_log2 = sm_scale * kLog2e;
   p.ws_o = static_cast<float *>(workspace);
   p.ws_ml = p.ws_o + n_items * Hq * Lq * splits * D;
@@ -565,8 +566,9 @@ extern "C" int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t 
   if (query_len == 0) return UC_OK;
   const int64_t total = quantized_tokens + residual_tokens;
   hipStream_t s = as_stream(stream);
-  const int64_t sp_packed = ceil_div(quantized_tokens, kDecodeSplitTokens);
-  const int64_t sp_res = ceil_div(residual_tokens, kDecodeSplitTokens);
+  const int64_t split_tokens = av_split_tokens(heads_q, query_len);
+  const int64_t sp_packed = ceil_div(quantized_tokens, split_tokens);
+  const int64_t sp_res = ceil_div(residual_tokens, split_tokens);
   const int64_t splits = sp_packed + sp_res;
   if (splits == 0) {
     // no keys: the product is zero
@@ -590,6 +592,7 @@ extern "C" int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t 
   DecodeParams p{};
   p.Hq = heads_q; p.Hkv = heads_kv; p.D = head_dim; p.Lq = query_len; p.group = heads_q / heads_kv;
   p.rows = p.group * query_len; p.splits_packed = sp_packed; p.splits_total = splits;
+  p.split_tokens = split_tokens;
   p.ws_o = static_cast<float *>(workspace);
   p.ws_ml = p.ws_o + heads_q * query_len * splits * head_dim;
   p.probs = probs; p.p_sh = p_sh; p.p_si = p_si; p.p_st = p_st;
