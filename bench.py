@@ -382,6 +382,29 @@ def secondary_rows(device, steps):
         ms, probs.numel() * 2 + 2 * HKV * tokens * 4)
     del probs
 
+    # batched physical attention (adapters/bagel.py:773-980): three CFG samples of
+    # config 2's queries over the packed VAE segment plus their own bf16 keys
+    from unicache_amd.adapters import run_batched_physical_attention
+
+    lq, vae, current = 1088, 1024, (1280, 1024, 256)
+    vk, vv = make_kv(vae, seed=25000, device=device)
+    vae_cache = PackedKIVICache.from_dense(vk, vv, logical_token_ids=torch.arange(vae, device=device),
+                                           token_type_id=3, k_bits=BITS, v_bits=BITS, group_size=GROUP,
+                                           residual_length=RESIDUAL, backend="cuda")
+    ck, cv = make_kv(sum(current), seed=25001, device=device)
+    cq = torch.randn(3 * lq, HQ, D, device=device).to(torch.bfloat16)
+    cu_q = torch.tensor([0, lq, 2 * lq, 3 * lq], dtype=torch.int32)
+    cu_k = torch.tensor([0, current[0], current[0] + current[1], sum(current)], dtype=torch.int32)
+    ms = time_steps(lambda: run_batched_physical_attention(cq, ck, cv, cu_q, cu_k, [[vae_cache]] * 3), steps, 2,
+                    stream)
+    flop = sum(4 * lq * HQ * (vae + c) * D for c in current)
+    rows["batched_cfg_c2"] = {
+        "workload": "three CFG samples of config 2 (1088 queries x 28 heads each) over the 2-bit VAE segment "
+                    "(896 packed + 128 residual) plus 1280 / 1024 / 256 current bf16 keys: "
+                    "run_batched_physical_attention, one fused pass per sample",
+        "ms": round(ms, 5), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+        "frac_of_bf16_mfma_peak": round(flop / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)}
+
     # LSE merge of config 2's three segment summaries (adapters/bagel.py:57-72)
     lq = 1088
     summaries = [(torch.randn(lq, HQ, D, device=device).to(torch.bfloat16), torch.randn(HQ, lq, device=device))

@@ -136,3 +136,42 @@ def test_segment_table_decode_matches_global_softmax(device):
     s1.residual_key = np.concatenate([s1.residual_key, f32(nk)])
     s1.residual_value = np.concatenate([s1.residual_value, f32(nv)])
     check([s1], None, 1)
+
+
+def test_batched_physical_attention_per_sample_softmax(device):
+    # apply_static_physical_attention_batch (adapters/bagel.py:773-980): four
+    # varlen samples (CFG branches) over frozen layouts -- mixed with a long and
+    # a one-token query, H2O-only (dense pass) with both query lengths
+    from unicache_amd.adapters import run_batched_physical_attention
+
+    ak, av = kv_pair(300, seed=41)
+    h2o_a = GQAH2OCache.from_dense(ak.to(device), av.to(device), logical_token_ids=torch.arange(300), token_type_id=1,
+                                   per_kv_head_scores=torch.rand(4, 300).to(device), target_tokens=60,
+                                   recent_tokens=15, selection_frozen=True)
+    bk, bv = kv_pair(200, seed=42)
+    h2o_b = GQAH2OCache.from_dense(bk.to(device), bv.to(device), logical_token_ids=torch.arange(200), token_type_id=2,
+                                   per_kv_head_scores=torch.rand(4, 200).to(device), target_tokens=50,
+                                   recent_tokens=10, selection_frozen=True)
+    pk, pv = kv_pair(1000, seed=43)
+    packed = PackedKIVICache.from_dense(pk.to(device), pv.to(device), logical_token_ids=torch.arange(1000),
+                                        token_type_id=3, k_bits=2, v_bits=2, group_size=32, residual_length=128,
+                                        backend="cuda")
+    seg = K.from_dense(f32(pk), f32(pv), k_bits=2, v_bits=2, group_size=32, residual_length=128)
+    layouts = [([h2o_a, packed], [seg]), ([h2o_b], []), ([h2o_b], []), ([packed], [seg])]
+    q_lens, k_lens = [40, 1, 40, 1], [64, 16, 32, 8]
+    q = queries(sum(q_lens), seed=44)
+    k, v = kv_pair(sum(k_lens), seed=45)
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)])
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)])
+    out = run_batched_physical_attention(q.to(device), k.to(device), v.to(device), torch.tensor(cu_q).to(device),
+                                         torch.tensor(cu_k).to(device), [lay[0] for lay in layouts])
+    assert out.shape == (sum(q_lens), 28, 128) and out.dtype == torch.bfloat16
+    for i, (segments, segs) in enumerate(layouts):
+        h2o = [s for s in segments if isinstance(s, GQAH2OCache)]
+        dense = (k[cu_k[i]:cu_k[i + 1]], v[cu_k[i]:cu_k[i + 1]])
+        ek, ev = _oracle_keys(dense, h2o, segs)
+        eo, _ = A.attention_summary(f32(q[cu_q[i]:cu_q[i + 1]]), ek, ev)
+        assert_close(f32(out[cu_q[i]:cu_q[i + 1]]), eo, what=f"sample {i}")
+    with pytest.raises(ValueError):
+        run_batched_physical_attention(q.to(device), k.to(device), v.to(device), cu_q[:-1], cu_k,
+                                       [lay[0] for lay in layouts[:-1]])

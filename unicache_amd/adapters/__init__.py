@@ -1,3 +1,3 @@
-from .bagel import merge_attention_summaries
+from .bagel import merge_attention_summaries, run_batched_physical_attention, run_fused_mixed_attention
 
-__all__ = ["merge_attention_summaries"]
+__all__ = ["merge_attention_summaries", "run_batched_physical_attention", "run_fused_mixed_attention"]

@@ -1,4 +1,5 @@
-"""Segment-summary merge of the BAGEL adapter on the MI355X kernels."""
+"""Segment-summary merge, fused mixed-segment attention and batched
+physical attention of the BAGEL adapter on the MI355X kernels."""
 
 from __future__ import annotations
 
@@ -84,3 +85,60 @@ def run_fused_mixed_attention(
         segment.update_scores_from_query(query, global_lse)
         segment.enforce_budget()
     return (output, global_lse) if return_lse else output
+
+
+def run_batched_physical_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q,
+    cu_seqlens_k,
+    physical_cache_by_sample: list,
+) -> torch.Tensor:
+    """Non-causal varlen attention of packed samples over their frozen physical
+    layouts (apply_static_physical_attention_batch, adapters/bagel.py:773-980):
+    sample i's queries q[cu_q[i]:cu_q[i+1]] attend to its current keys
+    k[cu_k[i]:cu_k[i+1]], the retained tokens of its GQAH2OCache segments and
+    the residual and packed prefix of its PackedKIVICache segments.  CFG
+    branches packed with pack_naive_caches are such samples.
+
+    Each sample is one fused pass (run_fused_mixed_attention; an H2O-only
+    sample is one dense pass), so the packed prefixes are read in place
+    instead of being dequantised into a varlen workspace.  Returns
+    [total queries, Hq, D] in q's dtype.  H2O segments must be frozen, as in
+    the reference fast path."""
+
+    from ..storage.kivi_cuda import dense_attention_summary
+    from ..storage.physical import GQAH2OCache, PackedKIVICache
+
+    cu_q = [int(x) for x in (cu_seqlens_q.tolist() if torch.is_tensor(cu_seqlens_q) else cu_seqlens_q)]
+    cu_k = [int(x) for x in (cu_seqlens_k.tolist() if torch.is_tensor(cu_seqlens_k) else cu_seqlens_k)]
+    samples = len(physical_cache_by_sample)
+    if len(cu_q) != samples + 1 or len(cu_k) != samples + 1:
+        raise ValueError("cu_seqlens must have one more entry than physical_cache_by_sample")
+    if cu_q[-1] != int(q.shape[0]) or cu_k[-1] != int(k.shape[0]) or k.shape != v.shape:
+        raise ValueError("cu_seqlens must cover q and k; k and v must match")
+    outputs = []
+    for i, segments in enumerate(physical_cache_by_sample):
+        if not segments:
+            raise ValueError(f"Sample {i} has no physical segments")
+        q_i = q[cu_q[i]:cu_q[i + 1]]
+        k_i, v_i = k[cu_k[i]:cu_k[i + 1]], v[cu_k[i]:cu_k[i + 1]]
+        h2o = [s for s in segments if isinstance(s, GQAH2OCache)]
+        packed = [s for s in segments if isinstance(s, PackedKIVICache)]
+        if any(not s.selection_frozen for s in h2o):
+            raise ValueError("Batched physical attention needs frozen H2O selections")
+        if q_i.shape[0] == 0:
+            outputs.append(q_i)
+            continue
+        if any(s.quantized_tokens for s in packed):
+            outputs.append(run_fused_mixed_attention(q_i, k_i, v_i, list(segments)).to(q.dtype))
+            continue
+        keys = [k_i] + [s.key.transpose(0, 1) for s in h2o] + [s.residual_key for s in packed if s.residual_tokens]
+        values = [v_i] + [s.value.transpose(0, 1) for s in h2o] + [
+            s.residual_value for s in packed if s.residual_tokens]
+        dk = torch.cat([x.to(k.dtype) for x in keys], dim=0)
+        dv = torch.cat([x.to(v.dtype) for x in values], dim=0)
+        outputs.append(dense_attention_summary(q_i, dk, dv)[0].to(q.dtype))
+    return torch.cat(outputs, dim=0)
+

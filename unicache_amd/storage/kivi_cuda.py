@@ -232,6 +232,47 @@ def packed_summary_with_dense(
     return out, lse
 
 
+def dense_attention_summary(
+    query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Softmax attention of query [Lq, Hq, D] over dense 16-bit keys/values
+    [T, Hkv, D] in one pass of the packed kernels with an empty packed prefix:
+    the bf16-only summary (flash_attention_summary, adapters/bagel.py:75-95).
+    (out [Lq, Hq, D] in the query dtype, lse [Hq, Lq])."""
+
+    if key.shape != value.shape or key.dim() != 3 or query.dim() != 3:
+        raise ValueError("Dense attention expects query [Lq, Hq, D] and matching [T, Hkv, D] keys/values")
+    lq, hq, d = map(int, query.shape)
+    tokens, hkv = int(key.shape[0]), int(key.shape[1])
+    if int(key.shape[2]) != d or hq % hkv:
+        raise ValueError("Dense attention: head_dim must match and query heads divide by KV heads")
+    if tokens == 0:
+        raise ValueError("Dense attention needs at least one key")
+    if key.dtype not in (torch.bfloat16, torch.float16) or value.dtype != key.dtype:
+        raise ValueError("Dense attention needs bf16 or fp16 keys and values")
+    if query.dtype not in (torch.bfloat16, torch.float16):
+        query = query.to(torch.bfloat16)
+    device = nat.require_device(query, key, value, what="Dense attention")
+    q, dk, dv = query.contiguous(), key.contiguous(), value.contiguous()
+    out = torch.empty((lq, hq, d), dtype=q.dtype, device=device)
+    lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
+    item = nat.KiviItem(None, None, None, None, None, None, dk.data_ptr(), dv.data_ptr(), q.data_ptr(),
+                        out.data_ptr(), lse.data_ptr(), 0, tokens)
+    bits, group = 2, 32  # no packed tokens: only the dense (residual) part is read
+    if lq <= max(1, 16 // (hq // hkv)):
+        ws_bytes = nat.decode_workspace_bytes(1, bits, group, hq, hkv, d, lq, 0, tokens)
+        entry = "uc_kivi_attn_decode"
+    else:
+        if d != 128:
+            raise ValueError("Dense attention over more than 16 query rows per KV head needs head_dim 128")
+        ws_bytes = nat.mq_workspace_bytes(hkv, d, 0, tokens)
+        entry = "uc_kivi_attn_mq"
+    ws = nat.workspace(device, ws_bytes)
+    nat.call(entry, item, bits, group, hq, hkv, d, lq, nat.dtype_code(q.dtype), nat.dtype_code(dk.dtype),
+             nat.dtype_code(q.dtype), 1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device))
+    return out, lse
+
+
 def packed_kivi_quantized_attention_summary(
     cache: "PackedKIVICache", query: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor]:
