@@ -1,6 +1,7 @@
 // H2O attention-mass accumulation, deterministic top-k selection and the GQA
 // compaction gather (operators/physical.py:51-101; physical.py:493-654).
 #include "uc_common.h"
+#include "uc_mfma.h"
 
 namespace uc {
 
@@ -193,28 +194,43 @@ __global__ __launch_bounds__(256) void colsum_kernel(ColsumArgs a) {
 }
 
 // Unit token stride: one workgroup per (KV head, 64 tokens), lane = token;
-// wave w sums the rows of query heads w, w + 8, ... in row order, sixteen
-// loads in flight, and wave 0 adds the heads in order -- the same additions
+// wave w sums the rows of query heads w, w + 8, ... in row order, 64 loads
+// in flight, and wave 0 adds the heads in order -- the same additions
 // as colsum_kernel, so the same result.
 constexpr int kCsWaves = 8;
 constexpr int kCsMaxGroup = 64;
+constexpr int kCsBatch = 64;  // loads in flight per wave: a CU's 7-8 waves keep ~60 KB moving
 
 template <int PD>
 __global__ __launch_bounds__(kCsWaves * kWave) void colsum_rows_kernel(ColsumArgs a) {
   __shared__ float part[kCsMaxGroup][kWave];
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  constexpr int kEl = PD == UC_FP32 ? 4 : 2;
+  const int lane = threadIdx.x & (kWave - 1);
+  // wave-uniform (scalar) so the buffer resources below stay in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int64_t tiles = (a.T + kWave - 1) / kWave;
   const int64_t h = blockIdx.x / tiles, t = (blockIdx.x % tiles) * kWave + lane;
   const int64_t tc = t < a.T ? t : a.T - 1;  // lanes past the end read the last column and store nothing
+  const uint32_t voff = static_cast<uint32_t>(tc * kEl);
   for (int64_t g = wave; g < a.group; g += kCsWaves) {
-    const int64_t base = (h * a.group + g) * a.p_sh + tc;
+    // the query head's rows through one buffer resource: the row offset is the
+    // same for every lane, so it rides in the scalar offset
+    const mf::Rsrc rs = mf::make_rsrc(static_cast<const char *>(a.p) + (h * a.group + g) * a.p_sh * kEl,
+                                      a.Lq * a.p_si * kEl);
+    const uint32_t row_bytes = static_cast<uint32_t>(a.p_si * kEl);
     float s = 0.0f;
-    for (int64_t i0 = 0; i0 < a.Lq; i0 += 16) {
-      float v[16];
+    for (int64_t i0 = 0; i0 < a.Lq; i0 += kCsBatch) {
+      float v[kCsBatch];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = i0 + j < a.Lq ? load_as_f32<PD>(a.p, base + (i0 + j) * a.p_si) : 0.0f;
+      for (int j = 0; j < kCsBatch; ++j) {
+        const uint32_t soff = static_cast<uint32_t>(i0 + j) * row_bytes;  // rows past Lq read zero
+        if constexpr (PD == UC_FP32)
+          v[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0));
+        else
+          v[j] = half_bits_to_f32<PD>(__builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, 0));
+      }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) s += v[j];  // + 0 past the last row: s starts at +0, so it is never -0
+      for (int j = 0; j < kCsBatch; ++j) s += v[j];  // + 0 past the last row: s starts at +0, so it is never -0
     }
     part[g][lane] = s;
   }
@@ -470,7 +486,8 @@ extern "C" int uc_h2o_colsum(const void *probs, int p_dtype, int64_t p_sh, int64
   a.Hq = heads_q; a.Lq = query_len; a.T = tokens; a.Hkv = heads_kv; a.group = heads_q / heads_kv;
   a.accumulate = accumulate; a.out = out;
   hipStream_t s = as_stream(stream);
-  if (p_st == 1 && a.group <= kCsMaxGroup) {
+  const int64_t el = p_dtype == UC_FP32 ? 4 : 2;
+  if (p_st == 1 && a.group <= kCsMaxGroup && p_si * el * (query_len + kCsBatch) < (int64_t(1) << 31)) {
     const int64_t blocks = heads_kv * ceil_div(tokens, int64_t(kWave));
     UC_DISPATCH_DTYPE(p_dtype, PD, [&] {
       hipLaunchKernelGGL((colsum_rows_kernel<PD>), dim3(blocks), dim3(kCsWaves * kWave), 0, s, a);

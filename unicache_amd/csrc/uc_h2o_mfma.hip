@@ -525,7 +525,8 @@ __global__ __launch_bounds__(kPvThreads) void pv_mfma_kernel(PvParams p) {
   constexpr int kAhead = kPvStages - 1;            // tiles in flight
   constexpr int kEl = PD == UC_FP32 ? 4 : 2;       // bytes per probability
   constexpr int kOps = 2 * PRaw<PD>::N + 4;        // memory ops per tile and thread: P halves + V^T slots
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: the P resource below stays in SGPRs
   const int r = lane & 15, kap = lane >> 4;
   const int64_t id = blockIdx.x, w = (id % kXcds) * p.per_xcd + id / kXcds;
   if (w >= p.items) return;  // uniform: the whole workgroup leaves
