@@ -322,6 +322,15 @@ def secondary_rows(device, steps):
             f"{label}: kivi_fake_quant_key + kivi_fake_quant_value on [{tokens}, 4, 128] bf16, 2-bit, G=32",
             ms, 2 * 2 * k.numel() * 2)
 
+    # native pack (kivi_cuda.py:157-190) of a 32k-token K/V in one call
+    from unicache_amd.storage.kivi_cuda import quantize_kivi_native
+
+    k, v = make_kv(32768, seed=21500, device=device)
+    ms = time_steps(lambda: quantize_kivi_native(k, v, k_bits=BITS, v_bits=BITS, group_size=GROUP), steps, 2, stream)
+    rows["pack_32k"] = _hbm_line(
+        "quantize_kivi_native of [32768, 4, 128] bf16 K and V, 2-bit, G=32 (codes + fp16 stats out)",
+        ms, 2 * k.numel() * 2 + 32768 * 384)
+
     # chunked dequantization (kivi_cuda.py:58-93) of a 32k-token packed cache
     tokens = 32768
     k, v = make_kv(tokens, seed=22000, device=device)
