@@ -357,26 +357,29 @@ __global__ __launch_bounds__(256) void dequant_key_native_kernel(DequantArgs a, 
   const int64_t w0 = a.start / TPW + run * kDqRunWords, w_end = (stop + TPW - 1) / TPW;
   const uint32_t *kc = static_cast<const uint32_t *>(a.key_code) + h * a.kc_sh + c * a.kc_sd;
   uint32_t wa[kDqRunWords], wb[kDqRunWords];
+  float s0[kDqRunWords], m0[kDqRunWords], s1[kDqRunWords], m1[kDqRunWords];
+  // every load of the run first (a word lies inside one group: TPW <= group_size)
 #pragma unroll
   for (int j = 0; j < kDqRunWords; ++j) {
     const bool ok = w0 + j < w_end;
     wa[j] = ok ? kc[w0 + j] : 0u;
     wb[j] = ok ? kc[a.kc_sd + w0 + j] : 0u;
+    const int64_t so = h * a.ks_sh + c * a.ks_sd + (((ok ? w0 + j : w0) * TPW) >> a.lg) * a.ks_sg;
+    s0[j] = load_dyn(a.key_scale, so, a.sd);
+    m0[j] = load_dyn(a.key_min, so, a.sd);
+    s1[j] = load_dyn(a.key_scale, so + a.ks_sd, a.sd);
+    m1[j] = load_dyn(a.key_min, so + a.ks_sd, a.sd);
   }
 #pragma unroll
   for (int j = 0; j < kDqRunWords; ++j) {
     const int64_t w = w0 + j;
     if (w >= w_end) break;
-    // a word lies inside one group (TPW <= group_size)
-    const int64_t so = h * a.ks_sh + c * a.ks_sd + ((w * TPW) >> a.lg) * a.ks_sg;
-    const float s0 = load_dyn(a.key_scale, so, a.sd), m0 = load_dyn(a.key_min, so, a.sd);
-    const float s1 = load_dyn(a.key_scale, so + a.ks_sd, a.sd), m1 = load_dyn(a.key_min, so + a.ks_sd, a.sd);
 #pragma unroll
     for (int p = 0; p < TPW; ++p) {
       const int64_t t = w * TPW + p;
       if (t < a.start || t >= stop) continue;
-      const float v0 = add_rn(mul_rn(float((wa[j] >> (p * BITS)) & kMask), s0), m0);
-      const float v1 = add_rn(mul_rn(float((wb[j] >> (p * BITS)) & kMask), s1), m1);
+      const float v0 = add_rn(mul_rn(float((wa[j] >> (p * BITS)) & kMask), s0[j]), m0[j]);
+      const float v1 = add_rn(mul_rn(float((wb[j] >> (p * BITS)) & kMask), s1[j]), m1[j]);
       store_pair<OD>(a.out_key, (a.offset + t - a.start) * a.o_st + h * a.o_sh + c, v0, v1);
     }
   }
@@ -384,7 +387,7 @@ __global__ __launch_bounds__(256) void dequant_key_native_kernel(DequantArgs a, 
 
 // Values: lane = (head, token, word), words fastest: one 4-byte word and its
 // group's stats in, 16 (2-bit) or 8 (4-bit) contiguous channels out.
-template <int BITS, int OD>
+template <int BITS, int OD, bool VEC>
 __global__ __launch_bounds__(256) void dequant_value_native_kernel(DequantArgs a) {
   constexpr int CPW = 32 / BITS;  // channels per word
   constexpr uint32_t kMask = (1u << BITS) - 1u;
@@ -397,11 +400,30 @@ __global__ __launch_bounds__(256) void dequant_value_native_kernel(DequantArgs a
   const int64_t so = h * a.vs_sh + t * a.vs_st + ((w * CPW) >> a.lg) * a.vs_sg;
   const float s = load_dyn(a.value_scale, so, a.sd), m = load_dyn(a.value_min, so, a.sd);
   const int64_t o = (a.offset + n) * a.o_st + h * a.o_sh + w * CPW;
+  float v[CPW];
 #pragma unroll
-  for (int p = 0; p < CPW; p += 2) {
-    const float v0 = add_rn(mul_rn(float((word >> (p * BITS)) & kMask), s), m);
-    const float v1 = add_rn(mul_rn(float((word >> ((p + 1) * BITS)) & kMask), s), m);
-    store_pair<OD>(a.out_value, o + p, v0, v1);
+  for (int p = 0; p < CPW; ++p) v[p] = add_rn(mul_rn(float((word >> (p * BITS)) & kMask), s), m);
+  if (VEC) {  // CPW contiguous outputs as whole 16-byte stores
+    constexpr int kPer16 = OD == UC_FP32 ? 4 : 8;
+#pragma unroll
+    for (int q = 0; q < CPW / kPer16; ++q) {
+      uint32_t r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (OD == UC_FP32) {
+          r[e] = __float_as_uint(v[q * 4 + e]);
+        } else {
+          const float lo = v[q * 8 + 2 * e], hi = v[q * 8 + 2 * e + 1];
+          r[e] = (OD == UC_BF16 ? f32_to_bf16_bits(lo) : f32_to_f16_bits(lo)) |
+                 (uint32_t(OD == UC_BF16 ? f32_to_bf16_bits(hi) : f32_to_f16_bits(hi)) << 16);
+        }
+      }
+      *reinterpret_cast<uint4 *>(static_cast<char *>(a.out_value) + (o + q * kPer16) * (OD == UC_FP32 ? 4 : 2)) =
+          make_uint4(r[0], r[1], r[2], r[3]);
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < CPW; p += 2) store_pair<OD>(a.out_value, o + p, v[p], v[p + 1]);
   }
 }
 
@@ -656,10 +678,19 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
       }
       if (value_code != nullptr) {
         const int64_t n = heads * count * (head_dim * v_bits / 32);
-        if (v_bits == 2)
-          hipLaunchKernelGGL((dequant_value_native_kernel<2, OD>), dim3(ceil_div(n, 256)), dim3(256), 0, s, a);
-        else
-          hipLaunchKernelGGL((dequant_value_native_kernel<4, OD>), dim3(ceil_div(n, 256)), dim3(256), 0, s, a);
+        // 16-byte stores when every run of a word's channels starts on 16 bytes
+        const int64_t per16 = 16 / out_bytes;
+        const bool vec = aligned(out_value, 16) && o_st % per16 == 0 && o_sh % per16 == 0 &&
+                         (32 / v_bits) % per16 == 0;
+        auto go = [&](auto vec_tag) {
+          constexpr bool VEC = decltype(vec_tag)::value;
+          if (v_bits == 2)
+            hipLaunchKernelGGL((dequant_value_native_kernel<2, OD, VEC>), dim3(ceil_div(n, 256)), dim3(256), 0, s, a);
+          else
+            hipLaunchKernelGGL((dequant_value_native_kernel<4, OD, VEC>), dim3(ceil_div(n, 256)), dim3(256), 0, s, a);
+        };
+        if (vec) go(std::true_type{});
+        else go(std::false_type{});
       }
     });
     return check_launch("uc_kivi_dequant");
