@@ -183,6 +183,25 @@ def test_gqa_pv_mfma_tiles(device, pdtype, vdtype):
     assert_close(f32(got), exp, max_abs=1e-2, mean_abs=1e-3, what="pv mfma")
 
 
+def test_gqa_generic_and_mfma_routes_agree(device):
+    # the same products through the MFMA tiles (contiguous inputs, >= 64 rows per
+    # KV head) and through the generic kernels (fp32 query; key-strided P): both
+    # within tolerance of the oracle and of each other
+    key, value = kv_pair(200, seed=35)
+    q = queries(80, seed=36)
+    mfma = gqa_query_key_logits(q.to(device), key.to(device))
+    generic = gqa_query_key_logits(q.float().to(device), key.float().to(device))
+    exp = A.gqa_logits(f32(q), f32(key))
+    assert_close(f32(mfma), exp, max_abs=2e-3, mean_abs=1e-4, what="qk mfma")
+    assert_close(f32(generic), exp, max_abs=2e-3, mean_abs=1e-4, what="qk generic")
+    p = torch.softmax(mfma / math.sqrt(128), -1).to(torch.bfloat16)
+    pv_mfma = gqa_probability_value(p, value.to(device))
+    pt = p.transpose(1, 2).contiguous().transpose(1, 2)  # same values, key stride != 1
+    pv_generic = gqa_probability_value(pt, value.to(device))
+    assert_close(f32(pv_mfma), f32(pv_generic), max_abs=1e-2, mean_abs=1e-3, what="pv routes")
+    assert_close(f32(pv_mfma), A.gqa_pv(f32(p), f32(value)), what="pv oracle")
+
+
 def test_lse_merge(device):
     # test_physical.py:181-202 on the GPU kernel
     torch.manual_seed(11)
