@@ -76,6 +76,34 @@ def build_workload(device, layers=LAYERS, batch=BATCH, tokens=TOKENS):
     return caches, queries, pack_ms, pack_bytes
 
 
+def pack_throughput(device, steps):
+    """uc_kivi_pack of one config-1 sequence (8064 packed tokens, 2-bit, G=32)
+    into preallocated native-layout outputs, calls back to back: the C-ABI pack
+    path without from_dense's per-cache allocations."""
+
+    from unicache_amd import _native as nat
+    from unicache_amd.storage.physical import _dense_strides, native_pack_layout
+
+    tq = TOKENS - RESIDUAL
+    key, value = make_kv(TOKENS, seed=26000, device=device)
+    qk, qv = key[:tq], value[:tq]
+    lay = native_pack_layout(tq, HKV, D, BITS, BITS, GROUP)
+    kc = torch.empty(lay["key_code"][0], dtype=torch.int32, device=device)
+    ks = torch.empty(lay["key_stats"][0], dtype=torch.float16, device=device)
+    km = torch.empty_like(ks)
+    vc = torch.empty(lay["value_code"][0], dtype=torch.int32, device=device)
+    vs = torch.empty(lay["value_stats"][0], dtype=torch.float16, device=device)
+    vm = torch.empty_like(vs)
+    stream = torch.cuda.current_stream(device)
+    args = (qk.data_ptr(), *_dense_strides(qk), qv.data_ptr(), *_dense_strides(qv), nat.dtype_code(qk.dtype), tq,
+            HKV, D, BITS, BITS, GROUP, nat.UC_FP16, kc.data_ptr(), *map(int, kc.stride()), ks.data_ptr(),
+            km.data_ptr(), *map(int, ks.stride()), vc.data_ptr(), *map(int, vc.stride()), vs.data_ptr(),
+            vm.data_ptr(), *map(int, vs.stride()), stream.cuda_stream)
+    ms = time_steps(lambda: nat.call("uc_kivi_pack", *args), steps, 3, stream)
+    nbytes = 2 * qk.numel() * 2 + tq * 384
+    return nbytes / (ms * 1e-3) / 1e9, ms
+
+
 def time_steps(fn, steps, warmup, stream):
     for _ in range(warmup):
         fn()
@@ -534,8 +562,12 @@ def main():
             "bytes_per_launch": step_bytes,
         },
         "per_layer_launches_gbs": round(step_bytes / (ms_layers * 1e-3) / 1e9, 2),
-        "pack_gbs": round(pack_bytes / (pack_ms * 1e-3) / 1e9, 2),
     }
+    pack_gbs, pack_call_ms = pack_throughput(device, max(20, args.steps))
+    result["pack_gbs"] = round(pack_gbs, 2)
+    result["pack_ms_per_sequence"] = round(pack_call_ms, 5)
+    # from_dense of the 224 cached sequences above, each allocating its own tensors
+    result["pack_from_dense_gbs"] = round(pack_bytes / (pack_ms * 1e-3) / 1e9, 2)
     del batch, per_layer, caches, queries
     torch.cuda.empty_cache()
     result["decode_32k"] = long_context_decode(device, max(5, args.steps // 2))
