@@ -313,3 +313,27 @@ def test_mq_is_deterministic(device):
     a, la = packed_kivi_attention_summary(cache, q)
     b, lb = packed_kivi_attention_summary(cache, q)
     assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+def test_batched_decode_doubled_split(device):
+    # 100 items x 4 KV heads of 4096 packed + 128 residual tokens: 3 splits per
+    # unit (1200 workgroups) exceed one round of slots, 2 splits (800) fit, so the
+    # batch runs 16 super-tiles per split; each item alone runs 8
+    from unicache_amd.storage.decode import KiviDecodeBatch
+
+    g = torch.Generator(device=device).manual_seed(61)
+    caches, qs = [], []
+    for i in range(100):
+        k = torch.randn(4224, 4, 128, generator=g, device=device).to(torch.bfloat16)
+        v = torch.randn(4224, 4, 128, generator=g, device=device).to(torch.bfloat16)
+        caches.append(PackedKIVICache.from_dense(k, v, logical_token_ids=torch.arange(4224, device=device),
+                                                 token_type_id=3, k_bits=2, v_bits=2, group_size=32,
+                                                 residual_length=128, backend="cuda"))
+        qs.append(torch.randn(1, 28, 128, generator=g, device=device).to(torch.bfloat16))
+    assert caches[0].quantized_tokens == 4096
+    batch = KiviDecodeBatch(caches, qs)
+    batch.run()
+    for i in (0, 37, 99):
+        out, lse = packed_kivi_attention_summary(caches[i], qs[i])
+        assert_close(f32(batch.outputs[i]), f32(out), max_abs=5e-3, mean_abs=2e-4, what=f"item {i}")
+        assert_close(f32(batch.lses[i]), f32(lse), max_abs=1e-4, mean_abs=1e-5, what=f"lse {i}")
