@@ -196,7 +196,8 @@ typedef struct uc_kivi_item {
  * packed_kivi_quantized_attention_summary (kivi_cuda.py:96-120) for Lq small.
  * `workspace` must hold uc_kivi_decode_workspace_bytes(1, ...) bytes.
  * head_dim 128 with bits 2/4 and group 32/64/128 runs the MFMA kernel; other
- * shapes a generic split-K kernel.
+ * shapes a generic split-K kernel.  The MFMA kernel takes fp16 operands: query,
+ * residual and dequantized values must stay below 65504 in magnitude.
  */
 int uc_kivi_attn_decode(const uc_kivi_item *item_host, int bits, int group_size,
                         int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t query_len,
@@ -244,7 +245,8 @@ int uc_kivi_attn_decode_segments(const uc_kivi_item *items_device, int64_t n_ite
  * group_size 32/64/128, q and residual bf16/fp16.  A first kernel dequantizes
  * the packed keys/values of every KV head once into `workspace` (fp16 keys and
  * transposed values, uc_kivi_mq_workspace_bytes bytes); a second streams them
- * in 64-key tiles through LDS for MFMA, 128 query rows per workgroup.
+ * in 64-key tiles through LDS for MFMA, 128 query rows per workgroup.  Operands
+ * are fp16: query, residual and dequantized values must stay below 65504 in magnitude.
  * Replaces: _packed_attention_kernel / packed_attention_tiled
  * (kivi_triton.py:216-382, 615-687) behind packed_kivi_quantized_attention_summary
  * (kivi_cuda.py:96-120) with backend "triton_tiled", plus the residual part.
