@@ -88,3 +88,45 @@ def test_workspace_bytes():
         (blocks + 768) * 256 * 8 + blocks * 4096 * 4)
     with pytest.raises(ValueError):
         nat.workspace_bytes(99, 1, 1, 1, 1, 1)
+
+
+def test_editing_validation():
+    item = nat.KiviItem()
+    item.quantized_tokens = 64
+    args = (28, 4, 128, 512, nat.UC_BF16, nat.UC_BF16, nat.UC_BF16, 0.1, None, 0, None)
+    with pytest.raises(ValueError, match="bits must be 2 or 4"):
+        nat.call("uc_kivi_attn_mq", ctypes.byref(item), 3, 32, *args)
+    with pytest.raises(ValueError, match="group_size must be 32, 64 or 128"):
+        nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 16, *args)
+    with pytest.raises(ValueError, match="head_dim must be 128"):
+        nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, 28, 4, 64, 512, nat.UC_BF16, nat.UC_BF16,
+                 nat.UC_BF16, 0.1, None, 0, None)
+    with pytest.raises(ValueError, match="multiple of KV heads"):
+        nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, 28, 3, 128, 512, nat.UC_BF16, nat.UC_BF16,
+                 nat.UC_BF16, 0.1, None, 0, None)
+    # the workspace check comes after every pointer check; the pointers are
+    # never dereferenced on the host, so aligned placeholders reach it
+    item.quantized_tokens = 0
+    item.residual_tokens = 128
+    item.query = item.out = item.residual_key = item.residual_value = 0x1000
+    with pytest.raises(ValueError, match="workspace too small"):
+        nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, *args)
+    item.out = 0x1008
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, *args)
+
+
+def test_merge_and_fake_quant_validation():
+    with pytest.raises(ValueError, match="At least one attention summary"):
+        nat.call("uc_lse_merge", None, None, 0, nat.UC_BF16, 4, 28, 128, None, None, None)
+    with pytest.raises(ValueError, match="at most 16 segments"):
+        nat.call("uc_lse_merge", None, None, 17, nat.UC_BF16, 4, 28, 128, None, None, None)
+    with pytest.raises(ValueError, match="Unsupported fake quant bits: 5"):
+        nat.call("uc_kivi_fake_quant", None, 512, 128, 1, nat.UC_BF16, 4, 4, 128, 5, 0, 32, None, None)
+    with pytest.raises(ValueError, match="dim must be 0"):
+        nat.call("uc_kivi_fake_quant", None, 512, 128, 1, nat.UC_BF16, 4, 4, 128, 2, 1, 32, None, None)
+    with pytest.raises(ValueError, match="divisible by KV heads for GQA H2O"):
+        nat.call("uc_h2o_colsum", None, nat.UC_BF16, 0, 0, 1, 28, 1, 64, 3, 0, None, None)
+    with pytest.raises(ValueError, match="divisible by KIVI KV heads"):
+        nat.call("uc_kivi_qk", None, nat.UC_BF16, 1, 28, None, None, None, nat.UC_FP16, 0, 2, 32,
+                 None, nat.UC_BF16, 16, 0, 0, 3, 128, 0.1, None, None)
