@@ -261,6 +261,23 @@ int64_t uc_kivi_mq_workspace_bytes(int64_t heads_kv, int64_t head_dim, int64_t q
                                    int64_t residual_tokens);
 
 /*
+ * uc_kivi_attn_mq over n_items (1..8) independent segments in one stage
+ * launch and one attention launch: item i attends its query_lens[i] queries
+ * (item.query / item.out / item.lse, laid out as in uc_kivi_attn_mq) to its
+ * own packed prefix and residual.  Every item shares bits, group_size, heads,
+ * head_dim and dtypes.  `workspace` holds the items' stagings back to back:
+ * sum_i uc_kivi_mq_workspace_bytes(heads_kv, head_dim, Tq_i, Tr_i) bytes.
+ * Results equal n_items calls of uc_kivi_attn_mq bit for bit.
+ * Replaces: the per-sample loop of apply_static_physical_attention_batch
+ * (adapters/bagel.py:773-980) for samples whose physical layout is one packed
+ * KIVI segment plus dense keys (CFG branches packed with pack_naive_caches).
+ */
+int uc_kivi_attn_mq_batch(const uc_kivi_item *items_host, const int64_t *query_lens, int n_items,
+                          int bits, int group_size, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
+                          int q_dtype, int res_dtype, int out_dtype, float sm_scale,
+                          void *workspace, int64_t workspace_bytes, uc_stream_t stream);
+
+/*
  * Merge normalised attention summaries of n_segments disjoint key segments:
  *   lse = logsumexp_s lse_s;  out = sum_s out_s * exp(lse_s - lse)
  * outs[s] are [Lq, Hq, D] of out_dtype (contiguous), lses[s] fp32 [Hq, Lq].

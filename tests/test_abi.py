@@ -130,3 +130,24 @@ def test_merge_and_fake_quant_validation():
     with pytest.raises(ValueError, match="divisible by KIVI KV heads"):
         nat.call("uc_kivi_qk", None, nat.UC_BF16, 1, 28, None, None, None, nat.UC_FP16, 0, 2, 32,
                  None, nat.UC_BF16, 16, 0, 0, 3, 128, 0.1, None, None)
+
+
+def test_editing_batch_validation():
+    items = (nat.KiviItem * 9)()
+    lens = (ctypes.c_int64 * 9)(*([512] * 9))
+    tail = (2, 32, 28, 4, 128, nat.UC_BF16, nat.UC_BF16, nat.UC_BF16, 0.1, None, 0, None)
+    with pytest.raises(ValueError, match="n_items must be 1..8"):
+        nat.call("uc_kivi_attn_mq_batch", items, lens, 0, *tail)
+    with pytest.raises(ValueError, match="n_items must be 1..8"):
+        nat.call("uc_kivi_attn_mq_batch", items, lens, 9, *tail)
+    with pytest.raises(ValueError, match="empty segment"):
+        nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)
+    # aligned placeholders (never dereferenced on the host) reach the workspace check
+    for it in items[:2]:
+        it.residual_tokens = 100
+        it.query = it.out = it.residual_key = it.residual_value = 0x1000
+    with pytest.raises(ValueError, match="workspace too small"):
+        nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)
+    lens[1] = 0
+    with pytest.raises(ValueError, match="query_len must be positive"):
+        nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)

@@ -175,3 +175,31 @@ def test_batched_physical_attention_per_sample_softmax(device):
     with pytest.raises(ValueError):
         run_batched_physical_attention(q.to(device), k.to(device), v.to(device), cu_q[:-1], cu_k,
                                        [lay[0] for lay in layouts[:-1]])
+
+
+def test_batched_packed_launch_matches_per_sample_passes(device):
+    # samples with one packed prefix plus dense keys share one stage and one
+    # attention launch per 8 (uc_kivi_attn_mq_batch); the results equal one
+    # fused pass per sample bit for bit.  Ten samples: two launches for the
+    # 2-bit / group-32 caches (chunks of 8 and 1) and one for the 4-bit /
+    # group-64 cache; ragged query and current-key lengths.
+    from unicache_amd.adapters import run_batched_physical_attention
+
+    caches = []
+    for j, (n, bits, group) in enumerate([(1000, 2, 32), (600, 2, 32), (1100, 4, 64)]):
+        ck, cv = kv_pair(n, seed=60 + j)
+        caches.append(PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(n),
+                                                 token_type_id=3, k_bits=bits, v_bits=bits, group_size=group,
+                                                 residual_length=128, backend="cuda"))
+    pick = [0, 1, 0, 2, 1, 0, 0, 1, 0, 1]
+    q_lens = [40, 300, 3, 129, 64, 200, 17, 96, 250, 5]
+    k_lens = [64, 0, 16, 128, 31, 200, 8, 100, 1, 77]
+    q = queries(sum(q_lens), seed=70).to(device)
+    k, v = (x.to(device) for x in kv_pair(sum(k_lens), seed=71))
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).tolist()
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)]).tolist()
+    out = run_batched_physical_attention(q, k, v, cu_q, cu_k, [[caches[c]] for c in pick])
+    for i, c in enumerate(pick):
+        want = run_fused_mixed_attention(q[cu_q[i]:cu_q[i + 1]], k[cu_k[i]:cu_k[i + 1]], v[cu_k[i]:cu_k[i + 1]],
+                                         [caches[c]])
+        assert torch.equal(out[cu_q[i]:cu_q[i + 1]], want), f"sample {i}"

@@ -86,6 +86,11 @@ _SIGNATURES = {
     ),
     "uc_kivi_attn_mq": (_I, [ctypes.POINTER(KiviItem), _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _P, _L, _P]),
     "uc_kivi_mq_workspace_bytes": (_L, [_L, _L, _L, _L]),
+    "uc_kivi_attn_mq_batch": (
+        _I,
+        [ctypes.POINTER(KiviItem), ctypes.POINTER(ctypes.c_int64), _I, _I, _I, _L, _L, _L, _I, _I, _I, _F, _P, _L,
+         _P],
+    ),
     "uc_lse_merge": (_I, [_P, _P, _I, _I, _L, _L, _L, _P, _P, _P]),
     "uc_h2o_scores": (
         _I,

@@ -19,6 +19,9 @@
 //                  accumulators, B = two 4-key runs of the value tile).
 // Output: normalised O (written through LDS as whole rows) and the
 // natural-log LSE.
+#include <type_traits>
+#include <utility>
+
 #include "uc_common.h"
 #include "uc_mfma.h"
 
@@ -55,6 +58,30 @@ struct StageParams {
   int64_t Hkv, keys, keys_pad;
   _Float16 *wk, *wv;
 };
+
+// Up to kMqMaxBatch segments (one query block each) in one stage launch and
+// one attention launch, passed by value as kernel arguments.  Item i owns
+// stage tiles [stage_begin[i], stage_begin[i+1]) and attention work items
+// (row block x KV head) [attn_begin[i], attn_begin[i+1]).  Work items are
+// launched in that order, longest segments first: each one fills a CU, and
+// starting the long ones first shortens the tail when the segments differ in
+// length.
+constexpr int kMqMaxBatch = 8;
+struct MqBatch {
+  uc_kivi_item it[kMqMaxBatch];
+  MqParams p[kMqMaxBatch];
+  StageParams sp[kMqMaxBatch];
+  int64_t stage_begin[kMqMaxBatch + 1], attn_begin[kMqMaxBatch + 1];
+  int n;
+};
+static_assert(sizeof(MqBatch) <= 4096, "the batch table fits the kernel argument space");
+
+// Item of a batch that owns index x of a cumulative range table (uniform).
+__device__ __forceinline__ int batch_item(const int64_t *begin, int n, int64_t x) {
+  int i = 0;
+  while (i + 1 < n && x >= begin[i + 1]) ++i;
+  return i;
+}
 
 // Packed words and stats of one 64-key tile, per thread.
 template <int BITS>
@@ -133,11 +160,11 @@ __device__ __forceinline__ void dequant_pair(uint32_t wa, uint32_t wb, uint32_t 
 constexpr int kStageThreads = kWave;
 
 template <int BITS, int G, int RD>
-__global__ __launch_bounds__(kStageThreads) void mq_stage_kernel(uc_kivi_item it, StageParams sp) {
+__device__ __forceinline__ void mq_stage_body(const uc_kivi_item &it, const StageParams &sp, int64_t tile) {
   using Gm = Geo<BITS>;
   const int tid = blockIdx.z * kStageThreads + threadIdx.x;  // work item of the tile, 0..255
   const int64_t h = blockIdx.y;
-  const int64_t x0 = int64_t(blockIdx.x) * kTile;  // first key of the tile
+  const int64_t x0 = tile * kTile;  // first key of the tile
   const int64_t Tq = it.quantized_tokens, Tr = it.residual_tokens, T = Tq + Tr;
   _Float16 *wk = sp.wk + h * sp.keys_pad * kD;
   _Float16 *wv = sp.wv + h * kD * sp.keys_pad;
@@ -230,6 +257,18 @@ __global__ __launch_bounds__(kStageThreads) void mq_stage_kernel(uc_kivi_item it
       }
     }
   }
+}
+
+template <int BITS, int G, int RD>
+__global__ __launch_bounds__(kStageThreads) void mq_stage_kernel(uc_kivi_item it, StageParams sp) {
+  mq_stage_body<BITS, G, RD>(it, sp, blockIdx.x);
+}
+
+template <int BITS, int G, int RD>
+__global__ __launch_bounds__(kStageThreads) void mq_stage_batch_kernel(MqBatch b) {
+  const int64_t tile = blockIdx.x;
+  const int i = batch_item(b.stage_begin, b.n, tile);
+  mq_stage_body<BITS, G, RD>(b.it[i], b.sp[i], tile - b.stage_begin[i]);
 }
 
 // --------------------------------------------------------- attention pass --
@@ -366,19 +405,13 @@ constexpr int kHalfThreads = kAttnThreads / 2;
 static_assert(kHalfThreads == 256, "tile loads map 256 threads per key half");
 constexpr int kMergeFloats = 2 * 8 * 4 + 4;  // O^T (2 query blocks x 8 channel blocks x 4) + m[2], l[2]
 
+// Work item w = h * row_blocks + rb of one segment: 128 query rows of KV head h.
 template <int QD, int OD>
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void mq_attention_kernel(
-    uc_kivi_item it, MqParams p) {
+__device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const MqParams &p, int64_t w) {
   __shared__ MqTile sh[2][2];  // [key half][buffer]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = wave / 4, rw = wave % 4, tid_h = tid % kHalfThreads;
   const int r = lane & 15, kap = lane >> 4;
-  // Workgroups are dealt to the 8 XCDs round-robin by launch index; work item
-  // w = h * row_blocks + rb goes to index 8 * (w % per_xcd) + w / per_xcd, so
-  // each XCD serves a contiguous run of row blocks -- mostly of one KV head,
-  // whose staged keys and values its own L2 then holds.
-  const int64_t id = blockIdx.x, w = (id % kXcds) * p.per_xcd + id / kXcds;
-  if (w >= p.row_blocks * p.Hkv) return;  // uniform: the whole workgroup leaves
   const int64_t h = w / p.row_blocks;
   const int64_t row0 = (w % p.row_blocks) * kMqRows + rw * kRowsPerWave;
 
@@ -493,6 +526,26 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
   }
 }
 
+// Workgroups are dealt to the 8 XCDs round-robin by launch index; work item w
+// goes to index 8 * (w % per_xcd) + w / per_xcd, so each XCD serves a
+// contiguous run of row blocks -- mostly of one KV head of one segment, whose
+// staged keys and values its own L2 then holds.
+template <int QD, int OD>
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void mq_attention_kernel(
+    uc_kivi_item it, MqParams p) {
+  const int64_t id = blockIdx.x, w = (id % kXcds) * p.per_xcd + id / kXcds;
+  if (w >= p.row_blocks * p.Hkv) return;  // uniform: the whole workgroup leaves
+  mq_attention_body<QD, OD>(it, p, w);
+}
+
+template <int QD, int OD>
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void mq_attention_batch_kernel(
+    MqBatch b) {
+  const int64_t w = blockIdx.x;
+  const int i = batch_item(b.attn_begin, b.n, w);
+  mq_attention_body<QD, OD>(b.it[i], b.p[i], w - b.attn_begin[i]);
+}
+
 }  // namespace
 }  // namespace uc
 
@@ -505,13 +558,42 @@ extern "C" int64_t uc_kivi_mq_workspace_bytes(int64_t heads_kv, int64_t head_dim
   return heads_kv * keys_pad * head_dim * 2 * int64_t(sizeof(_Float16));
 }
 
-extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int group_size, int64_t heads_q,
-                               int64_t heads_kv, int64_t head_dim, int64_t query_len, int q_dtype, int res_dtype,
-                               int out_dtype, float sm_scale, void *workspace, int64_t workspace_bytes,
-                               uc_stream_t stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
-  UC_REQUIRE(item_host != nullptr, "attn_mq: item is NULL");
-  const uc_kivi_item it = *item_host;
+namespace uc {
+namespace {
+
+template <int V>
+using IC = std::integral_constant<int, V>;
+
+// Calls f(IC<bits>, IC<group>, IC<residual dtype>) for the stage kernels.
+template <class F>
+void stage_config(int bits, int group_size, int res_dtype, F &&f) {
+  auto by_rd = [&](auto b, auto g) {
+    if (res_dtype == UC_FP16) f(b, g, IC<UC_FP16>{});
+    else f(b, g, IC<UC_BF16>{});
+  };
+  auto by_group = [&](auto b) {
+    if (group_size == 32) by_rd(b, IC<32>{});
+    else if (group_size == 64) by_rd(b, IC<64>{});
+    else by_rd(b, IC<128>{});
+  };
+  if (bits == 2) by_group(IC<2>{});
+  else by_group(IC<4>{});
+}
+
+// Calls f(IC<query dtype>, IC<out dtype>) for the attention kernels.
+template <class F>
+void attn_config(int q_dtype, int out_dtype, F &&f) {
+  auto by_out = [&](auto qd) {
+    if (out_dtype == UC_BF16) f(qd, IC<UC_BF16>{});
+    else if (out_dtype == UC_FP16) f(qd, IC<UC_FP16>{});
+    else f(qd, IC<UC_FP32>{});
+  };
+  if (q_dtype == UC_FP16) by_out(IC<UC_FP16>{});
+  else by_out(IC<UC_BF16>{});
+}
+
+int mq_check_config(int bits, int group_size, int64_t heads_q, int64_t heads_kv, int64_t head_dim, int q_dtype,
+                    int res_dtype, int out_dtype) {
   UC_REQUIRE(bits == 2 || bits == 4, "attn_mq: bits must be 2 or 4 (got %d)", bits);
   UC_REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
              "attn_mq: group_size must be 32, 64 or 128 (got %d)", group_size);
@@ -519,11 +601,15 @@ extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int grou
   UC_REQUIRE(heads_kv > 0 && heads_q > 0 && heads_q % heads_kv == 0,
              "attn_mq: query heads (%lld) must be a multiple of KV heads (%lld)", (long long)heads_q,
              (long long)heads_kv);
-  UC_REQUIRE(query_len > 0 && query_len * (heads_q / heads_kv) < (int64_t(1) << 31),
-             "attn_mq: query_len must be positive and query rows per KV head below 2^31");
   UC_REQUIRE((q_dtype == UC_BF16 || q_dtype == UC_FP16) && (res_dtype == UC_BF16 || res_dtype == UC_FP16),
              "attn_mq: query and residual must be bf16 or fp16");
   UC_REQUIRE(out_dtype == UC_BF16 || out_dtype == UC_FP16 || out_dtype == UC_FP32, "attn_mq: bad out dtype");
+  return UC_OK;
+}
+
+int mq_check_item(const uc_kivi_item &it, int group_size, int64_t heads_q, int64_t heads_kv, int64_t query_len) {
+  UC_REQUIRE(query_len > 0 && query_len * (heads_q / heads_kv) < (int64_t(1) << 31),
+             "attn_mq: query_len must be positive and query rows per KV head below 2^31");
   UC_REQUIRE(it.quantized_tokens >= 0 && it.residual_tokens >= 0 && it.quantized_tokens % group_size == 0,
              "attn_mq: quantized tokens must be a non-negative multiple of group_size");
   UC_REQUIRE(it.quantized_tokens + it.residual_tokens > 0, "attn_mq: empty segment");
@@ -534,39 +620,22 @@ extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int grou
                                           it.value_scale && it.value_min),
              "attn_mq: packed tensors are NULL");
   UC_REQUIRE(it.residual_tokens == 0 || (it.residual_key && it.residual_value), "attn_mq: residual is NULL");
-  const int64_t need = uc_kivi_mq_workspace_bytes(heads_kv, head_dim, it.quantized_tokens, it.residual_tokens);
-  UC_REQUIRE(workspace != nullptr && workspace_bytes >= need, "attn_mq: workspace too small (%lld < %lld bytes)",
-             (long long)workspace_bytes, (long long)need);
-  StageParams sp{};
+  const int64_t keys_pad = ceil_div(it.quantized_tokens + it.residual_tokens, int64_t(kTile)) * kTile;
+  UC_REQUIRE(keys_pad * mf::kD * 2 < (int64_t(1) << 31) && it.quantized_tokens * 64 < (int64_t(1) << 31),
+             "attn_mq: segment too long for 32-bit buffer offsets");
+  return UC_OK;
+}
+
+// Stage and attention parameters of one segment whose staged K and V start at ws.
+void mq_fill(const uc_kivi_item &it, int64_t heads_q, int64_t heads_kv, int64_t query_len, float sm_scale,
+             _Float16 *ws, StageParams &sp, MqParams &p) {
+  sp = StageParams{};
   sp.Hkv = heads_kv;
   sp.keys = it.quantized_tokens + it.residual_tokens;
   sp.keys_pad = ceil_div(sp.keys, int64_t(kTile)) * kTile;
-  UC_REQUIRE(sp.keys_pad * mf::kD * 2 < (int64_t(1) << 31) && it.quantized_tokens * 64 < (int64_t(1) << 31),
-             "attn_mq: segment too long for 32-bit buffer offsets");
-  sp.wk = static_cast<_Float16 *>(workspace);
-  sp.wv = sp.wk + heads_kv * sp.keys_pad * mf::kD;
-  const dim3 sgrid(static_cast<unsigned>(sp.keys_pad / kTile), static_cast<unsigned>(heads_kv),
-                   static_cast<unsigned>(kMqThreads / kStageThreads));
-#define UC_STAGE(B, G)                                                                                          \
-  do {                                                                                                          \
-    if (res_dtype == UC_FP16)                                                                                   \
-      hipLaunchKernelGGL((mq_stage_kernel<B, G, UC_FP16>), sgrid, dim3(kStageThreads), 0, stream, it, sp);         \
-    else                                                                                                        \
-      hipLaunchKernelGGL((mq_stage_kernel<B, G, UC_BF16>), sgrid, dim3(kStageThreads), 0, stream, it, sp);         \
-  } while (0)
-  if (bits == 2) {
-    if (group_size == 32) UC_STAGE(2, 32);
-    else if (group_size == 64) UC_STAGE(2, 64);
-    else UC_STAGE(2, 128);
-  } else {
-    if (group_size == 32) UC_STAGE(4, 32);
-    else if (group_size == 64) UC_STAGE(4, 64);
-    else UC_STAGE(4, 128);
-  }
-#undef UC_STAGE
-  int rc = check_launch("attn_mq (stage)");
-  if (rc != UC_OK) return rc;
-  MqParams p{};
+  sp.wk = ws;
+  sp.wv = ws + heads_kv * sp.keys_pad * mf::kD;
+  p = MqParams{};
   p.Hq = heads_q;
   p.Hkv = heads_kv;
   p.Lq = query_len;
@@ -580,18 +649,94 @@ extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int grou
   p.row_blocks = ceil_div(p.rows, int64_t(kMqRows));
   p.lq = make_fastdiv(static_cast<uint32_t>(query_len));
   p.per_xcd = ceil_div(p.row_blocks * heads_kv, int64_t(kXcds));
+}
+
+}  // namespace
+}  // namespace uc
+
+extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int group_size, int64_t heads_q,
+                               int64_t heads_kv, int64_t head_dim, int64_t query_len, int q_dtype, int res_dtype,
+                               int out_dtype, float sm_scale, void *workspace, int64_t workspace_bytes,
+                               uc_stream_t stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  UC_REQUIRE(item_host != nullptr, "attn_mq: item is NULL");
+  const uc_kivi_item it = *item_host;
+  int rc = mq_check_config(bits, group_size, heads_q, heads_kv, head_dim, q_dtype, res_dtype, out_dtype);
+  if (rc != UC_OK) return rc;
+  rc = mq_check_item(it, group_size, heads_q, heads_kv, query_len);
+  if (rc != UC_OK) return rc;
+  const int64_t need = uc_kivi_mq_workspace_bytes(heads_kv, head_dim, it.quantized_tokens, it.residual_tokens);
+  UC_REQUIRE(workspace != nullptr && workspace_bytes >= need, "attn_mq: workspace too small (%lld < %lld bytes)",
+             (long long)workspace_bytes, (long long)need);
+  StageParams sp;
+  MqParams p;
+  mq_fill(it, heads_q, heads_kv, query_len, sm_scale, static_cast<_Float16 *>(workspace), sp, p);
+  const dim3 sgrid(static_cast<unsigned>(sp.keys_pad / kTile), static_cast<unsigned>(heads_kv),
+                   static_cast<unsigned>(kMqThreads / kStageThreads));
+  stage_config(bits, group_size, res_dtype, [&](auto b, auto g, auto rd) {
+    hipLaunchKernelGGL((mq_stage_kernel<decltype(b)::value, decltype(g)::value, decltype(rd)::value>), sgrid,
+                       dim3(kStageThreads), 0, stream, it, sp);
+  });
+  rc = check_launch("attn_mq (stage)");
+  if (rc != UC_OK) return rc;
   const dim3 grid(static_cast<unsigned>(p.per_xcd * kXcds));
-#define UC_ATTN(QD)                                                                                \
-  do {                                                                                             \
-    if (out_dtype == UC_BF16)                                                                      \
-      hipLaunchKernelGGL((mq_attention_kernel<QD, UC_BF16>), grid, dim3(kAttnThreads), 0, stream, it, p); \
-    else if (out_dtype == UC_FP16)                                                                 \
-      hipLaunchKernelGGL((mq_attention_kernel<QD, UC_FP16>), grid, dim3(kAttnThreads), 0, stream, it, p); \
-    else                                                                                           \
-      hipLaunchKernelGGL((mq_attention_kernel<QD, UC_FP32>), grid, dim3(kAttnThreads), 0, stream, it, p); \
-  } while (0)
-  if (q_dtype == UC_FP16) UC_ATTN(UC_FP16);
-  else UC_ATTN(UC_BF16);
-#undef UC_ATTN
+  attn_config(q_dtype, out_dtype, [&](auto qd, auto od) {
+    hipLaunchKernelGGL((mq_attention_kernel<decltype(qd)::value, decltype(od)::value>), grid, dim3(kAttnThreads), 0,
+                       stream, it, p);
+  });
   return check_launch("attn_mq");
+}
+
+extern "C" int uc_kivi_attn_mq_batch(const uc_kivi_item *items_host, const int64_t *query_lens, int n_items,
+                                     int bits, int group_size, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
+                                     int q_dtype, int res_dtype, int out_dtype, float sm_scale, void *workspace,
+                                     int64_t workspace_bytes, uc_stream_t stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  UC_REQUIRE(n_items >= 1 && n_items <= kMqMaxBatch, "attn_mq_batch: n_items must be 1..%d (got %d)", kMqMaxBatch,
+             n_items);
+  UC_REQUIRE(items_host != nullptr && query_lens != nullptr, "attn_mq_batch: items or query_lens is NULL");
+  int rc = mq_check_config(bits, group_size, heads_q, heads_kv, head_dim, q_dtype, res_dtype, out_dtype);
+  if (rc != UC_OK) return rc;
+  int64_t need = 0;
+  for (int i = 0; i < n_items; ++i) {
+    rc = mq_check_item(items_host[i], group_size, heads_q, heads_kv, query_lens[i]);
+    if (rc != UC_OK) return rc;
+    need += uc_kivi_mq_workspace_bytes(heads_kv, head_dim, items_host[i].quantized_tokens,
+                                       items_host[i].residual_tokens);
+  }
+  UC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+             "attn_mq_batch: workspace too small (%lld < %lld bytes)", (long long)workspace_bytes, (long long)need);
+  // longest segments first: their work items start first on every XCD
+  int order[kMqMaxBatch];
+  for (int i = 0; i < n_items; ++i) order[i] = i;
+  const auto keys_of = [&](int i) { return items_host[i].quantized_tokens + items_host[i].residual_tokens; };
+  for (int i = 1; i < n_items; ++i)
+    for (int j = i; j > 0 && keys_of(order[j]) > keys_of(order[j - 1]); --j) std::swap(order[j], order[j - 1]);
+  MqBatch b{};
+  b.n = n_items;
+  _Float16 *ws = static_cast<_Float16 *>(workspace);
+  for (int i = 0; i < n_items; ++i) {
+    const int src = order[i];
+    b.it[i] = items_host[src];
+    mq_fill(items_host[src], heads_q, heads_kv, query_lens[src], sm_scale, ws, b.sp[i], b.p[i]);
+    ws += 2 * heads_kv * b.sp[i].keys_pad * mf::kD;  // staged K and V of segment i
+    b.stage_begin[i + 1] = b.stage_begin[i] + b.sp[i].keys_pad / kTile;
+    b.attn_begin[i + 1] = b.attn_begin[i] + b.p[i].row_blocks * heads_kv;
+  }
+  UC_REQUIRE(b.stage_begin[n_items] < (int64_t(1) << 31) && b.attn_begin[n_items] < (int64_t(1) << 31),
+             "attn_mq_batch: launch too large");
+  const dim3 sgrid(static_cast<unsigned>(b.stage_begin[n_items]), static_cast<unsigned>(heads_kv),
+                   static_cast<unsigned>(kMqThreads / kStageThreads));
+  stage_config(bits, group_size, res_dtype, [&](auto bb, auto g, auto rd) {
+    hipLaunchKernelGGL((mq_stage_batch_kernel<decltype(bb)::value, decltype(g)::value, decltype(rd)::value>), sgrid,
+                       dim3(kStageThreads), 0, stream, b);
+  });
+  rc = check_launch("attn_mq_batch (stage)");
+  if (rc != UC_OK) return rc;
+  const dim3 grid(static_cast<unsigned>(b.attn_begin[n_items]));
+  attn_config(q_dtype, out_dtype, [&](auto qd, auto od) {
+    hipLaunchKernelGGL((mq_attention_batch_kernel<decltype(qd)::value, decltype(od)::value>), grid,
+                       dim3(kAttnThreads), 0, stream, b);
+  });
+  return check_launch("attn_mq_batch");
 }

@@ -8,6 +8,7 @@ closed: a missing library raises RuntimeError, never a CPU or torch fallback.
 
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 from typing import TYPE_CHECKING, Callable
@@ -230,6 +231,78 @@ def packed_summary_with_dense(
         res_code, nat.dtype_code(q.dtype), 1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device),
     )
     return out, lse
+
+
+MQ_MAX_BATCH = 8  # segments per uc_kivi_attn_mq_batch launch
+
+
+def packed_batch_with_dense(items: list) -> None:
+    """packed_summary_with_dense for several independent segments in one stage
+    and one attention launch per MQ_MAX_BATCH of them (uc_kivi_attn_mq_batch):
+    the per-sample loop of apply_static_physical_attention_batch
+    (adapters/bagel.py:773-980) for samples whose layout is one packed prefix
+    plus dense keys.  items: (cache, query [Lq, Hq, D], key_parts, value_parts,
+    out [Lq, Hq, D]) where the parts are lists of [T_j, Hkv, D] tensors whose
+    concatenation is the item's dense keys / values; every out (contiguous,
+    the query dtype) is written in place.  The dense parts of all items are
+    gathered by one concatenation per launch.  All items share bits, group
+    size, heads, the 16-bit query dtype and the dense dtype (that of the first
+    key part), and take the multi-query path (Lq above the decode limit); the
+    results equal packed_summary_with_dense bit for bit."""
+
+    if not items:
+        return
+    cache0, q0 = items[0][0], items[0][1]
+    dtype = items[0][2][0].dtype
+    hq, d = int(q0.shape[1]), int(q0.shape[2])
+    if d != 128 or cache0.group_size not in (32, 64, 128) or cache0.k_bits not in (2, 4):
+        raise ValueError("Batched packed attention needs head_dim 128, group 32/64/128 and 2/4-bit codes")
+    if q0.dtype not in (torch.bfloat16, torch.float16) or dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("Batched packed attention needs 16-bit queries and dense keys")
+    for cache, query, kparts, vparts, out in items:
+        if (cache.k_bits, cache.v_bits, cache.group_size, cache.num_kv_heads) != (
+                cache0.k_bits, cache0.k_bits, cache0.group_size, cache0.num_kv_heads):
+            raise ValueError("Batched packed attention needs equal bits, group size and KV heads")
+        if not cache.quantized_tokens:
+            raise ValueError("Packed KIVI summary requires a non-empty quantized prefix")
+        _check_native(cache, "Batched packed attention")
+        if query.dtype != q0.dtype or out.dtype != q0.dtype:
+            raise ValueError("Batched packed attention needs one query dtype")
+        if tuple(query.shape[1:]) != (hq, d) or out.shape != query.shape or len(kparts) != len(vparts) or any(
+                x.shape != y.shape or x.dim() != 3 or tuple(x.shape[1:]) != (cache.num_kv_heads, d)
+                for x, y in zip(kparts, vparts)):
+            raise ValueError("Batched packed attention: inconsistent query, output or dense shapes")
+        if not (query.is_contiguous() and out.is_contiguous()):
+            raise ValueError("Batched packed attention needs contiguous queries and outputs")
+        if int(query.shape[0]) <= _max_decode_query_len(cache, hq):
+            raise ValueError("Batched packed attention covers multi-query segments only")
+    device = nat.require_device(q0, cache0.key_code, items[0][2][0], what="Batched packed attention")
+    for start in range(0, len(items), MQ_MAX_BATCH):
+        chunk = items[start:start + MQ_MAX_BATCH]
+        dk = torch.cat([x.to(dtype) for item in chunk for x in item[2]], dim=0)
+        dv = torch.cat([x.to(dtype) for item in chunk for x in item[3]], dim=0)
+        row_bytes = int(dk.stride(0)) * dk.element_size()
+        table = (nat.KiviItem * len(chunk))()
+        lens = (ctypes.c_int64 * len(chunk))()
+        ws_bytes = 0
+        row = 0
+        for j, (cache, query, kparts, _, out) in enumerate(chunk):
+            tr = sum(int(x.shape[0]) for x in kparts)
+            table[j] = nat.KiviItem(
+                cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
+                cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
+                dk.data_ptr() + row * row_bytes if tr else None, dv.data_ptr() + row * row_bytes if tr else None,
+                query.data_ptr(), out.data_ptr(), None, cache.quantized_tokens, tr,
+            )
+            row += tr
+            lens[j] = int(query.shape[0])
+            ws_bytes += nat.mq_workspace_bytes(cache.num_kv_heads, d, cache.quantized_tokens, tr)
+        ws = nat.workspace(device, ws_bytes)
+        nat.call(
+            "uc_kivi_attn_mq_batch", table, lens, len(chunk), cache0.k_bits, cache0.group_size, hq,
+            cache0.num_kv_heads, d, nat.dtype_code(q0.dtype), nat.dtype_code(dtype), nat.dtype_code(q0.dtype),
+            1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device),
+        )
 
 
 def dense_attention_summary(
