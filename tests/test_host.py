@@ -77,3 +77,20 @@ def test_operator_params_and_requests():
     with pytest.raises(ValueError):
         PhysicalCacheRequest(operator="x", segment_id="s", token_count=5, segment_mask=mask,
                              per_kv_head_scores=torch.zeros(2, 4))
+
+
+def test_batched_attention_argument_checks():
+    # run_batched_physical_attention (apply_static_physical_attention_batch,
+    # adapters/bagel.py:773-980) checks its varlen table on the host before any
+    # launch; the batch launcher rejects an empty or mixed item list the same way
+    from unicache_amd.adapters import run_batched_physical_attention
+
+    q = torch.zeros(6, 28, 128, dtype=torch.bfloat16)
+    k = torch.zeros(5, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="one more entry"):
+        run_batched_physical_attention(q, k, k, [0, 6], [0, 5], [[], []])
+    with pytest.raises(ValueError, match="must cover q and k"):
+        run_batched_physical_attention(q, k, k, [0, 3, 5], [0, 2, 5], [[], []])
+    with pytest.raises(ValueError, match="no physical segments"):
+        run_batched_physical_attention(q, k, k, [0, 3, 6], [0, 2, 5], [[], []])
+    kivi_cuda.packed_batch_with_dense([])  # nothing to launch
