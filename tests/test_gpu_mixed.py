@@ -203,3 +203,26 @@ def test_batched_packed_launch_matches_per_sample_passes(device):
         want = run_fused_mixed_attention(q[cu_q[i]:cu_q[i + 1]], k[cu_k[i]:cu_k[i + 1]], v[cu_k[i]:cu_k[i + 1]],
                                          [caches[c]])
         assert torch.equal(out[cu_q[i]:cu_q[i + 1]], want), f"sample {i}"
+
+
+def test_multi_prefix_launch_matches_separate_passes(device):
+    # two packed prefixes with long queries: both passes share one batched
+    # launch; the merged output equals one pass per prefix + LSE merge bit for bit
+    from unicache_amd.adapters.bagel import merge_attention_summaries
+    from unicache_amd.storage.kivi_cuda import packed_kivi_quantized_attention_summary, packed_summary_with_dense
+
+    segments = []
+    for j, n in enumerate((1000, 700)):
+        ck, cv = kv_pair(n, seed=80 + j)
+        segments.append(PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(n),
+                                                   token_type_id=3, k_bits=2, v_bits=2, group_size=32,
+                                                   residual_length=128, backend="cuda"))
+    q = queries(150, seed=82).to(device)
+    dk, dv = (x.to(device) for x in kv_pair(90, seed=83))
+    out, lse = run_fused_mixed_attention(q, dk, dv, segments, return_lse=True)
+    keys = torch.cat([dk] + [s.residual_key for s in segments if s.residual_tokens], dim=0)
+    values = torch.cat([dv] + [s.residual_value for s in segments if s.residual_tokens], dim=0)
+    parts = [packed_summary_with_dense(segments[0], q, keys, values),
+             packed_kivi_quantized_attention_summary(segments[1], q)]
+    want, want_lse = merge_attention_summaries(parts)
+    assert torch.equal(out, want) and torch.equal(lse, want_lse)

@@ -58,12 +58,13 @@ def run_fused_mixed_attention(
 
     The bf16 keys are gathered in UniCache's order [dense, H2O..., residuals...]
     and attended in the same fused pass as the first packed segment's prefix;
-    further packed prefixes get their own pass and the summaries are merged by
-    LSE.  Non-frozen H2O segments then receive exp(logit - global LSE) as
+    further packed prefixes get their own pass (all passes in one batched
+    launch for long queries) and the summaries are merged by LSE.  Non-frozen H2O segments then receive exp(logit - global LSE) as
     bf16 probabilities and are trimmed to their budget.  Returns the output
     (and the global LSE [Hq, Lq] with return_lse=True)."""
 
-    from ..storage.kivi_cuda import packed_kivi_quantized_attention_summary, packed_summary_with_dense
+    from ..storage.kivi_cuda import (_max_decode_query_len, packed_batch_with_dense,
+                                     packed_kivi_quantized_attention_summary, packed_summary_with_dense)
     from ..storage.physical import GQAH2OCache, PackedKIVICache
 
     h2o = [s for s in physical_segments if isinstance(s, GQAH2OCache)]
@@ -76,8 +77,24 @@ def run_fused_mixed_attention(
         s.residual_value for s in packed if s.residual_tokens]
     all_key = torch.cat([k.to(dense_key.dtype) for k in keys], dim=0)
     all_value = torch.cat([v.to(dense_value.dtype) for v in values], dim=0)
-    summaries = [packed_summary_with_dense(with_prefix[0], query, all_key, all_value)]
-    summaries += [packed_kivi_quantized_attention_summary(s, query) for s in with_prefix[1:]]
+    first = with_prefix[0]
+    lq, hq, d = map(int, query.shape)
+    if (len(with_prefix) > 1 and query.dtype in (torch.bfloat16, torch.float16)
+            and all_key.dtype in (torch.bfloat16, torch.float16) and all_value.dtype == all_key.dtype and d == 128
+            and first.group_size in (32, 64, 128) and first.k_bits in (2, 4) and lq > _max_decode_query_len(first, hq)
+            and all((s.k_bits, s.v_bits, s.group_size, s.num_kv_heads) == (first.k_bits, first.k_bits,
+                                                                          first.group_size, first.num_kv_heads)
+                    for s in with_prefix)):
+        # every packed prefix in one stage and one attention launch (the first
+        # with the dense keys), the same summaries as one pass per prefix
+        q = query.contiguous()
+        summaries = [(torch.empty_like(q), torch.empty((hq, lq), dtype=torch.float32, device=q.device))
+                     for _ in with_prefix]
+        packed_batch_with_dense([(s, q, [all_key] if j == 0 else [], [all_value] if j == 0 else [], o, lse)
+                                 for j, (s, (o, lse)) in enumerate(zip(with_prefix, summaries))])
+    else:
+        summaries = [packed_summary_with_dense(first, query, all_key, all_value)]
+        summaries += [packed_kivi_quantized_attention_summary(s, query) for s in with_prefix[1:]]
     output, global_lse = summaries[0] if len(summaries) == 1 else merge_attention_summaries(summaries)
     for segment in h2o:
         if segment.selection_frozen:

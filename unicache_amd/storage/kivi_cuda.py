@@ -242,9 +242,10 @@ def packed_batch_with_dense(items: list) -> None:
     the per-sample loop of apply_static_physical_attention_batch
     (adapters/bagel.py:773-980) for samples whose layout is one packed prefix
     plus dense keys.  items: (cache, query [Lq, Hq, D], key_parts, value_parts,
-    out [Lq, Hq, D]) where the parts are lists of [T_j, Hkv, D] tensors whose
-    concatenation is the item's dense keys / values; every out (contiguous,
-    the query dtype) is written in place.  The dense parts of all items are
+    out [Lq, Hq, D][, lse [Hq, Lq] fp32]) where the parts are lists (possibly
+    empty) of [T_j, Hkv, D] tensors whose concatenation is the item's dense
+    keys / values; every out (contiguous, the query dtype) and lse is written
+    in place.  The dense parts of all items are
     gathered by one concatenation per launch.  All items share bits, group
     size, heads, the 16-bit query dtype and the dense dtype (that of the first
     key part), and take the multi-query path (Lq above the decode limit); the
@@ -253,13 +254,17 @@ def packed_batch_with_dense(items: list) -> None:
     if not items:
         return
     cache0, q0 = items[0][0], items[0][1]
-    dtype = items[0][2][0].dtype
+    dtype = next((x.dtype for item in items for x in item[2]), q0.dtype)
     hq, d = int(q0.shape[1]), int(q0.shape[2])
     if d != 128 or cache0.group_size not in (32, 64, 128) or cache0.k_bits not in (2, 4):
         raise ValueError("Batched packed attention needs head_dim 128, group 32/64/128 and 2/4-bit codes")
     if q0.dtype not in (torch.bfloat16, torch.float16) or dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("Batched packed attention needs 16-bit queries and dense keys")
-    for cache, query, kparts, vparts, out in items:
+    for cache, query, kparts, vparts, out, *rest in items:
+        lse = rest[0] if rest else None
+        if lse is not None and (lse.dtype != torch.float32 or tuple(lse.shape) != (hq, int(query.shape[0]))
+                                or not lse.is_contiguous()):
+            raise ValueError("Batched packed attention: lse must be contiguous fp32 [Hq, Lq]")
         if (cache.k_bits, cache.v_bits, cache.group_size, cache.num_kv_heads) != (
                 cache0.k_bits, cache0.k_bits, cache0.group_size, cache0.num_kv_heads):
             raise ValueError("Batched packed attention needs equal bits, group size and KV heads")
@@ -276,23 +281,27 @@ def packed_batch_with_dense(items: list) -> None:
             raise ValueError("Batched packed attention needs contiguous queries and outputs")
         if int(query.shape[0]) <= _max_decode_query_len(cache, hq):
             raise ValueError("Batched packed attention covers multi-query segments only")
-    device = nat.require_device(q0, cache0.key_code, items[0][2][0], what="Batched packed attention")
+    device = nat.require_device(q0, cache0.key_code, what="Batched packed attention")
     for start in range(0, len(items), MQ_MAX_BATCH):
         chunk = items[start:start + MQ_MAX_BATCH]
-        dk = torch.cat([x.to(dtype) for item in chunk for x in item[2]], dim=0)
-        dv = torch.cat([x.to(dtype) for item in chunk for x in item[3]], dim=0)
-        row_bytes = int(dk.stride(0)) * dk.element_size()
+        kparts = [x.to(dtype) for item in chunk for x in item[2]]
+        vparts = [x.to(dtype) for item in chunk for x in item[3]]
+        dk = torch.cat(kparts, dim=0) if kparts else None
+        dv = torch.cat(vparts, dim=0) if vparts else None
+        row_bytes = int(dk.stride(0)) * dk.element_size() if dk is not None else 0
         table = (nat.KiviItem * len(chunk))()
         lens = (ctypes.c_int64 * len(chunk))()
         ws_bytes = 0
         row = 0
-        for j, (cache, query, kparts, _, out) in enumerate(chunk):
+        for j, (cache, query, kparts, _, out, *rest) in enumerate(chunk):
+            lse = rest[0] if rest else None
             tr = sum(int(x.shape[0]) for x in kparts)
             table[j] = nat.KiviItem(
                 cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
                 cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
                 dk.data_ptr() + row * row_bytes if tr else None, dv.data_ptr() + row * row_bytes if tr else None,
-                query.data_ptr(), out.data_ptr(), None, cache.quantized_tokens, tr,
+                query.data_ptr(), out.data_ptr(), lse.data_ptr() if lse is not None else None,
+                cache.quantized_tokens, tr,
             )
             row += tr
             lens[j] = int(query.shape[0])
