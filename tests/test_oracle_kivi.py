@@ -209,3 +209,97 @@ def test_streamed_split_matches_closed_form(initial, appended, flush_at, group):
     if initial < flush_at:
         assert packed == flush_at * ((initial + appended) // flush_at)
     assert packed % group == 0 and 0 <= initial + appended - packed < flush_at + group
+
+
+# ------------------------------------------------------ dequantize pinned --
+def _hand_segment(native: bool) -> K.PackedSegment:
+    """One KV head, 16 channels, 32 tokens, G=16, 2-bit, built word by word.
+
+    Every key channel d holds the codes [0,1,2,3]*4 in both of its words
+    (0xE4E4E4E4); group 0 has scale 0.5 / minimum -1, group 1 scale 2 /
+    minimum 3.  Every value token t holds the codes [3,2,1,0]*4
+    (0x1B1B1B1B) with scale 0.25 and minimum t.  All stats are exact in fp16
+    and bf16, so the expected values below are exact.
+    """
+
+    word_k = np.uint32(0xE4E4E4E4).view(np.int32)
+    word_v = np.uint32(0x1B1B1B1B).view(np.int32)
+    kc = np.full((1, 16, 2), word_k, dtype=np.int32)               # [Hkv, D, T/16]
+    ks = np.tile(np.array([0.5, 2.0], np.float32), (1, 16, 1))     # [Hkv, D, T/G]
+    km = np.tile(np.array([-1.0, 3.0], np.float32), (1, 16, 1))
+    vc = np.full((1, 32, 1), word_v, dtype=np.int32)               # [Hkv, T, D/16]
+    vs = np.full((1, 32, 1), 0.25, np.float32)                     # [Hkv, T, D/G]
+    vm = np.arange(32, dtype=np.float32).reshape(1, 32, 1)
+    if not native:  # UniCache's reference layout: K [T/16, Hkv, D], V [T, Hkv, D/16]
+        kc, ks, km = (np.ascontiguousarray(np.transpose(a, (2, 0, 1))) for a in (kc, ks, km))
+        vc, vs, vm = (np.ascontiguousarray(np.transpose(a, (1, 0, 2))) for a in (vc, vs, vm))
+    empty = np.zeros((0, 1, 16), np.float32)
+    return K.PackedSegment(kc, ks, km, vc, vs, vm, empty, empty, k_bits=2, v_bits=2, group_size=16,
+                           quantized_tokens=32, native=native)
+
+
+@pytest.mark.parametrize("native", [True, False])
+def test_dequantize_hand_built_words(native):
+    key, value = K.dequantize(_hand_segment(native), "fp32")
+    assert key.shape == (32, 1, 16) and value.shape == (32, 1, 16)
+    # keys: token t of channel d has code t % 4; group 0 -> code*0.5 - 1, group 1 -> code*2 + 3
+    assert key[:16, 0, 0].tolist() == [-1.0, -0.5, 0.0, 0.5] * 4
+    assert key[16:, 0, 0].tolist() == [3.0, 5.0, 7.0, 9.0] * 4
+    assert np.array_equal(key, np.broadcast_to(key[:, :, :1], key.shape))  # same in every channel
+    # values: channel c of token t has code 3 - c % 4, scale 0.25, minimum t
+    assert value[0, 0].tolist() == [0.75, 0.5, 0.25, 0.0] * 4
+    assert value[5, 0].tolist() == [5.75, 5.5, 5.25, 5.0] * 4
+    assert value[31, 0, :4].tolist() == [31.75, 31.5, 31.25, 31.0]
+
+
+def test_dequantize_hand_built_bf16_cast():
+    # with minimum 3 + 2^-6: 3 + 2^-6 is a bf16 value, 9 + 2^-6 is not and the
+    # output cast rounds it to 9 (a quarter ulp away)
+    seg = _hand_segment(True)
+    seg.key_minimum = seg.key_minimum + np.float32(2.0 ** -6)
+    key, _ = K.dequantize(seg, "bf16")
+    assert key[16, 0, 0] == 3.015625 and key[19, 0, 0] == 9.0 and key[0, 0, 0] == -0.984375
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_round_trip_error_bound_per_element(bits):
+    # |dequant(quant(x)) - x| <= s/2 from the rounding of the code, plus what
+    # storing s and m in fp16 (native) or bf16 (reference layout) and the final
+    # bf16 cast add: code*|s'-s| + |m'-m| + half an output ulp.
+    rng = np.random.default_rng(21 + bits)
+    key = rng.standard_normal((160, 2, 64)).astype(np.float32)
+    key[:, :, 5] *= 10.0
+    key = K.round_bf16(key)
+    value = K.round_bf16(rng.standard_normal((160, 2, 64)).astype(np.float32))
+    native = bits != 8
+    seg = K.from_dense(key, value, k_bits=bits, v_bits=bits, group_size=32, residual_length=0, native=native)
+    rk, rv = K.dequantize(seg, "bf16")
+    storage_ulp = 2.0 ** -10 if native else 2.0 ** -7  # relative half-ulp of fp16 / bf16 stats
+    top = (1 << bits) - 1
+    for x, r, gdim in ((key, rk, 0), (value, rv, 2)):
+        _, scale, mn = K.quantize_codes(x, bits=bits, group_dim=gdim, group_size=32)
+        s = np.repeat(scale, 32, axis=gdim).astype(np.float64)
+        m = np.repeat(mn, 32, axis=gdim).astype(np.float64)
+        bound = s / 2 * (1 + 1e-5) + top * s * storage_ulp + np.abs(m) * storage_ulp \
+            + np.abs(r.astype(np.float64)) * 2.0 ** -8
+        err = np.abs(r.astype(np.float64) - x)
+        assert np.all(err <= bound), float((err - bound).max())
+        # and the bound is tight enough to mean something: most errors use < s/2
+        assert float(np.mean(err <= s / 2 + 1e-6)) > 0.5
+
+
+def test_native_mean_error_not_worse_than_reference_layout():
+    # test_physical.py:1056-1068: the kernel-native cache's mean reconstruction
+    # error is at most 1.1x the reference layout's plus 1e-3
+    rng = np.random.default_rng(6)
+    key = K.round_bf16(rng.standard_normal((128, 2, 64)).astype(np.float32))
+    value = K.round_bf16(rng.standard_normal((128, 2, 64)).astype(np.float32))
+    nat = K.from_dense(key, value, k_bits=2, v_bits=2, group_size=64, residual_length=0, native=True)
+    ref = K.from_dense(key, value, k_bits=2, v_bits=2, group_size=64, residual_length=0, native=False)
+    for original, native_out, ref_out in zip((key, value), K.dequantize(nat, "bf16"), K.dequantize(ref, "bf16")):
+        assert np.isfinite(native_out).all()
+        native_error = np.abs(native_out - original).mean()
+        ref_error = np.abs(ref_out - original).mean()
+        assert native_error <= ref_error * 1.10 + 1e-3
+        # 2-bit codes over G=64 leave a mean error well under one scale step
+        assert 0.05 < native_error < 0.5
