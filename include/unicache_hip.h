@@ -205,6 +205,26 @@ int uc_kivi_attn_decode(const uc_kivi_item *item_host, int bits, int group_size,
                         void *workspace, int64_t workspace_bytes, uc_stream_t stream);
 
 /*
+ * uc_kivi_attn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No reference counterpart.  The split
+ * partials go to a fixed scratch array inside the library, one per GPU, of
+ * uc_kivi_decode_scratch_bytes() bytes (8 MiB: a 2-bit head_dim-128 segment of
+ * about 400k tokens at 4 KV heads); a call that would need more returns
+ * UC_EINVAL.  The call allocates nothing.  Every call on one GPU shares that
+ * GPU's scratch: calls that overlap on one GPU (different streams or host
+ * threads without ordering) race and give wrong results.  The device current
+ * on the calling thread must be the one that owns the item's tensors and
+ * `stream`.  Results equal uc_kivi_attn_decode's bit for bit.
+ */
+int uc_kivi_attn_decode_static(const uc_kivi_item *item_host, int bits, int group_size,
+                               int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t query_len,
+                               int q_dtype, int res_dtype, int out_dtype, float sm_scale, uc_stream_t stream);
+
+/* Size in bytes of the scratch array behind uc_kivi_attn_decode_static. */
+int64_t uc_kivi_decode_scratch_bytes(void);
+
+/*
  * The same kernel over `n_items` segments (sequences x layers) in one launch.
  * `items_device` is a device array of uc_kivi_item; every item shares bits,
  * group, head counts and query_len; token counts may differ, up to

@@ -76,6 +76,11 @@ _SIGNATURES = {
         _I,
         [ctypes.POINTER(KiviItem), _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _P, _L, _P],
     ),
+    "uc_kivi_attn_decode_static": (
+        _I,
+        [ctypes.POINTER(KiviItem), _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _P],
+    ),
+    "uc_kivi_decode_scratch_bytes": (_L, []),
     "uc_kivi_attn_decode_batch": (
         _I,
         [_P, _L, _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _L, _L, _P, _L, _P],

@@ -4,6 +4,8 @@
 // Geometry: one workgroup owns (item, KV head, token split).  The
 // group*query_len <= 16 query rows that share a KV head live in LDS, so
 // every packed word and scale is read from HBM once per (item, KV head).
+#include <mutex>
+
 #include "uc_common.h"
 #include "uc_decode.h"
 
@@ -618,4 +620,62 @@ extern "C" int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t 
   c.od = out_dtype;
   hipLaunchKernelGGL((decode_combine_kernel<false>), cgrid, dim3(128), 0, s, nullptr, it, c);
   return check_launch("uc_kivi_av");
+}
+
+// ------------------------------------------------- allocation-free decode --
+// Split partials of uc_kivi_attn_decode_static live in this file-scope array
+// (one copy per GPU, held until the process ends).  Host code never passes
+// `scratch` itself to a kernel: its name is a host-side stand-in.  The device
+// address comes from hipGetSymbolAddress, once per device, on that device's
+// first call.
+static constexpr int64_t kDecodeScratchBytes = int64_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+namespace {
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchMaxDevices];
+
+// Device address of `scratch` on the calling thread's current device.
+int scratch_address(void **out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  UC_REQUIRE_RT(err == hipSuccess, "uc_kivi_attn_decode_static: hipGetDevice failed: %s", hipGetErrorString(err));
+  UC_REQUIRE_RT(dev >= 0 && dev < kScratchMaxDevices, "uc_kivi_attn_decode_static: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    UC_REQUIRE_RT(err == hipSuccess && p != nullptr,
+                  "uc_kivi_attn_decode_static: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(err));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return UC_OK;
+}
+}  // namespace
+
+extern "C" int64_t uc_kivi_decode_scratch_bytes(void) { return kDecodeScratchBytes; }
+
+extern "C" int uc_kivi_attn_decode_static(const uc_kivi_item *item_host, int bits, int group_size,
+                                          int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t query_len,
+                                          int q_dtype, int res_dtype, int out_dtype, float sm_scale,
+                                          uc_stream_t stream) {
+  UC_REQUIRE(item_host != nullptr, "uc_kivi_attn_decode_static: item is NULL");
+  UC_REQUIRE(item_host->quantized_tokens >= 0 && item_host->residual_tokens >= 0,
+             "uc_kivi_attn_decode_static: negative token count");
+  const int64_t need = uc_kivi_decode_workspace_bytes(1, bits, group_size, heads_q, heads_kv, head_dim, query_len,
+                                                      item_host->quantized_tokens, item_host->residual_tokens);
+  UC_REQUIRE(need >= 0, "uc_kivi_attn_decode_static: bad arguments");
+  UC_REQUIRE(need <= kDecodeScratchBytes,
+             "uc_kivi_attn_decode_static: the call needs %lld bytes of split scratch, more than the library's "
+             "fixed %lld (use uc_kivi_attn_decode with a workspace)",
+             (long long)need, (long long)kDecodeScratchBytes);
+  void *ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != UC_OK) return rc;
+  return decode_common(nullptr, item_host, 1, bits, group_size, heads_q, heads_kv, head_dim, query_len, q_dtype,
+                       res_dtype, out_dtype, sm_scale, item_host->quantized_tokens, item_host->residual_tokens, ws,
+                       kDecodeScratchBytes, as_stream(stream), "uc_kivi_attn_decode_static");
 }
