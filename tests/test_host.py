@@ -37,9 +37,13 @@ def test_cpu_tensors_fail_closed():
     with pytest.raises(RuntimeError, match="CUDA"):
         PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3, k_bits=2,
                                    v_bits=2, group_size=32, residual_length=0, backend="cuda")
-    with pytest.raises(RuntimeError, match="reference"):
+    for backend in ("reference", "cuda"):  # both backends run on the HIP kernels only
+        with pytest.raises(RuntimeError, match="GPU|CUDA"):
+            PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3, k_bits=2,
+                                       v_bits=2, group_size=32, residual_length=0, backend=backend)
+    with pytest.raises(ValueError, match="Unknown KIVI physical backend"):
         PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3, k_bits=2,
-                                   v_bits=2, group_size=32, residual_length=0, backend="reference")
+                                   v_bits=2, group_size=32, residual_length=0, backend="triton")
     with pytest.raises(RuntimeError):
         GQAH2OCache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=1,
                                per_kv_head_scores=torch.rand(4, 64), target_tokens=8, recent_tokens=2)

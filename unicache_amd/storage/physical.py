@@ -5,10 +5,14 @@ arguments, attributes, return layouts and exceptions.  Every tensor operation
 on the cache contents (pack, dequantize, QK/AV, H2O selection and gather) runs
 in libunicache_hip.so; torch only allocates memory and orders streams.
 
-Backends: ``backend="cuda"`` (the engine's only GPU backend in UniCache) maps
-to the HIP kernels.  UniCache's ``backend="reference"`` is its CPU test oracle;
-this package does not ship a CPU path, so it is rejected with a RuntimeError
-(the CPU restatement lives under ``oracle/`` as test infrastructure).
+Backends, both on the HIP kernels: ``backend="cuda"`` stores 2/4-bit caches
+in KIVI's kernel-native layout (fp16 stats) that the fused attention kernels
+read; ``backend="reference"`` (UniCache's default) stores UniCache's own
+layout -- codes packed along tokens (keys) / channels (values), stats in the
+input dtype -- and attends by dequantizing, as UniCache's reference backend
+does (physical.py:452-475).  UniCache runs its reference backend on CPU
+tensors as well; here every backend needs GPU tensors and raises
+RuntimeError otherwise (there is no CPU path).
 """
 
 from __future__ import annotations
@@ -26,13 +30,8 @@ def tensor_bytes(tensor: torch.Tensor | None) -> int:
     return 0 if tensor is None else int(tensor.numel() * tensor.element_size())
 
 
-def _require_hip_backend(backend: str) -> None:
-    if backend == "reference":
-        raise RuntimeError(
-            "The MI355X engine implements the 'cuda' physical backend on HIP kernels only; "
-            "UniCache's CPU 'reference' backend is not part of this build"
-        )
-    if backend != "cuda":
+def _check_backend(backend: str) -> None:
+    if backend not in ("cuda", "reference"):
         raise ValueError(f"Unknown KIVI physical backend: {backend}")
 
 
@@ -216,7 +215,7 @@ class PackedKIVICache:
     quantized_tokens: int
     head_dim: int
     num_kv_heads: int
-    backend: str = "cuda"
+    backend: str = "reference"
     kernel_native_layout: bool = False
     budget_shortfall_events: int = 0
 
@@ -232,7 +231,7 @@ class PackedKIVICache:
         v_bits: int,
         group_size: int,
         residual_length: int,
-        backend: str = "cuda",
+        backend: str = "reference",
     ) -> "PackedKIVICache":
         """Split [tokens, Hkv, D] K/V into a group-aligned packed prefix and a
         residual suffix (physical.py:228-332)."""
@@ -244,7 +243,7 @@ class PackedKIVICache:
         tokens, heads, head_dim = map(int, key.shape)
         if group_size <= 0:
             raise ValueError("KIVI physical cache group_size must be positive")
-        _require_hip_backend(backend)
+        _check_backend(backend)
         if group_size not in {16, 32, 64, 128}:
             raise ValueError("The MI355X KIVI kernels support group_size 16, 32, 64 or 128")
         if head_dim % group_size != 0:
@@ -253,7 +252,7 @@ class PackedKIVICache:
         # keep any incomplete prefix group in the residual (physical.py:258-263)
         quantized = ((tokens - requested_residual) // group_size) * group_size
         q_key, q_value = key[:quantized], value[:quantized]
-        kernel_native_layout = bool(quantized and k_bits in {2, 4} and v_bits in {2, 4})
+        kernel_native_layout = bool(backend == "cuda" and quantized and k_bits in {2, 4} and v_bits in {2, 4})
         if quantized:
             if kernel_native_layout:
                 from .kivi_cuda import quantize_kivi_native
@@ -295,6 +294,17 @@ class PackedKIVICache:
     @property
     def token_count(self) -> int:
         return int(self.logical_token_ids.numel())
+
+    @property
+    def mutation_count(self) -> int:
+        """How many times this cache has replaced or grown its tensors (append,
+        flush_residual, repack_monotonic).  Item tables holding raw pointers
+        into the cache compare it to notice that they are stale."""
+
+        return getattr(self, "_mutations", 0)
+
+    def _mutated(self) -> None:
+        self._mutations = self.mutation_count + 1
 
     @property
     def residual_tokens(self) -> int:
@@ -401,9 +411,10 @@ class PackedKIVICache:
             residual_length=int(self.residual_key.shape[0]),
             backend=self.backend,
         )
-        shortfalls = self.budget_shortfall_events
+        shortfalls, mutations = self.budget_shortfall_events, self.mutation_count
         self.__dict__.update(replacement.__dict__)
         self.budget_shortfall_events = shortfalls
+        self._mutations = mutations + 1
         return True
 
     # ------------------------------------------------------------ streaming --
@@ -442,6 +453,7 @@ class PackedKIVICache:
         cap[1][tr:tr + n].copy_(value)
         self.residual_key, self.residual_value = cap[0][:tr + n], cap[1][:tr + n]
         self.logical_token_ids = torch.cat([self.logical_token_ids, logical_token_ids.to(self.logical_token_ids)])
+        self._mutated()
         if flush_at is not None and self.residual_tokens >= int(flush_at):
             return self.flush_residual()
         return 0
@@ -457,8 +469,8 @@ class PackedKIVICache:
             return 0
         if self.k_bits != self.v_bits or self.k_bits not in (2, 4):
             raise ValueError("Streaming KIVI flush supports equal 2-bit or 4-bit K/V")
-        if self.quantized_tokens and not self.kernel_native_layout:
-            raise RuntimeError("Streaming KIVI flush requires the kernel-native layout")
+        if self.backend != "cuda" or (self.quantized_tokens and not self.kernel_native_layout):
+            raise RuntimeError("Streaming KIVI flush requires the kernel-native layout (backend='cuda')")
         from .kivi_cuda import quantize_kivi_native
 
         new = quantize_kivi_native(self.residual_key[:count], self.residual_value[:count],
@@ -476,6 +488,7 @@ class PackedKIVICache:
         rest_v = self.residual_value[count:].clone()
         self.residual_key, self.residual_value = rest_k, rest_v
         self._residual_capacity = None
+        self._mutated()
         return count
 
     def attention_parts(
@@ -484,10 +497,18 @@ class PackedKIVICache:
         """Scaled logits over [packed | residual] and an AV closure
         (physical.py:452-475)."""
 
-        _require_hip_backend(self.backend)
-        from .kivi_cuda import packed_kivi_attention_parts
+        _check_backend(self.backend)
+        if self.backend == "cuda":
+            from .kivi_cuda import packed_kivi_attention_parts
 
-        return packed_kivi_attention_parts(self, query)
+            return packed_kivi_attention_parts(self, query)
+        key, value = self.dequantize(dtype=query.dtype)
+        logits = _dense_qk(query, key, scale=1.0 / math.sqrt(query.shape[-1]))
+
+        def apply_value(probabilities: torch.Tensor) -> torch.Tensor:
+            return gqa_probability_value(probabilities, value)
+
+        return logits, apply_value
 
 
 # ------------------------------------------------------------------- H2O --
