@@ -36,11 +36,16 @@ def _segments(device, *, second_packed):
                                          backend="cuda")]
     segs = [K.from_dense(f32(pk), f32(pv), k_bits=2, v_bits=2, group_size=32, residual_length=128)]
     if second_packed:
+        # "mixed": a 4-bit / group-64 prefix (its own pass); "same": a second
+        # 2-bit / group-32 prefix (both prefixes in one batched launch when the
+        # queries are long)
+        bits, group, resid = (4, 64, 32) if second_packed == "mixed" else (2, 32, 128)
         sk, sv = kv_pair(700, seed=25)
         packed.append(PackedKIVICache.from_dense(sk.to(device), sv.to(device), logical_token_ids=torch.arange(700),
-                                                 token_type_id=4, k_bits=4, v_bits=4, group_size=64,
-                                                 residual_length=32, backend="cuda"))
-        segs.append(K.from_dense(f32(sk), f32(sv), k_bits=4, v_bits=4, group_size=64, residual_length=32))
+                                                 token_type_id=4, k_bits=bits, v_bits=bits, group_size=group,
+                                                 residual_length=resid, backend="cuda"))
+        segs.append(K.from_dense(f32(sk), f32(sv), k_bits=bits, v_bits=bits, group_size=group,
+                                 residual_length=resid))
     return (dk, dv), [h2o_live, h2o_frozen], packed, segs
 
 
@@ -63,7 +68,7 @@ def _oracle_keys(dense, h2o, segs):
 
 
 @pytest.mark.parametrize("lq", [1, 40])
-@pytest.mark.parametrize("second_packed", [False, True])
+@pytest.mark.parametrize("second_packed", [None, "mixed", "same"])
 def test_mixed_attention_matches_global_softmax(device, lq, second_packed):
     dense, h2o, packed, segs = _segments(device, second_packed=second_packed)
     q = queries(lq, seed=30 + lq)
@@ -131,6 +136,8 @@ def test_segment_table_decode_matches_global_softmax(device):
     # a streaming append to group 1's residual, then refresh
     nk, nv = kv_pair(5, seed=46)
     c1.append(nk.to(device), nv.to(device), logical_token_ids=torch.arange(700, 705))
+    with pytest.raises(RuntimeError, match="refresh"):  # the table still points at the old residual
+        batch.run()
     batch.refresh()
     batch.run()
     s1.residual_key = np.concatenate([s1.residual_key, f32(nk)])
@@ -226,3 +233,70 @@ def test_multi_prefix_launch_matches_separate_passes(device):
              packed_kivi_quantized_attention_summary(segments[1], q)]
     want, want_lse = merge_attention_summaries(parts)
     assert torch.equal(out, want) and torch.equal(lse, want_lse)
+
+
+def test_batched_launch_rejects_bad_items_before_launch(device):
+    # every table pointer is checked on the host: a CPU dense part, mixed
+    # bits, a mixed query dtype, a bad LSE shape and decode-length queries
+    # raise before anything is launched
+    from unicache_amd.storage.kivi_cuda import packed_batch_with_dense
+
+    def cache(bits, group, seed):
+        ck, cv = kv_pair(500, seed=seed)
+        return PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(500),
+                                          token_type_id=3, k_bits=bits, v_bits=bits, group_size=group,
+                                          residual_length=128, backend="cuda")
+
+    c2, c4 = cache(2, 32, 90), cache(4, 32, 91)
+    q = queries(64, seed=92).to(device)
+    out = torch.empty_like(q)
+    dk, dv = kv_pair(40, seed=93)
+    lse = torch.empty((28, 64), dtype=torch.float32, device=device)
+    with pytest.raises(RuntimeError, match="GPU"):
+        packed_batch_with_dense([(c2, q, [dk], [dv], out, lse)])
+    with pytest.raises(RuntimeError, match="GPU"):
+        packed_batch_with_dense([(c2, q, [], [], out, lse), (c2, q, [dk.to(device)], [dv], out, lse)])
+    with pytest.raises(ValueError, match="equal bits"):
+        packed_batch_with_dense([(c2, q, [], [], out, lse), (c4, q, [], [], out, lse)])
+    with pytest.raises(ValueError, match="one query dtype"):
+        packed_batch_with_dense([(c2, q, [], [], out, lse), (c2, q.half(), [], [], out.half(), lse)])
+    with pytest.raises(ValueError, match="lse"):
+        packed_batch_with_dense([(c2, q, [], [], out, lse[:, :10])])
+    short = queries(2, seed=94).to(device)
+    with pytest.raises(ValueError, match="multi-query"):
+        packed_batch_with_dense([(c2, short, [], [], torch.empty_like(short))])
+
+
+def test_decode_batch_checks_pointers_and_staleness(device):
+    from unicache_amd.storage.decode import KiviDecodeBatch
+
+    ck, cv = kv_pair(1200, seed=95)
+    cache = PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(1200),
+                                       token_type_id=3, k_bits=2, v_bits=2, group_size=32, residual_length=128,
+                                       backend="cuda")
+    q = queries(1, seed=96).to(device)
+    flat = torch.empty(28 * 128 + 1, dtype=torch.bfloat16, device=device)
+    misaligned = flat[1:].view(1, 28, 128)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        KiviDecodeBatch([cache], [misaligned])
+    with pytest.raises(RuntimeError, match="GPU"):
+        KiviDecodeBatch([cache], [q.cpu()])
+    batch = KiviDecodeBatch([cache], [q])
+    batch.run()
+    seg = K.from_dense(f32(ck), f32(cv), k_bits=2, v_bits=2, group_size=32, residual_length=128)
+    eo, _ = A.packed_summary(seg, f32(q), kv_dtype="fp32")
+    assert_close(f32(batch.outputs[0]), eo, what="batch decode")
+    # a flush replaces the packed tensors: run() refuses until refresh()
+    nk, nv = kv_pair(130, seed=97)
+    for t in range(130):
+        cache.append(nk[t:t + 1].to(device), nv[t:t + 1].to(device), logical_token_ids=torch.tensor([1200 + t]),
+                     flush_at=256)
+    with pytest.raises(RuntimeError, match="refresh"):
+        batch.run()
+    batch.refresh()
+    batch.run()
+    seg = K.from_dense(np.concatenate([f32(ck), f32(nk)]), np.concatenate([f32(cv), f32(nv)]), k_bits=2, v_bits=2,
+                       group_size=32, residual_length=1330 - cache.quantized_tokens)
+    assert seg.quantized_tokens == cache.quantized_tokens
+    eo, _ = A.packed_summary(seg, f32(q), kv_dtype="fp32")
+    assert_close(f32(batch.outputs[0]), eo, what="batch decode after flush")

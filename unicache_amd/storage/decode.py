@@ -6,6 +6,12 @@ the outputs and the split-K workspace.  run() then enqueues a single
 uc_kivi_attn_decode_batch launch (and its LSE combine) and allocates nothing,
 so it can sit in a tight decode loop or a captured HIP graph.  Callers update
 the query tensors in place between steps.
+
+The device tables hold raw pointers, so both classes check every pointer on
+the host when they build a table (device, contiguity, 16-byte alignment of
+the vector-loaded rows), keep the tensors behind the table alive, and refuse
+to run once a packed cache has replaced its tensors (append, flush, repack)
+until refresh() rebuilds the table.
 """
 
 from __future__ import annotations
@@ -16,6 +22,54 @@ import math
 import torch
 
 from .. import _native as nat
+
+_PACKED = ("key_code", "key_scale", "key_minimum", "value_code", "value_scale", "value_minimum")
+
+
+def _check_rows(t: torch.Tensor, device: torch.device, what: str) -> None:
+    """A tensor whose rows the decode kernels read by address: on `device`,
+    contiguous, 16-byte aligned."""
+
+    if t.device != device:
+        raise RuntimeError(f"{what} must be on {device} (got {t.device})")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    if t.data_ptr() % 16:
+        raise ValueError(f"{what} must be 16-byte aligned")
+
+
+def _check_cache(c, device: torch.device, what: str) -> list[torch.Tensor]:
+    """Validate a packed cache's tensors for a device item table; returns
+    the tensors the table will point into."""
+
+    tensors = []
+    for name in _PACKED:
+        t = getattr(c, name)
+        if t.device != device:
+            raise RuntimeError(f"{what}: {name} must be on {device} (got {t.device})")
+        if not t.is_contiguous():
+            raise ValueError(f"{what}: {name} must be contiguous")
+        tensors.append(t)
+    if c.residual_tokens:
+        _check_rows(c.residual_key, device, f"{what}: residual_key")
+        _check_rows(c.residual_value, device, f"{what}: residual_value")
+        tensors += [c.residual_key, c.residual_value]
+    return tensors
+
+
+class _TableGuard:
+    """The tensors behind a device item table and the mutation counts of its
+    packed caches when the table was built."""
+
+    def __init__(self, caches, tensors) -> None:
+        self.tensors = list(tensors)
+        self.caches = list(caches)
+        self.counts = [c.mutation_count for c in self.caches]
+
+    def check(self, what: str) -> None:
+        for c, n in zip(self.caches, self.counts):
+            if c.mutation_count != n:
+                raise RuntimeError(f"{what}: a packed cache changed since the item table was built; call refresh()")
 
 
 class KiviDecodeBatch:
@@ -31,10 +85,11 @@ class KiviDecodeBatch:
             ):
                 raise ValueError("Batched decode segments must share bits, group size and head shapes")
         q0 = queries[0]
-        for q in queries:
-            if q.shape != q0.shape or q.dtype != q0.dtype or not q.is_contiguous():
-                raise ValueError("Batched decode queries must be contiguous and of one shape/dtype")
         self.device = nat.require_device(*queries, first.key_code, what="Batched KIVI decode")
+        for q in queries:
+            if q.shape != q0.shape or q.dtype != q0.dtype:
+                raise ValueError("Batched decode queries must be of one shape/dtype")
+            _check_rows(q, self.device, "Batched decode query")
         lq, hq, d = map(int, q0.shape)
         if hq % first.num_kv_heads:
             raise ValueError("Query heads must be divisible by KIVI KV heads")
@@ -47,6 +102,20 @@ class KiviDecodeBatch:
         self.queries = list(queries)
         self.outputs = [torch.empty((lq, hq, d), dtype=self.out_dtype, device=self.device) for _ in caches]
         self.lses = [torch.empty((hq, lq), dtype=torch.float32, device=self.device) for _ in caches]
+        self.shape = (lq, hq, d)
+        self.sm_scale = 1.0 / math.sqrt(d)
+        self.workspace = None
+        self.refresh()
+
+    def refresh(self) -> None:
+        """(Re)build the device item table from the caches' current tensors."""
+
+        caches, queries = self.caches, self.queries
+        first = caches[0]
+        lq, hq, d = self.shape
+        tensors = list(queries) + self.outputs + self.lses
+        for c in caches:
+            tensors += _check_cache(c, self.device, "Batched KIVI decode")
         items = (nat.KiviItem * len(caches))()
         for i, (c, q) in enumerate(zip(caches, queries)):
             tr = c.residual_tokens
@@ -62,9 +131,9 @@ class KiviDecodeBatch:
         self.max_tr = max(c.residual_tokens for c in caches)
         self.ws_bytes = nat.decode_workspace_bytes(len(caches), first.k_bits, first.group_size, hq,
                                                    first.num_kv_heads, d, lq, self.max_tq, self.max_tr)
-        self.workspace = nat.workspace(self.device, self.ws_bytes)
-        self.shape = (lq, hq, d)
-        self.sm_scale = 1.0 / math.sqrt(d)
+        if self.workspace is None or self.workspace.numel() < self.ws_bytes:
+            self.workspace = nat.workspace(self.device, self.ws_bytes)
+        self._guard = _TableGuard(caches, tensors)
 
     @property
     def algorithmic_bytes(self) -> int:
@@ -80,6 +149,7 @@ class KiviDecodeBatch:
         return total
 
     def run(self, stream: int | None = None) -> None:
+        self._guard.check("KiviDecodeBatch.run")
         lq, hq, d = self.shape
         first = self.caches[0]
         nat.call(
@@ -118,10 +188,11 @@ class MixedDecodeBatch:
             ):
                 raise ValueError("Mixed decode packed segments must share bits, group size and head shapes")
         q0 = queries[0]
-        for q in queries:
-            if q.shape != q0.shape or q.dtype != q0.dtype or not q.is_contiguous():
-                raise ValueError("Mixed decode queries must be contiguous and of one shape/dtype")
         self.device = nat.require_device(*queries, first.key_code, what="Mixed KIVI decode")
+        for q in queries:
+            if q.shape != q0.shape or q.dtype != q0.dtype:
+                raise ValueError("Mixed decode queries must be of one shape/dtype")
+            _check_rows(q, self.device, "Mixed decode query")
         lq, hq, d = map(int, q0.shape)
         dtypes = set()
         for g in groups:
@@ -130,8 +201,8 @@ class MixedDecodeBatch:
                     k, v = s
                     if k.shape != v.shape or k.dim() != 3 or tuple(k.shape[1:]) != (first.num_kv_heads, d):
                         raise ValueError("Dense segments must be matching [tokens, kv_heads, head_dim] tensors")
-                    if not (k.is_contiguous() and v.is_contiguous()):
-                        raise ValueError("Dense segments must be contiguous")
+                    if k.dtype != v.dtype:
+                        raise ValueError("Dense segment keys and values must share one dtype")
                     dtypes.add(k.dtype)
                 elif s.residual_tokens:
                     dtypes.add(s.residual_key.dtype)
@@ -150,6 +221,20 @@ class MixedDecodeBatch:
         self.refresh()
 
     def refresh(self) -> None:
+        """(Re)build the device item table from the segments' current tensors."""
+
+        tensors = list(self.queries) + self.outputs + self.lses
+        caches = []
+        for g in self.groups:
+            for s in g:
+                if isinstance(s, tuple):
+                    if int(s[0].shape[0]):
+                        _check_rows(s[0], self.device, "Mixed decode dense key segment")
+                        _check_rows(s[1], self.device, "Mixed decode dense value segment")
+                    tensors += list(s)
+                else:
+                    tensors += _check_cache(s, self.device, "Mixed KIVI decode")
+                    caches.append(s)
         n = len(self.groups) * self.segs
         items = (nat.KiviItem * n)()
         max_tq = max_tr = 0
@@ -184,6 +269,7 @@ class MixedDecodeBatch:
                                                    max_tq, max_tr)
         if getattr(self, "workspace", None) is None or self.workspace.numel() < self.ws_bytes:
             self.workspace = nat.workspace(self.device, self.ws_bytes)
+        self._guard = _TableGuard(caches, tensors)
 
     @property
     def algorithmic_bytes(self) -> int:
@@ -203,6 +289,7 @@ class MixedDecodeBatch:
         return total
 
     def run(self, stream: int | None = None) -> None:
+        self._guard.check("MixedDecodeBatch.run")
         lq, hq, d = self.shape
         nat.call(
             "uc_kivi_attn_decode_segments", self.table.data_ptr(), self.n_items, self.segs, self.bits,

@@ -281,7 +281,12 @@ def packed_batch_with_dense(items: list) -> None:
             raise ValueError("Batched packed attention needs contiguous queries and outputs")
         if int(query.shape[0]) <= _max_decode_query_len(cache, hq):
             raise ValueError("Batched packed attention covers multi-query segments only")
-    device = nat.require_device(q0, cache0.key_code, what="Batched packed attention")
+    # every pointer that goes into the launch table, on one GPU, checked before any launch
+    device = nat.require_device(
+        *(t for cache, query, kparts, vparts, out, *rest in items
+          for t in (query, out, *rest, *kparts, *vparts, cache.key_code, cache.key_scale, cache.key_minimum,
+                    cache.value_code, cache.value_scale, cache.value_minimum)),
+        what="Batched packed attention")
     for start in range(0, len(items), MQ_MAX_BATCH):
         chunk = items[start:start + MQ_MAX_BATCH]
         kparts = [x.to(dtype) for item in chunk for x in item[2]]
