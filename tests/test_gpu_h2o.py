@@ -80,8 +80,10 @@ def test_scores_from_probs(device):
     assert np.allclose(got.cpu().numpy(), H.scores_from_probs(f32(probs), 4), rtol=1e-5, atol=1e-5)
 
 
-def test_fused_scores_and_selection_margin(device):
-    # config 3 shape reduced in queries: Q [128, 28, 128], K [4096, 4, 128]
+def test_fused_scores_near_ties_only(device):
+    # Q [128, 28, 128], K [4096, 4, 128]: a seed whose selection margin is
+    # below the score error; the selections may then differ only in near-ties
+    # (config 3 itself is asserted bit-exact in test_gpu_full_size.py)
     key, _ = kv_pair(4096, seed=5, outliers=0)
     q = queries(128, seed=6)
     got = per_kv_head_scores_from_qk(q.to(device), key.to(device)).cpu().numpy()
@@ -90,16 +92,12 @@ def test_fused_scores_and_selection_margin(device):
     assert err.max() <= 1e-3 * max(1.0, float(np.abs(exp).max())), err.max()
     heavy_k, recent = 576, 192
     tol = float(err.max())
-    margin = H.min_selection_margin(exp, heavy_k, recent)
     got_idx = h2o_select_indices(torch.from_numpy(got).to(device), heavy_k=heavy_k, recent=recent).cpu().numpy()
     exp_idx = H.select(exp, heavy_k, recent)
-    if margin > 2 * tol:
-        assert np.array_equal(got_idx, exp_idx)
-    else:  # only near-ties may differ
-        for h in range(4):
-            diff = set(got_idx[h]) ^ set(exp_idx[h])
-            kth = np.sort(exp[h, : 4096 - recent])[::-1][heavy_k - 1]
-            assert all(abs(exp[h, i] - kth) <= 2 * tol for i in diff)
+    for h in range(4):
+        diff = set(got_idx[h]) ^ set(exp_idx[h])
+        kth = np.sort(exp[h, : 4096 - recent])[::-1][heavy_k - 1]
+        assert all(abs(exp[h, i] - kth) <= 2 * tol for i in diff)
 
 
 # (Lq, Hq, Hkv, T, D, dtype): ragged row blocks (group * Lq not a multiple of
