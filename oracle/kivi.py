@@ -95,6 +95,12 @@ def quantize_codes(data: np.ndarray, *, bits: int, group_dim: int, group_size: i
       mn = amin, mx = amax over the group        (exact)
       scale = max((mx - mn) / (2^b - 1), eps)    (two fp32 roundings)
       code  = clamp(rint((x - mn) / scale), 0, 2^b - 1)
+
+    NaN follows torch: amin / amax of a group holding a NaN are NaN, and
+    clamp_min keeps the NaN scale.  Such a group's codes are NaN in fp32;
+    torch's NaN -> uint8 cast (physical.py:166) is unspecified by C++ and
+    gives 0 on x86, which is the value written here (explicitly, rather than
+    through numpy's equally unspecified cast).
     """
 
     data = np.asarray(data, dtype=np.float32)
@@ -109,7 +115,7 @@ def quantize_codes(data: np.ndarray, *, bits: int, group_dim: int, group_size: i
         mx = chunk.max(axis=gd, keepdims=True)
         scale = np.maximum((mx - mn) / max_code, EPS).astype(F32)
         q = np.clip(np.rint((chunk - mn) / scale), F32(0), max_code)
-        codes.append(q.astype(np.uint8))
+        codes.append(np.where(np.isnan(q), F32(0), q).astype(np.uint8))
         scales.append(np.squeeze(scale, axis=gd))
         minima.append(np.squeeze(mn, axis=gd))
     return (

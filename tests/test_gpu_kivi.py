@@ -239,3 +239,36 @@ def test_streaming_decode_matches_fresh_cache(device):
     a, la = packed_kivi_attention_summary(cache, q)
     b, lb = packed_kivi_attention_summary(fresh, q)
     assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+@pytest.mark.parametrize("native", [True, False])
+def test_non_finite_inputs_match_oracle(device, native):
+    # NaN and +/-inf inside some key and value groups: torch.amin / amax
+    # propagate NaN (NaN stats, codes 0), inf gives inf / NaN stats; codes must
+    # match bit for bit and stats as values (NaN where the oracle has NaN)
+    key, value = kv_pair(256, seed=17)
+    key[5, 1, 7] = float("nan")        # key group 0 of (head 1, channel 7)
+    key[70, 2, 100] = float("inf")     # key group 2 of (head 2, channel 100)
+    key[200, 0, 3] = float("-inf")
+    value[9, 3, 40] = float("nan")     # value group 1 of (token 9, head 3)
+    value[100, 0, 127] = float("inf")
+    cache = PackedKIVICache.from_dense(key.to(device), value.to(device), logical_token_ids=torch.arange(256),
+                                       token_type_id=3, k_bits=2, v_bits=2, group_size=32, residual_length=0,
+                                       backend="cuda" if native else "reference")
+    with np.errstate(invalid="ignore"):
+        seg = K.from_dense(f32(key), f32(value), k_bits=2, v_bits=2, group_size=32, residual_length=0,
+                           native=native)
+    assert cache.kernel_native_layout == seg.native
+    for name in ("key_code", "value_code"):
+        assert np.array_equal(getattr(cache, name).cpu().numpy(), getattr(seg, name)), name
+    for name in ("key_scale", "key_minimum", "value_scale", "value_minimum"):
+        assert np.array_equal(f32(getattr(cache, name)), getattr(seg, name), equal_nan=True), name
+    assert np.isnan(f32(cache.key_scale)).sum() == 1 and np.isnan(f32(cache.value_minimum)).sum() == 1
+    # fake quant of the same tensors
+    from unicache_amd.operators import kivi_fake_quant_key, kivi_fake_quant_value
+
+    with np.errstate(invalid="ignore"):
+        fk = K.fake_quant(f32(key), bits=2, dim=0, group_size=32)
+        fv = K.fake_quant(f32(value), bits=2, dim=-1, group_size=32)
+    assert np.array_equal(f32(kivi_fake_quant_key(key.to(device), bits=2, group_size=32)), fk, equal_nan=True)
+    assert np.array_equal(f32(kivi_fake_quant_value(value.to(device), bits=2, group_size=32)), fv, equal_nan=True)

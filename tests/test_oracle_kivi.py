@@ -303,3 +303,22 @@ def test_native_mean_error_not_worse_than_reference_layout():
         assert native_error <= ref_error * 1.10 + 1e-3
         # 2-bit codes over G=64 leave a mean error well under one scale step
         assert 0.05 < native_error < 0.5
+
+
+def test_non_finite_groups_follow_torch():
+    # torch.amin / amax propagate NaN and clamp_min keeps it: a group with a NaN
+    # gets NaN scale and minimum, codes 0, and dequantizes to NaN; a +inf
+    # element gives an inf scale (every other code 0)
+    with np.errstate(invalid="ignore"):
+        codes, scale, mn = K.quantize_codes(np.array([[1.0], [np.nan], [3.0], [2.0]], np.float32), bits=2,
+                                            group_dim=0, group_size=4)
+        assert codes[:, 0].tolist() == [0, 0, 0, 0] and np.isnan(scale[0, 0]) and np.isnan(mn[0, 0])
+        codes, scale, mn = K.quantize_codes(np.array([[1.0], [np.inf], [3.0], [2.0]], np.float32), bits=2,
+                                            group_dim=0, group_size=4)
+        assert codes[:, 0].tolist() == [0, 0, 0, 0] and scale[0, 0] == np.inf and mn[0, 0] == 1.0
+        fq = K.fake_quant(np.array([0.0, np.nan, 2.0, 3.0], np.float32), bits=2, dim=0, group_size=4,
+                          out_dtype="fp32")
+        assert np.isnan(fq).all()
+        fq = K.fake_quant(np.array([0.0, 1.0, 2.0, 3.0], np.float32), bits=2, dim=0, group_size=4,
+                          out_dtype="fp32")
+        assert fq.tolist() == [0.0, 1.0, 2.0, 3.0]

@@ -62,6 +62,38 @@ __host__ __device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
   return static_cast<uint32_t>((uint64_t(n) * f.m) >> f.shift);
 }
 
+// Group range with the NaN rule of torch.amin / amax: a NaN anywhere in the
+// group makes both bounds NaN (fminf / fmaxf alone would skip it).
+struct GroupRange {
+  float mn, mx;
+  bool nan;
+  __device__ __forceinline__ void init(float x) {
+    mn = x;
+    mx = x;
+    nan = x != x;
+  }
+  __device__ __forceinline__ void add(float x) {
+    mn = fminf(mn, x);
+    mx = fmaxf(mx, x);
+    nan = nan || x != x;
+  }
+  // fold in the range held by lane (lane ^ o)
+  __device__ __forceinline__ void merge_xor(int o) {
+    mn = fminf(mn, __shfl_xor(mn, o, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    nan = __shfl_xor(static_cast<int>(nan), o, 64) != 0 || nan;
+  }
+  __device__ __forceinline__ void finish() {
+    if (nan) {
+      mn = __builtin_nanf("");
+      mx = mn;
+    }
+  }
+};
+
+// torch's clamp_min(v, lo): a NaN stays NaN.
+__device__ __forceinline__ float clamp_min_nan(float v, float lo) { return v != v ? v : fmaxf(v, lo); }
+
 inline bool valid_dtype(int d) { return d == UC_BF16 || d == UC_FP16 || d == UC_FP32; }
 inline bool half_dtype(int d) { return d == UC_BF16 || d == UC_FP16; }
 

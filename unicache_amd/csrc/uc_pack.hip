@@ -1,7 +1,10 @@
 // KIVI quantize/pack, dequantize and fake-quant kernels (HBM-bound byte work).
 //
 // Bit-exactness contract (physical.py:160-175, 190-201; builtin.py:42-53):
-// every value is widened to fp32; min/max are exact; the subtraction,
+// every value is widened to fp32; min/max are exact and, like torch.amin /
+// amax and clamp_min, turn a group containing NaN into NaN stats (whose codes
+// are then 0: the fp32 code is NaN and the clamp to [0, 2^b-1] yields 0,
+// which is also what torch's NaN -> uint8 cast gives on x86); the subtraction,
 // division (IEEE correctly rounded, the HIP default) and round-half-even
 // (v_rndne_f32) happen once each, in the same order as the torch code, and
 // dequantisation is a rounded multiply followed by a rounded add (never an
@@ -39,16 +42,19 @@ __device__ void pack_key_group(const void *__restrict__ key, int64_t st, int64_t
       x1[i] = has1 ? load_as_f32<IN>(key, off + sd) : 0.0f;
     }
   }
-  float mn0 = x0[0], mx0 = x0[0], mn1 = x1[0], mx1 = x1[0];
+  GroupRange r0, r1;
+  r0.init(x0[0]);
+  r1.init(x1[0]);
 #pragma unroll
   for (int i = 1; i < G; ++i) {
-    mn0 = fminf(mn0, x0[i]);
-    mx0 = fmaxf(mx0, x0[i]);
-    mn1 = fminf(mn1, x1[i]);
-    mx1 = fmaxf(mx1, x1[i]);
+    r0.add(x0[i]);
+    r1.add(x1[i]);
   }
-  const float s0 = fmaxf(div_rn(sub_rn(mx0, mn0), kMaxCode), kEps);
-  const float s1 = fmaxf(div_rn(sub_rn(mx1, mn1), kMaxCode), kEps);
+  r0.finish();
+  r1.finish();
+  const float mn0 = r0.mn, mn1 = r1.mn;
+  const float s0 = clamp_min_nan(div_rn(sub_rn(r0.mx, mn0), kMaxCode), kEps);
+  const float s1 = clamp_min_nan(div_rn(sub_rn(r1.mx, mn1), kMaxCode), kEps);
 
   if constexpr (BITS == 8) {
     uint8_t *out = static_cast<uint8_t *>(code);
@@ -141,19 +147,16 @@ __device__ void pack_value_chunk(const void *__restrict__ value, int64_t st, int
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = 0.0f;
   }
-  float mn = x[0], mx = x[0];
+  GroupRange r;
+  r.init(x[0]);
 #pragma unroll
-  for (int i = 1; i < 16; ++i) {
-    mn = fminf(mn, x[i]);
-    mx = fmaxf(mx, x[i]);
-  }
+  for (int i = 1; i < 16; ++i) r.add(x[i]);
 #pragma unroll
-  for (int o = 1; o < kLanesPerGroup; o <<= 1) {
-    mn = fminf(mn, __shfl_xor(mn, o, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-  }
+  for (int o = 1; o < kLanesPerGroup; o <<= 1) r.merge_xor(o);
   if (!active) return;
-  const float s = fmaxf(div_rn(sub_rn(mx, mn), kMaxCode), kEps);
+  r.finish();
+  const float mn = r.mn, mx = r.mx;
+  const float s = clamp_min_nan(div_rn(sub_rn(mx, mn), kMaxCode), kEps);
   uint32_t q[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i)
@@ -462,13 +465,12 @@ __global__ __launch_bounds__(256) void fake_quant_kernel(FakeQuantArgs a) {
   }
   const int64_t start = g * a.group;
   const int64_t stop = min(length, start + a.group);
-  float mn = load_as_f32<DT>(a.data, base + start * step), mx = mn;
-  for (int64_t i = start + 1; i < stop; ++i) {
-    const float x = load_as_f32<DT>(a.data, base + i * step);
-    mn = fminf(mn, x);
-    mx = fmaxf(mx, x);
-  }
-  const float scale = div_rn(fmaxf(sub_rn(mx, mn), kEps), a.max_code);
+  GroupRange r;
+  r.init(load_as_f32<DT>(a.data, base + start * step));
+  for (int64_t i = start + 1; i < stop; ++i) r.add(load_as_f32<DT>(a.data, base + i * step));
+  r.finish();
+  const float mn = r.mn;
+  const float scale = div_rn(clamp_min_nan(sub_rn(r.mx, mn), kEps), a.max_code);
   for (int64_t i = start; i < stop; ++i) {
     const float x = load_as_f32<DT>(a.data, base + i * step);
     const float code = fminf(fmaxf(rintf(div_rn(sub_rn(x, mn), scale)), 0.0f), a.max_code);
@@ -496,18 +498,21 @@ __global__ __launch_bounds__(256) void fake_quant_tokens_kernel(FakeQuantArgs a)
     x0[i] = half_bits_to_f32<DT>(pair);
     x1[i] = half_bits_to_f32<DT>(pair >> 16);
   }
-  float mn0 = x0[0], mx0 = x0[0], mn1 = x1[0], mx1 = x1[0];
+  GroupRange r0, r1;
+  r0.init(x0[0]);
+  r1.init(x1[0]);
 #pragma unroll
   for (int i = 1; i < GM; ++i) {
     if (i < n) {
-      mn0 = fminf(mn0, x0[i]);
-      mx0 = fmaxf(mx0, x0[i]);
-      mn1 = fminf(mn1, x1[i]);
-      mx1 = fmaxf(mx1, x1[i]);
+      r0.add(x0[i]);
+      r1.add(x1[i]);
     }
   }
-  const float s0 = div_rn(fmaxf(sub_rn(mx0, mn0), kEps), a.max_code);
-  const float s1 = div_rn(fmaxf(sub_rn(mx1, mn1), kEps), a.max_code);
+  r0.finish();
+  r1.finish();
+  const float mn0 = r0.mn, mn1 = r1.mn;
+  const float s0 = div_rn(clamp_min_nan(sub_rn(r0.mx, mn0), kEps), a.max_code);
+  const float s1 = div_rn(clamp_min_nan(sub_rn(r1.mx, mn1), kEps), a.max_code);
 #pragma unroll
   for (int i = 0; i < GM; ++i) {
     if (i < n) {
@@ -538,18 +543,15 @@ __global__ __launch_bounds__(256) void fake_quant_channels_kernel(FakeQuantArgs 
     x[2 * j] = half_bits_to_f32<DT>(w[j]);
     x[2 * j + 1] = half_bits_to_f32<DT>(w[j] >> 16);
   }
-  float mn = x[0], mx = x[0];
+  GroupRange r;
+  r.init(x[0]);
 #pragma unroll
-  for (int j = 1; j < 8; ++j) {
-    mn = fminf(mn, x[j]);
-    mx = fmaxf(mx, x[j]);
-  }
-  for (int o = 1; o < lanes_per_group; o <<= 1) {
-    mn = fminf(mn, __shfl_xor(mn, o, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-  }
+  for (int j = 1; j < 8; ++j) r.add(x[j]);
+  for (int o = 1; o < lanes_per_group; o <<= 1) r.merge_xor(o);
   if (!active) return;
-  const float s = div_rn(fmaxf(sub_rn(mx, mn), kEps), a.max_code);
+  r.finish();
+  const float mn = r.mn;
+  const float s = div_rn(clamp_min_nan(sub_rn(r.mx, mn), kEps), a.max_code);
   uint32_t o[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
