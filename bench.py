@@ -81,25 +81,15 @@ def pack_throughput(device, steps):
     into preallocated native-layout outputs, calls back to back: the C-ABI pack
     path without from_dense's per-cache allocations."""
 
-    from unicache_amd import _native as nat
-    from unicache_amd.storage.physical import _dense_strides, native_pack_layout
+    from unicache_amd.storage.physical import _native_storage, _pack_native_into
 
     tq = TOKENS - RESIDUAL
     key, value = make_kv(TOKENS, seed=26000, device=device)
     qk, qv = key[:tq], value[:tq]
-    lay = native_pack_layout(tq, HKV, D, BITS, BITS, GROUP)
-    kc = torch.empty(lay["key_code"][0], dtype=torch.int32, device=device)
-    ks = torch.empty(lay["key_stats"][0], dtype=torch.float16, device=device)
-    km = torch.empty_like(ks)
-    vc = torch.empty(lay["value_code"][0], dtype=torch.int32, device=device)
-    vs = torch.empty(lay["value_stats"][0], dtype=torch.float16, device=device)
-    vm = torch.empty_like(vs)
+    storage = _native_storage(tq, HKV, D, BITS, BITS, GROUP, device)
     stream = torch.cuda.current_stream(device)
-    args = (qk.data_ptr(), *_dense_strides(qk), qv.data_ptr(), *_dense_strides(qv), nat.dtype_code(qk.dtype), tq,
-            HKV, D, BITS, BITS, GROUP, nat.UC_FP16, kc.data_ptr(), *map(int, kc.stride()), ks.data_ptr(),
-            km.data_ptr(), *map(int, ks.stride()), vc.data_ptr(), *map(int, vc.stride()), vs.data_ptr(),
-            vm.data_ptr(), *map(int, vs.stride()), stream.cuda_stream)
-    ms = time_steps(lambda: nat.call("uc_kivi_pack", *args), steps, 3, stream)
+    pack = lambda: _pack_native_into(storage, 0, qk, qv, k_bits=BITS, v_bits=BITS, group_size=GROUP)  # noqa: E731
+    ms = time_steps(pack, steps, 3, stream)
     nbytes = 2 * qk.numel() * 2 + tq * 384
     return nbytes / (ms * 1e-3) / 1e9, ms
 
@@ -178,10 +168,8 @@ def editing_attention(device, steps, layers=LAYERS, bits=BITS):
         tr = int(dk.shape[0])
         ws_bytes = nat.mq_workspace_bytes(HKV, D, cache.quantized_tokens, tr)
         ws = nat.workspace(device, ws_bytes)
-        item = nat.KiviItem(cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
-                            cache.value_code.data_ptr(), cache.value_scale.data_ptr(),
-                            cache.value_minimum.data_ptr(), dk.data_ptr(), dv.data_ptr(), q.data_ptr(),
-                            out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr)
+        item = cache.native_item(q.data_ptr(), out.data_ptr(), lse.data_ptr(), residual_key_ptr=dk.data_ptr(),
+                                 residual_value_ptr=dv.data_ptr(), residual_tokens=tr)
         calls.append((item, ws, ws_bytes, cache, dk, dv, q, out, lse))
         del key, value, ik, iv, tk, tv
     keys = calls[0][3].quantized_tokens + int(calls[0][4].shape[0])

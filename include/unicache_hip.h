@@ -7,14 +7,22 @@
  *  - Every pointer argument is a device pointer unless the comment says
  *    otherwise.  Sizes and strides are int64 element counts (not bytes).
  *  - Tensors named "dense" are token-major [tokens, heads, head_dim] as in
- *    UniCache (physical.py:242-246).  Packed KIVI tensors use the kernel-native
- *    layout of kivi_cuda.py:177-182:
+ *    UniCache (physical.py:242-246).  Packed KIVI tensors have the shapes of
+ *    the kernel-native layout of kivi_cuda.py:177-182,
  *        key_code   int32 [Hkv, D, T*bits/32]   (codes LSB-first along tokens)
  *        key_scale  fp16  [Hkv, D, T/G]          key_min likewise
  *        value_code int32 [Hkv, T, D*bits/32]   (codes LSB-first along channels)
  *        value_scale fp16 [Hkv, T, D/G]          value_min likewise
- *    The pack/dequant entry points take explicit strides so the same kernels
- *    also produce UniCache's non-native "reference" layout (physical.py:291-304).
+ *    but are stored token-major in memory, each head's rows C tokens apart
+ *    (C = the packed capacity, >= T, a multiple of G; C = T when tight):
+ *        key_code   element (h, d, w) at h*(C*bits/32)*D + w*D + d
+ *        key_scale  element (h, d, g) at h*(C/G)*D + g*D + d
+ *        value_code element (h, t, w) at h*C*(D*bits/32) + t*(D*bits/32) + w
+ *        value_scale element (h, t, g) at h*C*(D/G) + t*(D/G) + g
+ *    so a token range of one head is one contiguous run of every tensor and a
+ *    cache can grow by whole rows.  The pack/dequant entry points take explicit
+ *    strides (any layout, including UniCache's non-native "reference" layout,
+ *    physical.py:291-304); the attention entry points take this layout.
  *  - The library never allocates or frees device memory and never
  *    synchronises: callers own every output and workspace, and all work is
  *    enqueued on the hipStream_t passed as `stream` (NULL = default stream).
@@ -31,7 +39,7 @@
 extern "C" {
 #endif
 
-#define UC_ABI_VERSION 1
+#define UC_ABI_VERSION 2
 
 /* element type codes */
 #define UC_BF16 0
@@ -123,7 +131,8 @@ int uc_kivi_fake_quant(const void *data, int64_t st, int64_t sh, int64_t sd,
 /*
  * Scaled logits over a packed segment plus its dense residual:
  *   logits[hq, i, t] = sm_scale * <query[i, hq, :], K[t, hq / group, :]>
- * for t < quantized_tokens from the packed keys (native layout, contiguous)
+ * for t < quantized_tokens from the packed keys (token-major with capacity
+ * packed_capacity, 0 meaning quantized_tokens; see the top of this file)
  * and t >= quantized_tokens from the dense residual_key, element (t, h, d) at
  * r_st*t + r_sh*h + d.  logits is fp32 [Hq, Lq, Tq+Tr] (contiguous).  With
  * quantized_tokens == 0 this is the dense GQA QK of gqa_query_key_logits
@@ -136,7 +145,7 @@ int uc_kivi_fake_quant(const void *data, int64_t st, int64_t sh, int64_t sd,
  */
 int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int64_t heads_q,
                const void *key_code, const void *key_scale, const void *key_min, int stats_dtype,
-               int64_t quantized_tokens, int bits, int group_size,
+               int64_t quantized_tokens, int64_t packed_capacity, int bits, int group_size,
                const void *residual_key, int res_dtype, int64_t residual_tokens,
                int64_t r_st, int64_t r_sh,
                int64_t heads_kv, int64_t head_dim, float sm_scale,
@@ -145,6 +154,7 @@ int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int64_t heads_
 /*
  * Probability-value product over a packed segment plus its residual:
  *   out[hq, i, :] = sum_t probs[hq, i, t] * V[t, hq / group, :]
+ * packed values with capacity packed_capacity (0: quantized_tokens);
  * probs [Hq, Lq, Tq+Tr] of p_dtype with strides (p_sh, p_si, p_st); out is
  * [Hq, Lq, D] of out_dtype (contiguous); residual_value element (t, h, d) at
  * r_st*t + r_sh*h + d.  `workspace` must hold
@@ -158,7 +168,7 @@ int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int64_t heads_
 int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t p_si, int64_t p_st,
                int64_t query_len, int64_t heads_q,
                const void *value_code, const void *value_scale, const void *value_min, int stats_dtype,
-               int64_t quantized_tokens, int bits, int group_size,
+               int64_t quantized_tokens, int64_t packed_capacity, int bits, int group_size,
                const void *residual_value, int res_dtype, int64_t residual_tokens,
                int64_t r_st, int64_t r_sh,
                int64_t heads_kv, int64_t head_dim,
@@ -170,8 +180,8 @@ int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t p_si, int64
  * points; a table of these lets one launch cover many sequences and layers.
  */
 typedef struct uc_kivi_item {
-  const void *key_code;      /* int32 [Hkv, D, Tq*bits/32] */
-  const void *key_scale;     /* fp16  [Hkv, D, Tq/G] */
+  const void *key_code;      /* int32 [Hkv, D, Tq*bits/32], token-major (see the top of this file) */
+  const void *key_scale;     /* fp16  [Hkv, D, Tq/G], token-major */
   const void *key_min;
   const void *value_code;    /* int32 [Hkv, Tq, D*bits/32] */
   const void *value_scale;   /* fp16  [Hkv, Tq, D/G] */
@@ -183,6 +193,7 @@ typedef struct uc_kivi_item {
   float *lse;                /* [Hq, Lq] natural-log LSE, may be NULL */
   int64_t quantized_tokens;  /* Tq, a multiple of group_size */
   int64_t residual_tokens;   /* Tr */
+  int64_t packed_capacity;   /* C: tokens between the heads of the packed tensors; 0 means Tq */
 } uc_kivi_item;
 
 /*

@@ -128,8 +128,11 @@ def test_merge_and_fake_quant_validation():
     with pytest.raises(ValueError, match="divisible by KV heads for GQA H2O"):
         nat.call("uc_h2o_colsum", None, nat.UC_BF16, 0, 0, 1, 28, 1, 64, 3, 0, None, None)
     with pytest.raises(ValueError, match="divisible by KIVI KV heads"):
-        nat.call("uc_kivi_qk", None, nat.UC_BF16, 1, 28, None, None, None, nat.UC_FP16, 0, 2, 32,
+        nat.call("uc_kivi_qk", None, nat.UC_BF16, 1, 28, None, None, None, nat.UC_FP16, 0, 0, 2, 32,
                  None, nat.UC_BF16, 16, 0, 0, 3, 128, 0.1, None, None)
+    with pytest.raises(ValueError, match="packed_capacity must be 0 or a multiple of group_size"):
+        nat.call("uc_kivi_qk", None, nat.UC_BF16, 1, 28, None, None, None, nat.UC_FP16, 64, 48, 2, 32,
+                 None, nat.UC_BF16, 16, 0, 0, 4, 128, 0.1, None, None)
 
 
 def test_editing_batch_validation():

@@ -203,9 +203,19 @@ def test_streaming_append_flush_equals_from_dense(device, bits, group, tokens, a
                                        k_bits=bits, v_bits=bits, group_size=group, residual_length=128,
                                        backend="cuda")
     tq0, tr0 = cache.quantized_tokens, cache.residual_tokens
-    flushed = 0
+    flushed = in_place = 0
     for t in range(tokens, tokens + appended):
-        flushed += cache.append(kd[t:t + 1], vd[t:t + 1], logical_token_ids=ids[t:t + 1], flush_at=128)
+        before = (cache.key_code.data_ptr(), cache.packed_capacity)
+        n = cache.append(kd[t:t + 1], vd[t:t + 1], logical_token_ids=ids[t:t + 1], flush_at=128)
+        flushed += n
+        assert cache.quantized_tokens <= cache.packed_capacity and cache.packed_capacity % group == 0
+        # a flush appends rows in place while the storage has room, else grows it by half
+        if n and before[1] >= cache.quantized_tokens:
+            assert (cache.key_code.data_ptr(), cache.packed_capacity) == before
+            in_place += 1
+        elif n:
+            assert cache.packed_capacity >= before[1] + before[1] // 2
+    assert flushed == 0 or in_place or cache.packed_capacity == cache.quantized_tokens
     expect_packed = tq0 + K.streamed_split(tr0, appended, flush_at=128, group_size=group)
     assert cache.quantized_tokens == expect_packed == tq0 + flushed
     total = tokens + appended

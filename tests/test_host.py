@@ -98,3 +98,49 @@ def test_batched_attention_argument_checks():
     with pytest.raises(ValueError, match="no physical segments"):
         run_batched_physical_attention(q, k, k, [0, 3, 6], [0, 2, 5], [[], []])
     kivi_cuda.packed_batch_with_dense([])  # nothing to launch
+
+
+def _native_cpu_cache(tokens, capacity, *, bits=2, group=32, heads=4, head_dim=128):
+    # layout checks only: CPU tensors never reach a kernel here
+    from unicache_amd.storage.physical import _native_storage, _native_views
+
+    store = _native_storage(capacity, heads, head_dim, bits, bits, group, "cpu")
+    kc, ks, km, vc, vs, vm = _native_views(store, tokens, bits, group)
+    res = torch.zeros(0, heads, head_dim, dtype=torch.bfloat16)
+    return PackedKIVICache(kc, ks, km, vc, vs, vm, res, res, torch.arange(tokens), 3, bits, bits, group, tokens,
+                           head_dim, heads, backend="cuda", kernel_native_layout=True)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_token_major_views_and_capacity(bits):
+    c = _native_cpu_cache(256, 416, bits=bits)
+    # reference shapes (kivi_cuda.py:177-182) over token-major storage
+    assert tuple(c.key_code.shape) == (4, 128, 256 * bits // 32) and tuple(c.key_scale.shape) == (4, 128, 8)
+    assert tuple(c.value_code.shape) == (4, 256, 128 * bits // 32) and tuple(c.value_minimum.shape) == (4, 256, 4)
+    assert c.key_code.stride() == (416 * bits // 32 * 128, 1, 128) and c.key_scale.stride() == (13 * 128, 1, 128)
+    assert c.packed_capacity == 416
+    *ptrs, cap = c.native_packed_pointers()
+    assert cap == 416 and ptrs[0] == c.key_code.data_ptr()
+    # code word (h, d, w) sits at h*(C*b/32)*D + w*D + d of the storage
+    flat = c.key_code.as_strided((4 * 416 * bits // 32 * 128,), (1,))
+    flat.zero_()
+    c.key_code[2, 5, 3] = 77
+    assert int(flat[2 * (416 * bits // 32) * 128 + 3 * 128 + 5]) == 77
+
+
+def test_token_major_layout_is_enforced():
+    c = _native_cpu_cache(256, 256)
+    assert c.packed_capacity == 256
+    c.native_packed_pointers()
+    # UniCache's word-major contiguous tensors of the same shapes are refused
+    c.key_code = c.key_code.contiguous()
+    with pytest.raises(ValueError, match="token-major"):
+        c.native_packed_pointers()
+    c = _native_cpu_cache(256, 256)
+    c.value_scale = c.value_scale.float()
+    with pytest.raises(ValueError, match="value_scale"):
+        c.native_packed_pointers()
+    c = _native_cpu_cache(256, 256)
+    c.kernel_native_layout = False
+    with pytest.raises(RuntimeError, match="kernel-native"):
+        c.native_packed_pointers()

@@ -20,12 +20,9 @@ def _summaries(cache, q, *, static):
     out = torch.full((lq, hq, d), float("nan"), dtype=q.dtype, device=q.device)
     lse = torch.full((hq, lq), float("nan"), dtype=torch.float32, device=q.device)
     tr = cache.residual_tokens
-    item = nat.KiviItem(
-        cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
-        cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
-        cache.residual_key.data_ptr() if tr else None, cache.residual_value.data_ptr() if tr else None,
-        q.data_ptr(), out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr,
-    )
+    item = cache.native_item(q.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                             residual_key_ptr=cache.residual_key.data_ptr() if tr else None,
+                             residual_value_ptr=cache.residual_value.data_ptr() if tr else None, residual_tokens=tr)
     args = (cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq, nat.dtype_code(q.dtype),
             nat.dtype_code(cache.residual_key.dtype), nat.dtype_code(q.dtype), 1.0 / math.sqrt(d))
     if static:

@@ -14,7 +14,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libunicache_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 UC_BF16, UC_FP16, UC_FP32 = 0, 1, 2
 UC_OK, UC_EINVAL, UC_ERUNTIME = 0, -1, -2
@@ -43,6 +43,7 @@ class KiviItem(ctypes.Structure):
         ("lse", _P),
         ("quantized_tokens", _L),
         ("residual_tokens", _L),
+        ("packed_capacity", _L),
     ]
 
 
@@ -65,11 +66,11 @@ _SIGNATURES = {
     "uc_kivi_fake_quant": (_I, [_P, _L, _L, _L, _I, _L, _L, _L, _I, _I, _I, _P, _P]),
     "uc_kivi_qk": (
         _I,
-        [_P, _I, _L, _L, _P, _P, _P, _I, _L, _I, _I, _P, _I, _L, _L, _L, _L, _L, _F, _P, _P],
+        [_P, _I, _L, _L, _P, _P, _P, _I, _L, _L, _I, _I, _P, _I, _L, _L, _L, _L, _L, _F, _P, _P],
     ),
     "uc_kivi_av": (
         _I,
-        [_P, _I, _L, _L, _L, _L, _L, _P, _P, _P, _I, _L, _I, _I, _P, _I, _L, _L, _L, _L, _L,
+        [_P, _I, _L, _L, _L, _L, _L, _P, _P, _P, _I, _L, _L, _I, _I, _P, _I, _L, _L, _L, _L, _L,
          _P, _I, _P, _P],
     ),
     "uc_kivi_attn_decode": (

@@ -54,8 +54,16 @@ def _hipcc() -> str:
     return path
 
 
+# Per-source flags.  The decode kernel rescales its MFMA output accumulators
+# in VALU code; keeping MFMA results in VGPRs avoids moving them between AGPRs
+# and VGPRs every iteration.
+SOURCE_FLAGS = {
+    "uc_decode_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str, obj: str, extra: list[str]) -> None:
-    cmd = [_hipcc(), *COMMON_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [_hipcc(), *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stdout}\n{proc.stderr}")

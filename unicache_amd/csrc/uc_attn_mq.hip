@@ -94,9 +94,10 @@ struct TilePf {
   uint32_t vs[NV], vm[NV];    // their scales / minima, packed (token 2tp | 2tp+1 << 16)
 };
 
+// One head's packed tensors (token-major: key words [word][D], key stats
+// [group][D], values [token][...]); each resource covers the Tq packed tokens.
 struct PackedSrc {
   Rsrc kcode, kscale, kmin, vcode, vscale, vmin;
-  uint32_t nkw, nkg;
 };
 
 template <int BITS, int G>
@@ -108,12 +109,11 @@ __device__ __forceinline__ void issue_tile(TilePf<BITS> &pf, const PackedSrc &sr
     const int cp = e % (kD / 2), j = e / (kD / 2);  // channel pair, word of the tile
     const uint32_t J = t0 / Gm::TPW + j;
     const uint32_t g = (t0 + j * Gm::TPW) / G;
-    pf.kwa[i] = bload32(src.kcode, ((2 * cp) * src.nkw + J) * 4u);
-    pf.kwb[i] = bload32(src.kcode, ((2 * cp + 1) * src.nkw + J) * 4u);
-    pf.ks[i] = bload16(src.kscale, ((2 * cp) * src.nkg + g) * 2u) |
-               (bload16(src.kscale, ((2 * cp + 1) * src.nkg + g) * 2u) << 16);
-    pf.km[i] = bload16(src.kmin, ((2 * cp) * src.nkg + g) * 2u) |
-               (bload16(src.kmin, ((2 * cp + 1) * src.nkg + g) * 2u) << 16);
+    const uint2 w = bload64(src.kcode, (J * kD + 2 * cp) * 4u);  // channels 2cp, 2cp+1 are neighbours
+    pf.kwa[i] = w.x;
+    pf.kwb[i] = w.y;
+    pf.ks[i] = bload32(src.kscale, (g * kD + 2 * cp) * 2u);
+    pf.km[i] = bload32(src.kmin, (g * kD + 2 * cp) * 2u);
   }
 #pragma unroll
   for (int i = 0; i < TilePf<BITS>::NV; ++i) {
@@ -171,16 +171,15 @@ __device__ __forceinline__ void mq_stage_body(const uc_kivi_item &it, const Stag
 
   if (x0 < Tq) {  // packed words (Tq is a multiple of G >= 32, so words never straddle it)
     PackedSrc src;
-    src.nkw = static_cast<uint32_t>(Tq / Gm::TPW);
-    src.nkg = static_cast<uint32_t>(Tq / G);
-    const int64_t kcode_bytes = int64_t(kD) * src.nkw * 4, kstat_bytes = int64_t(kD) * src.nkg * 2;
-    const int64_t vcode_bytes = Tq * Gm::VW * 4, vstat_bytes = Tq * (kD / G) * 2;
-    src.kcode = make_rsrc(static_cast<const char *>(it.key_code) + h * kcode_bytes, kcode_bytes);
-    src.kscale = make_rsrc(static_cast<const char *>(it.key_scale) + h * kstat_bytes, kstat_bytes);
-    src.kmin = make_rsrc(static_cast<const char *>(it.key_min) + h * kstat_bytes, kstat_bytes);
-    src.vcode = make_rsrc(static_cast<const char *>(it.value_code) + h * vcode_bytes, vcode_bytes);
-    src.vscale = make_rsrc(static_cast<const char *>(it.value_scale) + h * vstat_bytes, vstat_bytes);
-    src.vmin = make_rsrc(static_cast<const char *>(it.value_min) + h * vstat_bytes, vstat_bytes);
+    const int64_t cap = it.packed_capacity > 0 ? it.packed_capacity : Tq;  // tokens between heads
+    const int64_t kcode_row = int64_t(kD) * 4 / Gm::TPW, kstat_row = int64_t(kD) * 2 / G;  // bytes per token
+    const int64_t vcode_row = Gm::VW * 4, vstat_row = (kD / G) * 2;
+    src.kcode = make_rsrc(static_cast<const char *>(it.key_code) + h * cap * kcode_row, Tq * kcode_row);
+    src.kscale = make_rsrc(static_cast<const char *>(it.key_scale) + h * cap * kstat_row, Tq * kstat_row);
+    src.kmin = make_rsrc(static_cast<const char *>(it.key_min) + h * cap * kstat_row, Tq * kstat_row);
+    src.vcode = make_rsrc(static_cast<const char *>(it.value_code) + h * cap * vcode_row, Tq * vcode_row);
+    src.vscale = make_rsrc(static_cast<const char *>(it.value_scale) + h * cap * vstat_row, Tq * vstat_row);
+    src.vmin = make_rsrc(static_cast<const char *>(it.value_min) + h * cap * vstat_row, Tq * vstat_row);
     TilePf<BITS> pf;
     issue_tile<BITS, G>(pf, src, static_cast<uint32_t>(x0), tid);
 #pragma unroll
@@ -613,6 +612,9 @@ int mq_check_item(const uc_kivi_item &it, int group_size, int64_t heads_q, int64
   UC_REQUIRE(it.quantized_tokens >= 0 && it.residual_tokens >= 0 && it.quantized_tokens % group_size == 0,
              "attn_mq: quantized tokens must be a non-negative multiple of group_size");
   UC_REQUIRE(it.quantized_tokens + it.residual_tokens > 0, "attn_mq: empty segment");
+  UC_REQUIRE(it.packed_capacity == 0 ||
+                 (it.packed_capacity >= it.quantized_tokens && it.packed_capacity % group_size == 0),
+             "attn_mq: packed_capacity must be 0 or a multiple of group_size >= quantized_tokens");
   UC_REQUIRE(it.query != nullptr && it.out != nullptr, "attn_mq: query/out are NULL");
   UC_REQUIRE((reinterpret_cast<uintptr_t>(it.query) & 15) == 0 && (reinterpret_cast<uintptr_t>(it.out) & 15) == 0,
              "attn_mq: query and out must be 16-byte aligned");

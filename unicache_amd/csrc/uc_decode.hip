@@ -45,11 +45,24 @@ struct PackedView {
   int64_t r_st, r_sh;  // residual strides (token, head); channel stride 1
 };
 
-// Native-layout strides for contiguous packed tensors (kivi_cuda.py:177-182).
 __host__ __device__ inline int log2i(int x) {
   int l = 0;
   while ((1 << l) < x) ++l;
   return l;
+}
+
+// Strides of the 2/4-bit packed tensors in the ABI's token-major layout with
+// capacity `cap` tokens per head.
+__host__ __device__ inline void set_packed_strides(PackedView &v, int64_t cap, int bits, int group, int64_t D) {
+  const int64_t kw = cap * bits / 32, vw = D * bits / 32;
+  v.kc_sh = kw * D; v.kc_sd = 1; v.kc_sw = D;
+  v.ks_sh = (cap / group) * D; v.ks_sd = 1; v.ks_sg = D;
+  v.vc_sh = cap * vw; v.vc_st = vw; v.vc_sw = 1;
+  v.vs_sh = cap * (D / group); v.vs_st = D / group; v.vs_sg = 1;
+}
+
+__host__ __device__ inline int64_t item_capacity(const uc_kivi_item &it) {
+  return it.packed_capacity > 0 ? it.packed_capacity : it.quantized_tokens;
 }
 
 __host__ __device__ inline PackedView native_view(const uc_kivi_item &it, int bits, int group,
@@ -59,13 +72,9 @@ __host__ __device__ inline PackedView native_view(const uc_kivi_item &it, int bi
   v.sd = UC_FP16;
   v.rd = rd;
   const int64_t Tq = it.quantized_tokens;
-  const int64_t kw = Tq * bits / 32, vw = D * bits / 32;
   v.kcode = it.key_code; v.kscale = it.key_scale; v.kmin = it.key_min;
   v.vcode = it.value_code; v.vscale = it.value_scale; v.vmin = it.value_min;
-  v.kc_sh = D * kw; v.kc_sd = kw; v.kc_sw = 1;
-  v.ks_sh = D * (Tq / group); v.ks_sd = Tq / group; v.ks_sg = 1;
-  v.vc_sh = Tq * vw; v.vc_st = vw; v.vc_sw = 1;
-  v.vs_sh = Tq * (D / group); v.vs_st = D / group; v.vs_sg = 1;
+  set_packed_strides(v, item_capacity(it), bits, group, D);
   v.rkey = it.residual_key; v.rval = it.residual_value;
   v.Tq = Tq; v.Tr = it.residual_tokens; v.Hkv = Hkv; v.D = D;
   v.r_st = Hkv * D; v.r_sh = D;
@@ -361,8 +370,9 @@ __global__ __launch_bounds__(kThreads) void qk_kernel(PackedView v, QKParams p) 
 // Strides of the packed tensors for the QK/AV entry points: kernel-native
 // layout for 2/4-bit, UniCache's uint8 layout for 8-bit (physical.py:66-68).
 PackedView parts_view(const void *kc, const void *ks, const void *km, const void *vc, const void *vs,
-                             const void *vm, int64_t Tq, int bits, int group, const void *rk, const void *rv,
-                             int64_t Tr, int64_t r_st, int64_t r_sh, int64_t Hkv, int64_t D, int sd, int rd) {
+                             const void *vm, int64_t Tq, int64_t cap, int bits, int group, const void *rk,
+                             const void *rv, int64_t Tr, int64_t r_st, int64_t r_sh, int64_t Hkv, int64_t D, int sd,
+                             int rd) {
   PackedView v{};
   v.r_st = r_st;
   v.r_sh = r_sh;
@@ -377,11 +387,7 @@ PackedView parts_view(const void *kc, const void *ks, const void *km, const void
     v.vc_sh = D; v.vc_st = Hkv * D; v.vc_sw = 1;
     v.vs_sh = D / group; v.vs_st = Hkv * (D / group); v.vs_sg = 1;
   } else {
-    const int64_t kw = Tq * bits / 32, vw = D * bits / 32;
-    v.kc_sh = D * kw; v.kc_sd = kw; v.kc_sw = 1;
-    v.ks_sh = D * (Tq / group); v.ks_sd = Tq / group; v.ks_sg = 1;
-    v.vc_sh = Tq * vw; v.vc_st = vw; v.vc_sw = 1;
-    v.vs_sh = Tq * (D / group); v.vs_st = D / group; v.vs_sg = 1;
+    set_packed_strides(v, cap > 0 ? cap : Tq, bits, group, D);
   }
   return v;
 }
@@ -407,6 +413,9 @@ int decode_common(const uc_kivi_item *items_dev, const uc_kivi_item *single, int
   UC_REQUIRE(half_dtype(q_dtype) && half_dtype(res_dtype) && valid_dtype(out_dtype),
              "%s: query/residual must be bf16 or fp16", name);
   UC_REQUIRE(max_tq % group_size == 0, "%s: quantized tokens must be a multiple of group_size", name);
+  UC_REQUIRE(single == nullptr || single->packed_capacity == 0 ||
+                 (single->packed_capacity >= single->quantized_tokens && single->packed_capacity % group_size == 0),
+             "%s: packed_capacity must be 0 or a multiple of group_size >= quantized_tokens", name);
   if (n_items == 0) return UC_OK;
   UC_REQUIRE(segs == 1 || decode_mfma_supported(bits, group_size, D, (Hq / Hkv) * Lq),
              "%s: segment groups need head_dim 128, group 32/64/128 and at most 16 query rows per KV head", name);
@@ -514,7 +523,7 @@ extern "C" int uc_kivi_attn_decode_segments(const uc_kivi_item *items_device, in
 
 extern "C" int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int64_t heads_q,
                           const void *key_code, const void *key_scale, const void *key_min, int stats_dtype,
-                          int64_t quantized_tokens, int bits, int group_size,
+                          int64_t quantized_tokens, int64_t packed_capacity, int bits, int group_size,
                           const void *residual_key, int res_dtype, int64_t residual_tokens,
                           int64_t r_st, int64_t r_sh,
                           int64_t heads_kv, int64_t head_dim, float sm_scale,
@@ -525,6 +534,8 @@ extern "C" int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int
   UC_REQUIRE(heads_q > 0 && heads_kv > 0 && heads_q % heads_kv == 0, "Query heads must be divisible by KIVI KV heads");
   UC_REQUIRE(head_dim > 0 && head_dim <= kMaxD, "uc_kivi_qk: head_dim must be <= %d", kMaxD);
   UC_REQUIRE(quantized_tokens % group_size == 0 && residual_tokens >= 0, "uc_kivi_qk: bad token counts");
+  UC_REQUIRE(packed_capacity == 0 || (packed_capacity >= quantized_tokens && packed_capacity % group_size == 0),
+             "uc_kivi_qk: packed_capacity must be 0 or a multiple of group_size >= quantized_tokens");
   const int64_t total = quantized_tokens + residual_tokens;
   if (total == 0 || query_len == 0) return UC_OK;
   // dense keys and at least one wave of query rows per KV head: MFMA tiles
@@ -534,9 +545,9 @@ extern "C" int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int
                          query_len, heads_q, residual_tokens, heads_kv))
     return launch_qk_logits_mfma(q_dtype, query, heads_q * head_dim, head_dim, residual_key, r_st, r_sh, query_len,
                                  heads_q, residual_tokens, heads_kv, sm_scale, logits, as_stream(stream));
-  PackedView v = parts_view(key_code, key_scale, key_min, nullptr, nullptr, nullptr, quantized_tokens, bits,
-                            group_size, residual_key, nullptr, residual_tokens, r_st, r_sh, heads_kv, head_dim,
-                            stats_dtype, res_dtype);
+  PackedView v = parts_view(key_code, key_scale, key_min, nullptr, nullptr, nullptr, quantized_tokens,
+                            packed_capacity, bits, group_size, residual_key, nullptr, residual_tokens, r_st, r_sh,
+                            heads_kv, head_dim, stats_dtype, res_dtype);
   QKParams p{};
   p.Hq = heads_q; p.Lq = query_len; p.group = heads_q / heads_kv; p.rows = p.group * query_len;
   p.total = total; p.sm_scale = sm_scale; p.query = query; p.qd = q_dtype; p.logits = logits;
@@ -554,7 +565,7 @@ extern "C" int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int
 extern "C" int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t p_si, int64_t p_st,
                           int64_t query_len, int64_t heads_q,
                           const void *value_code, const void *value_scale, const void *value_min, int stats_dtype,
-                          int64_t quantized_tokens, int bits, int group_size,
+                          int64_t quantized_tokens, int64_t packed_capacity, int bits, int group_size,
                           const void *residual_value, int res_dtype, int64_t residual_tokens,
                           int64_t r_st, int64_t r_sh,
                           int64_t heads_kv, int64_t head_dim,
@@ -565,6 +576,8 @@ extern "C" int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t 
   UC_REQUIRE(heads_q > 0 && heads_kv > 0 && heads_q % heads_kv == 0, "Query heads must be divisible by KIVI KV heads");
   UC_REQUIRE(head_dim > 0 && head_dim <= kMaxD, "uc_kivi_av: head_dim must be <= %d", kMaxD);
   UC_REQUIRE(quantized_tokens % group_size == 0 && residual_tokens >= 0, "uc_kivi_av: bad token counts");
+  UC_REQUIRE(packed_capacity == 0 || (packed_capacity >= quantized_tokens && packed_capacity % group_size == 0),
+             "uc_kivi_av: packed_capacity must be 0 or a multiple of group_size >= quantized_tokens");
   if (query_len == 0) return UC_OK;
   const int64_t total = quantized_tokens + residual_tokens;
   hipStream_t s = as_stream(stream);
@@ -591,6 +604,7 @@ extern "C" int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t 
   it.value_code = value_code; it.value_scale = value_scale; it.value_min = value_min;
   it.residual_value = residual_value; it.out = out;
   it.quantized_tokens = quantized_tokens; it.residual_tokens = residual_tokens;
+  it.packed_capacity = packed_capacity;
   DecodeParams p{};
   p.Hq = heads_q; p.Hkv = heads_kv; p.D = head_dim; p.Lq = query_len; p.group = heads_q / heads_kv;
   p.rows = p.group * query_len; p.splits_packed = sp_packed; p.splits_total = splits;
@@ -602,8 +616,8 @@ extern "C" int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t 
   p.qd = UC_BF16; p.pd = p_dtype; p.rd = res_dtype;
   dim3 grid(splits, heads_kv, ceil_div(p.rows, kRows));
   const PackedView v = parts_view(nullptr, nullptr, nullptr, value_code, value_scale, value_min, quantized_tokens,
-                                  bits, group_size, nullptr, residual_value, residual_tokens, r_st, r_sh, heads_kv,
-                                  head_dim, stats_dtype, res_dtype);
+                                  packed_capacity, bits, group_size, nullptr, residual_value, residual_tokens, r_st,
+                                  r_sh, heads_kv, head_dim, stats_dtype, res_dtype);
   if (bits == 2)
     hipLaunchKernelGGL((decode_partial_kernel<2, true, false>), grid, dim3(kThreads), 0, s, nullptr, it, v, p);
   else if (bits == 4)

@@ -1,34 +1,32 @@
 // MFMA split-K decode over KIVI-packed KV (head_dim 128, 2/4-bit codes).
 //
-// One workgroup (2 waves) owns a packed split of one unit (item, KV head) --
+// One workgroup (4 waves) owns a packed split of one unit (item, KV head) --
 // every S-th super-tile (16 key words of every channel) starting at the split
 // index -- or a residual split.  The S splits of a unit run side by side on
 // one XCD, so the 128-byte lines of the channel-major key streams are read
 // from HBM about once although each split uses a part of them.  An iteration
-// stages one super-tile and each wave takes half of its token positions.  The
-// <= 16 query rows of a KV head (query heads x query length) form the N = 16
-// columns of every MFMA.
+// stages one super-tile in LDS; wave w takes its tiles w*TW .. w*TW + TW - 1
+// (a tile = 16 consecutive tokens).  The <= 16 query rows of a KV head (query
+// heads x query length) form the N = 16 columns of every MFMA.
 //
-// Keys (QK^T on v_mfma_f32_16x16x32_f16).  A key word holds TPW = 32/bits
-// tokens of one channel.  MFMA rows are 16 consecutive words at one token
-// position p, so each lane keeps its row's words for 32 channels in
-// registers and reuses them for all positions of its half.  A code at bit
-// offset BITS*e of a 16-bit half is turned into fp16 by OR-ing its bits into
-// the mantissa of 2^(10 - BITS*e), whose mantissa unit is then exactly 1, and
-// subtracting that power of two; one packed FMA with the fp16 scale/min gives
-// k = fp16(code*scale + min).  The query (fp16) is the constant B operand.
+// Keys (S^T = K Q^T on v_mfma_f32_16x16x32_f16).  MFMA rows are the 16 tokens
+// of a tile, which lie in one quantization group, so
+//     logit = sum_c (q_c s_c) code_c + sum_c q_c m_c :
+// the key scale is folded into the B operand once per group (B' = q * s), and
+// the minimum term is one MFMA per group whose A rows all hold the minima.
+// Staging interleaves the words of channel pairs (c, c+1) byte by byte: one
+// dword holds byte k of both words, in its two 16-bit halves, so each A
+// register -- two channels at the row's position -- is one AND that leaves
+// code << BITS*e (e < 8/BITS, at most 6 bits up) in each half: an fp16 value
+// code * 2^(BITS*e - 24), which the MFMA multiplies exactly.  The row's power of two, the
+// softmax scale and the minimum term are applied in one FMA per logit.
 //
-// Values (O^T += V^T P^T on v_mfma_f32_16x16x32_f16).  A value word holds
-// TPW channels of one token; the A operand wants token pairs of one channel
-// per register.  A 32-channel block is split into its even and odd channels
-// (MFMA row r = channel 32b + 2r + i), so the two channels of a lane share one
-// byte: one v_perm gathers that byte of two tokens into the two 16-bit halves
-// and one AND per channel leaves code << offset in each half -- an fp16
-// denormal code * 2^(offset - 24), which the MFMA multiplies exactly; the
-// power of two is undone per channel at the end.  The per-token value scale
-// rides in the B operand (P * scale); the per-token value minimum is folded
-// back with one more MFMA (min x P) whose rows all hold sum_t P*min of value
-// group g.
+// Values (O^T += V^T P^T).  MFMA rows are 16 channels, K = 32 tokens (two
+// tiles).  Staging interleaves the words of token pairs the same way, so each A
+// register (two tokens of the row's channel) is one AND; the power of two of
+// each output channel is undone once at the end.  The per-token value scale
+// rides in the B operand (P * scale, per channel group); the per-token value
+// minimum returns through one MFMA per K block whose A rows are the groups.
 //
 // Each split writes a normalised fp16 partial with its (max, sum); a second
 // kernel merges the splits with a log-sum-exp combine.
@@ -43,28 +41,61 @@ namespace {
 using namespace mf;
 
 constexpr int kXcds = 8;  // XCDs of an MI355X; workgroup i of a launch runs on XCD i % 8
-constexpr int kWaves = 2;
+constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
-constexpr int kResWaveTokens = 128;  // residual tokens per wave per residual split
+constexpr int kResWaveTokens = 64;  // residual tokens per wave per residual split (4 tiles)
+constexpr int kWgPerCu = 3;         // resident workgroups per CU (LDS: ~51 KB each; <= 168 VGPRs)
+constexpr float kLazyLog2 = 8.0f;   // softmax reference slack (log2 units)
+
+// Tile geometry of `BITS`-bit codes with groups of G tokens / channels.
+template <int BITS, int G>
+struct Tiles {
+  static constexpr int TPW = 32 / BITS;       // codes per word
+  static constexpr int CPB = 8 / BITS;        // codes per byte
+  static constexpr int ST = 16 * TPW;         // tokens per super-tile (16 key words)
+  static constexpr int NT = ST / 16;          // 16-token tiles per super-tile
+  static constexpr int TW = NT / kWaves;      // tiles per wave
+  static constexpr int KG = ST / G;           // key groups per super-tile
+  static constexpr int NGD = kD / G;          // value groups per token
+  static constexpr int VWPT = kD / TPW;       // value words per token
+  static constexpr int NTP = ST / 2;          // token pairs per super-tile
+  static constexpr uint32_t MASK = (1u << BITS) - 1u;
+  // Staged words are "byte spread": dword (byte k of word a, byte k of word
+  // b) at bits 0-7 and 16-23, so a code sits at most 6 bits up its 16-bit
+  // half and the AND leaves an fp16 denormal (or small normal) that is
+  // exactly code * 2^(BITS e - 24).
+  // key words [word j][byte k][channel pair]: rows of 64 pairs padded to 80
+  // dwords (the four bytes one read touches fall on different banks), words
+  // 324 dwords apart (the four word quads of one staging write likewise)
+  static constexpr int KROW = 80;
+  static constexpr int KJ = 4 * KROW + 4;
+  // value words [word w][byte k][token pair]
+  static constexpr int VROW = NTP + 16;
+  static constexpr int VWS = 4 * VROW + (BITS == 2 ? 8 : 4);
+  static_assert(TW >= 2 && TW % 2 == 0, "a wave owns whole 32-token value blocks");
+  static_assert(KG >= 1 && G % 16 == 0, "a tile lies in one group");
+};
+
+// v_perm selector: byte k of src1 at byte 0, byte k of src0 at byte 2, zeros elsewhere.
+__device__ __forceinline__ constexpr uint32_t byte_spread_sel(int k) {
+  return uint32_t(k) | (0x0cu << 8) | (uint32_t(4 + k) << 16) | (0x0cu << 24);
+}
 
 template <int BITS, int G>
 struct DecShared {
-  using Gm = Geo<BITS>;
-  static constexpr int T = Gm::ST;           // tokens staged per iteration (one super-tile)
-  static constexpr int KG = T / G;           // key groups per iteration
-  static constexpr int NGD = kD / G;         // value groups per token
-  static constexpr int JW = T / Gm::TPW;     // key words per channel per iteration
-  static constexpr int KPAD = kD + 16;       // key-stat row of 72 dwords: the 8 groups one read touches start 8 banks apart
-  _Float16 ks[KG][KPAD], km[KG][KPAD];                  // key stats [group][channel]
-  // value stats [group][position / 2][word / 4][position % 2][word % 4]: the
-  // 8 values one MFMA k-slice needs (words 4k..4k+3 at positions 2j, 2j+1) are
-  // one 16-byte read
-  _Float16 vs[NGD][Gm::TPW / 2][JW / 4][2][4], vm[NGD][Gm::TPW / 2][JW / 4][2][4];
-  uint32_t kw[4][4][16][8];                             // key words [block][k-slice][row][channel]
-  // value words [position][word][row], rows padded to 20 dwords: a lane reads
-  // four rows of one word as 16 bytes, and staging writes hit distinct banks
-  static constexpr int VROW = 20;
-  uint32_t vw[Gm::TPW][Gm::VW][VROW];
+  using Tl = Tiles<BITS, G>;
+  union {
+    struct {
+      uint32_t kw[16 * Tl::KJ];
+      uint32_t vw[Tl::VWPT * Tl::VWS];
+      _Float16 ks[Tl::KG][kD], km[Tl::KG][kD];   // key stats [group][channel]
+      _Float16 vs[Tl::NGD][Tl::ST], vm[Tl::NGD][Tl::ST];  // value stats [group][token]
+    } st;
+    struct {
+      float o[kWaves - 1][16][kD];  // waves 1.. : scaled partial outputs [query row][channel]
+      float ml[kWaves][16][2];      // every wave's (max, sum) per query row
+    } mrg;
+  };
 };
 
 struct MfmaParams {
@@ -90,78 +121,58 @@ __device__ __forceinline__ bool split_has_work(int64_t split, int64_t tq, int64_
 }
 
 // Online-softmax state of one wave.  The output is accumulated transposed
-// (O^T = V^T P^T): lane (n, k) owns query column n, so every rescale is
-// lane-local.
+// (O^T = V^T P^T): lane (n, k) owns query column n and output channels
+// 16 b + 4 k + v of accumulator b, so every rescale is lane-local.
 struct WaveState {
-  f4 o[8];     // lane (n = lane%16, k = lane/16): query n, channel out_channel(cb, k, v)
-  f4 cmin[4];  // sum_t P*min of value group g (every row of the block holds it)
-  float m;     // running max of query n (log2 units), equal across the k-slices
-  float l;     // this lane's share of the running sum (reduced over the k-slices at the end)
+  f4 o[8];
+  f4 cmin;  // row g < groups: sum_t P * value minimum of group g (packed splits)
+  float m;  // running max of query n (log2 units), equal across the k-slices
+  float l;  // this lane's share of the running sum (reduced over the k-slices at the end)
 };
 
-// Base-2 softmax of a tile of logits (acc[p][v] = row 4k+v of the C layout,
-// column = query), folded into the running state; returns with acc holding the
-// probabilities and the output rescaled.
+// Fold NP tiles of base-2 logits (acc[i][v]: token 16 i + 4 k + v of the
+// wave's tiles, column = query) into the running state; acc returns holding
+// the probabilities and the output is rescaled.  `valid_rows` tokens of the
+// wave's tiles are real (the rest of the last super-tile reads past the end).
 template <int NP>
-__device__ __forceinline__ void softmax_tile(f4 (&acc)[NP], const bool (&valid)[4], bool full, float scale_log2,
-                                             WaveState &st) {
-  if (!full) {  // only the last iteration of a segment has rows past its end
+__device__ __forceinline__ void softmax_tiles(f4 (&acc)[NP], int valid_rows, WaveState &st, int kap) {
+  if (valid_rows < 16 * NP) {
 #pragma unroll
-    for (int pp = 0; pp < NP; ++pp)
+    for (int i = 0; i < NP; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        if (!valid[v]) acc[pp][v] = kNegInf;
+        if (16 * i + 4 * kap + v >= valid_rows) acc[i][v] = kNegInf;
   }
   float mx = kNegInf;
 #pragma unroll
-  for (int pp = 0; pp < NP; ++pp)
+  for (int i = 0; i < NP; ++i)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) mx = fmaxf(mx, acc[pp][v]);
+    for (int v = 0; v < 4; ++v) mx = fmaxf(mx, acc[i][v]);
   mx = max_over_slices(mx);
-  const float m_new = fmaxf(st.m, mx * scale_log2);
+  // The reference m is raised only when a logit exceeds it by more than
+  // kLazyLog2 (-inf + kLazyLog2 = -inf: the first finite tile raises it), so
+  // the output is rarely rescaled and probabilities stay <= 2^kLazyLog2, well
+  // inside fp16.  (m, l) stay a consistent pair: l = sum 2^(x - m).
+  const bool raise = mx > st.m + kLazyLog2;
+  const float m_new = raise ? mx : st.m;
   const float m_ref = m_new == kNegInf ? 0.0f : m_new;  // keeps -inf - m_ref at -inf (exp 0), never NaN
   float sum = 0.0f;
 #pragma unroll
-  for (int pp = 0; pp < NP; ++pp)
+  for (int i = 0; i < NP; ++i)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const float e = fast_exp2(__builtin_fmaf(acc[pp][v], scale_log2, -m_ref));
-      acc[pp][v] = e;
+      const float e = fast_exp2(acc[i][v] - m_ref);
+      acc[i][v] = e;
       sum += e;
     }
-  const float alpha = fast_exp2(st.m - m_ref);
+  const float alpha = raise ? fast_exp2(st.m - m_ref) : 1.0f;
   st.l = st.l * alpha + sum;
   st.m = m_new;
-  if (__any(alpha != 1.0f)) {
+  if (__any(raise)) {
 #pragma unroll
     for (int b = 0; b < 8; ++b) st.o[b] *= alpha;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) st.cmin[g] *= alpha;
+    st.cmin *= alpha;
   }
-}
-
-// Output row v of accumulator cb in lane k-slice kap: channel
-// 32 (cb / 2) + 8 kap + 2 v + cb % 2 -- MFMA cb holds the even (cb % 2 = 0) or
-// odd channels of the 32-channel block cb / 2, so a lane's eight outputs of a
-// block are the contiguous channels 32 (cb / 2) + 8 kap + [0, 8).
-__device__ __forceinline__ constexpr int out_channel(int cb, int kap, int v) {
-  return 32 * (cb >> 1) + 8 * kap + 2 * v + (cb & 1);
-}
-
-// Bit offset of channel c's code inside the byte that holds it.
-template <int BITS>
-__device__ __forceinline__ constexpr int value_shift(int c) {
-  return BITS == 2 ? 2 * (c & 3) : 4 * (c & 1);
-}
-
-// Selection B operand that picks channel 2n + i of a 32-channel A fragment
-// into column n: B[k][n] = (k == 2n + i).
-__device__ __forceinline__ h8 channel_selector(int lane, int i) {
-  const int n = lane & 15, kap = lane >> 4;
-  h8 b;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) b[j] = to_h(8 * kap + j == 2 * n + i ? 1.0f : 0.0f);
-  return b;
 }
 
 // ------------------------------------------------------------ packed path --
@@ -172,7 +183,8 @@ constexpr int kQPad = kD + 8;
 template <int QD>
 __device__ __forceinline__ void stage_queries_t(_Float16 (*sq)[kQPad], const void *query, int64_t h,
                                                 const MfmaParams &p) {
-  // 16 rows x 128 channels; thread t converts 16 consecutive channels of row t/8
+  // 16 rows x 128 channels; thread t < 128 converts 16 consecutive channels of row t/8
+  if (threadIdx.x >= 128) return;
   const int n = threadIdx.x / 8, d0 = (threadIdx.x % 8) * 16;
   uint4 raw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
   if (n < p.rows) {
@@ -190,7 +202,6 @@ __device__ __forceinline__ void stage_queries_t(_Float16 (*sq)[kQPad], const voi
 // fp32 queries take the element-wise path.
 __device__ __forceinline__ void stage_queries(_Float16 (*sq)[kQPad], const void *query, int64_t h,
                                               const MfmaParams &p) {
-  static_assert(kThreads == 16 * 8, "one thread per 16 channels of a query row");
   if (p.qd == UC_BF16) {
     stage_queries_t<UC_BF16>(sq, query, h, p);
   } else if (p.qd == UC_FP16) {
@@ -212,272 +223,231 @@ __device__ __forceinline__ h8 query_frag(const _Float16 (*sq)[kQPad], int kb, in
   return *reinterpret_cast<const h8 *>(&sq[lane & 15][32 * kb + 8 * (lane >> 4)]);
 }
 
-// Everything one iteration (T tokens of one KV head) reads from HBM, held in
-// registers so the next iteration's loads overlap this iteration's MFMAs.
+// Everything one super-tile reads from HBM, held in registers so the next
+// super-tile's loads overlap this one's MFMAs.  The packed tensors are
+// token-major, so every stream of a super-tile is one contiguous run of the
+// head's rows.  Thread t loads:
+//   key words: channels 4c .. 4c+3 (c = t % 32) of words t / 32 and 8 + t / 32;
+//   value words: word quad t % NQ of tokens 2tp, 2tp+1 (tp = t / NQ);
+//   key stats: 8 channels (t % 16) of group (t % 128) / 16, scales (t < 128)
+//     or minima;
+//   value stats: 16 bytes of the scales (t < 128) or minima.
 template <int BITS, int G>
 struct Prefetch {
-  using Gm = Geo<BITS>;
-  using Sh = DecShared<BITS, G>;
-  static constexpr int NKD = (Sh::KG + 1) / 2 + 1;         // dwords of one key-stat row segment
-  static constexpr int NVS = Sh::T * Sh::NGD / 8;           // 16-byte chunks of value stats
-  static constexpr int VS4 = (NVS + kThreads - 1) / kThreads;
-  static constexpr int NVW = Gm::ST * Gm::VW / 4 / kThreads;  // 16-byte chunks of value words per thread
-  static constexpr int NKB = 4 / kWaves;                       // key-word blocks per thread
-  uint32_t ks[NKD], km[NKD];  // thread = channel: KG halves from a 4-byte aligned start
-  uint4 vs[VS4], vm[VS4];
-  uint4 vw[NVW];
-  uint32_t kw[NKB][8];
+  uint4 kw[2], vw[2];
+  uint4 ks, vs;
 };
 
-template <int BITS, int G>
 struct PackedRegion {
   Rsrc kcode, kscale, kmin, vcode, vscale, vmin;
-  uint32_t nkw, nkg;  // key words / key groups per channel row
 };
 
-// Which 16-byte chunk of value words load q of lane group a brings: the four
-// groups of one load land on four different 16-dword bank windows of the
-// [position][word][row] staging layout (block stride 20 dwords).
-template <int BITS>
-__device__ __forceinline__ void value_chunk(int q, int a, int &pos, int &quad) {
-  if constexpr (BITS == 2) {  // 8 words = 2 quads per token, 16 positions: 8 loads
-    pos = 2 * q + (a >> 1);
-    quad = a & 1;
-  } else {                    // 16 words = 4 quads per token, 8 positions: 8 loads
-    pos = q;
-    quad = a;
-  }
-}
-
-// The first N dwords of d: consecutive dwords from byte offset `off` (4-byte
-// aligned) in the fewest loads.
-template <int N, int M>
-__device__ __forceinline__ void load_dwords(uint32_t (&d)[M], Rsrc r, uint32_t off) {
-  static_assert(N <= M, "load fits the array");
-  int q = 0;
-#pragma unroll
-  for (; q + 4 <= N; q += 4) {
-    const uint4 v = bload128(r, off + 4u * q);
-    d[q] = v.x, d[q + 1] = v.y, d[q + 2] = v.z, d[q + 3] = v.w;
-  }
-  if constexpr (N % 4 >= 2) {
-    const uint2 v = bload64(r, off + 4u * q);
-    d[q] = v.x, d[q + 1] = v.y;
-    q += 2;
-  }
-  if constexpr (N % 2 == 1) d[N - 1] = bload32(r, off + 4u * (N - 1));
-}
-
-// Issue the loads of the iteration starting at token t0 (multiple of T).
+// Issue the loads of the super-tile starting at token t0 (a multiple of ST).
+// Rows past the packed tokens fall outside the buffer resources and read as 0.
 template <int BITS, int G>
-__device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedRegion<BITS, G> &rg, uint32_t t0) {
-  using Gm = Geo<BITS>;
-  using Sh = DecShared<BITS, G>;
-  using Pf = Prefetch<BITS, G>;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 15, kap = lane >> 4;
-  // key stats [D][nkg]: thread = channel, its KG groups as dwords from the
-  // 4-byte boundary at or below the first (realigned when staged)
-  // (one 16-byte load per four dwords: each load of a wave touches 64 rows, so
-  // fewer, wider loads mean fewer memory requests; when every row segment
-  // starts on a dword -- even nkg and t0 / G -- the last dword is not needed)
-  {
-    const uint32_t d0 = (tid * rg.nkg + t0 / G) >> 1;
-    if (((rg.nkg | (t0 / G)) & 1u) == 0u) {
-      load_dwords<Pf::NKD - 1>(pf.ks, rg.kscale, d0 * 4u);
-      load_dwords<Pf::NKD - 1>(pf.km, rg.kmin, d0 * 4u);
-      pf.ks[Pf::NKD - 1] = pf.km[Pf::NKD - 1] = 0u;  // read by the realignment with shift 0
-    } else {
-      load_dwords<Pf::NKD>(pf.ks, rg.kscale, d0 * 4u);
-      load_dwords<Pf::NKD>(pf.km, rg.kmin, d0 * 4u);
+__device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedRegion &rg, uint32_t t0) {
+  using Tl = Tiles<BITS, G>;
+  const int tid = threadIdx.x;
+  {  // key words [word][D]: 16 rows of 512 bytes
+    const uint32_t base = (t0 / Tl::TPW) * kD * 4u + 16u * tid;
+    pf.kw[0] = bload128(rg.kcode, base);
+    pf.kw[1] = bload128(rg.kcode, base + 8u * kD * 4u);
+  }
+  {  // value words of two neighbouring tokens
+    constexpr uint32_t NQ = Tl::VWPT / 4;
+    const uint32_t tp = tid / NQ, wq = tid % NQ;
+    const uint32_t tok = t0 + 2 * tp;
+    pf.vw[0] = bload128(rg.vcode, (tok * Tl::VWPT + 4 * wq) * 4u);
+    pf.vw[1] = bload128(rg.vcode, ((tok + 1) * Tl::VWPT + 4 * wq) * 4u);
+  }
+  {  // key stats [group][D]: KG rows of 256 bytes per stat
+    constexpr int NKS = Tl::KG * 16;  // 16-byte chunks per stat
+    const int i = tid & 127;
+    const Rsrc r = tid < 128 ? rg.kscale : rg.kmin;
+    pf.ks = i < NKS ? bload128(r, (t0 / G) * kD * 2u + 16u * i) : make_uint4(0, 0, 0, 0);
+  }
+  {  // value stats [Tq][NGD]: 16 bytes each
+    constexpr int NVC = Tl::ST * Tl::NGD / 8;  // 16-byte chunks per stat
+    const int i = tid & 127;
+    const Rsrc r = tid < 128 ? rg.vscale : rg.vmin;
+    pf.vs = i < NVC ? bload128(r, (t0 * Tl::NGD + 8 * i) * 2u) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Move a landed prefetch into the interleaved / transposed LDS layouts.
+template <int BITS, int G>
+__device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch<BITS, G> &pf) {
+  using Tl = Tiles<BITS, G>;
+  const int tid = threadIdx.x;
+  constexpr uint32_t kLo = 0x05040100u, kHi = 0x07060302u;  // low / high halves of (a, b)
+  {  // channels 4c .. 4c+3 = pairs 2c, 2c+1 of words j and j + 8
+    const uint32_t pc = 2 * (tid & 31), j = tid >> 5;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint4 w = pf.kw[h];
+      uint32_t *row = &sh.st.kw[(j + 8 * h) * Tl::KJ + pc];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<uint2 *>(&row[k * Tl::KROW]) =
+            make_uint2(__builtin_amdgcn_perm(w.y, w.x, byte_spread_sel(k)),
+                       __builtin_amdgcn_perm(w.w, w.z, byte_spread_sel(k)));
     }
   }
-  // value stats [Tq][NGD]
-#pragma unroll
-  for (int q = 0; q < Pf::VS4; ++q) {
-    const int i = q * kThreads + tid;
-    const uint32_t off = (t0 * Sh::NGD + 8 * (i < Pf::NVS ? i : 0)) * 2u;
-    pf.vs[q] = bload128(rg.vscale, off);
-    pf.vm[q] = bload128(rg.vmin, off);
-  }
-  // value words [Tq][VW] of the super-tile, 16 bytes (4 words of one token)
-  // per load: lane (row = lane%16, group a = lane/16) of wave w takes word-row
-  // `row` at (position, word quad) = value_chunk(q * kWaves + w, a)
-#pragma unroll
-  for (int q = 0; q < Pf::NVW; ++q) {
-    int pos, quad;
-    value_chunk<BITS>(q * kWaves + wave, lane >> 4, pos, quad);
-    const uint32_t tok = t0 + (lane & 15) * Gm::TPW + pos;
-    pf.vw[q] = bload128(rg.vcode, (tok * Gm::VW + 4 * quad) * 4u);
-  }
-  // key words [D][nkw]: lane (row r, k-slice kap) of wave w reads word J of
-  // the 16 channels 32 kb + 8 kap + [0, 8) of its blocks kb = NKB w + [0, NKB)
-  const uint32_t J = t0 / Gm::TPW + r;
-#pragma unroll
-  for (int b = 0; b < Pf::NKB; ++b)
-#pragma unroll
-    for (int c = 0; c < 8; ++c)
-      pf.kw[b][c] = bload32(rg.kcode, ((32 * (Pf::NKB * wave + b) + 8 * kap + c) * rg.nkw + J) * 4u);
-}
-
-// Move a landed prefetch into the LDS layouts the MFMA loops read.
-template <int BITS, int G>
-__device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch<BITS, G> &pf, uint32_t t0,
-                                          uint32_t nkg) {
-  using Gm = Geo<BITS>;
-  using Sh = DecShared<BITS, G>;
-  using Pf = Prefetch<BITS, G>;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 15, kap = lane >> 4;
   {
-    const uint32_t shift = ((tid * nkg + t0 / G) & 1u) * 16u;  // odd first element: start at the high half
+    constexpr uint32_t NQ = Tl::VWPT / 4;
+    const uint32_t tp = tid / NQ, wq = tid % NQ;
+    const uint32_t a[4] = {pf.vw[0].x, pf.vw[0].y, pf.vw[0].z, pf.vw[0].w};
+    const uint32_t b[4] = {pf.vw[1].x, pf.vw[1].y, pf.vw[1].z, pf.vw[1].w};
 #pragma unroll
-    for (int q = 0; q < (Sh::KG + 1) / 2; ++q) {
-      const uint32_t s2 = __builtin_amdgcn_alignbit(pf.ks[q + 1], pf.ks[q], shift);
-      const uint32_t m2 = __builtin_amdgcn_alignbit(pf.km[q + 1], pf.km[q], shift);
-      sh.ks[2 * q][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s2));
-      sh.km[2 * q][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(m2));
-      if (2 * q + 1 < Sh::KG) {
-        sh.ks[2 * q + 1][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s2 >> 16));
-        sh.km[2 * q + 1][tid] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(m2 >> 16));
+    for (int i = 0; i < 4; ++i) {
+      uint32_t *row = &sh.st.vw[(4 * wq + i) * Tl::VWS + tp];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) row[k * Tl::VROW] = __builtin_amdgcn_perm(b[i], a[i], byte_spread_sel(k));
+    }
+  }
+  {  // key stats arrive as [group][channel] rows already
+    constexpr int NKS = Tl::KG * 16;
+    const int i = tid & 127;
+    if (i < NKS) {
+      _Float16(*dst)[kD] = tid < 128 ? sh.st.ks : sh.st.km;
+      *reinterpret_cast<uint4 *>(&dst[i / 16][8 * (i % 16)]) = pf.ks;
+    }
+  }
+  {
+    constexpr int NVC = Tl::ST * Tl::NGD / 8;
+    const int i = tid & 127;
+    if (i < NVC) {
+      _Float16(*dst)[Tl::ST] = tid < 128 ? sh.st.vs : sh.st.vm;
+      const uint32_t w[4] = {pf.vs.x, pf.vs.y, pf.vs.z, pf.vs.w};
+      if constexpr (Tl::NGD == 4) {  // tokens 2i, 2i+1 x groups 0..3
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<uint32_t *>(&dst[g][2 * i]) =
+              __builtin_amdgcn_perm(w[2 + g / 2], w[g / 2], (g & 1) ? kHi : kLo);
+      } else if constexpr (Tl::NGD == 2) {  // tokens 4i .. 4i+3 x groups 0, 1
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+          *reinterpret_cast<uint2 *>(&dst[g][4 * i]) =
+              make_uint2(__builtin_amdgcn_perm(w[1], w[0], g ? kHi : kLo),
+                         __builtin_amdgcn_perm(w[3], w[2], g ? kHi : kLo));
+      } else {  // one group: tokens 8i .. 8i+7
+        *reinterpret_cast<uint4 *>(&dst[0][8 * i]) = pf.vs;
       }
     }
   }
-#pragma unroll
-  for (int q = 0; q < Pf::VS4; ++q) {
-    if (q * kThreads + tid >= Pf::NVS) break;
-    const int e0 = 8 * (q * kThreads + tid);
-    const uint32_t sw[4] = {pf.vs[q].x, pf.vs[q].y, pf.vs[q].z, pf.vs[q].w};
-    const uint32_t mw[4] = {pf.vm[q].x, pf.vm[q].y, pf.vm[q].z, pf.vm[q].w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int tl = (e0 + e) / Sh::NGD, gd = (e0 + e) % Sh::NGD;
-      const int pos = tl % Gm::TPW, row = tl / Gm::TPW;
-      sh.vs[gd][pos / 2][row / 4][pos % 2][row % 4] =
-          __builtin_bit_cast(_Float16, static_cast<uint16_t>(sw[e / 2] >> (16 * (e % 2))));
-      sh.vm[gd][pos / 2][row / 4][pos % 2][row % 4] =
-          __builtin_bit_cast(_Float16, static_cast<uint16_t>(mw[e / 2] >> (16 * (e % 2))));
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < Pf::NVW; ++q) {
-    int pos, quad;
-    value_chunk<BITS>(q * kWaves + wave, lane >> 4, pos, quad);
-    const uint32_t w4[4] = {pf.vw[q].x, pf.vw[q].y, pf.vw[q].z, pf.vw[q].w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sh.vw[pos][4 * quad + j][lane & 15] = w4[j];
-  }
-#pragma unroll
-  for (int b = 0; b < Pf::NKB; ++b) {
-    uint4 *dst = reinterpret_cast<uint4 *>(&sh.kw[Pf::NKB * wave + b][kap][r][0]);
-    dst[0] = make_uint4(pf.kw[b][0], pf.kw[b][1], pf.kw[b][2], pf.kw[b][3]);
-    dst[1] = make_uint4(pf.kw[b][4], pf.kw[b][5], pf.kw[b][6], pf.kw[b][7]);
-  }
 }
 
-// Logits, softmax and P.V of this wave's half of the staged super-tile.
+// Per-lane constants of the compute loop.
+template <int BITS, int G>
+struct LaneConst {
+  using Tl = Tiles<BITS, G>;
+  uint32_t kaddr;          // key-word read offset of the wave's first tile (without 16 kb)
+  uint32_t kmask;          // AND mask that leaves the row's codes of two channels
+  float pw[4];             // 2^(24 - BITS e) * softmax scale of logit row 4k + v
+  uint32_t vmask;          // AND mask of the lane's value row (channel) within a word half
+  uint32_t vaddr;          // value-word read offset: half and word part of block 0
+};
+
+template <int BITS, int G>
+__device__ __forceinline__ LaneConst<BITS, G> lane_const(int wave, int lane, float scale_log2) {
+  using Tl = Tiles<BITS, G>;
+  LaneConst<BITS, G> lc;
+  const int r = lane & 15, kap = lane >> 4;
+  {  // tile i of the wave starts 16 i / TPW words after its first tile; the row's byte and mask are the same
+    const int tok = 16 * wave * Tl::TW + r;  // token of row r of the wave's first tile within the super-tile
+    const int j = tok / Tl::TPW, pos = tok % Tl::TPW, k = pos / Tl::CPB, e = pos % Tl::CPB;
+    lc.kaddr = j * Tl::KJ + k * Tl::KROW + 4 * kap;
+    lc.kmask = (Tl::MASK << (BITS * e)) * 0x10001u;
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int e = ((4 * kap + v) % Tl::TPW) % Tl::CPB;  // tile row 4k + v: position in word, then in byte
+    lc.pw[v] = float(1 << (24 - BITS * e)) * scale_log2;
+  }
+  {
+    const int ci = r % Tl::TPW;          // channel r of a 16-channel block within its value word
+    const int k = ci / Tl::CPB, e = ci % Tl::CPB;
+    lc.vmask = (Tl::MASK << (BITS * e)) * 0x10001u;
+    lc.vaddr = (r / Tl::TPW) * Tl::VWS + k * Tl::VROW + 2 * kap;
+  }
+  return lc;
+}
+
+__device__ __forceinline__ h8 and_h8(uint4 x, uint32_t m) {
+  return __builtin_bit_cast(h8, make_uint4(x.x & m, x.y & m, x.z & m, x.w & m));
+}
+
+// Logits, softmax and P.V of this wave's tiles of the staged super-tile.
 template <int BITS, int G>
 __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const _Float16 (*sq)[kQPad],
-                                             uint32_t t0, uint32_t nkw, float scale_log2, WaveState &st) {
-  using Gm = Geo<BITS>;
-  using Sh = DecShared<BITS, G>;
-  const int tid = threadIdx.x, lane = tid & 63, half = tid >> 6;
-  const int r = lane & 15, kap = lane >> 4;
-  constexpr int NP = Gm::TPW / 2;  // positions per half word
-  const int gl = (r * Gm::TPW) / G;  // key group of this lane's row
-  bool valid[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) valid[v] = (t0 / Gm::TPW + 4 * kap + v) < nkw;
-  const bool full = t0 / Gm::TPW + 16 <= nkw;  // every word row of the iteration is a real token
+                                             const LaneConst<BITS, G> &lc, int wave, int valid_rows,
+                                             float scale_log2, WaveState &st) {
+  using Tl = Tiles<BITS, G>;
+  const int lane = threadIdx.x & 63, r = lane & 15, kap = lane >> 4;
+  constexpr int GT = G / 16;  // tiles per group
 
-  // ---- keys: logits for 16 word rows x NP positions x 16 query rows
-  f4 acc[NP];
+  // ---- keys: logits of the wave's TW tiles (16 tokens x 16 query rows each)
+  f4 acc[Tl::TW];
+  h8 bp[4];
+  float bias = 0.0f;
 #pragma unroll
-  for (int q = 0; q < NP; ++q) acc[q] = f4{0, 0, 0, 0};
-  const uint32_t sel_half = half ? 0x07060302u : 0x05040100u;
-  // field masks and per-offset fp16 powers of two, kept in registers so each
-  // extraction is a single v_and_or_b32 (as literals the compiler splits it
-  // in two); the empty asm only hides the constants from constant folding
-  uint32_t kmask[Gm::PMAX + 1], magic[Gm::PMAX + 1];
+  for (int i = 0; i < Tl::TW; ++i) {
+    if (i % GT == 0) {  // first tile of a group: B' = q * key scale, and the minimum term
+      const int g = (16 * (wave * Tl::TW + i)) / G;
+      f4 mb = f4{0, 0, 0, 0};
 #pragma unroll
-  for (int e = 0; e <= Gm::PMAX; ++e) {
-    kmask[e] = (Gm::MASK << (BITS * e)) | (Gm::MASK << (16 + BITS * e));
-    const uint32_t m16 = uint32_t(25 - BITS * e) << 10;  // fp16 2^(10 - BITS*e)
-    magic[e] = m16 | (m16 << 16);
-    asm("" : "+v"(kmask[e]));
-    asm("" : "+v"(magic[e]));
-  }
-#pragma unroll 1
-  for (int kb = 0; kb < 4; ++kb) {
-    const uint4 *kp = reinterpret_cast<const uint4 *>(&sh.kw[kb][kap][r][0]);
-    const uint4 w0 = kp[0], w1 = kp[1];
-    const uint32_t kw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-    const h8 s8 = *reinterpret_cast<const h8 *>(&sh.ks[gl][32 * kb + 8 * kap]);
-    const h8 m8 = *reinterpret_cast<const h8 *>(&sh.km[gl][32 * kb + 8 * kap]);
-    const h8 qfrag = query_frag(sq, kb, lane);
-    uint32_t y[4];
-    h2 sp[4], mp[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      y[u] = __builtin_amdgcn_perm(kw[2 * u + 1], kw[2 * u], sel_half);
-      sp[u] = h2{s8[2 * u], s8[2 * u + 1]};
-      mp[u] = h2{m8[2 * u], m8[2 * u + 1]};
-    }
-#pragma unroll
-    for (int pq = 0; pq < NP; ++pq) {
-      const bool direct = pq <= Gm::PMAX;
-      const int pe = direct ? pq : pq - (Gm::PMAX + 1);
-      h8 a;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t src = direct ? y[u] : (y[u] >> Gm::SH);
-        const h2 x = as_h2(and_or(src, kmask[pe], magic[pe])) - as_h2(magic[pe]);
-        const h2 k = __builtin_elementwise_fma(x, sp[u], mp[u]);
-        a[2 * u] = k[0];
-        a[2 * u + 1] = k[1];
+      for (int kb = 0; kb < 4; ++kb) {
+        const h8 qf = query_frag(sq, kb, lane);
+        const h8 s8 = *reinterpret_cast<const h8 *>(&sh.st.ks[g][32 * kb + 8 * kap]);
+        const h8 m8 = *reinterpret_cast<const h8 *>(&sh.st.km[g][32 * kb + 8 * kap]);
+        bp[kb] = qf * s8;
+        mb = mfma32(m8, qf, mb);  // every row of A = the minima: each row gets sum_c m_c q_c
       }
-      acc[pq] = mfma32(a, qfrag, acc[pq]);
+      bias = mb[0] * scale_log2;
     }
-  }
-  softmax_tile<NP>(acc, valid, full, scale_log2, st);
-
-  // ---- values of these positions, two at a time: O^T += V^T P^T on
-  // v_mfma_f32_16x16x32_f16 with k = (word rows 4k..4k+3) x (positions pa, pb).
-  // Row r of MFMA (b, i) is channel 32b + 2r + i: both channels of the lane
-  // sit in byte vbyte of word vword(b) of every token (2-bit: a byte holds 4
-  // channels, the lane takes two neighbours; 4-bit: a byte holds 2)
-  const int vbyte = BITS == 2 ? (r >> 1) & 3 : r & 3;
-  const int vword = BITS == 2 ? r >> 3 : r >> 2;  // word of the block
-  constexpr int WPB = 32 / Gm::TPW;               // value words per 32-channel block
-  const uint32_t vsel = uint32_t(vbyte) | (0x0cu << 8) | ((4u + vbyte) << 16) | (0x0cu << 24);  // [lo.b, 0, hi.b, 0]
-  const int o0 = value_shift<BITS>(2 * r);
-  uint32_t vmask[2] = {(Gm::MASK << o0) | (Gm::MASK << (16 + o0)), (Gm::MASK << (o0 + BITS)) | (Gm::MASK << (16 + o0 + BITS))};
+    f4 a = f4{0, 0, 0, 0};
 #pragma unroll
-  for (int j = 0; j < NP / 2; ++j) {
-    const int pa = half * NP + 2 * j, pb = pa + 1;
-    const h4 pa4 = cvt4(acc[2 * j]), pb4 = cvt4(acc[2 * j + 1]);
+    for (int kb = 0; kb < 4; ++kb) {
+      const uint4 x = *reinterpret_cast<const uint4 *>(&sh.st.kw[lc.kaddr + (16 * i / Tl::TPW) * Tl::KJ + 16 * kb]);
+      a = mfma32(and_h8(x, lc.kmask), bp[kb], a);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[i][v] = __builtin_fmaf(a[v], lc.pw[v], bias);
+  }
+  softmax_tiles<Tl::TW>(acc, valid_rows, st, kap);
+
+  // ---- values: O^T += V^T P^T over 32-token blocks (tiles 2kc, 2kc + 1):
+  // K slot 8k + j is token 4k + j of the first tile (j < 4) or 4k + j - 4 of
+  // the second, the layout of the two logit accumulators
+#pragma unroll
+  for (int kc = 0; kc < Tl::TW / 2; ++kc) {
+    const int ta = wave * Tl::TW + 2 * kc;  // first tile of the block within the super-tile
+    const h4 pa4 = cvt4(acc[2 * kc]), pb4 = cvt4(acc[2 * kc + 1]);
     const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
-    h8 ps[Sh::NGD];  // P * value scale, per value group
-#pragma unroll
-    for (int g = 0; g < Sh::NGD; ++g) {
-      const h8 s8 = *reinterpret_cast<const h8 *>(&sh.vs[g][pa / 2][kap][0][0]);
-      const h8 m8 = *reinterpret_cast<const h8 *>(&sh.vm[g][pa / 2][kap][0][0]);
-      ps[g] = p8 * s8;
-      // every row of A = the value minima: each output row gets sum_t P*min
-      st.cmin[g] = mfma32(m8, p8, st.cmin[g]);
-    }
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int wi = WPB * b + vword;
-      const uint4 wa = *reinterpret_cast<const uint4 *>(&sh.vw[pa][wi][4 * kap]);
-      const uint4 wb = *reinterpret_cast<const uint4 *>(&sh.vw[pb][wi][4 * kap]);
-      const uint32_t y[4] = {__builtin_amdgcn_perm(wa.y, wa.x, vsel), __builtin_amdgcn_perm(wa.w, wa.z, vsel),
-                             __builtin_amdgcn_perm(wb.y, wb.x, vsel), __builtin_amdgcn_perm(wb.w, wb.z, vsel)};
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const uint4 x = make_uint4(y[0] & vmask[i], y[1] & vmask[i], y[2] & vmask[i], y[3] & vmask[i]);
-        st.o[2 * b + i] = mfma32(__builtin_bit_cast(h8, x), ps[(32 * b) / G], st.o[2 * b + i]);
+    {  // A rows g < NGD: the value minima of group g
+      h8 am = h8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (r < Tl::NGD) {
+        const h4 ma = *reinterpret_cast<const h4 *>(&sh.st.vm[r][16 * ta + 4 * kap]);
+        const h4 mb = *reinterpret_cast<const h4 *>(&sh.st.vm[r][16 * ta + 16 + 4 * kap]);
+        am = h8{ma[0], ma[1], ma[2], ma[3], mb[0], mb[1], mb[2], mb[3]};
       }
+      st.cmin = mfma32(am, p8, st.cmin);
+    }
+    const uint32_t base = lc.vaddr + 8 * ta;
+    h8 ps;  // P * value scale of the current group, formed at its first block
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      if ((16 * blk) % G == 0) {
+        const int g = (16 * blk) / G;
+        const h4 sa = *reinterpret_cast<const h4 *>(&sh.st.vs[g][16 * ta + 4 * kap]);
+        const h4 sb = *reinterpret_cast<const h4 *>(&sh.st.vs[g][16 * ta + 16 + 4 * kap]);
+        ps = p8 * h8{sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+      }
+      // 16 channels per block = 16 / TPW value words
+      const uint32_t off = base + blk * (16 / Tl::TPW) * Tl::VWS;
+      const uint2 x0 = *reinterpret_cast<const uint2 *>(&sh.st.vw[off]);
+      const uint2 x1 = *reinterpret_cast<const uint2 *>(&sh.st.vw[off + 8]);
+      st.o[blk] = mfma32(and_h8(make_uint4(x0.x, x0.y, x1.x, x1.y), lc.vmask), ps, st.o[blk]);
     }
   }
 }
@@ -486,47 +456,55 @@ template <int BITS, int G>
 __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Float16 (*sq)[kQPad],
                                              const uc_kivi_item &it, int64_t h, int64_t split,
                                              const MfmaParams &p, WaveState &st) {
-  using Gm = Geo<BITS>;
-  using Sh = DecShared<BITS, G>;
+  using Tl = Tiles<BITS, G>;
   const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t Tq = it.quantized_tokens;
-  PackedRegion<BITS, G> rg;
-  rg.nkw = static_cast<uint32_t>(Tq / Gm::TPW);
-  rg.nkg = static_cast<uint32_t>(Tq / G);
-  const int64_t kcode_bytes = int64_t(kD) * rg.nkw * 4, kstat_bytes = int64_t(kD) * rg.nkg * 2;
-  const int64_t vcode_bytes = Tq * Gm::VW * 4, vstat_bytes = Tq * Sh::NGD * 2;
-  rg.kcode = make_rsrc(static_cast<const char *>(it.key_code) + h * kcode_bytes, kcode_bytes);
-  rg.kscale = make_rsrc(static_cast<const char *>(it.key_scale) + h * kstat_bytes, kstat_bytes);
-  rg.kmin = make_rsrc(static_cast<const char *>(it.key_min) + h * kstat_bytes, kstat_bytes);
-  rg.vcode = make_rsrc(static_cast<const char *>(it.value_code) + h * vcode_bytes, vcode_bytes);
-  rg.vscale = make_rsrc(static_cast<const char *>(it.value_scale) + h * vstat_bytes, vstat_bytes);
-  rg.vmin = make_rsrc(static_cast<const char *>(it.value_min) + h * vstat_bytes, vstat_bytes);
+  const int64_t cap = it.packed_capacity > 0 ? it.packed_capacity : Tq;  // tokens between heads
+  // each resource covers the head's Tq packed tokens: rows past them read as 0
+  const int64_t kcode_row = int64_t(kD) * 4 / Tl::TPW, kstat_row = int64_t(kD) * 2 / G;  // bytes per token
+  const int64_t vcode_row = Tl::VWPT * 4, vstat_row = Tl::NGD * 2;
+  PackedRegion rg;
+  rg.kcode = make_rsrc(static_cast<const char *>(it.key_code) + h * cap * kcode_row, Tq * kcode_row);
+  rg.kscale = make_rsrc(static_cast<const char *>(it.key_scale) + h * cap * kstat_row, Tq * kstat_row);
+  rg.kmin = make_rsrc(static_cast<const char *>(it.key_min) + h * cap * kstat_row, Tq * kstat_row);
+  rg.vcode = make_rsrc(static_cast<const char *>(it.value_code) + h * cap * vcode_row, Tq * vcode_row);
+  rg.vscale = make_rsrc(static_cast<const char *>(it.value_scale) + h * cap * vstat_row, Tq * vstat_row);
+  rg.vmin = make_rsrc(static_cast<const char *>(it.value_min) + h * cap * vstat_row, Tq * vstat_row);
+  const LaneConst<BITS, G> lc = lane_const<BITS, G>(wave, lane, p.scale_log2);
   // super-tiles split, split + S, split + 2S, ... (S = packed splits): the S
   // splits of a unit run side by side on one XCD and read neighbouring parts
   // of the same 128-byte key-code and key-stat lines at about the same time
-  const int64_t n_super = (Tq + Sh::T - 1) / Sh::T;
-  const int64_t stride = p.splits_packed * Sh::T;
+  const int64_t n_super = (Tq + Tl::ST - 1) / Tl::ST;
+  const int64_t stride = p.splits_packed * Tl::ST;
   const int n_it = static_cast<int>(min<int64_t>(p.nst, (n_super - split + p.splits_packed - 1) / p.splits_packed));
   Prefetch<BITS, G> pf;
-  issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(split * Sh::T));
+  issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(split * Tl::ST));
   for (int i = 0; i < n_it; ++i) {
-    const uint32_t t0 = static_cast<uint32_t>((split + int64_t(i) * p.splits_packed) * Sh::T);
-    __syncthreads();  // every wave is done reading the previous iteration from LDS
-    stage_lds<BITS, G>(sh, pf, t0, rg.nkg);
+    const uint32_t t0 = static_cast<uint32_t>((split + int64_t(i) * p.splits_packed) * Tl::ST);
+    __syncthreads();  // every wave is done reading the previous super-tile from LDS
+    stage_lds<BITS, G>(sh, pf);
     __syncthreads();
-    if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(t0 + stride));  // lands during this iteration
-    compute_tile<BITS, G>(sh, sq, t0, rg.nkw, p.scale_log2, st);
+    if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(t0 + stride));  // lands during compute
+    const int valid = static_cast<int>(min<int64_t>(int64_t(16 * Tl::TW),
+                                                    Tq - t0 - int64_t(16 * Tl::TW) * wave));
+    if (valid > 0) compute_tile<BITS, G>(sh, sq, lc, wave, valid, p.scale_log2, st);
   }
-  // undo the denormal code scaling 2^(e - 24) of each output channel (e
-  // depends on the channel mod 4 / mod 2, i.e. on cb and v) and add the
-  // value minima
+  // undo the denormal code scaling 2^(BITS e - 24) of each output channel
+  // (channel 16 b + 4 k + v: e depends on k and v only) and add the value
+  // minima: sum_t P min of the channel's group sits in row g of cmin, held by
+  // lane (n, k = 0) as element g
+  const int n = lane & 15, kap = lane >> 4;
+  float cm[Tl::NGD];
 #pragma unroll
-  for (int cb = 0; cb < 8; ++cb)
+  for (int g = 0; g < Tl::NGD; ++g) cm[g] = __shfl(st.cmin[g], n, kWave);
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-      st.o[cb][v] = st.o[cb][v] * (16777216.0f / float(1 << value_shift<BITS>(out_channel(cb, 0, v)))) +
-                    st.cmin[(32 * (cb >> 1)) / G][v];
-  (void)lane;
+  for (int v = 0; v < 4; ++v) {
+    const int e = ((4 * kap + v) % Tl::TPW) % Tl::CPB;
+    const float undo = float(1 << (24 - BITS * e));
+#pragma unroll
+    for (int b = 0; b < 8; ++b) st.o[b][v] = st.o[b][v] * undo + cm[(16 * b) / G];
+  }
 }
 
 // --------------------------------------------------------- residual path --
@@ -546,6 +524,16 @@ __device__ __forceinline__ h8 load8_h(Rsrc r, uint32_t off) {
   return out;
 }
 
+// Selection B operand that moves channel 16 par + n of a 32-channel A
+// fragment into column n: B[k][n] = (k == 16 par + n).
+__device__ __forceinline__ h8 channel_selector(int lane, int par) {
+  const int n = lane & 15, kap = lane >> 4;
+  h8 b;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) b[j] = to_h(8 * kap + j == 16 * par + n ? 1.0f : 0.0f);
+  return b;
+}
+
 template <int RD>
 __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], const uc_kivi_item &it, int64_t h,
                                                int64_t tr0, const MfmaParams &p, WaveState &st) {
@@ -555,71 +543,50 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
   const int64_t bytes = Tr * p.Hkv * kD * 2;
   const Rsrc rk = make_rsrc(it.residual_key, bytes), rv = make_rsrc(it.residual_value, bytes);
   const int64_t tw = tr0 + wave * kResWaveTokens;
-  constexpr int kBlocks = kResWaveTokens / 16;
+  constexpr int kTiles = kResWaveTokens / 16;
   const h8 csel[2] = {channel_selector(lane, 0), channel_selector(lane, 1)};
-  f4 acc[kBlocks];
+  f4 acc[kTiles];
 #pragma unroll
-  for (int b = 0; b < kBlocks; ++b) {
+  for (int b = 0; b < kTiles; ++b) {
     acc[b] = f4{0, 0, 0, 0};
     const uint32_t base = static_cast<uint32_t>(((tw + 16 * b + r) * p.Hkv + h) * kD * 2);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
       acc[b] = mfma32(load8_h<RD>(rk, base + (32 * kb + 8 * kap) * 2), query_frag(sq, kb, lane), acc[b]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[b][v] *= p.scale_log2;
   }
-  float mx = kNegInf;
+  const int valid = static_cast<int>(min<int64_t>(int64_t(kResWaveTokens), Tr - tw));
+  softmax_tiles<kTiles>(acc, valid, st, kap);
+  // O^T += V^T P^T: a lane loads 8 channels of one token per 32-channel
+  // block; a selection MFMA turns a tile of them into the A layout of
+  // accumulator b (row = channel 16 b + n, 4 tokens per lane)
 #pragma unroll
-  for (int b = 0; b < kBlocks; ++b)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const bool ok = tw + 16 * b + 4 * kap + v < Tr;
-      const float x = ok ? acc[b][v] : kNegInf;
-      acc[b][v] = x;
-      mx = fmaxf(mx, x);
-    }
-  const float m = max_over_slices(mx) * p.scale_log2;
-  const float m_ref = m == kNegInf ? 0.0f : m;
-  float sum = 0.0f;
-#pragma unroll
-  for (int b = 0; b < kBlocks; ++b)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float e = fast_exp2(__builtin_fmaf(acc[b][v], p.scale_log2, -m_ref));
-      acc[b][v] = e;
-      sum += e;
-    }
-  st.m = m;
-  st.l = sum;
-  // O^T += V^T P^T: the 8 channels x 16 tokens a lane loads from a residual
-  // row block come out of a selection MFMA as 4 tokens of channel 32b + 2n + i
-  // (the A layout of accumulator 2b + i, as in the packed path)
-#pragma unroll
-  for (int j = 0; j < kBlocks / 2; ++j) {
+  for (int j = 0; j < kTiles / 2; ++j) {
     const h4 pa4 = cvt4(acc[2 * j]), pb4 = cvt4(acc[2 * j + 1]);
     const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
     const uint32_t base0 = static_cast<uint32_t>(((tw + 32 * j + r) * p.Hkv + h) * kD * 2);
     const uint32_t base1 = static_cast<uint32_t>(((tw + 32 * j + 16 + r) * p.Hkv + h) * kD * 2);
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const h8 v0 = load8_h<RD>(rv, base0 + (32 * b + 8 * kap) * 2);
-      const h8 v1 = load8_h<RD>(rv, base1 + (32 * b + 8 * kap) * 2);
+    for (int b2 = 0; b2 < 4; ++b2) {
+      const h8 v0 = load8_h<RD>(rv, base0 + (32 * b2 + 8 * kap) * 2);
+      const h8 v1 = load8_h<RD>(rv, base1 + (32 * b2 + 8 * kap) * 2);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const h4 a0 = cvt4(mfma32(v0, csel[i], f4{0, 0, 0, 0})), a1 = cvt4(mfma32(v1, csel[i], f4{0, 0, 0, 0}));
-        st.o[2 * b + i] = mfma32(h8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, p8, st.o[2 * b + i]);
+      for (int par = 0; par < 2; ++par) {
+        const h4 a0 = cvt4(mfma32(v0, csel[par], f4{0, 0, 0, 0})), a1 = cvt4(mfma32(v1, csel[par], f4{0, 0, 0, 0}));
+        st.o[2 * b2 + par] = mfma32(h8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, p8, st.o[2 * b2 + par]);
       }
     }
   }
 }
 
 // ------------------------------------------------------------------ kernel --
-static_assert(kThreads == kD, "key-stat staging maps one thread per channel");
-
 template <int BITS, int G, int RD, bool TABLE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma_kernel(
-    const uc_kivi_item *items, uc_kivi_item single, MfmaParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void decode_mfma_kernel(
+    const uc_kivi_item *items, uc_kivi_item single,
+                                                               MfmaParams p) {
   __shared__ __align__(16) DecShared<BITS, G> sh;
-  __shared__ _Float16 sq[16][kQPad];
-  __shared__ float mrg_ml[kWaves][16][2];
+  __shared__ __align__(16) _Float16 sq[16][kQPad];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Workgroup i runs on XCD i % 8; with enough units its k = i / 8-th
   // workgroup there is split k % S of unit (item, KV head) u = 8 (k / S) + i % 8,
@@ -652,8 +619,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   WaveState st;
 #pragma unroll
   for (int b = 0; b < 8; ++b) st.o[b] = f4{0, 0, 0, 0};
-#pragma unroll
-  for (int g = 0; g < 4; ++g) st.cmin[g] = f4{0, 0, 0, 0};
+  st.cmin = f4{0, 0, 0, 0};
   st.m = kNegInf;
   st.l = 0.0f;
   __syncthreads();
@@ -662,52 +628,45 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // instead of forming its tail
   const int64_t splits_res = p.splits_total - p.splits_packed;
   if (split >= splits_res) {
-    const int64_t sp = split - splits_res;
-    if (sp * DecShared<BITS, G>::T < it.quantized_tokens) packed_split<BITS, G>(sh, sq, it, h, sp, p, st);
+    packed_split<BITS, G>(sh, sq, it, h, split - splits_res, p, st);
   } else {
     const int64_t tr0 = split * kWaves * kResWaveTokens;
-    if (tr0 < it.residual_tokens) residual_split<RD>(sq, it, h, tr0, p, st);
+    if (tr0 + wave * kResWaveTokens < it.residual_tokens) residual_split<RD>(sq, it, h, tr0, p, st);
   }
 
-  // ---- merge the two waves; lane (n, k) holds query n, channels out_channel(cb, k, v)
+  // ---- merge the waves; lane (n, k) holds query n, channels 16 b + 4 k + v
   const int kap = lane >> 4, n = lane & 15;
   const float l_all = sum_over_slices(st.l);
-  __syncthreads();
+  __syncthreads();  // the staging area becomes the merge area
   if (kap == 0) {
-    mrg_ml[wave][n][0] = st.m;
-    mrg_ml[wave][n][1] = l_all;
+    sh.mrg.ml[wave][n][0] = st.m;
+    sh.mrg.ml[wave][n][1] = l_all;
   }
   __syncthreads();
   float M = kNegInf;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mrg_ml[w][n][0]);
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sh.mrg.ml[w][n][0]);
   const float M_ref = M == kNegInf ? 0.0f : M;
   float L = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) L += mrg_ml[w][n][1] * fast_exp2(mrg_ml[w][n][0] - M_ref);
+  for (int w = 0; w < kWaves; ++w) L += sh.mrg.ml[w][n][1] * fast_exp2(sh.mrg.ml[w][n][0] - M_ref);
   const float mine = fast_exp2(st.m - M_ref);
-  float *fin = reinterpret_cast<float *>(sh.vw);  // [16][128] partial of wave 1
-  static_assert(sizeof(sh.vw) >= 16 * kD * sizeof(float), "wave merge fits the value-word staging");
-  if (wave == 1) {
+  if (wave > 0) {
 #pragma unroll
-    for (int cb = 0; cb < 8; ++cb)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) fin[n * kD + out_channel(cb, kap, v)] = st.o[cb][v] * mine;
+    for (int b = 0; b < 8; ++b)
+      *reinterpret_cast<f4 *>(&sh.mrg.o[wave - 1][n][16 * b + 4 * kap]) = st.o[b] * mine;
   }
   __syncthreads();
-  const int64_t slot = (item * p.Hkv + h) * p.splits_total + split;
   if (wave == 0) {
+    const int64_t slot = (item * p.Hkv + h) * p.splits_total + split;
     _Float16 *po = p.ws_o + slot * 16 * kD;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {  // channels 32b + 8kap + [0, 8): accumulators 2b (even), 2b + 1 (odd)
-      h8 o8;
+    for (int b = 0; b < 8; ++b) {
+      f4 s = st.o[b] * mine;
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          o8[2 * v + i] = to_h((st.o[2 * b + i][v] * mine + fin[n * kD + out_channel(2 * b + i, kap, v)]) * inv);
-      *reinterpret_cast<h8 *>(&po[n * kD + 32 * b + 8 * kap]) = o8;
+      for (int w = 0; w < kWaves - 1; ++w) s += *reinterpret_cast<const f4 *>(&sh.mrg.o[w][n][16 * b + 4 * kap]);
+      *reinterpret_cast<h4 *>(&po[n * kD + 16 * b + 4 * kap]) = cvt4(s * inv);
     }
     if (kap == 0) {
       p.ws_ml[(slot * 16 + n) * 2 + 0] = M;
@@ -848,14 +807,14 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
                        int out_dtype, float sm_scale, int64_t max_tq, int64_t max_tr, int64_t nst, int64_t segs,
                        void *workspace, int64_t workspace_bytes, hipStream_t stream) {
   // Twice the super-tiles per split when that fits the launch into one round of
-  // workgroup slots (4 per CU) and `nst` does not: a batch-1 32k context then
+  // workgroup slots (kWgPerCu per CU) and `nst` does not: a batch-1 32k context then
   // runs as one full round instead of ~1.9 (+3 % measured).  Fewer splits, so
   // the workspace sized for `nst` still fits.
   {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) == hipSuccess &&
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) {
-      const int64_t units = n_items * Hkv, round = 4 * int64_t(cus);
+      const int64_t units = n_items * Hkv, round = kWgPerCu * int64_t(cus);
       if (units * decode_mfma_num_splits(bits, nst, max_tq, max_tr) > round &&
           units * decode_mfma_num_splits(bits, 2 * nst, max_tq, max_tr) <= round)
         nst *= 2;

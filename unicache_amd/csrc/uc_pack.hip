@@ -365,8 +365,8 @@ __global__ __launch_bounds__(256) void dequant_key_native_kernel(DequantArgs a, 
 #pragma unroll
   for (int j = 0; j < kDqRunWords; ++j) {
     const bool ok = w0 + j < w_end;
-    wa[j] = ok ? kc[w0 + j] : 0u;
-    wb[j] = ok ? kc[a.kc_sd + w0 + j] : 0u;
+    wa[j] = ok ? kc[(w0 + j) * a.kc_sw] : 0u;
+    wb[j] = ok ? kc[a.kc_sd + (w0 + j) * a.kc_sw] : 0u;
     const int64_t so = h * a.ks_sh + c * a.ks_sd + (((ok ? w0 + j : w0) * TPW) >> a.lg) * a.ks_sg;
     s0[j] = load_dyn(a.key_scale, so, a.sd);
     m0[j] = load_dyn(a.key_min, so, a.sd);
@@ -664,7 +664,9 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
   const bool out_ok = o_sd == 1 && o_st % 2 == 0 && o_sh % 2 == 0 && head_dim % 32 == 0 &&
                       (out_key == nullptr || aligned(out_key, 2 * out_bytes)) &&
                       (out_value == nullptr || aligned(out_value, 2 * out_bytes));
-  const bool key_native = key_code != nullptr && (k_bits == 2 || k_bits == 4) && kc_sw == 1;
+  // word-major (UniCache's kernel-native tensors) or token-major (this
+  // library's native storage) key codes
+  const bool key_native = key_code != nullptr && (k_bits == 2 || k_bits == 4) && (kc_sw == 1 || kc_sd == 1);
   const bool value_native = value_code != nullptr && (v_bits == 2 || v_bits == 4) && vc_sw == 1;
   if (out_ok && (key_code == nullptr || key_native) && (value_code == nullptr || value_native)) {
     UC_DISPATCH_DTYPE(out_dtype, OD, [&] {

@@ -8,8 +8,9 @@ so it can sit in a tight decode loop or a captured HIP graph.  Callers update
 the query tensors in place between steps.
 
 The device tables hold raw pointers, so both classes check every pointer on
-the host when they build a table (device, contiguity, 16-byte alignment of
-the vector-loaded rows), keep the tensors behind the table alive, and refuse
+the host when they build a table (device, the token-major packed layout,
+contiguity and 16-byte alignment of the vector-loaded rows), keep the tensors
+behind the table alive, and refuse
 to run once a packed cache has replaced its tensors (append, flush, repack)
 until refresh() rebuilds the table.
 """
@@ -39,17 +40,15 @@ def _check_rows(t: torch.Tensor, device: torch.device, what: str) -> None:
 
 
 def _check_cache(c, device: torch.device, what: str) -> list[torch.Tensor]:
-    """Validate a packed cache's tensors for a device item table; returns
-    the tensors the table will point into."""
+    """Validate a packed cache's tensors for a device item table (the
+    token-major native layout, on `device`); returns the tensors the table
+    will point into."""
 
-    tensors = []
-    for name in _PACKED:
-        t = getattr(c, name)
-        if t.device != device:
-            raise RuntimeError(f"{what}: {name} must be on {device} (got {t.device})")
-        if not t.is_contiguous():
-            raise ValueError(f"{what}: {name} must be contiguous")
-        tensors.append(t)
+    try:
+        c.native_packed_pointers(device)
+    except (ValueError, RuntimeError) as exc:
+        raise type(exc)(f"{what}: {exc}") from None
+    tensors = [getattr(c, name) for name in _PACKED]
     if c.residual_tokens:
         _check_rows(c.residual_key, device, f"{what}: residual_key")
         _check_rows(c.residual_value, device, f"{what}: residual_value")
@@ -119,12 +118,10 @@ class KiviDecodeBatch:
         items = (nat.KiviItem * len(caches))()
         for i, (c, q) in enumerate(zip(caches, queries)):
             tr = c.residual_tokens
-            items[i] = nat.KiviItem(
-                c.key_code.data_ptr(), c.key_scale.data_ptr(), c.key_minimum.data_ptr(),
-                c.value_code.data_ptr(), c.value_scale.data_ptr(), c.value_minimum.data_ptr(),
-                c.residual_key.data_ptr() if tr else None, c.residual_value.data_ptr() if tr else None,
-                q.data_ptr(), self.outputs[i].data_ptr(), self.lses[i].data_ptr(), c.quantized_tokens, tr,
-            )
+            items[i] = c.native_item(q.data_ptr(), self.outputs[i].data_ptr(), self.lses[i].data_ptr(),
+                                     residual_key_ptr=c.residual_key.data_ptr() if tr else None,
+                                     residual_value_ptr=c.residual_value.data_ptr() if tr else None,
+                                     residual_tokens=tr)
         raw = bytes(ctypes.string_at(ctypes.addressof(items), ctypes.sizeof(items)))
         self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
         self.max_tq = max(c.quantized_tokens for c in caches)
@@ -245,21 +242,20 @@ class MixedDecodeBatch:
                 s = g[j] if j < len(g) else None
                 if s is None:  # padding: an empty segment
                     items[idx] = nat.KiviItem(None, None, None, None, None, None, None, None, q.data_ptr(),
-                                              out.data_ptr(), lse.data_ptr(), 0, 0)
+                                              out.data_ptr(), lse.data_ptr(), 0, 0, 0)
                 elif isinstance(s, tuple):
                     k, v = s
                     tr = int(k.shape[0])
                     items[idx] = nat.KiviItem(None, None, None, None, None, None, k.data_ptr() if tr else None,
                                               v.data_ptr() if tr else None, q.data_ptr(), out.data_ptr(),
-                                              lse.data_ptr(), 0, tr)
+                                              lse.data_ptr(), 0, tr, 0)
                     max_tr = max(max_tr, tr)
                 else:
                     tr = s.residual_tokens
-                    items[idx] = nat.KiviItem(
-                        s.key_code.data_ptr(), s.key_scale.data_ptr(), s.key_minimum.data_ptr(),
-                        s.value_code.data_ptr(), s.value_scale.data_ptr(), s.value_minimum.data_ptr(),
-                        s.residual_key.data_ptr() if tr else None, s.residual_value.data_ptr() if tr else None,
-                        q.data_ptr(), out.data_ptr(), lse.data_ptr(), s.quantized_tokens, tr)
+                    items[idx] = s.native_item(q.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                               residual_key_ptr=s.residual_key.data_ptr() if tr else None,
+                                               residual_value_ptr=s.residual_value.data_ptr() if tr else None,
+                                               residual_tokens=tr)
                     max_tq, max_tr = max(max_tq, s.quantized_tokens), max(max_tr, tr)
         raw = bytes(ctypes.string_at(ctypes.addressof(items), ctypes.sizeof(items)))
         self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)

@@ -99,12 +99,9 @@ def _decode_summary(cache: "PackedKIVICache", query: torch.Tensor, *, include_re
     tr = cache.residual_tokens if include_residual else 0
     out = torch.empty((lq, hq, d), dtype=out_dtype, device=device)
     lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
-    item = nat.KiviItem(
-        cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
-        cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
-        nat.ptr(cache.residual_key) if tr else None, nat.ptr(cache.residual_value) if tr else None,
-        q.data_ptr(), out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr,
-    )
+    item = cache.native_item(q.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                             residual_key_ptr=nat.ptr(cache.residual_key) if tr else None,
+                             residual_value_ptr=nat.ptr(cache.residual_value) if tr else None, residual_tokens=tr)
     ws_bytes = nat.decode_workspace_bytes(1, cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq,
                                           cache.quantized_tokens, tr)
     ws = nat.workspace(device, ws_bytes)
@@ -128,12 +125,9 @@ def _mq_summary(cache: "PackedKIVICache", query: torch.Tensor, *, include_residu
     tr = cache.residual_tokens if include_residual else 0
     out = torch.empty((lq, hq, d), dtype=out_dtype, device=device)
     lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
-    item = nat.KiviItem(
-        cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
-        cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
-        nat.ptr(cache.residual_key) if tr else None, nat.ptr(cache.residual_value) if tr else None,
-        q.data_ptr(), out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr,
-    )
+    item = cache.native_item(q.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                             residual_key_ptr=nat.ptr(cache.residual_key) if tr else None,
+                             residual_value_ptr=nat.ptr(cache.residual_value) if tr else None, residual_tokens=tr)
     res_dtype = cache.residual_key.dtype if tr else q.dtype
     ws_bytes = nat.mq_workspace_bytes(cache.num_kv_heads, d, cache.quantized_tokens, tr)
     ws = nat.workspace(device, ws_bytes)
@@ -208,12 +202,9 @@ def packed_summary_with_dense(
     tr = int(dk.shape[0])
     out = torch.empty((lq, hq, d), dtype=q.dtype, device=device)
     lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
-    item = nat.KiviItem(
-        cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
-        cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
-        dk.data_ptr() if tr else None, dv.data_ptr() if tr else None,
-        q.data_ptr(), out.data_ptr(), lse.data_ptr(), cache.quantized_tokens, tr,
-    )
+    item = cache.native_item(q.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                             residual_key_ptr=dk.data_ptr() if tr else None,
+                             residual_value_ptr=dv.data_ptr() if tr else None, residual_tokens=tr)
     res_code = nat.dtype_code(dk.dtype if tr else q.dtype)
     if lq <= _max_decode_query_len(cache, hq):
         ws_bytes = nat.decode_workspace_bytes(1, cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq,
@@ -281,6 +272,7 @@ def packed_batch_with_dense(items: list) -> None:
             raise ValueError("Batched packed attention needs contiguous queries and outputs")
         if int(query.shape[0]) <= _max_decode_query_len(cache, hq):
             raise ValueError("Batched packed attention covers multi-query segments only")
+        cache.native_packed_pointers(query.device)
     # every pointer that goes into the launch table, on one GPU, checked before any launch
     device = nat.require_device(
         *(t for cache, query, kparts, vparts, out, *rest in items
@@ -301,13 +293,10 @@ def packed_batch_with_dense(items: list) -> None:
         for j, (cache, query, kparts, _, out, *rest) in enumerate(chunk):
             lse = rest[0] if rest else None
             tr = sum(int(x.shape[0]) for x in kparts)
-            table[j] = nat.KiviItem(
-                cache.key_code.data_ptr(), cache.key_scale.data_ptr(), cache.key_minimum.data_ptr(),
-                cache.value_code.data_ptr(), cache.value_scale.data_ptr(), cache.value_minimum.data_ptr(),
-                dk.data_ptr() + row * row_bytes if tr else None, dv.data_ptr() + row * row_bytes if tr else None,
+            table[j] = cache.native_item(
                 query.data_ptr(), out.data_ptr(), lse.data_ptr() if lse is not None else None,
-                cache.quantized_tokens, tr,
-            )
+                residual_key_ptr=dk.data_ptr() + row * row_bytes if tr else None,
+                residual_value_ptr=dv.data_ptr() + row * row_bytes if tr else None, residual_tokens=tr)
             row += tr
             lens[j] = int(query.shape[0])
             ws_bytes += nat.mq_workspace_bytes(cache.num_kv_heads, d, cache.quantized_tokens, tr)
@@ -344,7 +333,7 @@ def dense_attention_summary(
     out = torch.empty((lq, hq, d), dtype=q.dtype, device=device)
     lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
     item = nat.KiviItem(None, None, None, None, None, None, dk.data_ptr(), dv.data_ptr(), q.data_ptr(),
-                        out.data_ptr(), lse.data_ptr(), 0, tokens)
+                        out.data_ptr(), lse.data_ptr(), 0, tokens, 0)
     bits, group = 2, 32  # no packed tokens: only the dense (residual) part is read
     if lq <= max(1, 16 // (hq // hkv)):
         ws_bytes = nat.decode_workspace_bytes(1, bits, group, hq, hkv, d, lq, 0, tokens)
@@ -379,7 +368,9 @@ def quantize_kivi_native(
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """KIVI's kernel-native packed layout in one HIP pass (kivi_cuda.py:157-190):
     keys grouped along tokens -> [Hkv, D, T*b/32] words, values grouped along
-    channels -> [Hkv, T, D*b/32] words, fp16 scale/minimum."""
+    channels -> [Hkv, T, D*b/32] words, fp16 scale/minimum.  The tensors have
+    these shapes but token-major strides (views of [Hkv, T*b/32, D] and
+    [Hkv, T/G, D] key storage), the layout the attention kernels read."""
 
     if key.shape != value.shape or key.dim() != 3:
         raise ValueError("KIVI native packing expects matching [tokens, heads, dim] KV")
@@ -412,11 +403,12 @@ def packed_kivi_attention_parts(
     tq, tr = cache.quantized_tokens, cache.residual_tokens
     res = cache.residual_key
     stats_dtype = cache.key_scale.dtype if tq else torch.float16
+    cap = cache.native_packed_pointers(device)[-1] if tq and cache.k_bits in (2, 4) else 0
     logits = torch.empty((hq, lq, tq + tr), dtype=torch.float32, device=device)
     nat.call(
         "uc_kivi_qk", q.data_ptr(), nat.dtype_code(q.dtype), lq, hq,
         nat.ptr(cache.key_code), nat.ptr(cache.key_scale), nat.ptr(cache.key_minimum),
-        nat.dtype_code(stats_dtype), tq, cache.k_bits, cache.group_size,
+        nat.dtype_code(stats_dtype), tq, cap, cache.k_bits, cache.group_size,
         res.data_ptr(), nat.dtype_code(res.dtype), tr, int(res.stride(0)), int(res.stride(1)),
         cache.num_kv_heads, d, 1.0 / math.sqrt(d), logits.data_ptr(), nat.stream(device),
     )
@@ -432,7 +424,7 @@ def packed_kivi_attention_parts(
             "uc_kivi_av", probabilities.data_ptr(), nat.dtype_code(probabilities.dtype),
             *map(int, probabilities.stride()), lq, hq,
             nat.ptr(cache.value_code), nat.ptr(cache.value_scale), nat.ptr(cache.value_minimum),
-            nat.dtype_code(stats_dtype), tq, cache.v_bits, cache.group_size,
+            nat.dtype_code(stats_dtype), tq, cap, cache.v_bits, cache.group_size,
             val.data_ptr(), nat.dtype_code(val.dtype), tr, int(val.stride(0)), int(val.stride(1)),
             cache.num_kv_heads, d, out.data_ptr(), nat.dtype_code(val.dtype), ws.data_ptr(),
             nat.stream(device),

@@ -84,7 +84,7 @@ def _dense_qk(query: torch.Tensor, key: torch.Tensor, *, scale: float) -> torch.
     logits = torch.empty((hq, lq, tokens), dtype=torch.float32, device=device)
     nat.call(
         "uc_kivi_qk", q.data_ptr(), nat.dtype_code(q.dtype), lq, hq,
-        None, None, None, nat.UC_FP16, 0, 2, 32,
+        None, None, None, nat.UC_FP16, 0, 0, 2, 32,
         key.data_ptr(), nat.dtype_code(key.dtype), tokens, int(key.stride(0)), int(key.stride(1)),
         hkv, d, float(scale), logits.data_ptr(), nat.stream(device),
     )
@@ -105,7 +105,7 @@ def _dense_av(probabilities: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
     nat.call(
         "uc_kivi_av", probabilities.data_ptr(), nat.dtype_code(probabilities.dtype),
         *map(int, probabilities.stride()), lq, hq,
-        None, None, None, nat.UC_FP16, 0, 2, 32,
+        None, None, None, nat.UC_FP16, 0, 0, 2, 32,
         value.data_ptr(), nat.dtype_code(value.dtype), tokens, int(value.stride(0)), int(value.stride(1)),
         hkv, d, out.data_ptr(), nat.dtype_code(value.dtype), ws.data_ptr(), nat.stream(device),
     )
@@ -124,29 +124,88 @@ def native_pack_layout(tokens: int, heads: int, head_dim: int, k_bits: int, v_bi
     }
 
 
-def _pack_native(key: torch.Tensor, value: torch.Tensor, *, k_bits: int, v_bits: int, group_size: int):
-    """HIP quantize+pack into the kernel-native layout (fp16 stats)."""
+# The kernel-native tensors keep the shapes above but live in token-major
+# storage with room for `capacity` tokens per head:
+#     key code   int32 [Hkv, C*kb/32, D]   key scale / minimum fp16 [Hkv, C/G, D]
+#     value code int32 [Hkv, C, D*vb/32]   value scale / minimum fp16 [Hkv, C, D/G]
+# The cache exposes views of the first T tokens, permuted back to the shapes
+# of native_pack_layout, so one head's token range is one contiguous run of
+# every tensor (the decode kernels stream it with 16-byte loads) and a flush
+# appends rows in place.  The attention entry points of the library take this
+# layout and the capacity C (uc_kivi_item.packed_capacity).
+def _native_storage(capacity: int, heads: int, head_dim: int, k_bits: int, v_bits: int, group_size: int,
+                    device) -> tuple[torch.Tensor, ...]:
+    kc = torch.empty((heads, capacity * k_bits // 32, head_dim), dtype=torch.int32, device=device)
+    ks = torch.empty((heads, capacity // group_size, head_dim), dtype=torch.float16, device=device)
+    vc = torch.empty((heads, capacity, head_dim * v_bits // 32), dtype=torch.int32, device=device)
+    vs = torch.empty((heads, capacity, head_dim // group_size), dtype=torch.float16, device=device)
+    return kc, ks, torch.empty_like(ks), vc, vs, torch.empty_like(vs)
 
-    device = nat.require_device(key, value, what="KIVI native packing")
-    tokens, heads, head_dim = map(int, key.shape)
-    lay = native_pack_layout(tokens, heads, head_dim, k_bits, v_bits, group_size)
-    kc = torch.empty(lay["key_code"][0], dtype=torch.int32, device=device)
-    ks = torch.empty(lay["key_stats"][0], dtype=torch.float16, device=device)
-    km = torch.empty_like(ks)
-    vc = torch.empty(lay["value_code"][0], dtype=torch.int32, device=device)
-    vs = torch.empty(lay["value_stats"][0], dtype=torch.float16, device=device)
-    vm = torch.empty_like(vs)
+
+def _native_views(storage, tokens: int, k_bits: int, group_size: int) -> tuple[torch.Tensor, ...]:
+    """The first `tokens` tokens of token-major storage in the native shapes."""
+
+    kc, ks, km, vc, vs, vm = storage
+    nw, ng = tokens * k_bits // 32, tokens // group_size
+    return (kc[:, :nw].transpose(1, 2), ks[:, :ng].transpose(1, 2), km[:, :ng].transpose(1, 2),
+            vc[:, :tokens], vs[:, :tokens], vm[:, :tokens])
+
+
+def _native_storage_of(views, capacity: int, k_bits: int, group_size: int) -> tuple[torch.Tensor, ...]:
+    """Token-major storage tensors behind native views of capacity C."""
+
+    kc, ks, km, vc, vs, vm = views
+    heads, head_dim = int(kc.shape[0]), int(kc.shape[1])
+    cw, cg = capacity * k_bits // 32, capacity // group_size
+    vw, vg = int(vc.shape[2]), int(vs.shape[2])
+    return (kc.as_strided((heads, cw, head_dim), (cw * head_dim, head_dim, 1)),
+            ks.as_strided((heads, cg, head_dim), (cg * head_dim, head_dim, 1)),
+            km.as_strided((heads, cg, head_dim), (cg * head_dim, head_dim, 1)),
+            vc.as_strided((heads, capacity, vw), (capacity * vw, vw, 1)),
+            vs.as_strided((heads, capacity, vg), (capacity * vg, vg, 1)),
+            vm.as_strided((heads, capacity, vg), (capacity * vg, vg, 1)))
+
+
+def _pack_native_into(storage, offset: int, key: torch.Tensor, value: torch.Tensor, *, k_bits: int, v_bits: int,
+                      group_size: int) -> None:
+    """HIP quantize+pack of [n, Hkv, D] K/V into tokens offset..offset+n of
+    token-major storage (offset a multiple of group_size)."""
+
+    device = nat.require_device(key, value, storage[0], what="KIVI native packing")
     if key.dtype != value.dtype:
         raise ValueError("KIVI packing expects key and value of one dtype")
+    kc, ks, km, vc, vs, vm = storage
+    tokens, heads, head_dim = map(int, key.shape)
+    kd = int(kc.shape[2])
+    kw0, g0 = offset * k_bits // 32, offset // group_size
+    vw, vg = int(vc.shape[2]), int(vs.shape[2])
     nat.call(
         "uc_kivi_pack",
         key.data_ptr(), *_dense_strides(key), value.data_ptr(), *_dense_strides(value),
         nat.dtype_code(key.dtype), tokens, heads, head_dim, k_bits, v_bits, group_size, nat.UC_FP16,
-        kc.data_ptr(), *map(int, kc.stride()), ks.data_ptr(), km.data_ptr(), *map(int, ks.stride()),
-        vc.data_ptr(), *map(int, vc.stride()), vs.data_ptr(), vm.data_ptr(), *map(int, vs.stride()),
+        # key code (h, d, w), key stats (h, d, g): token-major rows of D channels
+        kc.data_ptr() + 4 * kw0 * kd, int(kc.stride(0)), 1, kd,
+        ks.data_ptr() + 2 * g0 * kd, km.data_ptr() + 2 * g0 * kd, int(ks.stride(0)), 1, kd,
+        vc.data_ptr() + 4 * offset * vw, int(vc.stride(0)), vw, 1,
+        vs.data_ptr() + 2 * offset * vg, vm.data_ptr() + 2 * offset * vg, int(vs.stride(0)), vg, 1,
         nat.stream(device),
     )
-    return kc, ks, km, vc, vs, vm
+
+
+def _pack_native(key: torch.Tensor, value: torch.Tensor, *, k_bits: int, v_bits: int, group_size: int,
+                 capacity: int | None = None):
+    """HIP quantize+pack into the kernel-native layout (fp16 stats), in
+    token-major storage with room for `capacity` tokens (default: exactly the
+    input's)."""
+
+    device = nat.require_device(key, value, what="KIVI native packing")
+    tokens, heads, head_dim = map(int, key.shape)
+    capacity = tokens if capacity is None else int(capacity)
+    if capacity < tokens or capacity % group_size:
+        raise ValueError("KIVI packed capacity must be a multiple of group_size covering the tokens")
+    storage = _native_storage(capacity, heads, head_dim, k_bits, v_bits, group_size, device)
+    _pack_native_into(storage, 0, key, value, k_bits=k_bits, v_bits=v_bits, group_size=group_size)
+    return _native_views(storage, tokens, k_bits, group_size)
 
 
 def _reference_layout_shapes(tokens, heads, head_dim, bits, group_size, *, is_key):
@@ -311,6 +370,63 @@ class PackedKIVICache:
         return int(self.residual_key.shape[0])
 
     @property
+    def packed_capacity(self) -> int:
+        """Tokens per head that the native packed storage holds (>=
+        quantized_tokens; flushes append in place up to it); 0 without a
+        native packed prefix."""
+
+        if not self.kernel_native_layout or self.key_code is None:
+            return 0
+        return int(self.key_code.stride(0)) // self.head_dim * 32 // self.k_bits
+
+    def native_packed_pointers(self, device: torch.device | None = None) -> tuple[int, ...]:
+        """(key code, key scale, key minimum, value code, value scale, value
+        minimum) device addresses and the packed capacity, after checking that
+        the six tensors are the token-major native layout the attention
+        kernels read by address (dtypes, shapes, strides, device, 16-byte
+        alignment).  Raises ValueError / RuntimeError otherwise."""
+
+        if not self.kernel_native_layout or self.key_code is None:
+            raise RuntimeError("Packed KIVI attention requires kernel-native layout")
+        h, d, g, tq = self.num_kv_heads, self.head_dim, self.group_size, self.quantized_tokens
+        cap = self.packed_capacity
+        vw, vg = d * self.v_bits // 32, d // g
+        cw, cg = cap * self.k_bits // 32, cap // g
+        expected = (
+            ("key_code", torch.int32, (h, d, tq * self.k_bits // 32), (cw * d, 1, d)),
+            ("key_scale", torch.float16, (h, d, tq // g), (cg * d, 1, d)),
+            ("key_minimum", torch.float16, (h, d, tq // g), (cg * d, 1, d)),
+            ("value_code", torch.int32, (h, tq, vw), (cap * vw, vw, 1)),
+            ("value_scale", torch.float16, (h, tq, vg), (cap * vg, vg, 1)),
+            ("value_minimum", torch.float16, (h, tq, vg), (cap * vg, vg, 1)),
+        )
+        device = device or self.key_code.device
+        ptrs = []
+        for name, dtype, shape, stride in expected:
+            t = getattr(self, name)
+            if t.device != device:
+                raise RuntimeError(f"Packed KIVI {name} must be on {device} (got {t.device})")
+            if t.dtype != dtype or tuple(t.shape) != shape or tuple(t.stride()) != stride:
+                raise ValueError(
+                    f"Packed KIVI {name} is not in the token-major native layout: expected {dtype} {shape} "
+                    f"strides {stride}, got {t.dtype} {tuple(t.shape)} strides {tuple(t.stride())}")
+            if t.data_ptr() % 16:
+                raise ValueError(f"Packed KIVI {name} must be 16-byte aligned")
+            ptrs.append(t.data_ptr())
+        if cap < tq or cap % g:
+            raise ValueError("Packed KIVI capacity must be a multiple of group_size covering the packed tokens")
+        return (*ptrs, cap)
+
+    def native_item(self, query_ptr: int, out_ptr: int, lse_ptr: int | None, *, residual_key_ptr: int | None = None,
+                    residual_value_ptr: int | None = None, residual_tokens: int = 0) -> "nat.KiviItem":
+        """Launch-table entry (uc_kivi_item) for the packed prefix plus the
+        given residual rows."""
+
+        kc, ks, km, vc, vs, vm, cap = self.native_packed_pointers()
+        return nat.KiviItem(kc, ks, km, vc, vs, vm, residual_key_ptr, residual_value_ptr, query_ptr, out_ptr,
+                            lse_ptr, self.quantized_tokens, int(residual_tokens), cap)
+
+    @property
     def resident_bytes(self) -> int:
         tensors = (
             self.key_code, self.key_scale, self.key_minimum,
@@ -461,7 +577,9 @@ class PackedKIVICache:
     def flush_residual(self, keep: int = 0) -> int:
         """Quantize the residual except its last `keep` tokens (rounded so the
         packed length stays a multiple of group_size) and append it to the
-        packed prefix.  Returns the number of tokens packed."""
+        packed prefix: in place while the token-major storage has room
+        (packed_capacity), else into storage 1.5x larger.  Returns the number
+        of tokens packed."""
 
         tr = self.residual_tokens
         count = ((tr - max(0, int(keep))) // self.group_size) * self.group_size
@@ -471,18 +589,27 @@ class PackedKIVICache:
             raise ValueError("Streaming KIVI flush supports equal 2-bit or 4-bit K/V")
         if self.backend != "cuda" or (self.quantized_tokens and not self.kernel_native_layout):
             raise RuntimeError("Streaming KIVI flush requires the kernel-native layout (backend='cuda')")
-        from .kivi_cuda import quantize_kivi_native
-
-        new = quantize_kivi_native(self.residual_key[:count], self.residual_value[:count],
-                                   k_bits=self.k_bits, v_bits=self.v_bits, group_size=self.group_size)
-        if self.quantized_tokens:
-            old = (self.key_code, self.key_scale, self.key_minimum, self.value_code, self.value_scale,
-                   self.value_minimum)
-            dims = (2, 2, 2, 1, 1, 1)  # keys grow along token words / groups, values along rows
-            new = tuple(torch.cat([a, b], dim=d) for a, b, d in zip(old, new, dims))
+        device = nat.require_device(self.residual_key, self.residual_value, what="KIVI flush")
+        tq, bits, g = self.quantized_tokens, self.k_bits, self.group_size
+        cap = self.packed_capacity
+        old = (self.key_code, self.key_scale, self.key_minimum, self.value_code, self.value_scale,
+               self.value_minimum)
+        if tq:
+            self.native_packed_pointers(device)  # the storage below is only valid for this layout
+        if tq + count <= cap:
+            storage = _native_storage_of(old, cap, bits, g)
+        else:
+            # grow geometrically so a run of flushes copies the prefix O(log n) times
+            cap = -(-max(tq + count, cap + cap // 2) // g) * g
+            storage = _native_storage(cap, self.num_kv_heads, self.head_dim, bits, bits, g, device)
+            if tq:
+                for dst, src in zip(_native_views(storage, tq, bits, g), old):
+                    dst.copy_(src)
+        _pack_native_into(storage, tq, self.residual_key[:count], self.residual_value[:count], k_bits=bits,
+                          v_bits=bits, group_size=g)
         (self.key_code, self.key_scale, self.key_minimum,
-         self.value_code, self.value_scale, self.value_minimum) = new
-        self.quantized_tokens += count
+         self.value_code, self.value_scale, self.value_minimum) = _native_views(storage, tq + count, bits, g)
+        self.quantized_tokens = tq + count
         self.kernel_native_layout = True
         rest_k = self.residual_key[count:].clone()
         rest_v = self.residual_value[count:].clone()
