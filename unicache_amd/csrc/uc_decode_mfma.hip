@@ -51,29 +51,40 @@ constexpr float kLazyLog2 = 8.0f;   // softmax reference slack (log2 units)
 template <int BITS, int G>
 struct Tiles {
   static constexpr int TPW = 32 / BITS;       // codes per word
-  static constexpr int CPB = 8 / BITS;        // codes per byte
+  static constexpr int CPB = 8 / BITS;        // codes per byte = lanes that share one staged dword
+  static constexpr int NPL = 4 / CPB;         // dwords of a 4-dword A fragment one lane reads
   static constexpr int ST = 16 * TPW;         // tokens per super-tile (16 key words)
   static constexpr int NT = ST / 16;          // 16-token tiles per super-tile
   static constexpr int TW = NT / kWaves;      // tiles per wave
   static constexpr int KG = ST / G;           // key groups per super-tile
+  static constexpr int GW = (16 * TW) / G > 0 ? (16 * TW) / G : 1;  // key groups per wave
   static constexpr int NGD = kD / G;          // value groups per token
   static constexpr int VWPT = kD / TPW;       // value words per token
+  static constexpr int HW = 16 / TPW;         // value words per 16-channel block
   static constexpr int NTP = ST / 2;          // token pairs per super-tile
   static constexpr uint32_t MASK = (1u << BITS) - 1u;
   // Staged words are "byte spread": dword (byte k of word a, byte k of word
   // b) at bits 0-7 and 16-23, so a code sits at most 6 bits up its 16-bit
   // half and the AND leaves an fp16 denormal (or small normal) that is
   // exactly code * 2^(BITS e - 24).
-  // key words [word j][byte k][channel pair]: rows of 64 pairs padded to 80
-  // dwords (the four bytes one read touches fall on different banks), words
-  // 324 dwords apart (the four word quads of one staging write likewise)
-  static constexpr int KROW = 80;
-  static constexpr int KJ = 4 * KROW + 4;
-  // value words [word w][byte k][token pair]
-  static constexpr int VROW = NTP + 16;
-  static constexpr int VWS = 4 * VROW + (BITS == 2 ? 8 : 4);
+  //
+  // Key words: row (word j, byte k) of 64 dwords, dword 4q + kb = channel
+  // pair 16 kb + q.  Lane (row r, slice kap) of a tile needs the four pairs
+  // 16 kb + 4 kap + (0..3) of its row's (j, k) for every kb; the CPB lanes
+  // that share (j, k) each read NPL 16-byte pieces (all kb of NPL pairs) and
+  // exchange them with DPP.  Rows of odd k are rotated by 32 dwords, which
+  // keeps the four k rows one tile reads on different banks.
+  static constexpr int KROWS = 16 * 4;
+  // Value words: row (byte k, word-in-block h) of ST/32 blocks x 128 dwords;
+  // in a block (32 tokens = 16 token pairs), dword 64 (blk / 4) + 4 slot +
+  // blk % 4 holds word 16-channel block blk of token pair slot.  Slot 4 kap +
+  // jj holds the pair whose tokens lane slice kap needs in place jj of its
+  // fragment (pairs 2 kap, 2 kap + 1 of the first tile, then of the second),
+  // so a lane's NPL pairs are contiguous; odd k rotated as for the keys.
+  static constexpr int VRK = (ST / 32) * 128;
   static_assert(TW >= 2 && TW % 2 == 0, "a wave owns whole 32-token value blocks");
   static_assert(KG >= 1 && G % 16 == 0, "a tile lies in one group");
+  static_assert(GW == 1 || GW == 2, "the bias MFMA holds one or two groups per wave");
 };
 
 // v_perm selector: byte k of src1 at byte 0, byte k of src0 at byte 2, zeros elsewhere.
@@ -81,13 +92,20 @@ __device__ __forceinline__ constexpr uint32_t byte_spread_sel(int k) {
   return uint32_t(k) | (0x0cu << 8) | (uint32_t(4 + k) << 16) | (0x0cu << 24);
 }
 
+// Dword offset of a 4-dword piece at `off` (a multiple of 4) in row k.
+__device__ __forceinline__ uint32_t rot_row(uint32_t off, int k) { return (off + 32u * (k & 1)) & 63u; }
+
+// Slot of token pair p (0..15) of a 32-token block: pairs 2 kap, 2 kap + 1,
+// 2 kap + 8, 2 kap + 9 go to slots 4 kap .. 4 kap + 3.
+__device__ __forceinline__ uint32_t pair_slot(uint32_t p) { return 4 * ((p % 8) / 2) + p % 2 + 2 * (p / 8); }
+
 template <int BITS, int G>
 struct DecShared {
   using Tl = Tiles<BITS, G>;
   union {
     struct {
-      uint32_t kw[16 * Tl::KJ];
-      uint32_t vw[Tl::VWPT * Tl::VWS];
+      uint32_t kw[Tl::KROWS * 64];
+      uint32_t vw[4 * Tl::HW * Tl::VRK];
       _Float16 ks[Tl::KG][kD], km[Tl::KG][kD];   // key stats [group][channel]
       _Float16 vs[Tl::NGD][Tl::ST], vm[Tl::NGD][Tl::ST];  // value stats [group][token]
     } st;
@@ -125,16 +143,17 @@ __device__ __forceinline__ bool split_has_work(int64_t split, int64_t tq, int64_
 // 16 b + 4 k + v of accumulator b, so every rescale is lane-local.
 struct WaveState {
   f4 o[8];
-  f4 cmin;  // row g < groups: sum_t P * value minimum of group g (packed splits)
+  f4 cmin;  // packed splits: row g < groups: sum_t P * value minimum of group g; row NGD: sum_t P
   float m;  // running max of query n (log2 units), equal across the k-slices
-  float l;  // this lane's share of the running sum (reduced over the k-slices at the end)
+  float l;  // residual splits: this lane's share of the running sum (reduced over the k-slices at the end)
 };
 
 // Fold NP tiles of base-2 logits (acc[i][v]: token 16 i + 4 k + v of the
 // wave's tiles, column = query) into the running state; acc returns holding
 // the probabilities and the output is rescaled.  `valid_rows` tokens of the
 // wave's tiles are real (the rest of the last super-tile reads past the end).
-template <int NP>
+// SUM: keep the running sum in st.l (the packed path sums P by MFMA instead).
+template <int NP, bool SUM>
 __device__ __forceinline__ void softmax_tiles(f4 (&acc)[NP], int valid_rows, WaveState &st, int kap) {
   if (valid_rows < 16 * NP) {
 #pragma unroll
@@ -163,10 +182,10 @@ __device__ __forceinline__ void softmax_tiles(f4 (&acc)[NP], int valid_rows, Wav
     for (int v = 0; v < 4; ++v) {
       const float e = fast_exp2(acc[i][v] - m_ref);
       acc[i][v] = e;
-      sum += e;
+      if constexpr (SUM) sum += e;
     }
   const float alpha = raise ? fast_exp2(st.m - m_ref) : 1.0f;
-  st.l = st.l * alpha + sum;
+  if constexpr (SUM) st.l = st.l * alpha + sum;
   st.m = m_new;
   if (__any(raise)) {
 #pragma unroll
@@ -177,8 +196,9 @@ __device__ __forceinline__ void softmax_tiles(f4 (&acc)[NP], int valid_rows, Wav
 
 // ------------------------------------------------------------ packed path --
 // Query rows of the KV head staged once per workgroup as fp16 [row][channel]
-// (padded rows); lane (n, k-slice) reads its B fragment of block kb from here.
-constexpr int kQPad = kD + 8;
+// (rows padded to 72 dwords: the 16 rows of one fragment read hit distinct
+// banks); lane (n, k-slice) reads its B fragment of block kb from here.
+constexpr int kQPad = kD + 16;
 
 template <int QD>
 __device__ __forceinline__ void stage_queries_t(_Float16 (*sq)[kQPad], const void *query, int64_t h,
@@ -227,14 +247,15 @@ __device__ __forceinline__ h8 query_frag(const _Float16 (*sq)[kQPad], int kb, in
 // super-tile's loads overlap this one's MFMAs.  The packed tensors are
 // token-major, so every stream of a super-tile is one contiguous run of the
 // head's rows.  Thread t loads:
-//   key words: channels 4c .. 4c+3 (c = t % 32) of words t / 32 and 8 + t / 32;
+//   key words: channel pairs 16 kb + q (q = t % 16, kb = 0..3) of word t / 16;
 //   value words: word quad t % NQ of tokens 2tp, 2tp+1 (tp = t / NQ);
 //   key stats: 8 channels (t % 16) of group (t % 128) / 16, scales (t < 128)
 //     or minima;
 //   value stats: 16 bytes of the scales (t < 128) or minima.
 template <int BITS, int G>
 struct Prefetch {
-  uint4 kw[2], vw[2];
+  uint2 kw[4];
+  uint4 vw[2];
   uint4 ks, vs;
 };
 
@@ -249,9 +270,9 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
   using Tl = Tiles<BITS, G>;
   const int tid = threadIdx.x;
   {  // key words [word][D]: 16 rows of 512 bytes
-    const uint32_t base = (t0 / Tl::TPW) * kD * 4u + 16u * tid;
-    pf.kw[0] = bload128(rg.kcode, base);
-    pf.kw[1] = bload128(rg.kcode, base + 8u * kD * 4u);
+    const uint32_t base = ((t0 / Tl::TPW + (tid >> 4)) * kD + 2 * (tid & 15)) * 4u;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) pf.kw[kb] = bload64(rg.kcode, base + 128u * kb);
   }
   {  // value words of two neighbouring tokens
     constexpr uint32_t NQ = Tl::VWPT / 4;
@@ -274,35 +295,47 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
   }
 }
 
-// Move a landed prefetch into the interleaved / transposed LDS layouts.
+// Move a landed prefetch into the byte-spread / transposed LDS layouts.
 template <int BITS, int G>
 __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch<BITS, G> &pf) {
   using Tl = Tiles<BITS, G>;
   const int tid = threadIdx.x;
   constexpr uint32_t kLo = 0x05040100u, kHi = 0x07060302u;  // low / high halves of (a, b)
-  {  // channels 4c .. 4c+3 = pairs 2c, 2c+1 of words j and j + 8
-    const uint32_t pc = 2 * (tid & 31), j = tid >> 5;
+  {  // pairs 16 kb + q of word j: dwords 4q .. 4q + 3 of row (j, k)
+    const uint32_t j = tid >> 4, q = tid & 15;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint4 w = pf.kw[h];
-      uint32_t *row = &sh.st.kw[(j + 8 * h) * Tl::KJ + pc];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        *reinterpret_cast<uint2 *>(&row[k * Tl::KROW]) =
-            make_uint2(__builtin_amdgcn_perm(w.y, w.x, byte_spread_sel(k)),
-                       __builtin_amdgcn_perm(w.w, w.z, byte_spread_sel(k)));
+    for (int k = 0; k < 4; ++k) {
+      uint4 d;
+      d.x = __builtin_amdgcn_perm(pf.kw[0].y, pf.kw[0].x, byte_spread_sel(k));
+      d.y = __builtin_amdgcn_perm(pf.kw[1].y, pf.kw[1].x, byte_spread_sel(k));
+      d.z = __builtin_amdgcn_perm(pf.kw[2].y, pf.kw[2].x, byte_spread_sel(k));
+      d.w = __builtin_amdgcn_perm(pf.kw[3].y, pf.kw[3].x, byte_spread_sel(k));
+      *reinterpret_cast<uint4 *>(&sh.st.kw[(4 * j + k) * 64 + rot_row(4 * q, k)]) = d;
     }
   }
-  {
+  {  // words 4 wq + i of token pair tp: block tp / 16, slot of pair tp % 16
     constexpr uint32_t NQ = Tl::VWPT / 4;
     const uint32_t tp = tid / NQ, wq = tid % NQ;
     const uint32_t a[4] = {pf.vw[0].x, pf.vw[0].y, pf.vw[0].z, pf.vw[0].w};
     const uint32_t b[4] = {pf.vw[1].x, pf.vw[1].y, pf.vw[1].z, pf.vw[1].w};
+    const uint32_t in_block = (tp / 16) * 128, slot4 = 4 * pair_slot(tp % 16);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t *row = &sh.st.vw[(4 * wq + i) * Tl::VWS + tp];
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (Tl::HW == 1) {  // 2-bit: word = block blk = 4 wq + i
+        const uint4 d = make_uint4(__builtin_amdgcn_perm(b[0], a[0], byte_spread_sel(k)),
+                                   __builtin_amdgcn_perm(b[1], a[1], byte_spread_sel(k)),
+                                   __builtin_amdgcn_perm(b[2], a[2], byte_spread_sel(k)),
+                                   __builtin_amdgcn_perm(b[3], a[3], byte_spread_sel(k)));
+        *reinterpret_cast<uint4 *>(&sh.st.vw[k * Tl::VRK + in_block + wq * 64 + rot_row(slot4, k)]) = d;
+      } else {  // 4-bit: word 4 wq + i = block 2 wq + i / 2, half i % 2
 #pragma unroll
-      for (int k = 0; k < 4; ++k) row[k * Tl::VROW] = __builtin_amdgcn_perm(b[i], a[i], byte_spread_sel(k));
+        for (int hh = 0; hh < 2; ++hh) {
+          const uint2 d = make_uint2(__builtin_amdgcn_perm(b[hh], a[hh], byte_spread_sel(k)),
+                                     __builtin_amdgcn_perm(b[2 + hh], a[2 + hh], byte_spread_sel(k)));
+          *reinterpret_cast<uint2 *>(&sh.st.vw[(2 * k + hh) * Tl::VRK + in_block + (wq / 2) * 64 +
+                                               rot_row(slot4, k) + 2 * (wq % 2)]) = d;
+        }
+      }
     }
   }
   {  // key stats arrive as [group][channel] rows already
@@ -340,81 +373,114 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
 // Per-lane constants of the compute loop.
 template <int BITS, int G>
 struct LaneConst {
-  using Tl = Tiles<BITS, G>;
-  uint32_t kaddr;          // key-word read offset of the wave's first tile (without 16 kb)
-  uint32_t kmask;          // AND mask that leaves the row's codes of two channels
-  float pw[4];             // 2^(24 - BITS e) * softmax scale of logit row 4k + v
-  uint32_t vmask;          // AND mask of the lane's value row (channel) within a word half
-  uint32_t vaddr;          // value-word read offset: half and word part of block 0
+  uint32_t kaddr;   // key read offset (dwords) of the wave's first tile
+  uint32_t kmask;   // AND mask that leaves the row's codes of two channels
+  float pw[4];      // 2^(24 - BITS e) * softmax scale of logit row 4k + v
+  uint32_t vmask;   // AND mask of the lane's value row (channel) within a word half
+  uint32_t vaddr;   // value read offset (dwords) of the wave's first block
 };
 
 template <int BITS, int G>
 __device__ __forceinline__ LaneConst<BITS, G> lane_const(int wave, int lane, float scale_log2) {
   using Tl = Tiles<BITS, G>;
   LaneConst<BITS, G> lc;
-  const int r = lane & 15, kap = lane >> 4;
-  {  // tile i of the wave starts 16 i / TPW words after its first tile; the row's byte and mask are the same
+  const int r = lane & 15, kap = lane >> 4, e = r % Tl::CPB;
+  {  // tile i of the wave starts 16 i / TPW word rows after its first tile
     const int tok = 16 * wave * Tl::TW + r;  // token of row r of the wave's first tile within the super-tile
-    const int j = tok / Tl::TPW, pos = tok % Tl::TPW, k = pos / Tl::CPB, e = pos % Tl::CPB;
-    lc.kaddr = j * Tl::KJ + k * Tl::KROW + 4 * kap;
+    const int j = tok / Tl::TPW, k = (tok % Tl::TPW) / Tl::CPB;
+    lc.kaddr = (4 * j + k) * 64 + rot_row(4 * (4 * kap + Tl::NPL * e), k);
     lc.kmask = (Tl::MASK << (BITS * e)) * 0x10001u;
   }
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
-    const int e = ((4 * kap + v) % Tl::TPW) % Tl::CPB;  // tile row 4k + v: position in word, then in byte
-    lc.pw[v] = float(1 << (24 - BITS * e)) * scale_log2;
+    const int ev = ((4 * kap + v) % Tl::TPW) % Tl::CPB;  // tile row 4k + v: position in word, then in byte
+    lc.pw[v] = float(1 << (24 - BITS * ev)) * scale_log2;
   }
-  {
-    const int ci = r % Tl::TPW;          // channel r of a 16-channel block within its value word
-    const int k = ci / Tl::CPB, e = ci % Tl::CPB;
+  {  // channel 16 blk + r: word-in-block r / TPW, byte (r % TPW) / CPB
+    const int k = (r % Tl::TPW) / Tl::CPB, hh = r / Tl::TPW;
     lc.vmask = (Tl::MASK << (BITS * e)) * 0x10001u;
-    lc.vaddr = (r / Tl::TPW) * Tl::VWS + k * Tl::VROW + 2 * kap;
+    lc.vaddr = (Tl::HW * k + hh) * Tl::VRK + (wave * Tl::TW / 2) * 128 + rot_row(4 * (4 * kap + Tl::NPL * e), k);
   }
   return lc;
 }
 
-__device__ __forceinline__ h8 and_h8(uint4 x, uint32_t m) {
-  return __builtin_bit_cast(h8, make_uint4(x.x & m, x.y & m, x.z & m, x.w & m));
+// quad_perm control that gives lane (4a + b) dword jj of its CPB-lane group:
+// lanes of a group hold NPL consecutive dwords each.
+template <int CPB, int JJ>
+__device__ __forceinline__ constexpr int group_bcast_ctrl() {
+  constexpr int NPL = 4 / CPB;
+  int ctrl = 0;
+  for (int b = 0; b < 4; ++b) ctrl |= ((b / CPB) * CPB + JJ / NPL) << (2 * b);
+  return ctrl;
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_and(uint32_t x, uint32_t m) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, 0xf, 0xf, false)) & m;
+}
+
+// A fragment of pair dwords jj = 0..3 from the CPB-lane group: piece[s] holds
+// this lane's dwords s (NPL of them) of one kb / block.
+template <int CPB>
+__device__ __forceinline__ h8 gather_and(const uint32_t (&piece)[4 / CPB], uint32_t m) {
+  constexpr int NPL = 4 / CPB;
+  uint4 x;
+  x.x = dpp_and<group_bcast_ctrl<CPB, 0>()>(piece[0 % NPL], m);
+  x.y = dpp_and<group_bcast_ctrl<CPB, 1>()>(piece[1 % NPL], m);
+  x.z = dpp_and<group_bcast_ctrl<CPB, 2>()>(piece[2 % NPL], m);
+  x.w = dpp_and<group_bcast_ctrl<CPB, 3>()>(piece[3 % NPL], m);
+  return __builtin_bit_cast(h8, x);
 }
 
 // Logits, softmax and P.V of this wave's tiles of the staged super-tile.
 template <int BITS, int G>
-__device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const _Float16 (*sq)[kQPad],
+__device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const h8 (&qf)[4],
                                              const LaneConst<BITS, G> &lc, int wave, int valid_rows,
                                              float scale_log2, WaveState &st) {
   using Tl = Tiles<BITS, G>;
+  constexpr int NPL = Tl::NPL, CPB = Tl::CPB;
   const int lane = threadIdx.x & 63, r = lane & 15, kap = lane >> 4;
   constexpr int GT = G / 16;  // tiles per group
+  const int g0 = (16 * wave * Tl::TW) / G;  // first key group of the wave
+
+  // ---- key minimum term of the wave's groups: A row r = minima of group
+  // g0 + r % GW, so element v of every lane holds group v % GW's bias
+  f4 mb = f4{0, 0, 0, 0};
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+    mb = mfma32(*reinterpret_cast<const h8 *>(&sh.st.km[g0 + r % Tl::GW][32 * kb + 8 * kap]), qf[kb], mb);
 
   // ---- keys: logits of the wave's TW tiles (16 tokens x 16 query rows each)
   f4 acc[Tl::TW];
   h8 bp[4];
-  float bias = 0.0f;
 #pragma unroll
   for (int i = 0; i < Tl::TW; ++i) {
-    if (i % GT == 0) {  // first tile of a group: B' = q * key scale, and the minimum term
+    if (i % GT == 0) {  // first tile of a group: B' = q * key scale
       const int g = (16 * (wave * Tl::TW + i)) / G;
-      f4 mb = f4{0, 0, 0, 0};
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const h8 qf = query_frag(sq, kb, lane);
-        const h8 s8 = *reinterpret_cast<const h8 *>(&sh.st.ks[g][32 * kb + 8 * kap]);
-        const h8 m8 = *reinterpret_cast<const h8 *>(&sh.st.km[g][32 * kb + 8 * kap]);
-        bp[kb] = qf * s8;
-        mb = mfma32(m8, qf, mb);  // every row of A = the minima: each row gets sum_c m_c q_c
-      }
-      bias = mb[0] * scale_log2;
+      for (int kb = 0; kb < 4; ++kb)
+        bp[kb] = qf[kb] * *reinterpret_cast<const h8 *>(&sh.st.ks[g][32 * kb + 8 * kap]);
+    }
+    // NPL pieces of 4 kb each: pairs 16 kb + 4 kap + NPL e + s
+    uint32_t pc[NPL][4];
+#pragma unroll
+    for (int s = 0; s < NPL; ++s) {
+      const uint4 x = *reinterpret_cast<const uint4 *>(&sh.st.kw[lc.kaddr + (16 * i / Tl::TPW) * 256 + 4 * s]);
+      pc[s][0] = x.x; pc[s][1] = x.y; pc[s][2] = x.z; pc[s][3] = x.w;
     }
     f4 a = f4{0, 0, 0, 0};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const uint4 x = *reinterpret_cast<const uint4 *>(&sh.st.kw[lc.kaddr + (16 * i / Tl::TPW) * Tl::KJ + 16 * kb]);
-      a = mfma32(and_h8(x, lc.kmask), bp[kb], a);
+      uint32_t piece[NPL];
+#pragma unroll
+      for (int s = 0; s < NPL; ++s) piece[s] = pc[s][kb];
+      a = mfma32(gather_and<CPB>(piece, lc.kmask), bp[kb], a);
     }
+    const float bias = mb[((16 * i) / G) % Tl::GW] * scale_log2;
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[i][v] = __builtin_fmaf(a[v], lc.pw[v], bias);
   }
-  softmax_tiles<Tl::TW>(acc, valid_rows, st, kap);
+  softmax_tiles<Tl::TW, false>(acc, valid_rows, st, kap);
 
   // ---- values: O^T += V^T P^T over 32-token blocks (tiles 2kc, 2kc + 1):
   // K slot 8k + j is token 4k + j of the first tile (j < 4) or 4k + j - 4 of
@@ -424,16 +490,26 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
     const int ta = wave * Tl::TW + 2 * kc;  // first tile of the block within the super-tile
     const h4 pa4 = cvt4(acc[2 * kc]), pb4 = cvt4(acc[2 * kc + 1]);
     const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
-    {  // A rows g < NGD: the value minima of group g
+    {  // A rows g < NGD: the value minima of group g; row NGD: ones (the sum of P)
       h8 am = h8{0, 0, 0, 0, 0, 0, 0, 0};
       if (r < Tl::NGD) {
         const h4 ma = *reinterpret_cast<const h4 *>(&sh.st.vm[r][16 * ta + 4 * kap]);
-        const h4 mb = *reinterpret_cast<const h4 *>(&sh.st.vm[r][16 * ta + 16 + 4 * kap]);
-        am = h8{ma[0], ma[1], ma[2], ma[3], mb[0], mb[1], mb[2], mb[3]};
+        const h4 mb4 = *reinterpret_cast<const h4 *>(&sh.st.vm[r][16 * ta + 16 + 4 * kap]);
+        am = h8{ma[0], ma[1], ma[2], ma[3], mb4[0], mb4[1], mb4[2], mb4[3]};
+      } else if (r == Tl::NGD) {
+        am = h8{1, 1, 1, 1, 1, 1, 1, 1};
       }
       st.cmin = mfma32(am, p8, st.cmin);
     }
-    const uint32_t base = lc.vaddr + 8 * ta;
+    // this lane's NPL pairs of every 16-channel block: dwords blk of NPL slots
+    uint32_t pv[NPL][8];
+#pragma unroll
+    for (int s = 0; s < NPL; ++s)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const uint4 x = *reinterpret_cast<const uint4 *>(&sh.st.vw[lc.vaddr + kc * 128 + half * 64 + 4 * s]);
+        pv[s][4 * half + 0] = x.x; pv[s][4 * half + 1] = x.y; pv[s][4 * half + 2] = x.z; pv[s][4 * half + 3] = x.w;
+      }
     h8 ps;  // P * value scale of the current group, formed at its first block
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
@@ -443,11 +519,10 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
         const h4 sb = *reinterpret_cast<const h4 *>(&sh.st.vs[g][16 * ta + 16 + 4 * kap]);
         ps = p8 * h8{sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
       }
-      // 16 channels per block = 16 / TPW value words
-      const uint32_t off = base + blk * (16 / Tl::TPW) * Tl::VWS;
-      const uint2 x0 = *reinterpret_cast<const uint2 *>(&sh.st.vw[off]);
-      const uint2 x1 = *reinterpret_cast<const uint2 *>(&sh.st.vw[off + 8]);
-      st.o[blk] = mfma32(and_h8(make_uint4(x0.x, x0.y, x1.x, x1.y), lc.vmask), ps, st.o[blk]);
+      uint32_t piece[NPL];
+#pragma unroll
+      for (int s = 0; s < NPL; ++s) piece[s] = pv[s][blk];
+      st.o[blk] = mfma32(gather_and<CPB>(piece, lc.vmask), ps, st.o[blk]);
     }
   }
 }
@@ -472,9 +547,12 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
   rg.vscale = make_rsrc(static_cast<const char *>(it.value_scale) + h * cap * vstat_row, Tq * vstat_row);
   rg.vmin = make_rsrc(static_cast<const char *>(it.value_min) + h * cap * vstat_row, Tq * vstat_row);
   const LaneConst<BITS, G> lc = lane_const<BITS, G>(wave, lane, p.scale_log2);
+  h8 qf[4];  // this lane's query fragments, for the whole split
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) qf[kb] = query_frag(sq, kb, lane);
   // super-tiles split, split + S, split + 2S, ... (S = packed splits): the S
   // splits of a unit run side by side on one XCD and read neighbouring parts
-  // of the same 128-byte key-code and key-stat lines at about the same time
+  // of the same rows at about the same time
   const int64_t n_super = (Tq + Tl::ST - 1) / Tl::ST;
   const int64_t stride = p.splits_packed * Tl::ST;
   const int n_it = static_cast<int>(min<int64_t>(p.nst, (n_super - split + p.splits_packed - 1) / p.splits_packed));
@@ -488,16 +566,18 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
     if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(t0 + stride));  // lands during compute
     const int valid = static_cast<int>(min<int64_t>(int64_t(16 * Tl::TW),
                                                     Tq - t0 - int64_t(16 * Tl::TW) * wave));
-    if (valid > 0) compute_tile<BITS, G>(sh, sq, lc, wave, valid, p.scale_log2, st);
+    if (valid > 0) compute_tile<BITS, G>(sh, qf, lc, wave, valid, p.scale_log2, st);
   }
   // undo the denormal code scaling 2^(BITS e - 24) of each output channel
   // (channel 16 b + 4 k + v: e depends on k and v only) and add the value
   // minima: sum_t P min of the channel's group sits in row g of cmin, held by
-  // lane (n, k = 0) as element g
+  // lane (n, k = g / 4) as element g % 4; the sum of P sits in row NGD
   const int n = lane & 15, kap = lane >> 4;
   float cm[Tl::NGD];
 #pragma unroll
-  for (int g = 0; g < Tl::NGD; ++g) cm[g] = __shfl(st.cmin[g], n, kWave);
+  for (int g = 0; g < Tl::NGD; ++g) cm[g] = __shfl(st.cmin[g % 4], n + 16 * (g / 4), kWave);
+  const float l_all = __shfl(st.cmin[Tl::NGD % 4], n + 16 * (Tl::NGD / 4), kWave);
+  st.l = kap == 0 ? l_all : 0.0f;  // the merge sums the k-slices
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int e = ((4 * kap + v) % Tl::TPW) % Tl::CPB;
@@ -557,7 +637,7 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
     for (int v = 0; v < 4; ++v) acc[b][v] *= p.scale_log2;
   }
   const int valid = static_cast<int>(min<int64_t>(int64_t(kResWaveTokens), Tr - tw));
-  softmax_tiles<kTiles>(acc, valid, st, kap);
+  softmax_tiles<kTiles, true>(acc, valid, st, kap);
   // O^T += V^T P^T: a lane loads 8 channels of one token per 32-channel
   // block; a selection MFMA turns a tile of them into the A layout of
   // accumulator b (row = channel 16 b + n, 4 tokens per lane)
