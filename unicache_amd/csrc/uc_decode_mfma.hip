@@ -106,12 +106,15 @@ struct DecShared {
     struct {
       uint32_t kw[Tl::KROWS * 64];
       uint32_t vw[4 * Tl::HW * Tl::VRK];
-      _Float16 ks[Tl::KG][kD], km[Tl::KG][kD];   // key stats [group][channel]
-      _Float16 vs[Tl::NGD][Tl::ST], vm[Tl::NGD][Tl::ST];  // value stats [group][token]
+      // stats rows padded by 16 dwords: the two key-minimum rows of the bias
+      // MFMA and the value-minimum rows of the cmin MFMA sit on different banks
+      _Float16 ks[Tl::KG][kD + 32], km[Tl::KG][kD + 32];     // key stats [group][channel]
+      _Float16 vs[Tl::NGD][Tl::ST + 32], vm[Tl::NGD][Tl::ST + 32];  // value stats [group][token]
     } st;
     struct {
-      float o[kWaves - 1][16][kD];  // waves 1.. : scaled partial outputs [query row][channel]
-      float ml[kWaves][16][2];      // every wave's (max, sum) per query row
+      // rows padded by 4 dwords so the 16 query rows of one store hit distinct banks
+      float o[kWaves - 1][16][kD + 4];  // waves 1.. : scaled partial outputs [query row][channel]
+      float ml[kWaves][16][2];          // every wave's (max, sum) per query row
     } mrg;
   };
 };
@@ -342,7 +345,7 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
     constexpr int NKS = Tl::KG * 16;
     const int i = tid & 127;
     if (i < NKS) {
-      _Float16(*dst)[kD] = tid < 128 ? sh.st.ks : sh.st.km;
+      _Float16(*dst)[kD + 32] = tid < 128 ? sh.st.ks : sh.st.km;
       *reinterpret_cast<uint4 *>(&dst[i / 16][8 * (i % 16)]) = pf.ks;
     }
   }
@@ -350,7 +353,7 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
     constexpr int NVC = Tl::ST * Tl::NGD / 8;
     const int i = tid & 127;
     if (i < NVC) {
-      _Float16(*dst)[Tl::ST] = tid < 128 ? sh.st.vs : sh.st.vm;
+      _Float16(*dst)[Tl::ST + 32] = tid < 128 ? sh.st.vs : sh.st.vm;
       const uint32_t w[4] = {pf.vs.x, pf.vs.y, pf.vs.z, pf.vs.w};
       if constexpr (Tl::NGD == 4) {  // tokens 2i, 2i+1 x groups 0..3
 #pragma unroll
