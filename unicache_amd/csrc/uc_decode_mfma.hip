@@ -68,20 +68,27 @@ struct Tiles {
   // half and the AND leaves an fp16 denormal (or small normal) that is
   // exactly code * 2^(BITS e - 24).
   //
+  // Each wave stages and reads only its own WT tokens, so the waves of a
+  // workgroup never wait for each other inside the loop.
+  //
   // Key words: row (word j, byte k) of 64 dwords, dword 4q + kb = channel
   // pair 16 kb + q.  Lane (row r, slice kap) of a tile needs the four pairs
   // 16 kb + 4 kap + (0..3) of its row's (j, k) for every kb; the CPB lanes
   // that share (j, k) each read NPL 16-byte pieces (all kb of NPL pairs) and
   // exchange them with DPP.  Rows of odd k are rotated by 32 dwords, which
   // keeps the four k rows one tile reads on different banks.
-  static constexpr int KROWS = 16 * 4;
-  // Value words: row (byte k, word-in-block h) of ST/32 blocks x 128 dwords;
+  static constexpr int WT = 16 * TW;          // tokens per wave per super-tile
+  static constexpr int JW = WT / TPW;         // key word rows per wave
+  // Value words: row (byte k, word-in-block h) of WT/32 blocks x 128 dwords;
   // in a block (32 tokens = 16 token pairs), dword 64 (blk / 4) + 4 slot +
-  // blk % 4 holds word 16-channel block blk of token pair slot.  Slot 4 kap +
-  // jj holds the pair whose tokens lane slice kap needs in place jj of its
+  // blk % 4 holds 16-channel block blk of token pair slot.  Slot 4 kap + jj
+  // holds the pair whose tokens lane slice kap needs in place jj of its
   // fragment (pairs 2 kap, 2 kap + 1 of the first tile, then of the second),
   // so a lane's NPL pairs are contiguous; odd k rotated as for the keys.
-  static constexpr int VRK = (ST / 32) * 128;
+  static constexpr int VRKW = (WT / 32) * 128;
+  // value-stat rows [group][token] padded so the cmin MFMA's minima rows
+  // (one per group) sit on different banks
+  static constexpr int VSP = WT + (BITS == 2 ? 32 : 16);
   static_assert(TW >= 2 && TW % 2 == 0, "a wave owns whole 32-token value blocks");
   static_assert(KG >= 1 && G % 16 == 0, "a tile lies in one group");
   static_assert(GW == 1 || GW == 2, "the bias MFMA holds one or two groups per wave");
@@ -99,18 +106,22 @@ __device__ __forceinline__ uint32_t rot_row(uint32_t off, int k) { return (off +
 // 2 kap + 8, 2 kap + 9 go to slots 4 kap .. 4 kap + 3.
 __device__ __forceinline__ uint32_t pair_slot(uint32_t p) { return 4 * ((p % 8) / 2) + p % 2 + 2 * (p / 8); }
 
+// One wave's staging area for one super-tile.
+template <int BITS, int G>
+struct WaveStage {
+  using Tl = Tiles<BITS, G>;
+  uint32_t kw[Tl::JW * 4 * 64];
+  uint32_t vw[4 * Tl::HW * Tl::VRKW];
+  // rows padded by 16 dwords: the two key-minimum rows of the bias MFMA sit
+  // on different banks
+  _Float16 ks[Tl::GW][kD + 32], km[Tl::GW][kD + 32];    // key stats [group][channel]
+  _Float16 vs[Tl::NGD][Tl::VSP], vm[Tl::NGD][Tl::VSP];  // value stats [group][token]
+};
+
 template <int BITS, int G>
 struct DecShared {
-  using Tl = Tiles<BITS, G>;
   union {
-    struct {
-      uint32_t kw[Tl::KROWS * 64];
-      uint32_t vw[4 * Tl::HW * Tl::VRK];
-      // stats rows padded by 16 dwords: the two key-minimum rows of the bias
-      // MFMA and the value-minimum rows of the cmin MFMA sit on different banks
-      _Float16 ks[Tl::KG][kD + 32], km[Tl::KG][kD + 32];     // key stats [group][channel]
-      _Float16 vs[Tl::NGD][Tl::ST + 32], vm[Tl::NGD][Tl::ST + 32];  // value stats [group][token]
-    } st;
+    WaveStage<BITS, G> st[kWaves];
     struct {
       // rows padded by 4 dwords so the 16 query rows of one store hit distinct banks
       float o[kWaves - 1][16][kD + 4];  // waves 1.. : scaled partial outputs [query row][channel]
@@ -266,46 +277,53 @@ struct PackedRegion {
   Rsrc kcode, kscale, kmin, vcode, vscale, vmin;
 };
 
-// Issue the loads of the super-tile starting at token t0 (a multiple of ST).
-// Rows past the packed tokens fall outside the buffer resources and read as 0.
+// Issue this wave's loads of the super-tile starting at token t0 (a
+// multiple of ST): tokens t0 + WT wave ...  Rows past the packed tokens fall
+// outside the buffer resources and read as 0.  Lane l loads
+//   key words: channel pairs 16 kb + (l % 16), kb = 0..3, of word row l / 16;
+//   value words: word quad l % NQ of token pair l / NQ;
+//   key stats: 16 bytes of the wave's group rows, scales then minima;
+//   value stats: 16 bytes of the wave's tokens, scales then minima.
 template <int BITS, int G>
-__device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedRegion &rg, uint32_t t0) {
+__device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedRegion &rg, uint32_t t0, int wave) {
   using Tl = Tiles<BITS, G>;
-  const int tid = threadIdx.x;
-  {  // key words [word][D]: 16 rows of 512 bytes
-    const uint32_t base = ((t0 / Tl::TPW + (tid >> 4)) * kD + 2 * (tid & 15)) * 4u;
+  const int lane = threadIdx.x & 63;
+  const uint32_t tw = t0 + Tl::WT * wave;
+  {  // key words [word][D]: JW rows of 512 bytes
+    const uint32_t base = ((tw / Tl::TPW + (lane >> 4)) * kD + 2 * (lane & 15)) * 4u;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) pf.kw[kb] = bload64(rg.kcode, base + 128u * kb);
   }
   {  // value words of two neighbouring tokens
     constexpr uint32_t NQ = Tl::VWPT / 4;
-    const uint32_t tp = tid / NQ, wq = tid % NQ;
-    const uint32_t tok = t0 + 2 * tp;
+    const uint32_t tp = lane / NQ, wq = lane % NQ;
+    const uint32_t tok = tw + 2 * tp;
     pf.vw[0] = bload128(rg.vcode, (tok * Tl::VWPT + 4 * wq) * 4u);
     pf.vw[1] = bload128(rg.vcode, ((tok + 1) * Tl::VWPT + 4 * wq) * 4u);
   }
-  {  // key stats [group][D]: KG rows of 256 bytes per stat
-    constexpr int NKS = Tl::KG * 16;  // 16-byte chunks per stat
-    const int i = tid & 127;
-    const Rsrc r = tid < 128 ? rg.kscale : rg.kmin;
-    pf.ks = i < NKS ? bload128(r, (t0 / G) * kD * 2u + 16u * i) : make_uint4(0, 0, 0, 0);
+  {  // key stats [group][D]: GW rows of 256 bytes per stat
+    constexpr int NKS = Tl::GW * 16;  // 16-byte chunks per stat
+    const int i = lane % NKS, stat = lane / NKS;
+    const Rsrc r = stat == 0 ? rg.kscale : rg.kmin;
+    pf.ks = stat < 2 ? bload128(r, (tw / G) * kD * 2u + 16u * i) : make_uint4(0, 0, 0, 0);
   }
-  {  // value stats [Tq][NGD]: 16 bytes each
-    constexpr int NVC = Tl::ST * Tl::NGD / 8;  // 16-byte chunks per stat
-    const int i = tid & 127;
-    const Rsrc r = tid < 128 ? rg.vscale : rg.vmin;
-    pf.vs = i < NVC ? bload128(r, (t0 * Tl::NGD + 8 * i) * 2u) : make_uint4(0, 0, 0, 0);
+  {  // value stats [Tq][NGD]
+    constexpr int NVC = Tl::WT * Tl::NGD / 8;  // 16-byte chunks per stat
+    const int i = lane % NVC, stat = lane / NVC;
+    const Rsrc r = stat == 0 ? rg.vscale : rg.vmin;
+    pf.vs = stat < 2 ? bload128(r, (tw * Tl::NGD + 8 * i) * 2u) : make_uint4(0, 0, 0, 0);
   }
 }
 
-// Move a landed prefetch into the byte-spread / transposed LDS layouts.
+// Move this wave's landed prefetch into its byte-spread / transposed LDS
+// layouts.
 template <int BITS, int G>
-__device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch<BITS, G> &pf) {
+__device__ __forceinline__ void stage_lds(WaveStage<BITS, G> &ws, const Prefetch<BITS, G> &pf) {
   using Tl = Tiles<BITS, G>;
-  const int tid = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   constexpr uint32_t kLo = 0x05040100u, kHi = 0x07060302u;  // low / high halves of (a, b)
-  {  // pairs 16 kb + q of word j: dwords 4q .. 4q + 3 of row (j, k)
-    const uint32_t j = tid >> 4, q = tid & 15;
+  {  // pairs 16 kb + q of word row j: dwords 4q .. 4q + 3 of row (j, k)
+    const uint32_t j = lane >> 4, q = lane & 15;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       uint4 d;
@@ -313,12 +331,12 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
       d.y = __builtin_amdgcn_perm(pf.kw[1].y, pf.kw[1].x, byte_spread_sel(k));
       d.z = __builtin_amdgcn_perm(pf.kw[2].y, pf.kw[2].x, byte_spread_sel(k));
       d.w = __builtin_amdgcn_perm(pf.kw[3].y, pf.kw[3].x, byte_spread_sel(k));
-      *reinterpret_cast<uint4 *>(&sh.st.kw[(4 * j + k) * 64 + rot_row(4 * q, k)]) = d;
+      *reinterpret_cast<uint4 *>(&ws.kw[(4 * j + k) * 64 + rot_row(4 * q, k)]) = d;
     }
   }
   {  // words 4 wq + i of token pair tp: block tp / 16, slot of pair tp % 16
     constexpr uint32_t NQ = Tl::VWPT / 4;
-    const uint32_t tp = tid / NQ, wq = tid % NQ;
+    const uint32_t tp = lane / NQ, wq = lane % NQ;
     const uint32_t a[4] = {pf.vw[0].x, pf.vw[0].y, pf.vw[0].z, pf.vw[0].w};
     const uint32_t b[4] = {pf.vw[1].x, pf.vw[1].y, pf.vw[1].z, pf.vw[1].w};
     const uint32_t in_block = (tp / 16) * 128, slot4 = 4 * pair_slot(tp % 16);
@@ -329,31 +347,31 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
                                    __builtin_amdgcn_perm(b[1], a[1], byte_spread_sel(k)),
                                    __builtin_amdgcn_perm(b[2], a[2], byte_spread_sel(k)),
                                    __builtin_amdgcn_perm(b[3], a[3], byte_spread_sel(k)));
-        *reinterpret_cast<uint4 *>(&sh.st.vw[k * Tl::VRK + in_block + wq * 64 + rot_row(slot4, k)]) = d;
+        *reinterpret_cast<uint4 *>(&ws.vw[k * Tl::VRKW + in_block + wq * 64 + rot_row(slot4, k)]) = d;
       } else {  // 4-bit: word 4 wq + i = block 2 wq + i / 2, half i % 2
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const uint2 d = make_uint2(__builtin_amdgcn_perm(b[hh], a[hh], byte_spread_sel(k)),
                                      __builtin_amdgcn_perm(b[2 + hh], a[2 + hh], byte_spread_sel(k)));
-          *reinterpret_cast<uint2 *>(&sh.st.vw[(2 * k + hh) * Tl::VRK + in_block + (wq / 2) * 64 +
-                                               rot_row(slot4, k) + 2 * (wq % 2)]) = d;
+          *reinterpret_cast<uint2 *>(&ws.vw[(2 * k + hh) * Tl::VRKW + in_block + (wq / 2) * 64 +
+                                            rot_row(slot4, k) + 2 * (wq % 2)]) = d;
         }
       }
     }
   }
   {  // key stats arrive as [group][channel] rows already
-    constexpr int NKS = Tl::KG * 16;
-    const int i = tid & 127;
-    if (i < NKS) {
-      _Float16(*dst)[kD + 32] = tid < 128 ? sh.st.ks : sh.st.km;
+    constexpr int NKS = Tl::GW * 16;
+    const int i = lane % NKS, stat = lane / NKS;
+    if (stat < 2) {
+      _Float16(*dst)[kD + 32] = stat == 0 ? ws.ks : ws.km;
       *reinterpret_cast<uint4 *>(&dst[i / 16][8 * (i % 16)]) = pf.ks;
     }
   }
   {
-    constexpr int NVC = Tl::ST * Tl::NGD / 8;
-    const int i = tid & 127;
-    if (i < NVC) {
-      _Float16(*dst)[Tl::ST + 32] = tid < 128 ? sh.st.vs : sh.st.vm;
+    constexpr int NVC = Tl::WT * Tl::NGD / 8;
+    const int i = lane % NVC, stat = lane / NVC;
+    if (stat < 2) {
+      _Float16(*dst)[Tl::VSP] = stat == 0 ? ws.vs : ws.vm;
       const uint32_t w[4] = {pf.vs.x, pf.vs.y, pf.vs.z, pf.vs.w};
       if constexpr (Tl::NGD == 4) {  // tokens 2i, 2i+1 x groups 0..3
 #pragma unroll
@@ -373,6 +391,14 @@ __device__ __forceinline__ void stage_lds(DecShared<BITS, G> &sh, const Prefetch
   }
 }
 
+// Order this wave's LDS writes before its later reads (and reads before
+// later writes) without waiting for the other waves.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Per-lane constants of the compute loop.
 template <int BITS, int G>
 struct LaneConst {
@@ -384,13 +410,12 @@ struct LaneConst {
 };
 
 template <int BITS, int G>
-__device__ __forceinline__ LaneConst<BITS, G> lane_const(int wave, int lane, float scale_log2) {
+__device__ __forceinline__ LaneConst<BITS, G> lane_const(int lane, float scale_log2) {
   using Tl = Tiles<BITS, G>;
   LaneConst<BITS, G> lc;
   const int r = lane & 15, kap = lane >> 4, e = r % Tl::CPB;
   {  // tile i of the wave starts 16 i / TPW word rows after its first tile
-    const int tok = 16 * wave * Tl::TW + r;  // token of row r of the wave's first tile within the super-tile
-    const int j = tok / Tl::TPW, k = (tok % Tl::TPW) / Tl::CPB;
+    const int j = r / Tl::TPW, k = (r % Tl::TPW) / Tl::CPB;  // row r of the wave's first tile
     lc.kaddr = (4 * j + k) * 64 + rot_row(4 * (4 * kap + Tl::NPL * e), k);
     lc.kmask = (Tl::MASK << (BITS * e)) * 0x10001u;
   }
@@ -402,7 +427,7 @@ __device__ __forceinline__ LaneConst<BITS, G> lane_const(int wave, int lane, flo
   {  // channel 16 blk + r: word-in-block r / TPW, byte (r % TPW) / CPB
     const int k = (r % Tl::TPW) / Tl::CPB, hh = r / Tl::TPW;
     lc.vmask = (Tl::MASK << (BITS * e)) * 0x10001u;
-    lc.vaddr = (Tl::HW * k + hh) * Tl::VRK + (wave * Tl::TW / 2) * 128 + rot_row(4 * (4 * kap + Tl::NPL * e), k);
+    lc.vaddr = (Tl::HW * k + hh) * Tl::VRKW + rot_row(4 * (4 * kap + Tl::NPL * e), k);
   }
   return lc;
 }
@@ -437,21 +462,20 @@ __device__ __forceinline__ h8 gather_and(const uint32_t (&piece)[4 / CPB], uint3
 
 // Logits, softmax and P.V of this wave's tiles of the staged super-tile.
 template <int BITS, int G>
-__device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const h8 (&qf)[4],
-                                             const LaneConst<BITS, G> &lc, int wave, int valid_rows,
-                                             float scale_log2, WaveState &st) {
+__device__ __forceinline__ void compute_tile(const WaveStage<BITS, G> &ws, const h8 (&qf)[4],
+                                             const LaneConst<BITS, G> &lc, int valid_rows, float scale_log2,
+                                             WaveState &st) {
   using Tl = Tiles<BITS, G>;
   constexpr int NPL = Tl::NPL, CPB = Tl::CPB;
   const int lane = threadIdx.x & 63, r = lane & 15, kap = lane >> 4;
   constexpr int GT = G / 16;  // tiles per group
-  const int g0 = (16 * wave * Tl::TW) / G;  // first key group of the wave
 
-  // ---- key minimum term of the wave's groups: A row r = minima of group
-  // g0 + r % GW, so element v of every lane holds group v % GW's bias
+  // ---- key minimum term of the wave's groups: A row r = minima of the
+  // wave's group r % GW, so element v of every lane holds group v % GW's bias
   f4 mb = f4{0, 0, 0, 0};
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
-    mb = mfma32(*reinterpret_cast<const h8 *>(&sh.st.km[g0 + r % Tl::GW][32 * kb + 8 * kap]), qf[kb], mb);
+    mb = mfma32(*reinterpret_cast<const h8 *>(&ws.km[r % Tl::GW][32 * kb + 8 * kap]), qf[kb], mb);
 
   // ---- keys: logits of the wave's TW tiles (16 tokens x 16 query rows each)
   f4 acc[Tl::TW];
@@ -459,16 +483,16 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
 #pragma unroll
   for (int i = 0; i < Tl::TW; ++i) {
     if (i % GT == 0) {  // first tile of a group: B' = q * key scale
-      const int g = (16 * (wave * Tl::TW + i)) / G;
+      const int g = ((16 * i) / G) % Tl::GW;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
-        bp[kb] = qf[kb] * *reinterpret_cast<const h8 *>(&sh.st.ks[g][32 * kb + 8 * kap]);
+        bp[kb] = qf[kb] * *reinterpret_cast<const h8 *>(&ws.ks[g][32 * kb + 8 * kap]);
     }
     // NPL pieces of 4 kb each: pairs 16 kb + 4 kap + NPL e + s
     uint32_t pc[NPL][4];
 #pragma unroll
     for (int s = 0; s < NPL; ++s) {
-      const uint4 x = *reinterpret_cast<const uint4 *>(&sh.st.kw[lc.kaddr + (16 * i / Tl::TPW) * 256 + 4 * s]);
+      const uint4 x = *reinterpret_cast<const uint4 *>(&ws.kw[lc.kaddr + (16 * i / Tl::TPW) * 256 + 4 * s]);
       pc[s][0] = x.x; pc[s][1] = x.y; pc[s][2] = x.z; pc[s][3] = x.w;
     }
     f4 a = f4{0, 0, 0, 0};
@@ -490,14 +514,14 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
   // the second, the layout of the two logit accumulators
 #pragma unroll
   for (int kc = 0; kc < Tl::TW / 2; ++kc) {
-    const int ta = wave * Tl::TW + 2 * kc;  // first tile of the block within the super-tile
+    const int ta = 2 * kc;  // first tile of the block within the wave's tokens
     const h4 pa4 = cvt4(acc[2 * kc]), pb4 = cvt4(acc[2 * kc + 1]);
     const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
     {  // A rows g < NGD: the value minima of group g; row NGD: ones (the sum of P)
       h8 am = h8{0, 0, 0, 0, 0, 0, 0, 0};
       if (r < Tl::NGD) {
-        const h4 ma = *reinterpret_cast<const h4 *>(&sh.st.vm[r][16 * ta + 4 * kap]);
-        const h4 mb4 = *reinterpret_cast<const h4 *>(&sh.st.vm[r][16 * ta + 16 + 4 * kap]);
+        const h4 ma = *reinterpret_cast<const h4 *>(&ws.vm[r][16 * ta + 4 * kap]);
+        const h4 mb4 = *reinterpret_cast<const h4 *>(&ws.vm[r][16 * ta + 16 + 4 * kap]);
         am = h8{ma[0], ma[1], ma[2], ma[3], mb4[0], mb4[1], mb4[2], mb4[3]};
       } else if (r == Tl::NGD) {
         am = h8{1, 1, 1, 1, 1, 1, 1, 1};
@@ -510,7 +534,7 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
     for (int s = 0; s < NPL; ++s)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const uint4 x = *reinterpret_cast<const uint4 *>(&sh.st.vw[lc.vaddr + kc * 128 + half * 64 + 4 * s]);
+        const uint4 x = *reinterpret_cast<const uint4 *>(&ws.vw[lc.vaddr + kc * 128 + half * 64 + 4 * s]);
         pv[s][4 * half + 0] = x.x; pv[s][4 * half + 1] = x.y; pv[s][4 * half + 2] = x.z; pv[s][4 * half + 3] = x.w;
       }
     h8 ps;  // P * value scale of the current group, formed at its first block
@@ -518,8 +542,8 @@ __device__ __forceinline__ void compute_tile(const DecShared<BITS, G> &sh, const
     for (int blk = 0; blk < 8; ++blk) {
       if ((16 * blk) % G == 0) {
         const int g = (16 * blk) / G;
-        const h4 sa = *reinterpret_cast<const h4 *>(&sh.st.vs[g][16 * ta + 4 * kap]);
-        const h4 sb = *reinterpret_cast<const h4 *>(&sh.st.vs[g][16 * ta + 16 + 4 * kap]);
+        const h4 sa = *reinterpret_cast<const h4 *>(&ws.vs[g][16 * ta + 4 * kap]);
+        const h4 sb = *reinterpret_cast<const h4 *>(&ws.vs[g][16 * ta + 16 + 4 * kap]);
         ps = p8 * h8{sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
       }
       uint32_t piece[NPL];
@@ -549,27 +573,26 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
   rg.vcode = make_rsrc(static_cast<const char *>(it.value_code) + h * cap * vcode_row, Tq * vcode_row);
   rg.vscale = make_rsrc(static_cast<const char *>(it.value_scale) + h * cap * vstat_row, Tq * vstat_row);
   rg.vmin = make_rsrc(static_cast<const char *>(it.value_min) + h * cap * vstat_row, Tq * vstat_row);
-  const LaneConst<BITS, G> lc = lane_const<BITS, G>(wave, lane, p.scale_log2);
+  const LaneConst<BITS, G> lc = lane_const<BITS, G>(lane, p.scale_log2);
   h8 qf[4];  // this lane's query fragments, for the whole split
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) qf[kb] = query_frag(sq, kb, lane);
-  // super-tiles split, split + S, split + 2S, ... (S = packed splits): the S
-  // splits of a unit run side by side on one XCD and read neighbouring parts
-  // of the same rows at about the same time
+  WaveStage<BITS, G> &ws = sh.st[wave];
+  // super-tiles split, split + S, split + 2S, ... (S = packed splits); wave
+  // w stages and computes tokens WT w .. WT w + WT - 1 of each on its own
   const int64_t n_super = (Tq + Tl::ST - 1) / Tl::ST;
   const int64_t stride = p.splits_packed * Tl::ST;
   const int n_it = static_cast<int>(min<int64_t>(p.nst, (n_super - split + p.splits_packed - 1) / p.splits_packed));
   Prefetch<BITS, G> pf;
-  issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(split * Tl::ST));
+  issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(split * Tl::ST), wave);
   for (int i = 0; i < n_it; ++i) {
     const uint32_t t0 = static_cast<uint32_t>((split + int64_t(i) * p.splits_packed) * Tl::ST);
-    __syncthreads();  // every wave is done reading the previous super-tile from LDS
-    stage_lds<BITS, G>(sh, pf);
-    __syncthreads();
-    if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(t0 + stride));  // lands during compute
-    const int valid = static_cast<int>(min<int64_t>(int64_t(16 * Tl::TW),
-                                                    Tq - t0 - int64_t(16 * Tl::TW) * wave));
-    if (valid > 0) compute_tile<BITS, G>(sh, qf, lc, wave, valid, p.scale_log2, st);
+    wave_lds_sync();  // this wave is done reading its previous super-tile
+    stage_lds<BITS, G>(ws, pf);
+    wave_lds_sync();
+    if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(t0 + stride), wave);  // lands during compute
+    const int valid = static_cast<int>(min<int64_t>(int64_t(Tl::WT), Tq - t0 - int64_t(Tl::WT) * wave));
+    if (valid > 0) compute_tile<BITS, G>(ws, qf, lc, valid, p.scale_log2, st);
   }
   // undo the denormal code scaling 2^(BITS e - 24) of each output channel
   // (channel 16 b + 4 k + v: e depends on k and v only) and add the value
