@@ -133,13 +133,35 @@ def native_pack_layout(tokens: int, heads: int, head_dim: int, k_bits: int, v_bi
 # every tensor (the decode kernels stream it with 16-byte loads) and a flush
 # appends rows in place.  The attention entry points of the library take this
 # layout and the capacity C (uc_kivi_item.packed_capacity).
+_CARVE_ALIGN = 256
+
+
+def _carve(specs, device) -> list[torch.Tensor]:
+    """Tensors of the given (shape, dtype) carved from one allocation, each
+    starting on a 256-byte boundary: one allocator call per cache instead of
+    one per tensor."""
+
+    offsets, total = [], 0
+    for shape, dtype in specs:
+        offsets.append(total)
+        total += -(-math.prod(shape) * dtype.itemsize // _CARVE_ALIGN) * _CARVE_ALIGN
+    buf = torch.empty(max(total, _CARVE_ALIGN), dtype=torch.uint8, device=device)
+    return [buf[off:off + math.prod(shape) * dtype.itemsize].view(dtype).view(shape)
+            for (shape, dtype), off in zip(specs, offsets)]
+
+
+def _native_specs(capacity: int, heads: int, head_dim: int, k_bits: int, v_bits: int, group_size: int):
+    """(shape, dtype) of the token-major storage of the six packed tensors."""
+
+    stats = ((heads, capacity // group_size, head_dim), torch.float16)
+    vstats = ((heads, capacity, head_dim // group_size), torch.float16)
+    return [((heads, capacity * k_bits // 32, head_dim), torch.int32), stats, stats,
+            ((heads, capacity, head_dim * v_bits // 32), torch.int32), vstats, vstats]
+
+
 def _native_storage(capacity: int, heads: int, head_dim: int, k_bits: int, v_bits: int, group_size: int,
                     device) -> tuple[torch.Tensor, ...]:
-    kc = torch.empty((heads, capacity * k_bits // 32, head_dim), dtype=torch.int32, device=device)
-    ks = torch.empty((heads, capacity // group_size, head_dim), dtype=torch.float16, device=device)
-    vc = torch.empty((heads, capacity, head_dim * v_bits // 32), dtype=torch.int32, device=device)
-    vs = torch.empty((heads, capacity, head_dim // group_size), dtype=torch.float16, device=device)
-    return kc, ks, torch.empty_like(ks), vc, vs, torch.empty_like(vs)
+    return tuple(_carve(_native_specs(capacity, heads, head_dim, k_bits, v_bits, group_size), device))
 
 
 def _native_views(storage, tokens: int, k_bits: int, group_size: int) -> tuple[torch.Tensor, ...]:
@@ -312,17 +334,11 @@ class PackedKIVICache:
         quantized = ((tokens - requested_residual) // group_size) * group_size
         q_key, q_value = key[:quantized], value[:quantized]
         kernel_native_layout = bool(backend == "cuda" and quantized and k_bits in {2, 4} and v_bits in {2, 4})
+        if kernel_native_layout:
+            return cls._from_dense_native(key, value, quantized, logical_token_ids, token_type_id, k_bits, v_bits,
+                                          group_size)
         if quantized:
-            if kernel_native_layout:
-                from .kivi_cuda import quantize_kivi_native
-
-                packed = quantize_kivi_native(
-                    q_key, q_value, k_bits=k_bits, v_bits=v_bits, group_size=group_size
-                )
-            else:
-                packed = _pack_reference_layout(
-                    q_key, q_value, k_bits=k_bits, v_bits=v_bits, group_size=group_size
-                )
+            packed = _pack_reference_layout(q_key, q_value, k_bits=k_bits, v_bits=v_bits, group_size=group_size)
             key_code, key_scale, key_minimum, value_code, value_scale, value_minimum = packed
         else:
             nat.require_device(key, value, what="KIVI physical cache")
@@ -349,6 +365,52 @@ class PackedKIVICache:
             backend=str(backend),
             kernel_native_layout=kernel_native_layout,
         )
+
+    @classmethod
+    def _from_dense_native(cls, key, value, quantized, logical_token_ids, token_type_id, k_bits, v_bits,
+                           group_size) -> "PackedKIVICache":
+        """from_dense into the kernel-native layout: the packed storage and the
+        logical ids share one allocation and one HIP pass quantizes and packs;
+        the residual rows are compact clones, as UniCache's are."""
+
+        if key.device.type != "cuda":
+            raise RuntimeError("KIVI native packing requires CUDA tensors")  # kivi_cuda.py:157-190
+        device = nat.require_device(key, value, what="KIVI native packing")
+        if key.dtype != value.dtype:
+            raise ValueError("KIVI packing expects key and value of one dtype")
+        heads, head_dim = int(key.shape[1]), int(key.shape[2])
+        ids = logical_token_ids.detach()
+        ids_here = ids.device == device
+        specs = _native_specs(quantized, heads, head_dim, k_bits, v_bits, group_size)
+        if ids_here:
+            specs.append((tuple(ids.shape), ids.dtype))
+        parts = _carve(specs, device)
+        storage = tuple(parts[:6])
+        _pack_native_into(storage, 0, key[:quantized], value[:quantized], k_bits=k_bits, v_bits=v_bits,
+                          group_size=group_size)
+        # a clone, so a suffix view does not pin the whole dense segment (physical.py:316-319)
+        cache = cls(*_native_views(storage, quantized, k_bits, group_size), key[quantized:].clone(),
+                    value[quantized:].clone(), parts[6].copy_(ids) if ids_here else ids.clone(), int(token_type_id),
+                    int(k_bits), int(v_bits), int(group_size), quantized, head_dim, heads, "cuda", True)
+        cache._store = storage
+        return cache
+
+    def _native_store(self, device) -> tuple[torch.Tensor, ...] | None:
+        """Token-major storage behind the native packed tensors (None without a
+        packed prefix): the one this cache created when its tensors are still
+        views of it, else rebuilt after checking the tensors' layout."""
+
+        if not self.quantized_tokens:
+            return None
+        views = (self.key_code, self.key_scale, self.key_minimum, self.value_code, self.value_scale,
+                 self.value_minimum)
+        store = getattr(self, "_store", None)
+        if (store is not None and all(v.data_ptr() == t.data_ptr() for v, t in zip(views, store))
+                and int(self.key_code.shape[2]) == self.quantized_tokens * self.k_bits // 32
+                and int(self.value_code.shape[1]) == self.quantized_tokens):
+            return store
+        cap = self.native_packed_pointers(device)[-1]
+        return _native_storage_of(views, cap, self.k_bits, self.group_size)
 
     @property
     def token_count(self) -> int:
@@ -556,18 +618,22 @@ class PackedKIVICache:
         if int(logical_token_ids.numel()) != n:
             raise ValueError("KIVI append needs one logical id per appended token")
         tr = self.residual_tokens
-        cap = getattr(self, "_residual_capacity", None)
-        if cap is None or cap[0].shape[0] < tr + n or cap[0].data_ptr() != self.residual_key.data_ptr():
+        # residual K and V rows live in one [2, size, Hkv, D] buffer with room
+        # to grow, so a flush can slide the kept tail of both in one copy
+        buf = getattr(self, "_residual_capacity", None)
+        if (buf is None or int(buf.shape[1]) < tr + n or buf.dtype != key.dtype
+                or (tr and (buf[0].data_ptr() != self.residual_key.data_ptr()
+                            or buf[1].data_ptr() != self.residual_value.data_ptr()))):
             size = max(tr + n, 2 * max(tr, 64))
-            buf_k = torch.empty((size, self.num_kv_heads, self.head_dim), dtype=key.dtype, device=key.device)
-            buf_v = torch.empty_like(buf_k)
-            buf_k[:tr].copy_(self.residual_key)
-            buf_v[:tr].copy_(self.residual_value)
-            cap = (buf_k, buf_v)
-            self._residual_capacity = cap
-        cap[0][tr:tr + n].copy_(key)
-        cap[1][tr:tr + n].copy_(value)
-        self.residual_key, self.residual_value = cap[0][:tr + n], cap[1][:tr + n]
+            new = torch.empty((2, size, self.num_kv_heads, self.head_dim), dtype=key.dtype, device=key.device)
+            if tr:
+                new[0, :tr].copy_(self.residual_key)
+                new[1, :tr].copy_(self.residual_value)
+            buf = new
+            self._residual_capacity = buf
+        buf[0, tr:tr + n].copy_(key)
+        buf[1, tr:tr + n].copy_(value)
+        self.residual_key, self.residual_value = buf[0, :tr + n], buf[1, :tr + n]
         self.logical_token_ids = torch.cat([self.logical_token_ids, logical_token_ids.to(self.logical_token_ids)])
         self._mutated()
         if flush_at is not None and self.residual_tokens >= int(flush_at):
@@ -591,30 +657,35 @@ class PackedKIVICache:
             raise RuntimeError("Streaming KIVI flush requires the kernel-native layout (backend='cuda')")
         device = nat.require_device(self.residual_key, self.residual_value, what="KIVI flush")
         tq, bits, g = self.quantized_tokens, self.k_bits, self.group_size
-        cap = self.packed_capacity
-        old = (self.key_code, self.key_scale, self.key_minimum, self.value_code, self.value_scale,
-               self.value_minimum)
-        if tq:
-            self.native_packed_pointers(device)  # the storage below is only valid for this layout
-        if tq + count <= cap:
-            storage = _native_storage_of(old, cap, bits, g)
-        else:
+        store = self._native_store(device)
+        cap = int(store[3].shape[1]) if store is not None else 0
+        if tq + count > cap:
             # grow geometrically so a run of flushes copies the prefix O(log n) times
             cap = -(-max(tq + count, cap + cap // 2) // g) * g
-            storage = _native_storage(cap, self.num_kv_heads, self.head_dim, bits, bits, g, device)
+            grown = _native_storage(cap, self.num_kv_heads, self.head_dim, bits, bits, g, device)
             if tq:
-                for dst, src in zip(_native_views(storage, tq, bits, g), old):
+                for dst, src in zip(_native_views(grown, tq, bits, g), _native_views(store, tq, bits, g)):
                     dst.copy_(src)
-        _pack_native_into(storage, tq, self.residual_key[:count], self.residual_value[:count], k_bits=bits,
+            store = grown
+        _pack_native_into(store, tq, self.residual_key[:count], self.residual_value[:count], k_bits=bits,
                           v_bits=bits, group_size=g)
         (self.key_code, self.key_scale, self.key_minimum,
-         self.value_code, self.value_scale, self.value_minimum) = _native_views(storage, tq + count, bits, g)
+         self.value_code, self.value_scale, self.value_minimum) = _native_views(store, tq + count, bits, g)
+        self._store = store
         self.quantized_tokens = tq + count
         self.kernel_native_layout = True
-        rest_k = self.residual_key[count:].clone()
-        rest_v = self.residual_value[count:].clone()
-        self.residual_key, self.residual_value = rest_k, rest_v
-        self._residual_capacity = None
+        rest = tr - count
+        buf = getattr(self, "_residual_capacity", None)
+        if (buf is not None and rest <= count and buf[0].data_ptr() == self.residual_key.data_ptr()
+                and buf[1].data_ptr() == self.residual_value.data_ptr()):
+            # the kept tail slides to the front of the buffer (no overlap: rest <= count)
+            if rest:
+                buf[:, :rest].copy_(buf[:, count:tr])
+            self.residual_key, self.residual_value = buf[0, :rest], buf[1, :rest]
+        else:
+            self.residual_key = self.residual_key[count:].clone()
+            self.residual_value = self.residual_value[count:].clone()
+            self._residual_capacity = None
         self._mutated()
         return count
 
