@@ -168,9 +168,14 @@ def _native_views(storage, tokens: int, k_bits: int, group_size: int) -> tuple[t
     """The first `tokens` tokens of token-major storage in the native shapes."""
 
     kc, ks, km, vc, vs, vm = storage
+    heads, d = int(kc.shape[0]), int(kc.shape[2])
     nw, ng = tokens * k_bits // 32, tokens // group_size
-    return (kc[:, :nw].transpose(1, 2), ks[:, :ng].transpose(1, 2), km[:, :ng].transpose(1, 2),
-            vc[:, :tokens], vs[:, :tokens], vm[:, :tokens])
+    kcs, kss = int(kc.stride(0)), int(ks.stride(0))
+    vw, vg = int(vc.shape[2]), int(vs.shape[2])
+    vcs, vss = int(vc.stride(0)), int(vs.stride(0))
+    return (kc.as_strided((heads, d, nw), (kcs, 1, d)), ks.as_strided((heads, d, ng), (kss, 1, d)),
+            km.as_strided((heads, d, ng), (kss, 1, d)), vc.as_strided((heads, tokens, vw), (vcs, vw, 1)),
+            vs.as_strided((heads, tokens, vg), (vss, vg, 1)), vm.as_strided((heads, tokens, vg), (vss, vg, 1)))
 
 
 def _native_storage_of(views, capacity: int, k_bits: int, group_size: int) -> tuple[torch.Tensor, ...]:
@@ -189,15 +194,19 @@ def _native_storage_of(views, capacity: int, k_bits: int, group_size: int) -> tu
 
 
 def _pack_native_into(storage, offset: int, key: torch.Tensor, value: torch.Tensor, *, k_bits: int, v_bits: int,
-                      group_size: int) -> None:
+                      group_size: int, tokens: int | None = None, stream: int | None = None) -> None:
     """HIP quantize+pack of [n, Hkv, D] K/V into tokens offset..offset+n of
-    token-major storage (offset a multiple of group_size)."""
+    token-major storage (offset a multiple of group_size).  `tokens` packs
+    only the first rows of key / value; a caller that has checked the devices
+    passes its `stream`."""
 
-    device = nat.require_device(key, value, storage[0], what="KIVI native packing")
+    if stream is None:
+        stream = nat.stream(nat.require_device(key, value, storage[0], what="KIVI native packing"))
     if key.dtype != value.dtype:
         raise ValueError("KIVI packing expects key and value of one dtype")
     kc, ks, km, vc, vs, vm = storage
-    tokens, heads, head_dim = map(int, key.shape)
+    heads, head_dim = int(key.shape[1]), int(key.shape[2])
+    tokens = int(key.shape[0]) if tokens is None else int(tokens)
     kd = int(kc.shape[2])
     kw0, g0 = offset * k_bits // 32, offset // group_size
     vw, vg = int(vc.shape[2]), int(vs.shape[2])
@@ -210,7 +219,7 @@ def _pack_native_into(storage, offset: int, key: torch.Tensor, value: torch.Tens
         ks.data_ptr() + 2 * g0 * kd, km.data_ptr() + 2 * g0 * kd, int(ks.stride(0)), 1, kd,
         vc.data_ptr() + 4 * offset * vw, int(vc.stride(0)), vw, 1,
         vs.data_ptr() + 2 * offset * vg, vm.data_ptr() + 2 * offset * vg, int(vs.stride(0)), vg, 1,
-        nat.stream(device),
+        stream,
     )
 
 
@@ -411,6 +420,28 @@ class PackedKIVICache:
             return store
         cap = self.native_packed_pointers(device)[-1]
         return _native_storage_of(views, cap, self.k_bits, self.group_size)
+
+    def _residual_slot(self) -> tuple[torch.Tensor | None, int]:
+        """(buffer, first row) of the residual inside this cache's [2, size,
+        Hkv, D] residual buffer, or (None, 0) when the residual lives elsewhere."""
+
+        buf = getattr(self, "_residual_capacity", None)
+        if buf is None or self.residual_key.dtype != buf.dtype:
+            return None, 0
+        row = self.num_kv_heads * self.head_dim * buf.element_size()
+        size, tr = int(buf.shape[1]), self.residual_tokens
+        off, rem = divmod(self.residual_key.data_ptr() - buf.data_ptr(), row)
+        if (rem or not 0 <= off <= size - tr or not self.residual_key.is_contiguous()
+                or self.residual_value.data_ptr() != self.residual_key.data_ptr() + size * row):
+            return None, 0
+        return buf, off
+
+    def _set_residual(self, buf: torch.Tensor, off: int, tokens: int) -> None:
+        hd = self.num_kv_heads * self.head_dim
+        shape, stride = (tokens, self.num_kv_heads, self.head_dim), (hd, self.head_dim, 1)
+        base = buf.storage_offset() + off * hd
+        self.residual_key = buf.as_strided(shape, stride, base)
+        self.residual_value = buf.as_strided(shape, stride, base + int(buf.shape[1]) * hd)
 
     @property
     def token_count(self) -> int:
@@ -618,22 +649,26 @@ class PackedKIVICache:
         if int(logical_token_ids.numel()) != n:
             raise ValueError("KIVI append needs one logical id per appended token")
         tr = self.residual_tokens
-        # residual K and V rows live in one [2, size, Hkv, D] buffer with room
-        # to grow, so a flush can slide the kept tail of both in one copy
-        buf = getattr(self, "_residual_capacity", None)
-        if (buf is None or int(buf.shape[1]) < tr + n or buf.dtype != key.dtype
-                or (tr and (buf[0].data_ptr() != self.residual_key.data_ptr()
-                            or buf[1].data_ptr() != self.residual_value.data_ptr()))):
-            size = max(tr + n, 2 * max(tr, 64))
+        # residual K and V rows live at one offset of a [2, size, Hkv, D]
+        # buffer: appends write after them, a flush advances the offset, and
+        # the rows slide back to the front only when the end is reached
+        buf, off = self._residual_slot()
+        if buf is None or buf.dtype != key.dtype or int(buf.shape[1]) < tr + n:
+            size = max(4 * (tr + n), 256)
             new = torch.empty((2, size, self.num_kv_heads, self.head_dim), dtype=key.dtype, device=key.device)
             if tr:
                 new[0, :tr].copy_(self.residual_key)
                 new[1, :tr].copy_(self.residual_value)
-            buf = new
+            buf, off = new, 0
             self._residual_capacity = buf
-        buf[0, tr:tr + n].copy_(key)
-        buf[1, tr:tr + n].copy_(value)
-        self.residual_key, self.residual_value = buf[0, :tr + n], buf[1, :tr + n]
+        elif off + tr + n > int(buf.shape[1]):
+            if tr:
+                tail = buf[:, off:off + tr]
+                buf[:, :tr].copy_(tail if off >= tr else tail.clone())
+            off = 0
+        buf[0, off + tr:off + tr + n].copy_(key)
+        buf[1, off + tr:off + tr + n].copy_(value)
+        self._set_residual(buf, off, tr + n)
         self.logical_token_ids = torch.cat([self.logical_token_ids, logical_token_ids.to(self.logical_token_ids)])
         self._mutated()
         if flush_at is not None and self.residual_tokens >= int(flush_at):
@@ -656,6 +691,7 @@ class PackedKIVICache:
         if self.backend != "cuda" or (self.quantized_tokens and not self.kernel_native_layout):
             raise RuntimeError("Streaming KIVI flush requires the kernel-native layout (backend='cuda')")
         device = nat.require_device(self.residual_key, self.residual_value, what="KIVI flush")
+        stream = nat.stream(device)
         tq, bits, g = self.quantized_tokens, self.k_bits, self.group_size
         store = self._native_store(device)
         cap = int(store[3].shape[1]) if store is not None else 0
@@ -667,25 +703,19 @@ class PackedKIVICache:
                 for dst, src in zip(_native_views(grown, tq, bits, g), _native_views(store, tq, bits, g)):
                     dst.copy_(src)
             store = grown
-        _pack_native_into(store, tq, self.residual_key[:count], self.residual_value[:count], k_bits=bits,
-                          v_bits=bits, group_size=g)
+        _pack_native_into(store, tq, self.residual_key, self.residual_value, k_bits=bits, v_bits=bits, group_size=g,
+                          tokens=count, stream=stream)
         (self.key_code, self.key_scale, self.key_minimum,
          self.value_code, self.value_scale, self.value_minimum) = _native_views(store, tq + count, bits, g)
         self._store = store
         self.quantized_tokens = tq + count
         self.kernel_native_layout = True
-        rest = tr - count
-        buf = getattr(self, "_residual_capacity", None)
-        if (buf is not None and rest <= count and buf[0].data_ptr() == self.residual_key.data_ptr()
-                and buf[1].data_ptr() == self.residual_value.data_ptr()):
-            # the kept tail slides to the front of the buffer (no overlap: rest <= count)
-            if rest:
-                buf[:, :rest].copy_(buf[:, count:tr])
-            self.residual_key, self.residual_value = buf[0, :rest], buf[1, :rest]
+        buf, off = self._residual_slot()
+        if buf is not None:  # the kept tail stays where it is
+            self._set_residual(buf, off + count, tr - count)
         else:
             self.residual_key = self.residual_key[count:].clone()
             self.residual_value = self.residual_value[count:].clone()
-            self._residual_capacity = None
         self._mutated()
         return count
 
