@@ -452,41 +452,142 @@ def secondary_rows(device, steps):
     return rows
 
 
-def cpu_baseline(algorithmic_bytes_per_seq_layer, budget_s=12.0):
-    """The numpy oracle's decode (dequantize + fp64 attention) on one layer of
-    the workload, sequences processed until ~budget_s of CPU time."""
+def _host_cores():
+    """(threads, CPU model): the cores this process may use (affinity and a
+    cgroup CPU quota both bound it) and /proc/cpuinfo's model name."""
 
-    import numpy as np
-    from threadpoolctl import threadpool_limits
-
-    from oracle import attention as A
-    from oracle import kivi as K
-
-    g = torch.Generator().manual_seed(0)
-    key = torch.randn(TOKENS, HKV, D, generator=g)
-    value = torch.randn(TOKENS, HKV, D, generator=g)
-    for h in range(HKV):
-        key[:, h, torch.randperm(D, generator=g)[:8]] *= 10.0
-    kb = key.to(torch.bfloat16).float().numpy()
-    vb = value.to(torch.bfloat16).float().numpy()
-    seg = K.from_dense(kb, vb, k_bits=BITS, v_bits=BITS, group_size=GROUP, residual_length=RESIDUAL)
-    q = torch.randn(1, HQ, D, generator=g).to(torch.bfloat16).float().numpy()
-    done, t0 = 0, time.perf_counter()
-    with threadpool_limits(limits=1):
-        while True:
-            A.packed_summary(seg, q, include_residual=True, kv_dtype="bf16")
-            done += 1
-            if time.perf_counter() - t0 >= budget_s or done >= 64:
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) / int(period))))
+    except (OSError, ValueError):
+        pass
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
                 break
-    elapsed = time.perf_counter() - t0
+    except OSError:
+        pass
+    return n, model
+
+
+def _median_ms(fn, runs=5):
+    fn()  # warm-up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return sorted(times)[len(times) // 2]
+
+
+def cpu_baseline(c1_layer_bytes, c4_layer_bytes):
+    """the torch-CPU restatement of the path
+    (oracle/torch_cpu.py) timed on this host's cores, 1 warm-up and the
+    median of 5 runs per row, at each configuration's shapes.  Whole-step
+    figures for 28 layers are per-layer times x 28 (marked extrapolated)."""
+
+    from oracle import torch_cpu as T
+
+    threads, model = _host_cores()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+
+    def kv(tokens):
+        key = torch.randn(tokens, HKV, D, generator=g)
+        for h in range(HKV):
+            key[:, h, torch.randperm(D, generator=g)[:8]] *= 10.0
+        return key.to(torch.bfloat16), torch.randn(tokens, HKV, D, generator=g).to(torch.bfloat16)
+
+    def q(lq):
+        return torch.randn(lq, HQ, D, generator=g).to(torch.bfloat16)
+
+    rows = {}
+    try:
+        # C0: pack 2048 tokens (R=128), then one decode over packed + residual
+        k0, v0 = kv(2048)
+        rows["c0_pack_ms"] = _median_ms(lambda: T.from_dense(k0, v0, bits=BITS, group_size=GROUP,
+                                                             residual_length=RESIDUAL))
+        s0, q0 = T.from_dense(k0, v0, bits=BITS, group_size=GROUP, residual_length=RESIDUAL), q(1)
+        rows["c0_decode_ms"] = _median_ms(lambda: T.packed_decode(s0, q0))
+        # C1: one layer = 8 sequences of 8064 packed + 128 residual tokens, Lq=1
+        segs = [T.from_dense(*kv(TOKENS), bits=BITS, group_size=GROUP, residual_length=RESIDUAL)
+                for _ in range(BATCH)]
+        qs = [q(1) for _ in range(BATCH)]
+        c1 = _median_ms(lambda: [T.packed_decode(s, x) for s, x in zip(segs, qs)])
+        rows["c1_layer_ms"] = c1
+        rows["c1_all_layers_ms_extrapolated"] = c1 * LAYERS
+        rows["c1_gbs"] = c1_layer_bytes / (c1 * 1e-3) / 1e9
+        del segs
+        # C2: one layer of the editing pass, 1088 queries over the 2-bit VAE
+        # segment (896 packed + 128 residual) and 1280 bf16 tokens
+        s2 = T.from_dense(*kv(1024), bits=BITS, group_size=GROUP, residual_length=RESIDUAL)
+        dk, dv = kv(1280)
+        q2 = q(1088)
+
+        def editing():
+            pk, pv = T.dequantize(s2)
+            return T.attention_summary(q2, torch.cat([dk, pk]), torch.cat([dv, pv]))
+
+        c2 = _median_ms(editing)
+        rows["c2_layer_ms"] = c2
+        rows["c2_all_layers_ms_extrapolated"] = c2 * LAYERS
+        rows["c2_gflops"] = 4 * 1088 * HQ * 2304 * D / (c2 * 1e-3) / 1e9
+        # C3: H2O scores of 512 queries over 4096 keys; top-k + gather of the
+        # instruction (256 -> 51) and ViT (3840 -> 768) history at 20 %
+        k3, v3 = kv(4096)
+        q3 = q(512)
+        rows["c3_scores_ms"] = _median_ms(lambda: T.h2o_scores(q3, k3))
+        sc = T.h2o_scores(q3, k3)
+
+        def select_gather():
+            for lo, hi in ((0, 256), (256, 4096)):
+                n = hi - lo
+                target = max(1, int(round(n * 0.2)))
+                recent = int(round(target * 0.25))
+                T.h2o_select_gather(sc[:, lo:hi], k3[lo:hi], v3[lo:hi], heavy_k=target - recent, recent=recent)
+
+        rows["c3_topk_gather_ms"] = _median_ms(select_gather)
+        # C4: 64 decode steps of one layer over the VAE segment (20224 packed
+        # + 128 residual) and 2585 dense tokens, each appending one token to
+        # the residual; after step 32 one 128-token flush packs its head
+        s4 = T.from_dense(*kv(20352), bits=BITS, group_size=GROUP, residual_length=RESIDUAL)
+        dk4, dv4 = kv(2585)
+        nk, nv = kv(64)
+        q4 = q(1)
+
+        def steps64():
+            seg = dict(s4)
+            for t in range(64):
+                pk, pv = T.dequantize(seg)
+                T.attention_summary(q4, torch.cat([pk, dk4]), torch.cat([pv, dv4]))
+                seg["residual_key"] = torch.cat([seg["residual_key"], nk[t:t + 1]])
+                seg["residual_value"] = torch.cat([seg["residual_value"], nv[t:t + 1]])
+                if t == 31:
+                    seg = T.flush(seg, 128)
+
+        c4 = _median_ms(steps64) / 64
+        rows["c4_step_layer_ms"] = c4
+        rows["c4_step_all_layers_ms_extrapolated"] = c4 * LAYERS
+        rows["c4_gbs"] = c4_layer_bytes / (c4 * 1e-3) / 1e9
+    finally:
+        torch.set_num_threads(prev)
+    rows = {k: round(v, 4) for k, v in rows.items()}
     return {
-        "value": round(done * algorithmic_bytes_per_seq_layer / elapsed / 1e9, 4),
+        "value": rows["c1_gbs"],
         "unit": "GB/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"{done} sequence-layers of the config-1 decode (8064 packed 2-bit + 128 bf16 tokens, "
-                  f"GQA 28/4) through oracle.kivi.dequantize + oracle.attention, numpy, BLAS limited to 1 "
-                  f"thread, {elapsed:.1f} s",
+        "cpu_model": model,
+        "sample": "oracle/torch_cpu.py (torch-CPU restatement: dequantize + fp32 GQA attention with bf16 "
+                  "probabilities) on one config-1 layer (8 sequences x 8064 packed 2-bit + 128 bf16 tokens, "
+                  f"Lq=1), {threads} threads, median of 5 after 1 warm-up; value = the layer's algorithmic "
+                  "bytes / its time.  rows: C0-C4 at their shapes, 28-layer figures extrapolated x28",
+        "rows": rows,
     }
 
 
@@ -579,7 +680,8 @@ def main():
     torch.cuda.empty_cache()
     result["rows"] = secondary_rows(device, max(5, args.steps // 5))
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(seq_layer_bytes)
+        result["cpu_baseline"] = cpu_baseline(seq_layer_bytes * BATCH,
+                                              result["mixed_decode_c4"]["bytes_per_step"] // LAYERS)
     print(json.dumps(result))
 
 
