@@ -380,6 +380,21 @@ int uc_gqa_gather(const void *key, const void *value, int64_t k_st, int64_t k_sh
                   uc_stream_t stream);
 
 /*
+ * uc_h2o_select followed by uc_gqa_gather in one call: selects into
+ * `indices` (int64 [Hkv, heavy_k + recent], caller-owned) and gathers K, V,
+ * ids and scores through them.  Scores must be the [Hkv, tokens] fp32 rows
+ * that are also gathered (strides s_sh, s_st).  Same results as the two calls.
+ * Replaces: the whole selection + gather of GQAH2OCache.from_dense
+ * (physical.py:511-546) in one host round trip.
+ */
+int uc_h2o_select_gather(const void *key, const void *value, int64_t k_st, int64_t k_sh, int64_t k_sd,
+                         int dtype, int64_t heads_kv, int64_t tokens, int64_t head_dim,
+                         const float *scores, int64_t s_sh, int64_t s_st, int64_t heavy_k, int64_t recent,
+                         const int64_t *ids, int64_t ids_sh, int64_t ids_st, int64_t *indices,
+                         void *out_key, void *out_value, int64_t *out_ids, float *out_scores,
+                         uc_stream_t stream);
+
+/*
  * uc_h2o_scores with the softmax normaliser given instead of computed:
  *   P = bf16(exp(sm_scale * q_i . k_t - lse[h, i]))
  * lse is fp32 [Hq, Lq] (natural log), e.g. the global LSE of a mixed-segment

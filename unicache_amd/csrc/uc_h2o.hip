@@ -539,3 +539,16 @@ extern "C" int uc_gqa_gather(const void *key, const void *value, int64_t k_st, i
     hipLaunchKernelGGL((gqa_gather_kernel<uint16_t>), dim3(blocks), dim3(256), 0, s, a);
   return check_launch("uc_gqa_gather");
 }
+
+extern "C" int uc_h2o_select_gather(const void *key, const void *value, int64_t k_st, int64_t k_sh, int64_t k_sd,
+                                    int dtype, int64_t heads_kv, int64_t tokens, int64_t head_dim,
+                                    const float *scores, int64_t s_sh, int64_t s_st, int64_t heavy_k,
+                                    int64_t recent, const int64_t *ids, int64_t ids_sh, int64_t ids_st,
+                                    int64_t *indices, void *out_key, void *out_value, int64_t *out_ids,
+                                    float *out_scores, uc_stream_t stream) {
+  UC_REQUIRE(scores != nullptr && indices != nullptr, "uc_h2o_select_gather: scores and indices are required");
+  int rc = uc_h2o_select(scores, s_sh, s_st, heads_kv, tokens, heavy_k, recent, indices, stream);
+  if (rc != UC_OK) return rc;
+  return uc_gqa_gather(key, value, k_st, k_sh, k_sd, dtype, heads_kv, head_dim, indices, heavy_k + recent, ids,
+                       ids_sh, ids_st, scores, s_sh, s_st, out_key, out_value, out_ids, out_scores, stream);
+}

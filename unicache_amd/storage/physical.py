@@ -821,15 +821,28 @@ class GQAH2OCache:
         heavy = target - recent
         history_end = tokens - recent
         heavy_k = min(heavy, history_end)
-        scores = per_kv_head_scores.to(device=key.device)
-        indexes = h2o_select_indices(scores, heavy_k=heavy_k, recent=recent)
         logical = logical_token_ids.to(device=key.device)
         if logical.dim() != 1:
             raise ValueError("Physical H2O logical_token_ids must be [segment_tokens]")
-        out_key, out_value, out_ids, out_scores = _gather(
-            key, value, key.stride(), indexes, logical, (0, logical.stride(0)), scores,
-            heads=kv_heads, head_dim=head_dim,
+        device = nat.require_device(key, value, logical, what="GQA compaction")
+        scores = per_kv_head_scores.to(device=device)
+        if scores.dtype != torch.float32:
+            scores = scores.float()
+        ids64 = logical if logical.dtype == torch.int64 else logical.to(torch.int64)
+        # selection and gather in one call, into one allocation
+        retained = heavy_k + recent
+        index, out_key, out_value, out_ids, out_scores = _carve(
+            [((kv_heads, retained), torch.int64), ((kv_heads, retained, head_dim), key.dtype),
+             ((kv_heads, retained, head_dim), key.dtype), ((kv_heads, retained), torch.int64),
+             ((kv_heads, retained), torch.float32)], device)
+        nat.call(
+            "uc_h2o_select_gather", key.data_ptr(), value.data_ptr(), *map(int, key.stride()),
+            nat.dtype_code(key.dtype), kv_heads, tokens, head_dim, scores.data_ptr(), *map(int, scores.stride()),
+            heavy_k, recent, ids64.data_ptr(), 0, int(ids64.stride(0)), index.data_ptr(), out_key.data_ptr(),
+            out_value.data_ptr(), out_ids.data_ptr(), out_scores.data_ptr(), nat.stream(device),
         )
+        if logical.dtype != torch.int64:
+            out_ids = out_ids.to(logical.dtype)
         return cls(
             key=out_key,
             value=out_value,
