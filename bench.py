@@ -36,7 +36,7 @@ BITS, GROUP, RESIDUAL = 2, 32, 128
 # HBM bytes per step of the default workload from rocprofv3 PMC passes
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 over both decode kernels, the factors
 # from a 1 GiB device copy); profiles/decode_batch_c1.md has the commands.
-MEASURED_TRAFFIC_BYTES = 949_532_262
+MEASURED_TRAFFIC_BYTES = 784_447_898
 
 
 def make_kv(tokens, *, seed, device, heads=HKV, head_dim=D):
@@ -641,6 +641,8 @@ def main():
     parser.add_argument("--layers", type=int, default=LAYERS)
     parser.add_argument("--calibrate-copy", action="store_true",
                         help="only run a 1 GiB device copy (PMC traffic calibration)")
+    parser.add_argument("--only-decode", action="store_true",
+                        help="only build the config-1 workload and run its decode step (for counter passes)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decode hot path shards by sequence / KV head with no "
@@ -664,6 +666,10 @@ def main():
     sid = stream.cuda_stream
     run = lambda: batch.run(sid)  # noqa: E731
     ms = time_steps(run, args.steps, args.warmup, stream)
+    if args.only_decode:
+        print(json.dumps({"config1_decode_ms": round(ms, 5),
+                          "gbs": round(batch.algorithmic_bytes / (ms * 1e-3) / 1e9, 2)}))
+        return
     step_bytes = batch.algorithmic_bytes
     value = step_bytes / (ms * 1e-3) / 1e9
 
