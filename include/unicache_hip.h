@@ -431,6 +431,16 @@ int uc_compact_rows(const void *src, int64_t src_row_stride_bytes, int64_t row_b
                     const int32_t *dst_index, int64_t n, void *dst, uc_stream_t stream);
 
 /*
+ * The inverse of uc_compact_rows: for every t with dst_index[t] >= 0, the
+ * compact row dst_index[t] of src (row_bytes each) is copied to out + t *
+ * out_row_stride_bytes; other rows of out are left as they are.
+ * Replaces: the masked write-back k_out[quant_mask] = fake_quant(...) of the
+ * KIVI fake-quant operator (operators/builtin.py:420-430).
+ */
+int uc_scatter_rows(const void *src, int64_t row_bytes, const int32_t *dst_index, int64_t n, void *out,
+                    int64_t out_row_stride_bytes, uc_stream_t stream);
+
+/*
  * Bytes of caller-provided workspace an operation needs.
  *   UC_OP_KIVI_AV:     (1, heads_q, query_len, head_dim, total_tokens)
  *                      = max(4 Hq Lq S (D + 2), Hq Lq >= 64 ? 2 Hq D ceil64(T) : 0),

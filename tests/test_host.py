@@ -144,3 +144,16 @@ def test_token_major_layout_is_enforced():
     c.kernel_native_layout = False
     with pytest.raises(RuntimeError, match="kernel-native"):
         c.native_packed_pointers()
+
+
+def test_fake_quant_operator_params():
+    from unicache_amd.operators import KIVIQuantizationOperator
+
+    op = KIVIQuantizationOperator()
+    assert op.build_params({"bits": 2})["working_set_mode"] == "attention_view"
+    with pytest.raises(ValueError, match="k_bits=5 is unsupported"):
+        op.build_params({"bits": 4, "k_bits": 5})
+    with pytest.raises(ValueError, match="working_set_mode must be"):
+        op.build_params({"working_set_mode": "disk"})
+    with pytest.raises(ValueError, match="host_backed"):
+        op.build_params({"working_set_mode": "host_backed"})

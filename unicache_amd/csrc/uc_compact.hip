@@ -85,6 +85,31 @@ __global__ __launch_bounds__(256) void compact_rows_kernel(const char *src, int6
   *reinterpret_cast<V *>(dst + int64_t(d) * row_bytes + c * int64_t(sizeof(V))) = v;
 }
 
+// The inverse copy: compact row dst_index[t] back to row t of a strided array.
+template <typename V>
+__global__ __launch_bounds__(256) void scatter_rows_kernel(const char *src, int64_t row_bytes,
+                                                           const int32_t *dst_index, int64_t n, char *out,
+                                                           int64_t out_stride, int64_t per_row) {
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t t = idx / per_row, c = idx % per_row;
+  if (t >= n) return;
+  const int32_t d = dst_index[t];
+  if (d < 0) return;
+  const V v = *reinterpret_cast<const V *>(src + int64_t(d) * row_bytes + c * int64_t(sizeof(V)));
+  *reinterpret_cast<V *>(out + t * out_stride + c * int64_t(sizeof(V))) = v;
+}
+
+template <typename V>
+int launch_scatter(const void *src, int64_t row_bytes, const int32_t *dst_index, int64_t n, void *out,
+                   int64_t out_stride, hipStream_t s) {
+  const int64_t per_row = row_bytes / int64_t(sizeof(V));
+  const int64_t threads = n * per_row;
+  hipLaunchKernelGGL(scatter_rows_kernel<V>, dim3(static_cast<unsigned>(ceil_div(threads, int64_t(256)))), dim3(256),
+                     0, s, static_cast<const char *>(src), row_bytes, dst_index, n, static_cast<char *>(out),
+                     out_stride, per_row);
+  return check_launch("uc_scatter_rows");
+}
+
 template <typename V>
 int launch_compact(const void *src, int64_t src_stride, int64_t row_bytes, const int32_t *dst_index, int64_t n,
                    void *dst, hipStream_t s) {
@@ -128,4 +153,20 @@ extern "C" int uc_compact_rows(const void *src, int64_t src_row_stride_bytes, in
   if ((align & 3) == 0) return launch_compact<uint32_t>(src, src_row_stride_bytes, row_bytes, dst_index, n, dst, s);
   if ((align & 1) == 0) return launch_compact<uint16_t>(src, src_row_stride_bytes, row_bytes, dst_index, n, dst, s);
   return launch_compact<uint8_t>(src, src_row_stride_bytes, row_bytes, dst_index, n, dst, s);
+}
+
+extern "C" int uc_scatter_rows(const void *src, int64_t row_bytes, const int32_t *dst_index, int64_t n, void *out,
+                               int64_t out_row_stride_bytes, uc_stream_t stream) {
+  clear_error();
+  UC_REQUIRE(n >= 0 && row_bytes >= 0 && out_row_stride_bytes >= row_bytes, "uc_scatter_rows: bad shape");
+  if (n == 0 || row_bytes == 0) return UC_OK;
+  UC_REQUIRE(src != nullptr && out != nullptr && dst_index != nullptr, "uc_scatter_rows: null pointer");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(out) |
+                          static_cast<uintptr_t>(out_row_stride_bytes) | static_cast<uintptr_t>(row_bytes);
+  const hipStream_t s = as_stream(stream);
+  if ((align & 15) == 0) return launch_scatter<uint4>(src, row_bytes, dst_index, n, out, out_row_stride_bytes, s);
+  if ((align & 7) == 0) return launch_scatter<uint2>(src, row_bytes, dst_index, n, out, out_row_stride_bytes, s);
+  if ((align & 3) == 0) return launch_scatter<uint32_t>(src, row_bytes, dst_index, n, out, out_row_stride_bytes, s);
+  if ((align & 1) == 0) return launch_scatter<uint16_t>(src, row_bytes, dst_index, n, out, out_row_stride_bytes, s);
+  return launch_scatter<uint8_t>(src, row_bytes, dst_index, n, out, out_row_stride_bytes, s);
 }

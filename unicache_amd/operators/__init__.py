@@ -1,6 +1,6 @@
 """Physical-cache operators of the UniCache engine on MI355X."""
 
-from .builtin import asymmetric_fake_quant, kivi_fake_quant_key, kivi_fake_quant_value
+from .builtin import KIVIQuantizationOperator, asymmetric_fake_quant, kivi_fake_quant_key, kivi_fake_quant_value
 from .physical import (
     H2OPhysicalGQAOperator,
     KIVIPackedQuantizationOperator,
@@ -11,6 +11,7 @@ from .physical import (
 __all__ = [
     "H2OPhysicalGQAOperator",
     "KIVIPackedQuantizationOperator",
+    "KIVIQuantizationOperator",
     "asymmetric_fake_quant",
     "kivi_fake_quant_key",
     "kivi_fake_quant_value",
