@@ -389,6 +389,33 @@ def secondary_rows(device, steps):
             f"{label}: kivi_fake_quant_key + kivi_fake_quant_value on [{tokens}, 4, 128] bf16, 2-bit, G=32",
             ms, 2 * 2 * k.numel() * 2)
 
+    # the fake-quant segment operator (operators/builtin.py:281-476) at config 0:
+    # a 2048-token segment, the last 128 tokens and 16 protected ones kept
+    from types import SimpleNamespace
+
+    from unicache_amd.core.registry import OperatorExecutionContext
+    from unicache_amd.operators import KIVIQuantizationOperator
+
+    k0, v0 = make_kv(2048, seed=21900, device=device)
+    seg = torch.ones(2048, dtype=torch.bool, device=device)
+    prot = torch.zeros(2048, dtype=torch.bool, device=device)
+    prot[:16] = True
+    op = KIVIQuantizationOperator()
+    params = op.build_params({"bits": BITS, "group_size": GROUP, "residual_length": RESIDUAL})
+
+    def fq_operator():
+        ctx = OperatorExecutionContext(runtime=SimpleNamespace(kv_metadata={}), step=SimpleNamespace(segment_id=0),
+                                       params=params, q=None, k=k0, v=v0, attn_mask=None, key_type_ids=None,
+                                       segment_mask=seg, protected_mask=prot, state={}, record=lambda r: None,
+                                       set_storage_snapshot=lambda r: None, storage_num_kv_heads=HKV)
+        return op.execute(ctx)
+
+    ms = time_steps(fq_operator, steps, 2, stream)
+    rows["fake_quant_operator_c0"] = _hbm_line(
+        "config 0: KIVIQuantizationOperator.execute on a 2048-token segment (last 128 and 16 protected tokens "
+        "kept), 2-bit, G=32: masks, row gather, fake quant, write-back into copies of K and V",
+        ms, 2 * (2048 * HKV * D * 2 * 2 + 1904 * HKV * D * 2 * 2))
+
     # native pack (kivi_cuda.py:157-190) of a 32k-token K/V in one call
     from unicache_amd.storage.kivi_cuda import quantize_kivi_native
 
