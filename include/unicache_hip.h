@@ -273,11 +273,14 @@ int uc_kivi_attn_decode_segments(const uc_kivi_item *items_device, int64_t n_ite
  * Attention for long queries (image editing: group*query_len rows per KV head
  * in the thousands) over one packed segment plus residual: same inputs,
  * outputs and semantics as uc_kivi_attn_decode.  head_dim 128, bits 2/4,
- * group_size 32/64/128, q and residual bf16/fp16.  A first kernel dequantizes
- * the packed keys/values of every KV head once into `workspace` (fp16 keys and
- * transposed values, uc_kivi_mq_workspace_bytes bytes); a second streams them
- * in 64-key tiles through LDS for MFMA, 128 query rows per workgroup.  Operands
- * are fp16: query, residual and dequantized values must stay below 65504 in magnitude.
+ * group_size 32/64/128, q and residual bf16/fp16, sm_scale > 0; the residual
+ * (the dense keys) must be 16-byte aligned.  A first kernel dequantizes the
+ * packed prefix of every KV head once into `workspace` (fp16 key and value
+ * rows, uc_kivi_mq_workspace_bytes bytes); a second streams 64-key tiles of
+ * that prefix and of the residual, read where it lies, through LDS for MFMA,
+ * 128 query rows per workgroup.  Prefix tiles take fp16 operands (the query
+ * and the dequantized values must stay below 65504 in magnitude); residual
+ * tiles take the residual's dtype (bf16 keeps its range).
  * Replaces: _packed_attention_kernel / packed_attention_tiled
  * (kivi_triton.py:216-382, 615-687) behind packed_kivi_quantized_attention_summary
  * (kivi_cuda.py:96-120) with backend "triton_tiled", plus the residual part.
@@ -287,7 +290,7 @@ int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int group_size,
                     int q_dtype, int res_dtype, int out_dtype, float sm_scale,
                     void *workspace, int64_t workspace_bytes, uc_stream_t stream);
 
-/* Workspace of uc_kivi_attn_mq: heads_kv * ceil((Tq+Tr)/64)*64 * head_dim * 4 bytes. */
+/* Workspace of uc_kivi_attn_mq: 2 * heads_kv * Tq * head_dim * 2 bytes (0 when Tq == 0). */
 int64_t uc_kivi_mq_workspace_bytes(int64_t heads_kv, int64_t head_dim, int64_t quantized_tokens,
                                    int64_t residual_tokens);
 

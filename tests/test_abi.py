@@ -105,15 +105,27 @@ def test_editing_validation():
         nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, 28, 3, 128, 512, nat.UC_BF16, nat.UC_BF16,
                  nat.UC_BF16, 0.1, None, 0, None)
     # the workspace check comes after every pointer check; the pointers are
-    # never dereferenced on the host, so aligned placeholders reach it
-    item.quantized_tokens = 0
+    # never dereferenced on the host, so aligned placeholders reach it.  The
+    # workspace holds the staged prefix only: 2 * Hkv * Tq * 128 fp16
+    assert nat.mq_workspace_bytes(4, 128, 64, 128) == 2 * 4 * 64 * 128 * 2
+    assert nat.mq_workspace_bytes(4, 128, 0, 128) == 0
     item.residual_tokens = 128
-    item.query = item.out = item.residual_key = item.residual_value = 0x1000
+    for name in ("query", "out", "residual_key", "residual_value", "key_code", "key_scale", "key_min",
+                 "value_code", "value_scale", "value_min"):
+        setattr(item, name, 0x1000)
     with pytest.raises(ValueError, match="workspace too small"):
         nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, *args)
     item.out = 0x1008
     with pytest.raises(ValueError, match="16-byte aligned"):
         nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, *args)
+    item.out = 0x1000
+    item.residual_value = 0x1004
+    with pytest.raises(ValueError, match="residual keys and values must be 16-byte aligned"):
+        nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, *args)
+    item.residual_value = 0x1000
+    with pytest.raises(ValueError, match="sm_scale must be positive"):
+        nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, 28, 4, 128, 512, nat.UC_BF16, nat.UC_BF16,
+                 nat.UC_BF16, 0.0, None, 0, None)
 
 
 def test_merge_and_fake_quant_validation():
@@ -148,7 +160,10 @@ def test_editing_batch_validation():
     # aligned placeholders (never dereferenced on the host) reach the workspace check
     for it in items[:2]:
         it.residual_tokens = 100
-        it.query = it.out = it.residual_key = it.residual_value = 0x1000
+        it.quantized_tokens = 64
+        for name in ("query", "out", "residual_key", "residual_value", "key_code", "key_scale", "key_min",
+                     "value_code", "value_scale", "value_min"):
+            setattr(it, name, 0x1000)
     with pytest.raises(ValueError, match="workspace too small"):
         nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)
     lens[1] = 0
