@@ -188,43 +188,65 @@ __device__ __forceinline__ void mq_stage_body(const uc_kivi_item &it, const Stag
   uint32_t *wk = reinterpret_cast<uint32_t *>(sp.wk + h * Tq * kD);
   _Float16 *wv = sp.wv + h * Tq * kD;
 
+  // Every load of the thread is issued before any arithmetic: the packed
+  // words are cold in HBM and each thread has only a few of them.
   // keys: item (word j of the tile, channel pair cp); a wave writes whole
   // 256-byte rows, one per token of the word
-  for (int e = tid; e < KW * (kD / 2); e += kStageSplit * kStageThreads) {
-    const int cp = e % (kD / 2), j = e / (kD / 2);
-    const int64_t t = t0 + j * TPW;  // first token of the word (Tq is a multiple of G >= TPW)
-    if (t >= Tq) continue;
+  constexpr int kItems = kStageSplit * kStageThreads;
+  constexpr int NK = KW * (kD / 2) / kItems, NV = kTile * VW / kItems;
+  static_assert(NK >= 1 && NV >= 1 && KW * (kD / 2) % kItems == 0 && kTile * VW % kItems == 0, "stage items");
+  uint2 kw[NK];
+  uint32_t ks2[NK], km2[NK], vw[NV];
+  uint16_t vs1[NV], vm1[NV];
+#pragma unroll
+  for (int q = 0; q < NK; ++q) {
+    const int e = q * kItems + tid, cp = e % (kD / 2), j = e / (kD / 2);
+    const int64_t t = min(t0 + j * TPW, Tq - TPW);  // first token of the word (Tq is a multiple of G >= TPW)
     const int64_t w = t / TPW, g = t / G;
-    const uint2 words = *reinterpret_cast<const uint2 *>(kc + w * kD + 2 * cp);
-    const uint32_t s2 = *reinterpret_cast<const uint32_t *>(ks + g * kD + 2 * cp);
-    const uint32_t m2 = *reinterpret_cast<const uint32_t *>(km + g * kD + 2 * cp);
-    const float s0 = f16_bits_to_f32(s2 & 0xffffu), s1 = f16_bits_to_f32(s2 >> 16);
-    const float m0 = f16_bits_to_f32(m2 & 0xffffu), m1 = f16_bits_to_f32(m2 >> 16);
+    kw[q] = *reinterpret_cast<const uint2 *>(kc + w * kD + 2 * cp);
+    ks2[q] = *reinterpret_cast<const uint32_t *>(ks + g * kD + 2 * cp);
+    km2[q] = *reinterpret_cast<const uint32_t *>(km + g * kD + 2 * cp);
+  }
+#pragma unroll
+  for (int q = 0; q < NV; ++q) {
+    const int e = q * kItems + tid, w = e % VW;
+    const int64_t t = min(t0 + e / VW, Tq - 1);
+    const int g = (w * TPW) / G;
+    vw[q] = vc[t * VW + w];
+    vs1[q] = vs[t * (kD / G) + g];
+    vm1[q] = vm[t * (kD / G) + g];
+  }
+#pragma unroll
+  for (int q = 0; q < NK; ++q) {
+    const int e = q * kItems + tid, cp = e % (kD / 2), j = e / (kD / 2);
+    const int64_t t = t0 + j * TPW;
+    if (t >= Tq) continue;
+    const float s0 = f16_bits_to_f32(ks2[q] & 0xffffu), s1 = f16_bits_to_f32(ks2[q] >> 16);
+    const float m0 = f16_bits_to_f32(km2[q] & 0xffffu), m1 = f16_bits_to_f32(km2[q] >> 16);
 #pragma unroll
     for (int p = 0; p < TPW; ++p) {
-      const float v0 = add_rn(mul_rn(float((words.x >> (p * BITS)) & kMask), s0), m0);
-      const float v1 = add_rn(mul_rn(float((words.y >> (p * BITS)) & kMask), s1), m1);
+      const float v0 = add_rn(mul_rn(float((kw[q].x >> (p * BITS)) & kMask), s0), m0);
+      const float v1 = add_rn(mul_rn(float((kw[q].y >> (p * BITS)) & kMask), s1), m1);
       wk[(t + p) * (kD / 2) + cp] = uint32_t(f32_to_f16_bits(v0)) | (uint32_t(f32_to_f16_bits(v1)) << 16);
     }
   }
   // values: item (token of the tile, word); TPW contiguous channels out
-  for (int e = tid; e < kTile * VW; e += kStageSplit * kStageThreads) {
-    const int w = e % VW;
+#pragma unroll
+  for (int q = 0; q < NV; ++q) {
+    const int e = q * kItems + tid, w = e % VW;
     const int64_t t = t0 + e / VW;
     if (t >= Tq) continue;
-    const uint32_t word = vc[t * VW + w];
-    const int g = (w * TPW) / G;
-    const float s = f16_bits_to_f32(vs[t * (kD / G) + g]), m = f16_bits_to_f32(vm[t * (kD / G) + g]);
+    const float s = f16_bits_to_f32(vs1[q]), m = f16_bits_to_f32(vm1[q]);
     uint32_t o[TPW / 2];
 #pragma unroll
     for (int p = 0; p < TPW; p += 2) {
-      const float v0 = add_rn(mul_rn(float((word >> (p * BITS)) & kMask), s), m);
-      const float v1 = add_rn(mul_rn(float((word >> ((p + 1) * BITS)) & kMask), s), m);
+      const float v0 = add_rn(mul_rn(float((vw[q] >> (p * BITS)) & kMask), s), m);
+      const float v1 = add_rn(mul_rn(float((vw[q] >> ((p + 1) * BITS)) & kMask), s), m);
       o[p / 2] = uint32_t(f32_to_f16_bits(v0)) | (uint32_t(f32_to_f16_bits(v1)) << 16);
     }
     uint4 *dst = reinterpret_cast<uint4 *>(wv + t * kD + w * TPW);
 #pragma unroll
-    for (int q = 0; q < TPW / 8; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    for (int q2 = 0; q2 < TPW / 8; ++q2) dst[q2] = make_uint4(o[4 * q2], o[4 * q2 + 1], o[4 * q2 + 2], o[4 * q2 + 3]);
   }
 }
 
@@ -367,6 +389,10 @@ __device__ __forceinline__ void compute_tile(FragLane fl, const u32x4 (&qf)[2][4
   for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) acc[tb][qb] = f4{0, 0, 0, 0};
+  // The two waves of a SIMD run the same phases at the same time; the wave in
+  // a matrix-core phase takes issue priority over the one in the softmax, so
+  // whichever gets ahead keeps the matrix cores fed.
+  __builtin_amdgcn_s_setprio(3);
   // key fragments of k-block kb+1 are read while the MFMAs of kb run
   u32x4 ka[2][4];
 #pragma unroll
@@ -382,6 +408,7 @@ __device__ __forceinline__ void compute_tile(FragLane fl, const u32x4 (&qf)[2][4
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) acc[tb][qb] = Op::run(ka[kb & 1][tb], qf[qb][kb], acc[tb][qb]);
   }
+  __builtin_amdgcn_s_setprio(0);
   if (valid < kTile) {  // keys past the end of the source do not exist
     int k4 = 4 * kap;  // key 16 tb + 4 k + v exists while 4 k < valid - 16 tb - v
     asm volatile("" : "+v"(k4));
@@ -426,6 +453,7 @@ __device__ __forceinline__ void compute_tile(FragLane fl, const u32x4 (&qf)[2][4
     }
     st.l[qb] = sum;
   }
+  __builtin_amdgcn_s_setprio(3);
 #pragma unroll
   for (int tp = 0; tp < 2; ++tp) {
     // B: P^T of the 32 keys 32 tp .. 32 tp + 31, two 4-key runs per k-slice
@@ -451,6 +479,7 @@ __device__ __forceinline__ void compute_tile(FragLane fl, const u32x4 (&qf)[2][4
     __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // Query fragments of the wave's rows as the B operand of S^T = K Q^T in dtype
