@@ -482,10 +482,9 @@ __device__ __forceinline__ void compute_tile(FragLane fl, const u32x4 (&qf)[2][4
   __builtin_amdgcn_s_setprio(0);
 }
 
-// Query fragments of the wave's rows as the B operand of S^T = K Q^T in dtype
-// PD: lane (n, k) holds row row0 + 16 qb + n, channels 32 kb + 8 k .. + 7.
-// Rows past the end are zero.
-template <int QD, int PD>
+// Query fragments of the wave's rows, raw (dtype QD), as the B operand of
+// S^T = K Q^T: lane (n, k) holds row row0 + 16 qb + n, channels 32 kb + 8 k ..
+// + 7.  Rows past the end are zero.
 __device__ __forceinline__ void load_queries(u32x4 (&qf)[2][4], const uc_kivi_item &it, const MqParams &p, int64_t h,
                                              int64_t row0) {
   const int lane = threadIdx.x & 63, r = lane & 15, kap = lane >> 4;
@@ -498,8 +497,16 @@ __device__ __forceinline__ void load_queries(u32x4 (&qf)[2][4], const uc_kivi_it
     const uint16_t *q16 = static_cast<const uint16_t *>(it.query) + (i * p.Hq + h * p.group + g) * kD + 8 * kap;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-      qf[qb][kb] = convert8<QD, PD>(ok ? *reinterpret_cast<const u32x4 *>(q16 + 32 * kb) : u32x4{0, 0, 0, 0});
+      qf[qb][kb] = ok ? *reinterpret_cast<const u32x4 *>(q16 + 32 * kb) : u32x4{0, 0, 0, 0};
   }
+}
+
+template <int FROM, int TO>
+__device__ __forceinline__ void convert_queries(u32x4 (&qf)[2][4]) {
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) qf[qb][kb] = convert8<FROM, TO>(qf[qb][kb]);
 }
 
 // Work item w = h * row_blocks + rb of one segment: 128 query rows of KV head h.
@@ -527,9 +534,6 @@ __device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const 
   const uint32_t sh_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char *)&sh));
   const FragLane fl = frag_lane(sh_base + half * 2 * kSlotBytes);
 
-  u32x4 qf[2][4];
-  load_queries<QD, UC_FP16>(qf, it, p, h, row0);
-
   MqState st;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
@@ -553,6 +557,28 @@ __device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const 
     const RowSrc &s = tile_src(t, r0, valid);
     issue_tile(reinterpret_cast<uint4 *>(sh.slot[half][buf]), s, t >= p.nq ? dl_den : dl_pre, r0, valid, hw);
   };
+  // The first half loads the rows' query fragments and hands them to the
+  // wave with the same rows in the second half through LDS (buffer 1 of the
+  // first half, free until step 0), so each query row is read once.
+  u32x4 qf[2][4];
+  if (count > 0) issue(first, 0);
+  {
+    u32x4 *qs = reinterpret_cast<u32x4 *>(sh.slot[0][1]) + hw * 8 * kWave + lane;
+    if (half == 0) {
+      load_queries(qf, it, p, h, row0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qs[j * kWave] = qf[j / 4][j % 4];
+    }
+    __syncthreads();
+    if (half == 1) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qf[j / 4][j % 4] = qs[j * kWave];
+    }
+  }
+  const bool dense_first = first >= p.nq;  // this half starts with dense tiles
+  if (dense_first) convert_queries<QD, RD>(qf);
+  else convert_queries<QD, UC_FP16>(qf);
+
   // Step i: wait for tile first + i, start loading tile first + i + 1 into
   // the other buffer, compute tile first + i (steps past `count` only keep
   // the barrier count of the two halves equal).
@@ -578,12 +604,13 @@ __device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const 
     }
     if (i < end) step(i++, dt_tag, std::integral_constant<int, 0>{});
   };
-  if (count > 0) issue(first, 0);
   // both halves run n0 steps (the barrier is shared): the prefix tiles of this
-  // half with fp16 operands, then its dense tiles in their own dtype
+  // half with fp16 operands, then its dense tiles in their own dtype (the
+  // fp16 fragments go back to the dense dtype: exact when it is fp16, and for
+  // bf16 queries whose values fp16 holds)
   const int n_pre = static_cast<int>(max(0, min(count, p.nq - first)));
   run(std::integral_constant<int, UC_FP16>{}, n_pre);
-  if (n_pre < count) load_queries<QD, RD>(qf, it, p, h, row0);
+  if (n_pre < count && !dense_first) convert_queries<UC_FP16, RD>(qf);
   run(std::integral_constant<int, RD>{}, n0);
   __syncthreads();  // every wave is done reading its last tile
 
@@ -628,18 +655,19 @@ __device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const 
     }
   }
   __syncthreads();
-  if (half == 0) {
+  {  // each half writes 16 of the 32 rows
     constexpr int kChunk = 16 / sizeof(OutT);  // elements per 16-byte store
     constexpr int kPerRow = kD / kChunk;
+    const OutT *obw = reinterpret_cast<const OutT *>(sh.ep.ob) + hw * kRowsPerWave * kRowPad;
 #pragma unroll
-    for (int q = 0; q < kRowsPerWave * kPerRow / kWave; ++q) {
-      const int idx = q * kWave + lane, rr = idx / kPerRow, cc = (idx % kPerRow) * kChunk;
+    for (int q = 0; q < kRowsPerWave / 2 * kPerRow / kWave; ++q) {
+      const int idx = q * kWave + lane, rr = half * (kRowsPerWave / 2) + idx / kPerRow, cc = (idx % kPerRow) * kChunk;
       const int64_t row = row0 + rr;
       if (row >= p.rows) continue;
       const uint32_t gq = fast_div(static_cast<uint32_t>(row), p.lq);
       const int64_t g = gq, i = row - int64_t(gq) * p.Lq;
       *reinterpret_cast<uint4 *>(static_cast<OutT *>(it.out) + (i * p.Hq + h * p.group + g) * kD + cc) =
-          *reinterpret_cast<const uint4 *>(&ob[rr * kRowPad + cc]);
+          *reinterpret_cast<const uint4 *>(&obw[rr * kRowPad + cc]);
     }
   }
 }
