@@ -670,6 +670,8 @@ def main():
                         help="only run a 1 GiB device copy (PMC traffic calibration)")
     parser.add_argument("--only-decode", action="store_true",
                         help="only build the config-1 workload and run its decode step (for counter passes)")
+    parser.add_argument("--only-editing", type=int, choices=(2, 4), default=None,
+                        help="only run the config-2 editing attention at this bit width (for counter passes)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decode hot path shards by sequence / KV head with no "
@@ -683,6 +685,10 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration_copy_bytes": 1 << 30}))
+        return
+
+    if args.only_editing:
+        print(json.dumps(editing_attention(device, args.steps, layers=args.layers, bits=args.only_editing)))
         return
 
     from unicache_amd.storage.decode import KiviDecodeBatch
