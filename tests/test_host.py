@@ -157,3 +157,22 @@ def test_fake_quant_operator_params():
         op.build_params({"working_set_mode": "disk"})
     with pytest.raises(ValueError, match="host_backed"):
         op.build_params({"working_set_mode": "host_backed"})
+
+
+@pytest.mark.parametrize("bits,group", [(2, 32), (4, 128)])
+def test_native_block_matches_storage_views(bits, group):
+    # from_dense's one-allocation block: the same native shapes and strides as
+    # views of token-major storage, addresses on 256-byte boundaries, an ids slot
+    from unicache_amd.storage.physical import _native_block, _native_storage, _native_views
+
+    views, ptrs, ids = _native_block(512, 4, 128, bits, bits, group, "cpu", torch.int64, 512)
+    ref = _native_views(_native_storage(512, 4, 128, bits, bits, group, "cpu"), 512, bits, group)
+    for v, r, p in zip(views, ref, ptrs):
+        assert v.dtype == r.dtype and v.shape == r.shape and v.stride() == r.stride()
+        assert v.data_ptr() == p and (p - ptrs[0]) % 256 == 0  # 256-byte steps within the allocation
+    assert ids.shape == (512,) and ids.dtype == torch.int64 and (ids.data_ptr() - ptrs[0]) % 256 == 0
+    # the tensors do not overlap: each one starts past the previous one's last byte
+    firsts = sorted(v.data_ptr() for v in [*views, ids])
+    sizes = {v.data_ptr(): v.numel() * v.element_size() for v in [*views, ids]}
+    for a, b in zip(firsts, firsts[1:]):
+        assert a + sizes[a] <= b

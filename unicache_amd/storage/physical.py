@@ -202,25 +202,68 @@ def _pack_native_into(storage, offset: int, key: torch.Tensor, value: torch.Tens
 
     if stream is None:
         stream = nat.stream(nat.require_device(key, value, storage[0], what="KIVI native packing"))
+    kc, ks, km, vc, vs, vm = storage
+    _pack_native_at((kc.data_ptr(), ks.data_ptr(), km.data_ptr(), vc.data_ptr(), vs.data_ptr(), vm.data_ptr()),
+                    int(kc.shape[1]) * 32 // k_bits, offset, key, value, k_bits=k_bits, v_bits=v_bits,
+                    group_size=group_size, tokens=tokens, stream=stream)
+
+
+def _pack_native_at(ptrs, capacity: int, offset: int, key: torch.Tensor, value: torch.Tensor, *, k_bits: int,
+                    v_bits: int, group_size: int, tokens: int | None, stream: int) -> None:
+    """uc_kivi_pack into token-major storage of `capacity` tokens given by the
+    addresses of its six tensors (token 0 of head 0)."""
+
     if key.dtype != value.dtype:
         raise ValueError("KIVI packing expects key and value of one dtype")
-    kc, ks, km, vc, vs, vm = storage
     heads, head_dim = int(key.shape[1]), int(key.shape[2])
     tokens = int(key.shape[0]) if tokens is None else int(tokens)
-    kd = int(kc.shape[2])
+    kd, vw, vg = head_dim, head_dim * v_bits // 32, head_dim // group_size
     kw0, g0 = offset * k_bits // 32, offset // group_size
-    vw, vg = int(vc.shape[2]), int(vs.shape[2])
+    kc, ks, km, vc, vs, vm = ptrs
+    kcs, kss = capacity * k_bits // 32 * kd, capacity // group_size * kd  # head strides
     nat.call(
         "uc_kivi_pack",
         key.data_ptr(), *_dense_strides(key), value.data_ptr(), *_dense_strides(value),
         nat.dtype_code(key.dtype), tokens, heads, head_dim, k_bits, v_bits, group_size, nat.UC_FP16,
         # key code (h, d, w), key stats (h, d, g): token-major rows of D channels
-        kc.data_ptr() + 4 * kw0 * kd, int(kc.stride(0)), 1, kd,
-        ks.data_ptr() + 2 * g0 * kd, km.data_ptr() + 2 * g0 * kd, int(ks.stride(0)), 1, kd,
-        vc.data_ptr() + 4 * offset * vw, int(vc.stride(0)), vw, 1,
-        vs.data_ptr() + 2 * offset * vg, vm.data_ptr() + 2 * offset * vg, int(vs.stride(0)), vg, 1,
+        kc + 4 * kw0 * kd, kcs, 1, kd,
+        ks + 2 * g0 * kd, km + 2 * g0 * kd, kss, 1, kd,
+        vc + 4 * offset * vw, capacity * vw, vw, 1,
+        vs + 2 * offset * vg, vm + 2 * offset * vg, capacity * vg, vg, 1,
         stream,
     )
+
+
+def _native_block(capacity: int, heads: int, head_dim: int, k_bits: int, v_bits: int, group_size: int, device,
+                  ids_dtype=None, ids_len: int = 0):
+    """One allocation holding the token-major storage of `capacity` tokens and
+    optionally an ids slot: the six native views of all `capacity` tokens (one
+    view op each), the storage addresses, and the ids tensor (or None).  The
+    few host operations matter: from_dense runs once per materialised segment."""
+
+    specs = _native_specs(capacity, heads, head_dim, k_bits, v_bits, group_size)
+    if ids_dtype is not None:
+        specs.append(((ids_len,), ids_dtype))
+    offsets, total = [], 0
+    for shape, dtype in specs:
+        offsets.append(total)
+        total += -(-math.prod(shape) * dtype.itemsize // _CARVE_ALIGN) * _CARVE_ALIGN
+    buf = torch.empty(max(total, _CARVE_ALIGN), dtype=torch.uint8, device=device)
+    i32, f16 = buf.view(torch.int32), buf.view(torch.float16)
+    d, nw, ng = head_dim, capacity * k_bits // 32, capacity // group_size
+    vw, vg = head_dim * v_bits // 32, head_dim // group_size
+    o = offsets
+    views = (i32.as_strided((heads, d, nw), (nw * d, 1, d), o[0] // 4),
+             f16.as_strided((heads, d, ng), (ng * d, 1, d), o[1] // 2),
+             f16.as_strided((heads, d, ng), (ng * d, 1, d), o[2] // 2),
+             i32.as_strided((heads, capacity, vw), (capacity * vw, vw, 1), o[3] // 4),
+             f16.as_strided((heads, capacity, vg), (capacity * vg, vg, 1), o[4] // 2),
+             f16.as_strided((heads, capacity, vg), (capacity * vg, vg, 1), o[5] // 2))
+    base = buf.data_ptr()
+    ids = None
+    if ids_dtype is not None:
+        ids = buf.view(ids_dtype).as_strided((ids_len,), (1,), o[6] // ids_dtype.itemsize)
+    return views, tuple(base + off for off in o[:6]), ids
 
 
 def _pack_native(key: torch.Tensor, value: torch.Tensor, *, k_bits: int, v_bits: int, group_size: int,
@@ -389,20 +432,15 @@ class PackedKIVICache:
             raise ValueError("KIVI packing expects key and value of one dtype")
         heads, head_dim = int(key.shape[1]), int(key.shape[2])
         ids = logical_token_ids.detach()
-        ids_here = ids.device == device
-        specs = _native_specs(quantized, heads, head_dim, k_bits, v_bits, group_size)
-        if ids_here:
-            specs.append((tuple(ids.shape), ids.dtype))
-        parts = _carve(specs, device)
-        storage = tuple(parts[:6])
-        _pack_native_into(storage, 0, key[:quantized], value[:quantized], k_bits=k_bits, v_bits=v_bits,
-                          group_size=group_size)
+        ids_here = ids.device == device and ids.dim() == 1
+        views, ptrs, ids_slot = _native_block(quantized, heads, head_dim, k_bits, v_bits, group_size, device,
+                                              ids.dtype if ids_here else None, int(ids.shape[0]) if ids_here else 0)
+        _pack_native_at(ptrs, quantized, 0, key, value, k_bits=k_bits, v_bits=v_bits, group_size=group_size,
+                        tokens=quantized, stream=nat.stream(device))
         # a clone, so a suffix view does not pin the whole dense segment (physical.py:316-319)
-        cache = cls(*_native_views(storage, quantized, k_bits, group_size), key[quantized:].clone(),
-                    value[quantized:].clone(), parts[6].copy_(ids) if ids_here else ids.clone(), int(token_type_id),
-                    int(k_bits), int(v_bits), int(group_size), quantized, head_dim, heads, "cuda", True)
-        cache._store = storage
-        return cache
+        return cls(*views, key[quantized:].clone(), value[quantized:].clone(),
+                   ids_slot.copy_(ids) if ids_here else ids.clone(), int(token_type_id), int(k_bits), int(v_bits),
+                   int(group_size), quantized, head_dim, heads, "cuda", True)
 
     def _native_store(self, device) -> tuple[torch.Tensor, ...] | None:
         """Token-major storage behind the native packed tensors (None without a
