@@ -269,9 +269,10 @@ def h2o_eviction(device, steps):
     keep = torch.ones(tokens, dtype=torch.bool, device=device)
     keep[:256] = False
     keep[256:4096:2] = False
+    lens = torch.tensor([tokens], device=device)
     ms_compact = time_steps(lambda: TensorCacheStorageBackend.compact(
-        key=key, value=value, key_type_ids=None, sample_lens=torch.tensor([tokens], device=device),
-        keep_masks=[keep], sample_lengths=[tokens]), steps, 2, stream)
+        key=key, value=value, key_type_ids=None, sample_lens=lens, keep_masks=[keep], sample_lengths=[tokens]),
+        steps, 2, stream)
     kept = int(keep.sum())
     flop = 2 * lq * HQ * tokens * D
     gather_bytes = 2 * (2 * HKV * retained * D * 2) + 2 * HKV * retained * (8 + 4) + HKV * tokens * 4

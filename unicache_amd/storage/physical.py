@@ -146,8 +146,18 @@ def _carve(specs, device) -> list[torch.Tensor]:
         offsets.append(total)
         total += -(-math.prod(shape) * dtype.itemsize // _CARVE_ALIGN) * _CARVE_ALIGN
     buf = torch.empty(max(total, _CARVE_ALIGN), dtype=torch.uint8, device=device)
-    return [buf[off:off + math.prod(shape) * dtype.itemsize].view(dtype).view(shape)
-            for (shape, dtype), off in zip(specs, offsets)]
+    typed = {}  # one view per dtype, then one strided view per tensor
+    out = []
+    for (shape, dtype), off in zip(specs, offsets):
+        base = typed.get(dtype)
+        if base is None:
+            base = typed[dtype] = buf.view(dtype)
+        stride, acc = [], 1
+        for n in reversed(shape):
+            stride.append(acc)
+            acc *= n
+        out.append(base.as_strided(shape, tuple(reversed(stride)), off // dtype.itemsize))
+    return out
 
 
 def _native_specs(capacity: int, heads: int, head_dim: int, k_bits: int, v_bits: int, group_size: int):

@@ -218,13 +218,30 @@ class TensorCacheStorageBackend:
 
         lengths = _sample_lengths(sample_lens, sample_lengths)
         _check_cache(key, value, key_type_ids, lengths, keep_masks)
-        nat.require_device(key, value, what="Dense cache compaction")
-        masks = [m.to(device=key.device, dtype=torch.bool) for m in keep_masks]
-        summary = _Summary()
-        slots = [summary.add(m.sum()) for m in masks]
-        counts = summary.read()
-        return TensorCacheStorageBackend._compact_known(key, value, key_type_ids, sample_lens, masks,
-                                                        [counts[s] for s in slots])
+        device = nat.require_device(key, value, what="Dense cache compaction")
+        masks = [m.to(device=device, dtype=torch.bool) for m in keep_masks]
+        if len(masks) != 1 or key_type_ids is not None and key_type_ids.device != device:
+            summary = _Summary()
+            slots = [summary.add(m.sum()) for m in masks]
+            counts = summary.read()
+            return TensorCacheStorageBackend._compact_known(key, value, key_type_ids, sample_lens, masks,
+                                                            [counts[s] for s in slots])
+        # one sample: the mask scan's own total is the kept count (one host
+        # read) and, cast on the device, the new sample length
+        mask = _aligned_mask(masks[0], device)
+        dst, total = _scan(mask)
+        kept = int(total.item()) if mask.numel() else 0
+        compacted_key, compacted_value, compacted_types = (
+            None if t is None else _copy_rows(t, dst, kept) for t in (key, value, key_type_ids))
+        return CacheMutationResult(
+            key=compacted_key,
+            value=compacted_value,
+            key_type_ids=compacted_types,
+            sample_lens=total.to(device=sample_lens.device, dtype=sample_lens.dtype),
+            original_bytes=int(key.numel() * key.element_size() + value.numel() * value.element_size()),
+            compacted_bytes=int(compacted_key.numel() * compacted_key.element_size()
+                                + compacted_value.numel() * compacted_value.element_size()),
+        )
 
     @staticmethod
     def compact_and_materialize(
