@@ -444,6 +444,21 @@ int uc_scatter_rows(const void *src, int64_t row_bytes, const int32_t *dst_index
                     int64_t out_row_stride_bytes, uc_stream_t stream);
 
 /*
+ * Up to 8 independent device-to-device copies (span i: `bytes` bytes from src
+ * to dst, non-overlapping) in one launch; 16-byte units where a span's
+ * addresses and size allow.
+ * Replaces: the residual clones and the logical-id clone of
+ * PackedKIVICache.from_dense (physical.py:316-330), one copy kernel each.
+ */
+typedef struct uc_copy_span {
+  const void *src;
+  void *dst;
+  int64_t bytes;
+} uc_copy_span;
+
+int uc_copy_spans(const uc_copy_span *spans_host, int n, uc_stream_t stream);
+
+/*
  * Bytes of caller-provided workspace an operation needs.
  *   UC_OP_KIVI_AV:     (1, heads_q, query_len, head_dim, total_tokens)
  *                      = max(4 Hq Lq S (D + 2), Hq Lq >= 64 ? 2 Hq D ceil64(T) : 0),

@@ -169,3 +169,15 @@ def test_editing_batch_validation():
     lens[1] = 0
     with pytest.raises(ValueError, match="query_len must be positive"):
         nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)
+
+
+def test_copy_spans_validation():
+    with pytest.raises(ValueError, match="0..8 spans per call"):
+        nat.call("uc_copy_spans", None, 9, None)
+    table = (ctypes.c_int64 * 3)(0, 0, -1)
+    with pytest.raises(ValueError, match="negative size"):
+        nat.call("uc_copy_spans", ctypes.addressof(table), 1, None)
+    table = (ctypes.c_int64 * 3)(0, 0x1000, 16)
+    with pytest.raises(ValueError, match="null pointer"):
+        nat.call("uc_copy_spans", ctypes.addressof(table), 1, None)
+    nat.call("uc_copy_spans", None, 0, None)  # nothing to copy, nothing launched

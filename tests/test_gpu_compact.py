@@ -58,3 +58,26 @@ def test_compact_empty_cache(device):
                                             sample_lens=torch.zeros(0, dtype=torch.long, device=device),
                                             keep_masks=[])
     assert res.key.shape == (0, 4, 128) and res.sample_lens.numel() == 0
+
+
+def test_copy_spans_bit_exact(device):
+    # one launch for several copies: 16-byte aligned spans, an odd-sized one
+    # and an unaligned one, each equal to its source; bytes around the
+    # destinations stay untouched
+    import ctypes
+
+    from unicache_amd import _native as nat
+
+    g = torch.Generator().manual_seed(3)
+    srcs = [torch.randint(0, 256, (n,), generator=g, dtype=torch.uint8).to(device) for n in (4096, 1000, 77, 0)]
+    outs = [torch.full((n + 32,), 0xAB, dtype=torch.uint8, device=device) for n in (4096, 1000, 77, 0)]
+    offsets = (16, 16, 3, 0)  # destination offsets inside the padded outputs
+    spans = []
+    for s, o, off in zip(srcs, outs, offsets):
+        spans += [s.data_ptr(), o.data_ptr() + off, s.numel()]
+    table = (ctypes.c_int64 * len(spans))(*spans)
+    nat.call("uc_copy_spans", ctypes.addressof(table), len(srcs), nat.stream(device))
+    for s, o, off in zip(srcs, outs, offsets):
+        o = o.cpu()
+        assert torch.equal(o[off:off + s.numel()], s.cpu())
+        assert (o[:off] == 0xAB).all() and (o[off + s.numel():] == 0xAB).all()

@@ -111,6 +111,7 @@ _SIGNATURES = {
     "uc_mask_scan": (_I, [_P, _L, _P, _P, _P]),
     "uc_compact_rows": (_I, [_P, _L, _L, _P, _L, _P, _P]),
     "uc_scatter_rows": (_I, [_P, _L, _P, _L, _P, _L, _P]),
+    "uc_copy_spans": (_I, [_P, _I, _P]),
     "uc_h2o_select_gather": (
         _I,
         [_P, _P, _L, _L, _L, _I, _L, _L, _L, _P, _L, _L, _L, _L, _P, _L, _L, _P, _P, _P, _P, _P, _P],

@@ -10,6 +10,8 @@
 //
 // uc_compact_rows: one thread per 16 (or 8, 4, 2, 1) bytes of a row, rows of
 // dropped tokens exit at once; the copy of a kept row is fully coalesced.
+#include <algorithm>
+
 #include "uc_common.h"
 
 namespace uc {
@@ -169,4 +171,57 @@ extern "C" int uc_scatter_rows(const void *src, int64_t row_bytes, const int32_t
   if ((align & 3) == 0) return launch_scatter<uint32_t>(src, row_bytes, dst_index, n, out, out_row_stride_bytes, s);
   if ((align & 1) == 0) return launch_scatter<uint16_t>(src, row_bytes, dst_index, n, out, out_row_stride_bytes, s);
   return launch_scatter<uint8_t>(src, row_bytes, dst_index, n, out, out_row_stride_bytes, s);
+}
+
+namespace uc {
+namespace {
+
+constexpr int kMaxSpans = 8;
+struct CopySpans {
+  const uint8_t *src[kMaxSpans];
+  uint8_t *dst[kMaxSpans];
+  int64_t bytes[kMaxSpans];
+  int vec[kMaxSpans];  // 1: 16-byte units (addresses and size 16-aligned), 0: bytes
+};
+
+// Span blockIdx.y; thread i of the span's grid copies unit i (and i + grid
+// stride): 16 bytes when the span allows, else one byte.
+__global__ __launch_bounds__(256) void copy_spans_kernel(CopySpans c) {
+  const int s = blockIdx.y;
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c.vec[s]) {
+    const int64_t n = c.bytes[s] / 16;
+    for (; i < n; i += stride)
+      reinterpret_cast<uint4 *>(c.dst[s])[i] = reinterpret_cast<const uint4 *>(c.src[s])[i];
+  } else {
+    for (; i < c.bytes[s]; i += stride) c.dst[s][i] = c.src[s][i];
+  }
+}
+
+}  // namespace
+}  // namespace uc
+
+extern "C" int uc_copy_spans(const uc_copy_span *spans_host, int n, uc_stream_t stream) {
+  clear_error();
+  UC_REQUIRE(n >= 0 && n <= kMaxSpans, "uc_copy_spans: 0..%d spans per call (got %d)", kMaxSpans, n);
+  UC_REQUIRE(n == 0 || spans_host != nullptr, "uc_copy_spans: spans is NULL");
+  CopySpans c{};
+  int64_t most = 0;
+  for (int i = 0; i < n; ++i) {
+    const uc_copy_span &sp = spans_host[i];
+    UC_REQUIRE(sp.bytes >= 0, "uc_copy_spans: negative size");
+    UC_REQUIRE(sp.bytes == 0 || (sp.src != nullptr && sp.dst != nullptr), "uc_copy_spans: null pointer");
+    c.src[i] = static_cast<const uint8_t *>(sp.src);
+    c.dst[i] = static_cast<uint8_t *>(sp.dst);
+    c.bytes[i] = sp.bytes;
+    c.vec[i] = ((reinterpret_cast<uintptr_t>(sp.src) | reinterpret_cast<uintptr_t>(sp.dst) |
+                 static_cast<uintptr_t>(sp.bytes)) & 15) == 0;
+    most = std::max(most, c.vec[i] ? sp.bytes / 16 : sp.bytes);
+  }
+  if (most == 0) return UC_OK;
+  const int64_t blocks = std::min<int64_t>(ceil_div(most, int64_t(256)), 1024);
+  hipLaunchKernelGGL(copy_spans_kernel, dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(n)), dim3(256), 0,
+                     as_stream(stream), c);
+  return check_launch("uc_copy_spans");
 }

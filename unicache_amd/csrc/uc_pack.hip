@@ -216,9 +216,9 @@ constexpr int kPackThreads = 256;
 
 // wave -> (head, group, 128-channel slab); lane -> channel pair
 template <int IN, int KB, int G, bool VEC>
-__global__ __launch_bounds__(kPackThreads) void kivi_pack_key_kernel(PackArgs a) {
+__device__ __forceinline__ void pack_key_block(const PackArgs &a, int64_t block) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave = int64_t(blockIdx.x) * (kPackThreads / kWave) + (threadIdx.x / kWave);
+  const int64_t wave = block * (kPackThreads / kWave) + (threadIdx.x / kWave);
   if (wave >= a.key_waves) return;
   const int64_t slabs = (a.head_dim + 127) / 128;
   const int64_t groups = a.tokens / G;
@@ -234,9 +234,9 @@ __global__ __launch_bounds__(kPackThreads) void kivi_pack_key_kernel(PackArgs a)
 
 // wave -> (head, run of tokens); lane -> (token in run, 16-channel chunk)
 template <int IN, int VB, int G, bool VEC>
-__global__ __launch_bounds__(kPackThreads) void kivi_pack_value_kernel(PackArgs a) {
+__device__ __forceinline__ void pack_value_block(const PackArgs &a, int64_t block) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t vw = int64_t(blockIdx.x) * (kPackThreads / kWave) + (threadIdx.x / kWave);
+  const int64_t vw = block * (kPackThreads / kWave) + (threadIdx.x / kWave);
   if (vw >= a.value_waves) return;
   const int64_t lanes_per_token = a.head_dim / 16;
   const int64_t tokens_per_wave = kWave / lanes_per_token;
@@ -250,10 +250,40 @@ __global__ __launch_bounds__(kPackThreads) void kivi_pack_value_kernel(PackArgs 
                                    a.vs_sg);
 }
 
+template <int IN, int KB, int G, bool VEC>
+__global__ __launch_bounds__(kPackThreads) void kivi_pack_key_kernel(PackArgs a) {
+  pack_key_block<IN, KB, G, VEC>(a, blockIdx.x);
+}
+
+template <int IN, int VB, int G, bool VEC>
+__global__ __launch_bounds__(kPackThreads) void kivi_pack_value_kernel(PackArgs a) {
+  pack_value_block<IN, VB, G, VEC>(a, blockIdx.x);
+}
+
+// Keys and values of equal bits in one launch: the first key_blocks
+// workgroups pack keys, the rest values (one launch instead of two).
+template <int IN, int BITS, int G>
+__global__ __launch_bounds__(kPackThreads) void kivi_pack_kv_kernel(PackArgs a, int64_t key_blocks) {
+  const int64_t b = blockIdx.x;
+  if (b < key_blocks)
+    pack_key_block<IN, BITS, G, true>(a, b);
+  else
+    pack_value_block<IN, BITS, G, true>(a, b - key_blocks);
+}
+
 int64_t wave_blocks(int64_t waves) { return (waves + (kPackThreads / kWave) - 1) / (kPackThreads / kWave); }
 
 template <int IN, int G>
 void launch_pack(const PackArgs &a, int kb, int vb, bool kvec, bool vvec, hipStream_t stream) {
+  if (kb == vb && kb != 8 && kvec && vvec && a.key_waves > 0 && a.value_waves > 0) {
+    const int64_t key_blocks = wave_blocks(a.key_waves);
+    const dim3 grid(static_cast<unsigned>(key_blocks + wave_blocks(a.value_waves)));
+    if (kb == 2)
+      hipLaunchKernelGGL((kivi_pack_kv_kernel<IN, 2, G>), grid, dim3(kPackThreads), 0, stream, a, key_blocks);
+    else
+      hipLaunchKernelGGL((kivi_pack_kv_kernel<IN, 4, G>), grid, dim3(kPackThreads), 0, stream, a, key_blocks);
+    return;
+  }
   if (a.key_waves > 0) {
     const dim3 grid(wave_blocks(a.key_waves));
     UC_DISPATCH_BITS(kb, KB, [&] {

@@ -17,6 +17,8 @@ RuntimeError otherwise (there is no CPU path).
 
 from __future__ import annotations
 
+import ctypes
+
 import math
 from dataclasses import dataclass
 from typing import Callable
@@ -445,12 +447,29 @@ class PackedKIVICache:
         ids_here = ids.device == device and ids.dim() == 1
         views, ptrs, ids_slot = _native_block(quantized, heads, head_dim, k_bits, v_bits, group_size, device,
                                               ids.dtype if ids_here else None, int(ids.shape[0]) if ids_here else 0)
+        stream = nat.stream(device)
         _pack_native_at(ptrs, quantized, 0, key, value, k_bits=k_bits, v_bits=v_bits, group_size=group_size,
-                        tokens=quantized, stream=nat.stream(device))
-        # a clone, so a suffix view does not pin the whole dense segment (physical.py:316-319)
-        return cls(*views, key[quantized:].clone(), value[quantized:].clone(),
-                   ids_slot.copy_(ids) if ids_here else ids.clone(), int(token_type_id), int(k_bits), int(v_bits),
-                   int(group_size), quantized, head_dim, heads, "cuda", True)
+                        tokens=quantized, stream=stream)
+        # the residual rows as compact copies, so a suffix view does not pin
+        # the whole dense segment (physical.py:316-319), and the ids: one
+        # launch for the three copies
+        tail_k, tail_v = key[quantized:], value[quantized:]
+        res_k = torch.empty(tail_k.shape, dtype=key.dtype, device=device)
+        res_v = torch.empty(tail_v.shape, dtype=value.dtype, device=device)
+        if tail_k.is_contiguous() and tail_v.is_contiguous() and (not ids_here or ids.is_contiguous()):
+            nbytes = tail_k.numel() * tail_k.element_size()
+            spans = [tail_k.data_ptr(), res_k.data_ptr(), nbytes, tail_v.data_ptr(), res_v.data_ptr(), nbytes]
+            if ids_here:
+                spans += [ids.data_ptr(), ids_slot.data_ptr(), ids.numel() * ids.element_size()]
+            table = (ctypes.c_int64 * len(spans))(*spans)
+            nat.call("uc_copy_spans", ctypes.addressof(table), len(spans) // 3, stream)
+            ids_copy = ids_slot if ids_here else ids.clone()
+        else:
+            res_k.copy_(tail_k)
+            res_v.copy_(tail_v)
+            ids_copy = ids_slot.copy_(ids) if ids_here else ids.clone()
+        return cls(*views, res_k, res_v, ids_copy, int(token_type_id), int(k_bits), int(v_bits), int(group_size),
+                   quantized, head_dim, heads, "cuda", True)
 
     def _native_store(self, device) -> tuple[torch.Tensor, ...] | None:
         """Token-major storage behind the native packed tensors (None without a
