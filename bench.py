@@ -174,10 +174,11 @@ def long_context_decode(device, steps, layers=LAYERS, tokens=32768):
 def editing_attention(device, steps, layers=LAYERS, bits=BITS):
     """Config 2, the whole editing attention of a layer: 1088 queries x 28 heads
     against 2304 keys -- the 1024 source-VAE tokens (896 packed at `bits` + 128
-    residual) and the 256 instruction + 1024 ViT bf16 tokens -- in one fused
-    uc_kivi_attn_mq pass (stage + MFMA attention kernels), the bf16 segments
-    riding as its dense part; 28 layers of distinct caches.  TFLOP/s =
-    4*Lq*Hq*T*D per layer / time."""
+    residual) and the 256 instruction + 1024 ViT bf16 tokens -- in one
+    uc_kivi_attn_mq_segments launch (the packed prefix dequantized inside the
+    attention kernel, the residual and the two bf16 segments read where they
+    lie: the call run_fused_mixed_attention makes); 28 layers of distinct
+    caches.  TFLOP/s = 4*Lq*Hq*T*D per layer / time."""
 
     from unicache_amd import _native as nat
     from unicache_amd.storage import PackedKIVICache
@@ -191,28 +192,27 @@ def editing_attention(device, steps, layers=LAYERS, bits=BITS):
                                            residual_length=RESIDUAL, backend="cuda")
         ik, iv = make_kv(instr, seed=5100 + layer, device=device)
         tk, tv = make_kv(vit, seed=5200 + layer, device=device)
-        dk = torch.cat([ik, tk, cache.residual_key]).contiguous()
-        dv = torch.cat([iv, tv, cache.residual_value]).contiguous()
         g = torch.Generator(device=device).manual_seed(9000 + layer)
         q = torch.randn(lq, HQ, D, generator=g, device=device).to(torch.bfloat16)
         out = torch.empty_like(q)
         lse = torch.empty(HQ, lq, dtype=torch.float32, device=device)
-        tr = int(dk.shape[0])
-        ws_bytes = nat.mq_workspace_bytes(HKV, D, cache.quantized_tokens, tr)
-        ws = nat.workspace(device, ws_bytes)
-        item = cache.native_item(q.data_ptr(), out.data_ptr(), lse.data_ptr(), residual_key_ptr=dk.data_ptr(),
-                                 residual_value_ptr=dv.data_ptr(), residual_tokens=tr)
-        calls.append((item, ws, ws_bytes, cache, dk, dv, q, out, lse))
-        del key, value, ik, iv, tk, tv
-    keys = calls[0][3].quantized_tokens + int(calls[0][4].shape[0])
+        item = (nat.KiviItem * 1)(cache.native_item(None, None, None, residual_key_ptr=cache.residual_key.data_ptr(),
+                                                    residual_value_ptr=cache.residual_value.data_ptr(),
+                                                    residual_tokens=cache.residual_tokens))
+        dense = (nat.DenseSegment * 2)(
+            nat.DenseSegment(ik.data_ptr(), iv.data_ptr(), instr, HKV * D, D),
+            nat.DenseSegment(tk.data_ptr(), tv.data_ptr(), vit, HKV * D, D))
+        calls.append((item, dense, cache, q, out, lse, ik, iv, tk, tv))
+        del key, value
+    keys = calls[0][2].quantized_tokens + calls[0][2].residual_tokens + instr + vit
     stream = torch.cuda.current_stream(device)
     sid = stream.cuda_stream
     bf16 = nat.dtype_code(torch.bfloat16)
 
     def step():
-        for item, ws, ws_bytes, *_ in calls:
-            nat.call("uc_kivi_attn_mq", item, bits, GROUP, HQ, HKV, D, lq, bf16, bf16, bf16, 1.0 / math.sqrt(D),
-                     ws.data_ptr(), ws_bytes, sid)
+        for item, dense, cache, q, out, lse, *_ in calls:
+            nat.call("uc_kivi_attn_mq_segments", item, 1, dense, 2, q.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                     bits, GROUP, HQ, HKV, D, lq, bf16, bf16, bf16, 1.0 / math.sqrt(D), sid)
 
     ms = time_steps(step, steps, 2, stream)
     flop = 4 * lq * HQ * keys * D
@@ -220,7 +220,7 @@ def editing_attention(device, steps, layers=LAYERS, bits=BITS):
     return {
         "workload": f"config 2 editing attention: Lq=1088 x 28 heads over {keys} keys (VAE {vae} at {bits}-bit: "
                     f"896 packed + 128 residual; instruction {instr} + ViT {vit} bf16), {layers} layers, "
-                    f"one uc_kivi_attn_mq pass per layer",
+                    f"one uc_kivi_attn_mq_segments launch per layer",
         "ms_per_layer": round(ms / layers, 4),
         "tflops": round(tflops, 1),
         "frac_of_bf16_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
@@ -505,7 +505,7 @@ def secondary_rows(device, steps):
     rows["batched_cfg_c2"] = {
         "workload": "three CFG samples of config 2 (1088 queries x 28 heads each) over the 2-bit VAE segment "
                     "(896 packed + 128 residual) plus 1280 / 1024 / 256 current bf16 keys: "
-                    "run_batched_physical_attention: one stage and one attention launch for the three samples "
+                    "run_batched_physical_attention: one attention launch for the three samples "
                     "(uc_kivi_attn_mq_batch), host-side preparation included",
         "ms": round(ms, 5), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
         "frac_of_bf16_mfma_peak": round(flop / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)}

@@ -274,13 +274,14 @@ int uc_kivi_attn_decode_segments(const uc_kivi_item *items_device, int64_t n_ite
  * in the thousands) over one packed segment plus residual: same inputs,
  * outputs and semantics as uc_kivi_attn_decode.  head_dim 128, bits 2/4,
  * group_size 32/64/128, q and residual bf16/fp16, sm_scale > 0; the residual
- * (the dense keys) must be 16-byte aligned.  A first kernel dequantizes the
- * packed prefix of every KV head once into `workspace` (fp16 key and value
- * rows, uc_kivi_mq_workspace_bytes bytes); a second streams 64-key tiles of
- * that prefix and of the residual, read where it lies, through LDS for MFMA,
- * 128 query rows per workgroup.  Prefix tiles take fp16 operands (the query
- * and the dequantized values must stay below 65504 in magnitude); residual
- * tiles take the residual's dtype (bf16 keeps its range).
+ * (the dense keys) must be 16-byte aligned.  One kernel streams 64-key tiles
+ * through LDS for MFMA, 128 query rows per workgroup: packed tiles are
+ * dequantized from their codes into LDS inside the kernel (nothing is staged
+ * in HBM), residual tiles are read where they lie.  Packed tiles take fp16
+ * operands (the query and the dequantized values must stay below 65504 in
+ * magnitude); residual tiles take the residual's dtype (bf16 keeps its range).
+ * `workspace` is not used (uc_kivi_mq_workspace_bytes returns 0) and may be
+ * NULL; the arguments stay for callers written against the staged version.
  * Replaces: _packed_attention_kernel / packed_attention_tiled
  * (kivi_triton.py:216-382, 615-687) behind packed_kivi_quantized_attention_summary
  * (kivi_cuda.py:96-120) with backend "triton_tiled", plus the residual part.
@@ -290,18 +291,17 @@ int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int group_size,
                     int q_dtype, int res_dtype, int out_dtype, float sm_scale,
                     void *workspace, int64_t workspace_bytes, uc_stream_t stream);
 
-/* Workspace of uc_kivi_attn_mq: 2 * heads_kv * Tq * head_dim * 2 bytes (0 when Tq == 0). */
+/* Workspace of uc_kivi_attn_mq and uc_kivi_attn_mq_batch: 0 bytes (-1 for bad arguments). */
 int64_t uc_kivi_mq_workspace_bytes(int64_t heads_kv, int64_t head_dim, int64_t quantized_tokens,
                                    int64_t residual_tokens);
 
 /*
- * uc_kivi_attn_mq over n_items (1..8) independent segments in one stage
- * launch and one attention launch: item i attends its query_lens[i] queries
- * (item.query / item.out / item.lse, laid out as in uc_kivi_attn_mq) to its
- * own packed prefix and residual.  Every item shares bits, group_size, heads,
- * head_dim and dtypes.  `workspace` holds the items' stagings back to back:
- * sum_i uc_kivi_mq_workspace_bytes(heads_kv, head_dim, Tq_i, Tr_i) bytes.
- * Results equal n_items calls of uc_kivi_attn_mq bit for bit.
+ * uc_kivi_attn_mq over n_items (1..8) independent segments in one launch:
+ * item i attends its query_lens[i] queries (item.query / item.out /
+ * item.lse, laid out as in uc_kivi_attn_mq) to its own packed prefix and
+ * residual.  Every item shares bits, group_size, heads, head_dim and dtypes.
+ * `workspace` is not used and may be NULL.  Results equal n_items calls of
+ * uc_kivi_attn_mq bit for bit.
  * Replaces: the per-sample loop of apply_static_physical_attention_batch
  * (adapters/bagel.py:773-980) for samples whose physical layout is one packed
  * KIVI segment plus dense keys (CFG branches packed with pack_naive_caches).
@@ -310,6 +310,41 @@ int uc_kivi_attn_mq_batch(const uc_kivi_item *items_host, const int64_t *query_l
                           int bits, int group_size, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
                           int q_dtype, int res_dtype, int out_dtype, float sm_scale,
                           void *workspace, int64_t workspace_bytes, uc_stream_t stream);
+
+/*
+ * One dense 16-bit key/value segment of a segment-table call: key element
+ * (token t, KV head h, channel d) at key + t * token_stride + h * head_stride
+ * + d, strides in elements (multiples of 8), the same for value; key and
+ * value 16-byte aligned.  [T, Hkv, D] rows: token_stride = Hkv * D,
+ * head_stride = D; [Hkv, T, D] (an H2O segment): token_stride = D,
+ * head_stride = T * D.
+ */
+typedef struct uc_dense_segment {
+  const void *key;
+  const void *value;
+  int64_t tokens;
+  int64_t token_stride;
+  int64_t head_stride;
+} uc_dense_segment;
+
+/*
+ * Segment table for long queries: one softmax of query [Lq, Hq, 128] over
+ * the packed prefixes and residuals of `n_packed` items (their query / out /
+ * lse fields are not used) and `n_dense` dense segments, in one launch with
+ * no staging: out [Lq, Hq, 128] normalised, lse [Hq, Lq] natural-log (may be
+ * NULL).  Limits per call: 8 packed prefixes, 16 dense segments counting the
+ * items' residuals.  Shapes and dtypes as uc_kivi_attn_mq; dense_dtype is the
+ * dtype of every residual and dense segment.
+ * Replaces: for long queries, the concatenation of the bf16 segments, the
+ * per-prefix fused summaries and merge_attention_summaries of
+ * _run_fused_mixed_attention (adapters/bagel.py:1598-1858).
+ */
+int uc_kivi_attn_mq_segments(const uc_kivi_item *packed_host, int n_packed,
+                             const uc_dense_segment *dense_host, int n_dense,
+                             const void *query, void *out, float *lse,
+                             int bits, int group_size, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
+                             int64_t query_len, int q_dtype, int dense_dtype, int out_dtype, float sm_scale,
+                             uc_stream_t stream);
 
 /*
  * Merge normalised attention summaries of n_segments disjoint key segments:

@@ -104,23 +104,23 @@ def test_editing_validation():
     with pytest.raises(ValueError, match="multiple of KV heads"):
         nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, 28, 3, 128, 512, nat.UC_BF16, nat.UC_BF16,
                  nat.UC_BF16, 0.1, None, 0, None)
-    # the workspace check comes after every pointer check; the pointers are
-    # never dereferenced on the host, so aligned placeholders reach it.  The
-    # workspace holds the staged prefix only: 2 * Hkv * Tq * 128 fp16
-    assert nat.mq_workspace_bytes(4, 128, 64, 128) == 2 * 4 * 64 * 128 * 2
+    # the multi-query kernel dequantizes inside the attention pass: no workspace
+    assert nat.mq_workspace_bytes(4, 128, 64, 128) == 0
     assert nat.mq_workspace_bytes(4, 128, 0, 128) == 0
+    with pytest.raises(ValueError):
+        nat.mq_workspace_bytes(0, 128, 64, 128)
+    # aligned placeholders (never dereferenced on the host); each case below
+    # breaks one check, so no call reaches a launch
     item.residual_tokens = 128
     for name in ("query", "out", "residual_key", "residual_value", "key_code", "key_scale", "key_min",
                  "value_code", "value_scale", "value_min"):
         setattr(item, name, 0x1000)
-    with pytest.raises(ValueError, match="workspace too small"):
-        nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, *args)
     item.out = 0x1008
     with pytest.raises(ValueError, match="16-byte aligned"):
         nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, *args)
     item.out = 0x1000
     item.residual_value = 0x1004
-    with pytest.raises(ValueError, match="residual keys and values must be 16-byte aligned"):
+    with pytest.raises(ValueError, match="dense keys and values must be 16-byte aligned"):
         nat.call("uc_kivi_attn_mq", ctypes.byref(item), 2, 32, *args)
     item.residual_value = 0x1000
     with pytest.raises(ValueError, match="sm_scale must be positive"):
@@ -155,20 +155,74 @@ def test_editing_batch_validation():
         nat.call("uc_kivi_attn_mq_batch", items, lens, 0, *tail)
     with pytest.raises(ValueError, match="n_items must be 1..8"):
         nat.call("uc_kivi_attn_mq_batch", items, lens, 9, *tail)
+    with pytest.raises(ValueError, match="query/out are NULL"):
+        nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)
+    for it in items[:2]:
+        it.query = it.out = 0x1000
     with pytest.raises(ValueError, match="empty segment"):
         nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)
-    # aligned placeholders (never dereferenced on the host) reach the workspace check
+    # aligned placeholders (never dereferenced on the host); each case below
+    # breaks one check, so no call reaches a launch
     for it in items[:2]:
         it.residual_tokens = 100
         it.quantized_tokens = 64
         for name in ("query", "out", "residual_key", "residual_value", "key_code", "key_scale", "key_min",
                      "value_code", "value_scale", "value_min"):
             setattr(it, name, 0x1000)
-    with pytest.raises(ValueError, match="workspace too small"):
+    items[1].residual_key = 0x1008
+    with pytest.raises(ValueError, match="16-byte aligned"):
         nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)
+    items[1].residual_key = 0x1000
+    items[1].quantized_tokens = 48
+    with pytest.raises(ValueError, match="multiple of group_size"):
+        nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)
+    items[1].quantized_tokens = 64
     lens[1] = 0
     with pytest.raises(ValueError, match="query_len must be positive"):
         nat.call("uc_kivi_attn_mq_batch", items, lens, 2, *tail)
+
+
+def test_editing_segments_validation():
+    q = 0x1000
+    packed = (nat.KiviItem * 9)()
+    for it in packed:
+        it.quantized_tokens = 64
+        for name in ("key_code", "key_scale", "key_min", "value_code", "value_scale", "value_min"):
+            setattr(it, name, 0x2000)
+    dense = (nat.DenseSegment * 17)()
+    for d in dense:
+        d.key, d.value, d.tokens, d.token_stride, d.head_stride = 0x3000, 0x3000, 100, 512, 128
+    tail = (2, 32, 28, 4, 128, 512, nat.UC_BF16, nat.UC_BF16, nat.UC_BF16, 0.1, None)
+
+    def call(n_packed, n_dense, query=q):
+        nat.call("uc_kivi_attn_mq_segments", packed, n_packed, dense, n_dense, query, q, None, *tail)
+
+    with pytest.raises(ValueError, match="more than 8 packed segments"):
+        call(9, 0)
+    with pytest.raises(ValueError, match="more than 16 dense segments"):
+        call(1, 17)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        call(1, 1, query=0x1004)
+    dense[0].token_stride = 130  # not a multiple of 8 elements
+    with pytest.raises(ValueError, match="16-byte token and head strides"):
+        call(1, 1)
+    dense[0].token_stride = 512
+    dense[0].value = 0x3008
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        call(0, 1)
+    dense[0].value = 0x3000
+    dense[0].tokens = 1 << 22  # 2^22 rows of 1 KiB: past 32-bit offsets
+    with pytest.raises(ValueError, match="too long for 32-bit offsets"):
+        call(0, 1)
+    dense[0].tokens = 100
+    packed[0].packed_capacity = 32
+    with pytest.raises(ValueError, match="packed_capacity"):
+        call(1, 0)
+    packed[0].packed_capacity = 0
+    with pytest.raises(ValueError, match="empty segment"):
+        call(0, 0)
+    with pytest.raises(ValueError, match="bad segment arrays"):
+        nat.call("uc_kivi_attn_mq_segments", None, 1, dense, 0, q, q, None, *tail)
 
 
 def test_copy_spans_validation():

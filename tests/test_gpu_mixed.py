@@ -185,12 +185,13 @@ def test_batched_physical_attention_per_sample_softmax(device):
 
 
 def test_batched_packed_launch_matches_per_sample_passes(device):
-    # samples with one packed prefix plus dense keys share one stage and one
-    # attention launch per 8 (uc_kivi_attn_mq_batch); the results equal one
-    # fused pass per sample bit for bit.  Ten samples: two launches for the
+    # samples with one packed prefix plus dense keys share one attention
+    # launch per 8 (uc_kivi_attn_mq_batch); the results equal one fused pass
+    # per sample over the same [current keys, residual] rows bit for bit.  Ten samples: two launches for the
     # 2-bit / group-32 caches (chunks of 8 and 1) and one for the 4-bit /
     # group-64 cache; ragged query and current-key lengths.
     from unicache_amd.adapters import run_batched_physical_attention
+    from unicache_amd.storage.kivi_cuda import packed_summary_with_dense
 
     caches = []
     for j, (n, bits, group) in enumerate([(1000, 2, 32), (600, 2, 32), (1100, 4, 64)]):
@@ -207,23 +208,27 @@ def test_batched_packed_launch_matches_per_sample_passes(device):
     cu_k = np.concatenate([[0], np.cumsum(k_lens)]).tolist()
     out = run_batched_physical_attention(q, k, v, cu_q, cu_k, [[caches[c]] for c in pick])
     for i, c in enumerate(pick):
-        want = run_fused_mixed_attention(q[cu_q[i]:cu_q[i + 1]], k[cu_k[i]:cu_k[i + 1]], v[cu_k[i]:cu_k[i + 1]],
-                                         [caches[c]])
+        cache = caches[c]
+        dk = torch.cat([k[cu_k[i]:cu_k[i + 1]], cache.residual_key])
+        dv = torch.cat([v[cu_k[i]:cu_k[i + 1]], cache.residual_value])
+        want, _ = packed_summary_with_dense(cache, q[cu_q[i]:cu_q[i + 1]], dk, dv)
         assert torch.equal(out[cu_q[i]:cu_q[i + 1]], want), f"sample {i}"
 
 
-def test_multi_prefix_launch_matches_separate_passes(device):
-    # two packed prefixes with long queries: both passes share one batched
-    # launch; the merged output equals one pass per prefix + LSE merge bit for bit
+def test_segment_table_matches_separate_passes(device):
+    # two packed prefixes with long queries: one segment-table launch (both
+    # prefixes, both residuals and the dense keys read in place) against one
+    # pass per prefix plus the LSE merge, and both against the oracle
     from unicache_amd.adapters.bagel import merge_attention_summaries
     from unicache_amd.storage.kivi_cuda import packed_kivi_quantized_attention_summary, packed_summary_with_dense
 
-    segments = []
+    segments, segs = [], []
     for j, n in enumerate((1000, 700)):
         ck, cv = kv_pair(n, seed=80 + j)
         segments.append(PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(n),
                                                    token_type_id=3, k_bits=2, v_bits=2, group_size=32,
                                                    residual_length=128, backend="cuda"))
+        segs.append(K.from_dense(f32(ck), f32(cv), k_bits=2, v_bits=2, group_size=32, residual_length=128))
     q = queries(150, seed=82).to(device)
     dk, dv = (x.to(device) for x in kv_pair(90, seed=83))
     out, lse = run_fused_mixed_attention(q, dk, dv, segments, return_lse=True)
@@ -232,7 +237,49 @@ def test_multi_prefix_launch_matches_separate_passes(device):
     parts = [packed_summary_with_dense(segments[0], q, keys, values),
              packed_kivi_quantized_attention_summary(segments[1], q)]
     want, want_lse = merge_attention_summaries(parts)
-    assert torch.equal(out, want) and torch.equal(lse, want_lse)
+    assert_close(f32(out), f32(want), what="table vs passes")
+    assert_close(f32(lse), f32(want_lse), max_abs=1e-2, mean_abs=1e-3, what="table vs passes lse")
+    ek, ev = _oracle_keys((dk, dv), [], segs)
+    eo, el = A.attention_summary(f32(q), ek, ev)
+    assert_close(f32(out), eo, what="table out")
+    assert_close(f32(lse), el, max_abs=1e-2, mean_abs=1e-3, what="table lse")
+
+
+@pytest.mark.parametrize("bits,group,dtype,lq", [(2, 32, torch.bfloat16, 1088), (4, 32, torch.bfloat16, 1088),
+                                                 (2, 64, torch.float16, 257), (4, 128, torch.bfloat16, 257)])
+def test_segment_table_editing_layout(device, bits, group, dtype, lq):
+    # config 2's editing layout through uc_kivi_attn_mq_segments: 1088 (or 257) queries
+    # over the source-VAE cache (packed prefix + residual), a second packed
+    # prefix whose last tile is half full, the 256 instruction tokens
+    # ([T, Hkv, D]) and 1024 ViT tokens held as [Hkv, T, D] (read through their
+    # strides), against the fp32 oracle softmax over all of them
+    from unicache_amd.storage.kivi_cuda import packed_segments_summary
+
+    caches, segs = [], []
+    for j, (n, resid) in enumerate(((1024, 128), (group * 11 + 40, 40))):
+        ck, cv = kv_pair(n, seed=120 + j, dtype=dtype)
+        caches.append(PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(n),
+                                                 token_type_id=3, k_bits=bits, v_bits=bits, group_size=group,
+                                                 residual_length=resid, backend="cuda"))
+        segs.append(K.from_dense(f32(ck), f32(cv), k_bits=bits, v_bits=bits, group_size=group,
+                                 residual_length=resid, in_dtype="fp16" if dtype == torch.float16 else "bf16"))
+    assert caches[1].quantized_tokens % 64 == 32 or group != 32
+    ik, iv = kv_pair(256, seed=130, dtype=dtype)
+    tk, tv = kv_pair(1024, seed=131, dtype=dtype)
+    tk_hmajor = tk.transpose(0, 1).contiguous().to(device)  # [Hkv, T, D], like an H2O segment
+    tv_hmajor = tv.transpose(0, 1).contiguous().to(device)
+    q = queries(lq, seed=132, dtype=dtype)
+    dense = [(ik.to(device), iv.to(device)), (tk_hmajor.transpose(0, 1), tv_hmajor.transpose(0, 1))]
+    out, lse = packed_segments_summary(caches, q.to(device), dense)
+    assert out.shape == (lq, 28, 128) and out.dtype == dtype
+    ks, vs = [f32(ik), f32(tk)], [f32(iv), f32(tv)]
+    for seg in segs:
+        k, v = K.dequantize(seg, "fp32")
+        ks.append(k)
+        vs.append(v)
+    eo, el = A.attention_summary(f32(q), np.concatenate(ks), np.concatenate(vs))
+    assert_close(f32(out), eo, what=f"table {bits}-bit G{group}")
+    assert_close(f32(lse), el, max_abs=1e-2, mean_abs=1e-3, what=f"table lse {bits}-bit G{group}")
 
 
 def test_batched_launch_rejects_bad_items_before_launch(device):

@@ -47,6 +47,18 @@ class KiviItem(ctypes.Structure):
     ]
 
 
+class DenseSegment(ctypes.Structure):
+    """Mirror of ``uc_dense_segment`` (strides in elements)."""
+
+    _fields_ = [
+        ("key", _P),
+        ("value", _P),
+        ("tokens", _L),
+        ("token_stride", _L),
+        ("head_stride", _L),
+    ]
+
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     "uc_abi_version": (_I, []),
@@ -96,6 +108,11 @@ _SIGNATURES = {
         _I,
         [ctypes.POINTER(KiviItem), ctypes.POINTER(ctypes.c_int64), _I, _I, _I, _L, _L, _L, _I, _I, _I, _F, _P, _L,
          _P],
+    ),
+    "uc_kivi_attn_mq_segments": (
+        _I,
+        [ctypes.POINTER(KiviItem), _I, ctypes.POINTER(DenseSegment), _I, _P, _P, _P, _I, _I, _L, _L, _L, _L,
+         _I, _I, _I, _F, _P],
     ),
     "uc_lse_merge": (_I, [_P, _P, _I, _I, _L, _L, _L, _P, _P, _P]),
     "uc_h2o_scores": (

@@ -56,15 +56,22 @@ def run_fused_mixed_attention(
     prefix plus residual of PackedKIVICache segments
     (_run_fused_mixed_attention, adapters/bagel.py:1598-1858).
 
-    The bf16 keys are gathered in UniCache's order [dense, H2O..., residuals...]
-    and attended in the same fused pass as the first packed segment's prefix;
-    further packed prefixes get their own pass (all passes in one batched
-    launch for long queries) and the summaries are merged by LSE.  Non-frozen H2O segments then receive exp(logit - global LSE) as
-    bf16 probabilities and are trimmed to their budget.  Returns the output
-    (and the global LSE [Hq, Lq] with return_lse=True)."""
+    Long queries (image editing) take one launch over a segment table
+    (packed_segments_summary): every packed prefix is dequantized inside the
+    attention kernel and every bf16 part -- the dense KV, the H2O segments
+    (read through their [Hkv, T, D] strides) and the residuals -- is read
+    where it lies, in one softmax.  Otherwise the bf16 keys are gathered in
+    UniCache's order [dense, H2O..., residuals...] and attended in the same
+    fused pass as the first packed segment's prefix; further packed prefixes
+    get their own pass (all passes in one batched launch for long queries) and
+    the summaries are merged by LSE.  Non-frozen H2O segments then receive
+    exp(logit - global LSE) as bf16 probabilities and are trimmed to their
+    budget.  Returns the output (and the global LSE [Hq, Lq] with
+    return_lse=True)."""
 
     from ..storage.kivi_cuda import (_max_decode_query_len, packed_batch_with_dense,
-                                     packed_kivi_quantized_attention_summary, packed_summary_with_dense)
+                                     packed_kivi_quantized_attention_summary, packed_segments_summary,
+                                     packed_segments_supported, packed_summary_with_dense)
     from ..storage.physical import GQAH2OCache, PackedKIVICache
 
     h2o = [s for s in physical_segments if isinstance(s, GQAH2OCache)]
@@ -72,30 +79,38 @@ def run_fused_mixed_attention(
     with_prefix = [s for s in packed if s.quantized_tokens]
     if not with_prefix:
         raise RuntimeError("Fused mixed attention requires packed KIVI tokens")
-    keys = [dense_key] + [s.key.transpose(0, 1) for s in h2o] + [s.residual_key for s in packed if s.residual_tokens]
-    values = [dense_value] + [s.value.transpose(0, 1) for s in h2o] + [
-        s.residual_value for s in packed if s.residual_tokens]
-    all_key = torch.cat([k.to(dense_key.dtype) for k in keys], dim=0)
-    all_value = torch.cat([v.to(dense_value.dtype) for v in values], dim=0)
-    first = with_prefix[0]
     lq, hq, d = map(int, query.shape)
-    if (len(with_prefix) > 1 and query.dtype in (torch.bfloat16, torch.float16)
-            and all_key.dtype in (torch.bfloat16, torch.float16) and all_value.dtype == all_key.dtype and d == 128
-            and first.group_size in (32, 64, 128) and first.k_bits in (2, 4) and lq > _max_decode_query_len(first, hq)
-            and all((s.k_bits, s.v_bits, s.group_size, s.num_kv_heads) == (first.k_bits, first.k_bits,
-                                                                          first.group_size, first.num_kv_heads)
-                    for s in with_prefix)):
-        # every packed prefix in one stage and one attention launch (the first
-        # with the dense keys), the same summaries as one pass per prefix
-        q = query.contiguous()
-        summaries = [(torch.empty_like(q), torch.empty((hq, lq), dtype=torch.float32, device=q.device))
-                     for _ in with_prefix]
-        packed_batch_with_dense([(s, q, [all_key] if j == 0 else [], [all_value] if j == 0 else [], o, lse)
-                                 for j, (s, (o, lse)) in enumerate(zip(with_prefix, summaries))])
+    first = with_prefix[0]
+    dense_parts = [(dense_key, dense_value)] + [(s.key.transpose(0, 1), s.value.transpose(0, 1)) for s in h2o] + [
+        (s.residual_key, s.residual_value) for s in packed if not s.quantized_tokens and s.residual_tokens]
+    if dense_key.dtype in (torch.bfloat16, torch.float16) and packed_segments_supported(with_prefix, query,
+                                                                                      dense_parts):
+        output, global_lse = packed_segments_summary(with_prefix, query, dense_parts, dense_dtype=dense_key.dtype)
     else:
-        summaries = [packed_summary_with_dense(first, query, all_key, all_value)]
-        summaries += [packed_kivi_quantized_attention_summary(s, query) for s in with_prefix[1:]]
-    output, global_lse = summaries[0] if len(summaries) == 1 else merge_attention_summaries(summaries)
+        keys = [dense_key] + [s.key.transpose(0, 1) for s in h2o] + [
+            s.residual_key for s in packed if s.residual_tokens]
+        values = [dense_value] + [s.value.transpose(0, 1) for s in h2o] + [
+            s.residual_value for s in packed if s.residual_tokens]
+        all_key = torch.cat([k.to(dense_key.dtype) for k in keys], dim=0)
+        all_value = torch.cat([v.to(dense_value.dtype) for v in values], dim=0)
+        if (len(with_prefix) > 1 and query.dtype in (torch.bfloat16, torch.float16)
+                and all_key.dtype in (torch.bfloat16, torch.float16) and all_value.dtype == all_key.dtype
+                and d == 128 and first.group_size in (32, 64, 128) and first.k_bits in (2, 4)
+                and lq > _max_decode_query_len(first, hq)
+                and all((s.k_bits, s.v_bits, s.group_size, s.num_kv_heads) == (first.k_bits, first.k_bits,
+                                                                              first.group_size, first.num_kv_heads)
+                        for s in with_prefix)):
+            # every packed prefix in one attention launch (the first with the
+            # dense keys), the same summaries as one pass per prefix
+            q = query.contiguous()
+            summaries = [(torch.empty_like(q), torch.empty((hq, lq), dtype=torch.float32, device=q.device))
+                         for _ in with_prefix]
+            packed_batch_with_dense([(s, q, [all_key] if j == 0 else [], [all_value] if j == 0 else [], o, lse)
+                                     for j, (s, (o, lse)) in enumerate(zip(with_prefix, summaries))])
+        else:
+            summaries = [packed_summary_with_dense(first, query, all_key, all_value)]
+            summaries += [packed_kivi_quantized_attention_summary(s, query) for s in with_prefix[1:]]
+        output, global_lse = summaries[0] if len(summaries) == 1 else merge_attention_summaries(summaries)
     for segment in h2o:
         if segment.selection_frozen:
             continue

@@ -1,26 +1,26 @@
-// Multi-query attention over one KIVI-packed segment plus its dense keys
+// Multi-query attention over KIVI-packed segments and dense 16-bit segments
 // (head_dim 128, 2/4-bit codes): the long-query case of UniCache's packed
-// attention (image editing: ~1088 queries x 7 query heads per KV head).
-//
-// Two kernels.  mq_stage_kernel dequantizes the packed prefix of every KV head
-// once into a workspace of fp16 rows, keys and values alike [Hkv][Tq][128]
-// (code * scale + minimum in fp32, then one rounding to fp16); the ~60 query
-// blocks of a head then read fp16 rows instead of re-dequantizing the codes.
-// The dense keys (the segment's residual, or the bf16 tokens riding with it)
-// are not copied: the attention kernel reads their [T, Hkv, 128] rows where
-// they lie.
+// attention (image editing: ~1088 queries x 7 query heads per KV head), one
+// softmax over every segment of a query in one launch.
 //
 // mq_attention_kernel: one workgroup (8 waves) owns 128 query rows of one KV
-// head; waves 0-3 take the first half of the 64-key tiles and waves 4-7 the
-// second, 32 query rows per wave.  Tiles of keys and values stream into
-// double-buffered LDS slots by buffer-to-LDS loads (no registers held), one
-// barrier per tile, and each wave runs
+// head; waves 0-3 take half of the 64-key tiles (half of the packed tiles,
+// then part of the dense ones) and waves 4-7 the rest, 32 query rows per wave.
+// A tile's keys and values reach double-buffered LDS slots as fp16 or 16-bit
+// dense rows in one swizzled layout, one barrier per tile:
+//   packed tiles: the half's 256 threads load the tile's code words and fp16
+//     scales and minima into registers (issued before the previous tile's
+//     math), dequantize them (code * scale + minimum, one fp16 fma) and write
+//     the key and value rows -- the codes are read from HBM, never staged;
+//   dense tiles: buffer-to-LDS loads of the rows where they lie (any token
+//     and head stride), no registers held.
+// Then each wave runs
 //   S^T = K Q^T    (v_mfma_f32_16x16x32, rows = keys, columns = queries),
 //   online base-2 softmax over the key rows against a lazily raised reference,
 //   O^T += V^T P^T (v_mfma_f32_16x16x32; the V^T fragments come straight from
 //                   the value rows through the transposing LDS read
 //                   ds_read_b64_tr_b16, P^T straight from the S^T accumulators).
-// Prefix tiles use fp16 operands.  Dense tiles use the dense keys' own dtype:
+// Packed tiles use fp16 operands.  Dense tiles use the dense keys' own dtype:
 // bf16 tokens enter the matrix cores unrounded and keep their range.
 // Output: normalised O (written through LDS as whole rows) and the natural-log
 // LSE.
@@ -93,12 +93,11 @@ __device__ __forceinline__ u32x4 convert8(u32x4 raw) {
 constexpr int kXcds = 8;  // XCDs of an MI355X; launch index i runs on XCD i % 8
 constexpr int kTile = 64;  // keys per tile
 constexpr int kHalfWaves = 4;
+constexpr int kHalfThreads = kHalfWaves * kWave;
 constexpr int kAttnWaves = 2 * kHalfWaves;
 constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kRowsPerWave = 32;
 constexpr int kMqRows = kHalfWaves * kRowsPerWave;  // query rows per workgroup
-constexpr int kStageThreads = kWave;
-constexpr int kStageSplit = 4;  // one-wave workgroups per (tile, KV head) of the stage pass
 // The reference of a query column is raised only when a logit exceeds it by
 // more than kSlack (log2 units): probabilities stay below 2^kSlack, and most
 // tiles need no rescale of the output accumulators.
@@ -125,144 +124,289 @@ struct MqShared {
 };
 static_assert(sizeof(MqShared) <= 160 * 1024, "fits the LDS of a workgroup");
 
-struct MqParams {
-  int64_t Hq, Hkv, Lq, group, rows;  // rows = group * Lq query rows per KV head
-  int64_t Tq, Tr;                    // packed prefix and dense tokens
-  int nq, nd;                        // their 64-key tiles
+// ------------------------------------------------------------ launch table --
+// Everything a launch needs travels by value in the kernel arguments: up to
+// kMqMaxQueries queries, each attending its own run of packed and dense
+// segments of the table.
+constexpr int kMqMaxQueries = 8;
+constexpr int kMqMaxPacked = 8;
+constexpr int kMqMaxDense = 16;
+
+// A packed prefix: head 0 of the six native tensors (token-major words,
+// packed_capacity tokens between heads) and its token count.
+struct PackedSeg {
+  const char *kc, *ks, *km, *vc, *vs, *vm;
+  int64_t cap;
+  int tokens;  // a multiple of the group size
+};
+
+// A dense segment: key row (token t, head h) at k + t * tok_bytes + h * head_bytes.
+struct DenseSeg {
+  const char *k, *v;
+  int64_t tok_bytes, head_bytes;
+  int tokens;
+};
+
+struct MqQuery {
+  const void *query;  // [Lq, Hq, 128]
+  void *out;          // [Lq, Hq, 128]
+  float *lse;         // [Hq, Lq] or null
+  int64_t Lq, rows;   // rows = group * Lq query rows per KV head
+  FastDiv lq;         // row -> (query head of the group, query position)
+  int row_blocks;     // 128-row blocks per KV head
+  int per_xcd;        // work items (row block x KV head) per XCD
+  int slot0;          // the query's first launch slot on every XCD
+  int p0, np, d0, nd;  // its packed segments [p0, p0 + np) and dense ones [d0, d0 + nd)
+  int pt, dt;          // its packed and dense 64-key tiles
+};
+
+struct MqTable {
+  PackedSeg ps[kMqMaxPacked];
+  DenseSeg ds[kMqMaxDense];
+  MqQuery q[kMqMaxQueries];
+  int n_queries, Hkv, group, gshift;  // gshift = log2(group size)
+  int64_t Hq;
   float scale_log2;
-  const _Float16 *wk, *wv;           // staged prefix rows [Hkv][Tq][128]
-  int64_t row_blocks, per_xcd;       // row blocks per KV head; work items per XCD
-  FastDiv lq;                        // row -> (query head of the group, query position)
+};
+static_assert(sizeof(MqTable) <= 4096, "the launch table fits the kernel argument space");
+
+struct TileRef {
+  int seg, r0, valid;  // segment, first token, tokens of the tile that exist
 };
 
-struct StageParams {
-  int64_t Tq;
-  _Float16 *wk, *wv;
-};
-
-// Up to kMqMaxBatch segments (one query block each) in one stage launch and
-// one attention launch, passed by value as kernel arguments.  Item i owns
-// stage tiles [stage_begin[i], stage_begin[i+1]) and attention work items
-// (row block x KV head) [attn_begin[i], attn_begin[i+1]).  Work items are
-// launched in that order, longest segments first: each one fills a CU, and
-// starting the long ones first shortens the tail when the segments differ in
-// length.
-constexpr int kMqMaxBatch = 8;
-struct MqBatch {
-  uc_kivi_item it[kMqMaxBatch];
-  MqParams p[kMqMaxBatch];
-  StageParams sp[kMqMaxBatch];
-  int64_t stage_begin[kMqMaxBatch + 1], attn_begin[kMqMaxBatch + 1];
-  int n;
-};
-static_assert(sizeof(MqBatch) <= 4096, "the batch table fits the kernel argument space");
-
-// Item of a batch that owns index x of a cumulative range table (uniform).
-__device__ __forceinline__ int batch_item(const int64_t *begin, int n, int64_t x) {
-  int i = 0;
-  while (i + 1 < n && x >= begin[i + 1]) ++i;
-  return i;
+// A pointer the compiler must treat as wave-uniform (buffer resources are
+// scalar: a value it cannot prove uniform would cost a loop over the lanes).
+__device__ __forceinline__ const char *uniform_ptr(const char *p) {
+  const uint64_t x = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x >> 32));
+  return reinterpret_cast<const char *>((uint64_t(hi) << 32) | lo);
 }
 
-// ------------------------------------------------------------- stage pass --
-// Workgroup (tile, KV head, quarter): tokens [64*tile, 64*tile + 64) of the
-// packed prefix; the tile's 256 work items are spread over kStageSplit
-// one-wave workgroups (blockIdx.z).  Arithmetic as uc_kivi_dequant: a rounded
-// multiply and a rounded add in fp32, then the cast to fp16.
-template <int BITS, int G>
-__device__ __forceinline__ void mq_stage_body(const uc_kivi_item &it, const StageParams &sp, int64_t tile) {
-  constexpr int TPW = 32 / BITS;        // codes per word
-  constexpr int KW = kTile / TPW;       // key words per channel in a tile
-  constexpr int VW = kD / TPW;          // value words per token
-  constexpr uint32_t kMask = (1u << BITS) - 1u;
-  const int tid = blockIdx.z * kStageThreads + threadIdx.x;
-  const int64_t h = blockIdx.y;
-  const int64_t t0 = tile * kTile, Tq = sp.Tq;
-  const int64_t cap = it.packed_capacity > 0 ? it.packed_capacity : Tq;  // tokens between heads
-  const uint32_t *kc = static_cast<const uint32_t *>(it.key_code) + h * (cap / TPW) * kD;
-  const uint16_t *ks = static_cast<const uint16_t *>(it.key_scale) + h * (cap / G) * kD;
-  const uint16_t *km = static_cast<const uint16_t *>(it.key_min) + h * (cap / G) * kD;
-  const uint32_t *vc = static_cast<const uint32_t *>(it.value_code) + h * cap * VW;
-  const uint16_t *vs = static_cast<const uint16_t *>(it.value_scale) + h * cap * (kD / G);
-  const uint16_t *vm = static_cast<const uint16_t *>(it.value_min) + h * cap * (kD / G);
-  uint32_t *wk = reinterpret_cast<uint32_t *>(sp.wk + h * Tq * kD);
-  _Float16 *wv = sp.wv + h * Tq * kD;
+// Tile f of a run of segments of `tokens` tokens each (uniform scan).
+template <class Seg>
+__device__ __forceinline__ TileRef find_tile(const Seg *segs, int first, int n, int f) {
+  int s = first;
+  const int last = first + n - 1;
+  while (s < last) {
+    const int tiles = (segs[s].tokens + kTile - 1) / kTile;
+    if (f < tiles) break;
+    f -= tiles;
+    ++s;
+  }
+  const int r0 = f * kTile;
+  return TileRef{s, r0, min(kTile, segs[s].tokens - r0)};
+}
 
-  // Every load of the thread is issued before any arithmetic: the packed
-  // words are cold in HBM and each thread has only a few of them.
-  // keys: item (word j of the tile, channel pair cp); a wave writes whole
-  // 256-byte rows, one per token of the word
-  constexpr int kItems = kStageSplit * kStageThreads;
-  constexpr int NK = KW * (kD / 2) / kItems, NV = kTile * VW / kItems;
-  static_assert(NK >= 1 && NV >= 1 && KW * (kD / 2) % kItems == 0 && kTile * VW % kItems == 0, "stage items");
-  uint2 kw[NK];
-  uint32_t ks2[NK], km2[NK], vw[NV];
-  uint16_t vs1[NV], vm1[NV];
+// ---------------------------------------------------------- packed tiles --
+// A half's 256 threads turn the codes of one packed 64-token tile into fp16
+// key and value rows in the tile's LDS slot.
+//   Keys: thread (cb = tid % 16, tq = tid / 16) writes tokens 4 tq .. 4 tq + 3,
+//     channels 8 cb .. 8 cb + 7 (one chunk per token): it loads the eight
+//     channels' words of the word row holding those tokens and their fp16
+//     scale and minimum pairs.  A byte permute puts the four tokens' codes of
+//     two channels into the two 16-bit halves of one register; each code pair
+//     is OR-ed into the mantissa of 1024, 1024 is subtracted exactly and one
+//     packed fp16 fma applies scale and minimum.  The 16 lanes of a store hit
+//     one whole row: no bank conflict.
+//   Values: thread (c8 = tid % 8, t = tid / 8) writes channels 16 c8 ..
+//     16 c8 + 15 (two chunks) of tokens t and t + 32 from one word pair (4-bit)
+//     or word (2-bit) per token and the token's scale and minimum.  Even and
+//     odd channels are split into two registers whose bytes a permute
+//     interleaves, giving code pairs (2j, 2j + 1) of a chunk.  Tokens t and
+//     t + 1 share a 16-lane store group; they store their two chunks in
+//     opposite orders so that the group covers all 16 chunk positions.
+// Rows past the end of the segment repeat the last valid word row or token:
+// finite values under a probability of exactly zero.
+template <int BITS>
+struct PackedRegs;
+template <>
+struct PackedRegs<2> {
+  u32x4 kw[2], ks, km;       // 8 key words; 8 scales and 8 minima (fp16 pairs)
+  uint32_t vw[2];            // value word of tokens t and t + 32
+  uint32_t vs[2], vm[2];     // the aligned dwords holding their fp16 scale and minimum
+  uint32_t vhi;              // bit k: token k's stats are the dword's upper half
+};
+template <>
+struct PackedRegs<4> {
+  u32x4 kw[2], ks, km;
+  u32x2 vw[2];               // value word pair of tokens t and t + 32
+  uint32_t vs[2], vm[2];
+  uint32_t vhi;
+};
+
+// Lane constants of the dequantizing stores (slot-relative LDS byte offsets).
+struct DeqLane {
+  uint32_t ksel;      // permute selector: the thread's four tokens of two channels
+  uint32_t kaddr[4];  // key chunk of token 4 tq + i
+  uint32_t vsel[2];   // 2-bit: permute selector of store b; 4-bit: word of store b
+  uint32_t vaddr[2];  // value chunk of store b, token t (token t + 32: + 8192)
+};
+
+template <int BITS>
+__device__ __forceinline__ DeqLane deq_lane(int tid_h) {
+  constexpr int TPW = 32 / BITS;
+  asm volatile("" : "+v"(tid_h));  // recomputed at each use, not held across the tile loop
+  const uint32_t cb = tid_h & 15, tq = tid_h >> 4;
+  const uint32_t a = 4 * (tq % (TPW / 4));  // first token of the thread within its word
+  DeqLane d;
+  if constexpr (BITS == 2)  // byte a/4 of each channel's word: tokens a .. a+3
+    d.ksel = (a / 4) | (0x0cu << 8) | ((4 + a / 4) << 16) | (0x0cu << 24);
+  else  // bytes a/2, a/2+1: tokens a .. a+3
+    d.ksel = (a / 2) | ((a / 2 + 1) << 8) | ((4 + a / 2) << 16) | ((5 + a / 2) << 24);
 #pragma unroll
-  for (int q = 0; q < NK; ++q) {
-    const int e = q * kItems + tid, cp = e % (kD / 2), j = e / (kD / 2);
-    const int64_t t = min(t0 + j * TPW, Tq - TPW);  // first token of the word (Tq is a multiple of G >= TPW)
-    const int64_t w = t / TPW, g = t / G;
-    kw[q] = *reinterpret_cast<const uint2 *>(kc + w * kD + 2 * cp);
-    ks2[q] = *reinterpret_cast<const uint32_t *>(ks + g * kD + 2 * cp);
-    km2[q] = *reinterpret_cast<const uint32_t *>(km + g * kD + 2 * cp);
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t row = 4 * tq + i;
+    d.kaddr[i] = row * 256u + 16u * (cb ^ (row & 15u));
+  }
+  const uint32_t c8 = tid_h & 7, t = tid_h >> 3, odd = t & 1;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const uint32_t half8 = odd ^ b;  // store b writes chunk 2 c8 + half8
+    d.vsel[b] = BITS == 2 ? (half8 ? 0x07060302u : 0x05040100u) : half8;
+    d.vaddr[b] = kValueBytes + t * 256u + 16u * ((2 * c8 + half8) ^ ((2 * t) & 15u));
+  }
+  return d;
+}
+
+// One KV head of a packed segment: the first byte of each tensor's rows and
+// the token count.
+struct PackedHead {
+  const char *kc, *ks, *km, *vc, *vs, *vm;
+  int tokens;
+};
+
+template <int BITS>
+__device__ __forceinline__ PackedHead packed_head(const PackedSeg &ps, int64_t h, int gshift) {
+  constexpr int TPW = 32 / BITS, VW = kD / TPW;
+  const int64_t cap = ps.cap, vstat = (kD >> gshift) * 2;
+  return PackedHead{ps.kc + h * (cap / TPW) * 512, ps.ks + h * (cap >> gshift) * 256,
+                    ps.km + h * (cap >> gshift) * 256, ps.vc + h * cap * VW * 4,
+                    ps.vs + h * cap * vstat,        ps.vm + h * cap * vstat,
+                    ps.tokens};
+}
+
+// Loads of the packed tile of rows [r0, r0 + valid) of head `ph` into registers.
+template <int BITS>
+__device__ __forceinline__ void load_packed(PackedRegs<BITS> &pr, const PackedHead &ph, int r0, int valid, int gshift,
+                                            int tid_h) {
+  constexpr int TPW = 32 / BITS, VW = kD / TPW;
+  const int64_t Tq = ph.tokens;
+  const int vstat = (kD >> gshift) * 2;  // bytes of a token's value stats
+  asm volatile("" : "+v"(tid_h));  // lane offsets recomputed here, not held across the tile loop
+  const Rsrc kc = make_rsrc(ph.kc, (Tq / TPW) * 512);
+  const Rsrc ks = make_rsrc(ph.ks, (Tq >> gshift) * 256);
+  const Rsrc km = make_rsrc(ph.km, (Tq >> gshift) * 256);
+  const Rsrc vc = make_rsrc(ph.vc, Tq * VW * 4);
+  const Rsrc vs = make_rsrc(ph.vs, Tq * vstat);
+  const Rsrc vm = make_rsrc(ph.vm, Tq * vstat);
+  const uint32_t cb = tid_h & 15, tq = tid_h >> 4;
+  const uint32_t tqc = min(tq, static_cast<uint32_t>(valid / 4 - 1));  // last existing token quad
+  // keys: word row jc of the tile, channels 8 cb ..; stats of token r0 + 4 tqc
+  // (r0 is a multiple of 64, so its group offset separates for every group size)
+  const uint32_t jc = tqc / (TPW / 4);
+  const int kso = (r0 / TPW) * 512;
+  const uint32_t kvo = jc * 512u + 32u * cb;
+  pr.kw[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kc, kvo, kso, 0));
+  pr.kw[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kc, kvo + 16u, kso, 0));
+  const int sso = (r0 >> gshift) * 256;
+  const uint32_t svo = ((4u * tqc) >> gshift) * 256u + 16u * cb;
+  pr.ks = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ks, svo, sso, 0));
+  pr.km = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(km, svo, sso, 0));
+  // values: tokens t and t + 32 (the latter clamped), channels 16 c8 ..
+  const uint32_t c8 = tid_h & 7, t = tid_h >> 3;
+  const uint32_t t1 = min(t + 32u, static_cast<uint32_t>(valid - 1));
+  const int vso = r0 * VW * 4, vsso = r0 * vstat;
+  const uint32_t g = (16u * c8) >> gshift;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t tok = k ? t1 : t;
+    if constexpr (BITS == 2)
+      pr.vw[k] = __builtin_amdgcn_raw_buffer_load_b32(vc, tok * (VW * 4) + 4u * c8, vso, 0);
+    else
+      pr.vw[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(vc, tok * (VW * 4) + 8u * c8, vso, 0));
+    // the stats' dword (the tensors' sizes are multiples of 4 bytes, so the
+    // aligned dword stays in range): no 16-bit load, whose widening would
+    // wait for the load right away
+    const uint32_t so = tok * vstat + 2u * g;
+    pr.vs[k] = __builtin_amdgcn_raw_buffer_load_b32(vs, so & ~3u, vsso, 0);
+    pr.vm[k] = __builtin_amdgcn_raw_buffer_load_b32(vm, so & ~3u, vsso, 0);
+    if (k == 0) pr.vhi = (so >> 1) & 1u;
+    else pr.vhi |= so & 2u;
+  }
+}
+
+// code pair (low BITS of each 16-bit half of x) -> code * scale + minimum.
+// `magic` holds 0x64006400 in a register, so that mask and OR are one
+// v_and_or_b32 (an instruction takes one literal).
+template <int BITS>
+__device__ __forceinline__ uint32_t deq2(uint32_t x, h2 s, h2 m, uint32_t magic) {
+  constexpr uint32_t mask = ((1u << BITS) - 1u) * 0x00010001u;
+  const h2 c = as_h2((x & mask) | magic) - h2{to_h(1024.0f), to_h(1024.0f)};
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s, m));
+}
+
+typedef __attribute__((address_space(3))) u32x4 *lds_u4w;
+
+__device__ __forceinline__ void write_chunk(uint32_t addr, u32x4 v) { *(lds_u4w)(uintptr_t)addr = v; }
+
+// Dequantize the key (store_keys) or value (store_values) registers into the
+// slot at LDS byte address `slot`.
+template <int BITS>
+__device__ __forceinline__ void store_keys(const PackedRegs<BITS> &pr, int tid_h, uint32_t slot, uint32_t magic) {
+  DeqLane dl = deq_lane<BITS>(tid_h);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(dl.kaddr[i]));
+  u32x4 o[4];  // [token i][channel pair]
+#pragma unroll
+  for (int pi = 0; pi < 4; ++pi) {
+    const uint32_t w0 = pr.kw[pi >> 1][2 * (pi & 1)], w1 = pr.kw[pi >> 1][2 * (pi & 1) + 1];
+    const uint32_t u = __builtin_amdgcn_perm(w1, w0, dl.ksel);
+    const h2 s = as_h2(pr.ks[pi]), m = as_h2(pr.km[pi]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i][pi] = deq2<BITS>(u >> (BITS * i), s, m, magic);
   }
 #pragma unroll
-  for (int q = 0; q < NV; ++q) {
-    const int e = q * kItems + tid, w = e % VW;
-    const int64_t t = min(t0 + e / VW, Tq - 1);
-    const int g = (w * TPW) / G;
-    vw[q] = vc[t * VW + w];
-    vs1[q] = vs[t * (kD / G) + g];
-    vm1[q] = vm[t * (kD / G) + g];
-  }
+  for (int i = 0; i < 4; ++i) write_chunk(slot + dl.kaddr[i], o[i]);
+}
+
+template <int BITS>
+__device__ __forceinline__ void store_values(const PackedRegs<BITS> &pr, int tid_h, uint32_t slot, uint32_t magic) {
+  DeqLane dl = deq_lane<BITS>(tid_h);
 #pragma unroll
-  for (int q = 0; q < NK; ++q) {
-    const int e = q * kItems + tid, cp = e % (kD / 2), j = e / (kD / 2);
-    const int64_t t = t0 + j * TPW;
-    if (t >= Tq) continue;
-    const float s0 = f16_bits_to_f32(ks2[q] & 0xffffu), s1 = f16_bits_to_f32(ks2[q] >> 16);
-    const float m0 = f16_bits_to_f32(km2[q] & 0xffffu), m1 = f16_bits_to_f32(km2[q] >> 16);
+  for (int b = 0; b < 2; ++b) asm volatile("" : "+v"(dl.vaddr[b]));
 #pragma unroll
-    for (int p = 0; p < TPW; ++p) {
-      const float v0 = add_rn(mul_rn(float((kw[q].x >> (p * BITS)) & kMask), s0), m0);
-      const float v1 = add_rn(mul_rn(float((kw[q].y >> (p * BITS)) & kMask), s1), m1);
-      wk[(t + p) * (kD / 2) + cp] = uint32_t(f32_to_f16_bits(v0)) | (uint32_t(f32_to_f16_bits(v1)) << 16);
+  for (int k = 0; k < 2; ++k) {
+    // the token's fp16 scale and minimum in both halves
+    const uint32_t sel = 0x01000100u + ((pr.vhi >> k) & 1u) * 0x02020202u;
+    const h2 s = as_h2(__builtin_amdgcn_perm(pr.vs[k], pr.vs[k], sel));
+    const h2 m = as_h2(__builtin_amdgcn_perm(pr.vm[k], pr.vm[k], sel));
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      u32x4 o;
+      if constexpr (BITS == 2) {
+        // channel 2j at bits 4j of ye, 2j+1 at bits 4j of yo; the permute
+        // takes the chunk's half of both
+        const uint32_t w = pr.vw[k];
+        const uint32_t ye = w & 0x33333333u, yo = (w >> 2) & 0x33333333u;
+        const uint32_t z = __builtin_amdgcn_perm(yo, ye, dl.vsel[b]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = deq2<2>(z >> (4 * j), s, m, magic);
+      } else {
+        // one word per chunk: channel 2j at byte j of ye, 2j+1 at byte j of yo
+        const uint32_t w = dl.vsel[b] ? pr.vw[k][1] : pr.vw[k][0];
+        const uint32_t ye = w & 0x0f0f0f0fu, yo = (w >> 4) & 0x0f0f0f0fu;
+        const uint32_t za = __builtin_amdgcn_perm(yo, ye, 0x05040100u), zb = __builtin_amdgcn_perm(yo, ye, 0x07060302u);
+        o[0] = deq2<4>(za, s, m, magic);
+        o[1] = deq2<4>(za >> 8, s, m, magic);
+        o[2] = deq2<4>(zb, s, m, magic);
+        o[3] = deq2<4>(zb >> 8, s, m, magic);
+      }
+      write_chunk(slot + dl.vaddr[b] + 8192u * k, o);
     }
   }
-  // values: item (token of the tile, word); TPW contiguous channels out
-#pragma unroll
-  for (int q = 0; q < NV; ++q) {
-    const int e = q * kItems + tid, w = e % VW;
-    const int64_t t = t0 + e / VW;
-    if (t >= Tq) continue;
-    const float s = f16_bits_to_f32(vs1[q]), m = f16_bits_to_f32(vm1[q]);
-    uint32_t o[TPW / 2];
-#pragma unroll
-    for (int p = 0; p < TPW; p += 2) {
-      const float v0 = add_rn(mul_rn(float((vw[q] >> (p * BITS)) & kMask), s), m);
-      const float v1 = add_rn(mul_rn(float((vw[q] >> ((p + 1) * BITS)) & kMask), s), m);
-      o[p / 2] = uint32_t(f32_to_f16_bits(v0)) | (uint32_t(f32_to_f16_bits(v1)) << 16);
-    }
-    uint4 *dst = reinterpret_cast<uint4 *>(wv + t * kD + w * TPW);
-#pragma unroll
-    for (int q2 = 0; q2 < TPW / 8; ++q2) dst[q2] = make_uint4(o[4 * q2], o[4 * q2 + 1], o[4 * q2 + 2], o[4 * q2 + 3]);
-  }
 }
 
-template <int BITS, int G>
-__global__ __launch_bounds__(kStageThreads) void mq_stage_kernel(uc_kivi_item it, StageParams sp) {
-  mq_stage_body<BITS, G>(it, sp, blockIdx.x);
-}
-
-template <int BITS, int G>
-__global__ __launch_bounds__(kStageThreads) void mq_stage_batch_kernel(MqBatch b) {
-  const int64_t tile = blockIdx.x;
-  const int i = batch_item(b.stage_begin, b.n, tile);
-  mq_stage_body<BITS, G>(b.it[i], b.sp[i], tile - b.stage_begin[i]);
-}
-
-// --------------------------------------------------------- attention pass --
 // Output is kept transposed (O^T = V^T P^T) so that every lane owns one query
 // column: the softmax rescale needs no cross-lane traffic.
 struct MqState {
@@ -370,10 +514,12 @@ __device__ __forceinline__ u32x2 read_vt(uint32_t addr) {
 }
 
 // One tile: logits, lazy online softmax, P.V for the wave's 32 query rows,
-// operands of dtype DT.
-template <int DT, int BUF>
+// operands of dtype DT.  With HOOK, hook(tp) adds independent vector work
+// (the next tile's dequantization) that is interleaved with the 16 P.V MFMAs
+// of key half tp, so that it issues while the matrix cores are busy.
+template <int DT, int BUF, bool HOOK, class Hook>
 __device__ __forceinline__ void compute_tile(FragLane fl, const u32x4 (&qf)[2][4], int valid, float scale_log2,
-                                             MqState &st) {
+                                             MqState &st, Hook &&hook) {
   constexpr uint32_t kBuf = BUF * kSlotBytes;
   // opaque to loop-invariant code motion: the constant parts of the addresses
   // below stay next to their reads and fold into the instructions' offsets
@@ -477,7 +623,17 @@ __device__ __forceinline__ void compute_tile(FragLane fl, const u32x4 (&qf)[2][4
     // keep the 16 LDS reads ahead of the 16 MFMAs (the scheduler otherwise
     // pairs each read with its MFMAs and waits on every read)
     __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    if constexpr (HOOK) {
+      hook(tp);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);
+    } else {
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    }
   }
   __builtin_amdgcn_s_setprio(0);
 }
@@ -485,16 +641,16 @@ __device__ __forceinline__ void compute_tile(FragLane fl, const u32x4 (&qf)[2][4
 // Query fragments of the wave's rows, raw (dtype QD), as the B operand of
 // S^T = K Q^T: lane (n, k) holds row row0 + 16 qb + n, channels 32 kb + 8 k ..
 // + 7.  Rows past the end are zero.
-__device__ __forceinline__ void load_queries(u32x4 (&qf)[2][4], const uc_kivi_item &it, const MqParams &p, int64_t h,
+__device__ __forceinline__ void load_queries(u32x4 (&qf)[2][4], const MqQuery &Q, const MqTable &tb, int64_t h,
                                              int64_t row0) {
   const int lane = threadIdx.x & 63, r = lane & 15, kap = lane >> 4;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int64_t row = row0 + 16 * qb + r;
-    const bool ok = row < p.rows;
-    const uint32_t gq = ok ? fast_div(static_cast<uint32_t>(row), p.lq) : 0;
-    const int64_t g = gq, i = ok ? row - int64_t(gq) * p.Lq : 0;
-    const uint16_t *q16 = static_cast<const uint16_t *>(it.query) + (i * p.Hq + h * p.group + g) * kD + 8 * kap;
+    const bool ok = row < Q.rows;
+    const uint32_t gq = ok ? fast_div(static_cast<uint32_t>(row), Q.lq) : 0;
+    const int64_t g = gq, i = ok ? row - int64_t(gq) * Q.Lq : 0;
+    const uint16_t *q16 = static_cast<const uint16_t *>(Q.query) + (i * tb.Hq + h * tb.group + g) * kD + 8 * kap;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
       qf[qb][kb] = ok ? *reinterpret_cast<const u32x4 *>(q16 + 32 * kb) : u32x4{0, 0, 0, 0};
@@ -509,30 +665,28 @@ __device__ __forceinline__ void convert_queries(u32x4 (&qf)[2][4]) {
     for (int kb = 0; kb < 4; ++kb) qf[qb][kb] = convert8<FROM, TO>(qf[qb][kb]);
 }
 
-// Work item w = h * row_blocks + rb of one segment: 128 query rows of KV head h.
-// Tiles [0, nq) are the staged prefix (fp16), tiles [nq, nq + nd) the dense
-// keys (dtype RD).
-template <int QD, int RD, int OD>
-__device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const MqParams &p, int64_t w) {
+// Work item of query Q: 128 query rows (row block rb) of KV head h over every
+// segment of the query.  Each half takes half of the packed tiles (fp16
+// operands) and then dense tiles (dtype RD) up to n0 = ceil(tiles / 2) for
+// the first half.
+template <int BITS, int QD, int RD, int OD>
+__device__ __forceinline__ void mq_attention_body(const MqTable &tb, const MqQuery &Q, int64_t h, int64_t rb) {
   __shared__ __align__(16) MqShared sh;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: tile choices stay scalar
   const int half = wave / kHalfWaves, hw = wave % kHalfWaves;
+  const int tid_h = tid - half * kHalfThreads;
   const int r = lane & 15, kap = lane >> 4;
-  const int64_t h = w / p.row_blocks;
-  const int64_t row0 = (w % p.row_blocks) * kMqRows + hw * kRowsPerWave;
+  const int64_t row0 = rb * kMqRows + hw * kRowsPerWave;
 
-  const RowSrc pre = make_src(p.wk + h * p.Tq * kD, p.wv + h * p.Tq * kD, p.Tq, kD * 2);
-  const RowSrc den = p.Tr > 0 ? make_src(static_cast<const uint16_t *>(it.residual_key) + h * kD,
-                                         static_cast<const uint16_t *>(it.residual_value) + h * kD, p.Tr,
-                                         p.Hkv * kD * 2)
-                              : pre;
-  const int n_tiles = p.nq + p.nd;
-  const int n0 = (n_tiles + 1) / 2;  // tiles of the first half (the longer one)
-  const int first = half ? n0 : 0;
-  const int count = half ? n_tiles - n0 : n0;
+  const int n_tiles = Q.pt + Q.dt, n0 = (n_tiles + 1) / 2;
+  const int q0 = (Q.pt + 1) / 2, d0 = n0 - q0;  // the first half's packed and dense tiles
+  const int pb = half ? q0 : 0, db = half ? d0 : 0;
+  const int n_pre = half ? Q.pt - q0 : q0;
+  const int count = n_pre + (half ? Q.dt - d0 : d0);
   const uint32_t sh_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char *)&sh));
-  const FragLane fl = frag_lane(sh_base + half * 2 * kSlotBytes);
+  const uint32_t half_base = sh_base + half * 2 * kSlotBytes;
+  const FragLane fl = frag_lane(half_base);
 
   MqState st;
 #pragma unroll
@@ -543,31 +697,87 @@ __device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const 
     st.l[qb] = 0.0f;
   }
 
-  // tile t: its source, first source row and valid rows
-  auto tile_src = [&](int t, int64_t &r0, int &valid) -> const RowSrc & {
-    const bool d = t >= p.nq;
-    r0 = int64_t(d ? t - p.nq : t) * kTile;
-    valid = static_cast<int>(min<int64_t>(kTile, (d ? p.Tr : p.Tq) - r0));
-    return d ? den : pre;
+  // Cursors over the half's tiles, kept in registers: the dense segment and
+  // first row of the next dense tile, the packed segment (its head) and first
+  // row of the next packed tile.  Segment records are read from the launch
+  // table only when a cursor enters a new segment.
+  int dseg = Q.d0, dr0 = 0, drows = 0, dbytes = 0;
+  const char *dk = nullptr, *dv = nullptr;
+  auto dense_seg = [&](int sidx) {
+    const DenseSeg &ds = tb.ds[sidx];
+    dk = ds.k + h * ds.head_bytes;
+    dv = ds.v + h * ds.head_bytes;
+    drows = ds.tokens;
+    dbytes = static_cast<int>(ds.tok_bytes);
   };
-  const DmaLane dl_pre = dma_lane(pre.row_bytes), dl_den = dma_lane(den.row_bytes);
-  auto issue = [&](int t, int buf) {
-    int64_t r0;
-    int valid;
-    const RowSrc &s = tile_src(t, r0, valid);
-    issue_tile(reinterpret_cast<uint4 *>(sh.slot[half][buf]), s, t >= p.nq ? dl_den : dl_pre, r0, valid, hw);
+  if (count > n_pre) {
+    const TileRef tr = find_tile(tb.ds, Q.d0, Q.nd, db);
+    dseg = tr.seg;
+    dr0 = tr.r0;
+    dense_seg(dseg);
+  }
+  // next dense tile into buffer buf; returns its valid rows
+  auto issue_dense = [&](int buf) {
+    const int rows = __builtin_amdgcn_readfirstlane(drows), row_bytes = __builtin_amdgcn_readfirstlane(dbytes);
+    const int r0 = __builtin_amdgcn_readfirstlane(dr0);
+    const RowSrc src = make_src(uniform_ptr(dk), uniform_ptr(dv), rows, row_bytes);
+    const int valid = min(kTile, rows - r0);
+    issue_tile(reinterpret_cast<uint4 *>(sh.slot[half][buf]), src, dma_lane(src.row_bytes), r0, valid, hw);
+    dr0 = r0 + kTile;
+    if (dr0 >= rows && dseg + 1 < Q.d0 + Q.nd) {
+      dr0 = 0;
+      dense_seg(++dseg);
+    }
+    return valid;
   };
+  int pseg = Q.p0, pr0 = 0;
+  PackedHead ph{};
+  if (n_pre > 0) {
+    const TileRef tr = find_tile(tb.ps, Q.p0, Q.np, pb);
+    pseg = tr.seg;
+    pr0 = tr.r0;
+    ph = packed_head<BITS>(tb.ps[pseg], h, tb.gshift);
+  }
+  PackedRegs<BITS> pr;
+  // loads of the next packed tile; returns its valid rows
+  auto load_tile = [&]() {
+    const PackedHead u{uniform_ptr(ph.kc), uniform_ptr(ph.ks), uniform_ptr(ph.km), uniform_ptr(ph.vc),
+                       uniform_ptr(ph.vs), uniform_ptr(ph.vm), __builtin_amdgcn_readfirstlane(ph.tokens)};
+    const int r0 = __builtin_amdgcn_readfirstlane(pr0);
+    const int valid = min(kTile, u.tokens - r0);
+    load_packed<BITS>(pr, u, r0, valid, tb.gshift, tid_h);
+    pr0 = r0 + kTile;
+    if (pr0 >= u.tokens && pseg + 1 < Q.p0 + Q.np) {
+      pr0 = 0;
+      ph = packed_head<BITS>(tb.ps[++pseg], h, tb.gshift);
+    }
+    return valid;
+  };
+
   // The first half loads the rows' query fragments and hands them to the
   // wave with the same rows in the second half through LDS (buffer 1 of the
   // first half, free until step 0), so each query row is read once.
+  uint32_t magic = 0x64006400u;  // fp16 1024 in both halves, held in a register
+  asm volatile("" : "+v"(magic));
+  const int n_dense = count - n_pre;
+  // Each half runs its packed tiles first, then its dense ones.  The first
+  // half loads the rows' query fragments and hands them to the wave with the
+  // same rows in the second half through LDS (buffer 1 of the first half,
+  // free until step 0), so each query row is read once.
+  int cur_valid = 0;  // rows of the tile in the buffer the next step computes
+  if (n_pre > 0) cur_valid = load_tile();
+  else if (count > 0) cur_valid = issue_dense(0);
   u32x4 qf[2][4];
-  if (count > 0) issue(first, 0);
   {
     u32x4 *qs = reinterpret_cast<u32x4 *>(sh.slot[0][1]) + hw * 8 * kWave + lane;
     if (half == 0) {
-      load_queries(qf, it, p, h, row0);
+      load_queries(qf, Q, tb, h, row0);
 #pragma unroll
       for (int j = 0; j < 8; ++j) qs[j * kWave] = qf[j / 4][j % 4];
+    }
+    if (n_pre > 0) {
+      store_keys<BITS>(pr, tid_h, half_base, magic);
+      store_values<BITS>(pr, tid_h, half_base, magic);
     }
     __syncthreads();
     if (half == 1) {
@@ -575,43 +785,54 @@ __device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const 
       for (int j = 0; j < 8; ++j) qf[j / 4][j % 4] = qs[j * kWave];
     }
   }
-  const bool dense_first = first >= p.nq;  // this half starts with dense tiles
-  if (dense_first) convert_queries<QD, RD>(qf);
-  else convert_queries<QD, UC_FP16>(qf);
+  if (n_pre > 0) convert_queries<QD, UC_FP16>(qf);
+  else convert_queries<QD, RD>(qf);
 
-  // Step i: wait for tile first + i, start loading tile first + i + 1 into
-  // the other buffer, compute tile first + i (steps past `count` only keep
-  // the barrier count of the two halves equal).
-  auto step = [&](int i, auto dt_tag, auto buf_tag) {
+  // Step i: wait for tile i (in buffer i & 1), start bringing tile i + 1 into
+  // the other buffer (packed: its loads now, its dequantizing stores
+  // interleaved with tile i's P.V MFMAs), compute tile i (steps past `count`
+  // only keep the barrier count of the two halves equal).  NEXT_PACKED: tile
+  // i + 1 is packed.
+  auto step = [&](int i, auto dt_tag, auto buf_tag, auto packed_tag) {
     constexpr int DT = decltype(dt_tag)::value, BUF = decltype(buf_tag)::value;
+    constexpr bool NEXT_PACKED = decltype(packed_tag)::value;
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's loads of tile i are in LDS
     __syncthreads();                     // ... and everyone's; buffer BUF ^ 1 is free again
-    if (i + 1 < count) issue(first + i + 1, BUF ^ 1);
+    int next_valid = 0;
+    if constexpr (NEXT_PACKED) next_valid = load_tile();
+    else if (i + 1 < count) next_valid = issue_dense(BUF ^ 1);
+    const uint32_t next_slot = half_base + (BUF ^ 1) * kSlotBytes;
+    auto hook = [&](int tp) {
+      if (tp == 0) store_keys<BITS>(pr, tid_h, next_slot, magic);
+      else store_values<BITS>(pr, tid_h, next_slot, magic);
+    };
     if (i < count) {
-      int64_t r0;
-      int valid;
-      tile_src(first + i, r0, valid);
-      compute_tile<DT, BUF>(fl, qf, valid, p.scale_log2, st);
+      // a packed tile's dequantization rides in the P.V MFMAs of the
+      // previous (packed) tile
+      compute_tile<DT, BUF, NEXT_PACKED>(fl, qf, cur_valid, tb.scale_log2, st, hook);
     }
+    cur_valid = next_valid;
   };
   // steps [i, end) with operands of dtype DT, buffer i & 1, two per round
   int i = 0;
-  auto run = [&](auto dt_tag, int end) {
-    if (i < end && (i & 1)) step(i++, dt_tag, std::integral_constant<int, 1>{});
+  auto run = [&](auto dt_tag, auto packed_tag, int end) {
+    if (i < end && (i & 1)) step(i++, dt_tag, std::integral_constant<int, 1>{}, packed_tag);
     for (; i + 1 < end; i += 2) {
-      step(i, dt_tag, std::integral_constant<int, 0>{});
-      step(i + 1, dt_tag, std::integral_constant<int, 1>{});
+      step(i, dt_tag, std::integral_constant<int, 0>{}, packed_tag);
+      step(i + 1, dt_tag, std::integral_constant<int, 1>{}, packed_tag);
     }
-    if (i < end) step(i++, dt_tag, std::integral_constant<int, 0>{});
+    if (i < end) step(i++, dt_tag, std::integral_constant<int, 0>{}, packed_tag);
   };
-  // both halves run n0 steps (the barrier is shared): the prefix tiles of this
+  // both halves run n0 steps (the barrier is shared): the packed tiles of this
   // half with fp16 operands, then its dense tiles in their own dtype (the
   // fp16 fragments go back to the dense dtype: exact when it is fp16, and for
   // bf16 queries whose values fp16 holds)
-  const int n_pre = static_cast<int>(max(0, min(count, p.nq - first)));
-  run(std::integral_constant<int, UC_FP16>{}, n_pre);
-  if (n_pre < count && !dense_first) convert_queries<UC_FP16, RD>(qf);
-  run(std::integral_constant<int, RD>{}, n0);
+  using F16 = std::integral_constant<int, UC_FP16>;
+  using DR = std::integral_constant<int, RD>;
+  run(F16{}, std::true_type{}, n_pre - 1);
+  run(F16{}, std::false_type{}, n_pre);
+  if (n_pre > 0 && n_dense > 0) convert_queries<UC_FP16, RD>(qf);
+  run(DR{}, std::false_type{}, n0);
   __syncthreads();  // every wave is done reading its last tile
 
   // merge: the second half hands (O^T, m, l) of its lanes to the wave with the
@@ -648,9 +869,9 @@ __device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const 
           store_from_f32<OD>(ob, (16 * qb + r) * kRowPad + 16 * cb + 4 * kap + v, o * inv);
         }
       const int64_t row = row0 + 16 * qb + r;
-      if (kap == 0 && row < p.rows && it.lse != nullptr) {
+      if (kap == 0 && row < Q.rows && Q.lse != nullptr) {
         // (h * group + g) * Lq + i = h * rows + row
-        it.lse[h * p.rows + row] = l > 0.0f ? (M + log2f(l)) * kLn2 : kNegInf;
+        Q.lse[h * Q.rows + row] = l > 0.0f ? (M + log2f(l)) * kLn2 : kNegInf;
       }
     }
   }
@@ -663,33 +884,30 @@ __device__ __forceinline__ void mq_attention_body(const uc_kivi_item &it, const 
     for (int q = 0; q < kRowsPerWave / 2 * kPerRow / kWave; ++q) {
       const int idx = q * kWave + lane, rr = half * (kRowsPerWave / 2) + idx / kPerRow, cc = (idx % kPerRow) * kChunk;
       const int64_t row = row0 + rr;
-      if (row >= p.rows) continue;
-      const uint32_t gq = fast_div(static_cast<uint32_t>(row), p.lq);
-      const int64_t g = gq, i = row - int64_t(gq) * p.Lq;
-      *reinterpret_cast<uint4 *>(static_cast<OutT *>(it.out) + (i * p.Hq + h * p.group + g) * kD + cc) =
+      if (row >= Q.rows) continue;
+      const uint32_t gq = fast_div(static_cast<uint32_t>(row), Q.lq);
+      const int64_t g = gq, i = row - int64_t(gq) * Q.Lq;
+      *reinterpret_cast<uint4 *>(static_cast<OutT *>(Q.out) + (i * tb.Hq + h * tb.group + g) * kD + cc) =
           *reinterpret_cast<const uint4 *>(&obw[rr * kRowPad + cc]);
     }
   }
 }
 
-// Workgroups are dealt to the 8 XCDs round-robin by launch index; work item w
-// goes to index 8 * (w % per_xcd) + w / per_xcd, so each XCD serves a
-// contiguous run of row blocks -- mostly of one KV head of one segment, whose
-// keys and values its own L2 then holds.
-template <int QD, int RD, int OD>
+// Launch slot id runs on XCD x = id % 8 as that XCD's slot j = id / 8.  Each
+// query owns slots [slot0, slot0 + per_xcd) of every XCD, and XCD x serves its
+// work items x * per_xcd .. (row blocks of KV head h at h * row_blocks ..): a
+// contiguous run, mostly of one KV head, whose keys and values its own L2
+// then holds, and one eighth of every query.  Queries come longest first.
+template <int BITS, int QD, int RD, int OD>
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void mq_attention_kernel(
-    uc_kivi_item it, MqParams p) {
-  const int64_t id = blockIdx.x, w = (id % kXcds) * p.per_xcd + id / kXcds;
-  if (w >= p.row_blocks * p.Hkv) return;  // uniform: the whole workgroup leaves
-  mq_attention_body<QD, RD, OD>(it, p, w);
-}
-
-template <int QD, int RD, int OD>
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void mq_attention_batch_kernel(
-    MqBatch b) {
-  const int64_t w = blockIdx.x;
-  const int i = batch_item(b.attn_begin, b.n, w);
-  mq_attention_body<QD, RD, OD>(b.it[i], b.p[i], w - b.attn_begin[i]);
+    MqTable tb) {
+  const int x = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+  int qi = 0;
+  while (qi + 1 < tb.n_queries && j >= tb.q[qi + 1].slot0) ++qi;
+  const MqQuery &Q = tb.q[qi];
+  const int w = x * Q.per_xcd + (j - Q.slot0);
+  if (w >= Q.row_blocks * tb.Hkv) return;  // uniform: the whole workgroup leaves
+  mq_attention_body<BITS, QD, RD, OD>(tb, Q, w / Q.row_blocks, w % Q.row_blocks);
 }
 
 }  // namespace
@@ -700,7 +918,7 @@ using namespace uc;
 extern "C" int64_t uc_kivi_mq_workspace_bytes(int64_t heads_kv, int64_t head_dim, int64_t quantized_tokens,
                                               int64_t residual_tokens) {
   if (heads_kv <= 0 || head_dim <= 0 || quantized_tokens < 0 || residual_tokens < 0) return -1;
-  return 2 * heads_kv * quantized_tokens * head_dim * int64_t(sizeof(_Float16));
+  return 0;  // the packed codes are dequantized inside the attention kernel
 }
 
 namespace uc {
@@ -709,32 +927,24 @@ namespace {
 template <int V>
 using IC = std::integral_constant<int, V>;
 
-// Calls f(IC<bits>, IC<group>) for the stage kernels.
+// Calls f(IC<bits>, IC<query dtype>, IC<dense dtype>, IC<out dtype>).
 template <class F>
-void stage_config(int bits, int group_size, F &&f) {
-  auto by_group = [&](auto b) {
-    if (group_size == 32) f(b, IC<32>{});
-    else if (group_size == 64) f(b, IC<64>{});
-    else f(b, IC<128>{});
+void attn_config(int bits, int q_dtype, int res_dtype, int out_dtype, F &&f) {
+  auto by_out = [&](auto b, auto qd, auto rd) {
+    if (out_dtype == UC_BF16) f(b, qd, rd, IC<UC_BF16>{});
+    else if (out_dtype == UC_FP16) f(b, qd, rd, IC<UC_FP16>{});
+    else f(b, qd, rd, IC<UC_FP32>{});
   };
-  if (bits == 2) by_group(IC<2>{});
-  else by_group(IC<4>{});
-}
-
-// Calls f(IC<query dtype>, IC<dense dtype>, IC<out dtype>) for the attention kernels.
-template <class F>
-void attn_config(int q_dtype, int res_dtype, int out_dtype, F &&f) {
-  auto by_out = [&](auto qd, auto rd) {
-    if (out_dtype == UC_BF16) f(qd, rd, IC<UC_BF16>{});
-    else if (out_dtype == UC_FP16) f(qd, rd, IC<UC_FP16>{});
-    else f(qd, rd, IC<UC_FP32>{});
+  auto by_res = [&](auto b, auto qd) {
+    if (res_dtype == UC_FP16) by_out(b, qd, IC<UC_FP16>{});
+    else by_out(b, qd, IC<UC_BF16>{});
   };
-  auto by_res = [&](auto qd) {
-    if (res_dtype == UC_FP16) by_out(qd, IC<UC_FP16>{});
-    else by_out(qd, IC<UC_BF16>{});
+  auto by_q = [&](auto b) {
+    if (q_dtype == UC_FP16) by_res(b, IC<UC_FP16>{});
+    else by_res(b, IC<UC_BF16>{});
   };
-  if (q_dtype == UC_FP16) by_res(IC<UC_FP16>{});
-  else by_res(IC<UC_BF16>{});
+  if (bits == 2) by_q(IC<2>{});
+  else by_q(IC<4>{});
 }
 
 int mq_check_config(int bits, int group_size, int64_t heads_q, int64_t heads_kv, int64_t head_dim, int q_dtype,
@@ -753,55 +963,145 @@ int mq_check_config(int bits, int group_size, int64_t heads_q, int64_t heads_kv,
   return UC_OK;
 }
 
-int mq_check_item(const uc_kivi_item &it, int group_size, int64_t heads_q, int64_t heads_kv, int64_t query_len) {
-  UC_REQUIRE(query_len > 0 && query_len * (heads_q / heads_kv) < (int64_t(1) << 31),
-             "attn_mq: query_len must be positive and query rows per KV head below 2^31");
-  UC_REQUIRE(it.quantized_tokens >= 0 && it.residual_tokens >= 0 && it.quantized_tokens % group_size == 0,
-             "attn_mq: quantized tokens must be a non-negative multiple of group_size");
-  UC_REQUIRE(it.quantized_tokens + it.residual_tokens > 0, "attn_mq: empty segment");
-  UC_REQUIRE(it.packed_capacity == 0 ||
-                 (it.packed_capacity >= it.quantized_tokens && it.packed_capacity % group_size == 0),
-             "attn_mq: packed_capacity must be 0 or a multiple of group_size >= quantized_tokens");
-  UC_REQUIRE(it.query != nullptr && it.out != nullptr, "attn_mq: query/out are NULL");
-  UC_REQUIRE((reinterpret_cast<uintptr_t>(it.query) & 15) == 0 && (reinterpret_cast<uintptr_t>(it.out) & 15) == 0,
-             "attn_mq: query and out must be 16-byte aligned");
-  UC_REQUIRE(it.quantized_tokens == 0 || (it.key_code && it.key_scale && it.key_min && it.value_code &&
-                                          it.value_scale && it.value_min),
-             "attn_mq: packed tensors are NULL");
-  UC_REQUIRE(it.residual_tokens == 0 || (it.residual_key && it.residual_value), "attn_mq: residual is NULL");
-  UC_REQUIRE(it.residual_tokens == 0 || ((reinterpret_cast<uintptr_t>(it.residual_key) & 15) == 0 &&
-                                         (reinterpret_cast<uintptr_t>(it.residual_value) & 15) == 0),
-             "attn_mq: residual keys and values must be 16-byte aligned");
-  // buffer offsets are 32-bit: a head's staged rows and the dense rows' span
-  UC_REQUIRE(it.quantized_tokens * mf::kD * 2 < (int64_t(1) << 31) &&
-                 it.residual_tokens * heads_kv * mf::kD * 2 < (int64_t(1) << 31),
-             "attn_mq: segment too long for 32-bit buffer offsets");
-  return UC_OK;
-}
+constexpr int64_t kOffsetLimit = int64_t(1) << 31;  // buffer offsets are 32-bit
 
-// Stage and attention parameters of one segment whose staged K and V start at ws.
-void mq_fill(const uc_kivi_item &it, int64_t heads_q, int64_t heads_kv, int64_t query_len, float sm_scale,
-             _Float16 *ws, StageParams &sp, MqParams &p) {
-  sp = StageParams{};
-  sp.Tq = it.quantized_tokens;
-  sp.wk = ws;
-  sp.wv = ws + heads_kv * sp.Tq * mf::kD;
-  p = MqParams{};
-  p.Hq = heads_q;
-  p.Hkv = heads_kv;
-  p.Lq = query_len;
-  p.group = heads_q / heads_kv;
-  p.rows = p.group * query_len;
-  p.Tq = it.quantized_tokens;
-  p.Tr = it.residual_tokens;
-  p.nq = static_cast<int>(ceil_div(p.Tq, int64_t(kTile)));
-  p.nd = static_cast<int>(ceil_div(p.Tr, int64_t(kTile)));
-  p.scale_log2 = sm_scale * kLog2e;
-  p.wk = sp.wk;
-  p.wv = sp.wv;
-  p.row_blocks = ceil_div(p.rows, int64_t(kMqRows));
-  p.lq = make_fastdiv(static_cast<uint32_t>(query_len));
-  p.per_xcd = ceil_div(p.row_blocks * heads_kv, int64_t(kXcds));
+// Launch table under construction: segments are appended per query.
+struct TableBuilder {
+  MqTable t{};
+  int64_t heads_q, heads_kv;
+  int group_size;
+
+  int add_packed(const uc_kivi_item &it) {
+    UC_REQUIRE(it.quantized_tokens >= 0 && it.quantized_tokens % group_size == 0,
+               "attn_mq: quantized tokens must be a non-negative multiple of group_size");
+    if (it.quantized_tokens == 0) return UC_OK;
+    UC_REQUIRE(it.packed_capacity == 0 ||
+                   (it.packed_capacity >= it.quantized_tokens && it.packed_capacity % group_size == 0),
+               "attn_mq: packed_capacity must be 0 or a multiple of group_size >= quantized_tokens");
+    UC_REQUIRE(it.key_code && it.key_scale && it.key_min && it.value_code && it.value_scale && it.value_min,
+               "attn_mq: packed tensors are NULL");
+    const uintptr_t any_odd = reinterpret_cast<uintptr_t>(it.key_code) | reinterpret_cast<uintptr_t>(it.key_scale) |
+                              reinterpret_cast<uintptr_t>(it.key_min) | reinterpret_cast<uintptr_t>(it.value_code) |
+                              reinterpret_cast<uintptr_t>(it.value_scale) | reinterpret_cast<uintptr_t>(it.value_min);
+    UC_REQUIRE((any_odd & 3) == 0, "attn_mq: packed tensors must be 4-byte aligned");
+    // largest per-head extent: 4-bit value words, 64 bytes per token
+    UC_REQUIRE(it.quantized_tokens * 64 < kOffsetLimit, "attn_mq: packed segment too long for 32-bit offsets");
+    int n = 0;
+    for (int q = 0; q < t.n_queries; ++q) n += t.q[q].np;
+    UC_REQUIRE(n < kMqMaxPacked, "attn_mq: more than %d packed segments in one call", kMqMaxPacked);
+    PackedSeg &s = t.ps[n];
+    s.kc = static_cast<const char *>(it.key_code);
+    s.ks = static_cast<const char *>(it.key_scale);
+    s.km = static_cast<const char *>(it.key_min);
+    s.vc = static_cast<const char *>(it.value_code);
+    s.vs = static_cast<const char *>(it.value_scale);
+    s.vm = static_cast<const char *>(it.value_min);
+    s.cap = it.packed_capacity > 0 ? it.packed_capacity : it.quantized_tokens;
+    s.tokens = static_cast<int>(it.quantized_tokens);
+    MqQuery &q = t.q[t.n_queries - 1];
+    ++q.np;
+    q.pt += static_cast<int>(ceil_div(it.quantized_tokens, kTile));
+    return UC_OK;
+  }
+
+  // dense rows; strides in bytes
+  int add_dense(const void *k, const void *v, int64_t tokens, int64_t tok_bytes, int64_t head_bytes) {
+    UC_REQUIRE(tokens >= 0, "attn_mq: negative dense token count");
+    if (tokens == 0) return UC_OK;
+    UC_REQUIRE(k != nullptr && v != nullptr, "attn_mq: dense keys or values are NULL");
+    UC_REQUIRE((reinterpret_cast<uintptr_t>(k) & 15) == 0 && (reinterpret_cast<uintptr_t>(v) & 15) == 0 &&
+                   tok_bytes % 16 == 0 && head_bytes % 16 == 0 && tok_bytes > 0 && head_bytes >= 0,
+               "attn_mq: dense keys and values must be 16-byte aligned with 16-byte token and head strides");
+    UC_REQUIRE((tokens - 1) * tok_bytes + mf::kD * 2 < kOffsetLimit,
+               "attn_mq: dense segment too long for 32-bit offsets");
+    int n = 0;
+    for (int q = 0; q < t.n_queries; ++q) n += t.q[q].nd;
+    UC_REQUIRE(n < kMqMaxDense, "attn_mq: more than %d dense segments in one call", kMqMaxDense);
+    DenseSeg &s = t.ds[n];
+    s.k = static_cast<const char *>(k);
+    s.v = static_cast<const char *>(v);
+    s.tok_bytes = tok_bytes;
+    s.head_bytes = head_bytes;
+    s.tokens = static_cast<int>(tokens);
+    MqQuery &q = t.q[t.n_queries - 1];
+    ++q.nd;
+    q.dt += static_cast<int>(ceil_div(tokens, kTile));
+    return UC_OK;
+  }
+
+  int begin_query(const void *query, void *out, float *lse, int64_t query_len) {
+    UC_REQUIRE(t.n_queries < kMqMaxQueries, "attn_mq: more than %d queries in one call", kMqMaxQueries);
+    UC_REQUIRE(query_len > 0 && query_len * (heads_q / heads_kv) < kOffsetLimit,
+               "attn_mq: query_len must be positive and query rows per KV head below 2^31");
+    UC_REQUIRE(query != nullptr && out != nullptr, "attn_mq: query/out are NULL");
+    UC_REQUIRE((reinterpret_cast<uintptr_t>(query) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+               "attn_mq: query and out must be 16-byte aligned");
+    int p0 = 0, d0 = 0;
+    for (int q = 0; q < t.n_queries; ++q) {
+      p0 += t.q[q].np;
+      d0 += t.q[q].nd;
+    }
+    MqQuery &q = t.q[t.n_queries++];
+    q = MqQuery{};
+    q.query = query;
+    q.out = out;
+    q.lse = lse;
+    q.Lq = query_len;
+    q.rows = (heads_q / heads_kv) * query_len;
+    q.lq = make_fastdiv(static_cast<uint32_t>(query_len));
+    q.p0 = p0;
+    q.d0 = d0;
+    return UC_OK;
+  }
+
+  // Adds the packed prefix and residual of `it` to the current query.
+  int add_item(const uc_kivi_item &it) {
+    UC_REQUIRE(it.residual_tokens >= 0, "attn_mq: negative residual token count");
+    int rc = add_packed(it);
+    if (rc != UC_OK) return rc;
+    return add_dense(it.residual_key, it.residual_value, it.residual_tokens, heads_kv * mf::kD * 2, mf::kD * 2);
+  }
+
+  int end_query() {
+    MqQuery &q = t.q[t.n_queries - 1];
+    UC_REQUIRE(q.pt + q.dt > 0, "attn_mq: empty segment");
+    const int64_t row_blocks = ceil_div(q.rows, int64_t(kMqRows));
+    UC_REQUIRE(row_blocks * heads_kv < kOffsetLimit, "attn_mq: launch too large");
+    q.row_blocks = static_cast<int>(row_blocks);
+    q.per_xcd = static_cast<int>(ceil_div(row_blocks * heads_kv, int64_t(kXcds)));
+    return UC_OK;
+  }
+
+  // Orders the queries longest first (segments stay where they are), assigns
+  // the launch slots and returns the grid size.
+  int64_t finish(float sm_scale) {
+    const auto work = [](const MqQuery &q) { return int64_t(q.pt + q.dt) * q.rows; };
+    for (int i = 1; i < t.n_queries; ++i)
+      for (int j = i; j > 0 && work(t.q[j]) > work(t.q[j - 1]); --j) std::swap(t.q[j], t.q[j - 1]);
+    int slots = 0;
+    for (int i = 0; i < t.n_queries; ++i) {
+      t.q[i].slot0 = slots;
+      slots += t.q[i].per_xcd;
+    }
+    t.Hkv = static_cast<int>(heads_kv);
+    t.Hq = heads_q;
+    t.group = static_cast<int>(heads_q / heads_kv);
+    t.gshift = group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
+    t.scale_log2 = sm_scale * kLog2e;
+    return int64_t(slots) * kXcds;
+  }
+};
+
+int mq_launch(TableBuilder &b, int bits, int q_dtype, int res_dtype, int out_dtype, float sm_scale,
+              hipStream_t stream, const char *what) {
+  const int64_t grid = b.finish(sm_scale);
+  UC_REQUIRE(grid < kOffsetLimit, "%s: launch too large", what);
+  attn_config(bits, q_dtype, res_dtype, out_dtype, [&](auto bb, auto qd, auto rd, auto od) {
+    hipLaunchKernelGGL((mq_attention_kernel<decltype(bb)::value, decltype(qd)::value, decltype(rd)::value,
+                                            decltype(od)::value>),
+                       dim3(static_cast<unsigned>(grid)), dim3(kAttnThreads), 0, stream, b.t);
+  });
+  return check_launch(what);
 }
 
 }  // namespace
@@ -811,91 +1111,68 @@ extern "C" int uc_kivi_attn_mq(const uc_kivi_item *item_host, int bits, int grou
                                int64_t heads_kv, int64_t head_dim, int64_t query_len, int q_dtype, int res_dtype,
                                int out_dtype, float sm_scale, void *workspace, int64_t workspace_bytes,
                                uc_stream_t stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  (void)workspace;
+  (void)workspace_bytes;
   UC_REQUIRE(item_host != nullptr, "attn_mq: item is NULL");
-  const uc_kivi_item it = *item_host;
   int rc = mq_check_config(bits, group_size, heads_q, heads_kv, head_dim, q_dtype, res_dtype, out_dtype, sm_scale);
   if (rc != UC_OK) return rc;
-  rc = mq_check_item(it, group_size, heads_q, heads_kv, query_len);
-  if (rc != UC_OK) return rc;
-  const int64_t need = uc_kivi_mq_workspace_bytes(heads_kv, head_dim, it.quantized_tokens, it.residual_tokens);
-  UC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need &&
-                           (reinterpret_cast<uintptr_t>(workspace) & 15) == 0),
-             "attn_mq: workspace too small or misaligned (%lld < %lld bytes)", (long long)workspace_bytes,
-             (long long)need);
-  StageParams sp;
-  MqParams p;
-  mq_fill(it, heads_q, heads_kv, query_len, sm_scale, static_cast<_Float16 *>(workspace), sp, p);
-  if (p.nq > 0) {
-    const dim3 sgrid(static_cast<unsigned>(p.nq), static_cast<unsigned>(heads_kv), kStageSplit);
-    stage_config(bits, group_size, [&](auto b, auto g) {
-      hipLaunchKernelGGL((mq_stage_kernel<decltype(b)::value, decltype(g)::value>), sgrid, dim3(kStageThreads), 0,
-                         stream, it, sp);
-    });
-    rc = check_launch("attn_mq (stage)");
-    if (rc != UC_OK) return rc;
-  }
-  const dim3 grid(static_cast<unsigned>(p.per_xcd * kXcds));
-  attn_config(q_dtype, res_dtype, out_dtype, [&](auto qd, auto rd, auto od) {
-    hipLaunchKernelGGL((mq_attention_kernel<decltype(qd)::value, decltype(rd)::value, decltype(od)::value>), grid,
-                       dim3(kAttnThreads), 0, stream, it, p);
-  });
-  return check_launch("attn_mq");
+  TableBuilder b;
+  b.heads_q = heads_q;
+  b.heads_kv = heads_kv;
+  b.group_size = group_size;
+  const uc_kivi_item &it = *item_host;
+  if ((rc = b.begin_query(it.query, it.out, it.lse, query_len)) != UC_OK) return rc;
+  if ((rc = b.add_item(it)) != UC_OK) return rc;
+  if ((rc = b.end_query()) != UC_OK) return rc;
+  return mq_launch(b, bits, q_dtype, res_dtype, out_dtype, sm_scale, static_cast<hipStream_t>(stream_), "attn_mq");
 }
 
 extern "C" int uc_kivi_attn_mq_batch(const uc_kivi_item *items_host, const int64_t *query_lens, int n_items,
                                      int bits, int group_size, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
                                      int q_dtype, int res_dtype, int out_dtype, float sm_scale, void *workspace,
                                      int64_t workspace_bytes, uc_stream_t stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
-  UC_REQUIRE(n_items >= 1 && n_items <= kMqMaxBatch, "attn_mq_batch: n_items must be 1..%d (got %d)", kMqMaxBatch,
-             n_items);
+  (void)workspace;
+  (void)workspace_bytes;
+  UC_REQUIRE(n_items >= 1 && n_items <= kMqMaxQueries, "attn_mq_batch: n_items must be 1..%d (got %d)",
+             kMqMaxQueries, n_items);
   UC_REQUIRE(items_host != nullptr && query_lens != nullptr, "attn_mq_batch: items or query_lens is NULL");
   int rc = mq_check_config(bits, group_size, heads_q, heads_kv, head_dim, q_dtype, res_dtype, out_dtype, sm_scale);
   if (rc != UC_OK) return rc;
-  int64_t need = 0;
+  TableBuilder b;
+  b.heads_q = heads_q;
+  b.heads_kv = heads_kv;
+  b.group_size = group_size;
   for (int i = 0; i < n_items; ++i) {
-    rc = mq_check_item(items_host[i], group_size, heads_q, heads_kv, query_lens[i]);
-    if (rc != UC_OK) return rc;
-    need += uc_kivi_mq_workspace_bytes(heads_kv, head_dim, items_host[i].quantized_tokens,
-                                       items_host[i].residual_tokens);
+    const uc_kivi_item &it = items_host[i];
+    if ((rc = b.begin_query(it.query, it.out, it.lse, query_lens[i])) != UC_OK) return rc;
+    if ((rc = b.add_item(it)) != UC_OK) return rc;
+    if ((rc = b.end_query()) != UC_OK) return rc;
   }
-  UC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need &&
-                           (reinterpret_cast<uintptr_t>(workspace) & 15) == 0),
-             "attn_mq_batch: workspace too small or misaligned (%lld < %lld bytes)", (long long)workspace_bytes,
-             (long long)need);
-  // longest segments first: their work items start first on every XCD
-  int order[kMqMaxBatch];
-  for (int i = 0; i < n_items; ++i) order[i] = i;
-  const auto keys_of = [&](int i) { return items_host[i].quantized_tokens + items_host[i].residual_tokens; };
-  for (int i = 1; i < n_items; ++i)
-    for (int j = i; j > 0 && keys_of(order[j]) > keys_of(order[j - 1]); --j) std::swap(order[j], order[j - 1]);
-  MqBatch b{};
-  b.n = n_items;
-  _Float16 *ws = static_cast<_Float16 *>(workspace);
-  for (int i = 0; i < n_items; ++i) {
-    const int src = order[i];
-    b.it[i] = items_host[src];
-    mq_fill(items_host[src], heads_q, heads_kv, query_lens[src], sm_scale, ws, b.sp[i], b.p[i]);
-    ws += 2 * heads_kv * b.sp[i].Tq * mf::kD;  // staged K and V of segment i
-    b.stage_begin[i + 1] = b.stage_begin[i] + b.p[i].nq;
-    b.attn_begin[i + 1] = b.attn_begin[i] + b.p[i].row_blocks * heads_kv;
+  return mq_launch(b, bits, q_dtype, res_dtype, out_dtype, sm_scale, static_cast<hipStream_t>(stream_),
+                   "attn_mq_batch");
+}
+
+extern "C" int uc_kivi_attn_mq_segments(const uc_kivi_item *packed_host, int n_packed,
+                                        const uc_dense_segment *dense_host, int n_dense, const void *query, void *out,
+                                        float *lse, int bits, int group_size, int64_t heads_q, int64_t heads_kv,
+                                        int64_t head_dim, int64_t query_len, int q_dtype, int dense_dtype,
+                                        int out_dtype, float sm_scale, uc_stream_t stream_) {
+  UC_REQUIRE(n_packed >= 0 && n_dense >= 0 && (n_packed == 0 || packed_host) && (n_dense == 0 || dense_host),
+             "attn_mq_segments: bad segment arrays");
+  int rc = mq_check_config(bits, group_size, heads_q, heads_kv, head_dim, q_dtype, dense_dtype, out_dtype, sm_scale);
+  if (rc != UC_OK) return rc;
+  TableBuilder b;
+  b.heads_q = heads_q;
+  b.heads_kv = heads_kv;
+  b.group_size = group_size;
+  if ((rc = b.begin_query(query, out, lse, query_len)) != UC_OK) return rc;
+  for (int i = 0; i < n_packed; ++i)
+    if ((rc = b.add_item(packed_host[i])) != UC_OK) return rc;
+  for (int i = 0; i < n_dense; ++i) {
+    const uc_dense_segment &d = dense_host[i];
+    if ((rc = b.add_dense(d.key, d.value, d.tokens, d.token_stride * 2, d.head_stride * 2)) != UC_OK) return rc;
   }
-  UC_REQUIRE(b.stage_begin[n_items] < (int64_t(1) << 31) && b.attn_begin[n_items] < (int64_t(1) << 31),
-             "attn_mq_batch: launch too large");
-  if (b.stage_begin[n_items] > 0) {
-    const dim3 sgrid(static_cast<unsigned>(b.stage_begin[n_items]), static_cast<unsigned>(heads_kv), kStageSplit);
-    stage_config(bits, group_size, [&](auto bb, auto g) {
-      hipLaunchKernelGGL((mq_stage_batch_kernel<decltype(bb)::value, decltype(g)::value>), sgrid,
-                         dim3(kStageThreads), 0, stream, b);
-    });
-    rc = check_launch("attn_mq_batch (stage)");
-    if (rc != UC_OK) return rc;
-  }
-  const dim3 grid(static_cast<unsigned>(b.attn_begin[n_items]));
-  attn_config(q_dtype, res_dtype, out_dtype, [&](auto qd, auto rd, auto od) {
-    hipLaunchKernelGGL((mq_attention_batch_kernel<decltype(qd)::value, decltype(rd)::value, decltype(od)::value>),
-                       grid, dim3(kAttnThreads), 0, stream, b);
-  });
-  return check_launch("attn_mq_batch");
+  if ((rc = b.end_query()) != UC_OK) return rc;
+  return mq_launch(b, bits, q_dtype, dense_dtype, out_dtype, sm_scale, static_cast<hipStream_t>(stream_),
+                   "attn_mq_segments");
 }

@@ -129,12 +129,10 @@ def _mq_summary(cache: "PackedKIVICache", query: torch.Tensor, *, include_residu
                              residual_key_ptr=nat.ptr(cache.residual_key) if tr else None,
                              residual_value_ptr=nat.ptr(cache.residual_value) if tr else None, residual_tokens=tr)
     res_dtype = cache.residual_key.dtype if tr else q.dtype
-    ws_bytes = nat.mq_workspace_bytes(cache.num_kv_heads, d, cache.quantized_tokens, tr)
-    ws = nat.workspace(device, ws_bytes)
     nat.call(
         "uc_kivi_attn_mq", item, cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq,
         nat.dtype_code(q.dtype), nat.dtype_code(res_dtype), nat.dtype_code(out_dtype),
-        1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device),
+        1.0 / math.sqrt(d), None, 0, nat.stream(device),
     )
     return out, lse
 
@@ -214,12 +212,12 @@ def packed_summary_with_dense(
         if d != 128 or cache.group_size not in (32, 64, 128) or (tr and dk.dtype not in (torch.bfloat16,
                                                                                         torch.float16)):
             raise ValueError("Mixed-segment attention needs head_dim 128, group 32/64/128 and 16-bit dense KV")
-        ws_bytes = nat.mq_workspace_bytes(cache.num_kv_heads, d, cache.quantized_tokens, tr)
+        ws_bytes = 0  # the multi-query kernel needs no workspace
         entry = "uc_kivi_attn_mq"
-    ws = nat.workspace(device, ws_bytes)
+    ws = nat.workspace(device, ws_bytes) if ws_bytes else None
     nat.call(
         entry, item, cache.k_bits, cache.group_size, hq, cache.num_kv_heads, d, lq, nat.dtype_code(q.dtype),
-        res_code, nat.dtype_code(q.dtype), 1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device),
+        res_code, nat.dtype_code(q.dtype), 1.0 / math.sqrt(d), nat.ptr(ws), ws_bytes, nat.stream(device),
     )
     return out, lse
 
@@ -228,8 +226,8 @@ MQ_MAX_BATCH = 8  # segments per uc_kivi_attn_mq_batch launch
 
 
 def packed_batch_with_dense(items: list) -> None:
-    """packed_summary_with_dense for several independent segments in one stage
-    and one attention launch per MQ_MAX_BATCH of them (uc_kivi_attn_mq_batch):
+    """packed_summary_with_dense for several independent segments in one
+    attention launch per MQ_MAX_BATCH of them (uc_kivi_attn_mq_batch):
     the per-sample loop of apply_static_physical_attention_batch
     (adapters/bagel.py:773-980) for samples whose layout is one packed prefix
     plus dense keys.  items: (cache, query [Lq, Hq, D], key_parts, value_parts,
@@ -288,7 +286,6 @@ def packed_batch_with_dense(items: list) -> None:
         row_bytes = int(dk.stride(0)) * dk.element_size() if dk is not None else 0
         table = (nat.KiviItem * len(chunk))()
         lens = (ctypes.c_int64 * len(chunk))()
-        ws_bytes = 0
         row = 0
         for j, (cache, query, kparts, _, out, *rest) in enumerate(chunk):
             lse = rest[0] if rest else None
@@ -299,13 +296,112 @@ def packed_batch_with_dense(items: list) -> None:
                 residual_value_ptr=dv.data_ptr() + row * row_bytes if tr else None, residual_tokens=tr)
             row += tr
             lens[j] = int(query.shape[0])
-            ws_bytes += nat.mq_workspace_bytes(cache.num_kv_heads, d, cache.quantized_tokens, tr)
-        ws = nat.workspace(device, ws_bytes)
         nat.call(
             "uc_kivi_attn_mq_batch", table, lens, len(chunk), cache0.k_bits, cache0.group_size, hq,
             cache0.num_kv_heads, d, nat.dtype_code(q0.dtype), nat.dtype_code(dtype), nat.dtype_code(q0.dtype),
-            1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device),
+            1.0 / math.sqrt(d), None, 0, nat.stream(device),
         )
+
+
+MQ_MAX_PACKED, MQ_MAX_DENSE = 8, 16  # segments per uc_kivi_attn_mq_segments launch
+
+
+def _dense_segment(key: torch.Tensor, value: torch.Tensor):
+    """uc_dense_segment of [T, Hkv, D] key/value views read in place: unit
+    channel stride, token and head strides that are multiples of 8 elements
+    (the same for key and value), 16-byte aligned; other layouts are copied.
+    Returns (struct, tensors to keep alive)."""
+
+    def in_place(x):
+        return x.stride(2) == 1 and x.stride(0) % 8 == 0 and x.stride(1) % 8 == 0 and x.data_ptr() % 16 == 0
+
+    if not (in_place(key) and in_place(value) and key.stride() == value.stride()):
+        key, value = key.contiguous(), value.contiguous()
+    seg = nat.DenseSegment(key.data_ptr(), value.data_ptr(), int(key.shape[0]), int(key.stride(0)),
+                           int(key.stride(1)))
+    return seg, (key, value)
+
+
+def packed_segments_supported(packed: list, query: torch.Tensor, dense: list) -> bool:
+    """Whether packed_segments_summary takes this layout: long 16-bit queries,
+    head_dim 128, packed prefixes of equal 2- or 4-bit K/V, one group size and
+    KV head count, 16-bit dense parts, within the per-launch segment limits."""
+
+    if not packed or query.dim() != 3 or int(query.shape[2]) != 128 or query.dtype not in (torch.bfloat16,
+                                                                                             torch.float16):
+        return False
+    first = packed[0]
+    if first.k_bits not in (2, 4) or first.group_size not in (32, 64, 128):
+        return False
+    if any((s.k_bits, s.v_bits, s.group_size, s.num_kv_heads) != (first.k_bits, first.k_bits, first.group_size,
+                                                                  first.num_kv_heads) or not s.kernel_native_layout
+           for s in packed):
+        return False
+    if int(query.shape[0]) <= _max_decode_query_len(first, int(query.shape[1])):
+        return False
+    parts = [k for k, _ in dense] + [s.residual_key for s in packed if s.residual_tokens]
+    if any(x.dtype not in (torch.bfloat16, torch.float16) for x in parts):
+        return False
+    n_dense = sum(1 for k, _ in dense if int(k.shape[0])) + sum(1 for s in packed if s.residual_tokens)
+    return len(packed) <= MQ_MAX_PACKED and n_dense <= MQ_MAX_DENSE
+
+
+def packed_segments_summary(packed: list, query: torch.Tensor, dense: list,
+                            *, dense_dtype: torch.dtype | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """One softmax of query [Lq, Hq, 128] over the packed prefixes and
+    residuals of the PackedKIVICache segments `packed` and the dense
+    (key, value) [T, Hkv, 128] segments `dense`, in one launch of the
+    multi-query kernel (uc_kivi_attn_mq_segments): no concatenation of the
+    dense parts, no per-prefix summaries, no merge.  This is the long-query
+    form of _run_fused_mixed_attention (adapters/bagel.py:1598-1858).  Dense
+    parts and residuals are attended in `dense_dtype` (default: the first dense
+    part's dtype).  Returns (out [Lq, Hq, 128] in the query dtype, lse [Hq, Lq])."""
+
+    if not packed_segments_supported(packed, query, dense):
+        raise ValueError("Segment-table attention needs long 16-bit queries, head_dim 128, packed prefixes of "
+                         "equal 2/4-bit K/V sharing group size and KV heads, 16-bit dense parts and at most "
+                         f"{MQ_MAX_PACKED} prefixes and {MQ_MAX_DENSE} dense parts")
+    first = packed[0]
+    hkv = first.num_kv_heads
+    for key, value in dense:
+        if key.shape != value.shape or key.dim() != 3 or tuple(key.shape[1:]) != (hkv, 128):
+            raise ValueError("Dense segments must be matching [tokens, kv_heads, 128] tensors")
+    for cache in packed:
+        if not cache.quantized_tokens:
+            raise ValueError("Packed segments of a segment table need a quantized prefix")
+    if dense_dtype is None:
+        dense_dtype = next((k.dtype for k, _ in dense), None) or next(
+            (s.residual_key.dtype for s in packed if s.residual_tokens), torch.bfloat16)
+    q = query.contiguous()
+    lq, hq, d = map(int, q.shape)
+    device = nat.require_device(q, *(t for pair in dense for t in pair), *(s.key_code for s in packed),
+                                what="Segment-table attention")
+    keep = []
+    dense_structs = []
+    for key, value in dense:
+        if int(key.shape[0]) == 0:
+            continue
+        seg, tensors = _dense_segment(key.to(dense_dtype), value.to(dense_dtype))
+        dense_structs.append(seg)
+        keep.append(tensors)
+    items = (nat.KiviItem * len(packed))()
+    for j, cache in enumerate(packed):
+        tr = cache.residual_tokens
+        rk, rv = cache.residual_key, cache.residual_value
+        if tr and (rk.dtype != dense_dtype or not rk.is_contiguous() or not rv.is_contiguous()):
+            rk, rv = rk.to(dense_dtype).contiguous(), rv.to(dense_dtype).contiguous()
+            keep.append((rk, rv))
+        items[j] = cache.native_item(None, None, None, residual_key_ptr=rk.data_ptr() if tr else None,
+                                     residual_value_ptr=rv.data_ptr() if tr else None, residual_tokens=tr)
+    table = (nat.DenseSegment * max(1, len(dense_structs)))(*dense_structs)
+    out = torch.empty((lq, hq, d), dtype=q.dtype, device=device)
+    lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
+    nat.call(
+        "uc_kivi_attn_mq_segments", items, len(packed), table, len(dense_structs), q.data_ptr(), out.data_ptr(),
+        lse.data_ptr(), first.k_bits, first.group_size, hq, hkv, d, lq, nat.dtype_code(q.dtype),
+        nat.dtype_code(dense_dtype), nat.dtype_code(q.dtype), 1.0 / math.sqrt(d), nat.stream(device),
+    )
+    return out, lse
 
 
 def dense_attention_summary(
@@ -341,11 +437,11 @@ def dense_attention_summary(
     else:
         if d != 128:
             raise ValueError("Dense attention over more than 16 query rows per KV head needs head_dim 128")
-        ws_bytes = nat.mq_workspace_bytes(hkv, d, 0, tokens)
+        ws_bytes = 0  # the multi-query kernel needs no workspace
         entry = "uc_kivi_attn_mq"
-    ws = nat.workspace(device, ws_bytes)
+    ws = nat.workspace(device, ws_bytes) if ws_bytes else None
     nat.call(entry, item, bits, group, hq, hkv, d, lq, nat.dtype_code(q.dtype), nat.dtype_code(dk.dtype),
-             nat.dtype_code(q.dtype), 1.0 / math.sqrt(d), ws.data_ptr(), ws_bytes, nat.stream(device))
+             nat.dtype_code(q.dtype), 1.0 / math.sqrt(d), nat.ptr(ws), ws_bytes, nat.stream(device))
     return out, lse
 
 
