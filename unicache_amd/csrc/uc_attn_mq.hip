@@ -213,9 +213,11 @@ __device__ __forceinline__ TileRef find_tile(const Seg *segs, int first, int n, 
 //     16 c8 + 15 (two chunks) of tokens t and t + 32 from one word pair (4-bit)
 //     or word (2-bit) per token and the token's scale and minimum.  Even and
 //     odd channels are split into two registers whose bytes a permute
-//     interleaves, giving code pairs (2j, 2j + 1) of a chunk.  Tokens t and
-//     t + 1 share a 16-lane store group; they store their two chunks in
-//     opposite orders so that the group covers all 16 chunk positions.
+//     interleaves, giving code pairs (2j, 2j + 1) of a chunk.  A thread stores
+//     its chunks 2 c8 and 2 c8 + 1 in the order given by bit 2 of c8 and the
+//     token's parity: each 8 lanes of a store then cover 8 chunk positions
+//     that differ modulo 8, and each 16 lanes all 16 -- no bank conflict
+//     whether the LDS serves 128 or 256 bytes of a store per cycle.
 // Rows past the end of the segment repeat the last valid word row or token:
 // finite values under a probability of exactly zero.
 template <int BITS>
@@ -259,10 +261,10 @@ __device__ __forceinline__ DeqLane deq_lane(int tid_h) {
     const uint32_t row = 4 * tq + i;
     d.kaddr[i] = row * 256u + 16u * (cb ^ (row & 15u));
   }
-  const uint32_t c8 = tid_h & 7, t = tid_h >> 3, odd = t & 1;
+  const uint32_t c8 = tid_h & 7, t = tid_h >> 3, flip = ((c8 >> 2) ^ t) & 1;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    const uint32_t half8 = odd ^ b;  // store b writes chunk 2 c8 + half8
+    const uint32_t half8 = flip ^ b;  // store b writes chunk 2 c8 + half8
     d.vsel[b] = BITS == 2 ? (half8 ? 0x07060302u : 0x05040100u) : half8;
     d.vaddr[b] = kValueBytes + t * 256u + 16u * ((2 * c8 + half8) ^ ((2 * t) & 15u));
   }
