@@ -282,6 +282,30 @@ def test_segment_table_editing_layout(device, bits, group, dtype, lq):
     assert_close(f32(lse), el, max_abs=1e-2, mean_abs=1e-3, what=f"table lse {bits}-bit G{group}")
 
 
+def test_segment_table_rejects_bad_parts_before_launch(device):
+    # a CPU dense part, mismatched dense shapes, decode-length queries and a
+    # cache without a prefix raise before anything is launched
+    from unicache_amd.storage.kivi_cuda import packed_segments_summary
+
+    ck, cv = kv_pair(500, seed=140)
+    cache = PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(500),
+                                       token_type_id=3, k_bits=2, v_bits=2, group_size=32, residual_length=128,
+                                       backend="cuda")
+    q = queries(64, seed=141).to(device)
+    dk, dv = kv_pair(40, seed=142)
+    with pytest.raises(RuntimeError, match="GPU"):
+        packed_segments_summary([cache], q, [(dk, dv)])
+    with pytest.raises(ValueError, match="matching"):
+        packed_segments_summary([cache], q, [(dk.to(device), dv[:30].to(device))])
+    with pytest.raises(ValueError, match="Segment-table attention needs"):
+        packed_segments_summary([cache], queries(2, seed=143).to(device), [])
+    empty = PackedKIVICache.from_dense(ck[:50].to(device), cv[:50].to(device), logical_token_ids=torch.arange(50),
+                                       token_type_id=3, k_bits=2, v_bits=2, group_size=32, residual_length=128,
+                                       backend="cuda")
+    with pytest.raises(ValueError, match="Segment-table attention needs"):
+        packed_segments_summary([cache, empty], q, [])
+
+
 def test_batched_launch_rejects_bad_items_before_launch(device):
     # every table pointer is checked on the host: a CPU dense part, mixed
     # bits, a mixed query dtype, a bad LSE shape and decode-length queries

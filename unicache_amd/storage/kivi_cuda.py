@@ -374,8 +374,13 @@ def packed_segments_summary(packed: list, query: torch.Tensor, dense: list,
             (s.residual_key.dtype for s in packed if s.residual_tokens), torch.bfloat16)
     q = query.contiguous()
     lq, hq, d = map(int, q.shape)
-    device = nat.require_device(q, *(t for pair in dense for t in pair), *(s.key_code for s in packed),
-                                what="Segment-table attention")
+    # every tensor whose address goes into the launch table, on one GPU, before any launch
+    device = nat.require_device(
+        q, *(t for pair in dense for t in pair),
+        *(t for s in packed for t in (s.key_code, s.key_scale, s.key_minimum, s.value_code, s.value_scale,
+                                      s.value_minimum, s.residual_key if s.residual_tokens else None,
+                                      s.residual_value if s.residual_tokens else None)),
+        what="Segment-table attention")
     keep = []
     dense_structs = []
     for key, value in dense:
