@@ -254,14 +254,15 @@ def h2o_eviction(device, steps):
     ms_scores = time_steps(lambda: per_kv_head_scores_from_qk(q, key, out=scores, lse=lse), steps, 2, stream)
     ms_scores_stats = time_steps(lambda: per_kv_head_scores_from_qk(q, key, out=scores.zero_()), steps, 2, stream)
     spans = [(0, 256), (256, 4096)]
+    ids = [torch.arange(lo, hi, device=device) for lo, hi in spans]  # the caller's logical token ids
 
     def select_gather():
         segs = []
-        for lo, hi in spans:
+        for (lo, hi), seg_ids in zip(spans, ids):
             target, recent = h2o_budget(hi - lo, {"target_budget_ratio": 0.2})
-            segs.append(GQAH2OCache.from_dense(key[lo:hi], value[lo:hi], logical_token_ids=torch.arange(
-                lo, hi, device=device), token_type_id=1, per_kv_head_scores=scores[:, lo:hi],
-                target_tokens=target, recent_tokens=recent, selection_frozen=True))
+            segs.append(GQAH2OCache.from_dense(key[lo:hi], value[lo:hi], logical_token_ids=seg_ids,
+                                               token_type_id=1, per_kv_head_scores=scores[:, lo:hi],
+                                               target_tokens=target, recent_tokens=recent, selection_frozen=True))
         return segs
 
     ms_sel = time_steps(select_gather, steps, 2, stream)

@@ -268,9 +268,13 @@ struct SelectArgs {
 // Each pass counts into per-wave histograms (scores of a head share their top
 // bytes, so one shared histogram would serialise on a few bins), sums them per
 // bin, and wave 0 finds the bin holding the threshold with a suffix scan over
-// its lanes (4 bins each).
+// its lanes (4 bins each).  With REGS, the head's candidates (at most
+// kSelThreads * kSelRegs) are read once into registers and every pass and the
+// scan run on them; otherwise each pass reads the scores again.
 constexpr int kSelWaves = kSelThreads / kWave;
+constexpr int kSelRegs = 8;
 
+template <bool REGS>
 __global__ __launch_bounds__(kSelThreads) void h2o_select_kernel(SelectArgs a) {
   __shared__ uint32_t whist[kSelWaves][256];
   __shared__ uint32_t hist[256];
@@ -283,15 +287,32 @@ __global__ __launch_bounds__(kSelThreads) void h2o_select_kernel(SelectArgs a) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
 
   if (a.heavy_k > 0) {
+    // candidate keys of this thread (REGS): token r * kSelThreads + tid
+    uint32_t keys[REGS ? kSelRegs : 1];
+    if constexpr (REGS) {
+#pragma unroll
+      for (int r = 0; r < kSelRegs; ++r) {
+        const int64_t t = int64_t(r) * kSelThreads + tid;
+        keys[r] = t < hist_end ? order_key(sc[t * a.s_st]) : 0u;
+      }
+    }
     uint32_t prefix = 0, mask = 0;
     uint32_t need = static_cast<uint32_t>(a.heavy_k);
     for (int pass = 0; pass < 4; ++pass) {
       const int shift = 24 - 8 * pass;
       for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&whist[0][0])[i] = 0;
       __syncthreads();
-      for (int64_t t = tid; t < hist_end; t += kSelThreads) {
-        const uint32_t key = order_key(sc[t * a.s_st]);
-        if ((key & mask) == prefix) atomicAdd(&whist[wave][(key >> shift) & 255u], 1u);
+      if constexpr (REGS) {
+#pragma unroll
+        for (int r = 0; r < kSelRegs; ++r) {
+          const int64_t t = int64_t(r) * kSelThreads + tid;
+          if (t < hist_end && (keys[r] & mask) == prefix) atomicAdd(&whist[wave][(keys[r] >> shift) & 255u], 1u);
+        }
+      } else {
+        for (int64_t t = tid; t < hist_end; t += kSelThreads) {
+          const uint32_t key = order_key(sc[t * a.s_st]);
+          if ((key & mask) == prefix) atomicAdd(&whist[wave][(key >> shift) & 255u], 1u);
+        }
       }
       __syncthreads();
       if (tid < 256) {
@@ -340,7 +361,14 @@ __global__ __launch_bounds__(kSelThreads) void h2o_select_kernel(SelectArgs a) {
     for (int64_t c0 = 0; c0 < hist_end; c0 += kSelThreads) {
       const int64_t t = c0 + tid;
       uint32_t key = 0;
-      if (t < hist_end) key = order_key(sc[t * a.s_st]);
+      if constexpr (REGS) {
+        // chunk c0 / kSelThreads of the register keys (uniform index)
+#pragma unroll
+        for (int r = 0; r < kSelRegs; ++r)
+          if (c0 == int64_t(r) * kSelThreads) key = keys[r];
+      } else if (t < hist_end) {
+        key = order_key(sc[t * a.s_st]);
+      }
       const bool eq = t < hist_end && key == prefix;
       const bool gt = t < hist_end && key > prefix;
       // exclusive scan of eq, then of selection
@@ -510,7 +538,10 @@ extern "C" int uc_h2o_select(const float *scores, int64_t s_sh, int64_t s_st, in
   SelectArgs a{};
   a.scores = scores; a.s_sh = s_sh; a.s_st = s_st; a.T = tokens; a.heavy_k = heavy_k; a.recent = recent;
   a.indices = indices;
-  hipLaunchKernelGGL(h2o_select_kernel, dim3(heads_kv), dim3(kSelThreads), 0, as_stream(stream), a);
+  if (tokens - recent <= int64_t(kSelThreads) * kSelRegs)
+    hipLaunchKernelGGL(h2o_select_kernel<true>, dim3(heads_kv), dim3(kSelThreads), 0, as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(h2o_select_kernel<false>, dim3(heads_kv), dim3(kSelThreads), 0, as_stream(stream), a);
   return check_launch("uc_h2o_select");
 }
 
