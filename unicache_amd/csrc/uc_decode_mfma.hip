@@ -767,12 +767,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     const int64_t slot = (item * p.Hkv + h) * p.splits_total + split;
     _Float16 *po = p.ws_o + slot * 16 * kD;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    if (n < p.rows) {  // rows past the query rows are never read: not written
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      f4 s = st.o[b] * mine;
+      for (int b = 0; b < 8; ++b) {
+        f4 s = st.o[b] * mine;
 #pragma unroll
-      for (int w = 0; w < kWaves - 1; ++w) s += *reinterpret_cast<const f4 *>(&sh.mrg.o[w][n][16 * b + 4 * kap]);
-      *reinterpret_cast<h4 *>(&po[n * kD + 16 * b + 4 * kap]) = cvt4(s * inv);
+        for (int w = 0; w < kWaves - 1; ++w) s += *reinterpret_cast<const f4 *>(&sh.mrg.o[w][n][16 * b + 4 * kap]);
+        *reinterpret_cast<h4 *>(&po[n * kD + 16 * b + 4 * kap]) = cvt4(s * inv);
+      }
     }
     if (kap == 0) {
       p.ws_ml[(slot * 16 + n) * 2 + 0] = M;
