@@ -822,6 +822,44 @@ __global__ __launch_bounds__(kCombineThreads) void decode_mfma_combine(const uc_
   };
   // splits without work wrote (-inf, 0) and no output
   auto ml_at = [&](int f) { return *reinterpret_cast<const float2 *>(p.ws_ml + (slot(f) * 16 + row) * 2); };
+  const bool active = row < p.rows;
+  const int c4 = (part * kCombineLanes + j) * 4;
+  if (nflat <= kCombineLanes) {
+    // at most 8 slots: every load of the row -- its (max, sum) pairs and this
+    // thread's 4 channels of each partial -- is issued at once, before any
+    // arithmetic (two dependent rounds of loads would double the latency)
+    float2 ml[kCombineLanes];
+    h4 v[kCombineLanes];
+#pragma unroll
+    for (int u = 0; u < kCombineLanes; ++u) {
+      const int f = u < nflat ? u : 0;
+      ml[u] = ml_at(f);
+      v[u] = active ? *reinterpret_cast<const h4 *>(p.ws_o + (slot(f) * 16 + row) * kD + c4) : h4{0, 0, 0, 0};
+    }
+    float M = kNegInf, L = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kCombineLanes; ++u)
+      if (u < nflat) ml_fold(M, L, ml[u].x, ml[u].y);
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    if (active && part == 0 && j == 0 && it.lse != nullptr) {
+      const int64_t g = row / p.Lq, i = row % p.Lq;
+      it.lse[(h * p.group + g) * p.Lq + i] = L > 0.0f ? (M + log2f(L)) * kLn2 : kNegInf;
+    }
+    if (active) {
+      float o[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int u = 0; u < kCombineLanes; ++u) {
+        const float w = (u < nflat && ml[u].y > 0.0f && ml[u].x != kNegInf) ? ml[u].y * exp2f(ml[u].x - M) * inv
+                                                                           : 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = w != 0.0f ? fmaf(float(v[u][c]), w, o[c]) : o[c];
+      }
+      const int64_t g = row / p.Lq, i = row % p.Lq;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) store_dyn(it.out, (i * p.Hq + h * p.group + g) * kD + c4 + c, o[c], p.od);
+    }
+    return;
+  }
   // pass 1: this thread's slots, four loads in flight, then the row's 8 threads
   float M = kNegInf, L = 0.0f;
   for (int f0 = j; f0 < nflat; f0 += 4 * kCombineLanes) {
@@ -840,13 +878,11 @@ __global__ __launch_bounds__(kCombineThreads) void decode_mfma_combine(const uc_
     ml_fold(M, L, m2, l2);
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  const bool active = row < p.rows;
   if (active && part == 0 && j == 0 && it.lse != nullptr) {
     const int64_t g = row / p.Lq, i = row % p.Lq;
     it.lse[(h * p.group + g) * p.Lq + i] = L > 0.0f ? (M + log2f(L)) * kLn2 : kNegInf;
   }
   // pass 2: 4 channels of this part over every slot
-  const int c4 = (part * kCombineLanes + j) * 4;
   float o[4] = {0, 0, 0, 0};
   if (active) {
     for (int f0 = 0; f0 < nflat; f0 += 8) {
