@@ -36,7 +36,7 @@ BITS, GROUP, RESIDUAL = 2, 32, 128
 # HBM bytes per step of the default workload from rocprofv3 PMC passes
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 over both decode kernels, the factors
 # from a 1 GiB device copy); profiles/decode_batch_c1.md has the commands.
-MEASURED_TRAFFIC_BYTES = 784_447_898
+MEASURED_TRAFFIC_BYTES = 773_993_882
 
 
 def make_kv(tokens, *, seed, device, heads=HKV, head_dim=D):
