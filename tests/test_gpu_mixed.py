@@ -282,6 +282,28 @@ def test_segment_table_editing_layout(device, bits, group, dtype, lq):
     assert_close(f32(lse), el, max_abs=1e-2, mean_abs=1e-3, what=f"table lse {bits}-bit G{group}")
 
 
+@pytest.mark.parametrize("heads_q,dtype", [(4, torch.bfloat16), (28, torch.float16)])
+def test_segment_table_group_and_fp16(device, heads_q, dtype):
+    # one query head per KV head (group 1: 150 query rows per KV head), and an
+    # all-fp16 table (queries, packed stats and dense parts), against the oracle
+    from unicache_amd.storage.kivi_cuda import packed_segments_summary
+
+    ck, cv = kv_pair(900, seed=150, dtype=dtype)
+    cache = PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(900),
+                                       token_type_id=3, k_bits=4, v_bits=4, group_size=64, residual_length=100,
+                                       backend="cuda")
+    seg = K.from_dense(f32(ck), f32(cv), k_bits=4, v_bits=4, group_size=64, residual_length=100,
+                       in_dtype="fp16" if dtype == torch.float16 else "bf16")
+    dk, dv = kv_pair(333, seed=151, dtype=dtype)
+    q = queries(150, heads=heads_q, seed=152, dtype=dtype)
+    out, lse = packed_segments_summary([cache], q.to(device), [(dk.to(device), dv.to(device))])
+    assert out.dtype == dtype and out.shape == (150, heads_q, 128)
+    k, v = K.dequantize(seg, "fp32")
+    eo, el = A.attention_summary(f32(q), np.concatenate([k, f32(dk)]), np.concatenate([v, f32(dv)]))
+    assert_close(f32(out), eo, what=f"table Hq={heads_q} {dtype}")
+    assert_close(f32(lse), el, max_abs=1e-2, mean_abs=1e-3, what="table lse")
+
+
 def test_segment_table_rejects_bad_parts_before_launch(device):
     # a CPU dense part, mismatched dense shapes, decode-length queries and a
     # cache without a prefix raise before anything is launched
