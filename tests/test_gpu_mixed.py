@@ -215,6 +215,41 @@ def test_batched_packed_launch_matches_per_sample_passes(device):
         assert torch.equal(out[cu_q[i]:cu_q[i + 1]], want), f"sample {i}"
 
 
+def test_batched_table_with_several_prefixes_per_sample(device):
+    # five long-query samples, each over two packed prefixes, an H2O segment and
+    # its own current keys: ten prefixes exceed one table launch (8 per call),
+    # so the batch runs as two launches; every sample is one softmax over all of
+    # its segments (one cache without a residual window), compared with the oracle
+    from unicache_amd.adapters import run_batched_physical_attention
+
+    caches, segs = [], []
+    for j, n in enumerate((640, 1000, 480)):
+        ck, cv = kv_pair(n, seed=90 + j)
+        caches.append(PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(n),
+                                                 token_type_id=3, k_bits=2, v_bits=2, group_size=32,
+                                                 residual_length=128 if j != 1 else 0, backend="cuda"))
+        segs.append(K.from_dense(f32(ck), f32(cv), k_bits=2, v_bits=2, group_size=32,
+                                 residual_length=128 if j != 1 else 0))
+    hk, hv = kv_pair(300, seed=95)
+    h2o = GQAH2OCache.from_dense(hk.to(device), hv.to(device), logical_token_ids=torch.arange(300), token_type_id=1,
+                                 per_kv_head_scores=torch.rand(4, 300).to(device), target_tokens=60,
+                                 recent_tokens=15, selection_frozen=True)
+    picks = [(0, 1), (2, 0), (1, 2), (0, 2), (1, 0)]
+    q_lens, k_lens = [40, 130, 17, 64, 200], [64, 0, 33, 128, 7]
+    q = queries(sum(q_lens), seed=96)
+    k, v = kv_pair(sum(k_lens), seed=97)
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)])
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)])
+    layouts = [[h2o, caches[a], caches[b]] for a, b in picks]
+    out = run_batched_physical_attention(q.to(device), k.to(device), v.to(device), torch.tensor(cu_q).to(device),
+                                         torch.tensor(cu_k).to(device), layouts)
+    for i, (a, b) in enumerate(picks):
+        dense = (k[cu_k[i]:cu_k[i + 1]], v[cu_k[i]:cu_k[i + 1]])
+        ek, ev = _oracle_keys(dense, [h2o], [segs[a], segs[b]])
+        eo, _ = A.attention_summary(f32(q[cu_q[i]:cu_q[i + 1]]), ek, ev)
+        assert_close(f32(out[cu_q[i]:cu_q[i + 1]]), eo, what=f"sample {i}")
+
+
 def test_segment_table_matches_separate_passes(device):
     # two packed prefixes with long queries: one segment-table launch (both
     # prefixes, both residuals and the dense keys read in place) against one
