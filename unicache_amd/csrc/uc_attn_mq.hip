@@ -1038,6 +1038,7 @@ struct TableBuilder {
     UC_REQUIRE(query != nullptr && out != nullptr, "attn_mq: query/out are NULL");
     UC_REQUIRE((reinterpret_cast<uintptr_t>(query) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
                "attn_mq: query and out must be 16-byte aligned");
+    UC_REQUIRE((reinterpret_cast<uintptr_t>(lse) & 3) == 0, "attn_mq: lse must be 4-byte aligned");
     int p0 = 0, d0 = 0;
     for (int q = 0; q < t.n_queries; ++q) {
       p0 += t.q[q].np;
@@ -1195,8 +1196,8 @@ extern "C" int uc_kivi_attn_mq_table(const uc_mq_query *queries_host, int n_quer
   b.group_size = group_size;
   for (int qi = 0; qi < n_queries; ++qi) {
     const uc_mq_query &q = queries_host[qi];
-    UC_REQUIRE(q.packed_begin >= 0 && q.n_packed >= 0 && q.packed_begin + q.n_packed <= n_packed &&
-                   q.dense_begin >= 0 && q.n_dense >= 0 && q.dense_begin + q.n_dense <= n_dense,
+    UC_REQUIRE(q.packed_begin >= 0 && q.n_packed >= 0 && int64_t(q.packed_begin) + q.n_packed <= n_packed &&
+                   q.dense_begin >= 0 && q.n_dense >= 0 && int64_t(q.dense_begin) + q.n_dense <= n_dense,
                "attn_mq_table: query %d names segments outside the arrays", qi);
     if ((rc = b.begin_query(q.query, q.out, q.lse, q.query_len)) != UC_OK) return rc;
     for (int i = 0; i < q.n_packed; ++i)
