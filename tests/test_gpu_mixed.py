@@ -250,6 +250,33 @@ def test_batched_table_with_several_prefixes_per_sample(device):
         assert_close(f32(out[cu_q[i]:cu_q[i + 1]]), eo, what=f"sample {i}")
 
 
+def test_table_launch_writes_each_querys_lse(device):
+    # uc_kivi_attn_mq_table with an LSE per query: two queries of different
+    # lengths over their own prefixes and dense parts in one launch equal one
+    # segment-table call each, outputs and natural-log LSEs bit for bit
+    from unicache_amd.storage.kivi_cuda import packed_segments_summary, packed_table_summaries
+
+    caches = []
+    for j, n in enumerate((700, 1000)):
+        ck, cv = kv_pair(n, seed=110 + j)
+        caches.append(PackedKIVICache.from_dense(ck.to(device), cv.to(device), logical_token_ids=torch.arange(n),
+                                                 token_type_id=3, k_bits=2, v_bits=2, group_size=32,
+                                                 residual_length=128, backend="cuda"))
+    entries, wants = [], []
+    for i, (lq, nd, picks) in enumerate([(96, 150, (0,)), (300, 64, (1, 0))]):
+        q = queries(lq, seed=120 + i).to(device)
+        k, v = (x.to(device) for x in kv_pair(nd, seed=130 + i))
+        segs = [caches[c] for c in picks]
+        wants.append(packed_segments_summary(segs, q, [(k, v)]))
+        out = torch.empty_like(q)
+        lse = torch.empty(q.shape[1], lq, dtype=torch.float32, device=device)
+        entries.append((q, out, lse, segs, [(k, v)]))
+    packed_table_summaries(entries, dense_dtype=torch.bfloat16)
+    for i, ((_, out, lse, _, _), (want_o, want_l)) in enumerate(zip(entries, wants)):
+        assert torch.equal(out, want_o), f"query {i} output"
+        assert torch.equal(lse, want_l), f"query {i} lse"
+
+
 def test_segment_table_matches_separate_passes(device):
     # two packed prefixes with long queries: one segment-table launch (both
     # prefixes, both residuals and the dense keys read in place) against one
