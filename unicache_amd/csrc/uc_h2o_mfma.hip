@@ -405,21 +405,21 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
 // out[hq, i, :] = P[hq, i, :] . V[:, h, :] with P cast to the value dtype
 // first (physical.py:42-63), fp32 accumulation.  pv_stage_kernel writes V
 // transposed, [Hkv][128][Tp] (Tp = T rounded up to 64, zero tail); in
-// pv_mfma_kernel a workgroup owns 64 query rows of one KV head in two key
-// halves of 4 waves (a 16-row block per wave); each half streams the 64-key
-// tiles of its half of V^T through its own LDS ring and reads the P^T
+// pv_mfma_kernel a workgroup owns 64 query rows of one KV head in three key
+// parts of 4 waves (a 16-row block per wave); each part streams the 64-key
+// tiles of its third of V^T through its own LDS ring and reads the P^T
 // fragments straight from global memory:
 //   O^T[16 channels x 16 rows] += V^T[16 x 32 keys] . P^T[32 keys x 16 rows],
-// and the second half's sums are added to the first's through LDS at the end.
-// Two halves put 8 waves of loads in flight per CU for the ~224 workgroups
+// and the other parts' sums are added to the first's through LDS at the end.
+// Three parts put 12 waves of loads in flight per CU for the ~224 workgroups
 // of a config-3 layer (one per CU).
-constexpr int kPvWaves = 4;                          // waves per key half: 16 rows each
-constexpr int kPvHalves = 2;                         // key halves of a workgroup
-constexpr int kPvHalfThreads = kPvWaves * kWave;
-constexpr int kPvThreads = kPvHalves * kPvHalfThreads;
+constexpr int kPvWaves = 4;                          // waves per key part: 16 rows each
+constexpr int kPvParts = 3;                         // key parts of a workgroup
+constexpr int kPvPartThreads = kPvWaves * kWave;
+constexpr int kPvThreads = kPvParts * kPvPartThreads;
 constexpr int kPvRows = 16 * kPvWaves;
 constexpr int kPvTile = 64;
-constexpr int kPvStages = 4;
+constexpr int kPvStages = 3;
 
 template <int VD>
 struct PvOp;
@@ -472,7 +472,7 @@ struct PvParams {
 // V^T slot: channel row c (128 B = 8 chunks of 8 keys) keeps chunk q at
 // position q ^ (c & 7), so the 16 rows of a fragment read hit 8 bank groups twice.
 struct PvShared {
-  uint4 vt[kPvHalves][kPvStages][kD * 8];
+  uint4 vt[kPvParts][kPvStages][kD * 8];
 };
 
 // Raw P bytes of one lane's eight keys: one 16-byte load for 16-bit P, two for fp32.
@@ -532,8 +532,8 @@ __global__ __launch_bounds__(kPvThreads) void pv_mfma_kernel(PvParams p) {
   constexpr int kEl = PD == UC_FP32 ? 4 : 2;       // bytes per probability
   constexpr int kOps = 2 * PRaw<PD>::N + 4;        // memory ops per tile and thread: P halves + V^T slots
   const int tid = threadIdx.x, lane = tid & 63;
-  const int half = __builtin_amdgcn_readfirstlane(tid / kPvHalfThreads);
-  const int htid = tid % kPvHalfThreads;
+  const int part = __builtin_amdgcn_readfirstlane(tid / kPvPartThreads);
+  const int ptid = tid % kPvPartThreads;
   const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) % kPvWaves);  // scalar: the P resource stays in SGPRs
   const int r = lane & 15, kap = lane >> 4;
   const int64_t id = blockIdx.x, w = (id % kXcds) * p.per_xcd + id / kXcds;
@@ -547,11 +547,11 @@ __global__ __launch_bounds__(kPvThreads) void pv_mfma_kernel(PvParams p) {
                             nrows * p.p_si * kEl);
   const uint32_t p_lane = static_cast<uint32_t>((r * p.p_si + 8 * kap) * kEl);
   const Rsrc rs = make_rsrc(p.vt + h * kD * p.Tp, kD * p.Tp * 2);
-  // half 0 takes tiles [0, n_half), half 1 the rest; both run n_half steps
-  // (the barriers are shared), half 1 idling in its last one when the count is odd
+  // part k takes tiles [k n_part, (k + 1) n_part); every part runs n_part steps
+  // (the barriers are shared), the last ones idling when the count falls short
   const int n_tiles = static_cast<int>(p.Tp / kPvTile);
-  const int n_half = (n_tiles + 1) / 2;
-  const int first = half * n_half, mine = half == 0 ? n_half : n_tiles - n_half;
+  const int n_part = (n_tiles + kPvParts - 1) / kPvParts;
+  const int first = part * n_part, mine = max(0, min(n_part, n_tiles - first));
 
   auto load_p = [&](PRaw<PD> (&dst)[2], int i) {
     const int tile = first + i;
@@ -563,13 +563,13 @@ __global__ __launch_bounds__(kPvThreads) void pv_mfma_kernel(PvParams p) {
   };
   auto issue_vt = [&](int i) {
     const int64_t tile = first + i;
-    uint4 *slot = sh.vt[half][i % kPvStages];
+    uint4 *slot = sh.vt[part][i % kPvStages];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int s4 = q * kPvHalfThreads + htid, ch = s4 / 8, pos = s4 % 8, chunk = pos ^ (ch & 7);
+      const int s4 = q * kPvPartThreads + ptid, ch = s4 / 8, pos = s4 % 8, chunk = pos ^ (ch & 7);
       const uint32_t off = static_cast<uint32_t>((ch * p.Tp + tile * kPvTile) * 2 + chunk * 16);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void *)(slot + q * kPvHalfThreads + wave * kWave), 16, off, 0, 0,
+          rs, (__attribute__((address_space(3))) void *)(slot + q * kPvPartThreads + wave * kWave), 16, off, 0, 0,
           0);
     }
   };
@@ -585,7 +585,7 @@ __global__ __launch_bounds__(kPvThreads) void pv_mfma_kernel(PvParams p) {
   f4 o[8];
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) o[cb] = f4{0, 0, 0, 0};
-  for (int it = 0; it < n_half; ++it) {
+  for (int it = 0; it < n_part; ++it) {
     // tile it has landed once at most (later tiles issued) x kOps ops remain
     const int later = max(0, min(mine - 1, it + kAhead - 1) - it);
     if (later >= 2)
@@ -601,9 +601,9 @@ __global__ __launch_bounds__(kPvThreads) void pv_mfma_kernel(PvParams p) {
       load_p(nb, it + kAhead);
       issue_vt(it + kAhead);
     }
-    if (it < mine) {  // uniform per half
+    if (it < mine) {  // uniform per part
       const int64_t t0 = int64_t(first + it) * kPvTile;
-      const uint4 *vt = sh.vt[half][it % kPvStages];
+      const uint4 *vt = sh.vt[part][it % kPvStages];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const auto b = p_frag<PD, VD>(pb[0][ks], t0 + 32 * ks + 8 * kap, p.T);
@@ -618,32 +618,36 @@ __global__ __launch_bounds__(kPvThreads) void pv_mfma_kernel(PvParams p) {
     for (int t = 0; t + 1 < kAhead; ++t) pb[t][0] = pb[t + 1][0], pb[t][1] = pb[t + 1][1];
     if (more) pb[kAhead - 1][0] = nb[0], pb[kAhead - 1][1] = nb[1];
   }
-  __syncthreads();  // the rings are free: half 1 hands its sums to half 0 through LDS
+  __syncthreads();  // the rings are free: parts 1.. hand their sums to part 0 through LDS
   constexpr int kRedPad = kD + 4;  // fp32 row pad: the 16 rows of one store hit distinct banks
-  float *red = reinterpret_cast<float *>(&sh.vt[1][0][0]);  // [64 rows][132]
-  static_assert(sizeof(float) * kPvRows * kRedPad <= sizeof(sh.vt[1]), "the reduction rows fit half 1's ring");
-  if (half == 1) {
+  static_assert(sizeof(float) * kPvRows * kRedPad <= sizeof(sh.vt[1]), "the reduction rows fit a part's ring");
+  if (part > 0) {
+    float *red = reinterpret_cast<float *>(&sh.vt[part][0][0]);  // [64 rows][132]
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) *reinterpret_cast<f4 *>(&red[(wave * 16 + r) * kRedPad + 16 * cb + 4 * kap]) = o[cb];
   }
   __syncthreads();
   uint16_t *ob = reinterpret_cast<uint16_t *>(&sh.vt[0][0][0]);  // [64 rows][136]
   constexpr int kRowPad = kD + 8;
-  static_assert(sizeof(uint16_t) * kPvRows * kRowPad <= sizeof(sh.vt[0]), "output staging fits half 0's ring");
-  if (half == 0) {
+  static_assert(sizeof(uint16_t) * kPvRows * kRowPad <= sizeof(sh.vt[0]), "output staging fits part 0's ring");
+  if (part == 0) {
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) {
-      const f4 s = o[cb] + *reinterpret_cast<const f4 *>(&red[(wave * 16 + r) * kRedPad + 16 * cb + 4 * kap]);
+      f4 s = o[cb];
+#pragma unroll
+      for (int k = 1; k < kPvParts; ++k)
+        s += *reinterpret_cast<const f4 *>(reinterpret_cast<const float *>(&sh.vt[k][0][0]) +
+                                           (wave * 16 + r) * kRedPad + 16 * cb + 4 * kap);
 #pragma unroll
       for (int v = 0; v < 4; ++v) ob[(wave * 16 + r) * kRowPad + 16 * cb + 4 * kap + v] = PvOp<VD>::bits(s[v]);
     }
   }
   __syncthreads();
 #pragma unroll
-  for (int q = 0; q < kPvRows * (kD / 8) / kPvThreads; ++q) {  // 16-byte chunks of whole rows
+  for (int q = 0; q < (kPvRows * (kD / 8) + kPvThreads - 1) / kPvThreads; ++q) {  // 16-byte chunks of whole rows
     const int c = q * kPvThreads + tid, rr = c / (kD / 8), c8 = c % (kD / 8);
     const int64_t orow = rb * kPvRows + rr;
-    if (orow >= p.rows) continue;
+    if (c >= kPvRows * (kD / 8) || orow >= p.rows) continue;
     const int64_t og = orow / p.Lq, oi = orow % p.Lq;
     *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(p.out) + ((h * p.group + og) * p.Lq + oi) * kD + 8 * c8) =
         *reinterpret_cast<const uint4 *>(&ob[rr * kRowPad + 8 * c8]);
