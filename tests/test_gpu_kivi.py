@@ -44,6 +44,23 @@ def test_native_pack_bit_exact(device, bits, group):
     _assert_cache_equal(cache, seg)
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_pack_codes_at_exact_half_steps(device, bits):
+    # integer-valued groups whose range is an even multiple of the code count:
+    # (x - min) / scale lands exactly on halves, where the code is decided by
+    # round-half-even of the correctly rounded quotient (the kernels' exact
+    # fallback, not their reciprocal fast path), for keys and values alike
+    top = (1 << bits) - 1
+    t = torch.arange(256, dtype=torch.float32)
+    ramp = (t % (2 * top + 1))[:, None, None] + torch.arange(128, dtype=torch.float32)[None, None, :] % 3
+    key = (ramp.expand(256, 4, 128) + torch.arange(4, dtype=torch.float32)[None, :, None]).to(torch.bfloat16)
+    value = key.flip(0).contiguous()
+    cache = _cache(key, value, device, k_bits=bits, v_bits=bits, group_size=32, residual_length=0)
+    seg = K.from_dense(f32(key), f32(value), k_bits=bits, v_bits=bits, group_size=32, residual_length=0,
+                       native=True, in_dtype="bf16")
+    _assert_cache_equal(cache, seg)
+
+
 def test_config0_pack_with_outliers_and_residual(device):
     key, value = kv_pair(2048, seed=0)
     cache = _cache(key, value, device, k_bits=2, v_bits=2, group_size=32, residual_length=128)

@@ -189,6 +189,21 @@ __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, 
 __device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
 __device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
 
+// rint(div_rn(d, s)), the code of a quantization step (round half to even),
+// with the division replaced by a multiply by r = v_rcp_f32(s) wherever that
+// cannot change the code.  r is within one ulp of 1/s, so y = RN(d r) is
+// within |y| (2^-23 + 2^-24 + 2^-47) of d/s, and div_rn(d, s) within half an
+// ulp (|y| 2^-24) of it: both lie within |y| 2^-22 of each other.  When y is
+// farther than |y| 2^-20 from a half-integer they round to the same integer;
+// otherwise -- or when y is not finite, or r is not a normal number (v_rcp_f32
+// flushes denormal results) -- the correctly rounded division decides.
+__device__ __forceinline__ float quant_rint(float d, float s, float r) {
+  const float y = d * r;
+  const float q = rintf(y);
+  const float dist = fabsf(fabsf(y - q) - 0.5f);
+  return dist > fabsf(y) * 0x1p-20f && r >= 0x1p-126f ? q : rintf(div_rn(d, s));
+}
+
 // Code `pos_in_word` of the word at `word_off` (2/4-bit, LSB first), or the
 // byte at `word_off` for 8-bit codes (physical.py:88-104).
 template <int BITS>

@@ -55,15 +55,16 @@ __device__ void pack_key_group(const void *__restrict__ key, int64_t st, int64_t
   const float mn0 = r0.mn, mn1 = r1.mn;
   const float s0 = clamp_min_nan(div_rn(sub_rn(r0.mx, mn0), kMaxCode), kEps);
   const float s1 = clamp_min_nan(div_rn(sub_rn(r1.mx, mn1), kMaxCode), kEps);
+  const float rcp_s0 = __builtin_amdgcn_rcpf(s0), rcp_s1 = __builtin_amdgcn_rcpf(s1);
 
   if constexpr (BITS == 8) {
     uint8_t *out = static_cast<uint8_t *>(code);
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-      const float q0 = fminf(fmaxf(rintf(div_rn(sub_rn(x0[i], mn0), s0)), 0.0f), kMaxCode);
+      const float q0 = fminf(fmaxf(quant_rint(sub_rn(x0[i], mn0), s0, rcp_s0), 0.0f), kMaxCode);
       out[h * kc_sh + c * kc_sd + (t0 + i) * kc_sw] = static_cast<uint8_t>(q0);
       if (has1) {
-        const float q1 = fminf(fmaxf(rintf(div_rn(sub_rn(x1[i], mn1), s1)), 0.0f), kMaxCode);
+        const float q1 = fminf(fmaxf(quant_rint(sub_rn(x1[i], mn1), s1, rcp_s1), 0.0f), kMaxCode);
         out[h * kc_sh + (c + 1) * kc_sd + (t0 + i) * kc_sw] = static_cast<uint8_t>(q1);
       }
     }
@@ -78,9 +79,9 @@ __device__ void pack_key_group(const void *__restrict__ key, int64_t st, int64_t
       for (int j = 0; j < kPerWord; ++j) {
         const int i = w * kPerWord + j;
         const uint32_t q0 = static_cast<uint32_t>(
-            fminf(fmaxf(rintf(div_rn(sub_rn(x0[i], mn0), s0)), 0.0f), kMaxCode));
+            fminf(fmaxf(quant_rint(sub_rn(x0[i], mn0), s0, rcp_s0), 0.0f), kMaxCode));
         const uint32_t q1 = static_cast<uint32_t>(
-            fminf(fmaxf(rintf(div_rn(sub_rn(x1[i], mn1), s1)), 0.0f), kMaxCode));
+            fminf(fmaxf(quant_rint(sub_rn(x1[i], mn1), s1, rcp_s1), 0.0f), kMaxCode));
         w0 |= q0 << (j * BITS);
         w1 |= q1 << (j * BITS);
       }
@@ -157,10 +158,11 @@ __device__ void pack_value_chunk(const void *__restrict__ value, int64_t st, int
   r.finish();
   const float mn = r.mn, mx = r.mx;
   const float s = clamp_min_nan(div_rn(sub_rn(mx, mn), kMaxCode), kEps);
+  const float rcp_s = __builtin_amdgcn_rcpf(s);
   uint32_t q[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i)
-    q[i] = static_cast<uint32_t>(fminf(fmaxf(rintf(div_rn(sub_rn(x[i], mn), s)), 0.0f), kMaxCode));
+    q[i] = static_cast<uint32_t>(fminf(fmaxf(quant_rint(sub_rn(x[i], mn), s, rcp_s), 0.0f), kMaxCode));
 
   if constexpr (BITS == 8) {
     uint8_t *out = static_cast<uint8_t *>(code);
@@ -501,9 +503,10 @@ __global__ __launch_bounds__(256) void fake_quant_kernel(FakeQuantArgs a) {
   r.finish();
   const float mn = r.mn;
   const float scale = div_rn(clamp_min_nan(sub_rn(r.mx, mn), kEps), a.max_code);
+  const float rcp_scale = __builtin_amdgcn_rcpf(scale);
   for (int64_t i = start; i < stop; ++i) {
     const float x = load_as_f32<DT>(a.data, base + i * step);
-    const float code = fminf(fmaxf(rintf(div_rn(sub_rn(x, mn), scale)), 0.0f), a.max_code);
+    const float code = fminf(fmaxf(quant_rint(sub_rn(x, mn), scale, rcp_scale), 0.0f), a.max_code);
     store_from_f32<DT>(a.out, base + i * step, add_rn(mul_rn(code, scale), mn));
   }
 }
@@ -543,11 +546,12 @@ __global__ __launch_bounds__(256) void fake_quant_tokens_kernel(FakeQuantArgs a)
   const float mn0 = r0.mn, mn1 = r1.mn;
   const float s0 = div_rn(clamp_min_nan(sub_rn(r0.mx, mn0), kEps), a.max_code);
   const float s1 = div_rn(clamp_min_nan(sub_rn(r1.mx, mn1), kEps), a.max_code);
+  const float rcp_s0 = __builtin_amdgcn_rcpf(s0), rcp_s1 = __builtin_amdgcn_rcpf(s1);
 #pragma unroll
   for (int i = 0; i < GM; ++i) {
     if (i < n) {
-      const float c0 = fminf(fmaxf(rintf(div_rn(sub_rn(x0[i], mn0), s0)), 0.0f), a.max_code);
-      const float c1 = fminf(fmaxf(rintf(div_rn(sub_rn(x1[i], mn1), s1)), 0.0f), a.max_code);
+      const float c0 = fminf(fmaxf(quant_rint(sub_rn(x0[i], mn0), s0, rcp_s0), 0.0f), a.max_code);
+      const float c1 = fminf(fmaxf(quant_rint(sub_rn(x1[i], mn1), s1, rcp_s1), 0.0f), a.max_code);
       store_pair<DT>(a.out, base + i * a.st, add_rn(mul_rn(c0, s0), mn0), add_rn(mul_rn(c1, s1), mn1));
     }
   }
@@ -582,13 +586,14 @@ __global__ __launch_bounds__(256) void fake_quant_channels_kernel(FakeQuantArgs 
   r.finish();
   const float mn = r.mn;
   const float s = div_rn(clamp_min_nan(sub_rn(r.mx, mn), kEps), a.max_code);
+  const float rcp_s = __builtin_amdgcn_rcpf(s);
   uint32_t o[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float v[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const float c = fminf(fmaxf(rintf(div_rn(sub_rn(x[2 * j + e], mn), s)), 0.0f), a.max_code);
+      const float c = fminf(fmaxf(quant_rint(sub_rn(x[2 * j + e], mn), s, rcp_s), 0.0f), a.max_code);
       v[e] = add_rn(mul_rn(c, s), mn);
     }
     o[j] = DT == UC_BF16 ? (f32_to_bf16_bits(v[0]) | (uint32_t(f32_to_bf16_bits(v[1])) << 16))
