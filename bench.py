@@ -139,6 +139,49 @@ def time_steps(fn, steps, warmup, stream):
     return start.elapsed_time(stop) / steps
 
 
+# The GPU's clocks ramp up over the first ~20-50 ms of sustained work after an
+# idle spell; steps timed before that read 10-20 % slow.  settle() runs the
+# step (untimed, before the W warm-up steps) until SETTLE_MS of GPU time has
+# passed, so the K timed steps see the clocks a decode loop runs at.
+SETTLE_MS = 200.0
+
+
+def settle(fn, stream, settle_ms=SETTLE_MS, max_steps=20000):
+    """Run fn back to back until settle_ms of GPU time has elapsed (checked
+    every 16 steps); returns (steps run, GPU ms)."""
+
+    start = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    done, elapsed = 0, 0.0
+    while done < max_steps and elapsed < settle_ms:
+        for _ in range(16):
+            fn()
+        done += 16
+        mark = torch.cuda.Event(enable_timing=True)
+        mark.record(stream)
+        mark.synchronize()
+        elapsed = start.elapsed_time(mark)
+    return done, elapsed
+
+
+def time_steps_each(fn, steps, warmup, stream):
+    """W warm-up steps, then K timed steps with an event after each: returns
+    (mean ms per step over the K steps, [ms of each step]).  The mean is
+    first-to-last event time / K, the same bracket as time_steps."""
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    events[0].record(stream)
+    for i in range(steps):
+        fn()
+        events[i + 1].record(stream)
+    torch.cuda.synchronize()
+    each = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
+    return events[0].elapsed_time(events[-1]) / steps, each
+
+
 def long_context_decode(device, steps, layers=LAYERS, tokens=32768):
     """Config 4's packed segment as a pure-packed variant: batch 1, 28 layers x
     32768 tokens (32640 packed 2-bit + 128 residual), one decode step = one
@@ -159,6 +202,7 @@ def long_context_decode(device, steps, layers=LAYERS, tokens=32768):
     batch = KiviDecodeBatch(caches, queries)
     stream = torch.cuda.current_stream(device)
     sid = stream.cuda_stream
+    settle(lambda: batch.run(sid), stream)
     ms = time_steps(lambda: batch.run(sid), steps, max(20, steps), stream)
     gbs = batch.algorithmic_bytes / (ms * 1e-3) / 1e9
     return {
@@ -214,6 +258,7 @@ def editing_attention(device, steps, layers=LAYERS, bits=BITS):
             nat.call("uc_kivi_attn_mq_segments", item, 1, dense, 2, q.data_ptr(), out.data_ptr(), lse.data_ptr(),
                      bits, GROUP, HQ, HKV, D, lq, bf16, bf16, bf16, 1.0 / math.sqrt(D), sid)
 
+    settle(step, stream)
     ms = time_steps(step, steps, 2, stream)
     flop = 4 * lq * HQ * keys * D
     tflops = flop * layers / (ms * 1e-3) / 1e12
@@ -322,6 +367,7 @@ def mixed_decode(device, steps, layers=LAYERS):
     batch = MixedDecodeBatch(groups, queries)
     stream = torch.cuda.current_stream(device)
     sid = stream.cuda_stream
+    settle(lambda: batch.run(sid), stream)
     ms = time_steps(lambda: batch.run(sid), steps, max(20, steps), stream)
     step_bytes = batch.algorithmic_bytes
     gbs = step_bytes / (ms * 1e-3) / 1e9
@@ -700,7 +746,8 @@ def main():
     stream = torch.cuda.current_stream(device)
     sid = stream.cuda_stream
     run = lambda: batch.run(sid)  # noqa: E731
-    ms = time_steps(run, args.steps, args.warmup, stream)
+    settle_steps, settle_ms = settle(run, stream)
+    ms, step_ms = time_steps_each(run, args.steps, args.warmup, stream)
     if args.only_decode:
         print(json.dumps({"config1_decode_ms": round(ms, 5),
                           "gbs": round(batch.algorithmic_bytes / (ms * 1e-3) / 1e9, 2)}))
@@ -744,6 +791,10 @@ def main():
             "bytes_per_launch": step_bytes,
         },
         "per_layer_launches_gbs": round(step_bytes / (ms_layers * 1e-3) / 1e9, 2),
+        # untimed clock settling before the W warm-up steps, and each timed
+        # step's own event time (their mean is ms_per_step)
+        "clock_settle": {"steps": settle_steps, "gpu_ms": round(settle_ms, 1)},
+        "step_ms": [round(t, 5) for t in step_ms],
     }
     pack_gbs, pack_call_ms = pack_throughput(device, max(20, args.steps))
     result["pack_gbs"] = round(pack_gbs, 2)

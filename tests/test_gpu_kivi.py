@@ -157,6 +157,56 @@ def test_fake_quant_bit_exact(device, bits):
     assert asymmetric_fake_quant(key.to(device), bits=16, dim=0, group_size=32) is not None
 
 
+def _group_ends(x, dim, group, lo, hi):
+    # the first element of every group along `dim` is lo and the second hi, so
+    # each group's minimum and maximum are known
+    idx = torch.arange(x.shape[dim]) % group
+    shape = [1, 1, 1]
+    shape[dim] = -1
+    idx = idx.view(shape).expand_as(x)
+    return torch.where(idx == 0, torch.full_like(x, lo), torch.where(idx == 1, torch.full_like(x, hi), x))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float32, "fp32")])
+def test_fake_quant_at_exact_half_steps(device, bits, dtype, name):
+    # integer groups with minimum 0 and maximum 2(2^b - 1): the scale is exactly
+    # 2, so every odd element's (x - min) / scale is a half, decided by
+    # round-half-even of the correctly rounded quotient (the kernels' exact
+    # fallback).  Keys along tokens (200 tokens: a partial last group), values
+    # along channels; integers up to 256 (and 510) are exact in bf16.
+    top = (1 << bits) - 1
+    hi = 2 * top
+    g = torch.Generator().manual_seed(40 + bits)
+    base = torch.randint(0, min(hi, 256) + 1, (200, 4, 128), generator=g).to(torch.float32)
+    for fn, dim in ((kivi_fake_quant_key, 0), (kivi_fake_quant_value, 2)):
+        src = _group_ends(base, dim, 32, 0.0, float(hi)).to(dtype)
+        got = fn(src.to(device), bits=bits, group_size=32)
+        exp = K.fake_quant(f32(src), bits=bits, dim=dim, group_size=32, out_dtype=name)
+        assert np.array_equal(f32(got), exp), (bits, dim)
+
+
+@pytest.mark.parametrize("bits,exponent", [(2, -24), (3, -25), (4, -26), (8, -27)])
+def test_fake_quant_range_below_eps_times_codes(device, bits, exponent):
+    # groups whose range r satisfies eps <= r < eps * (2^b - 1) (and some below
+    # eps): operators/builtin.py:50 clamps the range, then divides, so the scale
+    # is below eps; a scale clamped after the division would be eps.  The
+    # elements are k * 2^e * 2^j with k <= 2^b - 1 and j in 0..3 (keys), exact
+    # in bf16, and every group holds k = 0 and k = 2^b - 1, so its scale is
+    # exactly 2^(e + j) and every code is k.
+    top = (1 << bits) - 1
+    g = torch.Generator().manual_seed(60 + bits)
+    k = torch.randint(0, top + 1, (200, 4, 128), generator=g).to(torch.float32)
+    col = (torch.arange(128) % 4).to(torch.float32).view(1, 1, -1)
+    for fn, dim in ((kivi_fake_quant_key, 0), (kivi_fake_quant_value, 2)):
+        steps = _group_ends(k, dim, 32, 0.0, float(top)) * (2.0 ** exponent)
+        src = (steps * torch.exp2(col if dim == 0 else torch.zeros_like(col))).to(torch.bfloat16)
+        got = fn(src.to(device), bits=bits, group_size=32)
+        exp = K.fake_quant(f32(src), bits=bits, dim=dim, group_size=32, out_dtype="bf16")
+        assert np.array_equal(f32(got), exp), (bits, dim)
+        assert torch.equal(got.cpu(), src)  # every scale is the exact step: the output is the input
+
+
 @pytest.mark.parametrize("group,dtype,name", [(16, torch.float16, "fp16"), (64, torch.bfloat16, "bf16"),
                                               (128, torch.bfloat16, "bf16"), (32, torch.float32, "fp32")])
 def test_fake_quant_groups_and_dtypes(device, group, dtype, name):

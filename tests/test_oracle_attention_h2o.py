@@ -3,7 +3,8 @@
 Known answers come from UniCache's tests (test_physical.py:181-202 LSE merge,
 1195-1215 H2O per-head selection, 1217-1270 budget counts); the rest are
 closed forms (LSE of the logits, GQA == repeated-KV attention computed by
-torch) and a brute-force selection by Python's sort.
+torch, packed logits and P.V over a segment built word by word) and a
+brute-force selection by Python's sort.
 """
 
 import math
@@ -14,6 +15,7 @@ import torch
 
 from oracle import attention as A
 from oracle import h2o as H
+from oracle import kivi as K
 
 
 def test_lse_merge_equals_global_softmax():
@@ -62,6 +64,108 @@ def test_attention_summary_closed_forms():
     out_c, _ = A.attention_summary(q, k, np.full_like(v, 2.5))
     assert np.allclose(out_c, 2.5)
     assert out.shape == (3, 14, 32)
+
+
+# ---------------------------------------------- packed attention parts --
+def _segment_parts():
+    """A 2-bit, kernel-native segment built word by word: 2 KV heads, D = 16
+    (so 1/sqrt(D) = 1/4 exactly), 32 packed tokens at G = 16 and 2 residual
+    tokens, with keys and values that differ.  Returns the segment and the
+    dequantized key / value as Python functions of (head, token, channel),
+    written from the construction (not from the oracle's unpacking).
+
+    Word 0xE4E4E4E4 holds the codes 0, 1, 2, 3 repeated (LSB first), word
+    0x1B1B1B1B the codes 3, 2, 1, 0.  Every value below is exact in fp16 and
+    bf16.
+    """
+
+    e4 = np.uint32(0xE4E4E4E4).view(np.int32)
+    w1b = np.uint32(0x1B1B1B1B).view(np.int32)
+    kc = np.empty((2, 16, 2), np.int32)                       # [Hkv, D, Tq/16]
+    kc[0], kc[1] = e4, w1b
+    ks = np.tile(np.array([0.5, 2.0], np.float32), (2, 16, 1))  # [Hkv, D, Tq/G]
+    km = np.array([-1.0, 3.0], np.float32)[None, None, :] + (np.arange(16, dtype=np.float32) / 8)[None, :, None]
+    km = np.ascontiguousarray(np.broadcast_to(km, (2, 16, 2)))
+    vc = np.empty((2, 32, 1), np.int32)                       # [Hkv, Tq, D/16]
+    vc[0], vc[1] = w1b, e4
+    vs = np.full((2, 32, 1), 0.25, np.float32)                # [Hkv, Tq, D/G]
+    vm = np.stack([np.arange(32), -np.arange(32)]).astype(np.float32)[:, :, None]
+
+    def key_code(h, t):
+        return t % 4 if h == 0 else 3 - t % 4
+
+    def value_code(h, c):
+        return 3 - c % 4 if h == 0 else c % 4
+
+    def khat(h, t, d):
+        if t < 32:
+            g = t // 16
+            return key_code(h, t) * (0.5, 2.0)[g] + (-1.0, 3.0)[g] + d / 8
+        return (d - 8) * 0.25 * (t - 31) * (h + 1)
+
+    def vhat(h, t, c):
+        if t < 32:
+            return value_code(h, c) * 0.25 + (t if h == 0 else -t)
+        return 10.0 * (t - 31) + c / 4 + h
+
+    rk = np.array([[[khat(h, t, d) for d in range(16)] for h in range(2)] for t in (32, 33)], np.float32)
+    rv = np.array([[[vhat(h, t, c) for c in range(16)] for h in range(2)] for t in (32, 33)], np.float32)
+    seg = K.PackedSegment(kc, ks, km, vc, vs, vm, rk, rv, k_bits=2, v_bits=2, group_size=16,
+                          quantized_tokens=32, native=True)
+    return seg, khat, vhat
+
+
+def _hand_query():
+    # [Lq = 2, Hq = 4, D = 16], small halves: query head h reads KV head h // 2
+    return np.array([[[((l + 2 * h + d) % 5 - 2) * 0.5 for d in range(16)] for h in range(4)] for l in range(2)],
+                    np.float32)
+
+
+def test_packed_logits_closed_form():
+    # kivi_cuda.py:283-287 / physical.py:469-470: logits over [packed | residual]
+    # tokens, q . k_hat scaled by 1/sqrt(D)
+    seg, khat, _ = _segment_parts()
+    q = _hand_query()
+    got = A.packed_logits(seg, q)
+    assert got.shape == (4, 2, 34)
+    expected = np.array([[[sum(float(q[l, h, d]) * khat(h // 2, t, d) for d in range(16)) / 4 for t in range(34)]
+                          for l in range(2)] for h in range(4)])
+    assert np.allclose(got, expected, rtol=0, atol=1e-12)
+    # the residual tokens come last: token 32's logit is q . (d - 8) / 4 * (h // 2 + 1) / 4
+    assert got[2, 1, 32] == sum(float(q[1, 2, d]) * (d - 8) * 0.5 for d in range(16)) / 4
+
+
+def test_packed_pv_closed_form():
+    # physical.py:472-473: the apply_value closure multiplies P by the
+    # dequantized values (not the keys) over [packed | residual]
+    seg, khat, vhat = _segment_parts()
+    rng = np.random.default_rng(31)
+    p = rng.random((4, 2, 34))
+    p /= p.sum(-1, keepdims=True)
+    got = A.packed_pv(seg, p)
+    assert got.shape == (4, 2, 16)
+    expected = np.array([[[sum(p[h, l, t] * vhat(h // 2, t, c) for t in range(34)) for c in range(16)]
+                          for l in range(2)] for h in range(4)])
+    assert np.allclose(got, expected, rtol=0, atol=1e-12)
+    # a one-hot row picks one value row: the packed token 5 of KV head 1, and residual token 33 of head 0
+    one = np.zeros((4, 2, 34))
+    one[3, 0, 5] = 1.0
+    one[0, 1, 33] = 1.0
+    picked = A.packed_pv(seg, one)
+    assert picked[3, 0].tolist() == [vhat(1, 5, c) for c in range(16)]
+    assert picked[0, 1].tolist() == [vhat(0, 33, c) for c in range(16)]
+    assert picked[3, 0].tolist() != [khat(1, 5, c) for c in range(16)]
+
+
+def test_packed_summary_equals_softmax_of_packed_logits():
+    # the fused summary of the whole segment is softmax(packed_logits) . V_hat
+    # with the natural-log LSE of those logits
+    seg, _, _ = _segment_parts()
+    q = _hand_query()
+    out, lse = A.packed_summary(seg, q)
+    logits = A.packed_logits(seg, q)
+    assert np.allclose(lse, np.log(np.exp(logits).sum(-1)), atol=1e-12)
+    assert np.allclose(out.transpose(1, 0, 2), A.packed_pv(seg, A.softmax(logits)), atol=1e-12)
 
 
 # --------------------------------------------------------------------- H2O --

@@ -122,6 +122,38 @@ def test_fake_quant_agrees_with_packed_codes():
             assert np.array_equal(fq, (codes.astype(np.float32) * s).astype(np.float32) + m)
 
 
+@pytest.mark.parametrize("bits,exponent", [(2, -24), (3, -25), (4, -26), (8, -27)])
+def test_fake_quant_clamps_the_range_before_dividing(bits, exponent):
+    # operators/builtin.py:50: scale = max(mx - mn, eps) / (2^b - 1).  For the
+    # ramp k * 2^e (k = 0 .. 2^b - 1) the range r = (2^b - 1) * 2^e lies in
+    # [eps, eps * (2^b - 1)), so the scale is exactly 2^e, every code is k and
+    # the ramp comes back unchanged.  The packing quantizer's
+    # max(r / (2^b - 1), eps) (physical.py:129) would clamp the scale to eps and
+    # round the ramp to multiples of eps instead.
+    top = (1 << bits) - 1
+    step = np.float32(2.0 ** exponent)
+    assert K.EPS <= top * step < K.EPS * top
+    ramp = np.arange(top + 1, dtype=np.float32) * step
+    for out_dtype in ("fp32", "bf16"):  # every ramp value has <= 8 significant bits
+        assert K.fake_quant(ramp, bits=bits, dim=0, group_size=top + 1, out_dtype=out_dtype).tolist() == ramp.tolist()
+    clamped_after = np.clip(np.rint(ramp / K.EPS), 0, top) * K.EPS
+    assert not np.array_equal(clamped_after, ramp)  # the two formulas really differ here
+    # groups along the last dim (values), two groups with their own minima
+    rows = np.stack([ramp, ramp[::-1] + np.float32(0.5)])[None]  # [1, 2, top + 1]
+    out = K.fake_quant(rows, bits=bits, dim=-1, group_size=top + 1, out_dtype="fp32")
+    assert out.tolist() == rows.tolist()
+
+
+def test_fake_quant_range_below_eps():
+    # r = 3 * 2^-26 < eps at 2 bits: the scale is fl(eps / 3) and the codes of
+    # 0, 2^-26, 2^-25, 3 * 2^-26 are rint(3k/8) = 0, 0, 1, 1 (scaled by 1 + O(2^-24)),
+    # so the output is [0, 0, s, s]; a scale clamped after dividing (eps) would
+    # give all zeros
+    s = np.float32(K.EPS / np.float32(3))
+    x = np.array([0, 1, 2, 3], np.float32) * np.float32(2.0 ** -26)
+    assert K.fake_quant(x, bits=2, dim=0, group_size=4, out_dtype="fp32").tolist() == [0.0, 0.0, s, s]
+
+
 def test_bf16_rounding_known_values():
     vals = np.array([1.0, 1.00390625, 1.005859375, 1.0078125, -0.0, np.inf, 3.0e38], dtype=np.float32)
     out = K.round_bf16(vals)
