@@ -133,6 +133,19 @@ def test_batched_decode_many_units_ragged(device, bits):
         check_summary(batch.outputs[i], batch.lses[i], segs[i], qs[i], what=f"item {i} ({lengths[i]} tokens)")
 
 
+@pytest.mark.parametrize("hq,hkv,lq", [(32, 4, 1), (8, 4, 2), (16, 2, 1), (28, 4, 2), (12, 4, 3)])
+def test_decode_query_rows_around_the_fold(device, hq, hkv, lq):
+    # 2-bit G=32 decode with at most 8 query rows per KV head (query heads per
+    # KV head x query length) uses each MFMA column half for one of a wave's two
+    # key groups; 9-16 rows use all 16 columns per group.  Lengths leave waves
+    # whose second half has no packed token (544 and 2464 packed tokens).
+    for tokens, seed in ((700, 140), (2600, 141)):
+        cache, seg = _pair(tokens, seed, 2, 32, 128, device, heads=hkv)
+        q = queries(lq, heads=hq, seed=seed + 10)
+        out, lse = packed_kivi_attention_summary(cache, q.to(device))
+        check_summary(out, lse, seg, q, what=f"Hq {hq} Hkv {hkv} Lq {lq} T {tokens}")
+
+
 def test_decode_is_deterministic(device):
     cache, _ = _pair(4096, 11, 2, 32, 128, device)
     q = queries(1, seed=2).to(device)

@@ -92,6 +92,7 @@ struct Tiles {
   static_assert(TW >= 2 && TW % 2 == 0, "a wave owns whole 32-token value blocks");
   static_assert(KG >= 1 && G % 16 == 0, "a tile lies in one group");
   static_assert(GW == 1 || GW == 2, "the bias MFMA holds one or two groups per wave");
+  static_assert(WT <= 64, "the cmin ones row covers a wave's tokens");
 };
 
 // v_perm selector: byte k of src1 at byte 0, byte k of src0 at byte 2, zeros elsewhere.
@@ -167,14 +168,17 @@ struct WaveState {
 // the probabilities and the output is rescaled.  `valid_rows` tokens of the
 // wave's tiles are real (the rest of the last super-tile reads past the end).
 // SUM: keep the running sum in st.l (the packed path sums P by MFMA instead).
+// tile_base: the wave-tile index of acc[0] (the column-folded path gives each
+// half of the columns its own tiles).
 template <int NP, bool SUM>
-__device__ __forceinline__ void softmax_tiles(f4 (&acc)[NP], int valid_rows, WaveState &st, int kap) {
-  if (valid_rows < 16 * NP) {
+__device__ __forceinline__ void softmax_tiles(f4 (&acc)[NP], int valid_rows, WaveState &st, int kap,
+                                              int tile_base = 0) {
+  if (valid_rows < 16 * (NP + tile_base)) {
 #pragma unroll
     for (int i = 0; i < NP; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        if (16 * i + 4 * kap + v >= valid_rows) acc[i][v] = kNegInf;
+        if (16 * (tile_base + i) + 4 * kap + v >= valid_rows) acc[i][v] = kNegInf;
   }
   float mx = kNegInf;
 #pragma unroll
@@ -213,16 +217,19 @@ __device__ __forceinline__ void softmax_tiles(f4 (&acc)[NP], int valid_rows, Wav
 // (rows padded to 72 dwords: the 16 rows of one fragment read hit distinct
 // banks); lane (n, k-slice) reads its B fragment of block kb from here.
 constexpr int kQPad = kD + 16;
+constexpr int kOnesLen = 64;  // >= the tokens a wave computes per super-tile (WT)
 
 template <int QD>
 __device__ __forceinline__ void stage_queries_t(_Float16 (*sq)[kQPad], const void *query, int64_t h,
-                                                const MfmaParams &p) {
-  // 16 rows x 128 channels; thread t < 128 converts 16 consecutive channels of row t/8
+                                                const MfmaParams &p, bool fold) {
+  // 16 rows x 128 channels; thread t < 128 converts 16 consecutive channels of
+  // row t/8 (rows 8-15 repeat rows 0-7 for the column-folded packed path)
   if (threadIdx.x >= 128) return;
   const int n = threadIdx.x / 8, d0 = (threadIdx.x % 8) * 16;
+  const int src = fold ? (n & 7) : n;
   uint4 raw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-  if (n < p.rows) {
-    const int64_t g = n / p.Lq, i = n % p.Lq;
+  if (src < p.rows) {
+    const int64_t g = src / p.Lq, i = src % p.Lq;
     const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(query) +
                                                        (i * p.Hq + h * p.group + g) * kD + d0);
     raw[0] = src[0];
@@ -235,17 +242,17 @@ __device__ __forceinline__ void stage_queries_t(_Float16 (*sq)[kQPad], const voi
 // Query rows of the KV head staged once per workgroup as fp16 [row][channel];
 // fp32 queries take the element-wise path.
 __device__ __forceinline__ void stage_queries(_Float16 (*sq)[kQPad], const void *query, int64_t h,
-                                              const MfmaParams &p) {
+                                              const MfmaParams &p, bool fold) {
   if (p.qd == UC_BF16) {
-    stage_queries_t<UC_BF16>(sq, query, h, p);
+    stage_queries_t<UC_BF16>(sq, query, h, p, fold);
   } else if (p.qd == UC_FP16) {
-    stage_queries_t<UC_FP16>(sq, query, h, p);
+    stage_queries_t<UC_FP16>(sq, query, h, p, fold);
   } else {
     for (int idx = threadIdx.x; idx < 16 * kD; idx += kThreads) {
-      const int n = idx / kD, d = idx % kD;
+      const int n = idx / kD, d = idx % kD, src = fold ? (n & 7) : n;
       float v = 0.0f;
-      if (n < p.rows) {
-        const int64_t g = n / p.Lq, i = n % p.Lq;
+      if (src < p.rows) {
+        const int64_t g = src / p.Lq, i = src % p.Lq;
         v = static_cast<const float *>(query)[(i * p.Hq + h * p.group + g) * kD + d];
       }
       sq[n][d] = to_h(v);
@@ -277,6 +284,10 @@ struct PackedRegion {
   Rsrc kcode, kscale, kmin, vcode, vscale, vmin;
 };
 
+// A buffer offset past every resource of this file (their sizes are checked to
+// stay below 2^31 bytes): the load returns 0 and touches no memory.
+constexpr uint32_t kOffOutside = 0x80000000u;
+
 // Issue this wave's loads of the super-tile starting at token t0 (a
 // multiple of ST): tokens t0 + WT wave ...  Rows past the packed tokens fall
 // outside the buffer resources and read as 0.  Lane l loads
@@ -301,6 +312,11 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
     pf.vw[0] = bload128(rg.vcode, (tok * Tl::VWPT + 4 * wq) * 4u);
     pf.vw[1] = bload128(rg.vcode, ((tok + 1) * Tl::VWPT + 4 * wq) * 4u);
   }
+  // Statistics: lanes of stat 0 load scales, of stat 1 minima.  Each load
+  // names one resource for the whole wave (a resource chosen per lane would be
+  // looped over its distinct values); lanes that do not take a load give it an
+  // offset past any resource (bit 31 set), which reads 0, and the two loads
+  // are OR-ed.
   {  // key stats [group][D]: GW rows of 256 bytes per stat
     constexpr int NKS = Tl::GW * 16;  // 16-byte chunks per stat
     const int i = lane % NKS, stat = lane / NKS;
@@ -464,7 +480,7 @@ __device__ __forceinline__ h8 gather_and(const uint32_t (&piece)[4 / CPB], uint3
 template <int BITS, int G>
 __device__ __forceinline__ void compute_tile(const WaveStage<BITS, G> &ws, const h8 (&qf)[4],
                                              const LaneConst<BITS, G> &lc, int valid_rows, float scale_log2,
-                                             WaveState &st) {
+                                             const _Float16 *ones, WaveState &st) {
   using Tl = Tiles<BITS, G>;
   constexpr int NPL = Tl::NPL, CPB = Tl::CPB;
   const int lane = threadIdx.x & 63, r = lane & 15, kap = lane >> 4;
@@ -517,16 +533,12 @@ __device__ __forceinline__ void compute_tile(const WaveStage<BITS, G> &ws, const
     const int ta = 2 * kc;  // first tile of the block within the wave's tokens
     const h4 pa4 = cvt4(acc[2 * kc]), pb4 = cvt4(acc[2 * kc + 1]);
     const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
-    {  // A rows g < NGD: the value minima of group g; row NGD: ones (the sum of P)
-      h8 am = h8{0, 0, 0, 0, 0, 0, 0, 0};
-      if (r < Tl::NGD) {
-        const h4 ma = *reinterpret_cast<const h4 *>(&ws.vm[r][16 * ta + 4 * kap]);
-        const h4 mb4 = *reinterpret_cast<const h4 *>(&ws.vm[r][16 * ta + 16 + 4 * kap]);
-        am = h8{ma[0], ma[1], ma[2], ma[3], mb4[0], mb4[1], mb4[2], mb4[3]};
-      } else if (r == Tl::NGD) {
-        am = h8{1, 1, 1, 1, 1, 1, 1, 1};
-      }
-      st.cmin = mfma32(am, p8, st.cmin);
+    {  // A rows g < NGD: the value minima of group g; rows from NGD on read a
+       // row of ones, so row NGD accumulates the sum of P (rows past it are unused)
+      const _Float16 *mrow = r < Tl::NGD ? &ws.vm[r][0] : ones;
+      const h4 ma = *reinterpret_cast<const h4 *>(mrow + 16 * ta + 4 * kap);
+      const h4 mb4 = *reinterpret_cast<const h4 *>(mrow + 16 * ta + 16 + 4 * kap);
+      st.cmin = mfma32(h8{ma[0], ma[1], ma[2], ma[3], mb4[0], mb4[1], mb4[2], mb4[3]}, p8, st.cmin);
     }
     // this lane's NPL pairs of every 16-channel block: dwords blk of NPL slots
     uint32_t pv[NPL][8];
@@ -554,10 +566,100 @@ __device__ __forceinline__ void compute_tile(const WaveStage<BITS, G> &ws, const
   }
 }
 
+// Per-lane constants of the column-folded path.
+struct FoldConst {
+  int half;               // 0: columns 0-7 (the wave's first 32 tokens), 1: columns 8-15 (the next 32)
+  const _Float16 *mrow;   // A row of the cmin MFMA (minima of the row's group and half, or ones)
+  int voff[2];            // value-stat read offset of block kc: the block's tokens, or a zeroed pad
+};
+
+// Column-folded variant of compute_tile for 2-bit codes in 32-token groups
+// with at most 8 query rows (decode at GQA 7:1): MFMA column n < 8 is query
+// row n over the wave's first group (tiles 0 and 1), column n + 8 the same
+// query row over its second group (tiles 2 and 3).  One B operand carries each
+// half's key scale; every lane keeps the logits of its own half's two tiles,
+// so its softmax covers 32 tokens, not 64.  The value products of a 32-token
+// block get zeros in the other half's columns (those value scales are read
+// from a zeroed pad of the stat rows), and one cmin MFMA serves both halves
+// (A rows 0-3: minima of the first block's tokens per group, rows 4-7: of the
+// second block's, row 8: ones).  The two halves of a column are merged once,
+// after the split's last super-tile.
 template <int BITS, int G>
+__device__ __forceinline__ void compute_tile_fold(const WaveStage<BITS, G> &ws, const h8 (&qf)[4],
+                                                  const LaneConst<BITS, G> &lc, const FoldConst &fc,
+                                                  int valid_rows, float scale_log2, WaveState &st) {
+  using Tl = Tiles<BITS, G>;
+  static_assert(Tl::TW == 4 && Tl::GW == 2 && Tl::NPL == 1 && Tl::NGD == 4 && Tl::TPW == 16,
+                "the folded path is the 2-bit, 32-token-group layout");
+  const int lane = threadIdx.x & 63, r = lane & 15, kap = lane >> 4;
+
+  // ---- key minimum term: A row r = minima of group r % 2, so element v
+  // holds group v % 2's bias for every column
+  f4 mb = f4{0, 0, 0, 0};
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+    mb = mfma32(*reinterpret_cast<const h8 *>(&ws.km[r % 2][32 * kb + 8 * kap]), qf[kb], mb);
+  const float bias = (fc.half ? mb[1] : mb[0]) * scale_log2;
+
+  // ---- keys: B' = q * key scale of this lane's half, then all four tiles
+  h8 bp[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) bp[kb] = qf[kb] * *reinterpret_cast<const h8 *>(&ws.ks[fc.half][32 * kb + 8 * kap]);
+  f4 a[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 x = *reinterpret_cast<const uint4 *>(&ws.kw[lc.kaddr + i * 256]);
+    const uint32_t pc[4] = {x.x, x.y, x.z, x.w};
+    a[i] = f4{0, 0, 0, 0};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const uint32_t piece[1] = {pc[kb]};
+      a[i] = mfma32(gather_and<Tl::CPB>(piece, lc.kmask), bp[kb], a[i]);
+    }
+  }
+  f4 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[j][v] = __builtin_fmaf(fc.half ? a[j + 2][v] : a[j][v], lc.pw[v], bias);
+  softmax_tiles<2, false>(acc, valid_rows, st, kap, 2 * fc.half);
+
+  const h4 pa4 = cvt4(acc[0]), pb4 = cvt4(acc[1]);
+  const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
+  {
+    const h4 ma = *reinterpret_cast<const h4 *>(fc.mrow);
+    const h4 mb4 = *reinterpret_cast<const h4 *>(fc.mrow + 16);
+    st.cmin = mfma32(h8{ma[0], ma[1], ma[2], ma[3], mb4[0], mb4[1], mb4[2], mb4[3]}, p8, st.cmin);
+  }
+  // ---- values: O^T += V^T P^T over the two 32-token blocks; block kc counts
+  // only in the columns of half kc (the other half's P * scale is zero)
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    uint32_t pv[8];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const uint4 x = *reinterpret_cast<const uint4 *>(&ws.vw[lc.vaddr + kc * 128 + hb * 64]);
+      pv[4 * hb + 0] = x.x; pv[4 * hb + 1] = x.y; pv[4 * hb + 2] = x.z; pv[4 * hb + 3] = x.w;
+    }
+    h8 ps;
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      if ((16 * blk) % G == 0) {
+        const int g = (16 * blk) / G;
+        const h4 sa = *reinterpret_cast<const h4 *>(&ws.vs[g][fc.voff[kc]]);
+        const h4 sb = *reinterpret_cast<const h4 *>(&ws.vs[g][fc.voff[kc] + 16]);
+        ps = p8 * h8{sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+      }
+      const uint32_t piece[1] = {pv[blk]};
+      st.o[blk] = mfma32(gather_and<Tl::CPB>(piece, lc.vmask), ps, st.o[blk]);
+    }
+  }
+}
+
+template <int BITS, int G, bool FOLD>
 __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Float16 (*sq)[kQPad],
-                                             const uc_kivi_item &it, int64_t h, int64_t split,
-                                             const MfmaParams &p, WaveState &st) {
+                                             const _Float16 *ones, const uc_kivi_item &it, int64_t h,
+                                             int64_t split, const MfmaParams &p, WaveState &st) {
   using Tl = Tiles<BITS, G>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -578,6 +680,18 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) qf[kb] = query_frag(sq, kb, lane);
   WaveStage<BITS, G> &ws = sh.st[wave];
+  FoldConst fc{};
+  if constexpr (FOLD) {
+    const int r = lane & 15, kap = lane >> 4;
+    fc.half = r >> 3;
+    fc.mrow = r < 4 ? &ws.vm[r][4 * kap] : r < 8 ? &ws.vm[r - 4][32 + 4 * kap] : ones + 4 * kap;
+    fc.voff[0] = fc.half == 0 ? 4 * kap : 64 + 4 * kap;
+    fc.voff[1] = fc.half == 1 ? 32 + 4 * kap : 64 + 4 * kap;
+    // the value-scale pads [64, 96) of every group row read as zeros
+    static_assert(Tiles<BITS, G>::VSP >= 96, "value-stat rows carry a 32-entry pad");
+    reinterpret_cast<uint32_t *>(&ws.vs[lane >> 4][64])[lane & 15] = 0u;
+    wave_lds_sync();
+  }
   // super-tiles split, split + S, split + 2S, ... (S = packed splits); wave
   // w stages and computes tokens WT w .. WT w + WT - 1 of each on its own
   const int64_t n_super = (Tq + Tl::ST - 1) / Tl::ST;
@@ -592,7 +706,38 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
     wave_lds_sync();
     if (i + 1 < n_it) issue_loads<BITS, G>(pf, rg, static_cast<uint32_t>(t0 + stride), wave);  // lands during compute
     const int valid = static_cast<int>(min<int64_t>(int64_t(Tl::WT), Tq - t0 - int64_t(Tl::WT) * wave));
-    if (valid > 0) compute_tile<BITS, G>(ws, qf, lc, valid, p.scale_log2, st);
+    if (valid > 0) {
+      if constexpr (FOLD)
+        compute_tile_fold<BITS, G>(ws, qf, lc, fc, valid, p.scale_log2, st);
+      else
+        compute_tile<BITS, G>(ws, qf, lc, valid, p.scale_log2, ones, st);
+    }
+  }
+  if constexpr (FOLD) {
+    // finish each half's column as below, then merge the halves of a column
+    // (lanes n and n ^ 8 hold the same query row over different tokens)
+    const int n = lane & 15, kap = lane >> 4, half = n >> 3;
+    float cm[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) cm[g] = __shfl(st.cmin[g], n + 16 * half, kWave);  // row g + 4 half
+    const float l_half = __shfl(st.cmin[0], n + 32, kWave);                      // row 8: sum of P
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int e = (4 * kap + v) % Tl::CPB;
+      const float undo = float(1 << (24 - BITS * e));
+#pragma unroll
+      for (int b = 0; b < 8; ++b) st.o[b][v] = st.o[b][v] * undo + cm[(16 * b) / G];
+    }
+    const float m_o = __shfl_xor(st.m, 8, kWave), l_o = __shfl_xor(l_half, 8, kWave);
+    const float M = fmaxf(st.m, m_o), M_ref = M == kNegInf ? 0.0f : M;
+    const float a_s = fast_exp2(st.m - M_ref), a_o = fast_exp2(m_o - M_ref);
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) st.o[b][v] = st.o[b][v] * a_s + __shfl_xor(st.o[b][v], 8, kWave) * a_o;
+    st.m = M;
+    st.l = kap == 0 ? l_half * a_s + l_o * a_o : 0.0f;  // the merge sums the k-slices
+    return;
   }
   // undo the denormal code scaling 2^(BITS e - 24) of each output channel
   // (channel 16 b + 4 k + v: e depends on k and v only) and add the value
@@ -687,12 +832,13 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
 }
 
 // ------------------------------------------------------------------ kernel --
-template <int BITS, int G, int RD, bool TABLE>
+template <int BITS, int G, int RD, bool TABLE, bool FOLD>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void decode_mfma_kernel(
     const uc_kivi_item *items, uc_kivi_item single,
                                                                MfmaParams p) {
   __shared__ __align__(16) DecShared<BITS, G> sh;
   __shared__ __align__(16) _Float16 sq[16][kQPad];
+  __shared__ __align__(16) _Float16 sones[kOnesLen];  // the ones rows of the cmin MFMA
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Workgroup i runs on XCD i % 8; with enough units its k = i / 8-th
   // workgroup there is split k % S of unit (item, KV head) u = 8 (k / S) + i % 8,
@@ -721,7 +867,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     return;
   }
 
-  stage_queries(sq, it.query, h, p);
+  stage_queries(sq, it.query, h, p, FOLD);
+  if (tid < kOnesLen / 2) reinterpret_cast<uint32_t *>(sones)[tid] = 0x3c003c00u;  // fp16 1.0 pairs
   WaveState st;
 #pragma unroll
   for (int b = 0; b < 8; ++b) st.o[b] = f4{0, 0, 0, 0};
@@ -734,7 +881,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   // instead of forming its tail
   const int64_t splits_res = p.splits_total - p.splits_packed;
   if (split >= splits_res) {
-    packed_split<BITS, G>(sh, sq, it, h, split - splits_res, p, st);
+    packed_split<BITS, G, FOLD>(sh, sq, sones, it, h, split - splits_res, p, st);
   } else {
     const int64_t tr0 = split * kWaves * kResWaveTokens;
     if (tr0 + wave * kResWaveTokens < it.residual_tokens) residual_split<RD>(sq, it, h, tr0, p, st);
@@ -928,13 +1075,30 @@ int64_t decode_mfma_workspace_bytes(int64_t n_items, int64_t heads_kv, int64_t s
   return slots * 16 * kD * int64_t(sizeof(_Float16)) + slots * 16 * 2 * int64_t(sizeof(float));
 }
 
+// The column-folded packed path: 2-bit codes, 32-token groups, <= 8 query rows.
+template <int BITS, int G>
+constexpr bool kFoldable = BITS == 2 && G == 32;
+
 template <int BITS, int G, int RD>
 static void launch_typed(bool table, dim3 grid, hipStream_t stream, const uc_kivi_item *items_dev,
                          const uc_kivi_item &one, const MfmaParams &p) {
+  if constexpr (kFoldable<BITS, G>) {
+    if (p.rows <= 8) {
+      if (table)
+        hipLaunchKernelGGL((decode_mfma_kernel<BITS, G, RD, true, true>), grid, dim3(kThreads), 0, stream, items_dev,
+                           one, p);
+      else
+        hipLaunchKernelGGL((decode_mfma_kernel<BITS, G, RD, false, true>), grid, dim3(kThreads), 0, stream, items_dev,
+                           one, p);
+      return;
+    }
+  }
   if (table)
-    hipLaunchKernelGGL((decode_mfma_kernel<BITS, G, RD, true>), grid, dim3(kThreads), 0, stream, items_dev, one, p);
+    hipLaunchKernelGGL((decode_mfma_kernel<BITS, G, RD, true, false>), grid, dim3(kThreads), 0, stream, items_dev,
+                       one, p);
   else
-    hipLaunchKernelGGL((decode_mfma_kernel<BITS, G, RD, false>), grid, dim3(kThreads), 0, stream, items_dev, one, p);
+    hipLaunchKernelGGL((decode_mfma_kernel<BITS, G, RD, false, false>), grid, dim3(kThreads), 0, stream, items_dev,
+                       one, p);
 }
 
 template <int BITS, int G>
