@@ -340,12 +340,20 @@ def h2o_eviction(device, steps):
 
 
 def mixed_decode(device, steps, layers=LAYERS):
-    """Config 4 decode step: per layer the VAE segment (20352 tokens: 20224
-    packed 2-bit + 128 fp16 residual) and the bf16 tokens kept dense (128
+    """Config 4: per layer the VAE segment (20352 tokens:
+    20224 packed 2-bit + 128 fp16 residual) and the bf16 tokens kept dense (128
     protected + instruction 4096 -> 819 and ViT 8192 -> 1638 after H2O at a 20%
     budget) attended as one softmax; all 28 layers in one
-    uc_kivi_attn_decode_segments launch.  Plus the residual flush: 128 tokens
-    quantized and appended to the packed prefix."""
+    uc_kivi_attn_decode_segments launch.
+
+    Two figures: the decode step itself (the static table, timed back to
+    back), and the 64-step decode loop of the configuration: each step runs
+    the decode launch, then appends one new token to every layer's residual
+    window (one uc_kivi_residual_append launch that also moves the device item
+    table's lengths), and a window that reaches 160 tokens is flushed -- 128 of
+    its tokens quantized into the packed prefix in place -- as the CPU row C4
+    does after its 32nd step.  The loop's host time (enqueueing) is reported
+    beside its GPU time."""
 
     from unicache_amd.storage import PackedKIVICache
     from unicache_amd.storage.decode import MixedDecodeBatch
@@ -371,39 +379,71 @@ def mixed_decode(device, steps, layers=LAYERS):
     ms = time_steps(lambda: batch.run(sid), steps, max(20, steps), stream)
     step_bytes = batch.algorithmic_bytes
     gbs = step_bytes / (ms * 1e-3) / 1e9
-    # residual flushes: 128 appended fp16 tokens quantized into the packed prefix
-    # (in place: the packed storage has room after the first growth).  The GPU
-    # time is taken with the stream kept busy (a 0.1 ms spin) so the host-side
-    # work of the call overlaps, as it does behind a decode step; the host time
-    # of the call is reported beside it.
-    c = caches[0]
-    nk, nv = make_kv(128, seed=14000, device=device)
-    flush_ms, flush_host_us = [], []
-    for i in range(7):
-        c.append(nk.half(), nv.half(), logical_token_ids=torch.arange(vae + 128 * i, vae + 128 * (i + 1),
-                                                                      device=device))
-        torch.cuda.synchronize()
-        torch.cuda._sleep(200_000)
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record(stream)
-        h0 = time.perf_counter()
-        c.flush_residual(keep=RESIDUAL)
-        h1 = time.perf_counter()
-        t1.record(stream)
-        torch.cuda.synchronize()
-        flush_ms.append(t0.elapsed_time(t1))
-        flush_host_us.append((h1 - h0) * 1e6)
+    packed0, window0 = caches[1].quantized_tokens, caches[1].residual_tokens
+
+    # the 64-step loop; the append kernel is loaded by a throwaway one-layer
+    # batch first, and the reserve is taken outside the timed loop
+    loop_steps, flush_at, keep = 64, 160, 32
+    nk, nv = make_kv(loop_steps * layers, seed=14000, device=device)
+    new_k = nk.half().view(loop_steps, layers, 1, HKV, D)
+    new_v = nv.half().view(loop_steps, layers, 1, HKV, D)
+    new_ids = (torch.arange(loop_steps, device=device).view(loop_steps, 1, 1) + vae).expand(
+        loop_steps, layers, 1).contiguous()
+    spare = PackedKIVICache.from_dense(nk[:256].half(), nv[:256].half(),
+                                       logical_token_ids=torch.arange(256, device=device), token_type_id=3,
+                                       k_bits=BITS, v_bits=BITS, group_size=GROUP, residual_length=RESIDUAL,
+                                       backend="cuda")
+    warm = MixedDecodeBatch([[spare]], [queries[0]])
+    warm.append(new_k[0, :1], new_v[0, :1], new_ids[0, :1], stream=sid)
+    warm.run(sid)
+    batch.reserve(loop_steps)
+    settle(lambda: batch.run(sid), stream, settle_ms=50.0)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    h0 = time.perf_counter()
+    flushed = 0
+    for t in range(loop_steps):
+        batch.run(sid)
+        flushed += batch.append(new_k[t], new_v[t], new_ids[t], flush_at=flush_at, keep=keep, stream=sid)
+    h1 = time.perf_counter()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    loop_ms = t0.elapsed_time(t1)
+    # attention bytes read over the loop: every step reads each layer's packed
+    # prefix (384 B / token), window and dense tokens (2048 B / token), q and out
+    # (codes of K and V, then fp16 scale + minimum of K (per channel, over a
+    # group of tokens) and of V (per group of channels))
+    per_tok_packed = HKV * (2 * D * BITS // 8 + 2 * 2 * D * 2 // GROUP)
+    per_tok_dense = HKV * D * 2 * 2
+    loop_bytes, tq, tr = 0, packed0, window0
+    for t in range(loop_steps):
+        loop_bytes += layers * (tq * per_tok_packed + (tr + dense_tokens) * per_tok_dense + 2 * HQ * D * 2)
+        tr += 1
+        if tr >= flush_at:
+            moved = (tr - keep) // GROUP * GROUP
+            tq, tr = tq + moved, tr - moved
+    assert (tq, tr) == (caches[1].quantized_tokens, caches[1].residual_tokens)
+    assert flushed == layers * (tq - packed0)
     return {
-        "workload": f"config 4 decode step: {layers} layers x (VAE {vae} tokens: {caches[1].quantized_tokens} packed "
-                    f"2-bit + {caches[1].residual_tokens} fp16 residual | {dense_tokens} dense tokens: 128 protected "
+        "workload": f"config 4 decode step: {layers} layers x (VAE {vae} tokens: {packed0} packed "
+                    f"2-bit + {window0} fp16 residual | {dense_tokens} dense tokens: 128 protected "
                     "+ 819 + 1638 H2O-retained), batch 1, Lq=1, one uc_kivi_attn_decode_segments launch",
         "ms_per_step": round(ms, 5),
         "gbs": round(gbs, 1),
         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
         "bytes_per_step": step_bytes,
-        "flush_ms_per_layer": round(sorted(flush_ms)[3], 4),
-        "flush_host_us_per_layer": round(sorted(flush_host_us)[3], 1),
+        "loop_64": {
+            "workload": f"configs[4] decode loop: {loop_steps} steps x {layers} layers; per step the decode "
+                        "launch, then one token appended to every layer's window (one uc_kivi_residual_append "
+                        f"launch), a window reaching {flush_at} tokens flushed ({flush_at - keep} tokens packed "
+                        "in place), as the CPU row C4",
+            "gpu_ms_per_step": round(loop_ms / loop_steps, 5),
+            "host_us_per_step": round((h1 - h0) * 1e6 / loop_steps, 1),
+            "attention_gbs": round(loop_bytes / (loop_ms * 1e-3) / 1e9, 1),
+            "flushed_tokens_per_layer": tq - packed0,
+        },
     }
 
 

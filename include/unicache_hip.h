@@ -526,6 +526,37 @@ typedef struct uc_copy_span {
 int uc_copy_spans(const uc_copy_span *spans_host, int n, uc_stream_t stream);
 
 /*
+ * Streaming decode over a device item table (as built for
+ * uc_kivi_attn_decode_batch / _segments): for each entry, first move the
+ * item's residual window past a flush that the caller has just packed, then
+ * append n_tokens rows to it, all in place on the device:
+ *   1. a = advance: quantized_tokens += a, residual_key and residual_value move
+ *      a rows forward, residual_tokens -= a (the caller has packed those a
+ *      rows into the packed tensors, which must have room for them);
+ *   2. key[e] / value[e] (rows [n_tokens, heads_kv, head_dim] of `dtype`, entry
+ *      e's block of contiguous [n_entries, n_tokens, heads_kv, head_dim]
+ *      tensors) are written at residual rows residual_tokens.. and
+ *      residual_tokens += n_tokens; ids[e] (int64 [n_entries, n_tokens], may be
+ *      NULL) go to entries[e].ids[quantized_tokens + residual_tokens ..]
+ *      (entries[e].ids may be NULL).
+ * Residual rows are [Tr, heads_kv, head_dim] contiguous and 16-byte aligned
+ * and must have room behind them; entries name distinct items (at most 128).
+ * Decode launches enqueued later on the stream see the new lengths.  No
+ * reference counterpart: UniCache builds a packed segment once
+ * (physical.py:228-332); this is the decode loop's per-step append, so the
+ * host neither rebuilds nor copies the item table per step.
+ */
+typedef struct uc_append_entry {
+  int64_t item;      /* index into the item table */
+  int64_t advance;   /* tokens packed by a flush since the previous call (0: none) */
+  int64_t *ids;      /* device int64 logical-id buffer of the segment, or NULL */
+} uc_append_entry;
+
+int uc_kivi_residual_append(uc_kivi_item *items_device, const uc_append_entry *entries_host, int n_entries,
+                            const void *key, const void *value, const int64_t *ids, int64_t n_tokens,
+                            int64_t heads_kv, int64_t head_dim, int dtype, uc_stream_t stream);
+
+/*
  * Bytes of caller-provided workspace an operation needs.
  *   UC_OP_KIVI_AV:     (1, heads_q, query_len, head_dim, total_tokens)
  *                      = max(4 Hq Lq S (D + 2), Hq Lq >= 64 ? 2 Hq D ceil64(T) : 0),

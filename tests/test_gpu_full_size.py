@@ -146,11 +146,18 @@ def test_config4_segment_table_and_flush(device):
         assert_close(f32(batch.lses[0]), el, max_abs=1e-2, mean_abs=1e-3, what=f"{what} lse")
 
     check(vk.half(), vv.half(), "config 4")
+    # decode steps append through the batch: one launch per step extends the
+    # window and the device item table, no refresh and no host copy of the table
     nk, nv = make_kv(128, seed=14000, device=device)
+    nk, nv = nk.half(), nv.half()
     packed_before = cache.quantized_tokens
+    batch.reserve(128)
+    ids = torch.arange(20352, 20352 + 128, device=device).view(128, 1, 1)
     for t in range(128):
-        cache.append(nk[t:t + 1].half(), nv[t:t + 1].half(),
-                     logical_token_ids=torch.tensor([20352 + t], device=device), flush_at=256)
+        batch.append(nk[t:t + 1][None], nv[t:t + 1][None], ids[t], flush_at=256)
+        if t == 63:
+            assert cache.residual_tokens == 192 and cache.quantized_tokens == packed_before
+            check(torch.cat([vk.half(), nk[:64]]), torch.cat([vv.half(), nv[:64]]), "config 4 after 64 appends")
     assert cache.quantized_tokens == packed_before + 256 and cache.residual_tokens == 0
-    batch.refresh()
-    check(torch.cat([vk, nk]).half(), torch.cat([vv, nv]).half(), "config 4 after flush")
+    assert torch.equal(cache.logical_token_ids.cpu(), torch.arange(20352 + 128))
+    check(torch.cat([vk.half(), nk]), torch.cat([vv.half(), nv]), "config 4 after flush")

@@ -259,6 +259,47 @@ def test_repack_monotonic(device):
     assert cache.resident_bytes < cache.full_precision_bytes
 
 
+def test_repack_after_streaming_frees_the_streamed_storage(device):
+    # a flush grows the packed storage (owned by the cache) and appends keep a
+    # residual window buffer; repack_monotonic replaces both, so the memory
+    # they held is released, and streaming continues on the new packing
+    import gc
+
+    key, value = kv_pair(1600, seed=150)
+    kd, vd = key.to(device), value.to(device)
+    ids = torch.arange(1600)
+    cache = PackedKIVICache.from_dense(kd[:1000], vd[:1000], logical_token_ids=ids[:1000], token_type_id=3,
+                                       k_bits=4, v_bits=4, group_size=32, residual_length=128, backend="cuda")
+    for t in range(1000, 1300):
+        cache.append(kd[t:t + 1], vd[t:t + 1], logical_token_ids=ids[t:t + 1], flush_at=128)
+    owner, store = cache._store
+    assert owner == id(cache) and cache.packed_capacity >= cache.quantized_tokens
+    streamed = store[0].untyped_storage().nbytes() + cache._residual_capacity.untyped_storage().nbytes()
+    dk, dv = cache.dequantize(torch.bfloat16)  # what the repack re-packs
+    del owner, store
+    gc.collect()
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(device)
+    assert cache.repack_monotonic(bits=2, group_size=64)
+    gc.collect()
+    torch.cuda.synchronize()
+    after = torch.cuda.memory_allocated(device)
+    assert "_store" not in cache.__dict__ and "_residual_capacity" not in cache.__dict__
+    new = cache.key_code.untyped_storage().nbytes() + 2 * cache.residual_key.untyped_storage().nbytes()
+    assert after <= before - streamed + new + (1 << 16), (before, after, streamed, new)
+    # appends and flushes after the repack equal packing the same tokens at once
+    tail = torch.cat([dk, kd[1300:]]), torch.cat([dv, vd[1300:]])
+    for t in range(1300, 1600):
+        cache.append(kd[t:t + 1], vd[t:t + 1], logical_token_ids=ids[t:t + 1], flush_at=128)
+    ref = PackedKIVICache.from_dense(tail[0], tail[1], logical_token_ids=ids, token_type_id=3, k_bits=2, v_bits=2,
+                                     group_size=64, residual_length=1600 - cache.quantized_tokens, backend="cuda")
+    assert ref.quantized_tokens == cache.quantized_tokens
+    for name in ("key_code", "key_scale", "key_minimum", "value_code", "value_scale", "value_minimum",
+                 "residual_key", "residual_value"):
+        assert torch.equal(getattr(cache, name), getattr(ref, name)), name
+    assert torch.equal(cache.logical_token_ids.cpu(), ids)
+
+
 @pytest.mark.parametrize("bits,group,tokens,appended", [(2, 32, 1000, 300), (4, 64, 640, 200), (2, 128, 300, 170)])
 def test_streaming_append_flush_equals_from_dense(device, bits, group, tokens, appended):
     # decode appends one token per step and flushes the residual at 128 tokens;

@@ -455,3 +455,101 @@ def test_decode_batch_checks_pointers_and_staleness(device):
     assert seg.quantized_tokens == cache.quantized_tokens
     eo, _ = A.packed_summary(seg, f32(q), kv_dtype="fp32")
     assert_close(f32(batch.outputs[0]), eo, what="batch decode after flush")
+
+
+def _stream_layer(device, layer, tokens):
+    key, value = kv_pair(tokens, seed=300 + layer, dtype=torch.float16)
+    cache = PackedKIVICache.from_dense(key.to(device), value.to(device),
+                                       logical_token_ids=torch.arange(tokens, device=device), token_type_id=3,
+                                       k_bits=2, v_bits=2, group_size=32, residual_length=128, backend="cuda")
+    dk, dv = kv_pair(150 + 50 * layer, seed=320 + layer, dtype=torch.float16)
+    return key, value, cache, (dk.to(device), dv.to(device))
+
+
+def test_streaming_decode_appends_on_device(device):
+    # three layers of decode steps with one token appended per layer and step
+    # through MixedDecodeBatch.append (one launch, device-side lengths, a
+    # flush of 128 tokens whenever a window holds 160), against caches
+    # appended one by one with a table rebuilt every step: outputs bit for
+    # bit, the caches' tensors and ids equal, and the oracle at the end
+    from unicache_amd.storage.decode import MixedDecodeBatch
+
+    lengths = (1500, 2100, 900)
+    steps = 200
+    streamed, shadow, dense, raw = [], [], [], []
+    for layer, tokens in enumerate(lengths):
+        key, value, c, d = _stream_layer(device, layer, tokens)
+        streamed.append(c)
+        dense.append(d)
+        raw.append((key, value))
+        shadow.append(_stream_layer(device, layer, tokens)[2])
+    qs = [queries(1, seed=340 + i).to(device) for i in range(3)]
+    batch = MixedDecodeBatch([[c, d] for c, d in zip(streamed, dense)], qs)
+    batch.reserve(steps)
+    g = torch.Generator().manual_seed(7)
+    new_k = torch.randn(steps, 3, 1, 4, 128, generator=g).half().to(device)
+    new_v = torch.randn(steps, 3, 1, 4, 128, generator=g).half().to(device)
+    new_ids = (torch.arange(steps).view(steps, 1, 1) + torch.tensor(lengths).view(1, 3, 1) + 10000).to(device)
+    for t in range(steps):
+        batch.append(new_k[t], new_v[t], new_ids[t], flush_at=160, keep=32)
+        for i, c in enumerate(shadow):
+            c.append(new_k[t, i], new_v[t, i], logical_token_ids=new_ids[t, i])
+            if c.residual_tokens >= 160:
+                c.flush_residual(keep=32)
+        if t in (0, 31, 32, 33, 120, steps - 1):
+            ref = MixedDecodeBatch([[c, d] for c, d in zip(shadow, dense)], qs)
+            batch.run()
+            ref.run()
+            for i in range(3):
+                assert torch.equal(batch.outputs[i], ref.outputs[i]), (t, i)
+                assert torch.equal(batch.lses[i], ref.lses[i]), (t, i)
+    for c, s in zip(streamed, shadow):
+        assert (c.quantized_tokens, c.residual_tokens) == (s.quantized_tokens, s.residual_tokens)
+        for name in ("key_code", "key_scale", "key_minimum", "value_code", "value_scale", "value_minimum",
+                     "residual_key", "residual_value", "logical_token_ids"):
+            assert torch.equal(getattr(c, name), getattr(s, name)), name
+    # the oracle over all the tokens of layer 2
+    key = np.concatenate([f32(raw[2][0]), f32(new_k[:, 2, 0])])
+    value = np.concatenate([f32(raw[2][1]), f32(new_v[:, 2, 0])])
+    seg = K.from_dense(key, value, k_bits=2, v_bits=2, group_size=32,
+                       residual_length=key.shape[0] - streamed[2].quantized_tokens, in_dtype="fp16")
+    assert seg.quantized_tokens == streamed[2].quantized_tokens
+    pk, pv = K.dequantize(seg, "fp32")
+    eo, el = A.attention_summary(f32(qs[2]), np.concatenate([pk, f32(dense[2][0])]),
+                                 np.concatenate([pv, f32(dense[2][1])]))
+    assert_close(f32(batch.outputs[2]), eo, what="streamed layer 2 out")
+    assert_close(f32(batch.lses[2]), el, max_abs=1e-2, mean_abs=1e-3, what="streamed layer 2 lse")
+
+
+def test_streaming_decode_guards(device):
+    # a cache changed behind the batch's back stops it until refresh(); a
+    # second batch streaming into the same cache makes the first one stale;
+    # the reserve grows by itself when used up
+    from unicache_amd.storage.decode import MixedDecodeBatch
+
+    _, _, cache, dense = _stream_layer(device, 0, 700)
+    q = queries(1, seed=350).to(device)
+    batch = MixedDecodeBatch([[cache, dense]], [q])
+    tr0 = cache.residual_tokens  # 156: 544 of the 700 tokens are packed
+    kv = torch.zeros(1, 1, 4, 128, dtype=torch.float16, device=device)
+    ids = torch.tensor([[5000]], device=device)
+    batch.append(kv, kv, ids)  # reserves on first use
+    assert cache.residual_tokens == tr0 + 1 and cache.token_count == 701
+    cache.append(kv[0], kv[0], logical_token_ids=ids[0])
+    with pytest.raises(RuntimeError, match="refresh"):
+        batch.append(kv, kv, ids)
+    batch.refresh()
+    batch.append(kv, kv, ids)
+    assert cache.residual_tokens == tr0 + 3
+    other = MixedDecodeBatch([[cache, dense]], [q])
+    other.reserve(8)
+    with pytest.raises(RuntimeError, match="refresh"):
+        batch.run()
+    room = other._room
+    for _ in range(room + 3):
+        other.append(kv, kv, ids)
+    assert cache.residual_tokens == tr0 + 3 + room + 3
+    with pytest.raises(ValueError):
+        other.append(kv[:, :, :2], kv[:, :, :2], ids)
+    with pytest.raises(ValueError):
+        other.append(kv.float(), kv.float(), ids)

@@ -59,6 +59,12 @@ class DenseSegment(ctypes.Structure):
     ]
 
 
+class AppendEntry(ctypes.Structure):
+    """Mirror of ``uc_append_entry``."""
+
+    _fields_ = [("item", _L), ("advance", _L), ("ids", _P)]
+
+
 class MqQuery(ctypes.Structure):
     """Mirror of ``uc_mq_query``."""
 
@@ -149,6 +155,7 @@ _SIGNATURES = {
     "uc_compact_rows": (_I, [_P, _L, _L, _P, _L, _P, _P]),
     "uc_scatter_rows": (_I, [_P, _L, _P, _L, _P, _L, _P]),
     "uc_copy_spans": (_I, [_P, _I, _P]),
+    "uc_kivi_residual_append": (_I, [_P, _P, _I, _P, _P, _P, _L, _L, _L, _I, _P]),
     "uc_h2o_select_gather": (
         _I,
         [_P, _P, _L, _L, _L, _I, _L, _L, _L, _P, _L, _L, _L, _L, _P, _L, _L, _P, _P, _P, _P, _P, _P],

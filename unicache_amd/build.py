@@ -28,6 +28,7 @@ SOURCES = [
     "uc_h2o.hip",
     "uc_h2o_mfma.hip",
     "uc_compact.hip",
+    "uc_stream.hip",
 ]
 
 # -ffp-contract=off keeps the pack/dequant arithmetic bit-exact (no implicit

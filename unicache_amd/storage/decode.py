@@ -168,7 +168,14 @@ class MixedDecodeBatch:
 
     Dense segments and residual windows must share one dtype (the kernel reads
     them as fp16 either way).  refresh() rebuilds the item table after
-    segments change (a residual append or flush); run() allocates nothing."""
+    segments change (a residual append or flush); run() allocates nothing.
+
+    Streaming decode: reserve(tokens) gives every packed segment room for that
+    many appended tokens; append() then adds a decode step's tokens to every
+    packed segment's residual window with one launch that also updates the
+    device item table (uc_kivi_residual_append), and flushes windows that
+    reach `flush_at` into the packed prefix in place -- no refresh, no host
+    copy of the table, no allocation until the reserve is used up."""
 
     def __init__(self, groups, queries, *, out_dtype: torch.dtype | None = None):
         if not groups or len(groups) != len(queries):
@@ -215,6 +222,7 @@ class MixedDecodeBatch:
         self.lses = [torch.empty((hq, lq), dtype=torch.float32, device=self.device) for _ in groups]
         self.shape = (lq, hq, d)
         self.sm_scale = 1.0 / math.sqrt(d)
+        self._room = 0  # tokens every packed segment can still take without allocating
         self.refresh()
 
     def refresh(self) -> None:
@@ -232,6 +240,7 @@ class MixedDecodeBatch:
                 else:
                     tensors += _check_cache(s, self.device, "Mixed KIVI decode")
                     caches.append(s)
+        streams = self._attach_streams(caches) if self._room > 0 else {}
         n = len(self.groups) * self.segs
         items = (nat.KiviItem * n)()
         max_tq = max_tr = 0
@@ -252,20 +261,142 @@ class MixedDecodeBatch:
                     max_tr = max(max_tr, tr)
                 else:
                     tr = s.residual_tokens
+                    st = streams.get(id(s))
+                    rk = s.residual_key.data_ptr() if tr else None
+                    rv = s.residual_value.data_ptr() if tr else None
+                    if st is not None:
+                        # a streamed window is addressed even while empty
+                        # (appends write there); an empty view has no address
+                        buf, row = st[2].buf, s.num_kv_heads * s.head_dim * st[2].buf.element_size()
+                        rk = buf.data_ptr() + st[2].off * row
+                        rv = buf.data_ptr() + (int(buf.shape[1]) + st[2].off) * row
+                        st[1].item = idx
                     items[idx] = s.native_item(q.data_ptr(), out.data_ptr(), lse.data_ptr(),
-                                               residual_key_ptr=s.residual_key.data_ptr() if tr else None,
-                                               residual_value_ptr=s.residual_value.data_ptr() if tr else None,
-                                               residual_tokens=tr)
+                                               residual_key_ptr=rk, residual_value_ptr=rv, residual_tokens=tr)
                     max_tq, max_tr = max(max_tq, s.quantized_tokens), max(max_tr, tr)
         raw = bytes(ctypes.string_at(ctypes.addressof(items), ctypes.sizeof(items)))
         self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
         self.n_items, self.max_tq, self.max_tr = n, max_tq, max_tr
         lq, hq, d = self.shape
+        # sized for the longest window the reserve allows, so appends keep it
         self.ws_bytes = nat.decode_workspace_bytes(n, self.bits, self.group_size, hq, self.kv_heads, d, lq,
-                                                   max_tq, max_tr)
+                                                   max_tq + self._room, max_tr + self._room)
         if getattr(self, "workspace", None) is None or self.workspace.numel() < self.ws_bytes:
             self.workspace = nat.workspace(self.device, self.ws_bytes)
+        self._streams = [streams[id(c)] for c in caches if id(c) in streams]
+        if self._streams:
+            self._entries = (nat.AppendEntry * len(self._streams))(*(e for _, e, _ in self._streams))
+            # the dense segments' lengths are fixed; the windows' longest grows with appends
+            self._dense_max_tr = max((int(s[0].shape[0]) for g in self.groups for s in g if isinstance(s, tuple)),
+                                     default=0)
+            self._stream_max_tr = max(st.tr for _, _, st in self._streams)
         self._guard = _TableGuard(caches, tensors)
+
+    # ------------------------------------------------------------ streaming --
+    def _attach_streams(self, caches) -> dict:
+        """Streaming state of every packed segment: {id(cache): (cache, append
+        entry, _StreamState)}; the item index is filled in by refresh()."""
+
+        from .physical import _StreamState
+
+        streams = {}
+        for c in caches:
+            if id(c) in streams:
+                raise ValueError("Streaming decode needs each packed segment in one group only")
+            buf, off = c._residual_slot()
+            ids = c.__dict__.get("_ids_capacity")
+            if buf is None or ids is None or c.logical_token_ids.data_ptr() != ids.data_ptr():
+                raise RuntimeError("Streaming decode: reserve() the packed segments first")
+            old = c.__dict__.get("_stream")
+            if old is not None and old is not getattr(self, "_owned_states", {}).get(id(c)):
+                c._mutated()  # another batch streamed into this cache: its table is now stale
+            state = _StreamState(buf, ids, off, c.residual_tokens, c.quantized_tokens)
+            c.__dict__["_stream"] = state
+            streams[id(c)] = (c, nat.AppendEntry(0, 0, ids.data_ptr()), state)
+        self._owned_states = {k: v[2] for k, v in streams.items()}
+        return streams
+
+    def reserve(self, tokens: int) -> None:
+        """Room for `tokens` more tokens appended to every packed segment (and
+        for flushing them) without allocation; rebuilds the item table."""
+
+        caches = [s for g in self.groups for s in g if not isinstance(s, tuple)]
+        for c in caches:
+            c.reserve(int(tokens))
+            if c.logical_token_ids.device != self.device:
+                raise RuntimeError("Streaming decode keeps the logical ids on the GPU")
+        self._room = int(tokens)
+        self.refresh()
+
+    def append(self, keys: torch.Tensor, values: torch.Tensor, logical_token_ids: torch.Tensor, *,
+               flush_at: int | None = None, keep: int = 0, stream: int | None = None) -> int:
+        """Append n tokens to the residual window of every packed segment, in
+        one launch: keys / values [S, n, Hkv, D] contiguous in the windows'
+        dtype and logical_token_ids int64 [S, n], all on the batch's GPU, S =
+        the packed segments in group order.  Segments whose window then holds
+        at least `flush_at` tokens are flushed (all but `keep` of the window,
+        in whole groups) into their packed prefix.  Returns the tokens packed,
+        summed over the segments.  The segments' residual_key / residual_value
+        / logical_token_ids views follow on their next read."""
+
+        self._guard.check("MixedDecodeBatch.append")
+        streams = self._streams if self._room > 0 else []
+        n = int(keys.shape[1]) if keys.dim() == 4 else -1
+        if not streams or n > self._room:
+            self.reserve(max(n, 2 * self._room, 256))
+            streams = self._streams
+        if (keys.shape != values.shape or keys.dim() != 4 or int(keys.shape[0]) != len(streams)
+                or tuple(keys.shape[2:]) != (self.kv_heads, self.shape[2])):
+            raise ValueError("Streaming decode expects keys / values [packed segments, n, kv_heads, head_dim]")
+        if keys.dtype != self.res_dtype or values.dtype != self.res_dtype:
+            raise ValueError("Streaming decode: appended tokens must be in the residual dtype")
+        if tuple(logical_token_ids.shape) != tuple(keys.shape[:2]) or logical_token_ids.dtype != torch.int64:
+            raise ValueError("Streaming decode: logical_token_ids must be int64 [packed segments, n]")
+        for t, what in ((keys, "keys"), (values, "values"), (logical_token_ids, "logical_token_ids")):
+            if t.device != self.device or not t.is_contiguous():
+                raise ValueError(f"Streaming decode: {what} must be contiguous on {self.device}")
+        sid = nat.stream(self.device) if stream is None else stream
+        nat.call("uc_kivi_residual_append", self.table.data_ptr(), ctypes.addressof(self._entries), len(streams),
+                 keys.data_ptr(), values.data_ptr(), logical_token_ids.data_ptr(), n, self.kv_heads,
+                 self.shape[2], nat.dtype_code(self.res_dtype), sid)
+        for _, _, st in streams:
+            st.tr += n
+            st.dirty = True
+        self._room -= n
+        self._stream_max_tr += n
+        self.max_tr = max(self._dense_max_tr, self._stream_max_tr)
+        if flush_at is None or self._stream_max_tr < int(flush_at):
+            return 0
+        return self._flush(int(flush_at), int(keep), sid)
+
+    def _flush(self, flush_at: int, keep: int, sid: int) -> int:
+        """Flush every window holding >= flush_at tokens (the packing kernels
+        write into the reserved packed storage in place), then move the
+        device items past the packed rows with one launch."""
+
+        moved = []
+        for c, entry, st in self._streams:
+            if st.tr < flush_at:
+                continue
+            count = c.flush_residual(keep)  # reads the pulled views; packs in place
+            if count:
+                st.tq += count
+                st.tr -= count
+                st.off += count
+                moved.append((c, entry, count))
+        if not moved:
+            return 0
+        adv = (nat.AppendEntry * len(moved))(*(nat.AppendEntry(e.item, count, None) for _, e, count in moved))
+        nat.call("uc_kivi_residual_append", self.table.data_ptr(), ctypes.addressof(adv), len(moved), None, None,
+                 None, 0, self.kv_heads, self.shape[2], nat.dtype_code(self.res_dtype), sid)
+        guard = self._guard
+        slot = {id(c): i for i, c in enumerate(guard.caches)}
+        for c, _, _ in moved:  # the flushes changed these caches on purpose
+            guard.counts[slot[id(c)]] = c.mutation_count
+        self.max_tq = max(max(st.tq for _, _, st in self._streams), self.max_tq)
+        self._stream_max_tr = max(st.tr for _, _, st in self._streams)
+        self.max_tr = max(self._dense_max_tr, self._stream_max_tr)
+        return sum(count for _, _, count in moved)
 
     @property
     def algorithmic_bytes(self) -> int:

@@ -426,7 +426,13 @@ def packed_table_summaries(entries: list, *, dense_dtype: torch.dtype) -> None:
     hq, d = int(q0.shape[1]), int(q0.shape[2])
     first = next((c for e in entries for c in e[3]), None)
     bits, group = (first.k_bits, first.group_size) if first is not None else (2, 32)
-    hkv = first.num_kv_heads if first is not None else int(entries[0][4][0][0].shape[1])
+    if first is not None:
+        hkv = first.num_kv_heads
+    else:
+        part = next((k for e in entries for k, _ in e[4] if k.dim() == 3), None)
+        if part is None:
+            raise ValueError("Table attention needs a packed cache or a dense [tokens, kv_heads, head_dim] part")
+        hkv = int(part.shape[1])
     tensors = []
     for query, out, lse, caches, dense in entries:
         if query.dtype != q0.dtype or out.dtype != q0.dtype or tuple(query.shape[1:]) != (hq, d) or \
@@ -437,6 +443,11 @@ def packed_table_summaries(entries: list, *, dense_dtype: torch.dtype) -> None:
             raise ValueError("Table attention: lse must be contiguous fp32 [Hq, Lq]")
         if caches and not packed_segments_supported(caches, query, dense):
             raise ValueError("Table attention: unsupported packed layout or query length")
+        if not caches and (d != 128 or query.dtype not in (torch.bfloat16, torch.float16)
+                           or any(k.dtype not in (torch.bfloat16, torch.float16) for k, _ in dense)):
+            # the dtype and head_dim checks packed_segments_supported makes for
+            # entries with caches (the kernel takes any query length)
+            raise ValueError("Table attention: dense-only entries need 16-bit queries and parts, head_dim 128")
         for cache in caches:
             if (cache.k_bits, cache.v_bits, cache.group_size, cache.num_kv_heads) != (bits, bits, group, hkv):
                 raise ValueError("Table attention needs equal bits, group size and KV heads")

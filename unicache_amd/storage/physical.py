@@ -478,15 +478,31 @@ class PackedKIVICache:
 
         if not self.quantized_tokens:
             return None
+        store = self._owned_store()
+        if store is not None:
+            return store
         views = (self.key_code, self.key_scale, self.key_minimum, self.value_code, self.value_scale,
                  self.value_minimum)
-        store = getattr(self, "_store", None)
-        if (store is not None and all(v.data_ptr() == t.data_ptr() for v, t in zip(views, store))
+        cap = self.native_packed_pointers(device)[-1]
+        return _native_storage_of(views, cap, self.k_bits, self.group_size)
+
+    def _owned_store(self) -> tuple[torch.Tensor, ...] | None:
+        """The token-major storage this cache allocated itself (a flush that
+        outgrew the previous one), while the packed tensors are still views of
+        it; None otherwise.  Only owned storage is written in place: storage
+        reached through tensors the cache was given, or shared with a copy of
+        this object, may back another cache's tokens."""
+
+        owner, store = self.__dict__.get("_store", (None, None))
+        if store is None or owner != id(self) or not self.quantized_tokens:
+            return None
+        views = (self.key_code, self.key_scale, self.key_minimum, self.value_code, self.value_scale,
+                 self.value_minimum)
+        if (all(v.data_ptr() == t.data_ptr() for v, t in zip(views, store))
                 and int(self.key_code.shape[2]) == self.quantized_tokens * self.k_bits // 32
                 and int(self.value_code.shape[1]) == self.quantized_tokens):
             return store
-        cap = self.native_packed_pointers(device)[-1]
-        return _native_storage_of(views, cap, self.k_bits, self.group_size)
+        return None
 
     def _residual_slot(self) -> tuple[torch.Tensor | None, int]:
         """(buffer, first row) of the residual inside this cache's [2, size,
@@ -688,6 +704,10 @@ class PackedKIVICache:
             backend=self.backend,
         )
         shortfalls, mutations = self.budget_shortfall_events, self.mutation_count
+        # drop the streaming buffers of the old packing (grown packed storage,
+        # residual window) so the repack frees them
+        for name in ("_store", "_residual_capacity", "_ids_capacity", "_stream"):
+            self.__dict__.pop(name, None)
         self.__dict__.update(replacement.__dict__)
         self.budget_shortfall_events = shortfalls
         self._mutations = mutations + 1
@@ -736,11 +756,79 @@ class PackedKIVICache:
         buf[0, off + tr:off + tr + n].copy_(key)
         buf[1, off + tr:off + tr + n].copy_(value)
         self._set_residual(buf, off, tr + n)
-        self.logical_token_ids = torch.cat([self.logical_token_ids, logical_token_ids.to(self.logical_token_ids)])
+        self._append_ids(logical_token_ids, n)
         self._mutated()
         if flush_at is not None and self.residual_tokens >= int(flush_at):
             return self.flush_residual()
         return 0
+
+    def reserve(self, tokens: int) -> None:
+        """Room for `tokens` more appended tokens, and for flushing all of
+        them into the packed prefix, with no further allocation: packed
+        storage owned by this cache with capacity for them, a residual-window
+        buffer with that many free rows behind the window, and logical-id
+        capacity on the cache's device.  Tensors move (and mutation_count
+        rises) only where room is missing.  Streaming caches only: native equal
+        2- or 4-bit K/V (backend='cuda')."""
+
+        tokens = int(tokens)
+        if tokens <= 0:
+            return
+        if self.k_bits != self.v_bits or self.k_bits not in (2, 4) or self.backend != "cuda" or (
+                self.quantized_tokens and not self.kernel_native_layout):
+            raise ValueError("KIVI reserve needs a native equal 2- or 4-bit cache (backend='cuda')")
+        device = nat.require_device(self.residual_key, self.residual_value, what="KIVI reserve")
+        heads, d, g, bits = self.num_kv_heads, self.head_dim, self.group_size, self.k_bits
+        tq, tr = self.quantized_tokens, self.residual_tokens
+        moved = False
+        need = -(-(tq + tr + tokens) // g) * g
+        owned = self._owned_store()
+        if owned is None or int(owned[3].shape[1]) < need:
+            old = self._native_store(device)
+            grown = _native_storage(need, heads, d, bits, bits, g, device)
+            if tq:
+                for dst, src in zip(_native_views(grown, tq, bits, g), _native_views(old, tq, bits, g)):
+                    dst.copy_(src)
+                (self.key_code, self.key_scale, self.key_minimum,
+                 self.value_code, self.value_scale, self.value_minimum) = _native_views(grown, tq, bits, g)
+            self._store = (id(self), grown)
+            moved = True
+        buf, off = self._residual_slot()
+        if buf is None or int(buf.shape[1]) - off < tr + tokens:
+            new = torch.empty((2, max(tr + tokens, 256), heads, d), dtype=self.residual_key.dtype, device=device)
+            if tr:
+                new[0, :tr].copy_(self.residual_key)
+                new[1, :tr].copy_(self.residual_value)
+            self._residual_capacity = new
+            self._set_residual(new, 0, tr)
+            moved = True
+        cur = self.logical_token_ids
+        ids = self.__dict__.get("_ids_capacity")
+        total = int(cur.numel())
+        if (ids is None or ids.device != device or int(ids.numel()) < total + tokens or ids.dtype != cur.dtype
+                or cur.device != device or cur.data_ptr() != ids.data_ptr() or not cur.is_contiguous()):
+            ids = torch.empty(total + tokens, dtype=cur.dtype, device=device)
+            ids[:total].copy_(cur)
+            self._ids_capacity = ids
+            self.logical_token_ids = ids[:total]
+            moved = True
+        if moved:
+            self._mutated()
+
+    def _append_ids(self, ids: torch.Tensor, n: int) -> None:
+        """Append n logical ids: they go after the current ones in a capacity
+        buffer that grows geometrically, so an append copies only its own ids."""
+
+        cur = self.logical_token_ids
+        total = int(cur.numel())
+        buf = self.__dict__.get("_ids_capacity")
+        if (buf is None or buf.dtype != cur.dtype or buf.device != cur.device or int(buf.numel()) < total + n
+                or cur.data_ptr() != buf.data_ptr() or not cur.is_contiguous()):
+            new = torch.empty(max(2 * (total + n), 1024), dtype=cur.dtype, device=cur.device)
+            new[:total].copy_(cur)
+            buf = self._ids_capacity = new
+        buf[total:total + n].copy_(ids.reshape(-1))
+        self.logical_token_ids = buf[:total + n]
 
     def flush_residual(self, keep: int = 0) -> int:
         """Quantize the residual except its last `keep` tokens (rounded so the
@@ -762,7 +850,8 @@ class PackedKIVICache:
         tq, bits, g = self.quantized_tokens, self.k_bits, self.group_size
         store = self._native_store(device)
         cap = int(store[3].shape[1]) if store is not None else 0
-        if tq + count > cap:
+        # in place only into storage this cache allocated (see _owned_store)
+        if tq + count > cap or self._owned_store() is None:
             # grow geometrically so a run of flushes copies the prefix O(log n) times
             cap = -(-max(tq + count, cap + cap // 2) // g) * g
             grown = _native_storage(cap, self.num_kv_heads, self.head_dim, bits, bits, g, device)
@@ -774,7 +863,7 @@ class PackedKIVICache:
                           tokens=count, stream=stream)
         (self.key_code, self.key_scale, self.key_minimum,
          self.value_code, self.value_scale, self.value_minimum) = _native_views(store, tq + count, bits, g)
-        self._store = store
+        self._store = (id(self), store)
         self.quantized_tokens = tq + count
         self.kernel_native_layout = True
         buf, off = self._residual_slot()
@@ -804,6 +893,49 @@ class PackedKIVICache:
             return gqa_probability_value(probabilities, value)
 
         return logits, apply_value
+
+
+# A packed cache that a MixedDecodeBatch streams into (MixedDecodeBatch.append)
+# has its residual window and logical ids extended on the device; the batch
+# records the new lengths in the cache's _StreamState, and the cache's
+# residual_key / residual_value / logical_token_ids views are rebuilt from it
+# on their next read.  Every reader -- the cache's own methods and outside
+# code alike -- therefore sees the appended tokens.
+class _StreamState:
+    __slots__ = ("buf", "ids", "off", "tr", "tq", "dirty")
+
+    def __init__(self, buf: torch.Tensor, ids: torch.Tensor, off: int, tr: int, tq: int) -> None:
+        self.buf, self.ids, self.off, self.tr, self.tq, self.dirty = buf, ids, off, tr, tq, False
+
+    def pull(self, cache: "PackedKIVICache") -> None:
+        d = cache.__dict__
+        heads, hd = cache.num_kv_heads, cache.head_dim
+        shape, stride = (self.tr, heads, hd), (heads * hd, hd, 1)
+        base = self.buf.storage_offset() + self.off * heads * hd
+        d["_residual_key"] = self.buf.as_strided(shape, stride, base)
+        d["_residual_value"] = self.buf.as_strided(shape, stride, base + int(self.buf.shape[1]) * heads * hd)
+        d["_logical_token_ids"] = self.ids[:self.tq + self.tr]
+        self.dirty = False
+
+
+def _streamed_field(name: str) -> property:
+    slot = "_" + name
+
+    def get(self):
+        d = self.__dict__
+        state = d.get("_stream")
+        if state is not None and state.dirty:
+            state.pull(self)
+        return d[slot]
+
+    def set(self, value):
+        self.__dict__[slot] = value
+
+    return property(get, set, doc=f"PackedKIVICache.{name} (current after device-side appends)")
+
+
+for _name in ("residual_key", "residual_value", "logical_token_ids"):
+    setattr(PackedKIVICache, _name, _streamed_field(_name))
 
 
 # ------------------------------------------------------------------- H2O --
