@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define UC_ABI_VERSION 2
+#define UC_ABI_VERSION 3
 
 /* element type codes */
 #define UC_BF16 0
@@ -194,6 +194,13 @@ typedef struct uc_kivi_item {
   int64_t quantized_tokens;  /* Tq, a multiple of group_size */
   int64_t residual_tokens;   /* Tr */
   int64_t packed_capacity;   /* C: tokens between the heads of the packed tensors; 0 means Tq */
+  /* residual element (t, h, d) at residual_key + t * residual_token_stride +
+   * h * residual_head_stride + d (elements, multiples of 8); 0 and 0 mean
+   * token-major rows [Tr, Hkv, D] (token stride Hkv * D, head stride D).  A
+   * head-major [Hkv, Tr, D] segment (a GQA H2O cache) has token stride D and
+   * head stride Tr * D.  uc_kivi_residual_append needs token-major rows. */
+  int64_t residual_token_stride;
+  int64_t residual_head_stride;
 } uc_kivi_item;
 
 /*
@@ -249,6 +256,22 @@ int uc_kivi_attn_decode_batch(const uc_kivi_item *items_device, int64_t n_items,
                               int q_dtype, int res_dtype, int out_dtype, float sm_scale,
                               int64_t max_quantized_tokens, int64_t max_residual_tokens,
                               void *workspace, int64_t workspace_bytes, uc_stream_t stream);
+
+/*
+ * uc_kivi_attn_decode_segments for ONE query over n_items (1..8) segments
+ * given in host memory: the items travel in the kernel arguments, so a call
+ * copies nothing to the device (a decode step of one layer).  The group's
+ * result goes to the first item's out / lse.  Workspace:
+ * uc_kivi_decode_workspace_bytes(n_items, ...).  Items may give residual
+ * strides (a head-major H2O segment as a dense item with quantized_tokens 0).
+ * Replaces: _run_fused_mixed_attention's per-segment summaries and merge for
+ * decode-length queries (adapters/bagel.py:1598-1858), without concatenating
+ * the bf16 parts.
+ */
+int uc_kivi_attn_decode_segments_host(const uc_kivi_item *items_host, int64_t n_items, int bits, int group_size,
+                                      int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t query_len,
+                                      int q_dtype, int res_dtype, int out_dtype, float sm_scale,
+                                      void *workspace, int64_t workspace_bytes, uc_stream_t stream);
 
 /*
  * Segment table: the n_items items form n_items / segments_per_query groups

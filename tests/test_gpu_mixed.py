@@ -92,6 +92,34 @@ def test_mixed_attention_matches_global_softmax(device, lq, second_packed):
     assert h2o[1].retained_tokens == 40
 
 
+@pytest.mark.parametrize("lq", [1, 2])
+def test_decode_length_mixed_attention_reads_segments_in_place(device, lq):
+    # decode-length queries go to the split-K decode kernels over the segments
+    # where they lie: the dense KV, both H2O segments through their [Hkv, R, D]
+    # strides, two packed prefixes with their residuals -- no concatenation
+    from unittest import mock
+
+    from unicache_amd.storage.kivi_cuda import decode_segments_summary
+
+    dense, h2o, packed, segs = _segments(device, second_packed="same")
+    for s in h2o:
+        s.selection_frozen = True
+    q = queries(lq, seed=60 + lq)
+    ek, ev = _oracle_keys(dense, h2o, segs)
+    eo, el = A.attention_summary(f32(q), ek, ev)
+    dk, dv, qd = dense[0].to(device), dense[1].to(device), q.to(device)
+    with mock.patch("torch.cat", side_effect=AssertionError("concatenated")):
+        out, lse = run_fused_mixed_attention(qd, dk, dv, [*h2o, *packed], return_lse=True)
+    assert_close(f32(out), eo, what=f"decode mixed out Lq {lq}")
+    assert_close(f32(lse), el, max_abs=1e-2, mean_abs=1e-3, what=f"decode mixed lse Lq {lq}")
+    # the same call through the function itself, with a head-major part
+    parts = [(dk, dv)] + [(s.key.transpose(0, 1), s.value.transpose(0, 1)) for s in h2o]
+    o2, l2 = decode_segments_summary(packed, qd, parts)
+    assert torch.equal(o2, out) and torch.equal(l2, lse)
+    with pytest.raises(ValueError):
+        decode_segments_summary(packed, qd, parts + [(dk.float(), dv.float())])
+
+
 def test_mixed_attention_requires_packed(device):
     dk, dv = kv_pair(16, seed=1)
     with pytest.raises(RuntimeError):

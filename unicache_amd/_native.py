@@ -14,7 +14,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libunicache_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 UC_BF16, UC_FP16, UC_FP32 = 0, 1, 2
 UC_OK, UC_EINVAL, UC_ERUNTIME = 0, -1, -2
@@ -44,6 +44,8 @@ class KiviItem(ctypes.Structure):
         ("quantized_tokens", _L),
         ("residual_tokens", _L),
         ("packed_capacity", _L),
+        ("residual_token_stride", _L),
+        ("residual_head_stride", _L),
     ]
 
 
@@ -118,6 +120,10 @@ _SIGNATURES = {
     "uc_kivi_attn_decode_batch": (
         _I,
         [_P, _L, _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _L, _L, _P, _L, _P],
+    ),
+    "uc_kivi_attn_decode_segments_host": (
+        _I,
+        [ctypes.POINTER(KiviItem), _L, _I, _I, _L, _L, _L, _L, _I, _I, _I, _F, _P, _L, _P],
     ),
     "uc_kivi_attn_decode_segments": (
         _I,

@@ -60,7 +60,9 @@ def run_fused_mixed_attention(
     (packed_segments_summary): every packed prefix is dequantized inside the
     attention kernel and every bf16 part -- the dense KV, the H2O segments
     (read through their [Hkv, T, D] strides) and the residuals -- is read
-    where it lies, in one softmax.  Otherwise the bf16 keys are gathered in
+    where it lies, in one softmax.  Decode-length queries take the split-K
+    decode kernels over the same segments, read in place
+    (decode_segments_summary).  Otherwise the bf16 keys are gathered in
     UniCache's order [dense, H2O..., residuals...] and attended in the same
     fused pass as the first packed segment's prefix; further packed prefixes
     get their own pass (all passes in one batched launch for long queries) and
@@ -69,9 +71,9 @@ def run_fused_mixed_attention(
     budget.  Returns the output (and the global LSE [Hq, Lq] with
     return_lse=True)."""
 
-    from ..storage.kivi_cuda import (_max_decode_query_len, packed_batch_with_dense,
-                                     packed_kivi_quantized_attention_summary, packed_segments_summary,
-                                     packed_segments_supported, packed_summary_with_dense)
+    from ..storage.kivi_cuda import (_max_decode_query_len, decode_segments_summary, decode_segments_supported,
+                                     packed_batch_with_dense, packed_kivi_quantized_attention_summary,
+                                     packed_segments_summary, packed_segments_supported, packed_summary_with_dense)
     from ..storage.physical import GQAH2OCache, PackedKIVICache
 
     h2o = [s for s in physical_segments if isinstance(s, GQAH2OCache)]
@@ -86,6 +88,8 @@ def run_fused_mixed_attention(
     if dense_key.dtype in (torch.bfloat16, torch.float16) and packed_segments_supported(with_prefix, query,
                                                                                       dense_parts):
         output, global_lse = packed_segments_summary(with_prefix, query, dense_parts, dense_dtype=dense_key.dtype)
+    elif decode_segments_supported(with_prefix, query, dense_parts):
+        output, global_lse = decode_segments_summary(with_prefix, query, dense_parts)
     else:
         keys = [dense_key] + [s.key.transpose(0, 1) for s in h2o] + [
             s.residual_key for s in packed if s.residual_tokens]

@@ -1062,7 +1062,9 @@ struct TableBuilder {
     UC_REQUIRE(it.residual_tokens >= 0, "attn_mq: negative residual token count");
     int rc = add_packed(it);
     if (rc != UC_OK) return rc;
-    return add_dense(it.residual_key, it.residual_value, it.residual_tokens, heads_kv * mf::kD * 2, mf::kD * 2);
+    int64_t ts, hs;
+    residual_strides(it, heads_kv, mf::kD, ts, hs);
+    return add_dense(it.residual_key, it.residual_value, it.residual_tokens, ts * 2, hs * 2);
   }
 
   int end_query() {

@@ -43,6 +43,19 @@ int check_launch(const char *what);
 
 inline hipStream_t as_stream(uc_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Residual row strides of an item, in elements (token, KV head): both fields
+// 0 mean token-major rows [Tr, Hkv, D].
+__host__ __device__ inline void residual_strides(const uc_kivi_item &it, int64_t hkv, int64_t d, int64_t &ts,
+                                                 int64_t &hs) {
+  if (it.residual_token_stride == 0 && it.residual_head_stride == 0) {
+    ts = hkv * d;
+    hs = d;
+  } else {
+    ts = it.residual_token_stride;
+    hs = it.residual_head_stride;
+  }
+}
+
 // Division of n < 2^31 by a launch constant d >= 1 without a divide sequence:
 // with l = ceil(log2 d) and m = floor(2^(31+l) / d) + 1 (< 2^32),
 // floor(n / d) = (n m) >> (31 + l) exactly (m d - 2^(31+l) is in (0, d] <= 2^l,

@@ -77,7 +77,7 @@ __host__ __device__ inline PackedView native_view(const uc_kivi_item &it, int bi
   set_packed_strides(v, item_capacity(it), bits, group, D);
   v.rkey = it.residual_key; v.rval = it.residual_value;
   v.Tq = Tq; v.Tr = it.residual_tokens; v.Hkv = Hkv; v.D = D;
-  v.r_st = Hkv * D; v.r_sh = D;
+  residual_strides(it, Hkv, D, v.r_st, v.r_sh);
   return v;
 }
 
@@ -519,6 +519,51 @@ extern "C" int uc_kivi_attn_decode_segments(const uc_kivi_item *items_device, in
                        q_dtype, res_dtype, out_dtype, sm_scale, max_quantized_tokens, max_residual_tokens,
                        workspace, workspace_bytes, as_stream(stream), "uc_kivi_attn_decode_segments",
                        segments_per_query);
+}
+
+extern "C" int uc_kivi_attn_decode_segments_host(const uc_kivi_item *items_host, int64_t n_items, int bits,
+                                                 int group_size, int64_t heads_q, int64_t heads_kv,
+                                                 int64_t head_dim, int64_t query_len, int q_dtype, int res_dtype,
+                                                 int out_dtype, float sm_scale, void *workspace,
+                                                 int64_t workspace_bytes, uc_stream_t stream) {
+  clear_error();
+  constexpr int64_t kMaxHostItems = 8;
+  UC_REQUIRE(items_host != nullptr && n_items >= 1 && n_items <= kMaxHostItems,
+             "uc_kivi_attn_decode_segments_host: 1..%lld items", (long long)kMaxHostItems);
+  UC_REQUIRE(heads_kv > 0 && head_dim > 0, "uc_kivi_attn_decode_segments_host: bad head shape");
+  uc_kivi_item items[kMaxHostItems];
+  int64_t max_tq = 0, max_tr = 0;
+  for (int64_t i = 0; i < n_items; ++i) {
+    uc_kivi_item it = items_host[i];
+    // one query group: every segment reads the first item's query; its out / lse get the result
+    it.query = items_host[0].query;
+    it.out = items_host[0].out;
+    it.lse = items_host[0].lse;
+    UC_REQUIRE(it.quantized_tokens >= 0 && it.residual_tokens >= 0 && it.quantized_tokens % group_size == 0,
+               "uc_kivi_attn_decode_segments_host: item %lld: bad token counts", (long long)i);
+    UC_REQUIRE(it.quantized_tokens == 0 ||
+                   (it.key_code && it.key_scale && it.key_min && it.value_code && it.value_scale && it.value_min &&
+                    (it.packed_capacity == 0 ||
+                     (it.packed_capacity >= it.quantized_tokens && it.packed_capacity % group_size == 0))),
+               "uc_kivi_attn_decode_segments_host: item %lld: packed tensors or capacity", (long long)i);
+    if (it.residual_tokens) {
+      int64_t ts, hs;
+      residual_strides(it, heads_kv, head_dim, ts, hs);
+      UC_REQUIRE(it.residual_key && it.residual_value &&
+                     ((reinterpret_cast<uintptr_t>(it.residual_key) | reinterpret_cast<uintptr_t>(it.residual_value)) &
+                      15) == 0 && ts > 0 && hs >= 0 && ts % 8 == 0 && hs % 8 == 0,
+                 "uc_kivi_attn_decode_segments_host: item %lld: residual rows must be 16-byte aligned with strides "
+                 "in multiples of 8 elements", (long long)i);
+      UC_REQUIRE(((it.residual_tokens - 1) * ts + (heads_kv - 1) * hs + head_dim) * 2 < (int64_t(1) << 31),
+                 "uc_kivi_attn_decode_segments_host: item %lld: residual rows span 2 GiB or more", (long long)i);
+    }
+    max_tq = max(max_tq, it.quantized_tokens);
+    max_tr = max(max_tr, it.residual_tokens);
+    items[i] = it;
+  }
+  return decode_common(nullptr, items, n_items, bits, group_size, heads_q, heads_kv, head_dim, query_len, q_dtype,
+                       res_dtype, out_dtype, sm_scale, max_tq, max_tr, workspace, workspace_bytes, as_stream(stream),
+                       "uc_kivi_attn_decode_segments_host", n_items);
 }
 
 extern "C" int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int64_t heads_q,

@@ -131,6 +131,13 @@ struct DecShared {
   };
 };
 
+// Items passed by value in the kernel arguments (calls that name at most
+// kArgItems items from host memory); the kernels index them like a table.
+constexpr int kArgItems = 8;
+struct ArgItems {
+  uc_kivi_item v[kArgItems];
+};
+
 struct MfmaParams {
   int64_t Hq, Hkv, Lq, group, rows;
   int64_t splits_packed, splits_total, nst;  // nst: super-tiles per packed split
@@ -791,8 +798,13 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kap = lane >> 4;
   const int64_t Tr = it.residual_tokens;
-  const int64_t bytes = Tr * p.Hkv * kD * 2;
+  int64_t ts, hs;  // token and head strides of the rows (elements)
+  residual_strides(it, p.Hkv, kD, ts, hs);
+  const int64_t bytes = ((Tr - 1) * ts + (p.Hkv - 1) * hs + kD) * 2;  // extent of the rows (Tr >= 1 here)
   const Rsrc rk = make_rsrc(it.residual_key, bytes), rv = make_rsrc(it.residual_value, bytes);
+  // byte offset of token row t of this head; rows past Tr repeat the last row
+  // (their probabilities are 0, and its values are finite data)
+  const auto row_off = [&](int64_t t) { return static_cast<uint32_t>((min(t, Tr - 1) * ts + h * hs) * 2); };
   const int64_t tw = tr0 + wave * kResWaveTokens;
   constexpr int kTiles = kResWaveTokens / 16;
   const h8 csel[2] = {channel_selector(lane, 0), channel_selector(lane, 1)};
@@ -800,7 +812,7 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
 #pragma unroll
   for (int b = 0; b < kTiles; ++b) {
     acc[b] = f4{0, 0, 0, 0};
-    const uint32_t base = static_cast<uint32_t>(((tw + 16 * b + r) * p.Hkv + h) * kD * 2);
+    const uint32_t base = row_off(tw + 16 * b + r);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
       acc[b] = mfma32(load8_h<RD>(rk, base + (32 * kb + 8 * kap) * 2), query_frag(sq, kb, lane), acc[b]);
@@ -816,8 +828,8 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
   for (int j = 0; j < kTiles / 2; ++j) {
     const h4 pa4 = cvt4(acc[2 * j]), pb4 = cvt4(acc[2 * j + 1]);
     const h8 p8 = h8{pa4[0], pa4[1], pa4[2], pa4[3], pb4[0], pb4[1], pb4[2], pb4[3]};
-    const uint32_t base0 = static_cast<uint32_t>(((tw + 32 * j + r) * p.Hkv + h) * kD * 2);
-    const uint32_t base1 = static_cast<uint32_t>(((tw + 32 * j + 16 + r) * p.Hkv + h) * kD * 2);
+    const uint32_t base0 = row_off(tw + 32 * j + r);
+    const uint32_t base1 = row_off(tw + 32 * j + 16 + r);
 #pragma unroll
     for (int b2 = 0; b2 < 4; ++b2) {
       const h8 v0 = load8_h<RD>(rv, base0 + (32 * b2 + 8 * kap) * 2);
@@ -834,8 +846,7 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
 // ------------------------------------------------------------------ kernel --
 template <int BITS, int G, int RD, bool TABLE, bool FOLD>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void decode_mfma_kernel(
-    const uc_kivi_item *items, uc_kivi_item single,
-                                                               MfmaParams p) {
+    const uc_kivi_item *items, ArgItems ai, MfmaParams p) {
   __shared__ __align__(16) DecShared<BITS, G> sh;
   __shared__ __align__(16) _Float16 sq[16][kQPad];
   __shared__ __align__(16) _Float16 sones[kOnesLen];  // the ones rows of the cmin MFMA
@@ -854,8 +865,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     split = blockIdx.x % p.splits_total;
   }
   if (u >= p.units) return;  // uniform: the whole workgroup leaves
-  const int64_t item = TABLE ? u / p.Hkv : 0;
-  const uc_kivi_item it = TABLE ? items[item] : single;
+  const int64_t item = u / p.Hkv;
+  const uc_kivi_item it = TABLE ? items[item] : ai.v[item];
   const int64_t h = u % p.Hkv;
   if (!split_has_work(split, it.quantized_tokens, it.residual_tokens, p)) {  // uniform
     // only the statistics: (-inf, 0) gives the split weight 0 in the combine,
@@ -953,10 +964,10 @@ __device__ __forceinline__ void ml_fold(float &M, float &L, float m, float l) {
 }
 
 template <bool TABLE>
-__global__ __launch_bounds__(kCombineThreads) void decode_mfma_combine(const uc_kivi_item *items, uc_kivi_item single,
+__global__ __launch_bounds__(kCombineThreads) void decode_mfma_combine(const uc_kivi_item *items, ArgItems ai,
                                                                        MfmaParams p) {
-  const int64_t first = TABLE ? blockIdx.y * p.segs : 0;
-  const uc_kivi_item it = TABLE ? items[first] : single;
+  const int64_t first = blockIdx.y * p.segs;
+  const uc_kivi_item it = TABLE ? items[first] : ai.v[first];
   const int64_t h = blockIdx.x;
   const int part = blockIdx.z;
   const int tid = threadIdx.x, row = tid / kCombineLanes, j = tid % kCombineLanes;
@@ -1081,7 +1092,7 @@ constexpr bool kFoldable = BITS == 2 && G == 32;
 
 template <int BITS, int G, int RD>
 static void launch_typed(bool table, dim3 grid, hipStream_t stream, const uc_kivi_item *items_dev,
-                         const uc_kivi_item &one, const MfmaParams &p) {
+                         const ArgItems &one, const MfmaParams &p) {
   if constexpr (kFoldable<BITS, G>) {
     if (p.rows <= 8) {
       if (table)
@@ -1103,7 +1114,7 @@ static void launch_typed(bool table, dim3 grid, hipStream_t stream, const uc_kiv
 
 template <int BITS, int G>
 static void launch_group(bool table, int rd, dim3 grid, hipStream_t stream, const uc_kivi_item *items_dev,
-                         const uc_kivi_item &one, const MfmaParams &p) {
+                         const ArgItems &one, const MfmaParams &p) {
   if (rd == UC_FP16)
     launch_typed<BITS, G, UC_FP16>(table, grid, stream, items_dev, one, p);
   else
@@ -1149,7 +1160,11 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   p.ws_o = static_cast<_Float16 *>(workspace);
   p.ws_ml = reinterpret_cast<float *>(static_cast<char *>(workspace) + slots * 16 * kD * sizeof(_Float16));
   const bool table = items_dev != nullptr;
-  const uc_kivi_item one = single ? *single : uc_kivi_item{};
+  UC_REQUIRE(table || (single != nullptr && n_items <= kArgItems), "decode: at most %d items from host memory",
+             kArgItems);
+  ArgItems one{};
+  if (!table)
+    for (int64_t i = 0; i < n_items; ++i) one.v[i] = single[i];
   p.units = n_items * Hkv;
   p.super_tokens = 16 * (32 / bits);
   p.xcd_grouped = p.units >= 4 * kXcds;  // at most one unit of imbalance per XCD in four
@@ -1172,8 +1187,8 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
     hipLaunchKernelGGL((decode_mfma_combine<true>), dim3(Hkv, n_items / segs, kCombineParts), dim3(kCombineThreads),
                        0, stream, items_dev, one, p);
   else
-    hipLaunchKernelGGL((decode_mfma_combine<false>), dim3(Hkv, n_items, kCombineParts), dim3(kCombineThreads), 0,
-                       stream, items_dev, one, p);
+    hipLaunchKernelGGL((decode_mfma_combine<false>), dim3(Hkv, n_items / segs, kCombineParts), dim3(kCombineThreads),
+                       0, stream, items_dev, one, p);
   return check_launch("decode (MFMA combine)");
 }
 

@@ -409,6 +409,95 @@ def packed_segments_summary(packed: list, query: torch.Tensor, dense: list,
     return out, lse
 
 
+DECODE_MAX_SEGMENTS = 8  # items one uc_kivi_attn_decode_segments_host call takes
+
+
+def decode_segments_supported(packed: list, query: torch.Tensor, dense: list) -> bool:
+    """Whether decode_segments_summary takes this layout: decode-length 16-bit
+    queries (at most 16 query rows per KV head), head_dim 128, native packed
+    prefixes of equal 2/4-bit K/V sharing group size (32/64/128) and KV heads,
+    dense parts and residuals of one 16-bit dtype in rows whose channels are
+    contiguous, and at most 8 segments (each prefix with its residual, each
+    non-empty dense part)."""
+
+    if not packed or query.dim() != 3 or int(query.shape[2]) != 128 or query.dtype not in (torch.bfloat16,
+                                                                                             torch.float16):
+        return False
+    first = packed[0]
+    if first.k_bits not in (2, 4) or first.group_size not in (32, 64, 128):
+        return False
+    if any((s.k_bits, s.v_bits, s.group_size, s.num_kv_heads) != (first.k_bits, first.k_bits, first.group_size,
+                                                                  first.num_kv_heads) or not s.kernel_native_layout
+           for s in packed):
+        return False
+    if int(query.shape[0]) > _max_decode_query_len(first, int(query.shape[1])):
+        return False
+    parts = [(k, v) for k, v in dense if int(k.shape[0])] + [
+        (s.residual_key, s.residual_value) for s in packed if s.residual_tokens]
+    if len({k.dtype for k, _ in parts} | {v.dtype for _, v in parts}) > 1:
+        return False
+    if any(k.dtype not in (torch.bfloat16, torch.float16) or k.stride() != v.stride() or k.stride(2) != 1
+           for k, v in parts):
+        return False
+    return len(packed) + sum(1 for k, _ in dense if int(k.shape[0])) <= DECODE_MAX_SEGMENTS
+
+
+def decode_segments_summary(packed: list, query: torch.Tensor, dense: list) -> tuple[torch.Tensor, torch.Tensor]:
+    """One softmax of a decode-length query [Lq, Hq, 128] over the packed
+    prefixes (with their residuals) of the PackedKIVICache segments `packed`
+    and the dense (key, value) [T, Hkv, 128] parts `dense` -- any token and
+    head strides, so an H2O segment's [Hkv, R, 128] tensors enter transposed,
+    as views -- in one launch of the split-K decode kernels
+    (uc_kivi_attn_decode_segments_host): the segments are read where they lie,
+    nothing is concatenated and no summaries are merged.  This is the decode
+    form of _run_fused_mixed_attention (adapters/bagel.py:1598-1858).  Returns
+    (out [Lq, Hq, 128] in the query dtype, lse [Hq, Lq])."""
+
+    if not decode_segments_supported(packed, query, dense):
+        raise ValueError("Decode segment attention needs decode-length 16-bit queries, head_dim 128, native packed "
+                         "prefixes of equal 2/4-bit K/V sharing group size and KV heads, dense parts and residuals "
+                         f"of one 16-bit dtype with contiguous channels, and at most {DECODE_MAX_SEGMENTS} segments")
+    first = packed[0]
+    hkv = first.num_kv_heads
+    for key, value in dense:
+        if key.shape != value.shape or key.dim() != 3 or tuple(key.shape[1:]) != (hkv, 128):
+            raise ValueError("Dense segments must be matching [tokens, kv_heads, 128] tensors")
+    q = query.contiguous()
+    lq, hq, d = map(int, q.shape)
+    parts = [(k, v) for k, v in dense if int(k.shape[0])]
+    device = nat.require_device(
+        q, *(t for pair in parts for t in pair),
+        *(t for s in packed for t in (s.key_code, s.residual_key if s.residual_tokens else None)),
+        what="Decode segment attention")
+    res_dtype = next((k.dtype for k, _ in parts), None) or next(
+        (s.residual_key.dtype for s in packed if s.residual_tokens), q.dtype)
+    out = torch.empty((lq, hq, d), dtype=q.dtype, device=device)
+    lse = torch.empty((hq, lq), dtype=torch.float32, device=device)
+    n = len(packed) + len(parts)
+    items = (nat.KiviItem * n)()
+    max_tq = max_tr = 0
+    for j, cache in enumerate(packed):
+        tr = cache.residual_tokens
+        rk, rv = cache.residual_key, cache.residual_value
+        items[j] = cache.native_item(q.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                     residual_key_ptr=rk.data_ptr() if tr else None,
+                                     residual_value_ptr=rv.data_ptr() if tr else None, residual_tokens=tr)
+        if tr:
+            items[j].residual_token_stride, items[j].residual_head_stride = rk.stride(0), rk.stride(1)
+        max_tq, max_tr = max(max_tq, cache.quantized_tokens), max(max_tr, tr)
+    for j, (key, value) in enumerate(parts, start=len(packed)):
+        t = int(key.shape[0])
+        items[j] = nat.KiviItem(None, None, None, None, None, None, key.data_ptr(), value.data_ptr(), q.data_ptr(),
+                                out.data_ptr(), lse.data_ptr(), 0, t, 0, key.stride(0), key.stride(1))
+        max_tr = max(max_tr, t)
+    ws_bytes = nat.decode_workspace_bytes(n, first.k_bits, first.group_size, hq, hkv, d, lq, max_tq, max_tr)
+    workspace = nat.workspace(device, ws_bytes)
+    nat.call("uc_kivi_attn_decode_segments_host", items, n, first.k_bits, first.group_size, hq, hkv, d, lq,
+             nat.dtype_code(q.dtype), nat.dtype_code(res_dtype), nat.dtype_code(q.dtype), 1.0 / math.sqrt(d),
+             workspace.data_ptr(), ws_bytes, nat.stream(device))
+    return out, lse
+
+
 def packed_table_summaries(entries: list, *, dense_dtype: torch.dtype) -> None:
     """Several independent long-query attentions in as few launches as the
     table limits allow (uc_kivi_attn_mq_table, 8 queries / 8 packed prefixes /
