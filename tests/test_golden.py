@@ -72,21 +72,19 @@ def test_product_known_answers(device):
     assert (p.quantized_tokens, p.residual_tokens) == (c["quantized_tokens"], c["residual_tokens"])
     assert torch.equal(p.dequantize()[0][-c["residual_tokens"]:], x[-c["residual_tokens"]:])
 
-    # the HIP kernels take groups of 16..128: the reference's group sizes are
-    # doubled (8 -> 16, 16 -> 32), which leaves the monotonic rule unchanged
+    # test_physical.py:1099-1132 as written: head_dim 16, group 8, the reference backend
     c = CASES["monotonic"]
-    x = torch.randn(c["tokens"], c["kv_heads"], 2 * c["head_dim"], generator=g).to(torch.bfloat16).to(device)
+    x = torch.randn(c["tokens"], c["kv_heads"], c["head_dim"], generator=g).to(torch.bfloat16).to(device)
     k = c["kivi"]
     p = PackedKIVICache.from_dense(x, x.clone(), logical_token_ids=torch.arange(c["tokens"]), token_type_id=3,
-                                   k_bits=k["bits"], v_bits=k["bits"], group_size=2 * k["group_size"],
-                                   residual_length=k["residual_length"], backend="cuda")
+                                   k_bits=k["bits"], v_bits=k["bits"], group_size=k["group_size"],
+                                   residual_length=k["residual_length"], backend="reference")
     bits, group, ok = k["repack_down"]
-    assert p.repack_monotonic(bits=bits, group_size=2 * group) is ok and p.k_bits == bits
+    assert p.repack_monotonic(bits=bits, group_size=group) is ok and p.k_bits == bits and p.group_size == group
     bits, group, ok = k["repack_up"]
-    assert p.repack_monotonic(bits=bits, group_size=2 * group) is ok
+    assert p.repack_monotonic(bits=bits, group_size=group) is ok
     assert p.budget_shortfall_events == k["shortfall_events"]
     hc = c["h2o"]
-    x = x[..., : c["head_dim"]].contiguous()
     h = GQAH2OCache.from_dense(x, x.clone(), logical_token_ids=torch.arange(c["tokens"]), token_type_id=1,
                                per_kv_head_scores=torch.rand(c["kv_heads"], c["tokens"]).to(device),
                                target_tokens=hc["target_tokens"], recent_tokens=hc["recent_tokens"])

@@ -84,6 +84,46 @@ def test_mixed_and_8bit_layouts(device, kb, vb):
     assert np.array_equal(f32(rk), ok) and np.array_equal(f32(rv), ov)
 
 
+@pytest.mark.parametrize("bits,group,head_dim,tokens", [(4, 8, 16, 72), (2, 12, 64, 100), (2, 48, 128, 200),
+                                                       (8, 96, 128, 200), (4, 5, 16, 61), (2, 128, 64, 300)])
+def test_reference_backend_any_group(device, bits, group, head_dim, tokens):
+    # backend="reference" takes any positive group (physical.py:247-248): key
+    # groups along tokens, value groups along channels ending in a partial group
+    # when head_dim % group != 0, code words shared by groups and zero-padded;
+    # codes, stats (in the input dtype) and the dequantized tensors bit-exact
+    key, value = kv_pair(tokens, heads=2, head_dim=head_dim, seed=200 + group, outliers=2)
+    cache = PackedKIVICache.from_dense(key.to(device), value.to(device), logical_token_ids=torch.arange(tokens),
+                                       token_type_id=3, k_bits=bits, v_bits=bits, group_size=group,
+                                       residual_length=20, backend="reference")
+    seg = K.from_dense(f32(key), f32(value), k_bits=bits, v_bits=bits, group_size=group, residual_length=20,
+                       native=False, in_dtype="bf16")
+    assert not cache.kernel_native_layout and cache.quantized_tokens == seg.quantized_tokens > 0
+    _assert_cache_equal(cache, seg)
+    for dtype, name in ((torch.bfloat16, "bf16"), (torch.float32, "fp32")):
+        rk, rv = cache.dequantize(dtype)
+        ok, ov = K.dequantize(seg, name)
+        assert np.array_equal(f32(rk), ok) and np.array_equal(f32(rv), ov), name
+    # the reference backend attends by dequantizing (physical.py:452-475)
+    q = queries(2, heads=4, head_dim=head_dim, seed=5)
+    logits, apply_value = cache.attention_parts(q.to(device))
+    from oracle import attention as A
+
+    exp = A.packed_logits(seg, f32(q), kv_dtype="bf16")
+    assert np.allclose(f32(logits), exp, atol=2e-2 * max(1.0, float(np.abs(exp).max())) / 50)
+
+
+def test_native_layout_keeps_its_group_sizes(device):
+    key, value = kv_pair(64, heads=2, head_dim=16, seed=3)
+    with pytest.raises(ValueError):
+        PackedKIVICache.from_dense(key.to(device), value.to(device), logical_token_ids=torch.arange(64),
+                                   token_type_id=3, k_bits=4, v_bits=4, group_size=8, residual_length=8,
+                                   backend="cuda")
+    with pytest.raises(ValueError):
+        PackedKIVICache.from_dense(key.to(device), value.to(device), logical_token_ids=torch.arange(64),
+                                   token_type_id=3, k_bits=4, v_bits=4, group_size=0, residual_length=8,
+                                   backend="reference")
+
+
 def test_fp16_and_strided_inputs(device):
     key, value = kv_pair(128, seed=4, dtype=torch.float16)
     seg = K.from_dense(f32(key), f32(value), k_bits=4, v_bits=4, group_size=64, residual_length=0)

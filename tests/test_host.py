@@ -57,9 +57,14 @@ def test_argument_errors_are_value_errors():
     with pytest.raises(ValueError):
         PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3,
                                    k_bits=3, v_bits=2, group_size=32, residual_length=0)
+    # the kernel-native layout (backend "cuda", 2/4-bit) keeps its group sizes;
+    # every backend refuses a group size below 1 (physical.py:247-256)
     with pytest.raises(ValueError):
         PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3,
-                                   k_bits=2, v_bits=2, group_size=48, residual_length=0)
+                                   k_bits=2, v_bits=2, group_size=48, residual_length=0, backend="cuda")
+    with pytest.raises(ValueError):
+        PackedKIVICache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=3,
+                                   k_bits=2, v_bits=2, group_size=0, residual_length=0)
     with pytest.raises(ValueError):
         GQAH2OCache.from_dense(key, key, logical_token_ids=torch.arange(64), token_type_id=1,
                                per_kv_head_scores=torch.rand(3, 64), target_tokens=8, recent_tokens=2)

@@ -308,6 +308,98 @@ void launch_pack(const PackArgs &a, int kb, int vb, bool kvec, bool vvec, hipStr
 
 bool aligned(const void *p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
+// ------------------------------------------------------- any group size --
+// UniCache's reference backend takes any positive group size
+// (physical.py:247-248): a value row of head_dim channels may end in a partial
+// group (physical.py:151-158), and one code word may hold codes of several
+// groups.  One thread owns a span of lcm(G, codes per word) positions of a key
+// row (one head and channel, along tokens) or a value row (one head and token,
+// along channels) -- whole groups and whole words -- and walks its groups in
+// order: the group's exact range, its fp32 scale and minimum (stored rounded to
+// the stats dtype), then each code into the current word, stored when the word
+// is full or the row ends (zero-padded, as physical.py:72-85 pads).
+struct GenericPackArgs {
+  PackArgs p;
+  int group, kb, vb;
+  int64_t kspan, vspan;        // positions per thread
+  int64_t kthreads, vthreads;  // threads doing key / value rows
+};
+
+template <int IN>
+__device__ void pack_generic_row(const void *src, int64_t base, int64_t stride, int64_t length, int64_t begin,
+                                 int64_t end, int group, int bits, void *code, int64_t code_base,
+                                 int64_t code_stride, void *scale, void *minimum, int64_t stat_base,
+                                 int64_t stat_stride, int stats_dtype) {
+  const float max_code = float((1 << bits) - 1);
+  const int per_word = bits == 8 ? 1 : 32 / bits;
+  uint32_t word = 0;
+  for (int64_t g0 = begin; g0 < end; g0 += group) {
+    const int64_t g1 = min(g0 + int64_t(group), length);
+    GroupRange r;
+    r.init(load_as_f32<IN>(src, base + g0 * stride));
+    for (int64_t i = g0 + 1; i < g1; ++i) r.add(load_as_f32<IN>(src, base + i * stride));
+    r.finish();
+    const float mn = r.mn;
+    const float s = clamp_min_nan(div_rn(sub_rn(r.mx, mn), max_code), kEps);
+    const int64_t so = stat_base + (g0 / group) * stat_stride;
+    store_dyn(scale, so, s, stats_dtype);
+    store_dyn(minimum, so, mn, stats_dtype);
+    const float rcp = __builtin_amdgcn_rcpf(s);
+    for (int64_t i = g0; i < g1; ++i) {
+      const float x = load_as_f32<IN>(src, base + i * stride);
+      const uint32_t q = static_cast<uint32_t>(fminf(fmaxf(quant_rint(sub_rn(x, mn), s, rcp), 0.0f), max_code));
+      if (bits == 8) {
+        static_cast<uint8_t *>(code)[code_base + i * code_stride] = static_cast<uint8_t>(q);
+        continue;
+      }
+      const int pos = static_cast<int>(i % per_word);
+      word |= q << (pos * bits);
+      if (pos == per_word - 1 || i == length - 1) {
+        static_cast<int32_t *>(code)[code_base + (i / per_word) * code_stride] = static_cast<int32_t>(word);
+        word = 0;
+      }
+    }
+  }
+}
+
+template <int IN>
+__global__ __launch_bounds__(kPackThreads) void kivi_pack_generic_kernel(GenericPackArgs g) {
+  const PackArgs &a = g.p;
+  int64_t idx = int64_t(blockIdx.x) * kPackThreads + threadIdx.x;
+  if (idx < g.kthreads) {
+    const int64_t chunks = (a.tokens + g.kspan - 1) / g.kspan;
+    const int64_t c = idx % chunks, d = (idx / chunks) % a.head_dim, h = idx / (chunks * a.head_dim);
+    const int64_t begin = c * g.kspan, end = min(a.tokens, begin + g.kspan);
+    pack_generic_row<IN>(a.key, h * a.k_sh + d * a.k_sd, a.k_st, a.tokens, begin, end, g.group, g.kb, a.key_code,
+                         h * a.kc_sh + d * a.kc_sd, a.kc_sw, a.key_scale, a.key_min, h * a.ks_sh + d * a.ks_sd,
+                         a.ks_sg, a.stats_dtype);
+    return;
+  }
+  idx -= g.kthreads;
+  if (idx < g.vthreads) {
+    const int64_t chunks = (a.head_dim + g.vspan - 1) / g.vspan;
+    const int64_t c = idx % chunks, t = (idx / chunks) % a.tokens, h = idx / (chunks * a.tokens);
+    const int64_t begin = c * g.vspan, end = min(a.head_dim, begin + g.vspan);
+    pack_generic_row<IN>(a.value, h * a.v_sh + t * a.v_st, a.v_sd, a.head_dim, begin, end, g.group, g.vb,
+                         a.value_code, h * a.vc_sh + t * a.vc_st, a.vc_sw, a.value_scale, a.value_min,
+                         h * a.vs_sh + t * a.vs_st, a.vs_sg, a.stats_dtype);
+  }
+}
+
+int64_t gcd64(int64_t x, int64_t y) {
+  while (y) {
+    const int64_t r = x % y;
+    x = y;
+    y = r;
+  }
+  return x;
+}
+
+// The group sizes the tuned pack / dequant kernels take.
+bool tuned_group(int group, int64_t head_dim) {
+  return (group == 16 || group == 32 || group == 64 || group == 128) && head_dim % group == 0;
+}
+
 // -------------------------------------------------------------- dequant --
 struct DequantArgs {
   const void *key_code;
@@ -321,8 +413,9 @@ struct DequantArgs {
   int64_t heads, head_dim, start, count;
   void *out_key, *out_value;
   int64_t o_st, o_sh, o_sd, offset;
-  int lg;      // log2(group_size)
-  int sd, od;  // stats and output dtype codes
+  int lg;         // log2(group_size) (tuned group sizes)
+  int64_t group;  // group_size (any)
+  int sd, od;     // stats and output dtype codes
 };
 
 // One thread per output element (token, head, channel); keys and values are
@@ -344,7 +437,7 @@ __global__ __launch_bounds__(256) void kivi_dequant_kernel(DequantArgs a) {
     constexpr int kPerWord = KB == 8 ? 1 : 32 / KB;
     const uint32_t c = read_code<KB>(a.key_code, h * a.kc_sh + d * a.kc_sd + (t / kPerWord) * a.kc_sw,
                                      t % kPerWord);
-    const int64_t so = h * a.ks_sh + d * a.ks_sd + (t >> a.lg) * a.ks_sg;
+    const int64_t so = h * a.ks_sh + d * a.ks_sd + (t / a.group) * a.ks_sg;
     const float s = load_dyn(a.key_scale, so, a.sd);
     const float m = load_dyn(a.key_min, so, a.sd);
     out = add_rn(mul_rn(float(c), s), m);
@@ -354,7 +447,7 @@ __global__ __launch_bounds__(256) void kivi_dequant_kernel(DequantArgs a) {
     constexpr int kPerWord = VB == 8 ? 1 : 32 / VB;
     const uint32_t c = read_code<VB>(a.value_code, h * a.vc_sh + t * a.vc_st + (d / kPerWord) * a.vc_sw,
                                      d % kPerWord);
-    const int64_t so = h * a.vs_sh + t * a.vs_st + (d >> a.lg) * a.vs_sg;
+    const int64_t so = h * a.vs_sh + t * a.vs_st + (d / a.group) * a.vs_sg;
     const float s = load_dyn(a.value_scale, so, a.sd);
     const float m = load_dyn(a.value_min, so, a.sd);
     out = add_rn(mul_rn(float(c), s), m);
@@ -619,13 +712,10 @@ extern "C" int uc_kivi_pack(const void *key, int64_t k_st, int64_t k_sh, int64_t
   UC_REQUIRE(valid_dtype(in_dtype) && valid_dtype(stats_dtype), "uc_kivi_pack: unknown dtype code");
   UC_REQUIRE(k_bits == 2 || k_bits == 4 || k_bits == 8, "KIVI physical cache supports 2, 4, or 8 bit payloads");
   UC_REQUIRE(v_bits == 2 || v_bits == 4 || v_bits == 8, "KIVI physical cache supports 2, 4, or 8 bit payloads");
-  UC_REQUIRE(group_size == 16 || group_size == 32 || group_size == 64 || group_size == 128,
-             "The MI355X KIVI kernels support group_size 16, 32, 64 or 128, got %d", group_size);
+  UC_REQUIRE(group_size > 0, "KIVI physical cache group_size must be positive");
   UC_REQUIRE(tokens >= 0 && heads > 0 && head_dim > 0, "uc_kivi_pack: bad shape");
   UC_REQUIRE(tokens % group_size == 0, "uc_kivi_pack: tokens (%lld) must be a multiple of group_size",
              (long long)tokens);
-  UC_REQUIRE(head_dim % group_size == 0,
-             "The MI355X KIVI value kernel requires head_dim divisible by group_size");
   UC_REQUIRE(head_dim <= 1024, "uc_kivi_pack: head_dim must be <= 1024");
   if (tokens == 0) return UC_OK;
   PackArgs a{};
@@ -636,6 +726,28 @@ extern "C" int uc_kivi_pack(const void *key, int64_t k_st, int64_t k_sh, int64_t
   a.key_scale = key_scale; a.key_min = key_min; a.ks_sh = ks_sh; a.ks_sd = ks_sd; a.ks_sg = ks_sg;
   a.value_code = value_code; a.vc_sh = vc_sh; a.vc_st = vc_st; a.vc_sw = vc_sw;
   a.value_scale = value_scale; a.value_min = value_min; a.vs_sh = vs_sh; a.vs_st = vs_st; a.vs_sg = vs_sg;
+  hipStream_t s = as_stream(stream);
+  if (!tuned_group(group_size, head_dim)) {
+    // any other group size, and value rows with a partial last group
+    GenericPackArgs g{};
+    g.p = a;
+    g.group = group_size;
+    g.kb = k_bits;
+    g.vb = v_bits;
+    const int64_t kpw = k_bits == 8 ? 1 : 32 / k_bits, vpw = v_bits == 8 ? 1 : 32 / v_bits;
+    g.kspan = group_size / gcd64(group_size, kpw) * kpw;
+    g.vspan = group_size / gcd64(group_size, vpw) * vpw;
+    g.kthreads = key ? heads * head_dim * ((tokens + g.kspan - 1) / g.kspan) : 0;
+    g.vthreads = value ? heads * tokens * ((head_dim + g.vspan - 1) / g.vspan) : 0;
+    const dim3 grid(static_cast<unsigned>(ceil_div(g.kthreads + g.vthreads, int64_t(kPackThreads))));
+    if (in_dtype == UC_BF16)
+      hipLaunchKernelGGL((kivi_pack_generic_kernel<UC_BF16>), grid, dim3(kPackThreads), 0, s, g);
+    else if (in_dtype == UC_FP16)
+      hipLaunchKernelGGL((kivi_pack_generic_kernel<UC_FP16>), grid, dim3(kPackThreads), 0, s, g);
+    else
+      hipLaunchKernelGGL((kivi_pack_generic_kernel<UC_FP32>), grid, dim3(kPackThreads), 0, s, g);
+    return check_launch("uc_kivi_pack");
+  }
   const int64_t slabs = (head_dim + 127) / 128;
   a.key_waves = key ? heads * (tokens / group_size) * slabs : 0;
   const int64_t lanes_per_token = head_dim / 16;
@@ -644,7 +756,6 @@ extern "C" int uc_kivi_pack(const void *key, int64_t k_st, int64_t k_sh, int64_t
   const bool half = half_dtype(in_dtype);
   const bool kvec = half && k_sd == 1 && (k_st % 2 == 0) && (k_sh % 2 == 0) && aligned(key, 4);
   const bool vvec = half && v_sd == 1 && (v_st % 8 == 0) && (v_sh % 8 == 0) && aligned(value, 16);
-  hipStream_t s = as_stream(stream);
   // 16-bit inputs only take the vectorised path; fp32 inputs use scalar loads
   auto go = [&](auto in_tag) {
     constexpr int IN = decltype(in_tag)::value;
@@ -673,8 +784,7 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
   UC_REQUIRE(valid_dtype(stats_dtype) && valid_dtype(out_dtype), "uc_kivi_dequant: unknown dtype code");
   UC_REQUIRE(k_bits == 2 || k_bits == 4 || k_bits == 8, "KIVI physical cache supports 2, 4, or 8 bit payloads");
   UC_REQUIRE(v_bits == 2 || v_bits == 4 || v_bits == 8, "KIVI physical cache supports 2, 4, or 8 bit payloads");
-  UC_REQUIRE(group_size == 16 || group_size == 32 || group_size == 64 || group_size == 128,
-             "The MI355X KIVI kernels support group_size 16, 32, 64 or 128, got %d", group_size);
+  UC_REQUIRE(group_size > 0, "KIVI physical cache group_size must be positive");
   UC_REQUIRE(heads > 0 && head_dim > 0 && start >= 0 && stop >= start && output_offset >= 0,
              "uc_kivi_dequant: bad range");
   UC_REQUIRE(key_code == nullptr || out_key != nullptr, "uc_kivi_dequant: missing key output");
@@ -692,6 +802,7 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
   const int64_t total = 2 * count * heads * head_dim;
   const int64_t blocks = ceil_div(total, 256);
   a.lg = group_size == 16 ? 4 : group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
+  a.group = group_size;
   a.sd = stats_dtype; a.od = out_dtype;
   hipStream_t s = as_stream(stream);
   // native 2/4-bit layout with pairwise-aligned unit-stride output rows
@@ -703,7 +814,8 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
   // library's native storage) key codes
   const bool key_native = key_code != nullptr && (k_bits == 2 || k_bits == 4) && (kc_sw == 1 || kc_sd == 1);
   const bool value_native = value_code != nullptr && (v_bits == 2 || v_bits == 4) && vc_sw == 1;
-  if (out_ok && (key_code == nullptr || key_native) && (value_code == nullptr || value_native)) {
+  if (out_ok && tuned_group(group_size, head_dim) && (key_code == nullptr || key_native) &&
+      (value_code == nullptr || value_native)) {
     UC_DISPATCH_DTYPE(out_dtype, OD, [&] {
       if (key_code != nullptr) {
         const int tpw = 32 / k_bits;

@@ -297,12 +297,13 @@ def _pack_native(key: torch.Tensor, value: torch.Tensor, *, k_bits: int, v_bits:
 def _reference_layout_shapes(tokens, heads, head_dim, bits, group_size, *, is_key):
     """UniCache's non-native layout: codes along dim 0 (K) / dim 2 (V)."""
 
+    per_word = 1 if bits == 8 else 32 // bits  # codes zero-padded to whole words (physical.py:72-85)
     if is_key:
-        code = (tokens if bits == 8 else tokens * bits // 32, heads, head_dim)
+        code = (-(-tokens // per_word), heads, head_dim)
         stats = (tokens // group_size, heads, head_dim)
     else:
-        code = (tokens, heads, head_dim if bits == 8 else head_dim * bits // 32)
-        stats = (tokens, heads, head_dim // group_size)
+        code = (tokens, heads, -(-head_dim // per_word))
+        stats = (tokens, heads, -(-head_dim // group_size))  # a partial last group (physical.py:151-158)
     return code, stats, (torch.uint8 if bits == 8 else torch.int32)
 
 
@@ -389,10 +390,12 @@ class PackedKIVICache:
         if group_size <= 0:
             raise ValueError("KIVI physical cache group_size must be positive")
         _check_backend(backend)
-        if group_size not in {16, 32, 64, 128}:
-            raise ValueError("The MI355X KIVI kernels support group_size 16, 32, 64 or 128")
-        if head_dim % group_size != 0:
-            raise ValueError("The MI355X KIVI value kernel requires head_dim divisible by group_size")
+        if backend == "cuda" and (k_bits in {2, 4} or v_bits in {2, 4}):
+            # the kernel-native layout (physical.py:247-256 pins 64 or 128 for it)
+            if group_size not in {16, 32, 64, 128}:
+                raise ValueError("The MI355X KIVI kernels support group_size 16, 32, 64 or 128")
+            if head_dim % group_size != 0:
+                raise ValueError("The MI355X KIVI value kernel requires head_dim divisible by group_size")
         requested_residual = min(tokens, max(0, int(residual_length)))
         # keep any incomplete prefix group in the residual (physical.py:258-263)
         quantized = ((tokens - requested_residual) // group_size) * group_size
