@@ -760,6 +760,10 @@ def main():
                         help="only build the config-1 workload and run its decode step (for counter passes)")
     parser.add_argument("--only-editing", type=int, choices=(2, 4), default=None,
                         help="only run the config-2 editing attention at this bit width (for counter passes)")
+    parser.add_argument("--only-h2o", action="store_true",
+                        help="only run the config-3 H2O line (for counter passes)")
+    parser.add_argument("--only-pack", action="store_true",
+                        help="only run the pack lines (for counter passes)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decode hot path shards by sequence / KV head with no "
@@ -777,6 +781,13 @@ def main():
 
     if args.only_editing:
         print(json.dumps(editing_attention(device, args.steps, layers=args.layers, bits=args.only_editing)))
+        return
+    if args.only_h2o:
+        print(json.dumps(h2o_eviction(device, args.steps)))
+        return
+    if args.only_pack:
+        gbs, ms = pack_throughput(device, args.steps)
+        print(json.dumps({"pack_gbs": round(gbs, 2), "pack_ms_per_sequence": round(ms, 5)}))
         return
 
     from unicache_amd.storage.decode import KiviDecodeBatch
