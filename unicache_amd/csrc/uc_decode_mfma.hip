@@ -1,35 +1,41 @@
 // MFMA split-K decode over KIVI-packed KV (head_dim 128, 2/4-bit codes).
 //
-// One workgroup (4 waves) owns a packed split of one unit (item, KV head) --
-// every S-th super-tile (16 key words of every channel) starting at the split
-// index -- or a residual split.  The S splits of a unit run side by side on
-// one XCD, so the 128-byte lines of the channel-major key streams are read
-// from HBM about once although each split uses a part of them.  An iteration
-// stages one super-tile in LDS; wave w takes its tiles w*TW .. w*TW + TW - 1
-// (a tile = 16 consecutive tokens).  The <= 16 query rows of a KV head (query
-// heads x query length) form the N = 16 columns of every MFMA.
+// Storage is token-major (a super-tile of one KV head is one contiguous run of
+// every stream: key words, key stats, value words, value stats).  One
+// workgroup (4 waves) owns a packed split of one unit (item, KV head) --
+// every S-th super-tile (16 key words per channel: 256 tokens at 2-bit)
+// starting at the split index -- or a residual split of 256 dense tokens.
+// Wave w loads, stages (in its own LDS area, no workgroup barrier in the loop)
+// and computes tokens 64w .. 64w + 63 of each super-tile; the next
+// super-tile's loads are issued before the current one is computed.  The
+// <= 16 query rows of a KV head (query heads x query length) form the N = 16
+// columns of every MFMA, so each packed byte is read once per unit.
 //
 // Keys (S^T = K Q^T on v_mfma_f32_16x16x32_f16).  MFMA rows are the 16 tokens
 // of a tile, which lie in one quantization group, so
 //     logit = sum_c (q_c s_c) code_c + sum_c q_c m_c :
 // the key scale is folded into the B operand once per group (B' = q * s), and
-// the minimum term is one MFMA per group whose A rows all hold the minima.
-// Staging interleaves the words of channel pairs (c, c+1) byte by byte: one
-// dword holds byte k of both words, in its two 16-bit halves, so each A
-// register -- two channels at the row's position -- is one AND that leaves
-// code << BITS*e (e < 8/BITS, at most 6 bits up) in each half: an fp16 value
-// code * 2^(BITS*e - 24), which the MFMA multiplies exactly.  The row's power of two, the
-// softmax scale and the minimum term are applied in one FMA per logit.
+// the minimum term is one MFMA set per wave whose A rows hold the minima of
+// the wave's groups.  Staging spreads the words of two channels byte by byte:
+// one dword holds byte k of both words in its two 16-bit halves, so each A
+// register is one AND (fused with the DPP quad exchange) that leaves
+// code << BITS*e in each half: an fp16 value code * 2^(BITS*e - 24), which the
+// MFMA multiplies exactly.  The row's power of two, the softmax scale and the
+// minimum term are applied in one FMA per logit.
 //
 // Values (O^T += V^T P^T).  MFMA rows are 16 channels, K = 32 tokens (two
-// tiles).  Staging interleaves the words of token pairs the same way, so each A
-// register (two tokens of the row's channel) is one AND; the power of two of
-// each output channel is undone once at the end.  The per-token value scale
-// rides in the B operand (P * scale, per channel group); the per-token value
-// minimum returns through one MFMA per K block whose A rows are the groups.
+// tiles), staged the same way by token pairs; the power of two of each output
+// channel is undone once at the end.  The value scale rides in the B operand
+// (P * scale, per channel group); one MFMA per K block adds the minima and, in
+// a row of ones, the softmax denominator sum_t P.
 //
-// Each split writes a normalised fp16 partial with its (max, sum); a second
-// kernel merges the splits with a log-sum-exp combine.
+// Column-folded form (2-bit, G = 32, at most 8 query rows): MFMA columns 0-7
+// serve the wave's first 32-token group and columns 8-15 its second, so the
+// B' products, logit FMAs and exponentials are halved; the two halves merge
+// by a lane exchange at the end of the split.
+//
+// Each split writes a normalised fp16 partial of its query rows with its
+// (max, sum); decode_mfma_combine merges the splits by log-sum-exp.
 #include "uc_common.h"
 #include "uc_decode.h"
 #include "uc_mfma.h"
@@ -290,10 +296,6 @@ struct Prefetch {
 struct PackedRegion {
   Rsrc kcode, kscale, kmin, vcode, vscale, vmin;
 };
-
-// A buffer offset past every resource of this file (their sizes are checked to
-// stay below 2^31 bytes): the load returns 0 and touches no memory.
-constexpr uint32_t kOffOutside = 0x80000000u;
 
 // Issue this wave's loads of the super-tile starting at token t0 (a
 // multiple of ST): tokens t0 + WT wave ...  Rows past the packed tokens fall
