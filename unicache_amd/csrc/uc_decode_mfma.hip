@@ -943,127 +943,124 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   }
 }
 
-// Merge the split partials of one (query, KV head) -- every split of the
-// p.segs items that share the query -- for a quarter of the channels
-// (blockIdx.z).  Thread (row = tid / 8, j = tid % 8) folds the (max, sum) of
-// slots j, j + 8, ... into an online (M, L), the 8 threads of a row combine
-// theirs with lane shuffles, and each then accumulates its 4 channels over all
-// slots with weights l_s 2^(m_s - M) / L, eight slots' loads in flight.  No
-// LDS and no barrier: the launch is a short chain of independent loads.  The
-// output goes to the first item of the group.
-constexpr int kCombineThreads = 128;
-constexpr int kCombineParts = 4;  // channel quarters per (query, KV head)
-constexpr int kCombineLanes = 8;  // threads per query row
+// Merge the split partials of one (query group, KV head) -- every split of the
+// p.segs items that share the query.  Thread (row = t / 16, c = t % 16) of a
+// part owns channels 8c .. 8c + 7 of one query row, so a row's 16 threads read
+// each partial row as one contiguous 256-byte run; a part has only the threads
+// of the query rows (rounded to whole waves).  The splits are dealt to
+// `parts` (1, 2 or 4) parts of the block in contiguous runs; a part takes its
+// run in rounds of kCombineRound, every load of a round issued before any
+// arithmetic, with an online (M, L): a round that raises the maximum rescales
+// the sums first.  The parts then merge through LDS, part 0 writes the output
+// and the LSE of the group's first item.  Splits without work wrote (-inf, 0)
+// and no partial: their weight is 0 and their partial is not read.
+constexpr int kCombineRound = 16;
+constexpr int kCombineMaxThreads = 1024;
 
-__device__ __forceinline__ void ml_fold(float &M, float &L, float m, float l) {
-  if (!(l > 0.0f) || m == kNegInf) return;
-  if (m > M) {
-    L = (L > 0.0f ? L * exp2f(M - m) : 0.0f) + l;
-    M = m;
-  } else {
-    L += l * exp2f(m - M);
+// Eight channels of output element `idx` on, from fp32 (one 16-byte store for
+// 16-bit outputs).
+__device__ __forceinline__ void store_out8(void *out, int64_t idx, const float *v, int od) {
+  if (od == UC_FP32) {
+    float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + idx);
+    o[0] = make_float4(v[0], v[1], v[2], v[3]);
+    o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    return;
   }
+  uint32_t w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t lo = od == UC_BF16 ? f32_to_bf16_bits(v[2 * k]) : f32_to_f16_bits(v[2 * k]);
+    const uint32_t hi = od == UC_BF16 ? f32_to_bf16_bits(v[2 * k + 1]) : f32_to_f16_bits(v[2 * k + 1]);
+    w[k] = lo | (hi << 16);
+  }
+  *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + idx) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 template <bool TABLE>
-__global__ __launch_bounds__(kCombineThreads) void decode_mfma_combine(const uc_kivi_item *items, ArgItems ai,
-                                                                       MfmaParams p) {
-  const int64_t first = blockIdx.y * p.segs;
-  const uc_kivi_item it = TABLE ? items[first] : ai.v[first];
-  const int64_t h = blockIdx.x;
-  const int part = blockIdx.z;
-  const int tid = threadIdx.x, row = tid / kCombineLanes, j = tid % kCombineLanes;
-  const int nflat = int(p.segs * p.splits_total);
-  static_assert(16 * kCombineLanes == kCombineThreads && kD / kCombineParts == 4 * kCombineLanes,
-                "thread = (row, 4 channels of the part)");
-  // flattened (segment, split) index -> workspace slot
-  auto slot = [&](int f) {
-    return ((first + f / p.splits_total) * p.Hkv + h) * p.splits_total + f % p.splits_total;
-  };
-  // splits without work wrote (-inf, 0) and no output
-  auto ml_at = [&](int f) { return *reinterpret_cast<const float2 *>(p.ws_ml + (slot(f) * 16 + row) * 2); };
-  const bool active = row < p.rows;
-  const int c4 = (part * kCombineLanes + j) * 4;
-  if (nflat <= kCombineLanes) {
-    // at most 8 slots: every load of the row -- its (max, sum) pairs and this
-    // thread's 4 channels of each partial -- is issued at once, before any
-    // arithmetic (two dependent rounds of loads would double the latency)
-    float2 ml[kCombineLanes];
-    h4 v[kCombineLanes];
-#pragma unroll
-    for (int u = 0; u < kCombineLanes; ++u) {
-      const int f = u < nflat ? u : 0;
-      ml[u] = ml_at(f);
-      v[u] = active ? *reinterpret_cast<const h4 *>(p.ws_o + (slot(f) * 16 + row) * kD + c4) : h4{0, 0, 0, 0};
-    }
-    float M = kNegInf, L = 0.0f;
-#pragma unroll
-    for (int u = 0; u < kCombineLanes; ++u)
-      if (u < nflat) ml_fold(M, L, ml[u].x, ml[u].y);
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    if (active && part == 0 && j == 0 && it.lse != nullptr) {
-      const int64_t g = row / p.Lq, i = row % p.Lq;
-      it.lse[(h * p.group + g) * p.Lq + i] = L > 0.0f ? (M + log2f(L)) * kLn2 : kNegInf;
-    }
-    if (active) {
-      float o[4] = {0, 0, 0, 0};
-#pragma unroll
-      for (int u = 0; u < kCombineLanes; ++u) {
-        const float w = (u < nflat && ml[u].y > 0.0f && ml[u].x != kNegInf) ? ml[u].y * exp2f(ml[u].x - M) * inv
-                                                                           : 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o[c] = w != 0.0f ? fmaf(float(v[u][c]), w, o[c]) : o[c];
-      }
-      const int64_t g = row / p.Lq, i = row % p.Lq;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) store_dyn(it.out, (i * p.Hq + h * p.group + g) * kD + c4 + c, o[c], p.od);
-    }
-    return;
-  }
-  // pass 1: this thread's slots, four loads in flight, then the row's 8 threads
+__global__ __launch_bounds__(kCombineMaxThreads) void decode_mfma_combine(const uc_kivi_item *items, ArgItems ai,
+                                                                          MfmaParams p, int parts) {
+  extern __shared__ float red[];  // per thread of parts 1..: M, L, 8 sums (10 floats)
+  const int64_t first = blockIdx.x * p.segs;
+  const int64_t h = blockIdx.y;
+  const int span = int(blockDim.x) / parts;  // threads per part (whole waves)
+  const int part = int(threadIdx.x) / span, t = int(threadIdx.x) % span;
+  const int r = t >> 4, c8 = (t & 15) * 8;
+  const bool active = r < p.rows;
+  const int splits = int(p.splits_total), nflat = int(p.segs) * splits;
+  const int run = (nflat + parts - 1) / parts, f_lo = part * run, f_hi = min(nflat, f_lo + run);
+  // (segment, split) f -> workspace slot: segment f / splits of the group
+  auto slot = [&](int f) { return ((first + f / splits) * p.Hkv + h) * p.splits_total + f % splits; };
   float M = kNegInf, L = 0.0f;
-  for (int f0 = j; f0 < nflat; f0 += 4 * kCombineLanes) {
-    float2 ml[4];
+  float acc[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int f = f0 + u * kCombineLanes;
-      ml[u] = f < nflat ? ml_at(f) : make_float2(kNegInf, 0.0f);
-    }
+  for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+  for (int f0 = f_lo; active && f0 < f_hi; f0 += kCombineRound) {
+    float2 ml[kCombineRound];
+    uint4 v[kCombineRound];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) ml_fold(M, L, ml[u].x, ml[u].y);
-  }
-#pragma unroll
-  for (int o = 1; o < kCombineLanes; o <<= 1) {
-    const float m2 = __shfl_xor(M, o, kWave), l2 = __shfl_xor(L, o, kWave);
-    ml_fold(M, L, m2, l2);
-  }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  if (active && part == 0 && j == 0 && it.lse != nullptr) {
-    const int64_t g = row / p.Lq, i = row % p.Lq;
-    it.lse[(h * p.group + g) * p.Lq + i] = L > 0.0f ? (M + log2f(L)) * kLn2 : kNegInf;
-  }
-  // pass 2: 4 channels of this part over every slot
-  float o[4] = {0, 0, 0, 0};
-  if (active) {
-    for (int f0 = 0; f0 < nflat; f0 += 8) {
-      h4 v[8];
-      float w[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int f = f0 + u < nflat ? f0 + u : f0;
-        const float2 ml = ml_at(f);
-        w[u] = (f0 + u < nflat && ml.y > 0.0f && ml.x != kNegInf) ? ml.y * exp2f(ml.x - M) * inv : 0.0f;
-        v[u] = *reinterpret_cast<const h4 *>(p.ws_o + (slot(f) * 16 + row) * kD + c4);
+    for (int u = 0; u < kCombineRound; ++u) {
+      if (f0 + u < f_hi) {
+        const int64_t sl = slot(f0 + u);
+        ml[u] = *reinterpret_cast<const float2 *>(p.ws_ml + (sl * 16 + r) * 2);
+        v[u] = *reinterpret_cast<const uint4 *>(p.ws_o + (sl * 16 + r) * kD + c8);
+      } else {
+        ml[u] = make_float2(kNegInf, 0.0f);
       }
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o[c] = w[u] != 0.0f ? fmaf(float(v[u][c]), w[u], o[c]) : o[c];
     }
-    const int64_t g = row / p.Lq, i = row % p.Lq;
+    float mr = M;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) store_dyn(it.out, (i * p.Hq + h * p.group + g) * kD + c4 + c, o[c], p.od);
+    for (int u = 0; u < kCombineRound; ++u)
+      if (ml[u].y > 0.0f && ml[u].x != kNegInf) mr = fmaxf(mr, ml[u].x);
+    if (mr > M) {  // rescale what earlier rounds summed
+      const float sc = M == kNegInf ? 0.0f : exp2f(M - mr);
+      L *= sc;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] *= sc;
+      M = mr;
+    }
+#pragma unroll
+    for (int u = 0; u < kCombineRound; ++u) {
+      if (!(ml[u].y > 0.0f) || ml[u].x == kNegInf) continue;
+      const float w = ml[u].y * exp2f(ml[u].x - M);
+      L += w;
+      const uint32_t wd[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] = fmaf(f16_bits_to_f32(uint16_t(wd[e] & 0xffffu)), w, acc[2 * e]);
+        acc[2 * e + 1] = fmaf(f16_bits_to_f32(uint16_t(wd[e] >> 16)), w, acc[2 * e + 1]);
+      }
+    }
   }
+  if (parts > 1) {  // uniform
+    if (part > 0) {
+      float *e = red + (threadIdx.x - span) * 10;
+      e[0] = M;
+      e[1] = L;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) e[2 + c] = acc[c];
+    }
+    __syncthreads();
+    if (part > 0) return;
+    for (int q = 1; q < parts; ++q) {
+      const float *e = red + ((q - 1) * span + t) * 10;
+      const float m2 = e[0], l2 = e[1];
+      if (!(l2 > 0.0f)) continue;
+      const float mn = fmaxf(M, m2);
+      const float s1 = M == kNegInf ? 0.0f : exp2f(M - mn), s2 = exp2f(m2 - mn);
+      L = L * s1 + l2 * s2;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] = acc[c] * s1 + e[2 + c] * s2;
+      M = mn;
+    }
+  }
+  if (!active) return;
+  const uc_kivi_item it = TABLE ? items[first] : ai.v[first];
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) acc[c] *= inv;
+  const int64_t g = r / p.Lq, i = r % p.Lq;
+  if (c8 == 0 && it.lse != nullptr) it.lse[(h * p.group + g) * p.Lq + i] = L > 0.0f ? (M + log2f(L)) * kLn2 : kNegInf;
+  store_out8(it.out, (i * p.Hq + h * p.group + g) * kD + c8, acc, p.od);
 }
 
 }  // namespace
@@ -1185,12 +1182,17 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   if (rc != UC_OK) return rc;
   UC_REQUIRE(segs >= 1 && n_items % segs == 0, "decode: %lld items do not form groups of %lld segments",
              (long long)n_items, (long long)segs);
+  // one block per (query group, KV head): `parts` runs of about 12 splits each
+  // (at most 4), each part with the threads of the query rows
+  const int64_t nflat = segs * p.splits_total;
+  const int parts = nflat > 36 ? 4 : nflat > 12 ? 2 : 1;
+  const dim3 cgrid(static_cast<unsigned>(n_items / segs), static_cast<unsigned>(Hkv));
+  const dim3 cblock(static_cast<unsigned>(parts * ceil_div(p.rows * 16, int64_t(kWave)) * kWave));
+  const size_t lds = size_t(cblock.x / parts) * (parts - 1) * 10 * sizeof(float);
   if (table)
-    hipLaunchKernelGGL((decode_mfma_combine<true>), dim3(Hkv, n_items / segs, kCombineParts), dim3(kCombineThreads),
-                       0, stream, items_dev, one, p);
+    hipLaunchKernelGGL((decode_mfma_combine<true>), cgrid, cblock, lds, stream, items_dev, one, p, parts);
   else
-    hipLaunchKernelGGL((decode_mfma_combine<false>), dim3(Hkv, n_items / segs, kCombineParts), dim3(kCombineThreads),
-                       0, stream, items_dev, one, p);
+    hipLaunchKernelGGL((decode_mfma_combine<false>), cgrid, cblock, lds, stream, items_dev, one, p, parts);
   return check_launch("decode (MFMA combine)");
 }
 
