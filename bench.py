@@ -301,14 +301,16 @@ def h2o_eviction(device, steps):
     spans = [(0, 256), (256, 4096)]
     ids = [torch.arange(lo, hi, device=device) for lo, hi in spans]  # the caller's logical token ids
 
+    budgets = [h2o_budget(hi - lo, {"target_budget_ratio": 0.2}) for lo, hi in spans]
+
     def select_gather():
-        segs = []
-        for (lo, hi), seg_ids in zip(spans, ids):
-            target, recent = h2o_budget(hi - lo, {"target_budget_ratio": 0.2})
-            segs.append(GQAH2OCache.from_dense(key[lo:hi], value[lo:hi], logical_token_ids=seg_ids,
-                                               token_type_id=1, per_kv_head_scores=scores[:, lo:hi],
-                                               target_tokens=target, recent_tokens=recent, selection_frozen=True))
-        return segs
+        # both segments of the layer, as compact_and_materialize builds them:
+        # one GQAH2OCache.from_dense_segments call, one launch
+        return GQAH2OCache.from_dense_segments([
+            dict(key=key[lo:hi], value=value[lo:hi], logical_token_ids=seg_ids, token_type_id=1,
+                 per_kv_head_scores=scores[:, lo:hi], target_tokens=target, recent_tokens=recent,
+                 selection_frozen=True)
+            for (lo, hi), seg_ids, (target, recent) in zip(spans, ids, budgets)])
 
     ms_sel = time_steps(select_gather, steps, 2, stream)
     retained = sum(s.retained_tokens for s in select_gather())

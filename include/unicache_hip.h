@@ -488,6 +488,40 @@ int uc_h2o_select_gather(const void *key, const void *value, int64_t k_st, int64
                          uc_stream_t stream);
 
 /*
+ * One H2O segment of uc_h2o_select_gather_segments: the uc_h2o_select_gather
+ * arguments of one segment (rows [tokens, Hkv, D] by element strides, fp32
+ * scores [Hkv, tokens], optional int64 ids, outputs [Hkv, heavy_k + recent]).
+ */
+typedef struct uc_h2o_segment {
+  const void *key, *value;
+  int64_t k_st, k_sh, k_sd;
+  const float *scores;
+  int64_t s_sh, s_st;
+  const int64_t *ids;  /* NULL: no ids (then out_ids NULL too) */
+  int64_t ids_sh, ids_st;
+  int64_t tokens, heavy_k, recent;
+  int64_t *indices;
+  void *out_key, *out_value;
+  int64_t *out_ids;
+  float *out_scores;   /* NULL: the scores are not gathered */
+} uc_h2o_segment;
+
+/*
+ * uc_h2o_select_gather for several segments (same dtype, KV heads and
+ * head_dim) in one launch: each (segment, KV head) selects in one workgroup
+ * and gathers through the indices it keeps in LDS, split over up to 16
+ * workgroups per head.  Results equal one uc_h2o_select_gather per segment.
+ * Up to 8 segments of 16-bit rows (16-byte aligned, strides multiples of 8
+ * elements) with at most 8192 tokens share the launch; any other segment runs
+ * through uc_h2o_select_gather on the same stream.
+ * No reference counterpart: GQAH2OCache.from_dense (physical.py:511-546) per
+ * segment is what a caller with several H2O segments (the instruction and ViT
+ * segments of one materialisation, storage/tensor_backend.py) replaces.
+ */
+int uc_h2o_select_gather_segments(const uc_h2o_segment *segments, int n_segments, int dtype,
+                                  int64_t heads_kv, int64_t head_dim, uc_stream_t stream);
+
+/*
  * uc_h2o_scores with the softmax normaliser given instead of computed:
  *   P = bf16(exp(sm_scale * q_i . k_t - lse[h, i]))
  * lse is fp32 [Hq, Lq] (natural log), e.g. the global LSE of a mixed-segment
@@ -522,6 +556,23 @@ int uc_mask_scan(const uint8_t *keep, int64_t n, int32_t *dst_index, int64_t *to
  */
 int uc_compact_rows(const void *src, int64_t src_row_stride_bytes, int64_t row_bytes,
                     const int32_t *dst_index, int64_t n, void *dst, uc_stream_t stream);
+
+/*
+ * Several uc_compact_rows copies that share one dst_index (the K and V rows
+ * of a compaction) in one launch.  Copies whose pointers, stride and row size
+ * are not all multiples of 16 bytes, and any past the fourth, run as
+ * uc_compact_rows on the same stream.
+ * Replaces: key[keep] and value[keep] of TensorCacheStorageBackend.compact
+ * (tensor_backend.py:66-77) as one operation.
+ */
+typedef struct uc_row_copy {
+  const void *src;
+  int64_t src_row_stride_bytes, row_bytes;
+  void *dst;
+} uc_row_copy;
+
+int uc_compact_rows_multi(const uc_row_copy *copies, int n_copies, const int32_t *dst_index, int64_t n,
+                          uc_stream_t stream);
 
 /*
  * The inverse of uc_compact_rows: for every t with dst_index[t] >= 0, the

@@ -52,6 +52,21 @@ def test_compact_strided_rows(device):
     assert torch.equal(out.cpu(), base[:, 1:3][keep])
 
 
+def test_compact_many_tensors_one_call(device):
+    # six tensors of one mask: four 16-byte-aligned ones share one launch, the
+    # fifth aligned one and the 12-byte rows take the per-tensor kernels
+    g = torch.Generator().manual_seed(11)
+    n = 1500
+    tensors = [torch.randn(n, 4, 128, generator=g).to(torch.bfloat16), torch.randn(n, 2, 64, generator=g).half(),
+               torch.randn(n, 8, generator=g), torch.randint(0, 99, (n, 2), generator=g, dtype=torch.int64),
+               torch.randn(n, 16, generator=g).to(torch.bfloat16), torch.randn(n, 3, generator=g)]
+    keep = torch.rand(n, generator=g) < 0.4
+    outs = compact_rows([t.to(device) for t in tensors] + [None], keep.to(device))
+    assert outs[-1] is None
+    for t, o in zip(tensors, outs):
+        assert torch.equal(o.cpu(), t[keep])
+
+
 def test_compact_empty_cache(device):
     key = torch.zeros(0, 4, 128, dtype=torch.bfloat16, device=device)
     res = TensorCacheStorageBackend.compact(key=key, value=key.clone(), key_type_ids=None,

@@ -73,6 +73,64 @@ def test_config3_from_dense(device):
     assert parts[0].retained_tokens + parts[1].retained_tokens == 819
 
 
+# (tokens, target, recent, score kind): ties, NaN, the 8192-token limit of the
+# one-launch kernel, a recent-only budget, and a 9000-token segment that the
+# entry point hands to the per-segment kernels within the same call
+SEGMENTS = [(256, 51, 12, "ties"), (3840, 768, 192, "nan"), (8192, 1638, 409, "normal"), (40, 40, 40, "ties"),
+            (9000, 900, 100, "normal"), (1000, 300, 0, "ties")]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_select_gather_segments_one_call(device, dtype):
+    rng = np.random.default_rng(7)
+    specs, expected = [], []
+    for n, (tokens, target, recent, kind) in enumerate(SEGMENTS):
+        key, value = kv_pair(tokens, seed=40 + n, dtype=dtype)
+        if kind == "ties":
+            scores = rng.integers(0, 20, size=(4, tokens)).astype(np.float32)
+        else:
+            scores = rng.standard_normal((4, tokens)).astype(np.float32)
+        if kind == "nan":
+            scores[2, ::7] = np.nan
+        ids = np.arange(1000 * n, 1000 * n + tokens)
+        kd, vd = key.to(device), value.to(device)
+        if n == 5:  # a strided view of a larger buffer: token stride 2 * Hkv * D
+            kd = torch.repeat_interleave(kd, 2, dim=0)[::2]
+            vd = torch.repeat_interleave(vd, 2, dim=0)[::2]
+        specs.append(dict(key=kd, value=vd, logical_token_ids=torch.from_numpy(ids).to(device), token_type_id=n,
+                          per_kv_head_scores=torch.from_numpy(scores).to(device), target_tokens=target,
+                          recent_tokens=recent))
+        expected.append(H.from_dense(f32(key), f32(value), ids, scores, target, recent))
+    caches = GQAH2OCache.from_dense_segments(specs)
+    for n, (c, (ok, ov, oid, osc, heavy, rec)) in enumerate(zip(caches, expected)):
+        print(f"segment {n}: {SEGMENTS[n]}", flush=True)
+        assert np.array_equal(f32(c.key), ok) and np.array_equal(f32(c.value), ov)
+        assert np.array_equal(c.logical_token_ids.cpu().numpy(), oid)
+        assert np.array_equal(c.cumulative_scores.cpu().numpy(), osc, equal_nan=True)
+        assert (c.heavy_tokens, c.recent_tokens, c.token_type_id) == (heavy, rec, n)
+    # one segment per call gives the same caches
+    for spec, c in zip(specs, caches):
+        one = GQAH2OCache.from_dense(**spec)
+        assert torch.equal(one.key, c.key) and torch.equal(one.logical_token_ids, c.logical_token_ids)
+
+
+def test_select_gather_segments_mixed_shapes(device):
+    # segments of different head_dim run as separate groups of the same call
+    rng = np.random.default_rng(8)
+    specs, expected = [], []
+    for n, (tokens, d) in enumerate(((500, 64), (700, 128), (300, 64))):
+        key, value = kv_pair(tokens, head_dim=d, seed=60 + n)
+        scores = rng.random((4, tokens)).astype(np.float32)
+        ids = np.arange(tokens)
+        specs.append(dict(key=key.to(device), value=value.to(device), logical_token_ids=torch.from_numpy(ids).to(device),
+                          token_type_id=1, per_kv_head_scores=torch.from_numpy(scores).to(device),
+                          target_tokens=tokens // 5, recent_tokens=tokens // 20))
+        expected.append(H.from_dense(f32(key), f32(value), ids, scores, tokens // 5, tokens // 20))
+    for c, (ok, ov, oid, osc, _, _) in zip(GQAH2OCache.from_dense_segments(specs), expected):
+        assert np.array_equal(f32(c.key), ok) and np.array_equal(f32(c.value), ov)
+        assert np.array_equal(c.logical_token_ids.cpu().numpy(), oid)
+
+
 def test_scores_from_probs(device):
     rng = np.random.default_rng(4)
     probs = torch.from_numpy(rng.random((28, 16, 300)).astype(np.float32)).to(torch.bfloat16)

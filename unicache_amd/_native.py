@@ -67,6 +67,24 @@ class AppendEntry(ctypes.Structure):
     _fields_ = [("item", _L), ("advance", _L), ("ids", _P)]
 
 
+class H2OSegment(ctypes.Structure):
+    """Mirror of ``uc_h2o_segment``."""
+
+    _fields_ = [
+        ("key", _P), ("value", _P), ("k_st", _L), ("k_sh", _L), ("k_sd", _L),
+        ("scores", _P), ("s_sh", _L), ("s_st", _L),
+        ("ids", _P), ("ids_sh", _L), ("ids_st", _L),
+        ("tokens", _L), ("heavy_k", _L), ("recent", _L),
+        ("indices", _P), ("out_key", _P), ("out_value", _P), ("out_ids", _P), ("out_scores", _P),
+    ]
+
+
+class RowCopy(ctypes.Structure):
+    """Mirror of ``uc_row_copy``."""
+
+    _fields_ = [("src", _P), ("src_row_stride_bytes", _L), ("row_bytes", _L), ("dst", _P)]
+
+
 class MqQuery(ctypes.Structure):
     """Mirror of ``uc_mq_query``."""
 
@@ -162,6 +180,8 @@ _SIGNATURES = {
     "uc_scatter_rows": (_I, [_P, _L, _P, _L, _P, _L, _P]),
     "uc_copy_spans": (_I, [_P, _I, _P]),
     "uc_kivi_residual_append": (_I, [_P, _P, _I, _P, _P, _P, _L, _L, _L, _I, _P]),
+    "uc_compact_rows_multi": (_I, [ctypes.POINTER(RowCopy), _I, _P, _L, _P]),
+    "uc_h2o_select_gather_segments": (_I, [ctypes.POINTER(H2OSegment), _I, _I, _L, _L, _P]),
     "uc_h2o_select_gather": (
         _I,
         [_P, _P, _L, _L, _L, _I, _L, _L, _L, _P, _L, _L, _L, _L, _P, _L, _L, _P, _P, _P, _P, _P, _P],

@@ -112,6 +112,26 @@ int launch_scatter(const void *src, int64_t row_bytes, const int32_t *dst_index,
   return check_launch("uc_scatter_rows");
 }
 
+// Several uc_compact_rows copies that share dst_index in one launch:
+// blockIdx.y selects the copy, 16-byte chunks.
+constexpr int kMaxRowCopies = 4;
+struct RowCopies {
+  uc_row_copy c[kMaxRowCopies];
+  int64_t per_row[kMaxRowCopies];
+};
+
+__global__ __launch_bounds__(256) void compact_rows_multi_kernel(RowCopies a, const int32_t *dst_index, int64_t n) {
+  const uc_row_copy &c = a.c[blockIdx.y];
+  const int64_t per_row = a.per_row[blockIdx.y];
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t t = idx / per_row, k = idx % per_row;
+  if (t >= n) return;
+  const int32_t d = dst_index[t];
+  if (d < 0) return;
+  const uint4 v = *reinterpret_cast<const uint4 *>(static_cast<const char *>(c.src) + t * c.src_row_stride_bytes + k * 16);
+  *reinterpret_cast<uint4 *>(static_cast<char *>(c.dst) + int64_t(d) * c.row_bytes + k * 16) = v;
+}
+
 template <typename V>
 int launch_compact(const void *src, int64_t src_stride, int64_t row_bytes, const int32_t *dst_index, int64_t n,
                    void *dst, hipStream_t s) {
@@ -224,4 +244,36 @@ extern "C" int uc_copy_spans(const uc_copy_span *spans_host, int n, uc_stream_t 
   hipLaunchKernelGGL(copy_spans_kernel, dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(n)), dim3(256), 0,
                      as_stream(stream), c);
   return check_launch("uc_copy_spans");
+}
+
+extern "C" int uc_compact_rows_multi(const uc_row_copy *copies, int n_copies, const int32_t *dst_index, int64_t n,
+                                     uc_stream_t stream) {
+  clear_error();
+  UC_REQUIRE(n_copies >= 0 && (n_copies == 0 || copies != nullptr) && n >= 0, "uc_compact_rows_multi: bad arguments");
+  if (n == 0 || n_copies == 0) return UC_OK;
+  UC_REQUIRE(dst_index != nullptr, "uc_compact_rows_multi: null pointer");
+  RowCopies a{};
+  int m = 0;
+  int64_t most = 0;
+  for (int i = 0; i < n_copies; ++i) {
+    const uc_row_copy &c = copies[i];
+    UC_REQUIRE(c.row_bytes >= 0 && c.src_row_stride_bytes >= c.row_bytes, "uc_compact_rows_multi: bad shape");
+    if (c.row_bytes == 0) continue;
+    UC_REQUIRE(c.src != nullptr && c.dst != nullptr, "uc_compact_rows_multi: null pointer");
+    const uintptr_t align = reinterpret_cast<uintptr_t>(c.src) | reinterpret_cast<uintptr_t>(c.dst) |
+                            static_cast<uintptr_t>(c.src_row_stride_bytes) | static_cast<uintptr_t>(c.row_bytes);
+    if ((align & 15) != 0 || m == kMaxRowCopies) {  // its own launch, the widest access its alignment allows
+      const int rc = uc_compact_rows(c.src, c.src_row_stride_bytes, c.row_bytes, dst_index, n, c.dst, stream);
+      if (rc != UC_OK) return rc;
+      continue;
+    }
+    a.c[m] = c;
+    a.per_row[m] = c.row_bytes / 16;
+    most = a.per_row[m] > most ? a.per_row[m] : most;
+    ++m;
+  }
+  if (m == 0) return UC_OK;
+  const dim3 grid(static_cast<unsigned>(ceil_div(n * most, int64_t(256))), static_cast<unsigned>(m));
+  hipLaunchKernelGGL(compact_rows_multi_kernel, grid, dim3(256), 0, as_stream(stream), a, dst_index, n);
+  return check_launch("uc_compact_rows_multi");
 }

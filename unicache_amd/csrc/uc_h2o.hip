@@ -430,6 +430,153 @@ __global__ __launch_bounds__(256) void gqa_gather_kernel(GatherArgs a) {
   }
 }
 
+
+// --------------------------------------- select + gather of several segments --
+// One launch for up to kSgMaxSegs H2O segments (uc_h2o_segment each).  A
+// workgroup serves (segment, KV head, part): it selects the head's kept tokens
+// itself -- the parts of a head repeat the selection, which costs far less
+// than a second launch -- and gathers its part of the kept rows.
+//
+// Selection.  The heavy_k-th largest order key th is found bit pair by bit
+// pair from the top: with th's higher bits fixed, the block counts the keys
+// >= th | 1 << b, th | 2 << b and th | 3 << b (three counts packed in one
+// word, summed over a wave by shuffles and over the 16 waves through LDS, one
+// barrier per pair) and keeps the largest candidate that still has heavy_k
+// keys at or above it.  Keys above th are all kept; keys equal to th are kept
+// in ascending token order until heavy_k are chosen (torch.topk's tie rule as
+// the reference applies it, physical.py:516-527).  A token's place in the
+// ascending output is (#kept-above before it) + min(#equal before it, need):
+// one block scan of per-(chunk, wave) counts gives both prefixes.  The recent
+// window follows (physical.py:528-531).
+constexpr int kSgMaxSegs = 8;
+constexpr int kSgThreads = 1024;
+constexpr int kSgWaves = kSgThreads / kWave;
+constexpr int kSgRegs = 8;                          // keys per thread: history <= 8192 tokens
+constexpr int kSgMaxKeep = kSgThreads * kSgRegs;    // kept rows held in LDS
+
+struct SgArgs {
+  uc_h2o_segment seg[kSgMaxSegs];
+  int wg_begin[kSgMaxSegs + 1];  // first workgroup of each segment
+  int parts[kSgMaxSegs];         // workgroups per KV head
+  int64_t Hkv, D;
+};
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__global__ __launch_bounds__(kSgThreads) void h2o_select_gather_kernel(SgArgs a) {
+  __shared__ uint32_t cnt[2][kSgWaves];
+  __shared__ uint32_t tab[2][kSgRegs * kSgWaves];  // gt / eq counts per (chunk, wave), then prefixes
+  __shared__ uint32_t totals[2];
+  __shared__ int32_t keep[kSgMaxKeep];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  int si = 0;
+  while (si + 1 < kSgMaxSegs && int(blockIdx.x) >= a.wg_begin[si + 1]) ++si;
+  const uc_h2o_segment &g = a.seg[si];
+  const int local = int(blockIdx.x) - a.wg_begin[si];
+  const int64_t h = local / a.parts[si];
+  const int part = local % a.parts[si];
+  const int64_t hist_end = g.tokens - g.recent, R = g.heavy_k + g.recent;
+  const uint32_t heavy = uint32_t(g.heavy_k);
+  const float *sc = g.scores + h * g.s_sh;
+
+  if (heavy > 0) {
+    uint32_t keys[kSgRegs];
+#pragma unroll
+    for (int r = 0; r < kSgRegs; ++r) {
+      const int64_t t = int64_t(r) * kSgThreads + tid;
+      keys[r] = t < hist_end ? order_key(sc[t * g.s_st]) : 0u;  // order keys of real scores are never 0
+    }
+    uint32_t th = 0;
+    for (int it = 0; it < 16; ++it) {
+      const int b = 30 - 2 * it;
+      const uint32_t c1 = th | (1u << b), c2 = th | (2u << b), c3 = th | (3u << b);
+      uint32_t n = 0;  // three counts of at most 8 per thread, 512 per wave: 10 bits each
+#pragma unroll
+      for (int r = 0; r < kSgRegs; ++r)
+        n += uint32_t(keys[r] >= c1) + (uint32_t(keys[r] >= c2) << 10) + (uint32_t(keys[r] >= c3) << 20);
+      n = wave_sum_u32(n);
+      if (lane == 0) cnt[it & 1][wave] = n;
+      __syncthreads();
+      uint32_t s1 = 0, s2 = 0, s3 = 0;
+#pragma unroll
+      for (int w = 0; w < kSgWaves; ++w) {
+        const uint32_t v = cnt[it & 1][w];
+        s1 += v & 1023u;
+        s2 += (v >> 10) & 1023u;
+        s3 += v >> 20;
+      }
+      th = s3 >= heavy ? c3 : s2 >= heavy ? c2 : s1 >= heavy ? c1 : th;
+    }
+    // per (chunk, wave) counts of keys above / equal to th
+    uint64_t gt_ball[kSgRegs], eq_ball[kSgRegs];
+#pragma unroll
+    for (int r = 0; r < kSgRegs; ++r) {
+      const bool ok = int64_t(r) * kSgThreads + tid < hist_end;
+      gt_ball[r] = __ballot(ok && keys[r] > th);
+      eq_ball[r] = __ballot(ok && keys[r] == th);
+      if (lane == 0) {
+        tab[0][r * kSgWaves + wave] = __popcll(gt_ball[r]);
+        tab[1][r * kSgWaves + wave] = __popcll(eq_ball[r]);
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {  // exclusive scans of the 128 (chunk, wave) counts, chunk-major
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const uint32_t x0 = tab[k][2 * lane], x1 = tab[k][2 * lane + 1];
+        uint32_t incl = x0 + x1;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t y = __shfl_up(incl, o, kWave);
+          if (lane >= o) incl += y;
+        }
+        const uint32_t excl = incl - x0 - x1;
+        tab[k][2 * lane] = excl;
+        tab[k][2 * lane + 1] = excl + x0;
+        if (lane == kWave - 1) totals[k] = incl;
+      }
+    }
+    __syncthreads();
+    const uint32_t need = heavy - totals[0];  // equal keys to keep, lowest tokens first
+    const uint64_t below = (uint64_t(1) << lane) - 1u;
+#pragma unroll
+    for (int r = 0; r < kSgRegs; ++r) {
+      const bool gt = (gt_ball[r] >> lane) & 1u, eq = (eq_ball[r] >> lane) & 1u;
+      if (!gt && !eq) continue;
+      const uint32_t gb = tab[0][r * kSgWaves + wave] + __popcll(gt_ball[r] & below);
+      const uint32_t eb = tab[1][r * kSgWaves + wave] + __popcll(eq_ball[r] & below);
+      if (gt || eb < need) keep[gb + (eb < need ? eb : need)] = r * kSgThreads + tid;
+    }
+  }
+  for (int64_t k = tid; k < g.recent; k += kSgThreads) keep[g.heavy_k + k] = int32_t(hist_end + k);
+  __syncthreads();
+
+  // gather this part's rows: 16-byte chunks of the K and V rows
+  const int64_t per = (R + a.parts[si] - 1) / a.parts[si];
+  const int64_t j0 = part * per, j1 = j0 + per < R ? j0 + per : R;
+  const int chunks = int(a.D / 8);  // 16-byte chunks per 16-bit row
+  const int rows_per = kSgThreads / chunks;
+  const int c = tid % chunks;
+  for (int64_t j = j0 + tid / chunks; j < j1; j += rows_per) {
+    const int64_t r = keep[j];
+    const int64_t src = r * g.k_st + h * g.k_sh + int64_t(c) * 8, dst = (h * R + j) * a.D + int64_t(c) * 8;
+    const uint4 kv = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g.key) + src);
+    const uint4 vv = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g.value) + src);
+    *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(g.out_key) + dst) = kv;
+    *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(g.out_value) + dst) = vv;
+  }
+  for (int64_t j = j0 + tid; j < j1; j += kSgThreads) {
+    const int64_t r = keep[j];
+    g.indices[h * R + j] = r;
+    if (g.out_ids) g.out_ids[h * R + j] = g.ids[h * g.ids_sh + r * g.ids_st];
+    if (g.out_scores) g.out_scores[h * R + j] = sc[r * g.s_st];
+  }
+}
+
 }  // namespace
 }  // namespace uc
 
@@ -582,4 +729,53 @@ extern "C" int uc_h2o_select_gather(const void *key, const void *value, int64_t 
   if (rc != UC_OK) return rc;
   return uc_gqa_gather(key, value, k_st, k_sh, k_sd, dtype, heads_kv, head_dim, indices, heavy_k + recent, ids,
                        ids_sh, ids_st, scores, s_sh, s_st, out_key, out_value, out_ids, out_scores, stream);
+}
+
+extern "C" int uc_h2o_select_gather_segments(const uc_h2o_segment *segments, int n_segments, int dtype,
+                                             int64_t heads_kv, int64_t head_dim, uc_stream_t stream) {
+  UC_REQUIRE(valid_dtype(dtype), "uc_h2o_select_gather_segments: unknown dtype code");
+  UC_REQUIRE(n_segments >= 0 && (n_segments == 0 || segments != nullptr),
+             "uc_h2o_select_gather_segments: segments is NULL");
+  UC_REQUIRE(heads_kv > 0 && head_dim > 0, "uc_h2o_select_gather_segments: bad shape");
+  SgArgs a{};
+  a.Hkv = heads_kv;
+  a.D = head_dim;
+  int n = 0, wg = 0;
+  const int64_t el = dtype == UC_FP32 ? 4 : 2;
+  for (int i = 0; i < n_segments; ++i) {
+    const uc_h2o_segment &g = segments[i];
+    UC_REQUIRE(g.scores != nullptr && g.indices != nullptr && g.key != nullptr && g.value != nullptr,
+               "uc_h2o_select_gather_segments: segment %d lacks scores, indices, key or value", i);
+    UC_REQUIRE((g.ids == nullptr) == (g.out_ids == nullptr),
+               "uc_h2o_select_gather_segments: ids and out_ids go together (segment %d)", i);
+    UC_REQUIRE(g.tokens >= 0 && g.heavy_k >= 0 && g.recent >= 0 && g.recent <= g.tokens &&
+                   g.heavy_k <= g.tokens - g.recent,
+               "uc_h2o_select_gather_segments: heavy_k + recent exceeds the token count (segment %d)", i);
+    const int64_t R = g.heavy_k + g.recent;
+    if (R == 0) continue;
+    // one launch takes 16-bit rows read as 16-byte chunks and a history of at
+    // most kSgMaxKeep tokens; other segments run as uc_h2o_select_gather
+    const bool fits = el == 2 && head_dim % 8 == 0 && g.k_sd == 1 && g.k_st % 8 == 0 && g.k_sh % 8 == 0 &&
+                      (reinterpret_cast<uintptr_t>(g.key) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(g.value) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(g.out_key) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(g.out_value) & 15) == 0 && g.tokens <= kSgMaxKeep &&
+                      n < kSgMaxSegs;
+    if (!fits) {
+      const int rc = uc_h2o_select_gather(g.key, g.value, g.k_st, g.k_sh, g.k_sd, dtype, heads_kv, g.tokens, head_dim,
+                                          g.scores, g.s_sh, g.s_st, g.heavy_k, g.recent, g.ids, g.ids_sh, g.ids_st,
+                                          g.indices, g.out_key, g.out_value, g.out_ids, g.out_scores, stream);
+      if (rc != UC_OK) return rc;
+      continue;
+    }
+    a.seg[n] = g;
+    a.parts[n] = int(R > 16 * 128 ? 16 : (R + 127) / 128);
+    a.wg_begin[n] = wg;
+    wg += int(heads_kv) * a.parts[n];
+    ++n;
+  }
+  if (n == 0) return UC_OK;
+  for (int i = n; i <= kSgMaxSegs; ++i) a.wg_begin[i] = wg;
+  hipLaunchKernelGGL(h2o_select_gather_kernel, dim3(wg), dim3(kSgThreads), 0, as_stream(stream), a);
+  return check_launch("uc_h2o_select_gather_segments");
 }

@@ -1009,6 +1009,70 @@ class GQAH2OCache:
         recent_tokens: int,
         selection_frozen: bool = False,
     ) -> "GQAH2OCache":
+        """Select and gather one segment (physical.py:499-557)."""
+
+        return cls.from_dense_segments([dict(
+            key=key, value=value, logical_token_ids=logical_token_ids, token_type_id=token_type_id,
+            per_kv_head_scores=per_kv_head_scores, target_tokens=target_tokens, recent_tokens=recent_tokens,
+            selection_frozen=selection_frozen)])[0]
+
+    @classmethod
+    def from_dense_segments(cls, segments: list) -> list:
+        """``from_dense`` for several segments -- each a dict of its keyword
+        arguments plus ``key`` and ``value`` -- with one allocation and one
+        uc_h2o_select_gather_segments launch for all of them (segments that
+        share dtype, KV heads and head_dim; others are grouped by shape).
+        Results equal one ``from_dense`` call per segment."""
+
+        prepared = [cls._prepare(**seg) for seg in segments]
+        out: list = [None] * len(prepared)
+        groups: dict = {}
+        for i, p in enumerate(prepared):
+            groups.setdefault((p["key"].dtype, p["key"].device, p["kv_heads"], p["head_dim"]), []).append(i)
+        for (dtype, device, kv_heads, head_dim), idx in groups.items():
+            specs = []
+            for i in idx:
+                r = prepared[i]["retained"]
+                specs += [((kv_heads, r), torch.int64), ((kv_heads, r, head_dim), dtype),
+                          ((kv_heads, r, head_dim), dtype), ((kv_heads, r), torch.int64),
+                          ((kv_heads, r), torch.float32)]
+            views = _carve(specs, device)
+            table = (nat.H2OSegment * len(idx))()
+            for n, i in enumerate(idx):
+                p = prepared[i]
+                index, out_key, out_value, out_ids, out_scores = views[5 * n:5 * n + 5]
+                key, scores, ids64 = p["key"], p["scores"], p["ids64"]
+                table[n] = nat.H2OSegment(
+                    key.data_ptr(), p["value"].data_ptr(), *map(int, key.stride()), scores.data_ptr(),
+                    *map(int, scores.stride()), ids64.data_ptr(), 0, int(ids64.stride(0)), p["tokens"],
+                    p["heavy_k"], p["recent"], index.data_ptr(), out_key.data_ptr(), out_value.data_ptr(),
+                    out_ids.data_ptr(), out_scores.data_ptr())
+                p["outputs"] = (out_key, out_value, out_ids, out_scores)
+            nat.call("uc_h2o_select_gather_segments", table, len(idx), nat.dtype_code(dtype), kv_heads, head_dim,
+                     nat.stream(device))
+            for i in idx:
+                p = prepared[i]
+                out_key, out_value, out_ids, out_scores = p["outputs"]
+                if p["ids_dtype"] != torch.int64:
+                    out_ids = out_ids.to(p["ids_dtype"])
+                out[i] = cls(
+                    key=out_key,
+                    value=out_value,
+                    logical_token_ids=out_ids,
+                    cumulative_scores=out_scores,
+                    token_type_id=int(p["token_type_id"]),
+                    original_tokens=p["tokens"],
+                    heavy_tokens=p["heavy"],
+                    recent_tokens=p["recent"],
+                    selection_frozen=bool(p["selection_frozen"]),
+                )
+        return out
+
+    @staticmethod
+    def _prepare(*, key, value, logical_token_ids, token_type_id, per_kv_head_scores, target_tokens, recent_tokens,
+                 selection_frozen=False) -> dict:
+        """Checks and budget arithmetic of one segment (physical.py:499-515)."""
+
         if key.shape != value.shape or key.dim() != 3:
             raise ValueError("Physical H2O expects matching [tokens, kv_heads, head_dim] tensors")
         tokens, kv_heads, head_dim = map(int, key.shape)
@@ -1031,31 +1095,9 @@ class GQAH2OCache:
         if scores.dtype != torch.float32:
             scores = scores.float()
         ids64 = logical if logical.dtype == torch.int64 else logical.to(torch.int64)
-        # selection and gather in one call, into one allocation
-        retained = heavy_k + recent
-        index, out_key, out_value, out_ids, out_scores = _carve(
-            [((kv_heads, retained), torch.int64), ((kv_heads, retained, head_dim), key.dtype),
-             ((kv_heads, retained, head_dim), key.dtype), ((kv_heads, retained), torch.int64),
-             ((kv_heads, retained), torch.float32)], device)
-        nat.call(
-            "uc_h2o_select_gather", key.data_ptr(), value.data_ptr(), *map(int, key.stride()),
-            nat.dtype_code(key.dtype), kv_heads, tokens, head_dim, scores.data_ptr(), *map(int, scores.stride()),
-            heavy_k, recent, ids64.data_ptr(), 0, int(ids64.stride(0)), index.data_ptr(), out_key.data_ptr(),
-            out_value.data_ptr(), out_ids.data_ptr(), out_scores.data_ptr(), nat.stream(device),
-        )
-        if logical.dtype != torch.int64:
-            out_ids = out_ids.to(logical.dtype)
-        return cls(
-            key=out_key,
-            value=out_value,
-            logical_token_ids=out_ids,
-            cumulative_scores=out_scores,
-            token_type_id=int(token_type_id),
-            original_tokens=tokens,
-            heavy_tokens=heavy,
-            recent_tokens=recent,
-            selection_frozen=bool(selection_frozen),
-        )
+        return dict(key=key, value=value, scores=scores, ids64=ids64, ids_dtype=logical.dtype, tokens=tokens,
+                    kv_heads=kv_heads, head_dim=head_dim, heavy=heavy, heavy_k=heavy_k, recent=recent,
+                    retained=heavy_k + recent, token_type_id=token_type_id, selection_frozen=selection_frozen)
 
     @property
     def num_kv_heads(self) -> int:

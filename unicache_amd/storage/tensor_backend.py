@@ -50,7 +50,7 @@ def _scan(mask: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
     n = int(mask.numel())
     dst = torch.empty(n, dtype=torch.int32, device=mask.device)
-    total = torch.zeros(1, dtype=torch.int64, device=mask.device)
+    total = torch.empty(1, dtype=torch.int64, device=mask.device)  # the scan always writes it
     nat.call("uc_mask_scan", mask.data_ptr(), n, dst.data_ptr(), total.data_ptr(), nat.stream(mask.device))
     return dst, total
 
@@ -72,6 +72,32 @@ def _copy_rows(src: torch.Tensor, dst: torch.Tensor, kept: int) -> torch.Tensor:
     return out
 
 
+def _copy_rows_many(srcs: list[torch.Tensor | None], dst: torch.Tensor, kept: int) -> list[torch.Tensor | None]:
+    """_copy_rows for several tensors through one uc_compact_rows_multi call
+    (one launch for the 16-byte-aligned ones)."""
+
+    n = int(dst.numel())
+    outs: list[torch.Tensor | None] = []
+    copies = []
+    for src in srcs:
+        if src is None:
+            outs.append(None)
+            continue
+        if int(src.shape[0]) != n:
+            raise ValueError("Keep mask does not match the cache token count")
+        if n and not src[0].is_contiguous():
+            src = src.contiguous()
+        out = torch.empty((kept, *src.shape[1:]), dtype=src.dtype, device=dst.device)
+        outs.append(out)
+        if kept:
+            copies.append(nat.RowCopy(src.data_ptr(), int(src.stride(0)) * src.element_size(),
+                                      int(src[0].numel()) * src.element_size(), out.data_ptr()))
+    if copies:
+        nat.call("uc_compact_rows_multi", (nat.RowCopy * len(copies))(*copies), len(copies), dst.data_ptr(), n,
+                 nat.stream(dst.device))
+    return outs
+
+
 def compact_rows(tensors: list[torch.Tensor | None], keep: torch.Tensor,
                  kept: int | None = None) -> list[torch.Tensor | None]:
     """tensor[keep] for every tensor (rows along dim 0), in order, on the HIP
@@ -83,7 +109,7 @@ def compact_rows(tensors: list[torch.Tensor | None], keep: torch.Tensor,
     dst, total = _scan(mask)
     if kept is None:
         kept = int(total.item()) if mask.numel() else 0
-    return [None if t is None else _copy_rows(t, dst, int(kept)) for t in tensors]
+    return _copy_rows_many(tensors, dst, int(kept))
 
 
 # --------------------------------------------------------------- results --
@@ -231,8 +257,7 @@ class TensorCacheStorageBackend:
         mask = _aligned_mask(masks[0], device)
         dst, total = _scan(mask)
         kept = int(total.item()) if mask.numel() else 0
-        compacted_key, compacted_value, compacted_types = (
-            None if t is None else _copy_rows(t, dst, kept) for t in (key, value, key_type_ids))
+        compacted_key, compacted_value, compacted_types = _copy_rows_many([key, value, key_type_ids], dst, kept)
         return CacheMutationResult(
             key=compacted_key,
             value=compacted_value,
@@ -320,8 +345,11 @@ class TensorCacheStorageBackend:
                         row.span is not None or vals[row.count_slot] > 0):
                     raise ValueError("Physical H2O request is missing per-KV-head scores")
 
-        # 4. segments, then the dense remainder
+        # 4. segments, then the dense remainder; the H2O segments of every
+        # sample are selected and gathered together in one launch
         physical_by_sample: list[list[Any]] = []
+        h2o_specs: list[dict] = []
+        h2o_slots: list[tuple[int, int]] = []
         for s, rows in enumerate(planned):
             sample_key = key[offsets[s]:offsets[s + 1]]
             sample_value = value[offsets[s]:offsets[s + 1]]
@@ -333,8 +361,16 @@ class TensorCacheStorageBackend:
                 type_id = row.type_id
                 if type_id < 0 and row.type_slot >= 0 and vals[row.type_slot] == vals[row.type_slot + 1]:
                     type_id = vals[row.type_slot]
-                segments.append(_build_segment(row, sample_key, sample_value, lengths[s], count, type_id))
+                built = _build_segment(row, sample_key, sample_value, lengths[s], count, type_id)
+                if isinstance(built, dict):  # an H2O segment, built below with the others
+                    h2o_slots.append((s, len(segments)))
+                    h2o_specs.append(built)
+                    built = None
+                segments.append(built)
             physical_by_sample.append(segments)
+        if h2o_specs:
+            for (s, j), cache in zip(h2o_slots, GQAH2OCache.from_dense_segments(h2o_specs)):
+                physical_by_sample[s][j] = cache
         for s, keep in enumerate(new_masks):
             if keep_masks[s].device == keep.device and keep_masks[s].dtype == torch.bool:
                 keep_masks[s].copy_(keep)
@@ -348,7 +384,9 @@ class TensorCacheStorageBackend:
 
 def _build_segment(row: _Planned, sample_key, sample_value, length: int, count: int, type_id: int):
     """The physical segment of one request: rows by view (token span) or by
-    one mask scan and row copies, then the KIVI pack or H2O selection."""
+    one mask scan and row copies, then the KIVI pack; for an H2O request the
+    keyword arguments of its GQAH2OCache.from_dense, which the caller builds
+    together with the call's other H2O segments."""
 
     request, device = row.request, sample_key.device
     scores = None
@@ -364,9 +402,7 @@ def _build_segment(row: _Planned, sample_key, sample_value, length: int, count: 
         mask = _aligned_mask(row.mask, device)
         dst, _ = _scan(mask)
         positions = torch.arange(length, device=device, dtype=torch.int64)
-        dense_key = _copy_rows(sample_key, dst, count)
-        dense_value = _copy_rows(sample_value, dst, count)
-        logical_ids = _copy_rows(positions, dst, count)
+        dense_key, dense_value, logical_ids = _copy_rows_many([sample_key, sample_value, positions], dst, count)
         if scores is not None:
             scores = _copy_rows(scores.t(), dst, count).t()
     params = request.params
@@ -380,8 +416,8 @@ def _build_segment(row: _Planned, sample_key, sample_value, length: int, count: 
             backend=str(params.get("backend", "reference")),
         )
     target, recent = h2o_budget(count, params)
-    return GQAH2OCache.from_dense(
-        dense_key, dense_value, logical_token_ids=logical_ids, token_type_id=type_id,
-        per_kv_head_scores=scores, target_tokens=target, recent_tokens=recent,
-        selection_frozen=bool(params.get("selection_frozen", False)),
-    )
+    # GQAH2OCache.from_dense's arguments (physical.py:493-547): the caller
+    # builds every H2O segment of the call with one from_dense_segments
+    return dict(key=dense_key, value=dense_value, logical_token_ids=logical_ids, token_type_id=type_id,
+                per_kv_head_scores=scores, target_tokens=target, recent_tokens=recent,
+                selection_frozen=bool(params.get("selection_frozen", False)))
