@@ -120,15 +120,9 @@ __device__ void pack_key_group(const void *__restrict__ key, int64_t st, int64_t
 // One lane owns 16 consecutive channels of one (head, token); a value group
 // of G channels spans G/16 neighbouring lanes, reduced with shuffles.  The 16
 // codes of a lane form exactly one 2-bit word / two 4-bit words.
-template <int IN, int BITS, int G, bool VEC>
-__device__ void pack_value_chunk(const void *__restrict__ value, int64_t st, int64_t sh, int64_t sd,
-                                 int64_t h, int64_t t, int64_t chunk, bool active,
-                                 void *__restrict__ code, int64_t vc_sh, int64_t vc_st, int64_t vc_sw,
-                                 void *__restrict__ vscale, void *__restrict__ vmin, int stats_dtype,
-                                 int64_t vs_sh, int64_t vs_st, int64_t vs_sg) {
-  constexpr float kMaxCode = float((1 << BITS) - 1);
-  constexpr int kLanesPerGroup = G / 16;
-  float x[16];
+template <int IN, bool VEC>
+__device__ __forceinline__ void load_value_chunk(const void *__restrict__ value, int64_t st, int64_t sh, int64_t sd,
+                                                 int64_t h, int64_t t, int64_t chunk, bool active, float (&x)[16]) {
   if (active) {
     const int64_t base = t * st + h * sh + chunk * 16 * sd;
     if constexpr (VEC) {
@@ -148,6 +142,16 @@ __device__ void pack_value_chunk(const void *__restrict__ value, int64_t st, int
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = 0.0f;
   }
+}
+
+template <int BITS, int G>
+__device__ __forceinline__ void quant_value_chunk(const float (&x)[16], int64_t h, int64_t t, int64_t chunk,
+                                                  bool active, void *__restrict__ code, int64_t vc_sh,
+                                                  int64_t vc_st, int64_t vc_sw, void *__restrict__ vscale,
+                                                  void *__restrict__ vmin, int stats_dtype, int64_t vs_sh,
+                                                  int64_t vs_st, int64_t vs_sg) {
+  constexpr float kMaxCode = float((1 << BITS) - 1);
+  constexpr int kLanesPerGroup = G / 16;
   GroupRange r;
   r.init(x[0]);
 #pragma unroll
@@ -234,7 +238,11 @@ __device__ __forceinline__ void pack_key_block(const PackArgs &a, int64_t block)
                                    a.ks_sg);
 }
 
-// wave -> (head, run of tokens); lane -> (token in run, 16-channel chunk)
+// wave -> (head, kVRuns consecutive runs of tokens); lane -> (token in run,
+// 16-channel chunk).  The loads of all the wave's runs are issued before any
+// run is quantized.
+constexpr int kVRuns = 2;
+
 template <int IN, int VB, int G, bool VEC>
 __device__ __forceinline__ void pack_value_block(const PackArgs &a, int64_t block) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -243,13 +251,22 @@ __device__ __forceinline__ void pack_value_block(const PackArgs &a, int64_t bloc
   const int64_t lanes_per_token = a.head_dim / 16;
   const int64_t tokens_per_wave = kWave / lanes_per_token;
   const int64_t runs = (a.tokens + tokens_per_wave - 1) / tokens_per_wave;
-  const int64_t h = vw / runs;
-  const int64_t t = (vw % runs) * tokens_per_wave + lane / lanes_per_token;
+  const int64_t groups = (runs + kVRuns - 1) / kVRuns;
+  const int64_t h = vw / groups;
   const int64_t chunk = lane % lanes_per_token;
-  const bool active = (lane < tokens_per_wave * lanes_per_token) && t < a.tokens;
-  pack_value_chunk<IN, VB, G, VEC>(a.value, a.v_st, a.v_sh, a.v_sd, h, t, chunk, active, a.value_code, a.vc_sh,
-                                   a.vc_st, a.vc_sw, a.value_scale, a.value_min, a.stats_dtype, a.vs_sh, a.vs_st,
-                                   a.vs_sg);
+  int64_t t[kVRuns];
+  bool active[kVRuns];
+  float x[kVRuns][16];
+#pragma unroll
+  for (int k = 0; k < kVRuns; ++k) {
+    t[k] = ((vw % groups) * kVRuns + k) * tokens_per_wave + lane / lanes_per_token;
+    active[k] = (lane < tokens_per_wave * lanes_per_token) && t[k] < a.tokens;
+    load_value_chunk<IN, VEC>(a.value, a.v_st, a.v_sh, a.v_sd, h, t[k], chunk, active[k], x[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < kVRuns; ++k)
+    quant_value_chunk<VB, G>(x[k], h, t[k], chunk, active[k], a.value_code, a.vc_sh, a.vc_st, a.vc_sw,
+                             a.value_scale, a.value_min, a.stats_dtype, a.vs_sh, a.vs_st, a.vs_sg);
 }
 
 template <int IN, int KB, int G, bool VEC>
@@ -752,7 +769,7 @@ extern "C" int uc_kivi_pack(const void *key, int64_t k_st, int64_t k_sh, int64_t
   a.key_waves = key ? heads * (tokens / group_size) * slabs : 0;
   const int64_t lanes_per_token = head_dim / 16;
   const int64_t tokens_per_wave = kWave / lanes_per_token;
-  a.value_waves = value ? heads * ((tokens + tokens_per_wave - 1) / tokens_per_wave) : 0;
+  a.value_waves = value ? heads * ceil_div(ceil_div(tokens, tokens_per_wave), int64_t(kVRuns)) : 0;
   const bool half = half_dtype(in_dtype);
   const bool kvec = half && k_sd == 1 && (k_st % 2 == 0) && (k_sh % 2 == 0) && aligned(key, 4);
   const bool vvec = half && v_sd == 1 && (v_st % 8 == 0) && (v_sh % 8 == 0) && aligned(value, 16);

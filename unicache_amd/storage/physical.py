@@ -289,6 +289,11 @@ def _pack_native(key: torch.Tensor, value: torch.Tensor, *, k_bits: int, v_bits:
     capacity = tokens if capacity is None else int(capacity)
     if capacity < tokens or capacity % group_size:
         raise ValueError("KIVI packed capacity must be a multiple of group_size covering the tokens")
+    if capacity == tokens:  # the views of the whole storage: one view op per tensor
+        views, ptrs, _ = _native_block(capacity, heads, head_dim, k_bits, v_bits, group_size, device)
+        _pack_native_at(ptrs, capacity, 0, key, value, k_bits=k_bits, v_bits=v_bits, group_size=group_size,
+                        tokens=None, stream=nat.stream(device))
+        return views
     storage = _native_storage(capacity, heads, head_dim, k_bits, v_bits, group_size, device)
     _pack_native_into(storage, 0, key, value, k_bits=k_bits, v_bits=v_bits, group_size=group_size)
     return _native_views(storage, tokens, k_bits, group_size)
