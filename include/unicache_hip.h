@@ -575,6 +575,19 @@ int uc_compact_rows_multi(const uc_row_copy *copies, int n_copies, const int32_t
                           uc_stream_t stream);
 
 /*
+ * The rows KIVIQuantizationOperator.execute fake-quantizes, in one launch:
+ * segment tokens (bool bytes) except the last residual_length of them and,
+ * with preserve_protected, the protected ones; none with bypass.  Writes
+ * dst_index [n] (row in the compact order, or -1), src_index [selected] (the
+ * inverse) and counts [3] = (segment tokens, selected tokens, protected
+ * segment tokens), all on the device.
+ * Replaces: the mask arithmetic and counts of operators/builtin.py:394-410.
+ */
+int uc_fake_quant_mask(const uint8_t *segment, const uint8_t *protected_mask, int64_t n, int64_t residual_length,
+                       int preserve_protected, int bypass, int32_t *dst_index, int32_t *src_index, int64_t *counts,
+                       uc_stream_t stream);
+
+/*
  * The inverse of uc_compact_rows: for every t with dst_index[t] >= 0, the
  * compact row dst_index[t] of src (row_bytes each) is copied to out + t *
  * out_row_stride_bytes; other rows of out are left as they are.

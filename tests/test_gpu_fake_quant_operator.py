@@ -81,3 +81,50 @@ def test_bypass_and_whole_segment_residual(device):
     ek, ev, n = _expected(key, value, seg.numpy(), prot.numpy(), bits=4, group=32, residual=0, preserve=False)
     assert n == 64 and records[0]["protected_tokens_preserved"] == 0
     assert np.array_equal(f32(ctx.k), ek) and np.array_equal(f32(ctx.v), ev)
+
+
+@pytest.mark.parametrize("n,residual,preserve,bypass", [(0, 4, 1, 0), (1, 0, 1, 0), (33, 5, 0, 0), (2048, 128, 1, 0),
+                                                        (2048, 128, 1, 1), (70001, 5000, 1, 0), (5000, 0, 0, 0)])
+def test_fake_quant_mask_kernel(device, n, residual, preserve, bypass):
+    # uc_fake_quant_mask on scattered segment and protected masks: the selected
+    # rows (segment minus its last `residual` tokens minus protected ones),
+    # their compact order both ways and the three counts
+    from unicache_amd import _native as nat
+
+    rng = np.random.default_rng(n + residual)
+    seg = rng.random(n) < 0.7
+    prot = rng.random(n) < 0.05
+    quant = seg.copy()
+    idx = np.flatnonzero(seg)
+    if residual > 0 and idx.size:
+        quant[idx[-residual:]] = False
+    if preserve:
+        quant &= ~prot
+    if bypass:
+        quant[:] = False
+    sd, pd = torch.from_numpy(seg).to(device), torch.from_numpy(prot).to(device)
+    dst = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+    src = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+    counts = torch.empty(3, dtype=torch.int64, device=device)
+    nat.call("uc_fake_quant_mask", sd.data_ptr(), pd.data_ptr(), n, residual, preserve, bypass, dst.data_ptr(),
+             src.data_ptr(), counts.data_ptr(), nat.stream(device))
+    sel = np.flatnonzero(quant)
+    exp_dst = np.full(n, -1, dtype=np.int32)
+    exp_dst[sel] = np.arange(sel.size)
+    assert counts.cpu().tolist() == [int(seg.sum()), int(sel.size), int((seg & prot).sum())]
+    assert np.array_equal(dst[:n].cpu().numpy(), exp_dst)
+    assert np.array_equal(src[:sel.size].cpu().numpy(), sel)
+
+
+def test_segment_masking_scattered_segment(device):
+    # a segment of scattered tokens through the whole operator
+    key, value = kv_pair(700, seed=9)
+    rng = np.random.default_rng(9)
+    seg = rng.random(700) < 0.6
+    prot = rng.random(700) < 0.03
+    ctx, records, _ = _ctx(key.to(device), value.to(device), torch.from_numpy(seg).to(device),
+                           torch.from_numpy(prot).to(device), {"bits": 2, "group_size": 32, "residual_length": 40})
+    KIVIQuantizationOperator().execute(ctx)
+    ek, ev, n = _expected(key, value, seg, prot, bits=2, group=32, residual=40)
+    assert records[0]["quantized_tokens"] == n
+    assert np.array_equal(f32(ctx.k), ek) and np.array_equal(f32(ctx.v), ev)

@@ -181,6 +181,7 @@ _SIGNATURES = {
     "uc_copy_spans": (_I, [_P, _I, _P]),
     "uc_kivi_residual_append": (_I, [_P, _P, _I, _P, _P, _P, _L, _L, _L, _I, _P]),
     "uc_compact_rows_multi": (_I, [ctypes.POINTER(RowCopy), _I, _P, _L, _P]),
+    "uc_fake_quant_mask": (_I, [_P, _P, _L, _L, _I, _I, _P, _P, _P, _P]),
     "uc_h2o_select_gather_segments": (_I, [ctypes.POINTER(H2OSegment), _I, _I, _L, _L, _P]),
     "uc_h2o_select_gather": (
         _I,

@@ -74,6 +74,96 @@ __global__ __launch_bounds__(kScanThreads) void mask_scan_kernel(const uint8_t *
   }
 }
 
+// Block-wide exclusive scan of one int64 count per thread (1024 threads):
+// returns the thread's exclusive prefix and writes the total to *total_out.
+__device__ __forceinline__ int64_t block_exclusive_scan(int64_t cnt, int64_t *part, int64_t *total_out) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  int64_t incl = cnt;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int64_t v = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += v;
+  }
+  if (lane == kWave - 1) part[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int64_t w = lane < kScanThreads / kWave ? part[lane] : 0, wi = w;
+#pragma unroll
+    for (int o = 1; o < kScanThreads / kWave; o <<= 1) {
+      const int64_t v = __shfl_up(wi, o, kWave);
+      if (lane >= o) wi += v;
+    }
+    if (lane < kScanThreads / kWave) part[kScanThreads / kWave + lane] = wi - w;
+    if (lane == kScanThreads / kWave - 1) part[2 * kScanThreads / kWave] = wi;
+  }
+  __syncthreads();
+  const int64_t pre = part[kScanThreads / kWave + wave] + incl - cnt;
+  *total_out = part[2 * kScanThreads / kWave];
+  __syncthreads();  // `part` is reused by the next scan
+  return pre;
+}
+
+// The rows KIVIQuantizationOperator fake-quantizes (operators/builtin.py:
+// 394-404): segment tokens, except the last residual_length of them (a token
+// whose suffix count of segment tokens, itself included, is at most
+// residual_length) and, with preserve, the protected ones; none with bypass.
+// One workgroup, a contiguous chunk per thread: a scan of the segment counts
+// gives each token's suffix count, a scan of the selected counts its row in
+// the compact order (dst, -1 when not selected) and src the inverse.
+// counts = (segment tokens, selected tokens, protected segment tokens).
+__global__ __launch_bounds__(kScanThreads) void fake_quant_mask_kernel(const uint8_t *segment, const uint8_t *prot,
+                                                                      int64_t n, int64_t chunk, int64_t residual,
+                                                                      int preserve, int bypass, int32_t *dst,
+                                                                      int32_t *src, int64_t *counts) {
+  __shared__ int64_t part[2 * kScanThreads / kWave + 1];
+  const int tid = threadIdx.x;
+  const int64_t b = tid * chunk, e = min(n, b + chunk);
+  int64_t seg = 0, pseg = 0;
+  for (int64_t t = b; t < e; ++t) {
+    const bool sgt = segment[t] != 0;
+    seg += sgt;
+    pseg += sgt && prot[t] != 0;
+  }
+  int64_t seg_total = 0, pseg_total = 0;
+  int64_t seg_before = block_exclusive_scan(seg, part, &seg_total);
+  block_exclusive_scan(pseg, part, &pseg_total);
+  // selected count of this chunk
+  int64_t sel = 0;
+  {
+    int64_t sb = seg_before;
+    for (int64_t t = b; t < e; ++t) {
+      if (segment[t] == 0) continue;
+      const int64_t from_end = seg_total - sb;  // segment tokens at t or later
+      ++sb;
+      const bool q = !bypass && (residual <= 0 || from_end > residual) && !(preserve && prot[t] != 0);
+      sel += q;
+    }
+  }
+  int64_t sel_total = 0;
+  int64_t pos = block_exclusive_scan(sel, part, &sel_total);
+  int64_t sb = seg_before;
+  for (int64_t t = b; t < e; ++t) {
+    bool q = false;
+    if (segment[t] != 0) {
+      const int64_t from_end = seg_total - sb;
+      ++sb;
+      q = !bypass && (residual <= 0 || from_end > residual) && !(preserve && prot[t] != 0);
+    }
+    if (q) {
+      dst[t] = static_cast<int32_t>(pos);
+      src[pos] = static_cast<int32_t>(t);
+      ++pos;
+    } else {
+      dst[t] = -1;
+    }
+  }
+  if (tid == 0) {
+    counts[0] = seg_total;
+    counts[1] = sel_total;
+    counts[2] = pseg_total;
+  }
+}
+
 template <typename V>
 __global__ __launch_bounds__(256) void compact_rows_kernel(const char *src, int64_t src_stride, int64_t row_bytes,
                                                            const int32_t *dst_index, int64_t n, char *dst,
@@ -276,4 +366,19 @@ extern "C" int uc_compact_rows_multi(const uc_row_copy *copies, int n_copies, co
   const dim3 grid(static_cast<unsigned>(ceil_div(n * most, int64_t(256))), static_cast<unsigned>(m));
   hipLaunchKernelGGL(compact_rows_multi_kernel, grid, dim3(256), 0, as_stream(stream), a, dst_index, n);
   return check_launch("uc_compact_rows_multi");
+}
+
+extern "C" int uc_fake_quant_mask(const uint8_t *segment, const uint8_t *protected_mask, int64_t n,
+                                  int64_t residual_length, int preserve_protected, int bypass, int32_t *dst_index,
+                                  int32_t *src_index, int64_t *counts, uc_stream_t stream) {
+  clear_error();
+  UC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "uc_fake_quant_mask: row count %lld out of range", (long long)n);
+  UC_REQUIRE(counts != nullptr && (n == 0 || (segment != nullptr && protected_mask != nullptr &&
+                                              dst_index != nullptr && src_index != nullptr)),
+             "uc_fake_quant_mask: null pointer");
+  const int64_t chunk = ceil_div(n, int64_t(kScanThreads));
+  hipLaunchKernelGGL(fake_quant_mask_kernel, dim3(1), dim3(kScanThreads), 0, as_stream(stream), segment,
+                     protected_mask, n, chunk > 0 ? chunk : 1, residual_length, preserve_protected, bypass, dst_index,
+                     src_index, counts);
+  return check_launch("uc_fake_quant_mask");
 }

@@ -109,20 +109,21 @@ class KIVIQuantizationOperator(ProcessingOperator):
             raise ValueError(f"{self.name} supports the attention_view working set only")
 
         device = nat.require_device(ctx.k, ctx.v, what="KIVI fake quantization")
-        segment = ctx.segment_mask.to(device=device, dtype=torch.bool)
-        protected = ctx.protected_mask.to(device=device, dtype=torch.bool)
-        quant = segment.clone()
-        if residual_length > 0:
-            # the last residual_length tokens of the segment stay in full precision:
-            # a token is among them when at most that many segment tokens start at it
-            from_end = segment.flip(0).cumsum(0).flip(0)
-            quant &= from_end > residual_length
-        if preserve_protected:
-            quant &= ~protected
-        if bypass_quantization:
-            quant.zero_()
-        counts = torch.stack([segment.sum(), quant.sum(), (protected & segment).sum()]).tolist()
-        segment_tokens, quant_tokens, protected_in_segment = map(int, counts)
+        segment = ctx.segment_mask.to(device=device, dtype=torch.bool).contiguous()
+        protected = ctx.protected_mask.to(device=device, dtype=torch.bool).contiguous()
+        n = int(segment.numel())
+        if int(protected.numel()) != n:
+            raise RuntimeError("segment_mask and protected_mask must have the same length")
+        # one launch: the rows to quantize -- segment tokens but the last
+        # residual_length of them and, with preserve, the protected ones; none
+        # with bypass -- their compact order, and the three counts; one host read
+        dst = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+        src = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+        counts = torch.empty(3, dtype=torch.int64, device=device)
+        nat.call("uc_fake_quant_mask", segment.data_ptr(), protected.data_ptr(), n, residual_length,
+                 int(preserve_protected), int(bypass_quantization), dst.data_ptr(), src.data_ptr(),
+                 counts.data_ptr(), nat.stream(device))
+        segment_tokens, quant_tokens, protected_in_segment = map(int, counts.tolist())
 
         full_precision_tokens = segment_tokens - quant_tokens
         elem_bytes = max(1, ctx.k.element_size())
@@ -147,8 +148,8 @@ class KIVIQuantizationOperator(ProcessingOperator):
         ideal_storage = full_precision_bytes + packed_payload_bytes + metadata_bytes
 
         if quant_tokens > 0:
-            ctx.k, ctx.v = fake_quant_rows(ctx.k, ctx.v, quant, quant_tokens, k_bits=k_bits, v_bits=v_bits,
-                                           group_size=group_size)
+            ctx.k, ctx.v = _fake_quant_rows_at(ctx.k, ctx.v, dst[:n], quant_tokens, k_bits=k_bits, v_bits=v_bits,
+                                               group_size=group_size)
         ctx.record({
             "quantized_tokens": quant_tokens,
             "protected_tokens_preserved": protected_in_segment if preserve_protected else 0,
@@ -178,16 +179,29 @@ def fake_quant_rows(key: torch.Tensor, value: torch.Tensor, mask: torch.Tensor, 
     order -- key[mask] = fake_quant(key[mask]) of operators/builtin.py:420-430,
     on the mask scan, row copy and row scatter kernels."""
 
-    from ..storage.tensor_backend import _aligned_mask, _copy_rows, _scan
+    from ..storage.tensor_backend import _aligned_mask, _scan
 
     device = nat.require_device(key, value, mask, what="KIVI fake quantization")
     dst, _ = _scan(_aligned_mask(mask, device))
+    return _fake_quant_rows_at(key, value, dst, count, k_bits=k_bits, v_bits=v_bits, group_size=group_size)
+
+
+def _fake_quant_rows_at(key: torch.Tensor, value: torch.Tensor, dst: torch.Tensor, count: int, *, k_bits: int,
+                        v_bits: int, group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """fake_quant_rows with the compact order of the rows (dst, -1 for the
+    others) already on the device: K and V rows gathered in one launch,
+    fake-quantized, and scattered into copies of K and V."""
+
+    from ..storage.tensor_backend import _copy_rows_many
+
+    device = key.device
     stream = nat.stream(device)
+    rows_k, rows_v = _copy_rows_many([key, value], dst, count)
     outs = []
-    for data, fq, b in ((key, kivi_fake_quant_key, k_bits), (value, kivi_fake_quant_value, v_bits)):
-        rows = fq(_copy_rows(data, dst, count), bits=b, group_size=group_size)
-        out = torch.empty(data.shape, dtype=data.dtype, device=device)
-        out.copy_(data)
+    for data, rows, fq, b in ((key, rows_k, kivi_fake_quant_key, k_bits), (value, rows_v, kivi_fake_quant_value,
+                                                                          v_bits)):
+        rows = fq(rows, bits=b, group_size=group_size)
+        out = data.clone(memory_format=torch.contiguous_format)
         row_bytes = int(rows[0].numel()) * rows.element_size()
         nat.call("uc_scatter_rows", rows.contiguous().data_ptr(), row_bytes, dst.data_ptr(), int(dst.numel()),
                  out.data_ptr(), int(out.stride(0)) * out.element_size(), stream)
