@@ -667,6 +667,78 @@ __global__ __launch_bounds__(256) void fake_quant_tokens_kernel(FakeQuantArgs a)
   }
 }
 
+// The same for head_dim 128 with the group's tokens split over the four
+// waves of a workgroup (workgroup = (group, head), lane = channel pair): each
+// wave holds TPW tokens in registers, the four partial ranges meet in LDS,
+// then every wave quantizes its own tokens.  Four times the waves of the
+// kernel above, a quarter of the serial loads per lane.
+template <int DT, int TPW>
+__global__ __launch_bounds__(256) void fake_quant_tokens_split_kernel(FakeQuantArgs a) {
+  __shared__ float rmn[4][kWave], rmx[4][kWave];
+  __shared__ int rnan[4][kWave];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int64_t g = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
+  const int64_t t0 = g * a.group, n = min(a.group, a.tokens - t0);
+  const int64_t w0 = int64_t(wave) * TPW;  // this wave's first token of the group
+  const int64_t base = (t0 + w0) * a.st + h * a.sh + 2 * lane;
+  float x0[TPW], x1[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const uint32_t pair = w0 + i < n ? *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(a.data) +
+                                                                          base + i * a.st)
+                                     : 0u;
+    x0[i] = half_bits_to_f32<DT>(pair);
+    x1[i] = half_bits_to_f32<DT>(pair >> 16);
+  }
+  GroupRange r0, r1;
+  r0.mn = r1.mn = __builtin_inff();
+  r0.mx = r1.mx = -__builtin_inff();
+  r0.nan = r1.nan = false;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    if (w0 + i < n) {
+      r0.add(x0[i]);
+      r1.add(x1[i]);
+    }
+  }
+  // lane l owns channels 2l, 2l + 1: slots 0 and 1 of a 2-wide LDS row
+  rmn[wave][lane] = r0.mn;
+  rmx[wave][lane] = r0.mx;
+  rnan[wave][lane] = int(r0.nan) | (int(r1.nan) << 1);
+  __syncthreads();
+  float mn0 = rmn[0][lane], mx0 = rmx[0][lane];
+  int nan = rnan[0][lane];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    mn0 = fminf(mn0, rmn[w][lane]);
+    mx0 = fmaxf(mx0, rmx[w][lane]);
+    nan |= rnan[w][lane];
+  }
+  __syncthreads();
+  rmn[wave][lane] = r1.mn;
+  rmx[wave][lane] = r1.mx;
+  __syncthreads();
+  float mn1 = rmn[0][lane], mx1 = rmx[0][lane];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    mn1 = fminf(mn1, rmn[w][lane]);
+    mx1 = fmaxf(mx1, rmx[w][lane]);
+  }
+  if (nan & 1) mn0 = mx0 = __builtin_nanf("");
+  if (nan & 2) mn1 = mx1 = __builtin_nanf("");
+  const float s0 = div_rn(clamp_min_nan(sub_rn(mx0, mn0), kEps), a.max_code);
+  const float s1 = div_rn(clamp_min_nan(sub_rn(mx1, mn1), kEps), a.max_code);
+  const float rcp_s0 = __builtin_amdgcn_rcpf(s0), rcp_s1 = __builtin_amdgcn_rcpf(s1);
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    if (w0 + i < n) {
+      const float c0 = fminf(fmaxf(quant_rint(sub_rn(x0[i], mn0), s0, rcp_s0), 0.0f), a.max_code);
+      const float c1 = fminf(fmaxf(quant_rint(sub_rn(x1[i], mn1), s1, rcp_s1), 0.0f), a.max_code);
+      store_pair<DT>(a.out, base + i * a.st, add_rn(mul_rn(c0, s0), mn0), add_rn(mul_rn(c1, s1), mn1));
+    }
+  }
+}
+
 // Groups along channels (8 to 64 channels, dividing head_dim), 16-bit data
 // with unit channel stride: lane = 8 channels of one (token, head), a group
 // spans group/8 neighbouring lanes reduced with shuffles.
@@ -892,6 +964,21 @@ extern "C" int uc_kivi_fake_quant(const void *data, int64_t st, int64_t sh, int6
   const int64_t blocks = ceil_div(fixed * groups, 256);
   hipStream_t s = as_stream(stream);
   const bool half = dtype == UC_BF16 || dtype == UC_FP16;
+  if (half && dim == 0 && sd == 1 && head_dim == 2 * kWave && st % 2 == 0 && sh % 2 == 0 && aligned(data, 4) &&
+      aligned(out, 4) && a.group <= 64) {
+    const dim3 grid(static_cast<unsigned>(groups * heads));
+    UC_DISPATCH_DTYPE(dtype, DT, [&] {
+      if constexpr (DT != UC_FP32) {
+        if (a.group <= 16)
+          hipLaunchKernelGGL((fake_quant_tokens_split_kernel<DT, 4>), grid, dim3(256), 0, s, a);
+        else if (a.group <= 32)
+          hipLaunchKernelGGL((fake_quant_tokens_split_kernel<DT, 8>), grid, dim3(256), 0, s, a);
+        else
+          hipLaunchKernelGGL((fake_quant_tokens_split_kernel<DT, 16>), grid, dim3(256), 0, s, a);
+      }
+    });
+    return check_launch("uc_kivi_fake_quant");
+  }
   if (half && dim == 0 && sd == 1 && head_dim % 2 == 0 && st % 2 == 0 && sh % 2 == 0 && aligned(data, 4) &&
       aligned(out, 4) && a.group <= 64) {
     const int64_t n = groups * heads * (head_dim / 2);
