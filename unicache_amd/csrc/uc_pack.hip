@@ -530,6 +530,69 @@ __global__ __launch_bounds__(256) void dequant_key_native_kernel(DequantArgs a, 
   }
 }
 
+// Keys from token-major storage (channel stride 1 for words and stats) into
+// 16-bit rows with 16-byte alignment: lane = (head, run of 4 words, 8
+// channels), channel octets fastest.  A lane loads its octet's words of the
+// run (two 16-byte loads per word) and their groups' scales and minima (16
+// bytes each), then writes one 16-byte store per token: a wave writes whole
+// 256-byte head rows, four times the bytes per store of the pairwise kernel.
+template <int BITS, int OD, int SD>
+__global__ __launch_bounds__(256) void dequant_key_octet_kernel(DequantArgs a, int64_t runs) {
+  constexpr int TPW = 32 / BITS;
+  constexpr uint32_t kMask = (1u << BITS) - 1u;
+  const int64_t octets = a.head_dim / 8;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= a.heads * runs * octets) return;
+  const int64_t oc = idx % octets, run = (idx / octets) % runs, h = idx / (octets * runs);
+  const int64_t c = 8 * oc, stop = a.start + a.count;
+  const int64_t w0 = a.start / TPW + run * kDqRunWords, w_end = (stop + TPW - 1) / TPW;
+  const uint32_t *kc = static_cast<const uint32_t *>(a.key_code) + h * a.kc_sh + c;
+  uint32_t wd[kDqRunWords][8];
+  float sc[kDqRunWords][8], mn[kDqRunWords][8];
+#pragma unroll
+  for (int j = 0; j < kDqRunWords; ++j) {
+    const bool ok = w0 + j < w_end;
+    const int64_t w = ok ? w0 + j : w0;
+    const uint4 lo = *reinterpret_cast<const uint4 *>(kc + w * a.kc_sw);
+    const uint4 hi = *reinterpret_cast<const uint4 *>(kc + w * a.kc_sw + 4);
+    wd[j][0] = lo.x; wd[j][1] = lo.y; wd[j][2] = lo.z; wd[j][3] = lo.w;
+    wd[j][4] = hi.x; wd[j][5] = hi.y; wd[j][6] = hi.z; wd[j][7] = hi.w;
+    const int64_t so = h * a.ks_sh + c + ((w * TPW) >> a.lg) * a.ks_sg;
+    const uint4 sv = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.key_scale) + so);
+    const uint4 mv = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.key_min) + so);
+    const uint32_t s4[4] = {sv.x, sv.y, sv.z, sv.w}, m4[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      sc[j][2 * k] = half_bits_to_f32<SD>(s4[k]);
+      sc[j][2 * k + 1] = half_bits_to_f32<SD>(s4[k] >> 16);
+      mn[j][2 * k] = half_bits_to_f32<SD>(m4[k]);
+      mn[j][2 * k + 1] = half_bits_to_f32<SD>(m4[k] >> 16);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kDqRunWords; ++j) {
+    const int64_t w = w0 + j;
+    if (w >= w_end) break;
+#pragma unroll
+    for (int p = 0; p < TPW; ++p) {
+      const int64_t t = w * TPW + p;
+      if (t < a.start || t >= stop) continue;
+      uint32_t out[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float v0 = add_rn(mul_rn(float((wd[j][2 * k] >> (p * BITS)) & kMask), sc[j][2 * k]), mn[j][2 * k]);
+        const float v1 =
+            add_rn(mul_rn(float((wd[j][2 * k + 1] >> (p * BITS)) & kMask), sc[j][2 * k + 1]), mn[j][2 * k + 1]);
+        const uint32_t b0 = OD == UC_BF16 ? f32_to_bf16_bits(v0) : f32_to_f16_bits(v0);
+        const uint32_t b1 = OD == UC_BF16 ? f32_to_bf16_bits(v1) : f32_to_f16_bits(v1);
+        out[k] = b0 | (b1 << 16);
+      }
+      *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.out_key) + (a.offset + t - a.start) * a.o_st +
+                                 h * a.o_sh + c) = make_uint4(out[0], out[1], out[2], out[3]);
+    }
+  }
+}
+
 // Values: lane = (head, token, word), words fastest: one 4-byte word and its
 // group's stats in, 16 (2-bit) or 8 (4-bit) contiguous channels out.
 template <int BITS, int OD, bool VEC>
@@ -906,7 +969,27 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
   if (out_ok && tuned_group(group_size, head_dim) && (key_code == nullptr || key_native) &&
       (value_code == nullptr || value_native)) {
     UC_DISPATCH_DTYPE(out_dtype, OD, [&] {
-      if (key_code != nullptr) {
+      // token-major words and stats (channel stride 1), 16-bit stats and
+      // output, 16-byte aligned rows: the octet kernel
+      const bool octet = key_code != nullptr && kc_sd == 1 && ks_sd == 1 && OD != UC_FP32 && stats_dtype != UC_FP32 &&
+                         head_dim % 8 == 0 && kc_sw % 4 == 0 && kc_sh % 4 == 0 && ks_sg % 8 == 0 && ks_sh % 8 == 0 &&
+                         o_st % 8 == 0 && o_sh % 8 == 0 && aligned(key_code, 16) && aligned(key_scale, 16) &&
+                         aligned(key_min, 16) && aligned(out_key, 16);
+      if (octet) {
+        const int tpw = 32 / k_bits;
+        const int64_t words = (start + count + tpw - 1) / tpw - start / tpw;
+        const int64_t runs = ceil_div(words, int64_t(kDqRunWords));
+        const dim3 grid(static_cast<unsigned>(ceil_div(heads * runs * (head_dim / 8), int64_t(256))));
+        auto go_key = [&](auto sd_tag) {
+          constexpr int SD = decltype(sd_tag)::value;
+          if (k_bits == 2)
+            hipLaunchKernelGGL((dequant_key_octet_kernel<2, OD, SD>), grid, dim3(256), 0, s, a, runs);
+          else
+            hipLaunchKernelGGL((dequant_key_octet_kernel<4, OD, SD>), grid, dim3(256), 0, s, a, runs);
+        };
+        if (stats_dtype == UC_BF16) go_key(std::integral_constant<int, UC_BF16>{});
+        else go_key(std::integral_constant<int, UC_FP16>{});
+      } else if (key_code != nullptr) {
         const int tpw = 32 / k_bits;
         const int64_t words = (start + count + tpw - 1) / tpw - start / tpw;
         const int64_t runs = ceil_div(words, int64_t(kDqRunWords));
