@@ -290,11 +290,15 @@ __global__ __launch_bounds__(kSelThreads) void h2o_select_kernel(SelectArgs a) {
     // candidate keys of this thread (REGS): token r * kSelThreads + tid
     uint32_t keys[REGS ? kSelRegs : 1];
     if constexpr (REGS) {
+      // every load issued before any is used; tokens past the history read token 0
+      float v[kSelRegs];
 #pragma unroll
       for (int r = 0; r < kSelRegs; ++r) {
         const int64_t t = int64_t(r) * kSelThreads + tid;
-        keys[r] = t < hist_end ? order_key(sc[t * a.s_st]) : 0u;
+        v[r] = sc[(t < hist_end ? t : 0) * a.s_st];
       }
+#pragma unroll
+      for (int r = 0; r < kSelRegs; ++r) keys[r] = int64_t(r) * kSelThreads + tid < hist_end ? order_key(v[r]) : 0u;
     }
     uint32_t prefix = 0, mask = 0;
     uint32_t need = static_cast<uint32_t>(a.heavy_k);
@@ -461,12 +465,6 @@ struct SgArgs {
   int64_t Hkv, D;
 };
 
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-
 __global__ __launch_bounds__(kSgThreads) void h2o_select_gather_kernel(SgArgs a) {
   __shared__ uint32_t cnt[2][kSgWaves];
   __shared__ uint32_t tab[2][kSgRegs * kSgWaves];  // gt / eq counts per (chunk, wave), then prefixes
@@ -484,22 +482,32 @@ __global__ __launch_bounds__(kSgThreads) void h2o_select_gather_kernel(SgArgs a)
   const float *sc = g.scores + h * g.s_sh;
 
   if (heavy > 0) {
-    uint32_t keys[kSgRegs];
+    // every load issued before any is used (a load under the token test would
+    // be waited for one at a time); tokens past the history read token 0
+    float v[kSgRegs];
 #pragma unroll
     for (int r = 0; r < kSgRegs; ++r) {
       const int64_t t = int64_t(r) * kSgThreads + tid;
-      keys[r] = t < hist_end ? order_key(sc[t * g.s_st]) : 0u;  // order keys of real scores are never 0
+      v[r] = sc[(t < hist_end ? t : 0) * g.s_st];
     }
+    uint32_t keys[kSgRegs];
+#pragma unroll
+    for (int r = 0; r < kSgRegs; ++r)  // order keys of real scores are never 0
+      keys[r] = int64_t(r) * kSgThreads + tid < hist_end ? order_key(v[r]) : 0u;
     uint32_t th = 0;
     for (int it = 0; it < 16; ++it) {
       const int b = 30 - 2 * it;
       const uint32_t c1 = th | (1u << b), c2 = th | (2u << b), c3 = th | (3u << b);
-      uint32_t n = 0;  // three counts of at most 8 per thread, 512 per wave: 10 bits each
+      // wave counts by ballots (keys of invalid tokens are 0, below every
+      // candidate): at most 512 per wave, 10 bits each of one word
+      uint32_t n1 = 0, n2 = 0, n3 = 0;
 #pragma unroll
-      for (int r = 0; r < kSgRegs; ++r)
-        n += uint32_t(keys[r] >= c1) + (uint32_t(keys[r] >= c2) << 10) + (uint32_t(keys[r] >= c3) << 20);
-      n = wave_sum_u32(n);
-      if (lane == 0) cnt[it & 1][wave] = n;
+      for (int r = 0; r < kSgRegs; ++r) {
+        n1 += __popcll(__ballot(keys[r] >= c1));
+        n2 += __popcll(__ballot(keys[r] >= c2));
+        n3 += __popcll(__ballot(keys[r] >= c3));
+      }
+      if (lane == 0) cnt[it & 1][wave] = n1 + (n2 << 10) + (n3 << 20);
       __syncthreads();
       uint32_t s1 = 0, s2 = 0, s3 = 0;
 #pragma unroll

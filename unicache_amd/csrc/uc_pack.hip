@@ -531,11 +531,13 @@ __global__ __launch_bounds__(256) void dequant_key_native_kernel(DequantArgs a, 
 }
 
 // Keys from token-major storage (channel stride 1 for words and stats) into
-// 16-bit rows with 16-byte alignment: lane = (head, run of 4 words, 8
-// channels), channel octets fastest.  A lane loads its octet's words of the
+// 16-bit rows with 16-byte alignment: lane = (head, key word, 8 channels),
+// channel octets fastest.  A lane loads its octet's words of the
 // run (two 16-byte loads per word) and their groups' scales and minima (16
 // bytes each), then writes one 16-byte store per token: a wave writes whole
 // 256-byte head rows, four times the bytes per store of the pairwise kernel.
+constexpr int kDqOctetWords = 1;  // key words per lane of the octet kernel: enough lanes to fill the chip
+
 template <int BITS, int OD, int SD>
 __global__ __launch_bounds__(256) void dequant_key_octet_kernel(DequantArgs a, int64_t runs) {
   constexpr int TPW = 32 / BITS;
@@ -545,12 +547,12 @@ __global__ __launch_bounds__(256) void dequant_key_octet_kernel(DequantArgs a, i
   if (idx >= a.heads * runs * octets) return;
   const int64_t oc = idx % octets, run = (idx / octets) % runs, h = idx / (octets * runs);
   const int64_t c = 8 * oc, stop = a.start + a.count;
-  const int64_t w0 = a.start / TPW + run * kDqRunWords, w_end = (stop + TPW - 1) / TPW;
+  const int64_t w0 = a.start / TPW + run * kDqOctetWords, w_end = (stop + TPW - 1) / TPW;
   const uint32_t *kc = static_cast<const uint32_t *>(a.key_code) + h * a.kc_sh + c;
-  uint32_t wd[kDqRunWords][8];
-  float sc[kDqRunWords][8], mn[kDqRunWords][8];
+  uint32_t wd[kDqOctetWords][8];
+  float sc[kDqOctetWords][8], mn[kDqOctetWords][8];
 #pragma unroll
-  for (int j = 0; j < kDqRunWords; ++j) {
+  for (int j = 0; j < kDqOctetWords; ++j) {
     const bool ok = w0 + j < w_end;
     const int64_t w = ok ? w0 + j : w0;
     const uint4 lo = *reinterpret_cast<const uint4 *>(kc + w * a.kc_sw);
@@ -570,7 +572,7 @@ __global__ __launch_bounds__(256) void dequant_key_octet_kernel(DequantArgs a, i
     }
   }
 #pragma unroll
-  for (int j = 0; j < kDqRunWords; ++j) {
+  for (int j = 0; j < kDqOctetWords; ++j) {
     const int64_t w = w0 + j;
     if (w >= w_end) break;
 #pragma unroll
@@ -978,7 +980,7 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
       if (octet) {
         const int tpw = 32 / k_bits;
         const int64_t words = (start + count + tpw - 1) / tpw - start / tpw;
-        const int64_t runs = ceil_div(words, int64_t(kDqRunWords));
+        const int64_t runs = ceil_div(words, int64_t(kDqOctetWords));
         const dim3 grid(static_cast<unsigned>(ceil_div(heads * runs * (head_dim / 8), int64_t(256))));
         auto go_key = [&](auto sd_tag) {
           constexpr int SD = decltype(sd_tag)::value;
