@@ -61,6 +61,36 @@ def test_pack_codes_at_exact_half_steps(device, bits):
     _assert_cache_equal(cache, seg)
 
 
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("group", [16, 32, 64])
+@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float16, "fp16")])
+def test_pack_groups_dtypes_half_steps_and_non_finite(device, bits, group, dtype, name):
+    # random rows, integer ramps whose quotients land exactly on half steps in
+    # some lanes (the exact recomputation inside an otherwise reciprocal-rounded
+    # group), one NaN and one inf per tensor: keys and values, every group size
+    # and 16-bit input the 2/4-bit kernel-native pack takes
+    tokens = 4 * group + 2 * 64
+    g = torch.Generator().manual_seed(100 * bits + group)
+    key = torch.randn(tokens, 4, 128, generator=g)
+    value = torch.randn(tokens, 4, 128, generator=g)
+    top = (1 << bits) - 1
+    ramp = torch.arange(group, dtype=torch.float32) % (2 * top + 1)
+    key[group:2 * group, 1, 10:20] = ramp[:, None]          # key groups along tokens
+    value[5, 2, :group] = ramp                              # one value group along channels
+    key[3 * group + 1, 3, 77] = float("nan")
+    value[7, 0, 100] = float("inf")
+    key, value = key.to(dtype), value.to(dtype)
+    cache = _cache(key, value, device, k_bits=bits, v_bits=bits, group_size=group, residual_length=0)
+    with np.errstate(invalid="ignore"):
+        seg = K.from_dense(f32(key), f32(value), k_bits=bits, v_bits=bits, group_size=group, residual_length=0,
+                           native=True, in_dtype=name)
+    assert cache.kernel_native_layout
+    for attr in ("key_code", "value_code"):
+        assert np.array_equal(getattr(cache, attr).cpu().numpy(), getattr(seg, attr)), attr
+    for attr in ("key_scale", "key_minimum", "value_scale", "value_minimum"):
+        assert np.array_equal(f32(getattr(cache, attr)), getattr(seg, attr), equal_nan=True), attr
+
+
 def test_config0_pack_with_outliers_and_residual(device):
     key, value = kv_pair(2048, seed=0)
     cache = _cache(key, value, device, k_bits=2, v_bits=2, group_size=32, residual_length=128)

@@ -10,6 +10,7 @@
 // dequantisation is a rounded multiply followed by a rounded add (never an
 // FMA: the library is built with -ffp-contract=off and these use __f*_rn).
 #include "uc_common.h"
+#include "uc_mfma.h"
 
 #include <type_traits>
 
@@ -291,6 +292,301 @@ __global__ __launch_bounds__(kPackThreads) void kivi_pack_kv_kernel(PackArgs a, 
 }
 
 int64_t wave_blocks(int64_t waves) { return (waves + (kPackThreads / kWave) - 1) / (kPackThreads / kWave); }
+
+// ------------------------------------------------------ fast 2/4-bit pack --
+// Keys and values of equal 2/4 bits, head_dim 128, 16-bit rows with unit
+// channel stride into token-major storage (unit channel / word strides).  A
+// key unit is one token group of one head (lane = channel pair, G loads of 4
+// bytes), a value unit VR runs of 8 tokens of one head (lane = token of the
+// run and 16-channel chunk, two 16-byte loads per run); heads are the fastest
+// index, so the four waves of a workgroup read whole token rows.  Wave w of
+// the grid takes unit w: key units first, then value units.  A lane's raw
+// 16-bit pairs stay in registers: read once for the range, once for the codes.
+//
+// The range uses IEEE minimum/maximum (v_minimum3 / v_maximum3, two elements
+// per instruction), which propagate NaN as torch.amin / amax do.  Codes are
+// rint((x - mn) * rcp(scale)), with the correctly rounded division only for
+// elements near a half step (code_of), and are converted and byte-packed by
+// v_cvt_pk_u8_f32 (exact for these integer values): byte m of dword c holds
+// code m * (8 / b) + c, so shifting the dwords together puts code j at bit
+// b * j, LSB first (physical.py:72-85).  A group with NaN or inf, or a scale
+// past 2^126, takes the generic arithmetic (quant_rint and the clamp).
+template <int IN>
+__device__ __forceinline__ float lo16(uint32_t r) {
+  if constexpr (IN == UC_BF16) return __uint_as_float(r << 16);
+  else return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r)));
+}
+template <int IN>
+__device__ __forceinline__ float hi16(uint32_t r) {
+  if constexpr (IN == UC_BF16) return __uint_as_float(r & 0xffff0000u);
+  else return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r >> 16)));
+}
+__device__ __forceinline__ float min_nan(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// Integer-valued code q (0..255) into byte m of d.
+__device__ __forceinline__ uint32_t put_code_byte(int m, float q, uint32_t d) {
+  switch (m) {
+    case 0: return __builtin_amdgcn_cvt_pk_u8_f32(q, 0, d);
+    case 1: return __builtin_amdgcn_cvt_pk_u8_f32(q, 1, d);
+    case 2: return __builtin_amdgcn_cvt_pk_u8_f32(q, 2, d);
+    default: return __builtin_amdgcn_cvt_pk_u8_f32(q, 3, d);
+  }
+}
+
+// Scale of a group from its range (physical.py:160-175); a NaN range gives
+// the canonical NaN statistics of GroupRange.
+template <int BITS>
+__device__ __forceinline__ float group_scale(float &mn, float &mx) {
+  if (mn != mn) {
+    mn = __builtin_nanf("");
+    mx = mn;
+  }
+  return clamp_min_nan(div_rn(sub_rn(mx, mn), float((1 << BITS) - 1)), kEps);
+}
+
+// Code of one element of a group whose scale s is finite with a normal
+// reciprocal r: y = (x - mn) * r lies in [0, 2^b - 1 + 2^-20], so rint(y)
+// needs no clamp, and it is the code of the correctly rounded quotient
+// whenever y is farther than 2^b 2^-20 >= |y| 2^-20 from a half-integer (the
+// argument of quant_rint).  Inside that band -- about one element in a
+// thousand for bf16 data, whose groups often hold exact half steps -- the
+// correctly rounded division decides, for the lanes that need it.
+template <int BITS>
+__device__ __forceinline__ float code_of(float x, float mn, float s, float r) {
+  constexpr float kNearHalf = 0.5f - float(1 << BITS) * 0x1p-20f;
+  const float d = sub_rn(x, mn);
+  const float y = mul_rn(d, r);
+  float q = rintf(y);
+  if (fabsf(sub_rn(y, q)) >= kNearHalf) q = rintf(div_rn(d, s));
+  return q;
+}
+
+// Groups the fast codes serve: finite scale (no NaN or inf in the group) with
+// a normal reciprocal.  Others take the generic arithmetic (quant_rint, clamp).
+__device__ __forceinline__ bool fast_group(float s, float r) { return s <= 3.0e38f && r >= 0x1p-126f; }
+
+// Word k of the codes from the byte dwords d (code m * (8 / BITS) + c of the
+// word in byte m of d[c]).
+template <int BITS>
+__device__ __forceinline__ uint32_t merge_code_bytes(const uint32_t (&d)[8 / BITS]) {
+  uint32_t w = d[0];
+#pragma unroll
+  for (int c = 1; c < 8 / BITS; ++c) w |= d[c] << (BITS * c);
+  return w;
+}
+
+// The codes of one word by the generic kernels' arithmetic (quant_rint, clamp).
+template <int BITS>
+__device__ __forceinline__ uint32_t exact_code_word(const float (&x)[32 / BITS], float mn, float s, float r) {
+  uint32_t word = 0;
+#pragma unroll
+  for (int j = 0; j < 32 / BITS; ++j) {
+    const float q = fminf(fmaxf(quant_rint(sub_rn(x[j], mn), s, r), 0.0f), float((1 << BITS) - 1));
+    word |= static_cast<uint32_t>(q) << (j * BITS);
+  }
+  return word;
+}
+
+__device__ __forceinline__ uint32_t stat_bits(float v, int stats_dtype) {
+  return stats_dtype == UC_FP16 ? f32_to_f16_bits(v) : f32_to_bf16_bits(v);
+}
+
+template <int IN, int BITS, int G>
+__device__ __forceinline__ void fast_key_unit(const PackArgs &a, int64_t unit, int lane) {
+  constexpr int kPer = 32 / BITS, kPerByte = 8 / BITS, kWords = G / kPer;
+  // heads fastest: the waves of a workgroup read whole token rows
+  const int64_t h = unit % a.heads, g = unit / a.heads;
+  const uint16_t *src = static_cast<const uint16_t *>(a.key) + g * G * a.k_st + h * a.k_sh;
+  const mf::Rsrc rs = mf::make_rsrc(src, (G - 1) * a.k_st * 2 + 256);
+  const uint32_t row = static_cast<uint32_t>(a.k_st * 2);
+  uint32_t raw[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) raw[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, 4u * lane, i * row, 0);
+  float mn0 = lo16<IN>(raw[0]), mx0 = mn0, mn1 = hi16<IN>(raw[0]), mx1 = mn1;
+#pragma unroll
+  for (int i = 1; i < G; ++i) {
+    const float x0 = lo16<IN>(raw[i]), x1 = hi16<IN>(raw[i]);
+    mn0 = min_nan(mn0, x0);
+    mx0 = max_nan(mx0, x0);
+    mn1 = min_nan(mn1, x1);
+    mx1 = max_nan(mx1, x1);
+  }
+  const float s0 = group_scale<BITS>(mn0, mx0), s1 = group_scale<BITS>(mn1, mx1);
+  const float r0 = __builtin_amdgcn_rcpf(s0), r1 = __builtin_amdgcn_rcpf(s1);
+  // converting again costs less than keeping the range pass's 2G floats live
+#pragma unroll
+  for (int i = 0; i < G; ++i) asm volatile("" : "+v"(raw[i]));
+  // both channels element by element, so each raw pair dies at its last use
+  const bool fast0 = fast_group(s0, r0), fast1 = fast_group(s1, r1);
+  uint32_t w0[kWords], w1[kWords];
+  if (fast0 && fast1) {
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) {
+      uint32_t d0[kPerByte], d1[kPerByte];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+#pragma unroll
+        for (int c = 0; c < kPerByte; ++c) {
+          const uint32_t v = raw[k * kPer + m * kPerByte + c];
+          d0[c] = put_code_byte(m, code_of<BITS>(lo16<IN>(v), mn0, s0, r0), m ? d0[c] : 0u);
+          d1[c] = put_code_byte(m, code_of<BITS>(hi16<IN>(v), mn1, s1, r1), m ? d1[c] : 0u);
+        }
+      }
+      w0[k] = merge_code_bytes<BITS>(d0);
+      w1[k] = merge_code_bytes<BITS>(d1);
+    }
+  } else {
+    // rare (NaN or inf in a group, a scale past 2^126): both channels by the
+    // generic arithmetic
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) {
+      float x0[kPer], x1[kPer];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        x0[j] = lo16<IN>(raw[k * kPer + j]);
+        x1[j] = hi16<IN>(raw[k * kPer + j]);
+      }
+      w0[k] = exact_code_word<BITS>(x0, mn0, s0, r0);
+      w1[k] = exact_code_word<BITS>(x1, mn1, s1, r1);
+    }
+  }
+  const int64_t c = 2 * lane;
+  uint32_t *kc = static_cast<uint32_t *>(a.key_code) + h * a.kc_sh + g * kWords * a.kc_sw + c;
+#pragma unroll
+  for (int w = 0; w < kWords; ++w) *reinterpret_cast<uint2 *>(kc + w * a.kc_sw) = make_uint2(w0[w], w1[w]);
+  const int64_t so = h * a.ks_sh + g * a.ks_sg + c;
+  *reinterpret_cast<uint32_t *>(static_cast<uint16_t *>(a.key_scale) + so) =
+      stat_bits(s0, a.stats_dtype) | (stat_bits(s1, a.stats_dtype) << 16);
+  *reinterpret_cast<uint32_t *>(static_cast<uint16_t *>(a.key_min) + so) =
+      stat_bits(mn0, a.stats_dtype) | (stat_bits(mn1, a.stats_dtype) << 16);
+}
+
+template <int IN, int BITS, int G, int VR>
+__device__ __forceinline__ void fast_value_unit(const PackArgs &a, int64_t unit, int lane) {
+  constexpr int kRuns = VR;       // runs of 8 tokens per unit
+  constexpr int kLanes = G / 16;  // lanes of one value group
+  constexpr int kPer = 32 / BITS, kPerByte = 8 / BITS, kWords = 16 / kPer;
+  const int64_t h = unit % a.heads, g = unit / a.heads;
+  const int tok = lane >> 3, chunk = lane & 7;
+  const uint16_t *src = static_cast<const uint16_t *>(a.value) + g * (8 * VR) * a.v_st + h * a.v_sh;
+  const mf::Rsrc rs = mf::make_rsrc(src, (8 * VR - 1) * a.v_st * 2 + 256);
+  const uint32_t voff = static_cast<uint32_t>((tok * a.v_st + chunk * 16) * 2);
+  const uint32_t run = static_cast<uint32_t>(8 * a.v_st * 2);
+  uint4 raw[kRuns][2];
+#pragma unroll
+  for (int r = 0; r < kRuns; ++r) {
+    raw[r][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, r * run, 0));
+    raw[r][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16u, r * run, 0));
+  }
+#pragma unroll
+  for (int r = 0; r < kRuns; ++r) {
+    const uint32_t p[8] = {raw[r][0].x, raw[r][0].y, raw[r][0].z, raw[r][0].w,
+                           raw[r][1].x, raw[r][1].y, raw[r][1].z, raw[r][1].w};
+    auto x = [&](int i) { return (i & 1) ? hi16<IN>(p[i >> 1]) : lo16<IN>(p[i >> 1]); };
+    float mn = x(0), mx = mn;
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+      mn = min_nan(mn, x(i));
+      mx = max_nan(mx, x(i));
+    }
+#pragma unroll
+    for (int o = 1; o < kLanes; o <<= 1) {
+      mn = min_nan(mn, __shfl_xor(mn, o, kWave));
+      mx = max_nan(mx, __shfl_xor(mx, o, kWave));
+    }
+    const float s = group_scale<BITS>(mn, mx);
+    const float rc = __builtin_amdgcn_rcpf(s);
+    uint32_t w[kWords];
+    if (fast_group(s, rc)) {
+#pragma unroll
+      for (int k = 0; k < kWords; ++k) {
+        uint32_t d[kPerByte];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+#pragma unroll
+          for (int c = 0; c < kPerByte; ++c)
+            d[c] = put_code_byte(m, code_of<BITS>(x(k * kPer + m * kPerByte + c), mn, s, rc), m ? d[c] : 0u);
+        }
+        w[k] = merge_code_bytes<BITS>(d);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kWords; ++k) {
+        float xs[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) xs[j] = x(k * kPer + j);
+        w[k] = exact_code_word<BITS>(xs, mn, s, rc);
+      }
+    }
+    const int64_t t = g * (8 * VR) + r * 8 + tok;
+    uint32_t *vc = static_cast<uint32_t *>(a.value_code) + h * a.vc_sh + t * a.vc_st + chunk * kWords;
+    if constexpr (kWords == 1) *vc = w[0];
+    else *reinterpret_cast<uint2 *>(vc) = make_uint2(w[0], w[1]);
+    if ((chunk % kLanes) == 0) {
+      const int64_t so = h * a.vs_sh + t * a.vs_st + chunk / kLanes;
+      static_cast<uint16_t *>(a.value_scale)[so] = static_cast<uint16_t>(stat_bits(s, a.stats_dtype));
+      static_cast<uint16_t *>(a.value_min)[so] = static_cast<uint16_t>(stat_bits(mn, a.stats_dtype));
+    }
+  }
+}
+
+// waves per SIMD the register budget is sized for (G raw key pairs per lane)
+template <int G>
+constexpr int kFastPackWaves = G <= 16 ? 8 : G <= 32 ? 6 : 3;
+
+template <int IN, int BITS, int G, int VR>
+__global__ __launch_bounds__(kPackThreads) __attribute__((amdgpu_waves_per_eu(kFastPackWaves<G>))) void
+kivi_pack_fast_kernel(PackArgs a, int64_t key_units, int64_t value_units) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t u = int64_t(blockIdx.x) * (kPackThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  if (u < key_units)
+    fast_key_unit<IN, BITS, G>(a, u, lane);
+  else if (u < key_units + value_units)
+    fast_value_unit<IN, BITS, G, VR>(a, u - key_units, lane);
+}
+
+// Whether uc_kivi_pack's arguments fit kivi_pack_fast_kernel.
+bool fast_pack_fits(const PackArgs &a, int in_dtype, int kb, int vb, int group) {
+  auto al = [](const void *p, int b) { return (reinterpret_cast<uintptr_t>(p) % b) == 0; };
+  const bool shape = a.key && a.value && kb == vb && (kb == 2 || kb == 4) && a.head_dim == 128 &&
+                     (group == 16 || group == 32 || group == 64) && (in_dtype == UC_BF16 || in_dtype == UC_FP16) &&
+                     (a.stats_dtype == UC_BF16 || a.stats_dtype == UC_FP16);
+  if (!shape) return false;
+  const bool in = a.k_sd == 1 && a.v_sd == 1 && a.k_st > 0 && a.v_st > 0 && a.k_sh >= 0 && a.v_sh >= 0 &&
+                  a.k_st % 2 == 0 && a.k_sh % 2 == 0 && al(a.key, 4) && a.v_st % 8 == 0 && a.v_sh % 8 == 0 &&
+                  al(a.value, 16) && int64_t(group) * a.k_st * 2 + 256 < (int64_t(1) << 31) &&
+                  int64_t(group) * a.v_st * 2 + 256 < (int64_t(1) << 31);
+  const bool kout = a.kc_sd == 1 && a.kc_sw % 2 == 0 && a.kc_sh % 2 == 0 && al(a.key_code, 8) && a.ks_sd == 1 &&
+                    a.ks_sg % 2 == 0 && a.ks_sh % 2 == 0 && al(a.key_scale, 4) && al(a.key_min, 4);
+  const bool vout = a.vc_sw == 1 && (kb == 2 || (a.vc_st % 2 == 0 && a.vc_sh % 2 == 0 && al(a.value_code, 8))) &&
+                    al(a.value_code, 4) && a.vs_sg == 1 && al(a.value_scale, 2) && al(a.value_min, 2);
+  return in && kout && vout;
+}
+
+template <int IN, int BITS, int G>
+void launch_pack_fast_g(const PackArgs &a, hipStream_t stream) {
+  const int64_t key_units = a.heads * (a.tokens / G);
+  // value runs of 8 tokens per wave: two for launches of a few waves per SIMD
+  // (a config-1 sequence: 7.7 against 8.0 us), one above (32k tokens: 20.1
+  // against 20.9 us)
+  const int vr = a.heads * a.tokens >= 65536 ? 1 : 2;
+  const int64_t value_units = a.heads * (a.tokens / (8 * vr));
+  const dim3 grid(static_cast<unsigned>(wave_blocks(key_units + value_units)));
+  if (vr == 1)
+    hipLaunchKernelGGL((kivi_pack_fast_kernel<IN, BITS, G, 1>), grid, dim3(kPackThreads), 0, stream, a, key_units,
+                       value_units);
+  else
+    hipLaunchKernelGGL((kivi_pack_fast_kernel<IN, BITS, G, 2>), grid, dim3(kPackThreads), 0, stream, a, key_units,
+                       value_units);
+}
+
+template <int IN, int BITS>
+void launch_pack_fast(const PackArgs &a, int group, hipStream_t stream) {
+  if (group == 16) launch_pack_fast_g<IN, BITS, 16>(a, stream);
+  else if (group == 32) launch_pack_fast_g<IN, BITS, 32>(a, stream);
+  else launch_pack_fast_g<IN, BITS, 64>(a, stream);
+}
 
 template <int IN, int G>
 void launch_pack(const PackArgs &a, int kb, int vb, bool kvec, bool vvec, hipStream_t stream) {
@@ -900,6 +1196,16 @@ extern "C" int uc_kivi_pack(const void *key, int64_t k_st, int64_t k_sh, int64_t
       hipLaunchKernelGGL((kivi_pack_generic_kernel<UC_FP16>), grid, dim3(kPackThreads), 0, s, g);
     else
       hipLaunchKernelGGL((kivi_pack_generic_kernel<UC_FP32>), grid, dim3(kPackThreads), 0, s, g);
+    return check_launch("uc_kivi_pack");
+  }
+  if (fast_pack_fits(a, in_dtype, k_bits, v_bits, group_size)) {
+    if (in_dtype == UC_BF16) {
+      if (k_bits == 2) launch_pack_fast<UC_BF16, 2>(a, group_size, s);
+      else launch_pack_fast<UC_BF16, 4>(a, group_size, s);
+    } else {
+      if (k_bits == 2) launch_pack_fast<UC_FP16, 2>(a, group_size, s);
+      else launch_pack_fast<UC_FP16, 4>(a, group_size, s);
+    }
     return check_launch("uc_kivi_pack");
   }
   const int64_t slabs = (head_dim + 127) / 128;
