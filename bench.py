@@ -108,25 +108,32 @@ def from_dense_throughput(device, rounds=28):
     return nbytes / (ms * 1e-3) / 1e9, ms / BATCH
 
 
-def pack_throughput(device, steps):
+def pack_throughput(device, steps, tokens=TOKENS, residual=RESIDUAL):
     """uc_kivi_pack of one config-1 sequence (8064 packed tokens, 2-bit, G=32)
     into preallocated native-layout outputs, calls back to back: the C-ABI pack
-    path without from_dense's per-cache allocations."""
+    path without from_dense's per-cache allocations.  `tokens` / `residual`
+    give other lengths (the 32k line of --only-pack)."""
 
     from unicache_amd.storage.physical import _native_storage, _pack_native_into
 
-    tq = TOKENS - RESIDUAL
-    key, value = make_kv(TOKENS, seed=26000, device=device)
+    tq = tokens - residual
+    key, value = make_kv(tokens, seed=26000, device=device)
     qk, qv = key[:tq], value[:tq]
     storage = _native_storage(tq, HKV, D, BITS, BITS, GROUP, device)
     stream = torch.cuda.current_stream(device)
     pack = lambda: _pack_native_into(storage, 0, qk, qv, k_bits=BITS, v_bits=BITS, group_size=GROUP)  # noqa: E731
-    ms = time_steps(pack, steps, 3, stream)
+    ms = time_steps(pack, steps, 3, stream, settle_ms=ROW_SETTLE_MS)
     nbytes = 2 * qk.numel() * 2 + tq * 384
     return nbytes / (ms * 1e-3) / 1e9, ms
 
 
-def time_steps(fn, steps, warmup, stream):
+def time_steps(fn, steps, warmup, stream, settle_ms=0.0):
+    """Mean ms per call of fn over `steps` calls timed back to back with HIP
+    events, after `warmup` untimed calls (and, with settle_ms, after running fn
+    for that much GPU time first, so the clocks have ramped up)."""
+
+    if settle_ms:
+        settle(fn, stream, settle_ms=settle_ms)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -144,6 +151,8 @@ def time_steps(fn, steps, warmup, stream):
 # step (untimed, before the W warm-up steps) until SETTLE_MS of GPU time has
 # passed, so the K timed steps see the clocks a decode loop runs at.
 SETTLE_MS = 200.0
+# the same for each operator row (h2o_c3, rows): 30 ms of the operator first
+ROW_SETTLE_MS = 30.0
 
 
 def settle(fn, stream, settle_ms=SETTLE_MS, max_steps=20000):
@@ -296,8 +305,10 @@ def h2o_eviction(device, steps):
     from unicache_amd.storage.kivi_cuda import dense_attention_summary
 
     _, lse = dense_attention_summary(q, key, value)
-    ms_scores = time_steps(lambda: per_kv_head_scores_from_qk(q, key, out=scores, lse=lse), steps, 2, stream)
-    ms_scores_stats = time_steps(lambda: per_kv_head_scores_from_qk(q, key, out=scores.zero_()), steps, 2, stream)
+    ms_scores = time_steps(lambda: per_kv_head_scores_from_qk(q, key, out=scores, lse=lse), steps, 2, stream,
+                           settle_ms=ROW_SETTLE_MS)
+    ms_scores_stats = time_steps(lambda: per_kv_head_scores_from_qk(q, key, out=scores.zero_()), steps, 2, stream,
+                                 settle_ms=ROW_SETTLE_MS)
     spans = [(0, 256), (256, 4096)]
     ids = [torch.arange(lo, hi, device=device) for lo, hi in spans]  # the caller's logical token ids
 
@@ -312,7 +323,7 @@ def h2o_eviction(device, steps):
                  selection_frozen=True)
             for (lo, hi), seg_ids, (target, recent) in zip(spans, ids, budgets)])
 
-    ms_sel = time_steps(select_gather, steps, 2, stream)
+    ms_sel = time_steps(select_gather, steps, 2, stream, settle_ms=ROW_SETTLE_MS)
     retained = sum(s.retained_tokens for s in select_gather())
     keep = torch.ones(tokens, dtype=torch.bool, device=device)
     keep[:256] = False
@@ -320,7 +331,7 @@ def h2o_eviction(device, steps):
     lens = torch.tensor([tokens], device=device)
     ms_compact = time_steps(lambda: TensorCacheStorageBackend.compact(
         key=key, value=value, key_type_ids=None, sample_lens=lens, keep_masks=[keep], sample_lengths=[tokens]),
-        steps, 2, stream)
+        steps, 2, stream, settle_ms=ROW_SETTLE_MS)
     kept = int(keep.sum())
     flop = 2 * lq * HQ * tokens * D
     gather_bytes = 2 * (2 * HKV * retained * D * 2) + 2 * HKV * retained * (8 + 4) + HKV * tokens * 4
@@ -474,7 +485,8 @@ def secondary_rows(device, steps):
     for tokens, label in ((2048, "config 0"), (32768, "32k tokens")):
         k, v = make_kv(tokens, seed=21000 + tokens, device=device)
         ms = time_steps(lambda: (kivi_fake_quant_key(k, bits=BITS, group_size=GROUP),
-                                 kivi_fake_quant_value(v, bits=BITS, group_size=GROUP)), steps, 2, stream)
+                                 kivi_fake_quant_value(v, bits=BITS, group_size=GROUP)), steps, 2, stream,
+                        settle_ms=ROW_SETTLE_MS)
         rows[f"fake_quant_{tokens}"] = _hbm_line(
             f"{label}: kivi_fake_quant_key + kivi_fake_quant_value on [{tokens}, 4, 128] bf16, 2-bit, G=32",
             ms, 2 * 2 * k.numel() * 2)
@@ -500,7 +512,7 @@ def secondary_rows(device, steps):
                                        set_storage_snapshot=lambda r: None, storage_num_kv_heads=HKV)
         return op.execute(ctx)
 
-    ms = time_steps(fq_operator, steps, 2, stream)
+    ms = time_steps(fq_operator, steps, 2, stream, settle_ms=ROW_SETTLE_MS)
     rows["fake_quant_operator_c0"] = _hbm_line(
         "config 0: KIVIQuantizationOperator.execute on a 2048-token segment (last 128 and 16 protected tokens "
         "kept), 2-bit, G=32: masks, row gather, fake quant, write-back into copies of K and V",
@@ -510,7 +522,8 @@ def secondary_rows(device, steps):
     from unicache_amd.storage.kivi_cuda import quantize_kivi_native
 
     k, v = make_kv(32768, seed=21500, device=device)
-    ms = time_steps(lambda: quantize_kivi_native(k, v, k_bits=BITS, v_bits=BITS, group_size=GROUP), steps, 2, stream)
+    ms = time_steps(lambda: quantize_kivi_native(k, v, k_bits=BITS, v_bits=BITS, group_size=GROUP), steps, 2, stream,
+                    settle_ms=ROW_SETTLE_MS)
     rows["pack_32k"] = _hbm_line(
         "quantize_kivi_native of [32768, 4, 128] bf16 K and V, 2-bit, G=32 (codes + fp16 stats out)",
         ms, 2 * k.numel() * 2 + 32768 * 384)
@@ -525,7 +538,7 @@ def secondary_rows(device, steps):
     out_k = torch.empty(tq, HKV, D, dtype=torch.bfloat16, device=device)
     out_v = torch.empty_like(out_k)
     ms = time_steps(lambda: dequantize_kivi_chunk(cache, start=0, stop=tq, dtype=torch.bfloat16, output_key=out_k,
-                                                  output_value=out_v), steps, 2, stream)
+                                                  output_value=out_v), steps, 2, stream, settle_ms=ROW_SETTLE_MS)
     rows["dequantize_chunk_32k"] = _hbm_line(
         f"dequantize_kivi_chunk of {tq} packed 2-bit tokens into bf16 K/V workspaces (GQA 4 x 128)",
         ms, tq * 384 + 2 * tq * HKV * D * 2)
@@ -542,7 +555,7 @@ def secondary_rows(device, steps):
         logits, apply_value = packed_kivi_attention_parts(c0, q1)
         return apply_value(torch.softmax(logits, -1))
 
-    ms = time_steps(parts, steps, 2, stream)
+    ms = time_steps(parts, steps, 2, stream, settle_ms=ROW_SETTLE_MS)
     t_all = c0.quantized_tokens + c0.residual_tokens
     rows["attention_parts_c0"] = _hbm_line(
         f"config 0: packed_kivi_attention_parts ({c0.quantized_tokens} packed + {c0.residual_tokens} residual, "
@@ -553,13 +566,13 @@ def secondary_rows(device, steps):
     lq, tokens = 512, 4096
     k, v = make_kv(tokens, seed=24000, device=device)
     q = torch.randn(lq, HQ, D, device=device).to(torch.bfloat16)
-    ms = time_steps(lambda: gqa_query_key_logits(q, k), max(3, steps // 4), 1, stream)
+    ms = time_steps(lambda: gqa_query_key_logits(q, k), max(3, steps // 4), 1, stream, settle_ms=ROW_SETTLE_MS)
     rows["gqa_logits_c3"] = _hbm_line(
         "config 3 shapes: gqa_query_key_logits, q [512, 28, 128] bf16 x k [4096, 4, 128] -> fp32 [28, 512, 4096]",
         ms, q.numel() * 2 + k.numel() * 2 + HQ * lq * tokens * 4,
         tflops=round(2 * lq * HQ * tokens * D / (ms * 1e-3) / 1e12, 1))
     probs = torch.softmax(gqa_query_key_logits(q, k) / math.sqrt(D), -1).to(torch.bfloat16)
-    ms = time_steps(lambda: gqa_probability_value(probs, v), max(3, steps // 4), 1, stream)
+    ms = time_steps(lambda: gqa_probability_value(probs, v), max(3, steps // 4), 1, stream, settle_ms=ROW_SETTLE_MS)
     rows["gqa_pv_c3"] = _hbm_line(
         "config 3 shapes: gqa_probability_value, p [28, 512, 4096] bf16 x v [4096, 4, 128] -> [28, 512, 128]",
         ms, probs.numel() * 2 + v.numel() * 2 + HQ * lq * D * 2,
@@ -569,7 +582,7 @@ def secondary_rows(device, steps):
     seg = GQAH2OCache.from_dense(k, v, logical_token_ids=torch.arange(tokens, device=device), token_type_id=1,
                                  per_kv_head_scores=torch.rand(HKV, tokens, device=device), target_tokens=tokens,
                                  recent_tokens=0, selection_frozen=True)
-    ms = time_steps(lambda: seg.update_scores(probs), steps, 2, stream)
+    ms = time_steps(lambda: seg.update_scores(probs), steps, 2, stream, settle_ms=ROW_SETTLE_MS)
     rows["h2o_update_scores_c3"] = _hbm_line(
         "config 3 shapes: GQAH2OCache.update_scores, bf16 probabilities [28, 512, 4096] summed per KV head",
         ms, probs.numel() * 2 + 2 * HKV * tokens * 4)
@@ -589,7 +602,7 @@ def secondary_rows(device, steps):
     cu_q = torch.tensor([0, lq, 2 * lq, 3 * lq], dtype=torch.int32)
     cu_k = torch.tensor([0, current[0], current[0] + current[1], sum(current)], dtype=torch.int32)
     ms = time_steps(lambda: run_batched_physical_attention(cq, ck, cv, cu_q, cu_k, [[vae_cache]] * 3), steps, 2,
-                    stream)
+                    stream, settle_ms=ROW_SETTLE_MS)
     flop = sum(4 * lq * HQ * (vae + c) * D for c in current)
     rows["batched_cfg_c2"] = {
         "workload": "three CFG samples of config 2 (1088 queries x 28 heads each) over the 2-bit VAE segment "
@@ -603,7 +616,7 @@ def secondary_rows(device, steps):
     lq = 1088
     summaries = [(torch.randn(lq, HQ, D, device=device).to(torch.bfloat16), torch.randn(HQ, lq, device=device))
                  for _ in range(3)]
-    ms = time_steps(lambda: merge_attention_summaries(summaries), steps, 2, stream)
+    ms = time_steps(lambda: merge_attention_summaries(summaries), steps, 2, stream, settle_ms=ROW_SETTLE_MS)
     rows["lse_merge_c2"] = _hbm_line(
         "config 2: merge_attention_summaries of 3 segment summaries ([1088, 28, 128] bf16 + LSE [28, 1088])",
         ms, (3 + 1) * (lq * HQ * D * 2 + HQ * lq * 4))
@@ -789,7 +802,9 @@ def main():
         return
     if args.only_pack:
         gbs, ms = pack_throughput(device, args.steps)
-        print(json.dumps({"pack_gbs": round(gbs, 2), "pack_ms_per_sequence": round(ms, 5)}))
+        gbs32, ms32 = pack_throughput(device, args.steps, tokens=32768, residual=0)
+        print(json.dumps({"pack_gbs": round(gbs, 2), "pack_ms_per_sequence": round(ms, 5),
+                          "pack_32k_into_gbs": round(gbs32, 2), "pack_32k_into_ms": round(ms32, 5)}))
         return
 
     from unicache_amd.storage.decode import KiviDecodeBatch
