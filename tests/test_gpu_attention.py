@@ -65,6 +65,29 @@ def test_attention_parts_qk_av(device, bits, lq):
     assert_close(f32(out), exp, what="av")
 
 
+@pytest.mark.parametrize("bits,group,tokens,residual,lq", [(2, 16, 200, 32, 1), (4, 32, 250, 20, 3),
+                                                         (2, 128, 1100, 60, 2), (4, 16, 2048, 128, 1)])
+def test_attention_parts_tiles_groups_and_rows(device, bits, group, tokens, residual, lq):
+    # token tiles that mix packed and residual tokens (groups 16 and 32 with
+    # quantized counts of 160 and 224, not multiples of 64), groups 16 to 128,
+    # several query rows per head and a second chunk of 16 rows (lq = 3: 21 rows
+    # per KV head)
+    cache, seg = _pair(tokens, 11, bits, group, residual, device)
+    q = queries(lq, seed=13)
+    logits, apply_value = cache.attention_parts(q.to(device))
+    exp_logits = A.packed_logits(seg, f32(q), kv_dtype="fp32")
+    assert_close(f32(logits), exp_logits, max_abs=2e-3, mean_abs=2e-4, what="logits")
+    probs = torch.softmax(logits, dim=-1).to(torch.bfloat16)
+    out = apply_value(probs)
+    assert_close(f32(out), A.packed_pv(seg, f32(probs), kv_dtype="bf16"), what="av")
+    # fp32 probabilities and an fp16 query
+    logits16, apply16 = cache.attention_parts(q.half().to(device))
+    assert_close(f32(logits16), A.packed_logits(seg, f32(q.half()), kv_dtype="fp32"), max_abs=2e-3,
+                 mean_abs=2e-4, what="fp16-query logits")
+    p32 = torch.softmax(logits16, dim=-1)
+    assert_close(f32(apply16(p32)), A.packed_pv(seg, f32(p32), kv_dtype="bf16"), what="fp32-probability av")
+
+
 @pytest.mark.parametrize("bits", [2, 4])
 def test_decode_summary_config0(device, bits):
     # config 0: 2048 tokens (1920 packed + 128 residual), G=32, q [1, 28, 128]

@@ -8,6 +8,7 @@ raises ``RuntimeError``: the engine has no CPU or torch fallback.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 
@@ -299,6 +300,7 @@ def require_device(*tensors: torch.Tensor | None, what: str) -> torch.device:
     return device
 
 
+@functools.lru_cache(maxsize=256)
 def workspace_bytes(op: int, n_items: int, heads_q: int, query_len: int, head_dim: int, max_tokens: int) -> int:
     size = int(lib().uc_workspace_bytes(op, n_items, heads_q, query_len, head_dim, max_tokens))
     if size < 0:
@@ -306,6 +308,7 @@ def workspace_bytes(op: int, n_items: int, heads_q: int, query_len: int, head_di
     return size
 
 
+@functools.lru_cache(maxsize=256)
 def decode_workspace_bytes(n_items, bits, group_size, heads_q, heads_kv, head_dim, query_len, max_tq, max_tr) -> int:
     size = int(lib().uc_kivi_decode_workspace_bytes(n_items, bits, group_size, heads_q, heads_kv, head_dim,
                                                     query_len, max_tq, max_tr))

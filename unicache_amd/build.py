@@ -29,6 +29,7 @@ SOURCES = [
     "uc_h2o_mfma.hip",
     "uc_compact.hip",
     "uc_stream.hip",
+    "uc_parts.hip",
 ]
 
 # -ffp-contract=off keeps the pack/dequant arithmetic bit-exact (no implicit

@@ -27,6 +27,18 @@ inline int64_t av_num_splits(int64_t heads_q, int64_t query_len, int64_t max_tok
   return (max_tokens + s - 1) / s + 1;
 }
 
+// attention_parts over the kernel-native 2/4-bit layout (uc_parts.hip).
+bool parts_fast_supported(int bits, int group, int64_t head_dim, int stats_dtype, int res_dtype, int64_t r_st,
+                          int64_t r_sh, const void *residual, int64_t residual_tokens);
+int launch_parts_qk(const void *query, int q_dtype, int64_t Lq, int64_t Hq, const void *kc, const void *ks,
+                    const void *km, int sd, int64_t Tq, int64_t cap, int bits, int G, const void *rk, int rd,
+                    int64_t Tr, int64_t r_st, int64_t r_sh, int64_t Hkv, float sm_scale, float *logits,
+                    hipStream_t stream);
+int launch_parts_av(const void *probs, int p_dtype, int64_t p_sh, int64_t p_si, int64_t p_st, int64_t Lq, int64_t Hq,
+                    const void *vc, const void *vs, const void *vm, int sd, int64_t Tq, int64_t cap, int bits, int G,
+                    const void *rv, int rd, int64_t Tr, int64_t r_st, int64_t r_sh, int64_t Hkv, void *out, int od,
+                    void *workspace, int64_t split_tokens, hipStream_t stream);
+
 // MFMA decode (uc_decode_mfma.hip): head_dim 128, 2/4-bit codes.
 #ifndef UC_DECODE_MFMA_NST
 #define UC_DECODE_MFMA_NST 8

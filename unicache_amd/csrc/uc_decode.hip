@@ -590,6 +590,11 @@ extern "C" int uc_kivi_qk(const void *query, int q_dtype, int64_t query_len, int
                          query_len, heads_q, residual_tokens, heads_kv))
     return launch_qk_logits_mfma(q_dtype, query, heads_q * head_dim, head_dim, residual_key, r_st, r_sh, query_len,
                                  heads_q, residual_tokens, heads_kv, sm_scale, logits, as_stream(stream));
+  if (parts_fast_supported(bits, group_size, head_dim, stats_dtype, res_dtype, r_st, r_sh, residual_key,
+                           residual_tokens))
+    return launch_parts_qk(query, q_dtype, query_len, heads_q, key_code, key_scale, key_min, stats_dtype,
+                           quantized_tokens, packed_capacity, bits, group_size, residual_key, res_dtype,
+                           residual_tokens, r_st, r_sh, heads_kv, sm_scale, logits, as_stream(stream));
   PackedView v = parts_view(key_code, key_scale, key_min, nullptr, nullptr, nullptr, quantized_tokens,
                             packed_capacity, bits, group_size, residual_key, nullptr, residual_tokens, r_st, r_sh,
                             heads_kv, head_dim, stats_dtype, res_dtype);
@@ -644,6 +649,11 @@ extern "C" int uc_kivi_av(const void *probs, int p_dtype, int64_t p_sh, int64_t 
                         heads_q / heads_kv * query_len, total))
     return launch_pv_mfma(p_dtype, probs, p_sh, p_si, res_dtype, residual_value, r_st, r_sh, query_len, heads_q, total,
                           heads_kv, out, workspace, s);
+  if (parts_fast_supported(bits, group_size, head_dim, stats_dtype, res_dtype, r_st, r_sh, residual_value,
+                           residual_tokens))
+    return launch_parts_av(probs, p_dtype, p_sh, p_si, p_st, query_len, heads_q, value_code, value_scale, value_min,
+                           stats_dtype, quantized_tokens, packed_capacity, bits, group_size, residual_value, res_dtype,
+                           residual_tokens, r_st, r_sh, heads_kv, out, out_dtype, workspace, split_tokens, s);
   (void)total;
   uc_kivi_item it{};
   it.value_code = value_code; it.value_scale = value_scale; it.value_min = value_min;

@@ -20,6 +20,7 @@ from __future__ import annotations
 import ctypes
 
 import math
+import weakref
 from dataclasses import dataclass
 from typing import Callable
 
@@ -572,6 +573,18 @@ class PackedKIVICache:
 
         if not self.kernel_native_layout or self.key_code is None:
             raise RuntimeError("Packed KIVI attention requires kernel-native layout")
+        views = (self.key_code, self.key_scale, self.key_minimum, self.value_code, self.value_scale,
+                 self.value_minimum)
+        device = device or self.key_code.device
+        # the checks below hold as long as the six tensor objects, their storage
+        # addresses, the token count and the capacity are the ones last checked
+        # (decode and attention_parts calls check them on every call)
+        memo = self.__dict__.get("_layout_memo")
+        state = (self.quantized_tokens, self.packed_capacity, device)
+        if memo is not None and memo[1] == state and all(r() is t for r, t in zip(memo[0], views)):
+            ptrs = tuple(t.data_ptr() for t in views)
+            if ptrs == memo[2][:6]:
+                return memo[2]
         h, d, g, tq = self.num_kv_heads, self.head_dim, self.group_size, self.quantized_tokens
         cap = self.packed_capacity
         vw, vg = d * self.v_bits // 32, d // g
@@ -584,7 +597,6 @@ class PackedKIVICache:
             ("value_scale", torch.float16, (h, tq, vg), (cap * vg, vg, 1)),
             ("value_minimum", torch.float16, (h, tq, vg), (cap * vg, vg, 1)),
         )
-        device = device or self.key_code.device
         ptrs = []
         for name, dtype, shape, stride in expected:
             t = getattr(self, name)
@@ -599,7 +611,9 @@ class PackedKIVICache:
             ptrs.append(t.data_ptr())
         if cap < tq or cap % g:
             raise ValueError("Packed KIVI capacity must be a multiple of group_size covering the packed tokens")
-        return (*ptrs, cap)
+        result = (*ptrs, cap)
+        self.__dict__["_layout_memo"] = (tuple(weakref.ref(t) for t in views), state, result)
+        return result
 
     def native_item(self, query_ptr: int, out_ptr: int, lse_ptr: int | None, *, residual_key_ptr: int | None = None,
                     residual_value_ptr: int | None = None, residual_tokens: int = 0) -> "nat.KiviItem":
