@@ -1028,74 +1028,106 @@ __global__ __launch_bounds__(256) void fake_quant_tokens_kernel(FakeQuantArgs a)
   }
 }
 
+// Fake-quant value of one element of a group whose scale s is finite with a
+// normal reciprocal r (builtin.py:42-53): the code is rint((x - mn) * r), the
+// correctly rounded division deciding within (max_code + 1) 2^-20 of a half
+// step, as in code_of (y lies in [0, max_code + 2^-20] here, so no clamp);
+// then code * s + mn with two roundings.  `near` = 0.5 - (max_code + 1) 2^-20.
+__device__ __forceinline__ float fake_value(float x, float mn, float s, float r, float near) {
+  const float d = sub_rn(x, mn);
+  const float y = mul_rn(d, r);
+  float q = rintf(y);
+  if (fabsf(sub_rn(y, q)) >= near) q = rintf(div_rn(d, s));
+  return add_rn(mul_rn(q, s), mn);
+}
+
+// The generic arithmetic (quant_rint and the clamp) for the other groups.
+__device__ __forceinline__ float fake_value_generic(float x, float mn, float s, float r, float max_code) {
+  const float q = fminf(fmaxf(quant_rint(sub_rn(x, mn), s, r), 0.0f), max_code);
+  return add_rn(mul_rn(q, s), mn);
+}
+
+// fake quant's scale (builtin.py:50: clamp, then divide) from a NaN-propagating
+// range; a NaN range gives the canonical NaN of GroupRange
+__device__ __forceinline__ float fake_scale(float &mn, float &mx, float max_code) {
+  if (mn != mn) {
+    mn = __builtin_nanf("");
+    mx = mn;
+  }
+  return div_rn(clamp_min_nan(sub_rn(mx, mn), kEps), max_code);
+}
+
+// Two 16-bit results packed, each rounded to nearest even (NaN canonical for
+// bf16, as torch's casts).
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float v0, float v1) {
+  return DT == UC_BF16 ? (uint32_t(f32_to_bf16_bits(v0)) | (uint32_t(f32_to_bf16_bits(v1)) << 16))
+                       : (uint32_t(f32_to_f16_bits(v0)) | (uint32_t(f32_to_f16_bits(v1)) << 16));
+}
+
 // The same for head_dim 128 with the group's tokens split over the four
 // waves of a workgroup (workgroup = (group, head), lane = channel pair): each
-// wave holds TPW tokens in registers, the four partial ranges meet in LDS,
-// then every wave quantizes its own tokens.  Four times the waves of the
-// kernel above, a quarter of the serial loads per lane.
+// wave holds TPW tokens in registers as raw 16-bit pairs, the four partial
+// ranges (IEEE minimum / maximum, NaN-propagating) meet in LDS, then every wave
+// quantizes its own tokens.
 template <int DT, int TPW>
 __global__ __launch_bounds__(256) void fake_quant_tokens_split_kernel(FakeQuantArgs a) {
-  __shared__ float rmn[4][kWave], rmx[4][kWave];
-  __shared__ int rnan[4][kWave];
+  __shared__ float rmn[4][2 * kWave], rmx[4][2 * kWave];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int64_t g = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
   const int64_t t0 = g * a.group, n = min(a.group, a.tokens - t0);
   const int64_t w0 = int64_t(wave) * TPW;  // this wave's first token of the group
   const int64_t base = (t0 + w0) * a.st + h * a.sh + 2 * lane;
-  float x0[TPW], x1[TPW];
+  uint32_t raw[TPW];
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const uint32_t pair = w0 + i < n ? *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(a.data) +
-                                                                          base + i * a.st)
-                                     : 0u;
-    x0[i] = half_bits_to_f32<DT>(pair);
-    x1[i] = half_bits_to_f32<DT>(pair >> 16);
-  }
-  GroupRange r0, r1;
-  r0.mn = r1.mn = __builtin_inff();
-  r0.mx = r1.mx = -__builtin_inff();
-  r0.nan = r1.nan = false;
+  for (int i = 0; i < TPW; ++i)
+    raw[i] = w0 + i < n ? *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(a.data) + base +
+                                                              i * a.st)
+                        : 0u;
+  float mn0 = __builtin_inff(), mx0 = -__builtin_inff(), mn1 = __builtin_inff(), mx1 = -__builtin_inff();
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     if (w0 + i < n) {
-      r0.add(x0[i]);
-      r1.add(x1[i]);
+      const float x0 = half_bits_to_f32<DT>(raw[i]), x1 = half_bits_to_f32<DT>(raw[i] >> 16);
+      mn0 = min_nan(mn0, x0);
+      mx0 = max_nan(mx0, x0);
+      mn1 = min_nan(mn1, x1);
+      mx1 = max_nan(mx1, x1);
     }
   }
-  // lane l owns channels 2l, 2l + 1: slots 0 and 1 of a 2-wide LDS row
-  rmn[wave][lane] = r0.mn;
-  rmx[wave][lane] = r0.mx;
-  rnan[wave][lane] = int(r0.nan) | (int(r1.nan) << 1);
+  rmn[wave][2 * lane] = mn0;
+  rmn[wave][2 * lane + 1] = mn1;
+  rmx[wave][2 * lane] = mx0;
+  rmx[wave][2 * lane + 1] = mx1;
   __syncthreads();
-  float mn0 = rmn[0][lane], mx0 = rmx[0][lane];
-  int nan = rnan[0][lane];
 #pragma unroll
-  for (int w = 1; w < 4; ++w) {
-    mn0 = fminf(mn0, rmn[w][lane]);
-    mx0 = fmaxf(mx0, rmx[w][lane]);
-    nan |= rnan[w][lane];
+  for (int w = 0; w < 4; ++w) {
+    mn0 = min_nan(mn0, rmn[w][2 * lane]);
+    mn1 = min_nan(mn1, rmn[w][2 * lane + 1]);
+    mx0 = max_nan(mx0, rmx[w][2 * lane]);
+    mx1 = max_nan(mx1, rmx[w][2 * lane + 1]);
   }
-  __syncthreads();
-  rmn[wave][lane] = r1.mn;
-  rmx[wave][lane] = r1.mx;
-  __syncthreads();
-  float mn1 = rmn[0][lane], mx1 = rmx[0][lane];
+  const float s0 = fake_scale(mn0, mx0, a.max_code), s1 = fake_scale(mn1, mx1, a.max_code);
+  const float r0 = __builtin_amdgcn_rcpf(s0), r1 = __builtin_amdgcn_rcpf(s1);
+  const float near = 0.5f - (a.max_code + 1.0f) * 0x1p-20f;
+  uint16_t *out = static_cast<uint16_t *>(a.out);
+  if (fast_group(s0, r0) && fast_group(s1, r1)) {
 #pragma unroll
-  for (int w = 1; w < 4; ++w) {
-    mn1 = fminf(mn1, rmn[w][lane]);
-    mx1 = fmaxf(mx1, rmx[w][lane]);
-  }
-  if (nan & 1) mn0 = mx0 = __builtin_nanf("");
-  if (nan & 2) mn1 = mx1 = __builtin_nanf("");
-  const float s0 = div_rn(clamp_min_nan(sub_rn(mx0, mn0), kEps), a.max_code);
-  const float s1 = div_rn(clamp_min_nan(sub_rn(mx1, mn1), kEps), a.max_code);
-  const float rcp_s0 = __builtin_amdgcn_rcpf(s0), rcp_s1 = __builtin_amdgcn_rcpf(s1);
+    for (int i = 0; i < TPW; ++i) {
+      if (w0 + i < n) {
+        const float v0 = fake_value(half_bits_to_f32<DT>(raw[i]), mn0, s0, r0, near);
+        const float v1 = fake_value(half_bits_to_f32<DT>(raw[i] >> 16), mn1, s1, r1, near);
+        *reinterpret_cast<uint32_t *>(out + base + i * a.st) = pack2<DT>(v0, v1);
+      }
+    }
+  } else {
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    if (w0 + i < n) {
-      const float c0 = fminf(fmaxf(quant_rint(sub_rn(x0[i], mn0), s0, rcp_s0), 0.0f), a.max_code);
-      const float c1 = fminf(fmaxf(quant_rint(sub_rn(x1[i], mn1), s1, rcp_s1), 0.0f), a.max_code);
-      store_pair<DT>(a.out, base + i * a.st, add_rn(mul_rn(c0, s0), mn0), add_rn(mul_rn(c1, s1), mn1));
+    for (int i = 0; i < TPW; ++i) {
+      if (w0 + i < n) {
+        const float v0 = fake_value_generic(half_bits_to_f32<DT>(raw[i]), mn0, s0, r0, a.max_code);
+        const float v1 = fake_value_generic(half_bits_to_f32<DT>(raw[i] >> 16), mn1, s1, r1, a.max_code);
+        *reinterpret_cast<uint32_t *>(out + base + i * a.st) = pack2<DT>(v0, v1);
+      }
     }
   }
 }
@@ -1120,27 +1152,30 @@ __global__ __launch_bounds__(256) void fake_quant_channels_kernel(FakeQuantArgs 
     x[2 * j] = half_bits_to_f32<DT>(w[j]);
     x[2 * j + 1] = half_bits_to_f32<DT>(w[j] >> 16);
   }
-  GroupRange r;
-  r.init(x[0]);
+  float mn = x[0], mx = x[0];
 #pragma unroll
-  for (int j = 1; j < 8; ++j) r.add(x[j]);
-  for (int o = 1; o < lanes_per_group; o <<= 1) r.merge_xor(o);
+  for (int j = 1; j < 8; ++j) {
+    mn = min_nan(mn, x[j]);
+    mx = max_nan(mx, x[j]);
+  }
+  for (int o = 1; o < lanes_per_group; o <<= 1) {
+    mn = min_nan(mn, __shfl_xor(mn, o, kWave));
+    mx = max_nan(mx, __shfl_xor(mx, o, kWave));
+  }
   if (!active) return;
-  r.finish();
-  const float mn = r.mn;
-  const float s = div_rn(clamp_min_nan(sub_rn(r.mx, mn), kEps), a.max_code);
-  const float rcp_s = __builtin_amdgcn_rcpf(s);
+  const float s = fake_scale(mn, mx, a.max_code);
+  const float r = __builtin_amdgcn_rcpf(s);
   uint32_t o[4];
+  if (fast_group(s, r)) {
+    const float near = 0.5f - (a.max_code + 1.0f) * 0x1p-20f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v[2];
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack2<DT>(fake_value(x[2 * j], mn, s, r, near), fake_value(x[2 * j + 1], mn, s, r, near));
+  } else {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const float c = fminf(fmaxf(quant_rint(sub_rn(x[2 * j + e], mn), s, rcp_s), 0.0f), a.max_code);
-      v[e] = add_rn(mul_rn(c, s), mn);
-    }
-    o[j] = DT == UC_BF16 ? (f32_to_bf16_bits(v[0]) | (uint32_t(f32_to_bf16_bits(v[1])) << 16))
-                         : (f32_to_f16_bits(v[0]) | (uint32_t(f32_to_f16_bits(v[1])) << 16));
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack2<DT>(fake_value_generic(x[2 * j], mn, s, r, a.max_code),
+                       fake_value_generic(x[2 * j + 1], mn, s, r, a.max_code));
   }
   *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.out) + off) = make_uint4(o[0], o[1], o[2], o[3]);
 }
