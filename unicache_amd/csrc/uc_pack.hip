@@ -827,21 +827,22 @@ __global__ __launch_bounds__(256) void dequant_key_native_kernel(DequantArgs a, 
 }
 
 // Keys from token-major storage (channel stride 1 for words and stats) into
-// 16-bit rows with 16-byte alignment: lane = (head, key word, 8 channels),
-// channel octets fastest.  A lane loads its octet's words of the
+// 16-bit rows with 16-byte alignment: lane = (key word, head, 8 channels),
+// channel octets fastest, then heads.  A lane loads its octet's words of the
 // run (two 16-byte loads per word) and their groups' scales and minima (16
 // bytes each), then writes one 16-byte store per token: a wave writes whole
 // 256-byte head rows, four times the bytes per store of the pairwise kernel.
 constexpr int kDqOctetWords = 1;  // key words per lane of the octet kernel: enough lanes to fill the chip
 
 template <int BITS, int OD, int SD>
-__global__ __launch_bounds__(256) void dequant_key_octet_kernel(DequantArgs a, int64_t runs) {
+__device__ __forceinline__ void dequant_key_octet_block(const DequantArgs &a, int64_t runs, int64_t block) {
   constexpr int TPW = 32 / BITS;
   constexpr uint32_t kMask = (1u << BITS) - 1u;
   const int64_t octets = a.head_dim / 8;
-  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t idx = block * 256 + threadIdx.x;
   if (idx >= a.heads * runs * octets) return;
-  const int64_t oc = idx % octets, run = (idx / octets) % runs, h = idx / (octets * runs);
+  // octets, then heads fastest: the lanes of a wave write whole token rows
+  const int64_t oc = idx % octets, h = (idx / octets) % a.heads, run = idx / (octets * a.heads);
   const int64_t c = 8 * oc, stop = a.start + a.count;
   const int64_t w0 = a.start / TPW + run * kDqOctetWords, w_end = (stop + TPW - 1) / TPW;
   const uint32_t *kc = static_cast<const uint32_t *>(a.key_code) + h * a.kc_sh + c;
@@ -891,16 +892,23 @@ __global__ __launch_bounds__(256) void dequant_key_octet_kernel(DequantArgs a, i
   }
 }
 
-// Values: lane = (head, token, word), words fastest: one 4-byte word and its
-// group's stats in, 16 (2-bit) or 8 (4-bit) contiguous channels out.
+// Values: lane = (token, head, word), words fastest, then heads: one 4-byte
+// word and its group's stats in, 16 (2-bit) or 8 (4-bit) contiguous channels
+// out.
+template <int BITS, int OD, int SD>
+__global__ __launch_bounds__(256) void dequant_key_octet_kernel(DequantArgs a, int64_t runs) {
+  dequant_key_octet_block<BITS, OD, SD>(a, runs, blockIdx.x);
+}
+
 template <int BITS, int OD, bool VEC>
-__global__ __launch_bounds__(256) void dequant_value_native_kernel(DequantArgs a) {
+__device__ __forceinline__ void dequant_value_native_block(const DequantArgs &a, int64_t block) {
   constexpr int CPW = 32 / BITS;  // channels per word
   constexpr uint32_t kMask = (1u << BITS) - 1u;
   const int64_t words = a.head_dim / CPW;
-  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t idx = block * 256 + threadIdx.x;
   if (idx >= a.heads * a.count * words) return;
-  const int64_t w = idx % words, n = (idx / words) % a.count, h = idx / (words * a.count);
+  // words, then heads fastest: the lanes of a wave write whole token rows
+  const int64_t w = idx % words, h = (idx / words) % a.heads, n = idx / (words * a.heads);
   const int64_t t = a.start + n;
   const uint32_t word = static_cast<const uint32_t *>(a.value_code)[h * a.vc_sh + t * a.vc_st + w];
   const int64_t so = h * a.vs_sh + t * a.vs_st + ((w * CPW) >> a.lg) * a.vs_sg;
@@ -931,6 +939,22 @@ __global__ __launch_bounds__(256) void dequant_value_native_kernel(DequantArgs a
 #pragma unroll
     for (int p = 0; p < CPW; p += 2) store_pair<OD>(a.out_value, o + p, v[p], v[p + 1]);
   }
+}
+
+template <int BITS, int OD, bool VEC>
+__global__ __launch_bounds__(256) void dequant_value_native_kernel(DequantArgs a) {
+  dequant_value_native_block<BITS, OD, VEC>(a, blockIdx.x);
+}
+
+// Keys (the first key_blocks workgroups, octet form) and values of equal bits
+// in one launch.
+template <int BITS, int OD, int SD, bool VEC>
+__global__ __launch_bounds__(256) void dequant_kv_kernel(DequantArgs a, int64_t runs, int64_t key_blocks) {
+  const int64_t b = blockIdx.x;
+  if (b < key_blocks)
+    dequant_key_octet_block<BITS, OD, SD>(a, runs, b);
+  else
+    dequant_value_native_block<BITS, OD, VEC>(a, b - key_blocks);
 }
 
 // ----------------------------------------------------------- fake quant --
@@ -1318,6 +1342,28 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
                          head_dim % 8 == 0 && kc_sw % 4 == 0 && kc_sh % 4 == 0 && ks_sg % 8 == 0 && ks_sh % 8 == 0 &&
                          o_st % 8 == 0 && o_sh % 8 == 0 && aligned(key_code, 16) && aligned(key_scale, 16) &&
                          aligned(key_min, 16) && aligned(out_key, 16);
+      const int64_t per16 = 16 / out_bytes;
+      const bool vvec = value_code != nullptr && aligned(out_value, 16) && o_st % per16 == 0 && o_sh % per16 == 0 &&
+                        (32 / v_bits) % per16 == 0;
+      if (octet && value_code != nullptr && k_bits == v_bits && vvec) {
+        // keys and values in one launch
+        const int tpw = 32 / k_bits;
+        const int64_t words = (start + count + tpw - 1) / tpw - start / tpw;
+        const int64_t runs = ceil_div(words, int64_t(kDqOctetWords));
+        const int64_t key_blocks = ceil_div(heads * runs * (head_dim / 8), int64_t(256));
+        const int64_t value_blocks = ceil_div(heads * count * (head_dim * v_bits / 32), int64_t(256));
+        const dim3 grid(static_cast<unsigned>(key_blocks + value_blocks));
+        auto go_kv = [&](auto sd_tag) {
+          constexpr int SD = decltype(sd_tag)::value;
+          if (k_bits == 2)
+            hipLaunchKernelGGL((dequant_kv_kernel<2, OD, SD, true>), grid, dim3(256), 0, s, a, runs, key_blocks);
+          else
+            hipLaunchKernelGGL((dequant_kv_kernel<4, OD, SD, true>), grid, dim3(256), 0, s, a, runs, key_blocks);
+        };
+        if (stats_dtype == UC_BF16) go_kv(std::integral_constant<int, UC_BF16>{});
+        else go_kv(std::integral_constant<int, UC_FP16>{});
+        return;
+      }
       if (octet) {
         const int tpw = 32 / k_bits;
         const int64_t words = (start + count + tpw - 1) / tpw - start / tpw;
@@ -1345,9 +1391,7 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
       if (value_code != nullptr) {
         const int64_t n = heads * count * (head_dim * v_bits / 32);
         // 16-byte stores when every run of a word's channels starts on 16 bytes
-        const int64_t per16 = 16 / out_bytes;
-        const bool vec = aligned(out_value, 16) && o_st % per16 == 0 && o_sh % per16 == 0 &&
-                         (32 / v_bits) % per16 == 0;
+        const bool vec = vvec;
         auto go = [&](auto vec_tag) {
           constexpr bool VEC = decltype(vec_tag)::value;
           if (v_bits == 2)
