@@ -15,6 +15,7 @@ numpy oracle on a bounded sample of the same workload, rank 0, N=1).
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -130,19 +131,26 @@ def pack_throughput(device, steps, tokens=TOKENS, residual=RESIDUAL):
 def time_steps(fn, steps, warmup, stream, settle_ms=0.0):
     """Mean ms per call of fn over `steps` calls timed back to back with HIP
     events, after `warmup` untimed calls (and, with settle_ms, after running fn
-    for that much GPU time first, so the clocks have ramped up)."""
+    for that much GPU time first, so the clocks have ramped up).  Python's
+    cyclic garbage collector is paused over the timed calls (collected just
+    before), so a collection pass does not land inside a host-bound line."""
 
     if settle_ms:
         settle(fn, stream, settle_ms=settle_ms)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        fn()
-    stop.record(stream)
-    torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()
+    try:
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        stop.record(stream)
+        torch.cuda.synchronize()
+    finally:
+        gc.enable()
     return start.elapsed_time(stop) / steps
 
 
@@ -182,11 +190,16 @@ def time_steps_each(fn, steps, warmup, stream):
         fn()
     torch.cuda.synchronize()
     events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    events[0].record(stream)
-    for i in range(steps):
-        fn()
-        events[i + 1].record(stream)
-    torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()
+    try:
+        events[0].record(stream)
+        for i in range(steps):
+            fn()
+            events[i + 1].record(stream)
+        torch.cuda.synchronize()
+    finally:
+        gc.enable()
     each = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
     return events[0].elapsed_time(events[-1]) / steps, each
 
