@@ -321,11 +321,12 @@ __device__ __forceinline__ void issue_loads(Prefetch<BITS, G> &pf, const PackedR
     pf.vw[0] = bload128(rg.vcode, (tok * Tl::VWPT + 4 * wq) * 4u);
     pf.vw[1] = bload128(rg.vcode, ((tok + 1) * Tl::VWPT + 4 * wq) * 4u);
   }
-  // Statistics: lanes of stat 0 load scales, of stat 1 minima, each in its
-  // own branch so that every load names one resource for the whole wave (a
-  // resource chosen per lane becomes a loop over its distinct values; the
-  // same speed here).  Two full-wave loads with an out-of-range offset for the
-  // other half, OR-ed, ran 3-7 % slower on the decode lines.
+  // Statistics: lanes of stat 0 load scales, of stat 1 minima.  The compiler
+  // merges the two branches into one load whose resource is chosen per lane,
+  // i.e. a loop over its two values (readfirstlane, compare, masked load).
+  // That form is the fastest measured: two loads masked to their halves and
+  // OR-ed ran 5-7 % slower on the decode lines, and two full-wave loads with
+  // an out-of-range offset for the other half 3-7 % slower.
   {  // key stats [group][D]: GW rows of 256 bytes per stat
     constexpr int NKS = Tl::GW * 16;  // 16-byte chunks per stat
     const int i = lane % NKS, stat = lane / NKS;
