@@ -188,10 +188,12 @@ def test_gqa_helpers(device):
     assert_close(f32(pv), A.gqa_pv(f32(p), f32(value)), what="pv")
 
 
-@pytest.mark.parametrize("lq,tokens,dtype", [(100, 300, torch.bfloat16), (70, 1000, torch.float16)])
+@pytest.mark.parametrize("lq,tokens,dtype", [(100, 300, torch.bfloat16), (70, 1000, torch.float16),
+                                             (90, 301, torch.bfloat16)])
 def test_gqa_logits_mfma_tiles(device, lq, tokens, dtype):
     # >= 64 query rows per KV head take the MFMA logits kernel: ragged row
-    # blocks and key chunks; fp32 accumulation of up to ~100-sized products
+    # blocks and key chunks; fp32 accumulation of up to ~100-sized products.
+    # 301 keys: rows that do not start on 16 bytes take the 4-byte stores
     key, _ = kv_pair(tokens, seed=31, dtype=dtype)
     q = queries(lq, seed=32, dtype=dtype)
     got = gqa_query_key_logits(q.to(device), key.to(device))

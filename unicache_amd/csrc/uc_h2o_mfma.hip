@@ -347,9 +347,10 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
   }
 }
 
-// Logits of dense keys: the S = Q K^T tiles of h2o_scores_kernel written out
-// as scale * S, fp32 [Hq][Lq][T] (physical.py:20-39).  Each store of a
-// (query block, v) covers 16 consecutive keys of four rows.
+// Logits of dense keys, fp32 [Hq][Lq][T] = scale * q . k (physical.py:20-39).
+// The tiles are computed as S^T = K Q^T, so lane (n, k) holds four
+// consecutive keys 16 tb + 4k .. + 3 of row 16 qb + n and writes them with one
+// 16-byte store: a store instruction covers 16 rows x 64 contiguous bytes.
 template <int DT>
 __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3))) void qk_logits_kernel(HsParams p) {
   __shared__ __align__(16) HsShared sh;
@@ -360,20 +361,20 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
   const int64_t rb = it.rb, c = it.c, h = it.h;
   const int64_t t_begin = c * p.chunk, t_end = min(p.T, t_begin + p.chunk);
   const int64_t row0 = rb * kHsRows + wave * kHsRowsPerWave;
+  // 16-byte stores need rows that start on 16 bytes (uniform)
+  const bool vec = (p.T & 3) == 0 && (reinterpret_cast<uintptr_t>(p.logits) & 15) == 0;
 
   typename HsOp<DT>::V qf[kHsQB][4];
   load_queries<DT>(qf, p, h, row0);
-  // start of the logits row of rows 16*qb + 4*kap + v (the rows lane (n, k)
-  // holds in S); -1 past the last row
-  int64_t ro[kHsQB][4];
+  // start of the logits row of row 16*qb + n, the row lane (n, k) holds in
+  // S^T; -1 past the last row
+  int64_t ro[kHsQB];
 #pragma unroll
-  for (int qb = 0; qb < kHsQB; ++qb)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t row = row0 + 16 * qb + 4 * kap + v;
-      const int64_t g = row / p.Lq, i = row % p.Lq;
-      ro[qb][v] = row < p.rows ? ((h * p.group + g) * p.Lq + i) * p.T : -1;
-    }
+  for (int qb = 0; qb < kHsQB; ++qb) {
+    const int64_t row = row0 + 16 * qb + r;
+    const int64_t g = row / p.Lq, i = row % p.Lq;
+    ro[qb] = row < p.rows ? ((h * p.group + g) * p.Lq + i) * p.T : -1;
+  }
   const KeyStream ks(p, h, t_begin, t_end);
   ks.prologue(sh);
   for (int i = 0; i < ks.n_tiles; ++i) {
@@ -385,16 +386,20 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
       typename HsOp<DT>::V kf[4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) kf[kb] = key_frag<DT>(kt, 16 * tb + r, 4 * kb + kap);
-      const int64_t t = t0 + 16 * tb + r;
+      const int64_t t = t0 + 16 * tb + 4 * kap;  // first of this lane's four keys
 #pragma unroll
       for (int qb = 0; qb < kHsQB; ++qb) {
-        f4 s = f4{0, 0, 0, 0};  // lane (n, k): rows 16*qb + 4k + v, key 16*tb + n
+        f4 s = f4{0, 0, 0, 0};  // lane (n, k): keys 16*tb + 4k + v of row 16*qb + n
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) s = HsOp<DT>::mma(qf[qb][kb], kf[kb], s);
-        if (t < t_end) {
+        for (int kb = 0; kb < 4; ++kb) s = HsOp<DT>::mma(kf[kb], qf[qb][kb], s);
+        if (ro[qb] < 0) continue;
+        float *dst = p.logits + ro[qb] + t;
+        if (vec && t + 4 <= t_end) {
+          *reinterpret_cast<f4 *>(dst) = s * p.scale;
+        } else {
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            if (ro[qb][v] >= 0) p.logits[ro[qb][v] + t] = s[v] * p.scale;
+            if (t + v < t_end) dst[v] = s[v] * p.scale;
         }
       }
     }
