@@ -15,7 +15,9 @@ numpy oracle on a bounded sample of the same workload, rank 0, N=1).
 from __future__ import annotations
 
 import argparse
+import functools
 import gc
+import itertools
 import json
 import math
 import os
@@ -100,11 +102,16 @@ def from_dense_throughput(device, rounds=28):
         held = one_round()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(rounds):
-        held = one_round()
-    stop.record()
-    torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()
+    try:
+        start.record()
+        for _ in range(rounds):
+            held = one_round()
+        stop.record()
+        torch.cuda.synchronize()
+    finally:
+        gc.enable()
     ms = start.elapsed_time(stop) / rounds
     return nbytes / (ms * 1e-3) / 1e9, ms / BATCH
 
@@ -118,13 +125,15 @@ def pack_throughput(device, steps, tokens=TOKENS, residual=RESIDUAL):
     from unicache_amd.storage.physical import _native_storage, _pack_native_into
 
     tq = tokens - residual
-    key, value = make_kv(tokens, seed=26000, device=device)
-    qk, qv = key[:tq], value[:tq]
-    storage = _native_storage(tq, HKV, D, BITS, BITS, GROUP, device)
+    nbytes = 2 * tq * HKV * D * 2 + tq * 384
+    calls = []
+    for s in range(rotation(nbytes)):
+        key, value = make_kv(tokens, seed=26000 + s, device=device)
+        storage = _native_storage(tq, HKV, D, BITS, BITS, GROUP, device)
+        calls.append(functools.partial(_pack_native_into, storage, 0, key[:tq], value[:tq], k_bits=BITS, v_bits=BITS,
+                                       group_size=GROUP))
     stream = torch.cuda.current_stream(device)
-    pack = lambda: _pack_native_into(storage, 0, qk, qv, k_bits=BITS, v_bits=BITS, group_size=GROUP)  # noqa: E731
-    ms = time_steps(pack, steps, 3, stream, settle_ms=ROW_SETTLE_MS)
-    nbytes = 2 * qk.numel() * 2 + tq * 384
+    ms = time_steps(cycling(calls), steps, 3, stream, settle_ms=ROW_SETTLE_MS)
     return nbytes / (ms * 1e-3) / 1e9, ms
 
 
@@ -161,6 +170,24 @@ def time_steps(fn, steps, warmup, stream, settle_ms=0.0):
 SETTLE_MS = 200.0
 # the same for each operator row (h2o_c3, rows): 30 ms of the operator first
 ROW_SETTLE_MS = 30.0
+# The MI355X's last-level cache holds 256 MB, so an operator timed back to back
+# on one set of inputs would read part of them from it.  The HBM lines whose
+# working set is smaller cycle through enough distinct input (and output) sets
+# to exceed ROTATE_BYTES together, so the timed calls stream from HBM.
+ROTATE_BYTES = 512 << 20
+
+
+def rotation(footprint, cap=64):
+    """Distinct sets a line with this many bytes per call cycles through."""
+
+    return max(1, min(cap, -(-ROTATE_BYTES // max(1, int(footprint)))))
+
+
+def cycling(calls):
+    """One callable running calls[0], calls[1], ... in turn."""
+
+    it = itertools.cycle(calls)
+    return lambda: next(it)()
 
 
 def settle(fn, stream, settle_ms=SETTLE_MS, max_steps=20000):
@@ -495,14 +522,19 @@ def secondary_rows(device, steps):
 
     # fake quantization (operators/builtin.py:31-65): K over 32-token groups, V over
     # 32-channel groups, bf16 in and out
+    def fake_quant(k, v):
+        return kivi_fake_quant_key(k, bits=BITS, group_size=GROUP), kivi_fake_quant_value(v, bits=BITS,
+                                                                                          group_size=GROUP)
+
     for tokens, label in ((2048, "config 0"), (32768, "32k tokens")):
-        k, v = make_kv(tokens, seed=21000 + tokens, device=device)
-        ms = time_steps(lambda: (kivi_fake_quant_key(k, bits=BITS, group_size=GROUP),
-                                 kivi_fake_quant_value(v, bits=BITS, group_size=GROUP)), steps, 2, stream,
+        nbytes = 2 * 2 * tokens * HKV * D * 2
+        sets = [make_kv(tokens, seed=21000 + tokens + s, device=device) for s in range(rotation(nbytes))]
+        ms = time_steps(cycling([functools.partial(fake_quant, k, v) for k, v in sets]), steps, 2, stream,
                         settle_ms=ROW_SETTLE_MS)
         rows[f"fake_quant_{tokens}"] = _hbm_line(
-            f"{label}: kivi_fake_quant_key + kivi_fake_quant_value on [{tokens}, 4, 128] bf16, 2-bit, G=32",
-            ms, 2 * 2 * k.numel() * 2)
+            f"{label}: kivi_fake_quant_key + kivi_fake_quant_value on [{tokens}, 4, 128] bf16, 2-bit, G=32 "
+            f"({len(sets)} input sets in turn)", ms, nbytes)
+        del sets
 
     # the fake-quant segment operator (operators/builtin.py:281-476) at config 0:
     # a 2048-token segment, the last 128 tokens and 16 protected ones kept
@@ -534,27 +566,35 @@ def secondary_rows(device, steps):
     # native pack (kivi_cuda.py:157-190) of a 32k-token K/V in one call
     from unicache_amd.storage.kivi_cuda import quantize_kivi_native
 
-    k, v = make_kv(32768, seed=21500, device=device)
-    ms = time_steps(lambda: quantize_kivi_native(k, v, k_bits=BITS, v_bits=BITS, group_size=GROUP), steps, 2, stream,
-                    settle_ms=ROW_SETTLE_MS)
+    nbytes = 2 * 32768 * HKV * D * 2 + 32768 * 384
+    sets = [make_kv(32768, seed=21500 + s, device=device) for s in range(rotation(nbytes))]
+    ms = time_steps(cycling([functools.partial(quantize_kivi_native, k, v, k_bits=BITS, v_bits=BITS, group_size=GROUP)
+                             for k, v in sets]), steps, 2, stream, settle_ms=ROW_SETTLE_MS)
     rows["pack_32k"] = _hbm_line(
-        "quantize_kivi_native of [32768, 4, 128] bf16 K and V, 2-bit, G=32 (codes + fp16 stats out)",
-        ms, 2 * k.numel() * 2 + 32768 * 384)
+        "quantize_kivi_native of [32768, 4, 128] bf16 K and V, 2-bit, G=32 (codes + fp16 stats out; "
+        f"{len(sets)} input sets in turn)", ms, nbytes)
+    del sets
 
     # chunked dequantization (kivi_cuda.py:58-93) of a 32k-token packed cache
     tokens = 32768
-    k, v = make_kv(tokens, seed=22000, device=device)
-    cache = PackedKIVICache.from_dense(k, v, logical_token_ids=torch.arange(tokens, device=device), token_type_id=3,
-                                       k_bits=BITS, v_bits=BITS, group_size=GROUP, residual_length=RESIDUAL,
-                                       backend="cuda")
-    tq = cache.quantized_tokens
-    out_k = torch.empty(tq, HKV, D, dtype=torch.bfloat16, device=device)
-    out_v = torch.empty_like(out_k)
-    ms = time_steps(lambda: dequantize_kivi_chunk(cache, start=0, stop=tq, dtype=torch.bfloat16, output_key=out_k,
-                                                  output_value=out_v), steps, 2, stream, settle_ms=ROW_SETTLE_MS)
+    tq = tokens - RESIDUAL
+    nbytes = tq * 384 + 2 * tq * HKV * D * 2
+    calls = []
+    for s in range(rotation(nbytes)):
+        k, v = make_kv(tokens, seed=22000 + s, device=device)
+        cache = PackedKIVICache.from_dense(k, v, logical_token_ids=torch.arange(tokens, device=device),
+                                           token_type_id=3, k_bits=BITS, v_bits=BITS, group_size=GROUP,
+                                           residual_length=RESIDUAL, backend="cuda")
+        assert cache.quantized_tokens == tq
+        out_k = torch.empty(tq, HKV, D, dtype=torch.bfloat16, device=device)
+        calls.append(functools.partial(dequantize_kivi_chunk, cache, start=0, stop=tq, dtype=torch.bfloat16,
+                                       output_key=out_k, output_value=torch.empty_like(out_k)))
+        del k, v
+    ms = time_steps(cycling(calls), steps, 2, stream, settle_ms=ROW_SETTLE_MS)
     rows["dequantize_chunk_32k"] = _hbm_line(
-        f"dequantize_kivi_chunk of {tq} packed 2-bit tokens into bf16 K/V workspaces (GQA 4 x 128)",
-        ms, tq * 384 + 2 * tq * HKV * D * 2)
+        f"dequantize_kivi_chunk of {tq} packed 2-bit tokens into bf16 K/V workspaces (GQA 4 x 128; "
+        f"{len(calls)} caches in turn)", ms, nbytes)
+    del calls
 
     # packed attention parts (kivi_cuda.py:238-329): logits then P.V at config 0
     tokens = 2048
@@ -584,10 +624,17 @@ def secondary_rows(device, steps):
         "config 3 shapes: gqa_query_key_logits, q [512, 28, 128] bf16 x k [4096, 4, 128] -> fp32 [28, 512, 4096]",
         ms, q.numel() * 2 + k.numel() * 2 + HQ * lq * tokens * 4,
         tflops=round(2 * lq * HQ * tokens * D / (ms * 1e-3) / 1e12, 1))
-    probs = torch.softmax(gqa_query_key_logits(q, k) / math.sqrt(D), -1).to(torch.bfloat16)
-    ms = time_steps(lambda: gqa_probability_value(probs, v), max(3, steps // 4), 1, stream, settle_ms=ROW_SETTLE_MS)
+    p_bytes = HQ * lq * tokens * 2
+    prob_sets = []
+    for s in range(rotation(p_bytes)):
+        qs = q if s == 0 else torch.randn(lq, HQ, D, device=device).to(torch.bfloat16)
+        prob_sets.append(torch.softmax(gqa_query_key_logits(qs, k) / math.sqrt(D), -1).to(torch.bfloat16))
+    probs = prob_sets[0]
+    ms = time_steps(cycling([functools.partial(gqa_probability_value, p, v) for p in prob_sets]), max(3, steps // 4),
+                    1, stream, settle_ms=ROW_SETTLE_MS)
     rows["gqa_pv_c3"] = _hbm_line(
-        "config 3 shapes: gqa_probability_value, p [28, 512, 4096] bf16 x v [4096, 4, 128] -> [28, 512, 128]",
+        "config 3 shapes: gqa_probability_value, p [28, 512, 4096] bf16 x v [4096, 4, 128] -> [28, 512, 128] "
+        f"({len(prob_sets)} probability sets in turn)",
         ms, probs.numel() * 2 + v.numel() * 2 + HQ * lq * D * 2,
         tflops=round(2 * lq * HQ * tokens * D / (ms * 1e-3) / 1e12, 1))
 
@@ -595,11 +642,13 @@ def secondary_rows(device, steps):
     seg = GQAH2OCache.from_dense(k, v, logical_token_ids=torch.arange(tokens, device=device), token_type_id=1,
                                  per_kv_head_scores=torch.rand(HKV, tokens, device=device), target_tokens=tokens,
                                  recent_tokens=0, selection_frozen=True)
-    ms = time_steps(lambda: seg.update_scores(probs), steps, 2, stream, settle_ms=ROW_SETTLE_MS)
+    ms = time_steps(cycling([functools.partial(seg.update_scores, p) for p in prob_sets]), steps, 2, stream,
+                    settle_ms=ROW_SETTLE_MS)
     rows["h2o_update_scores_c3"] = _hbm_line(
-        "config 3 shapes: GQAH2OCache.update_scores, bf16 probabilities [28, 512, 4096] summed per KV head",
+        "config 3 shapes: GQAH2OCache.update_scores, bf16 probabilities [28, 512, 4096] summed per KV head "
+        f"({len(prob_sets)} probability sets in turn)",
         ms, probs.numel() * 2 + 2 * HKV * tokens * 4)
-    del probs
+    del probs, prob_sets
 
     # batched physical attention (adapters/bagel.py:773-980): three CFG samples of
     # config 2's queries over the packed VAE segment plus their own bf16 keys
