@@ -102,7 +102,6 @@ def from_dense_throughput(device, rounds=28):
         held = one_round()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    gc.collect()
     gc.disable()
     try:
         start.record()
@@ -141,15 +140,16 @@ def time_steps(fn, steps, warmup, stream, settle_ms=0.0):
     """Mean ms per call of fn over `steps` calls timed back to back with HIP
     events, after `warmup` untimed calls (and, with settle_ms, after running fn
     for that much GPU time first, so the clocks have ramped up).  Python's
-    cyclic garbage collector is paused over the timed calls (collected just
-    before), so a collection pass does not land inside a host-bound line."""
+    cyclic garbage collector is paused over the timed calls, so a collection
+    pass does not land inside a host-bound line.  It is not run just before
+    them: a full collection here idled the GPU for ~45 ms between the clock
+    settling and the timed calls, which then ran on re-ramping clocks."""
 
     if settle_ms:
         settle(fn, stream, settle_ms=settle_ms)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    gc.collect()
     gc.disable()
     try:
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -217,7 +217,6 @@ def time_steps_each(fn, steps, warmup, stream):
         fn()
     torch.cuda.synchronize()
     events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    gc.collect()
     gc.disable()
     try:
         events[0].record(stream)
