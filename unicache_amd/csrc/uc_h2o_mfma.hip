@@ -667,12 +667,12 @@ __global__ __launch_bounds__(64) void h2o_reduce_kernel(const float *partial, in
   const float *src = partial + idx;  // (rb * Hkv + h) * T + t = rb * Hkv * T + idx
   const int64_t stride = Hkv * T;
   float s = 0.0f;
-  for (int64_t rb0 = 0; rb0 < row_blocks; rb0 += 8) {
-    float v[8];
+  for (int64_t rb0 = 0; rb0 < row_blocks; rb0 += 16) {  // 16 loads in flight: config 3's 14 row blocks in one round
+    float v[16];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = rb0 + j < row_blocks ? src[(rb0 + j) * stride] : 0.0f;
+    for (int j = 0; j < 16; ++j) v[j] = rb0 + j < row_blocks ? src[(rb0 + j) * stride] : 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += v[j];
+    for (int j = 0; j < 16; ++j) s += v[j];
   }
   scores[idx] = accumulate ? scores[idx] + s : s;
 }
