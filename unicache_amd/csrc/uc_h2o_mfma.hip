@@ -82,14 +82,18 @@ struct HsItem {
   bool valid;
 };
 
+// 32-bit arithmetic: the launch keeps the grid and every item count below 2^31
+// (64-bit divisions cost the scalar unit a few hundred instructions each).
 __device__ __forceinline__ HsItem hs_item(const HsParams &p) {
-  const int64_t id = blockIdx.x;
-  const int64_t w = (id % kXcds) * p.per_xcd + id / kXcds;
+  const uint32_t id = blockIdx.x;
+  const uint32_t chunks = static_cast<uint32_t>(p.chunks), row_blocks = static_cast<uint32_t>(p.row_blocks);
+  const uint32_t w = (id % kXcds) * static_cast<uint32_t>(p.per_xcd) + id / kXcds;
   HsItem it;
-  it.valid = w < p.items;
-  it.c = w % p.chunks;
-  it.rb = (w / p.chunks) % p.row_blocks;
-  it.h = w / (p.chunks * p.row_blocks);
+  it.valid = w < static_cast<uint32_t>(p.items);
+  const uint32_t q = w / chunks;
+  it.c = w - q * chunks;
+  it.rb = q % row_blocks;
+  it.h = q / row_blocks;
   return it;
 }
 
@@ -267,6 +271,11 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
   const int64_t rb = it.rb, c = it.c, h = it.h;
   const int64_t t_begin = c * p.chunk, t_end = min(p.T, t_begin + p.chunk);
   const int64_t row0 = rb * kHsRows + wave * kHsRowsPerWave;
+  // the first key tiles are requested before the query rows and the
+  // normaliser, so the three latencies overlap (the normaliser is used before
+  // the first tile, and a use waits for every load issued before it)
+  const KeyStream ks(p, h, t_begin, t_end);
+  ks.prologue(sh);
 
   typename HsOp<DT>::V qf[kHsQB][4];
   load_queries<DT>(qf, p, h, row0);
@@ -276,9 +285,10 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
   float bias;
   if (p.lse != nullptr) {  // probabilities against the caller's normaliser
     const int64_t row = row0 + lane;
-    const int64_t rc = row < p.rows ? row : 0;
-    const int64_t g = rc / p.Lq, i = rc % p.Lq;
-    bias = row < p.rows ? p.lse[(h * p.group + g) * p.Lq + i] * kLog2e : __builtin_inff();
+    const uint32_t rc = row < p.rows ? static_cast<uint32_t>(row) : 0u, lq = static_cast<uint32_t>(p.Lq);
+    const uint32_t g = rc / lq, i = rc - g * lq;
+    const float l = p.lse[(h * p.group + g) * p.Lq + i];  // row rc exists: loaded unconditionally
+    bias = row < p.rows ? l * kLog2e : __builtin_inff();
   } else {
     const float2 *src = p.ml + (h * p.row_blocks + rb) * p.chunks * kHsRows + wave * kHsRowsPerWave + lane;
     float mt = kNegInf, lt = 0.0f;
@@ -295,8 +305,6 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
     }
     bias = row0 + lane < p.rows ? mt + __log2f(lt) : __builtin_inff();
   }
-  const KeyStream ks(p, h, t_begin, t_end);
-  ks.prologue(sh);
   float nb[kHsQB][4];  // -bias of rows 16*qb + 4k + v, the rows lane (n, k) sees in Q K^T
 #pragma unroll
   for (int qb = 0; qb < kHsQB; ++qb)
