@@ -372,19 +372,22 @@ __global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(3)))
   // 16-byte stores need rows that start on 16 bytes (uniform)
   const bool vec = (p.T & 3) == 0 && (reinterpret_cast<uintptr_t>(p.logits) & 15) == 0;
 
+  // the first key tiles are requested before the query rows, so the two
+  // latencies overlap
+  const KeyStream ks(p, h, t_begin, t_end);
+  ks.prologue(sh);
   typename HsOp<DT>::V qf[kHsQB][4];
   load_queries<DT>(qf, p, h, row0);
   // start of the logits row of row 16*qb + n, the row lane (n, k) holds in
-  // S^T; -1 past the last row
+  // S^T; -1 past the last row (rows < 2^31: 32-bit division)
   int64_t ro[kHsQB];
 #pragma unroll
   for (int qb = 0; qb < kHsQB; ++qb) {
     const int64_t row = row0 + 16 * qb + r;
-    const int64_t g = row / p.Lq, i = row % p.Lq;
+    const uint32_t lq = static_cast<uint32_t>(p.Lq), g = static_cast<uint32_t>(row) / lq;
+    const uint32_t i = static_cast<uint32_t>(row) - g * lq;
     ro[qb] = row < p.rows ? ((h * p.group + g) * p.Lq + i) * p.T : -1;
   }
-  const KeyStream ks(p, h, t_begin, t_end);
-  ks.prologue(sh);
   for (int i = 0; i < ks.n_tiles; ++i) {
     ks.acquire(sh, i);
     const int64_t t0 = t_begin + int64_t(i) * kHsTile;
