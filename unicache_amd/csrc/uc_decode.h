@@ -47,7 +47,7 @@ constexpr int64_t kDecodeMfmaNst = UC_DECODE_MFMA_NST;  // super-tiles per packe
 bool decode_mfma_supported(int bits, int group, int64_t head_dim, int64_t rows);
 int64_t decode_mfma_split_tokens(int bits, int64_t nst);
 int64_t decode_mfma_num_splits(int bits, int64_t nst, int64_t max_tq, int64_t max_tr);
-int64_t decode_mfma_res_split_tokens();
+int64_t decode_mfma_res_split_tokens(int64_t max_tr);
 int64_t decode_mfma_workspace_bytes(int64_t n_items, int64_t heads_kv, int64_t splits);
 int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single, int64_t n_items, int bits,
                        int group_size, int64_t Hq, int64_t Hkv, int64_t Lq, int q_dtype, int res_dtype,

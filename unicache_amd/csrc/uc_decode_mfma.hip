@@ -49,7 +49,13 @@ using namespace mf;
 constexpr int kXcds = 8;  // XCDs of an MI355X; workgroup i of a launch runs on XCD i % 8
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
-constexpr int kResWaveTokens = 64;  // residual tokens per wave per residual split (4 tiles)
+// Residual tokens per wave of a residual split: 32 (2 tiles) when every
+// item's residual fits one split that way (the usual R = 128 window: all four
+// waves busy), else 64 (4 tiles; long dense segments then need half the splits).
+constexpr int kResWaveTokensShort = 32, kResWaveTokensLong = 64;
+inline int64_t res_wave_tokens(int64_t max_tr) {
+  return max_tr <= kWaves * kResWaveTokensShort ? kResWaveTokensShort : kResWaveTokensLong;
+}
 constexpr int kWgPerCu = 3;         // resident workgroups per CU (LDS: ~51 KB each; <= 168 VGPRs)
 constexpr float kLazyLog2 = 8.0f;   // softmax reference slack (log2 units)
 
@@ -148,6 +154,7 @@ struct MfmaParams {
   int64_t Hq, Hkv, Lq, group, rows;
   int64_t splits_packed, splits_total, nst;  // nst: super-tiles per packed split
   int64_t segs;                              // consecutive items that share one query and output
+  int64_t res_wave;                          // residual tokens per wave of a residual split (32 or 64)
   int64_t units;                             // items x KV heads
   int64_t super_tokens;                      // tokens per super-tile (16 key words)
   int xcd_grouped;                           // splits of a unit on one XCD (see the kernel)
@@ -163,7 +170,7 @@ struct MfmaParams {
 // segment table whose items differ in length launches cheap empty splits.
 __device__ __forceinline__ bool split_has_work(int64_t split, int64_t tq, int64_t tr, const MfmaParams &p) {
   const int64_t splits_res = p.splits_total - p.splits_packed;
-  return split >= splits_res ? (split - splits_res) * p.super_tokens < tq : split * kWaves * kResWaveTokens < tr;
+  return split >= splits_res ? (split - splits_res) * p.super_tokens < tq : split * kWaves * p.res_wave < tr;
 }
 
 // Online-softmax state of one wave.  The output is accumulated transposed
@@ -773,7 +780,7 @@ __device__ __forceinline__ void packed_split(DecShared<BITS, G> &sh, const _Floa
 }
 
 // --------------------------------------------------------- residual path --
-// Dense residual tokens [tw, tw + kResWaveTokens) of this wave ([Tr, Hkv, 128]
+// Dense residual tokens [tw, tw + RWT) of this wave ([Tr, Hkv, 128]
 // contiguous, bf16 or fp16), converted to fp16 for the same MFMAs; rows past
 // Tr read as zero through the buffer range check and are masked.
 template <int RD>
@@ -799,7 +806,7 @@ __device__ __forceinline__ h8 channel_selector(int lane, int par) {
   return b;
 }
 
-template <int RD>
+template <int RD, int RWT>
 __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], const uc_kivi_item &it, int64_t h,
                                                int64_t tr0, const MfmaParams &p, WaveState &st) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -812,8 +819,8 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
   // byte offset of token row t of this head; rows past Tr repeat the last row
   // (their probabilities are 0, and its values are finite data)
   const auto row_off = [&](int64_t t) { return static_cast<uint32_t>((min(t, Tr - 1) * ts + h * hs) * 2); };
-  const int64_t tw = tr0 + wave * kResWaveTokens;
-  constexpr int kTiles = kResWaveTokens / 16;
+  const int64_t tw = tr0 + wave * RWT;
+  constexpr int kTiles = RWT / 16;
   const h8 csel[2] = {channel_selector(lane, 0), channel_selector(lane, 1)};
   f4 acc[kTiles];
 #pragma unroll
@@ -826,7 +833,7 @@ __device__ __forceinline__ void residual_split(const _Float16 (*sq)[kQPad], cons
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[b][v] *= p.scale_log2;
   }
-  const int valid = static_cast<int>(min<int64_t>(int64_t(kResWaveTokens), Tr - tw));
+  const int valid = static_cast<int>(min<int64_t>(int64_t(RWT), Tr - tw));
   softmax_tiles<kTiles, true>(acc, valid, st, kap);
   // O^T += V^T P^T: a lane loads 8 channels of one token per 32-channel
   // block; a selection MFMA turns a tile of them into the A layout of
@@ -901,8 +908,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   if (split >= splits_res) {
     packed_split<BITS, G, FOLD>(sh, sq, sones, it, h, split - splits_res, p, st);
   } else {
-    const int64_t tr0 = split * kWaves * kResWaveTokens;
-    if (tr0 + wave * kResWaveTokens < it.residual_tokens) residual_split<RD>(sq, it, h, tr0, p, st);
+    const int64_t tr0 = split * kWaves * p.res_wave;
+    if (tr0 + wave * p.res_wave < it.residual_tokens) {
+      if (p.res_wave == kResWaveTokensShort) residual_split<RD, kResWaveTokensShort>(sq, it, h, tr0, p, st);
+      else residual_split<RD, kResWaveTokensLong>(sq, it, h, tr0, p, st);
+    }
   }
 
   // ---- merge the waves; lane (n, k) holds query n, channels 16 b + 4 k + v
@@ -1074,11 +1084,11 @@ __global__ __launch_bounds__(kCombineMaxThreads) void decode_mfma_combine(const 
 // split x tokens per super-tile).
 int64_t decode_mfma_split_tokens(int bits, int64_t nst) { return nst * 16 * (32 / bits); }
 
-int64_t decode_mfma_res_split_tokens() { return kWaves * kResWaveTokens; }
+int64_t decode_mfma_res_split_tokens(int64_t max_tr) { return kWaves * res_wave_tokens(max_tr); }
 
 // Splits per (item, KV head): packed splits, then residual splits.
 int64_t decode_mfma_num_splits(int bits, int64_t nst, int64_t max_tq, int64_t max_tr) {
-  return ceil_div(max_tq, decode_mfma_split_tokens(bits, nst)) + ceil_div(max_tr, decode_mfma_res_split_tokens());
+  return ceil_div(max_tq, decode_mfma_split_tokens(bits, nst)) + ceil_div(max_tr, decode_mfma_res_split_tokens(max_tr));
 }
 
 bool decode_mfma_supported(int bits, int group, int64_t D, int64_t rows) {
@@ -1148,6 +1158,7 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   p.Hq = Hq; p.Hkv = Hkv; p.Lq = Lq; p.group = Hq / Hkv; p.rows = p.group * Lq;
   p.splits_packed = ceil_div(max_tq, s_tok);
   p.splits_total = decode_mfma_num_splits(bits, nst, max_tq, max_tr);
+  p.res_wave = res_wave_tokens(max_tr);
   p.nst = nst;
   p.segs = segs;
   p.scale_log2 = sm_scale * kLog2e;
