@@ -156,6 +156,29 @@ def test_batched_decode_many_units_ragged(device, bits):
         check_summary(batch.outputs[i], batch.lses[i], segs[i], qs[i], what=f"item {i} ({lengths[i]} tokens)")
 
 
+@pytest.mark.parametrize("residuals", [(1, 31, 32, 33, 64, 100, 127, 128), (1, 97, 128, 129, 200, 255, 256, 257)])
+def test_batched_decode_residual_split_sizes(device, residuals):
+    # residual splits take 32 tokens a wave when the longest residual of the
+    # launch fits one split that way (<= 128 tokens) and 64 otherwise: lengths
+    # around both rules, partial waves and tiles, and one item with a single
+    # packed group (dense segments without packed tokens: the segment tables
+    # of test_gpu_mixed.py)
+    from unicache_amd.storage.decode import KiviDecodeBatch
+
+    caches, segs, qs = [], [], []
+    for i, tr in enumerate(residuals):
+        packed = 32 if i == len(residuals) - 2 else 512
+        c, s = _pair(packed + tr, 80 + i, 2, 32, tr, device)
+        assert c.quantized_tokens == packed and c.residual_tokens == tr
+        caches.append(c)
+        segs.append(s)
+        qs.append(queries(1, seed=90 + i))
+    batch = KiviDecodeBatch(caches, [q.to(device) for q in qs])
+    batch.run()
+    for i, tr in enumerate(residuals):
+        check_summary(batch.outputs[i], batch.lses[i], segs[i], qs[i], what=f"item {i} (residual {tr})")
+
+
 @pytest.mark.parametrize("hq,hkv,lq", [(32, 4, 1), (8, 4, 2), (16, 2, 1), (28, 4, 2), (12, 4, 3)])
 def test_decode_query_rows_around_the_fold(device, hq, hkv, lq):
     # 2-bit G=32 decode with at most 8 query rows per KV head (query heads per
