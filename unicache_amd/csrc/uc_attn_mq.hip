@@ -248,7 +248,6 @@ struct DeqLane {
 template <int BITS>
 __device__ __forceinline__ DeqLane deq_lane(int tid_h) {
   constexpr int TPW = 32 / BITS;
-  asm volatile("" : "+v"(tid_h));  // recomputed at each use, not held across the tile loop
   const uint32_t cb = tid_h & 15, tq = tid_h >> 4;
   const uint32_t a = 4 * (tq % (TPW / 4));  // first token of the thread within its word
   DeqLane d;
@@ -295,7 +294,6 @@ __device__ __forceinline__ void load_packed(PackedRegs<BITS> &pr, const PackedHe
   constexpr int TPW = 32 / BITS, VW = kD / TPW;
   const int64_t Tq = ph.tokens;
   const int vstat = (kD >> gshift) * 2;  // bytes of a token's value stats
-  asm volatile("" : "+v"(tid_h));  // lane offsets recomputed here, not held across the tile loop
   const Rsrc kc = make_rsrc(ph.kc, (Tq / TPW) * 512);
   const Rsrc ks = make_rsrc(ph.ks, (Tq >> gshift) * 256);
   const Rsrc km = make_rsrc(ph.km, (Tq >> gshift) * 256);
@@ -357,8 +355,6 @@ __device__ __forceinline__ void write_chunk(uint32_t addr, u32x4 v) { *(lds_u4w)
 template <int BITS>
 __device__ __forceinline__ void store_keys(const PackedRegs<BITS> &pr, int tid_h, uint32_t slot, uint32_t magic) {
   DeqLane dl = deq_lane<BITS>(tid_h);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(dl.kaddr[i]));
   u32x4 o[4];  // [token i][channel pair]
 #pragma unroll
   for (int pi = 0; pi < 4; ++pi) {
@@ -375,8 +371,6 @@ __device__ __forceinline__ void store_keys(const PackedRegs<BITS> &pr, int tid_h
 template <int BITS>
 __device__ __forceinline__ void store_values(const PackedRegs<BITS> &pr, int tid_h, uint32_t slot, uint32_t magic) {
   DeqLane dl = deq_lane<BITS>(tid_h);
-#pragma unroll
-  for (int b = 0; b < 2; ++b) asm volatile("" : "+v"(dl.vaddr[b]));
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     // the token's fp16 scale and minimum in both halves
@@ -523,12 +517,6 @@ template <int DT, int BUF, bool HOOK, class Hook>
 __device__ __forceinline__ void compute_tile(FragLane fl, const u32x4 (&qf)[2][4], int valid, float scale_log2,
                                              MqState &st, Hook &&hook) {
   constexpr uint32_t kBuf = BUF * kSlotBytes;
-  // opaque to loop-invariant code motion: the constant parts of the addresses
-  // below stay next to their reads and fold into the instructions' offsets
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(fl.ak[kb]));
-#pragma unroll
-  for (int cb = 0; cb < 8; ++cb) asm volatile("" : "+v"(fl.av[cb]));
   using Op = Mma<DT>;
   const int lane = threadIdx.x & 63;
   const int kap = lane >> 4;
