@@ -249,7 +249,8 @@ __device__ __forceinline__ void stage_queries_t(_Float16 (*sq)[kQPad], const voi
   const int src = fold ? (n & 7) : n;
   uint4 raw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
   if (src < p.rows) {
-    const int64_t g = src / p.Lq, i = src % p.Lq;
+    const int lq = static_cast<int>(p.Lq), g32 = src / lq;
+    const int64_t g = g32, i = src - g32 * lq;
     const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(query) +
                                                        (i * p.Hq + h * p.group + g) * kD + d0);
     raw[0] = src[0];
@@ -869,19 +870,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   // workgroup there is split k % S of unit (item, KV head) u = 8 (k / S) + i % 8,
   // so the S splits of a unit are dispatched back to back on one XCD and share
   // its L2.  A launch of few units spreads each unit's splits over the XCDs.
-  int64_t u, split;
+  // 32-bit index arithmetic (the launch keeps the grid below 2^31; a 64-bit
+  // division costs the scalar unit a few hundred instructions)
+  const uint32_t splits = static_cast<uint32_t>(p.splits_total), hkv = static_cast<uint32_t>(p.Hkv);
+  uint32_t u32, split32;
   if (p.xcd_grouped) {
-    const int64_t x = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
-    u = (k / p.splits_total) * kXcds + x;
-    split = k % p.splits_total;
+    const uint32_t x = blockIdx.x % kXcds, k = blockIdx.x / kXcds, q = k / splits;
+    u32 = q * kXcds + x;
+    split32 = k - q * splits;
   } else {
-    u = blockIdx.x / p.splits_total;
-    split = blockIdx.x % p.splits_total;
+    u32 = blockIdx.x / splits;
+    split32 = blockIdx.x - u32 * splits;
   }
-  if (u >= p.units) return;  // uniform: the whole workgroup leaves
-  const int64_t item = u / p.Hkv;
+  if (u32 >= static_cast<uint32_t>(p.units)) return;  // uniform: the whole workgroup leaves
+  const int64_t split = split32;
+  const uint32_t item32 = u32 / hkv;
+  const int64_t item = item32;
   const uc_kivi_item it = TABLE ? items[item] : ai.v[item];
-  const int64_t h = u % p.Hkv;
+  const int64_t h = u32 - item32 * hkv;
   if (!split_has_work(split, it.quantized_tokens, it.residual_tokens, p)) {  // uniform
     // only the statistics: (-inf, 0) gives the split weight 0 in the combine,
     // which then never reads its (unwritten) partial output
@@ -1183,8 +1189,9 @@ int launch_decode_mfma(const uc_kivi_item *items_dev, const uc_kivi_item *single
   p.units = n_items * Hkv;
   p.super_tokens = 16 * (32 / bits);
   p.xcd_grouped = p.units >= 4 * kXcds;  // at most one unit of imbalance per XCD in four
-  const dim3 grid(static_cast<unsigned>((p.xcd_grouped ? ceil_div(p.units, int64_t(kXcds)) * kXcds : p.units) *
-                                        p.splits_total));
+  const int64_t n_groups = (p.xcd_grouped ? ceil_div(p.units, int64_t(kXcds)) * kXcds : p.units) * p.splits_total;
+  UC_REQUIRE(n_groups < (int64_t(1) << 31), "decode: grid too large (%lld workgroups)", (long long)n_groups);
+  const dim3 grid(static_cast<unsigned>(n_groups));
   if (bits == 2) {
     if (group_size == 32) launch_group<2, 32>(table, res_dtype, grid, stream, items_dev, one, p);
     else if (group_size == 64) launch_group<2, 64>(table, res_dtype, grid, stream, items_dev, one, p);
