@@ -842,7 +842,10 @@ __device__ __forceinline__ void dequant_key_octet_block(const DequantArgs &a, in
   const int64_t idx = block * 256 + threadIdx.x;
   if (idx >= a.heads * runs * octets) return;
   // octets, then heads fastest: the lanes of a wave write whole token rows
-  const int64_t oc = idx % octets, h = (idx / octets) % a.heads, run = idx / (octets * a.heads);
+  // (32-bit divisions: the launch keeps the index below 2^31)
+  const uint32_t i32 = static_cast<uint32_t>(idx), oct32 = static_cast<uint32_t>(octets);
+  const uint32_t hd32 = static_cast<uint32_t>(a.heads), q = i32 / oct32, r32 = q / hd32;
+  const int64_t oc = i32 - q * oct32, h = q - r32 * hd32, run = r32;
   const int64_t c = 8 * oc, stop = a.start + a.count;
   const int64_t w0 = a.start / TPW + run * kDqOctetWords, w_end = (stop + TPW - 1) / TPW;
   const uint32_t *kc = static_cast<const uint32_t *>(a.key_code) + h * a.kc_sh + c;
@@ -908,7 +911,10 @@ __device__ __forceinline__ void dequant_value_native_block(const DequantArgs &a,
   const int64_t idx = block * 256 + threadIdx.x;
   if (idx >= a.heads * a.count * words) return;
   // words, then heads fastest: the lanes of a wave write whole token rows
-  const int64_t w = idx % words, h = (idx / words) % a.heads, n = idx / (words * a.heads);
+  // (32-bit divisions: the launch keeps the index below 2^31)
+  const uint32_t i32 = static_cast<uint32_t>(idx), wd32 = static_cast<uint32_t>(words);
+  const uint32_t hd32 = static_cast<uint32_t>(a.heads), q = i32 / wd32, n32 = q / hd32;
+  const int64_t w = i32 - q * wd32, h = q - n32 * hd32, n = n32;
   const int64_t t = a.start + n;
   const uint32_t word = static_cast<const uint32_t *>(a.value_code)[h * a.vc_sh + t * a.vc_st + w];
   const int64_t so = h * a.vs_sh + t * a.vs_st + ((w * CPW) >> a.lg) * a.vs_sg;
@@ -1335,6 +1341,9 @@ extern "C" int uc_kivi_dequant(const void *key_code, int64_t kc_sh, int64_t kc_s
   const bool value_native = value_code != nullptr && (v_bits == 2 || v_bits == 4) && vc_sw == 1;
   if (out_ok && tuned_group(group_size, head_dim) && (key_code == nullptr || key_native) &&
       (value_code == nullptr || value_native)) {
+    UC_REQUIRE(heads * (count + 64) * head_dim < (int64_t(1) << 31),
+               "uc_kivi_dequant: chunk too large for one call (%lld tokens x %lld heads)", (long long)count,
+               (long long)heads);
     UC_DISPATCH_DTYPE(out_dtype, OD, [&] {
       // token-major words and stats (channel stride 1), 16-bit stats and
       // output, 16-byte aligned rows: the octet kernel
