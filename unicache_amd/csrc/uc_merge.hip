@@ -69,8 +69,12 @@ __global__ __launch_bounds__(256) void lse_merge_vec_kernel(MergeArgs a) {
   const int64_t chunks = a.D / CH;
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= a.Lq * a.Hq * chunks) return;
-  const int64_t c = idx % chunks, row = idx / chunks;  // row = i * Hq + hq (memory order of out)
-  const int64_t i = row / a.Hq, hq = row % a.Hq;
+  // row = i * Hq + hq (memory order of out); 32-bit divisions: the launch
+  // keeps the index below 2^31
+  const uint32_t i32 = static_cast<uint32_t>(idx), c32 = static_cast<uint32_t>(chunks);
+  const uint32_t hq32 = static_cast<uint32_t>(a.Hq), r32 = i32 / c32, q32 = r32 / hq32;
+  const int64_t c = i32 - r32 * c32, row = r32;
+  const int64_t i = q32, hq = r32 - q32 * hq32;
   float w[kMaxSegments];
   const float total = merge_weights(a, hq * a.Lq + i, w);
   const int64_t off = row * a.D + c * CH;
@@ -132,6 +136,7 @@ extern "C" int uc_lse_merge(const void *const *outs, const float *const *lses, i
   for (int i = 0; i < n_segments; ++i) vec = vec && (reinterpret_cast<uintptr_t>(outs[i]) & 15) == 0;
   if (vec) {
     const int64_t n = query_len * heads_q * (head_dim / ch);
+    UC_REQUIRE(n < (int64_t(1) << 31), "uc_lse_merge: too many elements for one call");
     UC_DISPATCH_DTYPE(out_dtype, OD, [&] {
       hipLaunchKernelGGL((lse_merge_vec_kernel<OD>), dim3(ceil_div(n, int64_t(256))), dim3(256), 0, s, a);
     });

@@ -1171,8 +1171,10 @@ __global__ __launch_bounds__(256) void fake_quant_channels_kernel(FakeQuantArgs 
   const int64_t total = a.tokens * a.heads * chunks;
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const bool active = idx < total;  // whole groups are active or not: total is a multiple of the group lanes
-  const int64_t k = active ? idx : 0;
-  const int64_t ch = k % chunks, h = (k / chunks) % a.heads, t = k / (chunks * a.heads);
+  // 32-bit divisions: the launch keeps tokens * heads * chunks below 2^31
+  const uint32_t k = active ? static_cast<uint32_t>(idx) : 0u, c32 = static_cast<uint32_t>(chunks);
+  const uint32_t h32 = static_cast<uint32_t>(a.heads), q = k / c32, t32 = q / h32;
+  const int64_t ch = k - q * c32, h = q - t32 * h32, t = t32;
   const int64_t off = t * a.st + h * a.sh + 8 * ch;
   const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.data) + off);
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -1478,6 +1480,7 @@ extern "C" int uc_kivi_fake_quant(const void *data, int64_t st, int64_t sh, int6
   if (half && dim == 2 && sd == 1 && a.group % 8 == 0 && (lanes == 1 || lanes == 2 || lanes == 4 || lanes == 8) &&
       head_dim % a.group == 0 && st % 8 == 0 && sh % 8 == 0 && aligned(data, 16) && aligned(out, 16)) {
     const int64_t n = tokens * heads * (head_dim / 8);
+    UC_REQUIRE(tokens * heads * (head_dim / 8) < (int64_t(1) << 31), "uc_kivi_fake_quant: too many elements for one call");
     const dim3 grid(static_cast<unsigned>(ceil_div(n, 256)));
     UC_DISPATCH_DTYPE(dtype, DT, [&] {
       if constexpr (DT != UC_FP32)
