@@ -443,10 +443,9 @@ __global__ __launch_bounds__(256) void gqa_gather_kernel(GatherArgs a) {
 //
 // Selection.  The heavy_k-th largest order key th is found bit pair by bit
 // pair from the top: with th's higher bits fixed, the block counts the keys
-// >= th | 1 << b, th | 2 << b and th | 3 << b (three counts packed in one
-// word, summed over a wave by shuffles and over the 16 waves through LDS, one
-// barrier per pair) and keeps the largest candidate that still has heavy_k
-// keys at or above it.  Keys above th are all kept; keys equal to th are kept
+// >= th | 1 << b, th | 2 << b and th | 3 << b (counted per wave by ballots,
+// summed over the 16 waves by one 64-bit LDS add each, one barrier per pair)
+// and keeps the largest candidate that still has heavy_k keys at or above it.  Keys above th are all kept; keys equal to th are kept
 // in ascending token order until heavy_k are chosen (torch.topk's tie rule as
 // the reference applies it, physical.py:516-527).  A token's place in the
 // ascending output is (#kept-above before it) + min(#equal before it, need):
@@ -466,7 +465,7 @@ struct SgArgs {
 };
 
 __global__ __launch_bounds__(kSgThreads) void h2o_select_gather_kernel(SgArgs a) {
-  __shared__ uint32_t cnt[2][kSgWaves];
+  __shared__ unsigned long long cnt[3];  // block counts of one bit pair, 21 bits each
   __shared__ uint32_t tab[2][kSgRegs * kSgWaves];  // gt / eq counts per (chunk, wave), then prefixes
   __shared__ uint32_t totals[2];
   __shared__ int32_t keep[kSgMaxKeep];
@@ -494,12 +493,14 @@ __global__ __launch_bounds__(kSgThreads) void h2o_select_gather_kernel(SgArgs a)
 #pragma unroll
     for (int r = 0; r < kSgRegs; ++r)  // order keys of real scores are never 0
       keys[r] = int64_t(r) * kSgThreads + tid < hist_end ? order_key(v[r]) : 0u;
+    if (tid == 0) cnt[0] = 0;
+    __syncthreads();
     uint32_t th = 0;
     for (int it = 0; it < 16; ++it) {
       const int b = 30 - 2 * it;
       const uint32_t c1 = th | (1u << b), c2 = th | (2u << b), c3 = th | (3u << b);
       // wave counts by ballots (keys of invalid tokens are 0, below every
-      // candidate): at most 512 per wave, 10 bits each of one word
+      // candidate): at most 512 per wave, 8192 per block
       uint32_t n1 = 0, n2 = 0, n3 = 0;
 #pragma unroll
       for (int r = 0; r < kSgRegs; ++r) {
@@ -507,16 +508,18 @@ __global__ __launch_bounds__(kSgThreads) void h2o_select_gather_kernel(SgArgs a)
         n2 += __popcll(__ballot(keys[r] >= c2));
         n3 += __popcll(__ballot(keys[r] >= c3));
       }
-      if (lane == 0) cnt[it & 1][wave] = n1 + (n2 << 10) + (n3 << 20);
-      __syncthreads();
-      uint32_t s1 = 0, s2 = 0, s3 = 0;
-#pragma unroll
-      for (int w = 0; w < kSgWaves; ++w) {
-        const uint32_t v = cnt[it & 1][w];
-        s1 += v & 1023u;
-        s2 += (v >> 10) & 1023u;
-        s3 += v >> 20;
+      // one 64-bit LDS add per wave sums the three counts over the block.
+      // Slots rotate over three words: slot it % 3 was cleared in round
+      // it - 1, and slot (it + 1) % 3 was last read in round it - 2, before
+      // every wave reached the previous barrier.
+      if (lane == 0) {
+        if (wave == 0) cnt[(it + 1) % 3] = 0;
+        atomicAdd(&cnt[it % 3], (unsigned long long)n1 | (unsigned long long)n2 << 21 |
+                                    (unsigned long long)n3 << 42);
       }
+      __syncthreads();
+      const unsigned long long sum = cnt[it % 3];
+      const uint32_t s1 = uint32_t(sum) & 0x1fffffu, s2 = uint32_t(sum >> 21) & 0x1fffffu, s3 = uint32_t(sum >> 42);
       th = s3 >= heavy ? c3 : s2 >= heavy ? c2 : s1 >= heavy ? c1 : th;
     }
     // per (chunk, wave) counts of keys above / equal to th
